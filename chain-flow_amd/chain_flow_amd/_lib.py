@@ -1,0 +1,100 @@
+"""ctypes binding of libcfhip.so (the C ABI declared in include/cfhip.h).
+
+The library is loaded from this package directory.  There is no fallback: if it is missing or a
+call fails, the caller gets an exception naming the entry point and the status.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libcfhip.so"
+
+_lib = None
+
+
+class FlowDims(C.Structure):
+    _fields_ = [("d", C.c_int), ("ffn_mult", C.c_int), ("heads", C.c_int), ("layers", C.c_int),
+                ("ctx_rows", C.c_int), ("draft_length", C.c_int), ("chunk_size", C.c_int),
+                ("flow_steps", C.c_int)]
+
+
+_VP = C.c_void_p
+_I = C.c_int
+_I64 = C.c_int64
+
+# name -> (restype, argtypes); mirrors include/cfhip.h
+SIGNATURES = {
+    "cfh_version": (_I, []),
+    "cfh_error_string": (C.c_char_p, [_I]),
+    "cfh_last_hip_error": (_I, []),
+    "cfh_pack_linear": (_I, [_VP, _I, _I, _VP, _VP]),
+    "cfh_caps": (_I, [C.POINTER(FlowDims), _I, C.POINTER(_I64)]),
+    "cfh_flow_expert_bytes": (_I64, [C.POINTER(FlowDims)]),
+    "cfh_flow_pack_expert": (_I, [C.POINTER(FlowDims), C.POINTER(_VP), _I, _VP, _VP]),
+    "cfh_flow_integrate": (_I, [C.POINTER(FlowDims), C.POINTER(_VP), _VP, _VP, _VP, _I, _VP]),
+    "cfh_head_logits": (_I, [_VP, _I, _I, _VP, _VP, _I, _VP, _I, _VP, _VP, _VP]),
+    "cfh_row_topk": (_I, [_VP, _I, _I, _I, _VP, _VP, _VP, _VP]),
+    "cfh_head_topk": (_I, [_VP, _I, _I, _VP, _VP, _I, _VP, _I, _VP, _I, _VP, _VP, _VP, _VP, _VP]),
+    "cfh_head_gemm_topk": (_I, [_VP, _I, _I, _VP, _VP, _I, _I, _VP, _VP, _VP, _VP, _VP]),
+    "cfh_path_ws_bytes": (_I64, [_I, _I, _I, _I]),
+    "cfh_path_residual": (_I, [C.POINTER(_VP), _I, _I, _I, _VP, _I, _I, _VP, _VP, _VP, _VP, _VP]),
+    "cfh_gdn_tree": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _VP, _VP, _VP]),
+}
+
+
+def lib():
+    """The loaded library (raises if libcfhip.so has not been built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with "
+                               f"`python chain-flow_amd/csrc/build.py` (hipcc, gfx950)")
+        h = C.CDLL(str(LIB_PATH), mode=os.RTLD_NOW | getattr(os, "RTLD_GLOBAL", 0))
+        for name, (res, args) in SIGNATURES.items():
+            try:
+                fn = getattr(h, name)
+            except AttributeError:
+                continue          # reported by missing_symbols(); calling it raises
+            fn.restype = res
+            fn.argtypes = args
+        _lib = h
+    return _lib
+
+
+def missing_symbols():
+    """Entry points of include/cfhip.h that the loaded library does not export."""
+    h = lib()
+    out = []
+    for name in SIGNATURES:
+        try:
+            getattr(h, name)
+        except AttributeError:
+            out.append(name)
+    return out
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        L = lib()
+        msg = L.cfh_error_string(status).decode()
+        hip = L.cfh_last_hip_error() if status == 3 else 0
+        raise RuntimeError(f"{what} failed: {msg} (status {status}"
+                           + (f", hipError {hip}" if hip else "") + ")")
+
+
+def ptr(t) -> int | None:
+    """Device (or host) address of a tensor, None for None."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return C.c_void_p(s.cuda_stream)
+
+
+def ptr_array(ptrs):
+    arr = (C.c_void_p * len(ptrs))(*ptrs)
+    return arr

@@ -1,0 +1,100 @@
+// Shared device helpers for the chain-flow MI355X (gfx950) kernels.
+//
+// Conventions used by every kernel in this library:
+//   * wave64; MFMA v_mfma_f32_16x16x32_{f16,bf16}.  Operand layout (checked on the device):
+//       A[i][k]  : lane = i + 16*(k/8), element k%8      (i = output row / activation row)
+//       B[k][n]  : lane = n + 16*(k/8), element k%8      (n = weight row / output column)
+//       D[i][n]  : lane = n + 16*(i/4), accumulator i%4
+//   * A linear layer W[N][K] (row-major, nn.Linear layout) is PACKED so that the B fragment of
+//     (n-tile t, k-step s) is 64 lanes x 16 bytes = 1 KiB contiguous:
+//         packed[(t*(K/32) + s)*64 + lane] = W[16t + lane%16][32s + 8*(lane/16) .. +7]
+//     so one wave streaming one n-tile reads one contiguous run of 16*K halves.
+//   * fp16 rounding (r16) is round-to-nearest-even via v_cvt_f16_f32.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 h16;
+typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+#define CFH_WAVE 64
+
+__device__ __forceinline__ f32x4 mfma_f16(h16x8 a, h16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float r16(float x) { return (float)(h16)x; }
+
+__device__ __forceinline__ float gelu_erf(float x) {
+  return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// Agent-scope release/acquire around the "last arriver" counters used for split-K fixups and
+// per-head attention.  All lanes execute the fences; lane 0 performs the RMW.
+__device__ __forceinline__ unsigned arrive_count(unsigned* ctr) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  unsigned old = 0;
+  if ((threadIdx.x & 63) == 0) old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  old = __shfl(old, 0);
+  return old;
+}
+
+__device__ __forceinline__ void acquire_fence() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+
+__device__ __forceinline__ void reset_count(unsigned* ctr) {
+  if ((threadIdx.x & 63) == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Packed index (in h16x8 units) of the B fragment for (tile, kstep) of a layer with K inputs.
+__host__ __device__ __forceinline__ size_t packed_index(int tile, int kstep, int K, int lane) {
+  return ((size_t)tile * (size_t)(K / 32) + (size_t)kstep) * 64 + lane;
+}
+
+// Stream nsteps k-steps of one packed n-tile against an A operand held in LDS.
+//   wp   : packed fragments of this tile starting at the first k-step of the chunk (+lane added here)
+//   As   : LDS rows [rows][lda] (halves); lane reads row (lane&15), k-offset 8*(lane>>4) + 32*s
+//   rows : number of valid A rows (<= 16); lanes on padding rows feed zeros
+// Keeps PF fragment loads in flight per wave.
+template <int PF>
+__device__ __forceinline__ f32x4 stream_tile(const h16x8* __restrict__ wp, const h16* As, int lda,
+                                             int rows, int nsteps, f32x4 acc) {
+  const int lane = threadIdx.x & 63;
+  const int row = lane & 15;
+  const int kg = lane >> 4;
+  const bool live = row < rows;
+  const h16* arow = As + row * lda + kg * 8;
+  wp += lane;
+  h16x8 buf[PF];
+#pragma unroll
+  for (int p = 0; p < PF; ++p)
+    if (p < nsteps) buf[p] = __builtin_nontemporal_load(wp + (size_t)p * 64);
+  const h16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int s0 = 0; s0 < nsteps; s0 += PF) {
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+      const int s = s0 + p;
+      if (s < nsteps) {
+        const h16x8 b = buf[p];
+        if (s + PF < nsteps) buf[p] = __builtin_nontemporal_load(wp + (size_t)(s + PF) * 64);
+        const h16x8 a = live ? *(const h16x8*)(arow + s * 32) : zero;
+        acc = mfma_f16(a, b, acc);
+      }
+    }
+  }
+  return acc;
+}

@@ -1,0 +1,39 @@
+// Host-side helpers shared by the C-ABI translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "cfhip.h"
+
+namespace cfh {
+
+int set_hip_error(hipError_t e);
+int last_hip_error();
+
+#define CFH_HIP(expr)                                     \
+  do {                                                    \
+    hipError_t _e = (expr);                               \
+    if (_e != hipSuccess) return ::cfh::set_hip_error(_e); \
+  } while (0)
+
+#define CFH_LAUNCH_CHECK() CFH_HIP(hipGetLastError())
+
+inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Byte layout of one packed chunk expert (cfh_flow_pack_expert).  Vectors are fp16 copies of the
+// state_dict tensors; matrices are in MFMA tile order (cfh_common.h).
+struct ExpertLayout {
+  size_t pos, tw0, tb0, tw2, tb2;          // position_embedding, time_mlp
+  size_t blk0, blkstride;                  // block region base / stride
+  // offsets inside a block region
+  size_t sn_w, sn_b, qkv, qkv_b, o, o_b, xn_w, xn_b, cn_w, cn_b, qc, qc_b, kv, kv_b, oc, oc_b,
+      fn_w, fn_b, w1, w1_b, w2, w2_b;
+  size_t on_w, on_b, out, out_b;           // out_norm, out_proj
+  size_t total;
+};
+
+bool flow_dims_ok(const cfh_flow_dims* d);
+ExpertLayout expert_layout(const cfh_flow_dims* d);
+
+}  // namespace cfh

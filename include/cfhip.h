@@ -1,0 +1,144 @@
+/* cfhip.h -- C ABI of the MI355X (gfx950) chain-flow drafting hot path (libcfhip.so).
+ *
+ * Every entry point takes plain device pointers and sizes, an explicit HIP stream (hipStream_t
+ * passed as void*; NULL = the null stream) and returns 0 (CFH_OK) or an error code
+ * (cfh_error_string() names it).  Nothing here allocates device memory: callers own the weights,
+ * the workspace and the outputs.  All launches are asynchronous on the given stream and may be
+ * recorded into a HIP graph (no memset nodes, no host synchronisation inside).
+ *
+ * The reference (Cosmos-YTU/chain-flow, `cf/` = src/chain_flow/) binds its hot path through a
+ * pybind torch extension (cf/csrc/fused_block.cu:793-862) plus plain torch ops; each entry point
+ * below says which reference interface it replaces.
+ *
+ * fp16 = IEEE half, bf16 = bfloat16; "packed" = the MFMA tile order produced by cfh_pack_linear.
+ */
+#ifndef CFHIP_H
+#define CFHIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CFH_OK 0
+#define CFH_E_INVALID 1          /* bad argument (null pointer, size out of range)        */
+#define CFH_E_UNSUPPORTED 2      /* shape this build does not support                     */
+#define CFH_E_HIP 3              /* a HIP runtime call failed (cfh_last_hip_error)        */
+
+/* Library version (major*10000 + minor*100 + patch). */
+int cfh_version(void);
+/* Human-readable text for a status code. */
+const char* cfh_error_string(int status);
+/* The hipError_t of the last failing HIP call made by this library on this thread. */
+int cfh_last_hip_error(void);
+
+/* ---------------------------------------------------------------- weight packing
+ * Pack a row-major linear weight W[n][k] (nn.Linear layout, fp16 or bf16 -- the packing is
+ * dtype-agnostic 2-byte data) into MFMA tile order: out holds n*k halves.  n % 16 == 0,
+ * k % 32 == 0.  Replaces the reference's host-side weight packing
+ * (cf/cuda_block.py:269-318, layout cf/csrc/fused_block.cu:47-79). */
+int cfh_pack_linear(const void* w, int n, int k, void* out, void* stream);
+
+/* ---------------------------------------------------------------- flow (velocity net + Euler)
+ * Shape of one TreeFlowDrafter flow: HiddenKVFlowExpert chunk experts
+ * (cf/drafters/tree_flow.py:40-77, cf/drafters/chunked_flow.py:205-414). */
+typedef struct cfh_flow_dims {
+  int d;             /* hidden size (expert_dim == target hidden size); d % 512 == 0       */
+  int ffn_mult;      /* ffn multiplier (6)                                                 */
+  int heads;         /* attention heads (8); (d / heads) % 64 == 0                         */
+  int layers;        /* HiddenKVFlowBlocks per expert (num_drafter_layers)                 */
+  int ctx_rows;      /* context_size (8); 2 <= ctx_rows <= 16                              */
+  int draft_length;  /* draft_length (8); <= 16                                            */
+  int chunk_size;    /* chunk_size (4); draft_length % chunk_size == 0                     */
+  int flow_steps;    /* num_flow_steps E (Euler steps); 1 <= E <= 16                       */
+} cfh_flow_dims;
+
+/* Capability/shape gate: 0 (CFH_OK) if this build runs `dims` at `batch`, with the workspace
+ * size in *ws_bytes; CFH_E_UNSUPPORTED otherwise.  Replaces cuda_block.supported()/max_grid()
+ * (cf/cuda_block.py:95-163, cf/csrc/fused_block.cu:836-856). */
+int cfh_caps(const cfh_flow_dims* dims, int batch, int64_t* ws_bytes);
+
+/* Bytes of one expert's packed weight image. */
+int64_t cfh_flow_expert_bytes(const cfh_flow_dims* dims);
+
+/* Pack one chunk expert.  raw[] = device pointers to the expert's fp16 parameters in
+ * state_dict order (n_raw = 9 + 20*layers):
+ *   position_embedding.weight, time_mlp.0.weight, time_mlp.0.bias, time_mlp.2.weight,
+ *   time_mlp.2.bias, then per block l: self_norm.{weight,bias}, self_attn.in_proj_{weight,bias},
+ *   self_attn.out_proj.{weight,bias}, cross_norm.{weight,bias}, context_norm.{weight,bias},
+ *   cross_attn.in_proj_{weight,bias}, cross_attn.out_proj.{weight,bias}, ffn.0.{weight,bias},
+ *   ffn.1.{weight,bias}, ffn.4.{weight,bias}, then out_norm.{weight,bias}, out_proj.{weight,bias}.
+ * Replaces FusedExpertBlocks.__init__ packing (cf/cuda_block.py:269-318). */
+int cfh_flow_pack_expert(const cfh_flow_dims* dims, const void* const* raw, int n_raw, void* packed,
+                         void* stream);
+
+/* TreeFlowDrafter.predict_hidden (cf/drafters/tree_flow.py:229-244): init_latents(ctx) then all
+ * E Euler steps of both chunk experts (every block of every expert, cross-K/V hoisted once).
+ *   experts : n_chunks = draft_length/chunk_size packed expert images (chunk order)
+ *   ctx     : [batch][ctx_rows][d] fp16 context hidden states (already front-padded)
+ *   z_out   : [batch][draft_length][d] fp16 predicted hiddens
+ *   ws      : workspace of cfh_caps() bytes
+ * Replaces the per-Euler-step torch loop plus the fused kernel launch
+ * (cf/cuda_block.py:407-431 / pybind `expert`, `cross_kv`, cf/csrc/fused_block.cu:793-862). */
+int cfh_flow_integrate(const cfh_flow_dims* dims, const void* const* experts, const void* ctx,
+                       void* z_out, void* ws, int batch, void* stream);
+
+/* ---------------------------------------------------------------- shortlisted lm_head
+ * logits[m][j] = fp16( fp16(h[m] . W[row_j]) + fp16(a[m] . W2[row_j]) ),  row_j = sl ? sl[j] : j
+ *   h [M][d] fp16, W [V][d] fp16 (the target's full lm_head; rows gathered through sl),
+ *   a [M][r] fp16 / W2 [V][r] fp16 optional markov bias (both NULL = none), M <= 16.
+ *   logits [M][n] fp16.
+ * Replaces FlowDrafterProposer._head + _bias (cf/vllm_plugin/flow_proposer.py:1021-1025) with a
+ * row-gather GEMV over the int32 shortlist (no gathered copy of lm_w[sl]). */
+int cfh_head_logits(const void* h, int M, int d, const void* W, const int32_t* sl, int n,
+                    const void* a, int r, const void* W2, void* logits, void* stream);
+
+/* Per-row log-softmax top-k of fp16 logits [M][n]: vals[m][i] = logit - logsumexp (fp32),
+ * ids[m][i] = column, descending, ties to the lower column; lse[m] (may be NULL).  k <= 16.
+ * Replaces torch.log_softmax(logits.float()).topk(k) (cf/vllm_plugin/flow_proposer.py:1249-1250). */
+int cfh_row_topk(const void* logits, int M, int n, int k, float* vals, int32_t* ids, float* lse,
+                 void* stream);
+
+/* cfh_head_logits followed by cfh_row_topk; `logits` is caller scratch [M][n] fp16. */
+int cfh_head_topk(const void* h, int M, int d, const void* W, const int32_t* sl, int n,
+                  const void* a, int r, const void* W2, int k, void* logits, float* vals,
+                  int32_t* ids, float* lse, void* stream);
+
+/* Batched (M up to 256) bf16 skinny-GEMM head with per-row top-k: the two-pass candidate head's
+ * pass A (cf/vllm_plugin/flow_proposer.py:1142-1165) as one MFMA kernel.
+ *   x [M][d] bf16, W [V][d] bf16 gathered through sl (or contiguous if sl == NULL),
+ *   logits [M][n] bf16 scratch, vals/ids [M][k], lse [M] (may be NULL).  k <= 16. */
+int cfh_head_gemm_topk(const void* x, int M, int d, const void* W, const int32_t* sl, int n, int k,
+                       void* logits, float* vals, int32_t* ids, float* lse, void* stream);
+
+/* ---------------------------------------------------------------- draft search
+ * Path-conditioned residual of the PathHead, fused form (cf/vllm_plugin/fused.py:25-37):
+ *   hsum[m] = fp16( pred + MLP(LN( sum_{j<nlive} mask_j (W_j emb(lastp[m][j]) + b_j) )) )
+ * with emb = embed_w rows of the global ids in lastp [M][order] (int32, -1 = no ancestor).
+ * ph = path head fp16 parameters, device pointers in this order:
+ *   offset_proj.{0..order-1}.weight (each [d][d]), offset_proj.{0..order-1}.bias,
+ *   norm.weight, norm.bias, mlp.0.weight [f*d][d], mlp.0.bias, mlp.3.weight [d][f*d], mlp.3.bias
+ * pred [d] fp16 (the marginal hidden of this depth, shared by the M rows). ws: cfh_path_ws_bytes. */
+int64_t cfh_path_ws_bytes(int M, int d, int ffn_mult, int order);
+int cfh_path_residual(const void* const* ph, int order, int ffn_mult, int d, const int32_t* lastp,
+                      int M, int nlive, const void* embed_w, const void* pred, void* hsum, void* ws,
+                      void* stream);
+
+/* ---------------------------------------------------------------- tree gated delta net
+ * tree_gated_delta_scan (cf/kernels/tree_scan.py:41-73): per node n (BFS order, parent[n] < n,
+ * -1 = root reading S0): S = exp(g) S_parent; delta = (v - S^T k) beta; S += k (x) delta;
+ * out = S^T q, with q,k l2-normalised (l2mode 0: x/(|x|+1e-6), 1: x/sqrt(|x|^2+1e-6)) and
+ * q scaled by Dk^-1/2.
+ *   q,k [N][H][Dk] bf16, v [N][H][Dv] bf16, g,beta [N][H] fp32, S0 [H][Dk][Dv] fp32,
+ *   out [N][H][Dv] fp32, states [N][H][Dk][Dv] fp32 or NULL.  Dk == 128, Dv % 64 == 0, N <= 256.
+ * Replaces the fork's gdn_verify (patch:4606-4660) / tree_ssm Triton kernels for this layout. */
+int cfh_gdn_tree(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                 const float* S0, const int32_t* parent, int N, int H, int Dk, int Dv,
+                 int use_l2norm, int l2mode, float* out, float* states, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CFHIP_H */

@@ -1,0 +1,207 @@
+"""Oracle: the chain-flow velocity net and Euler integrator (``TreeFlowDrafter.predict_hidden``).
+
+Follows, in the reference (``cf/`` = ``src/chain_flow/``):
+
+* ``cf/drafters/tree_flow.py:143-148``  ``_context`` front-padding (repeat the oldest row)
+* ``cf/drafters/tree_flow.py:150-161``  ``init_latents`` (mode ``delta`` / ``repeat_last``)
+* ``cf/drafters/tree_flow.py:163-174``  ``_chunk_args`` (previous rows are sliced from the step input)
+* ``cf/drafters/tree_flow.py:176-190``  ``flow_velocity`` (one expert per chunk, velocities concatenated)
+* ``cf/drafters/tree_flow.py:229-235``  ``integrate`` (Euler, dt = 1/E, tau = s*dt)
+* ``cf/drafters/chunked_flow.py:264-275, 333-380``  ``pre_blocks`` (positions, time MLP, causal mask)
+* ``cf/drafters/chunked_flow.py:185-202``  ``HiddenKVFlowBlock.forward`` (pre-LN self-MHA, cross-MHA,
+  LN -> Linear(d, f*d) -> erf-GELU -> Linear(f*d, d))
+* ``cf/drafters/chunked_flow.py:382-384``  ``post_blocks`` (out_norm + out_proj on the current rows)
+* ``cf/csrc/fused_block.cu:280-325, 452-668, 674-722``  the fused-kernel numerics: fp32 residual,
+  fp16-parked LayerNorm rows, fp16 q/k/v, attention output and GELU output; cross K/V from
+  ``context_norm(ctx)`` computed once per draft.
+
+Weights come in as a dict keyed by the reference's ``state_dict`` names
+(``expert.blocks.{l}.self_attn.in_proj_weight`` ...), values float arrays already holding the exact
+values the device path uses (fp16-representable for the fp16 path).
+"""
+from __future__ import annotations
+
+import numpy as np
+from scipy.special import erf
+
+LN_EPS = 1e-5
+
+
+def r16(x, numerics):
+    """Round to fp16 when the fp16 path materialises this tensor; identity for fp32 numerics."""
+    if numerics == "fp16":
+        return np.asarray(x, dtype=np.float64).astype(np.float16).astype(np.float64)
+    return np.asarray(x, dtype=np.float64)
+
+
+def layer_norm(x, w, b, numerics, eps=LN_EPS):
+    """``nn.LayerNorm`` over the last dim (biased variance).  The input row is first parked as fp16
+    for the fp16 path, which is the dtype the reference's LayerNorm sees
+    (``cf/csrc/fused_block.cu:291-304``)."""
+    xx = r16(x, numerics)
+    mu = xx.mean(-1, keepdims=True)
+    var = ((xx - mu) ** 2).mean(-1, keepdims=True)
+    return (xx - mu) / np.sqrt(var + eps) * w + b
+
+
+def gelu(x):
+    """``nn.GELU()`` default (approximate='none'): 0.5 x (1 + erf(x / sqrt 2))."""
+    return 0.5 * x * (1.0 + erf(x / np.sqrt(2.0)))
+
+
+def silu(x):
+    return x / (1.0 + np.exp(-x))
+
+
+def attention(q, k, v, heads, mask=None):
+    """Scaled dot-product attention per head for ``nn.MultiheadAttention`` (batch_first).
+
+    q [B, Sq, d], k/v [B, Sk, d] -> [B, Sq, d] (heads merged), scale 1/sqrt(d/heads), additive mask
+    [Sq, Sk] (``cf/drafters/chunked_flow.py:273-275``)."""
+    B, Sq, d = q.shape
+    Sk = k.shape[1]
+    hd = d // heads
+    qh = q.reshape(B, Sq, heads, hd).transpose(0, 2, 1, 3)
+    kh = k.reshape(B, Sk, heads, hd).transpose(0, 2, 1, 3)
+    vh = v.reshape(B, Sk, heads, hd).transpose(0, 2, 1, 3)
+    s = qh @ kh.transpose(0, 1, 3, 2) / np.sqrt(hd)
+    if mask is not None:
+        s = s + mask
+    s = s - s.max(-1, keepdims=True)
+    p = np.exp(s)
+    p = p / p.sum(-1, keepdims=True)
+    o = p @ vh
+    return o.transpose(0, 2, 1, 3).reshape(B, Sq, d)
+
+
+def causal_mask(S):
+    """``torch.triu(full(-inf), diagonal=1)`` (``cf/drafters/chunked_flow.py:273-275``)."""
+    m = np.zeros((S, S))
+    m[np.triu_indices(S, 1)] = -np.inf
+    return m
+
+
+def front_pad_context(hidden, context_size):
+    """``TreeFlowDrafter._context`` (``cf/drafters/tree_flow.py:143-148``): the last C rows; fewer
+    than C are front-padded by repeating the OLDEST row."""
+    n = hidden.shape[1]
+    if n >= context_size:
+        return hidden[:, -context_size:]
+    pad = np.repeat(hidden[:, :1], context_size - n, axis=1)
+    return np.concatenate([pad, hidden], axis=1)
+
+
+def init_latents(context, draft_length, numerics, mode="delta"):
+    """``TreeFlowDrafter.init_latents`` (``cf/drafters/tree_flow.py:150-161``), computed in the
+    expert dtype: fp16 rounding of the delta, of ``steps * delta`` and of the sum."""
+    last = context[:, -1:, :]
+    if mode == "repeat_last":
+        return np.repeat(last, draft_length, axis=1).copy()
+    if mode != "delta":
+        raise ValueError("init_mode must be 'delta' or 'repeat_last' (noise is not deterministic)")
+    if context.shape[1] > 1:
+        delta = r16(context[:, -1:, :] - context[:, -2:-1, :], numerics)
+    else:
+        delta = np.zeros_like(last)
+    steps = np.arange(1, draft_length + 1, dtype=np.float64).reshape(1, draft_length, 1)
+    return r16(last + r16(steps * delta, numerics), numerics)
+
+
+def _lin(x, w, b):
+    y = x @ w.T
+    return y + b if b is not None else y
+
+
+def tau_embedding(W, pfx, tau, numerics):
+    """``time_mlp(tau)`` = Linear(1, d) -> SiLU -> Linear(d, d) (``cf/drafters/chunked_flow.py:230-234,
+    264-271``).  tau is a scalar shared by the batch."""
+    h = r16(tau * W[pfx + "time_mlp.0.weight"][:, 0] + W[pfx + "time_mlp.0.bias"], numerics)
+    h = r16(silu(h), numerics)
+    return r16(_lin(h, W[pfx + "time_mlp.2.weight"], W[pfx + "time_mlp.2.bias"]), numerics)
+
+
+def cross_kv(W, bp, ctx, numerics):
+    """Cross-attention K/V of one block: ``context_norm(ctx)`` through in_proj rows [d:3d]
+    (``cf/drafters/chunked_flow.py:194-199``; hoisted once per draft as in
+    ``cf/csrc/fused_block.cu:674-722``)."""
+    d = ctx.shape[-1]
+    c = r16(layer_norm(ctx, W[bp + "context_norm.weight"], W[bp + "context_norm.bias"], numerics), numerics)
+    w = W[bp + "cross_attn.in_proj_weight"]
+    b = W[bp + "cross_attn.in_proj_bias"]
+    k = r16(_lin(c, w[d:2 * d], b[d:2 * d]), numerics)
+    v = r16(_lin(c, w[2 * d:], b[2 * d:]), numerics)
+    return k, v
+
+
+def block_forward(W, bp, res, kv, mask, heads, numerics):
+    """One ``HiddenKVFlowBlock`` on the fp32 residual ``res`` [B, S, d]
+    (``cf/drafters/chunked_flow.py:185-202``; stage structure of ``cf/csrc/fused_block.cu:528-662``)."""
+    d = res.shape[-1]
+    # 1-2: self attention
+    a = r16(layer_norm(res, W[bp + "self_norm.weight"], W[bp + "self_norm.bias"], numerics), numerics)
+    w, b = W[bp + "self_attn.in_proj_weight"], W[bp + "self_attn.in_proj_bias"]
+    qkv = r16(_lin(a, w, b), numerics)
+    o = r16(attention(qkv[..., :d], qkv[..., d:2 * d], qkv[..., 2 * d:], heads, mask), numerics)
+    res = res + _lin(o, W[bp + "self_attn.out_proj.weight"], W[bp + "self_attn.out_proj.bias"])
+    # 3-4: cross attention over the (hoisted) context K/V
+    a = r16(layer_norm(res, W[bp + "cross_norm.weight"], W[bp + "cross_norm.bias"], numerics), numerics)
+    w, b = W[bp + "cross_attn.in_proj_weight"], W[bp + "cross_attn.in_proj_bias"]
+    q = r16(_lin(a, w[:d], b[:d]), numerics)
+    o = r16(attention(q, kv[0], kv[1], heads, None), numerics)
+    res = res + _lin(o, W[bp + "cross_attn.out_proj.weight"], W[bp + "cross_attn.out_proj.bias"])
+    # 5-6: feed-forward
+    a = r16(layer_norm(res, W[bp + "ffn.0.weight"], W[bp + "ffn.0.bias"], numerics), numerics)
+    u = _lin(a, W[bp + "ffn.1.weight"], W[bp + "ffn.1.bias"])
+    g = r16(gelu(u), numerics)
+    return res + _lin(g, W[bp + "ffn.4.weight"], W[bp + "ffn.4.bias"])
+
+
+def expert_velocity(W, pfx, prev, cur, tau_add, chunk_start, kvs, cfg, numerics):
+    """``HiddenKVFlowExpert.forward`` = pre_blocks -> L blocks -> post_blocks
+    (``cf/drafters/chunked_flow.py:333-414``).  prev [B, P, d], cur [B, c, d] -> velocity [B, c, d]."""
+    x = np.concatenate([prev, cur], axis=1)
+    P, c = prev.shape[1], cur.shape[1]
+    pos = np.concatenate([np.arange(P), chunk_start + np.arange(c)])
+    if max(P - 1, chunk_start + c - 1) >= cfg["draft_length"]:
+        raise ValueError("hidden_kv_flow position exceeds configured draft length")
+    x = r16(x + W[pfx + "position_embedding.weight"][pos][None], numerics)
+    x[:, P:] = r16(x[:, P:] + tau_add[None, None, :], numerics)
+    mask = causal_mask(P + c)
+    res = x.copy()
+    for l in range(cfg["num_layers"]):
+        res = block_forward(W, f"{pfx}blocks.{l}.", res, kvs[l], mask, cfg["num_heads"], numerics)
+    a = r16(layer_norm(res[:, P:], W[pfx + "out_norm.weight"], W[pfx + "out_norm.bias"], numerics), numerics)
+    return r16(_lin(a, W[pfx + "out_proj.weight"], W[pfx + "out_proj.bias"]), numerics)
+
+
+def expert_prefixes(num_chunks):
+    """State-dict prefixes of the chunk experts, in chunk order (``cf/drafters/tree_flow.py:113-131``)."""
+    return ["expert."] + [f"extra_experts.{i}." for i in range(num_chunks - 1)]
+
+
+def predict_hidden(W, context, cfg, numerics="fp16", return_trace=False):
+    """``TreeFlowDrafter.predict_hidden`` (``cf/drafters/tree_flow.py:229-244``).
+
+    context [B, C, d] (values in the expert dtype) -> z_E [B, draft_length, d].
+    cfg keys: draft_length, chunk_size, num_layers, num_heads, num_flow_steps, init_mode."""
+    context = r16(context, numerics)
+    K, cs, E = cfg["draft_length"], cfg["chunk_size"], cfg["num_flow_steps"]
+    nch = K // cs
+    pfxs = expert_prefixes(nch)
+    kvs = [[cross_kv(W, f"{p}blocks.{l}.", context, numerics) for l in range(cfg["num_layers"])]
+           for p in pfxs]
+    z = init_latents(context, K, numerics, cfg.get("init_mode", "delta"))
+    trace = [z.copy()]
+    dt = 1.0 / E
+    for s in range(E):
+        tau = r16(np.float64(s * dt), numerics)
+        vels = []
+        for ci, p in enumerate(pfxs):
+            start = ci * cs
+            tau_add = tau_embedding(W, p, tau, numerics)
+            vels.append(expert_velocity(W, p, z[:, :start], z[:, start:start + cs], tau_add, start,
+                                        kvs[ci], cfg, numerics))
+        v = np.concatenate(vels, axis=1)
+        z = r16(z + r16(dt * v, numerics), numerics)
+        trace.append(z.copy())
+    return (z, trace) if return_trace else z

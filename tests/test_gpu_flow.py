@@ -1,0 +1,47 @@
+"""GPU parity of the fused flow (cfh_flow_integrate) against the CPU oracle.
+
+Contract: predicted hiddens within 2e-3 norm-relative of the oracle's fp16-path restatement of
+``TreeFlowDrafter.predict_hidden`` on the same seeded weights and context.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_err, to64, weights64
+from chain_flow_amd.config import flownet
+from chain_flow_amd.flow import FusedFlow
+from chain_flow_amd.weights import make_weights, synthetic_context
+from oracle import flow as oflow
+
+TOL_FP16 = 2e-3
+
+
+def _ocfg(cfg):
+    return dict(draft_length=cfg.draft_length, chunk_size=cfg.chunk_size,
+                num_layers=cfg.num_drafter_layers, num_heads=cfg.num_heads,
+                num_flow_steps=cfg.num_flow_steps, init_mode=cfg.init_mode)
+
+
+def _flow_weights(cfg, init="test", seed=0):
+    from chain_flow_amd.weights import param_specs
+    names = [n for n in param_specs(cfg, 16, target=False) if n.startswith(("expert.", "extra_experts."))]
+    return make_weights(cfg, 16, init=init, base_seed=seed, names=set(names), target=False)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("d,layers,steps", [(512, 1, 1), (512, 2, 2), (1024, 2, 3)])
+def test_flow_matches_oracle(cuda, d, layers, steps):
+    cfg = flownet(d, layers=layers, flow_steps=steps)
+    W = _flow_weights(cfg)
+    ctx = synthetic_context(1, cfg.context_size, d, seed=1)
+    print(f"[flow parity] d={d} L={layers} E={steps}", flush=True)
+    ff = FusedFlow(cfg, {k: v.to(cuda) for k, v in W.items()}, device=cuda)
+    z = ff.predict_hidden(ctx.to(cuda))
+    torch.cuda.synchronize()
+    ref = oflow.predict_hidden(weights64(W), to64(ctx), _ocfg(cfg), numerics="fp16")
+    err = rel_err(to64(z), ref)
+    print(f"  rel err {err:.3e}", flush=True)
+    assert np.isfinite(to64(z)).all()
+    assert err < TOL_FP16

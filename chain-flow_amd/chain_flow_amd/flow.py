@@ -37,6 +37,8 @@ class FusedFlow:
             raise ValueError("the fused flow implements init_mode='delta' (the drafter default)")
         self.cfg = cfg
         self.device = torch.device(device)
+        if self.device.type == "cuda" and self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
         self.dims = flow_dims(cfg)
         L = _lib.lib()
         ws = caps(cfg, 1)

@@ -65,36 +65,71 @@ __host__ __device__ __forceinline__ size_t packed_index(int tile, int kstep, int
   return ((size_t)tile * (size_t)(K / 32) + (size_t)kstep) * 64 + lane;
 }
 
-// Stream nsteps k-steps of one packed n-tile against an A operand held in LDS.
-//   wp   : packed fragments of this tile starting at the first k-step of the chunk (+lane added here)
+// Weight-streaming MFMA loop over one packed n-tile, split in two so that the first PF fragment
+// loads can be issued before the activation chunk is staged (the weights do not depend on it):
+//   TileStream<PF> ts; ts.begin(wp, nsteps);  ...stage A, __syncthreads()...;  acc = ts.run(...)
+//   wp   : packed fragments of this tile at the first k-step of the chunk (lane offset added here)
 //   As   : LDS rows [rows][lda] (halves); lane reads row (lane&15), k-offset 8*(lane>>4) + 32*s
 //   rows : number of valid A rows (<= 16); lanes on padding rows feed zeros
-// Keeps PF fragment loads in flight per wave.
+// When nsteps is a multiple of PF the loads are issued unconditionally PF steps ahead, so the
+// compiler keeps PF fragment loads in flight per wave (vmcnt(PF-1) waits); other step counts
+// take a plain loop.
 template <int PF>
-__device__ __forceinline__ f32x4 stream_tile(const h16x8* __restrict__ wp, const h16* As, int lda,
-                                             int rows, int nsteps, f32x4 acc) {
-  const int lane = threadIdx.x & 63;
-  const int row = lane & 15;
-  const int kg = lane >> 4;
-  const bool live = row < rows;
-  const h16* arow = As + row * lda + kg * 8;
-  wp += lane;
+struct TileStream {
   h16x8 buf[PF];
+  const h16x8* wp;
+  int nsteps;
+  bool piped;
+
+  __device__ __forceinline__ void begin(const h16x8* __restrict__ w, int n) {
+    wp = w + (threadIdx.x & 63);
+    nsteps = n;
+    piped = (n >= PF) && (n % PF == 0);
+    if (piped) {
 #pragma unroll
-  for (int p = 0; p < PF; ++p)
-    if (p < nsteps) buf[p] = __builtin_nontemporal_load(wp + (size_t)p * 64);
-  const h16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int s0 = 0; s0 < nsteps; s0 += PF) {
+      for (int p = 0; p < PF; ++p) buf[p] = __builtin_nontemporal_load(wp + (size_t)p * 64);
+    }
+  }
+
+  __device__ __forceinline__ f32x4 run(const h16* As, int lda, int rows, f32x4 acc) {
+    const int lane = threadIdx.x & 63;
+    const int row = lane & 15;
+    const int kg = lane >> 4;
+    const bool live = row < rows;
+    const h16* arow = As + (live ? row : 0) * lda + kg * 8;
+    const h16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (piped) {
+      int s0 = 0;
+      for (; s0 < nsteps - PF; s0 += PF) {
 #pragma unroll
-    for (int p = 0; p < PF; ++p) {
-      const int s = s0 + p;
-      if (s < nsteps) {
-        const h16x8 b = buf[p];
-        if (s + PF < nsteps) buf[p] = __builtin_nontemporal_load(wp + (size_t)(s + PF) * 64);
+        for (int p = 0; p < PF; ++p) {
+          const h16x8 b = buf[p];
+          buf[p] = __builtin_nontemporal_load(wp + (size_t)(s0 + PF + p) * 64);
+          const h16x8 a = live ? *(const h16x8*)(arow + (s0 + p) * 32) : zero;
+          acc = mfma_f16(a, b, acc);
+        }
+      }
+#pragma unroll
+      for (int p = 0; p < PF; ++p) {
+        const h16x8 a = live ? *(const h16x8*)(arow + (s0 + p) * 32) : zero;
+        acc = mfma_f16(a, buf[p], acc);
+      }
+    } else {
+      for (int s = 0; s < nsteps; ++s) {
+        const h16x8 b = __builtin_nontemporal_load(wp + (size_t)s * 64);
         const h16x8 a = live ? *(const h16x8*)(arow + s * 32) : zero;
         acc = mfma_f16(a, b, acc);
       }
     }
+    return acc;
   }
-  return acc;
+};
+
+// One-call form: stream nsteps k-steps of a packed tile against LDS rows.
+template <int PF>
+__device__ __forceinline__ f32x4 stream_tile(const h16x8* __restrict__ wp, const h16* As, int lda,
+                                             int rows, int nsteps, f32x4 acc) {
+  TileStream<PF> ts;
+  ts.begin(wp, nsteps);
+  return ts.run(As, lda, rows, acc);
 }

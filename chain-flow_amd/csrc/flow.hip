@@ -6,26 +6,32 @@
 // numerics cf/csrc/fused_block.cu:280-325, 452-668, 674-722 (fp32 residual, fp16-parked LayerNorm
 // rows, fp16 q/k/v, attention and GELU outputs, cross K/V hoisted once per draft).
 //
-// Execution plan (one launch sequence per draft, every launch on the caller's stream):
-//   init  : z0 = init_latents(ctx); x rows of step 0 (pre_blocks) and their LayerNorm moments
-//   kv    : cross-attention K/V of every block of every chunk expert (once per draft)
-//   tau   : time_mlp(tau_s) for all E steps (tau only depends on s)
-//   per Euler step s, per block l, both chunk experts in the same launch:
-//     QKV : LN_self(x) -> q,k,v (fp16); the last wave to finish a head runs its causal attention
-//     O   : x += attn W_o^T + b_o                          (+ LayerNorm moments of the new x)
-//     QC  : LN_cross(x) -> q (fp16); the last wave of a head runs cross attention on the hoisted K/V
-//     OC  : x += attn W_oc^T + b_oc                        (+ moments)
-//     W1  : g = GELU(LN_ffn(x) W1^T + b1) (fp16)
-//     W2  : x += g W2^T + b2                               (+ moments)
-//   OUT   : v = out_proj(out_norm(x[cur rows])); z = fp16(z + dt v); next step's pre_blocks rows
+// Execution plan: one launch sequence per draft on the caller's stream, both chunk experts in
+// every launch.  Work that needs a whole row or a whole head sits at a kernel boundary; there is
+// no cross-workgroup synchronisation inside any kernel (no fences, no atomics, no spin-waits), so
+// every result is deterministic.
 //
-// Every GEMV is a weight-streaming MFMA loop (cfh_common.h stream_tile): a wave owns one
-// (n-tile of 16 outputs, k-chunk) unit and streams its contiguous packed fragments while the
-// activation rows (<= 16) sit in LDS.  Split-K units leave fp32 partials; the last unit of a tile
-// to finish (agent-scope counter) sums them in k-chunk order and runs the epilogue, so results do
-// not depend on arrival order.  LayerNorm moments (sum, sum of squares of the fp16-parked row) are
-// accumulated by the residual epilogues with fp32 atomics, so the next LayerNorm needs no extra
-// pass over the row.
+//   per draft : KV  (cross K/V of every block) -> REDUCE ; TAU (time_mlp(tau_s), all s) -> REDUCE ;
+//               ROWS(init): z0 = init_latents(ctx), step-0 rows x, LN_self of block 0
+//   per step s, per block l:
+//     QKV  GEMV  A = LN_self(x)         -> fp32 partials
+//     ATTN       q,k,v = fp16(sum partials + b); causal self attention -> attn (fp16)
+//     O    GEMV  A = attn               -> partials
+//     NORM       x += sum + b_o; A = fp16(LN_cross(fp16(x)))
+//     QC   GEMV  A = LN_cross(x)        -> partials
+//     ATTN       q = fp16(sum + b); attention over the hoisted context K/V -> attn
+//     OC   GEMV  A = attn               -> partials
+//     NORM       x += sum + b_oc; A = LN_ffn(x)
+//     W1   GEMV  A = LN_ffn(x)          -> partials
+//     GELU       g = fp16(gelu(sum + b1))
+//     W2   GEMV  A = g                  -> partials
+//     NORM       x += sum + b2; A = LN_self of the next block (out_norm after the last block)
+//   OUT  GEMV  A = out_norm(x[current rows]) -> partials
+//   ROWS(euler): v = fp16(sum + b_out); z = fp16(z + fp16(dt v)); next step's rows and LN_self
+//
+// Every GEMV is split-K over workgroups: a wave owns one (n-tile of 16 outputs, k-chunk) unit,
+// streams the tile's packed fragments (cfh_common.h stream_tile) against the activation chunk held
+// in LDS, and stores its fp32 partial tile; the next kernel sums the partials in chunk order.
 #include <stdio.h>
 
 #include <algorithm>
@@ -35,171 +41,60 @@
 
 namespace {
 
-constexpr int WPB = 4;          // waves per workgroup
-constexpr int PF = 8;           // fragment loads in flight per wave
-constexpr int MAXR = 16;        // max activation rows per expert
+constexpr int WPB = 4;            // waves per GEMV workgroup
+constexpr int PF = 8;             // fragment loads in flight per wave
+constexpr int MAXR = 16;          // max activation rows per expert (draft_length, ctx rows, steps)
+constexpr int ROWT = 1024;        // threads of the row kernels (NORM / ROWS)
+constexpr int ROWE = 16;          // max elements per thread in the row kernels (d <= 16384)
 constexpr float LN_EPS = 1e-5f;
-constexpr int MAX_UNITS = 16384;  // split-K (tile, k-chunk) units per expert per phase
 
-enum Kind { K_QKV = 0, K_O, K_QC, K_OC, K_W1, K_W2, K_OUT, K_KV, K_TAU };
+enum Src { SRC_BUF = 0, SRC_CTX, SRC_TAU };
 
-struct PhaseEx {
-  const h16x8* w;        // packed matrix of this phase (layer 0 of the unit range for KV)
-  const h16* bias;       // [N]
-  const h16* lng;        // LayerNorm gamma (A1/KV) | time_mlp.0.weight (TAU)
-  const h16* lnb;        // LayerNorm beta          | time_mlp.0.bias   (TAU)
-  const float* st_in;    // [MAXR][2] LayerNorm moments of x (A1)
-  float* st_out;         // [MAXR][2] moments of the updated x (residual epilogues)
-  float* x;              // [srows][d] fp32 residual
-  h16* x16;              // [srows][d] fp16 copy of x (what LayerNorm reads)
-  h16* qkv;              // [srows][3d]
-  h16* attn;             // [srows][d]
-  h16* g;                // [srows][f*d]
-  const h16* kv;         // [2][C][d] cross K/V of this block (QC)
-  h16* out;              // KV: [L][2][C][d]   TAU: [E][d]
-  const h16* pos;        // OUT: position_embedding [KD][d]
-  const h16* tau_next;   // OUT: time_mlp(tau_{s+1}) [d]
-  float* st_next;        // OUT: [MAXR][2] moments of next step's x
-  float* x_next;         // OUT: next step's residual rows (the other ping-pong buffer)
-  h16* x16_next;         // OUT: fp16 copy of x_next
-  int rows;              // activation rows of this phase
-  int row0;              // first x row read by this phase (OUT: current chunk)
-  int srows;             // rows of this expert's sequence (prev + current)
+// ---------------------------------------------------------------------------- GEMV
+struct GemvEx {
+  const h16x8* w;      // packed weight fragments (layer 0 when nl > 1)
+  const h16* a;        // SRC_BUF: activation rows [rows][lda]; SRC_CTX: context rows [rows][K]
+  int lda;
+  const h16* g0;       // SRC_CTX: context_norm weight (layer 0) | SRC_TAU: time_mlp.0.weight
+  const h16* b0;       // SRC_CTX: context_norm bias             | SRC_TAU: time_mlp.0.bias
+  float* pout;         // partial outputs [(l*ks + kc)][rows][N]
+  const float* mom;    // SRC_CTX: context row moments [rows][2] = (mean, rstd)
+  int rows;
 };
 
-struct PhaseArgs {
-  PhaseEx ex[4];
-  int nex, nl;
-  long long wstride, vstride;   // KV: bytes between consecutive layers' packed / vector params
-  int d, N, K, ksplit, tiles, heads, hd, CS, C, E, FD;
-  float dt;
-  int has_next;
-  float* z;                     // [KD][d] fp32 (fp16-valued)
-  h16* z_out;                   // [KD][d] fp16 (last step)
-  float* partials;              // [units][256]
-  unsigned* tile_ctr;           // [nex * nl * tiles]
-  unsigned* head_ctr;           // [nex * heads]
-  const h16* ctx;               // [C][d]
+struct GemvArgs {
+  GemvEx ex[4];
+  int nex, nl, ks, tiles, N, K, E;
+  long long wstride, vstride;   // bytes between consecutive layers (packed weights / vectors)
 };
 
-// ---------------------------------------------------------------------------- attention
-// One wave computes softmax(q k^T / sqrt(hd) [+ causal]) v for one head: rows Sq queries, Sk keys.
-// Lane owns head dims [lane*dpl, lane*dpl + dpl).  Scores are reduced across the wave.
-__device__ void wave_attention(const h16* q, int ldq, const h16* k, int ldk, const h16* v, int ldv,
-                               int Sq, int Sk, bool causal, int hd, h16* out, int ldo) {
-  const int lane = threadIdx.x & 63;
-  const int dpl = hd / 64;
-  const int c0 = lane * dpl;
-  const float scale = 1.0f / sqrtf((float)hd);
-  for (int i = 0; i < Sq; ++i) {
-    const int nk = causal ? i + 1 : Sk;
-    float sc[MAXR];
-    float m = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < MAXR; ++j) {
-      sc[j] = -INFINITY;
-      if (j < nk) {
-        float p = 0.f;
-        for (int t = 0; t < dpl; ++t) p += (float)q[i * ldq + c0 + t] * (float)k[j * ldk + c0 + t];
-        const float s = wave_sum(p) * scale;
-        sc[j] = s;
-        m = fmaxf(m, s);
-      }
-    }
-    float den = 0.f;
-#pragma unroll
-    for (int j = 0; j < MAXR; ++j) {
-      const float e = (j < nk) ? expf(sc[j] - m) : 0.f;
-      sc[j] = e;
-      den += e;
-    }
-    const float inv = 1.0f / den;
-    for (int t = 0; t < dpl; ++t) {
-      float o = 0.f;
-#pragma unroll
-      for (int j = 0; j < MAXR; ++j)
-        if (j < nk) o += sc[j] * inv * (float)v[j * ldv + c0 + t];
-      out[i * ldo + c0 + t] = (h16)o;
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------- A staging
-__device__ __forceinline__ void ln_moments(const float* st, int row, int d, float& mean, float& rstd) {
-  const float s = st[row * 2], q = st[row * 2 + 1];
-  mean = s / (float)d;
-  const float var = fmaxf(q / (float)d - mean * mean, 0.f);
-  rstd = 1.0f / sqrtf(var + LN_EPS);
-}
-
-template <int KIND>
-__device__ void stage_A(const PhaseArgs& a, const PhaseEx& ep, int l, int kc, h16* As, int lda) {
-  __shared__ float sm_mean[MAXR], sm_rstd[MAXR];
-  const int KC = a.K / a.ksplit;
+template <int SRC>
+__device__ void stage_A(const GemvArgs& a, const GemvEx& ep, int l, int kc, h16* As, int lda) {
+  const int KC = a.K / a.ks;
   const int k0 = kc * KC;
   const int rows = ep.rows;
   const int nvec = KC / 8;
-  if constexpr (KIND == K_QKV || KIND == K_QC || KIND == K_W1 || KIND == K_OUT) {
-    if (threadIdx.x < rows) {
-      float mu, rs;
-      ln_moments(ep.st_in, ep.row0 + threadIdx.x, a.d, mu, rs);
-      sm_mean[threadIdx.x] = mu;
-      sm_rstd[threadIdx.x] = rs;
-    }
-    __syncthreads();
+  if constexpr (SRC == SRC_BUF) {
     for (int idx = threadIdx.x; idx < rows * nvec; idx += blockDim.x) {
       const int i = idx / nvec, kk = (idx - i * nvec) * 8;
-      const h16x8 xv = *(const h16x8*)(ep.x16 + (size_t)(ep.row0 + i) * a.d + k0 + kk);
-      const h16x8 gv = *(const h16x8*)(ep.lng + k0 + kk);
-      const h16x8 bv = *(const h16x8*)(ep.lnb + k0 + kk);
-      const float mu = sm_mean[i], rs = sm_rstd[i];
-      h16x8 o;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = (h16)(((float)xv[e] - mu) * rs * (float)gv[e] + (float)bv[e]);
-      *(h16x8*)(As + i * lda + kk) = o;
+      *(h16x8*)(As + i * lda + kk) = *(const h16x8*)(ep.a + (size_t)i * ep.lda + k0 + kk);
     }
-  } else if constexpr (KIND == K_O || KIND == K_OC || KIND == K_W2) {
-    const h16* src = (KIND == K_W2) ? ep.g : ep.attn;
-    const int ld = (KIND == K_W2) ? a.FD : a.d;
+  } else if constexpr (SRC == SRC_CTX) {
+    // context_norm(ctx) of layer l; the row moments (mean, rstd) come precomputed in ep.mom
+    const h16* gw = (const h16*)((const char*)ep.g0 + (size_t)l * a.vstride);
+    const h16* gb = (const h16*)((const char*)ep.b0 + (size_t)l * a.vstride);
     for (int idx = threadIdx.x; idx < rows * nvec; idx += blockDim.x) {
       const int i = idx / nvec, kk = (idx - i * nvec) * 8;
-      *(h16x8*)(As + i * lda + kk) = *(const h16x8*)(src + (size_t)i * ld + k0 + kk);
-    }
-  } else if constexpr (KIND == K_KV) {
-    // context_norm(ctx) of block l: moments of the fp16 context rows computed here (two-pass).
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (int i = wave; i < rows; i += blockDim.x / 64) {
-      const h16* cr = a.ctx + (size_t)i * a.d;
-      float s = 0.f;
-      for (int c = lane; c < a.d; c += 64) s += (float)cr[c];
-      s = wave_sum(s);
-      const float mu = s / (float)a.d;
-      float q = 0.f;
-      for (int c = lane; c < a.d; c += 64) {
-        const float t = (float)cr[c] - mu;
-        q += t * t;
-      }
-      q = wave_sum(q);
-      if (lane == 0) {
-        sm_mean[i] = mu;
-        sm_rstd[i] = 1.0f / sqrtf(q / (float)a.d + LN_EPS);
-      }
-    }
-    __syncthreads();
-    const h16* gw = (const h16*)((const char*)ep.lng + (size_t)l * a.vstride);
-    const h16* gb = (const h16*)((const char*)ep.lnb + (size_t)l * a.vstride);
-    for (int idx = threadIdx.x; idx < rows * nvec; idx += blockDim.x) {
-      const int i = idx / nvec, kk = (idx - i * nvec) * 8;
-      const h16x8 xv = *(const h16x8*)(a.ctx + (size_t)i * a.d + k0 + kk);
+      const h16x8 xv = *(const h16x8*)(ep.a + (size_t)i * a.K + k0 + kk);
       const h16x8 gv = *(const h16x8*)(gw + k0 + kk);
       const h16x8 bv = *(const h16x8*)(gb + k0 + kk);
-      const float mu = sm_mean[i], rs = sm_rstd[i];
+      const float mu = ep.mom[2 * i], rs = ep.mom[2 * i + 1];
       h16x8 o;
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = (h16)(((float)xv[e] - mu) * rs * (float)gv[e] + (float)bv[e]);
       *(h16x8*)(As + i * lda + kk) = o;
     }
-  } else if constexpr (KIND == K_TAU) {
+  } else if constexpr (SRC == SRC_TAU) {
     // rows = Euler steps: a_s = fp16(silu(fp16(tau_s * w0 + b0))), tau_s = fp16(s / E)
     for (int idx = threadIdx.x; idx < rows * nvec; idx += blockDim.x) {
       const int i = idx / nvec, kk = (idx - i * nvec) * 8;
@@ -207,7 +102,7 @@ __device__ void stage_A(const PhaseArgs& a, const PhaseEx& ep, int l, int kc, h1
       h16x8 o;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float h = r16(tau * (float)ep.lng[k0 + kk + e] + (float)ep.lnb[k0 + kk + e]);
+        const float h = r16(tau * (float)ep.g0[k0 + kk + e] + (float)ep.b0[k0 + kk + e]);
         o[e] = (h16)silu(h);
       }
       *(h16x8*)(As + i * lda + kk) = o;
@@ -216,329 +111,557 @@ __device__ void stage_A(const PhaseArgs& a, const PhaseEx& ep, int l, int kc, h1
   __syncthreads();
 }
 
-// Sum the 16 lanes of a 16-lane group (lanes sharing lane>>4).
-__device__ __forceinline__ float group16_sum(float v) {
-  v += __shfl_xor(v, 1);
-  v += __shfl_xor(v, 2);
-  v += __shfl_xor(v, 4);
-  v += __shfl_xor(v, 8);
-  return v;
-}
-
-// Residual update of one (row, col) value with LayerNorm-moment accumulation.
-__device__ __forceinline__ void moments_add(float* st, int row, bool valid, float xv16) {
-  float s1 = valid ? xv16 : 0.f, s2 = valid ? xv16 * xv16 : 0.f;
-  s1 = group16_sum(s1);
-  s2 = group16_sum(s2);
-  if (valid && (threadIdx.x & 15) == 0) {
-    atomicAdd(st + row * 2, s1);
-    atomicAdd(st + row * 2 + 1, s2);
-  }
-}
-
-// ---------------------------------------------------------------------------- phase kernel
-template <int KIND>
-__global__ void __launch_bounds__(WPB * 64) k_phase(PhaseArgs a) {
+template <int SRC>
+__global__ void __launch_bounds__(WPB * 64) k_gemv(GemvArgs a) {
   extern __shared__ __align__(16) h16 As[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int per_ex = a.nl * a.ksplit * a.tiles;
-  const int u = blockIdx.x * WPB + wave;
+  const int per_ex = a.nl * a.ks * a.tiles;
   const int u0 = blockIdx.x * WPB;
   const int e = u0 / per_ex;
   int rem = u0 - e * per_ex;
-  const int l = rem / (a.ksplit * a.tiles);
-  rem -= l * a.ksplit * a.tiles;
+  const int l = rem / (a.ks * a.tiles);
+  rem -= l * a.ks * a.tiles;
   const int kc = rem / a.tiles;
-  const int t = (u - u0) + (rem - kc * a.tiles);  // tile of this wave (WG never straddles (e,l,kc))
-  const PhaseEx& ep = a.ex[e];
-  const int KC = a.K / a.ksplit;
+  const int t = wave + (rem - kc * a.tiles);   // a workgroup never straddles (e, l, kc)
+  const GemvEx& ep = a.ex[e];
+  const int KC = a.K / a.ks;
   const int lda = KC + 8;
 
-  stage_A<KIND>(a, ep, l, kc, As, lda);
-
+  // The weight stream does not depend on the activations: put its first PF fragment loads in
+  // flight before staging the activation chunk.
   const h16x8* wbase = (const h16x8*)((const char*)ep.w + (size_t)l * a.wstride);
-  const h16x8* wp = wbase + packed_index(t, kc * (KC / 32), a.K, 0);
+  TileStream<PF> ts;
+  ts.begin(wbase + packed_index(t, kc * (KC / 32), a.K, 0), KC / 32);
+  stage_A<SRC>(a, ep, l, kc, As, lda);
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  acc = stream_tile<PF>(wp, As, lda, ep.rows, KC / 32, acc);
+  acc = ts.run(As, lda, ep.rows, acc);
 
-  const int col = lane & 15;
-  const int rbase = 4 * (lane >> 4);
-  if (a.ksplit > 1) {
-    const size_t tix = ((size_t)e * a.nl + l) * a.tiles + t;
-    float* pp = a.partials + tix * a.ksplit * 256;
+  const int col = lane & 15, rbase = 4 * (lane >> 4);
+  float* po = ep.pout + ((size_t)(l * a.ks + kc) * ep.rows) * a.N + t * 16 + col;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (rbase + j < ep.rows) pp[kc * 256 + (rbase + j) * 16 + col] = acc[j];
-    const unsigned old = arrive_count(a.tile_ctr + tix);
-    if (old != (unsigned)(a.ksplit - 1)) return;
-    acquire_fence();
-    reset_count(a.tile_ctr + tix);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float s = 0.f;
-      if (rbase + j < ep.rows)
-        for (int q = 0; q < a.ksplit; ++q) s += pp[q * 256 + (rbase + j) * 16 + col];
-      acc[j] = s;
+  for (int j = 0; j < 4; ++j)
+    if (rbase + j < ep.rows) po[(size_t)(rbase + j) * a.N] = acc[j];
+}
+
+// ---------------------------------------------------------------------------- partial reduce
+// out = fp16(sum_kc P[kc] + b), used for the per-draft cross K/V and time embeddings.
+struct ReduceArgs {
+  const float* P[4];
+  const h16* b[4];
+  h16* out[4];
+  int nex, nl, ks, rows, N, d, kv;   // kv: N = 2d split into [2][rows][d] per layer
+  long long vstride;
+};
+
+__global__ void __launch_bounds__(256) k_reduce(ReduceArgs a) {
+  const size_t per_l = (size_t)a.rows * a.N;
+  const size_t per_e = per_l * a.nl;
+  const size_t total = per_e * a.nex;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    const int e = (int)(i / per_e);
+    size_t r = i - e * per_e;
+    const int l = (int)(r / per_l);
+    r -= (size_t)l * per_l;
+    const int row = (int)(r / a.N), n = (int)(r - (size_t)row * a.N);
+    const float* P = a.P[e] + (size_t)l * a.ks * per_l + (size_t)row * a.N + n;
+    float s = 0.f;
+    for (int q = 0; q < a.ks; ++q) s += P[(size_t)q * per_l];
+    const h16* b = (const h16*)((const char*)a.b[e] + (size_t)l * a.vstride);
+    const float v = s + (float)b[n];
+    size_t o;
+    if (a.kv) {
+      const int part = n / a.d, nn = n - part * a.d;
+      o = (((size_t)l * 2 + part) * a.rows + row) * a.d + nn;
+    } else {
+      o = ((size_t)l * a.rows + row) * a.N + n;
+    }
+    a.out[e][o] = (h16)v;
+  }
+}
+
+// ---------------------------------------------------------------------------- attention
+// One workgroup per (expert, head): softmax(q k^T / sqrt(hd) [+ causal mask]) v for <= 16 query
+// rows and <= 16 keys.  q (and k, v for self attention) are reduced from the projection's fp32
+// partials and rounded to fp16 as the reference materialises them; cross attention reads the
+// hoisted fp16 context K/V.  Causal mask = triu(-inf, 1) (cf/drafters/chunked_flow.py:273-275).
+struct AttnArgs {
+  const float* P[4];   // projection partials [ks][Sq][ldp]
+  const h16* bias[4];  // in_proj_bias (q at 0, k at d, v at 2d)
+  const h16* kv[4];    // cross: [2][Sk][d] of this block (null for self attention)
+  h16* out[4];         // [Sq][d]
+  int Sq[4], Sk[4];
+  int ks, ldp, d, heads, hd, causal;
+};
+
+__global__ void __launch_bounds__(1024) k_attn(AttnArgs a) {
+  extern __shared__ __align__(16) h16 sm[];
+  __shared__ float P[MAXR][MAXR + 1];
+  const int e = blockIdx.x / a.heads, h = blockIdx.x - e * a.heads;
+  const int Sq = a.Sq[e], Sk = a.Sk[e], hd = a.hd, d = a.d;
+  const int c0 = h * hd;
+  h16* sq = sm;
+  h16* sk = sm + (size_t)Sq * hd;
+  h16* sv = sk + (size_t)Sk * hd;
+  const size_t pstride = (size_t)Sq * a.ldp;
+  // q (and k, v) = fp16(sum of partials + bias), four columns per thread-step
+  const int nsrc = a.kv[e] ? 1 : 3;
+  const int hq = hd / 4;
+  for (int idx = threadIdx.x; idx < nsrc * Sq * hq; idx += blockDim.x) {
+    const int part = idx / (Sq * hq);
+    const int r = idx - part * Sq * hq;
+    const int i = r / hq, c = (r - i * hq) * 4;
+    const int col = part * d + c0 + c;
+    const float* Pp = a.P[e] + (size_t)i * a.ldp + col;
+    float4 s4 = *(const float4*)Pp;
+    for (int q = 1; q < a.ks; ++q) {
+      const float4 t = *(const float4*)(Pp + q * pstride);
+      s4.x += t.x; s4.y += t.y; s4.z += t.z; s4.w += t.w;
+    }
+    const h16* bb = a.bias[e] + col;
+    h16* dst = (part == 0 ? sq : (part == 1 ? sk : sv)) + i * hd + c;
+    dst[0] = (h16)(s4.x + (float)bb[0]);
+    dst[1] = (h16)(s4.y + (float)bb[1]);
+    dst[2] = (h16)(s4.z + (float)bb[2]);
+    dst[3] = (h16)(s4.w + (float)bb[3]);
+  }
+  if (a.kv[e]) {
+    const int nv = hd / 8;
+    for (int idx = threadIdx.x; idx < Sk * nv; idx += blockDim.x) {
+      const int j = idx / nv, c = (idx - j * nv) * 8;
+      *(h16x8*)(sk + j * hd + c) = *(const h16x8*)(a.kv[e] + (size_t)j * d + c0 + c);
+      *(h16x8*)(sv + j * hd + c) = *(const h16x8*)(a.kv[e] + (size_t)(Sk + j) * d + c0 + c);
     }
   }
+  __syncthreads();
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+  const float scale = 1.0f / sqrtf((float)hd);
+  for (int pr = wave; pr < Sq * Sk; pr += nw) {
+    const int i = pr / Sk, j = pr - i * Sk;
+    float part = 0.f;
+    for (int c = lane * 8; c < hd; c += 512) {
+      const h16x8 qa = *(const h16x8*)(sq + i * hd + c);
+      const h16x8 kb = *(const h16x8*)(sk + j * hd + c);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) part += (float)qa[t] * (float)kb[t];
+    }
+    const float s = wave_sum(part) * scale;
+    if (lane == 0) P[i][j] = (a.causal && j > i) ? -INFINITY : s;
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < Sq) {
+    const int i = threadIdx.x;
+    float m = -INFINITY;
+    for (int j = 0; j < Sk; ++j) m = fmaxf(m, P[i][j]);
+    float den = 0.f;
+    for (int j = 0; j < Sk; ++j) {
+      const float ex = expf(P[i][j] - m);
+      P[i][j] = ex;
+      den += ex;
+    }
+    const float inv = 1.0f / den;
+    for (int j = 0; j < Sk; ++j) P[i][j] *= inv;
+  }
+  __syncthreads();
+  const int nv = hd / 8;
+  for (int idx = threadIdx.x; idx < Sq * nv; idx += blockDim.x) {
+    const int i = idx / nv, c = (idx - i * nv) * 8;
+    float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int j = 0; j < Sk; ++j) {
+      const float p = P[i][j];
+      const h16x8 vb = *(const h16x8*)(sv + j * hd + c);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) o[t] += p * (float)vb[t];
+    }
+    h16x8 ov;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) ov[t] = (h16)o[t];
+    *(h16x8*)(a.out[e] + (size_t)i * d + c0 + c) = ov;
+  }
+}
 
-  const int n = t * 16 + col;
-  const h16* bias = (const h16*)((const char*)ep.bias + (size_t)l * a.vstride);
-  const float bn = (float)bias[n];
-  if constexpr (KIND == K_QKV || KIND == K_QC) {
-    const int ld = 3 * a.d;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (rbase + j < ep.rows) ep.qkv[(size_t)(rbase + j) * ld + n] = (h16)(acc[j] + bn);
-    const int h = (n % a.d) / a.hd;
-    const unsigned total = (KIND == K_QKV) ? 3u * (unsigned)(a.hd / 16) : (unsigned)(a.hd / 16);
-    unsigned* hc = a.head_ctr + e * a.heads + h;
-    const unsigned old = arrive_count(hc);
-    if (old != total - 1) return;
-    acquire_fence();
-    reset_count(hc);
-    const int c0 = h * a.hd;
-    if constexpr (KIND == K_QKV) {
-      wave_attention(ep.qkv + c0, ld, ep.qkv + a.d + c0, ld, ep.qkv + 2 * a.d + c0, ld, ep.rows, ep.rows,
-                     true, a.hd, ep.attn + c0, a.d);
-    } else {
-      wave_attention(ep.qkv + c0, ld, ep.kv + c0, a.d, ep.kv + (size_t)a.C * a.d + c0, a.d, ep.rows, a.C,
-                     false, a.hd, ep.attn + c0, a.d);
+// ---------------------------------------------------------------------------- GELU
+// g = fp16(gelu(sum_kc P[kc] + b1)) for every row of every expert.
+struct GeluArgs {
+  const float* P[4];
+  const h16* b[4];
+  h16* g[4];
+  int rows[4];
+  int nex, ks, N;
+};
+
+__global__ void __launch_bounds__(256) k_gelu(GeluArgs a) {
+  size_t total = 0;
+  for (int e = 0; e < a.nex; ++e) total += (size_t)a.rows[e] * a.N / 4;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    int e = 0;
+    size_t j = i;
+    while (j >= (size_t)a.rows[e] * a.N / 4) j -= (size_t)a.rows[e++] * a.N / 4;
+    const size_t per_kc = (size_t)a.rows[e] * a.N;
+    const float* P = a.P[e] + j * 4;
+    float4 s4 = *(const float4*)P;
+    for (int q = 1; q < a.ks; ++q) {
+      const float4 t = *(const float4*)(P + q * per_kc);
+      s4.x += t.x; s4.y += t.y; s4.z += t.z; s4.w += t.w;
     }
-  } else if constexpr (KIND == K_O || KIND == K_OC || KIND == K_W2) {
+    const int n = (int)((j * 4) % a.N);
+    const h16* bb = a.b[e] + n;
+    h16* g = a.g[e] + j * 4;
+    g[0] = (h16)gelu_erf(s4.x + (float)bb[0]);
+    g[1] = (h16)gelu_erf(s4.y + (float)bb[1]);
+    g[2] = (h16)gelu_erf(s4.z + (float)bb[2]);
+    g[3] = (h16)gelu_erf(s4.w + (float)bb[3]);
+  }
+}
+
+// ---------------------------------------------------------------------------- row kernels
+// Block-wide sum over the workgroup.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t += red[w];
+  return t;
+}
+
+// LayerNorm of one row held as fp16-valued floats: thread t owns the float4 column groups
+// t, t + blockDim, ... (vals[k] = group k); two-pass moments; fp16 output.
+constexpr int ROWQ = ROWE / 4;   // float4 groups per thread
+
+__device__ void ln_row4(const float4* vals, int d, const h16* g, const h16* b, h16* out, float* red) {
+  const int nq = d / 4;
+  float s = 0.f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = rbase + j;
-      const bool valid = row < ep.rows;
-      float x16v = 0.f;
-      if (valid) {
-        const size_t ix = (size_t)row * a.d + n;
-        const float xn = ep.x[ix] + (acc[j] + bn);
-        ep.x[ix] = xn;
-        x16v = r16(xn);
-        ep.x16[ix] = (h16)x16v;
-      }
-      moments_add(ep.st_out, row, valid, x16v);
+  for (int k = 0; k < ROWQ; ++k) {
+    const int q = threadIdx.x + k * blockDim.x;
+    if (q < nq) s += (vals[k].x + vals[k].y) + (vals[k].z + vals[k].w);
+  }
+  const float mean = block_sum(s, red) / (float)d;
+  float v = 0.f;
+#pragma unroll
+  for (int k = 0; k < ROWQ; ++k) {
+    const int q = threadIdx.x + k * blockDim.x;
+    if (q < nq) {
+      const float a0 = vals[k].x - mean, a1 = vals[k].y - mean, a2 = vals[k].z - mean, a3 = vals[k].w - mean;
+      v += (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
     }
-  } else if constexpr (KIND == K_W1) {
+  }
+  const float rstd = 1.0f / sqrtf(block_sum(v, red) / (float)d + LN_EPS);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (rbase + j < ep.rows) ep.g[(size_t)(rbase + j) * a.FD + n] = (h16)gelu_erf(acc[j] + bn);
-  } else if constexpr (KIND == K_KV) {
-    // output n < d -> K, else V; layout [L][2][C][d]
-    const int part = n / a.d, nn = n - part * a.d;
-    h16* o = ep.out + (((size_t)l * 2 + part) * a.C) * a.d;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (rbase + j < ep.rows) o[(size_t)(rbase + j) * a.d + nn] = (h16)(acc[j] + bn);
-  } else if constexpr (KIND == K_TAU) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (rbase + j < ep.rows) ep.out[(size_t)(rbase + j) * a.d + n] = (h16)(acc[j] + bn);
-  } else if constexpr (KIND == K_OUT) {
-    // v = fp16(out_proj(out_norm(x_cur))); z = fp16(z + fp16(dt v)); then the next step's
-    // pre_blocks rows fed by this z row: fp16(fp16(z + pos[row]) + [current rows] tau_next).
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i = rbase + j;
-      const bool valid = i < ep.rows;
-      const int zr = e * a.CS + i;
-      float zn = 0.f;
-      if (valid) {
-        const float v16 = r16(acc[j] + bn);
-        zn = r16(a.z[(size_t)zr * a.d + n] + r16(a.dt * v16));
-        a.z[(size_t)zr * a.d + n] = zn;
-        if (!a.has_next) a.z_out[(size_t)zr * a.d + n] = (h16)zn;
-      }
-      if (a.has_next) {
-        for (int c2 = 0; c2 < a.nex; ++c2) {
-          const PhaseEx& e2 = a.ex[c2];
-          const bool use = valid && zr < e2.srows;
-          float xv = 0.f;
-          if (use) {
-            xv = r16(zn + (float)e2.pos[(size_t)zr * a.d + n]);
-            if (zr >= c2 * a.CS) xv = r16(xv + (float)e2.tau_next[n]);
-            e2.x_next[(size_t)zr * a.d + n] = xv;
-            e2.x16_next[(size_t)zr * a.d + n] = (h16)xv;
-          }
-          // moments: every lane of the wave takes part in the shuffles
-          float s1 = use ? xv : 0.f, s2 = use ? xv * xv : 0.f;
-          s1 = group16_sum(s1);
-          s2 = group16_sum(s2);
-          if (use && (lane & 15) == 0) {
-            atomicAdd(e2.st_next + zr * 2, s1);
-            atomicAdd(e2.st_next + zr * 2 + 1, s2);
-          }
-        }
-      }
+  for (int k = 0; k < ROWQ; ++k) {
+    const int q = threadIdx.x + k * blockDim.x;
+    if (q < nq) {
+      const int c = q * 4;
+      out[c + 0] = (h16)((vals[k].x - mean) * rstd * (float)g[c + 0] + (float)b[c + 0]);
+      out[c + 1] = (h16)((vals[k].y - mean) * rstd * (float)g[c + 1] + (float)b[c + 1]);
+      out[c + 2] = (h16)((vals[k].z - mean) * rstd * (float)g[c + 2] + (float)b[c + 2]);
+      out[c + 3] = (h16)((vals[k].w - mean) * rstd * (float)g[c + 3] + (float)b[c + 3]);
     }
   }
 }
 
-// ---------------------------------------------------------------------------- init kernel
-// One workgroup per z row r: z0[r] = init_latents(ctx) (delta mode, fp16 arithmetic as in the
-// expert dtype), then the step-0 pre_blocks rows of every expert that reads z row r, with their
-// full-row LayerNorm moments.  Workgroups also clear the counters and the moment buffers of all
-// later generations.
-struct InitArgs {
-  const h16* ctx;     // [C][d]
-  float* z;           // [KD][d]
-  int d, C, KD, CS, nch, init_mode;
+__device__ __forceinline__ float4 r16x4(float4 v) { return make_float4(r16(v.x), r16(v.y), r16(v.z), r16(v.w)); }
+
+// NORM: x[r] += sum_kc P[kc][r] + bias; a[r] = fp16(LN(fp16(x[r]))).  One workgroup per row.
+struct NormArgs {
   float* x[4];
-  h16* x16[4];
-  float* st0[4];      // generation-0 moments per expert [MAXR][2]
-  const h16* pos[4];
-  const h16* tau0[4]; // time_mlp(tau_0) per expert
-  int srows[4];
-  float* zero_f; size_t nzero_f;      // later-generation moments
-  unsigned* zero_u; size_t nzero_u;   // counters
+  const float* P[4];
+  const h16* bias[4];
+  const h16* g[4];
+  const h16* b[4];
+  h16* a[4];
+  int rows[4];
+  int nex, ks, d;
 };
 
-__global__ void __launch_bounds__(256) k_flow_init(InitArgs a) {
-  const int r = blockIdx.x;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.nzero_f; i += (size_t)gridDim.x * blockDim.x)
-    a.zero_f[i] = 0.f;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.nzero_u; i += (size_t)gridDim.x * blockDim.x)
-    a.zero_u[i] = 0u;
-  __shared__ float red[2][4][8];
-  const h16* last = a.ctx + (size_t)(a.C - 1) * a.d;
-  const h16* prev = a.ctx + (size_t)(a.C - 2) * a.d;
-  const float step = (float)(r + 1);
-  float s1[4] = {0, 0, 0, 0}, s2[4] = {0, 0, 0, 0};
-  for (int c = threadIdx.x; c < a.d; c += blockDim.x) {
-    const float lv = (float)last[c];
-    float z0;
-    if (a.init_mode == 1) {
-      z0 = lv;  // repeat_last
-    } else {
-      const float delta = r16(lv - (float)prev[c]);
-      z0 = r16(lv + r16(step * delta));
-    }
-    a.z[(size_t)r * a.d + c] = z0;
+__global__ void __launch_bounds__(ROWT) k_norm(NormArgs a) {
+  __shared__ float red[ROWT / 64];
+  int e = 0, r = blockIdx.x;
+  while (e + 1 < a.nex && r >= a.rows[e]) r -= a.rows[e++];
+  const int d = a.d, nq = d / 4;
+  const size_t pst = (size_t)a.rows[e] * d;
+  float* xr = a.x[e] + (size_t)r * d;
+  const float* Pr = a.P[e] + (size_t)r * d;
+  float4 acc[ROWQ], xv[ROWQ];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if (e >= a.nch || r >= a.srows[e]) continue;
-      float xv = r16(z0 + (float)a.pos[e][(size_t)r * a.d + c]);
-      if (r >= e * a.CS) xv = r16(xv + (float)a.tau0[e][c]);
-      a.x[e][(size_t)r * a.d + c] = xv;
-      a.x16[e][(size_t)r * a.d + c] = (h16)xv;
-      s1[e] += xv;
-      s2[e] += xv * xv;
+  for (int k = 0; k < ROWQ; ++k) {
+    const int q = threadIdx.x + k * blockDim.x;
+    if (q < nq) {
+      xv[k] = *(const float4*)(xr + q * 4);
+      acc[k] = *(const float4*)(Pr + q * 4);
     }
   }
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll 4
+  for (int kc = 1; kc < a.ks; ++kc) {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float t1 = wave_sum(s1[e]), t2 = wave_sum(s2[e]);
-    if (lane == 0) {
-      red[0][e][wave] = t1;
-      red[1][e][wave] = t2;
-    }
-  }
-  __syncthreads();
-  if (threadIdx.x < a.nch) {
-    const int e = threadIdx.x;
-    if (r < a.srows[e]) {
-      float t1 = 0.f, t2 = 0.f;
-      for (int w = 0; w < (int)(blockDim.x >> 6); ++w) {
-        t1 += red[0][e][w];
-        t2 += red[1][e][w];
+    for (int k = 0; k < ROWQ; ++k) {
+      const int q = threadIdx.x + k * blockDim.x;
+      if (q < nq) {
+        const float4 t = *(const float4*)(Pr + kc * pst + q * 4);
+        acc[k].x += t.x; acc[k].y += t.y; acc[k].z += t.z; acc[k].w += t.w;
       }
-      a.st0[e][r * 2] = t1;
-      a.st0[e][r * 2 + 1] = t2;
     }
+  }
+  float4 vals[ROWQ];
+#pragma unroll
+  for (int k = 0; k < ROWQ; ++k) {
+    const int q = threadIdx.x + k * blockDim.x;
+    vals[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (q < nq) {
+      const h16* bb = a.bias[e] + q * 4;
+      float4 xn;
+      xn.x = xv[k].x + (acc[k].x + (float)bb[0]);
+      xn.y = xv[k].y + (acc[k].y + (float)bb[1]);
+      xn.z = xv[k].z + (acc[k].z + (float)bb[2]);
+      xn.w = xv[k].w + (acc[k].w + (float)bb[3]);
+      *(float4*)(xr + q * 4) = xn;
+      vals[k] = r16x4(xn);
+    }
+  }
+  ln_row4(vals, d, a.g[e], a.b[e], a.a[e] + (size_t)r * d, red);
+}
+
+// ROWS: one workgroup per z row r.
+//   init  : z[r] = init_latents(ctx)[r] (delta mode, fp16 arithmetic)
+//   euler : v = fp16(sum_kc Pout[kc][i] + b_out) for the chunk c, row i owning z row r;
+//           z[r] = fp16(z[r] + fp16(dt v))   (z_out[r] = z[r] after the last step)
+// then, unless this was the last step, the next step's rows: for every expert c2 that reads z row
+// r: x = fp16(fp16(z + pos[r]) + [current rows] tau), residual x = that, a = LN_self of block 0.
+struct RowsArgs {
+  const h16* ctx;
+  float* ctx_mom;      // init: [C][2] (mean, rstd) of the fp16 context rows
+  float* z;
+  h16* z_out;
+  const float* Pout[4];
+  const h16* bout[4];
+  float* x[4];
+  const h16* pos[4];
+  const h16* tau[4];
+  const h16* g[4];
+  const h16* b[4];
+  h16* a[4];
+  float dt;
+  int euler, last, ks, d, C, CS, nch;
+};
+
+__global__ void __launch_bounds__(ROWT) k_rows(RowsArgs a) {
+  __shared__ float red[ROWT / 64];
+  const int r = blockIdx.x, d = a.d, nq = d / 4;
+  float4 zv[ROWQ];
+  if (!a.euler) {
+    // moments of context rows r, r + gridDim.x, ... (read by the cross K/V GEMV)
+    for (int cr = r; cr < a.C; cr += gridDim.x) {
+      const h16* row = a.ctx + (size_t)cr * d;
+      float sm = 0.f;
+      for (int c = threadIdx.x; c < d; c += blockDim.x) sm += (float)row[c];
+      const float mu = block_sum(sm, red) / (float)d;
+      float sq = 0.f;
+      for (int c = threadIdx.x; c < d; c += blockDim.x) {
+        const float t = (float)row[c] - mu;
+        sq += t * t;
+      }
+      const float rs = 1.0f / sqrtf(block_sum(sq, red) / (float)d + LN_EPS);
+      if (threadIdx.x == 0) {
+        a.ctx_mom[2 * cr] = mu;
+        a.ctx_mom[2 * cr + 1] = rs;
+      }
+    }
+    const h16* last = a.ctx + (size_t)(a.C - 1) * d;
+    const h16* prev = a.ctx + (size_t)(a.C - 2) * d;
+    const float step = (float)(r + 1);
+#pragma unroll
+    for (int k = 0; k < ROWQ; ++k) {
+      const int q = threadIdx.x + k * blockDim.x;
+      zv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (q < nq) {
+        float o[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float lv = (float)last[q * 4 + t];
+          const float delta = r16(lv - (float)prev[q * 4 + t]);
+          o[t] = r16(lv + r16(step * delta));
+        }
+        zv[k] = make_float4(o[0], o[1], o[2], o[3]);
+        *(float4*)(a.z + (size_t)r * d + q * 4) = zv[k];
+      }
+    }
+  } else {
+    const int c = r / a.CS, i = r - c * a.CS;
+    const size_t pst = (size_t)a.CS * d;
+    const float* Pr = a.Pout[c] + (size_t)i * d;
+    float4 acc[ROWQ], zo[ROWQ];
+#pragma unroll
+    for (int k = 0; k < ROWQ; ++k) {
+      const int q = threadIdx.x + k * blockDim.x;
+      if (q < nq) {
+        acc[k] = *(const float4*)(Pr + q * 4);
+        zo[k] = *(const float4*)(a.z + (size_t)r * d + q * 4);
+      }
+    }
+    for (int kc = 1; kc < a.ks; ++kc) {
+#pragma unroll
+      for (int k = 0; k < ROWQ; ++k) {
+        const int q = threadIdx.x + k * blockDim.x;
+        if (q < nq) {
+          const float4 t = *(const float4*)(Pr + kc * pst + q * 4);
+          acc[k].x += t.x; acc[k].y += t.y; acc[k].z += t.z; acc[k].w += t.w;
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < ROWQ; ++k) {
+      const int q = threadIdx.x + k * blockDim.x;
+      zv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (q < nq) {
+        const h16* bo = a.bout[c] + q * 4;
+        float4 zn;
+        zn.x = r16(zo[k].x + r16(a.dt * r16(acc[k].x + (float)bo[0])));
+        zn.y = r16(zo[k].y + r16(a.dt * r16(acc[k].y + (float)bo[1])));
+        zn.z = r16(zo[k].z + r16(a.dt * r16(acc[k].z + (float)bo[2])));
+        zn.w = r16(zo[k].w + r16(a.dt * r16(acc[k].w + (float)bo[3])));
+        *(float4*)(a.z + (size_t)r * d + q * 4) = zn;
+        if (a.last) {
+          h16* zo16 = a.z_out + (size_t)r * d + q * 4;
+          zo16[0] = (h16)zn.x; zo16[1] = (h16)zn.y; zo16[2] = (h16)zn.z; zo16[3] = (h16)zn.w;
+        }
+        zv[k] = zn;
+      }
+    }
+  }
+  if (a.last) return;
+  for (int c2 = 0; c2 < a.nch; ++c2) {
+    if (r >= (c2 + 1) * a.CS) continue;          // expert c2 reads z rows [0, (c2+1)*CS)
+    const bool cur = r >= c2 * a.CS;
+    float4 vals[ROWQ];
+#pragma unroll
+    for (int k = 0; k < ROWQ; ++k) {
+      const int q = threadIdx.x + k * blockDim.x;
+      vals[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (q < nq) {
+        const h16* pp = a.pos[c2] + (size_t)r * d + q * 4;
+        const h16* tt = a.tau[c2] + q * 4;
+        float o[4] = {zv[k].x, zv[k].y, zv[k].z, zv[k].w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          float xv = r16(o[t] + (float)pp[t]);
+          if (cur) xv = r16(xv + (float)tt[t]);
+          o[t] = xv;
+        }
+        vals[k] = make_float4(o[0], o[1], o[2], o[3]);
+        *(float4*)(a.x[c2] + (size_t)r * d + q * 4) = vals[k];
+      }
+    }
+    ln_row4(vals, d, a.g[c2], a.b[c2], a.a[c2] + (size_t)r * d, red);
   }
 }
 
 // ---------------------------------------------------------------------------- host side
-struct WS {
-  float* z;
-  float* x[4][2];
-  h16* x16[4][2];
-  h16* qkv[4];
-  h16* attn[4];
-  h16* g[4];
-  h16* tau[4];
-  h16* kvc[4];
-  float* stats;      // [ngen][nch][MAXR][2]
-  float* partials;
-  unsigned* tile_ctr;
-  unsigned* head_ctr;
-  size_t total, ngen, stats_floats, n_tile_ctr, n_head_ctr, partial_floats;
-};
-
-int ksplit_for(int nex_units, int tiles, int K, int rows) {
-  // smallest power of two giving >= 2048 wave units, an LDS A chunk <= 48 KiB and >= 4 k-steps
-  int ks = 1;
-  while (true) {
-    const int KC = K / ks;
-    const bool lds_ok = (size_t)rows * (KC + 8) * 2 <= 48 * 1024;
-    const bool units_ok = (long long)nex_units * tiles * ks >= 2048;
-    if (lds_ok && units_ok) break;
-    const int nks = ks * 2;
-    if (K % (nks * 32) != 0 || K / nks < 128) break;
-    ks = nks;
-  }
-  return ks;
-}
-
 size_t lds_bytes(int rows, int KC) { return (size_t)rows * (KC + 8) * 2; }
 
-WS carve(const cfh_flow_dims* dm, char* base) {
-  WS w;
-  const size_t d = dm->d, fd = (size_t)dm->ffn_mult * dm->d;
-  const int nch = dm->draft_length / dm->chunk_size;
+// Split-K factor: the smallest divisor ks of the k-step count such that every unit streams a
+// whole number of PF-step prefetch blocks, the A chunk fits in 48 KiB of LDS (two or three
+// workgroups per CU) and the phase has >= 2048 wave units; else the largest valid one.
+int ksplit_for(int nex_units, int tiles, int K, int rows) {
+  const int steps = K / 32;
+  int best = -1;
+  for (int ks = 1; ks <= steps; ++ks) {
+    if (steps % ks) continue;
+    if ((steps / ks) % PF) continue;
+    if (lds_bytes(rows, K / ks) > 48 * 1024) continue;
+    best = ks;
+    if ((long long)nex_units * tiles * ks >= 2048) break;
+  }
+  if (best > 0) return best;
+  for (int ks = 1; ks <= steps; ++ks)
+    if (steps % ks == 0 && lds_bytes(rows, K / ks) <= 48 * 1024) return ks;
+  return steps;
+}
+
+struct Plan {
+  int d, fd, CS, E, NL, C, KD, H, nch;
+  int ks_qkv, ks_o, ks_w1, ks_w2, ks_out, ks_kv, ks_tau;
+};
+
+Plan make_plan(const cfh_flow_dims* dm) {
+  Plan p;
+  p.d = dm->d; p.fd = dm->ffn_mult * dm->d; p.CS = dm->chunk_size; p.E = dm->flow_steps;
+  p.NL = dm->layers; p.C = dm->ctx_rows; p.KD = dm->draft_length; p.H = dm->heads;
+  p.nch = p.KD / p.CS;
+  p.ks_qkv = ksplit_for(p.nch, 3 * p.d / 16, p.d, p.KD);
+  p.ks_o = ksplit_for(p.nch, p.d / 16, p.d, p.KD);
+  p.ks_w1 = ksplit_for(p.nch, p.fd / 16, p.d, p.KD);
+  p.ks_w2 = ksplit_for(p.nch, p.d / 16, p.fd, p.KD);
+  p.ks_out = ksplit_for(p.nch, p.d / 16, p.d, p.CS);
+  p.ks_kv = ksplit_for(p.nch * p.NL, 2 * p.d / 16, p.d, p.C);
+  p.ks_tau = ksplit_for(p.nch, p.d / 16, p.d, p.E);
+  return p;
+}
+
+struct WS {
+  float* z;
+  float* x[4];
+  h16* abuf[4];
+  h16* attn[4];
+  h16* g[4];
+  float* P[4];        // partials of the current GEMV
+  float* Pw1[4];      // W1 partials (read by GELU)
+  h16* tau[4];        // [E][d]
+  h16* kvc[4];        // [L][2][C][d]
+  float* Pkv;         // [nch][L][ks][C][2d]
+  float* Ptau;        // [nch][ks][E][d]
+  float* ctx_mom;     // [C][2]
+  size_t total;
+};
+
+WS carve(const Plan& p, char* base) {
+  WS w = {};
   size_t off = 0;
   auto take = [&](size_t bytes) -> char* {
-    char* p = base ? base + off : nullptr;
+    char* q = base ? base + off : nullptr;
     off = cfh::align256(off + bytes);
-    return p;
+    return q;
   };
-  w.z = (float*)take(dm->draft_length * d * 4);
-  for (int c = 0; c < nch; ++c) {
-    const size_t S = (size_t)(c + 1) * dm->chunk_size;
-    for (int p = 0; p < 2; ++p) {
-      w.x[c][p] = (float*)take(S * d * 4);
-      w.x16[c][p] = (h16*)take(S * d * 2);
-    }
-    w.qkv[c] = (h16*)take(S * 3 * d * 2);
+  const size_t d = p.d, fd = p.fd;
+  w.z = (float*)take((size_t)p.KD * d * 4);
+  for (int c = 0; c < p.nch; ++c) {
+    const size_t S = (size_t)(c + 1) * p.CS;
+    w.x[c] = (float*)take(S * d * 4);
+    w.abuf[c] = (h16*)take(S * d * 2);
     w.attn[c] = (h16*)take(S * d * 2);
     w.g[c] = (h16*)take(S * fd * 2);
-    w.tau[c] = (h16*)take((size_t)dm->flow_steps * d * 2);
-    w.kvc[c] = (h16*)take((size_t)dm->layers * 2 * dm->ctx_rows * d * 2);
+    size_t pmax = (size_t)p.ks_qkv * S * 3 * d;
+    pmax = std::max(pmax, (size_t)p.ks_o * S * d);
+    pmax = std::max(pmax, (size_t)p.ks_w2 * S * d);
+    pmax = std::max(pmax, (size_t)p.ks_out * p.CS * d);
+    w.P[c] = (float*)take(pmax * 4);
+    w.Pw1[c] = (float*)take((size_t)p.ks_w1 * S * fd * 4);
+    w.tau[c] = (h16*)take((size_t)p.E * d * 2);
+    w.kvc[c] = (h16*)take((size_t)p.NL * 2 * p.C * d * 2);
   }
-  w.ngen = 1 + (size_t)dm->flow_steps * (3 * dm->layers + 1);
-  w.stats_floats = w.ngen * nch * MAXR * 2;
-  w.stats = (float*)take(w.stats_floats * 4);
-  // split-K partials and tile counters: launch_phase refuses a phase above MAX_UNITS per expert
-  w.partial_floats = (size_t)nch * MAX_UNITS * 256;
-  w.partials = (float*)take(w.partial_floats * 4);
-  w.n_tile_ctr = (size_t)nch * MAX_UNITS;
-  w.tile_ctr = (unsigned*)take(w.n_tile_ctr * 4);
-  w.n_head_ctr = (size_t)nch * dm->heads;
-  w.head_ctr = (unsigned*)take(w.n_head_ctr * 4);
+  w.Pkv = (float*)take((size_t)p.nch * p.NL * p.ks_kv * p.C * 2 * d * 4);
+  w.Ptau = (float*)take((size_t)p.nch * p.ks_tau * p.E * d * 4);
+  w.ctx_mom = (float*)take((size_t)p.C * 2 * 4);
   w.total = off;
   return w;
 }
 
-struct Ctx {
-  const cfh_flow_dims* dm;
-  cfh::ExpertLayout L;
-  const char* ex[4];
-  WS ws;
-  int nch, d, fd, CS;
-  hipStream_t st;
-};
-
-template <int KIND>
-int launch_phase(PhaseArgs& a, int rows_max, hipStream_t st) {
-  const int per_ex = a.nl * a.ksplit * a.tiles;
-  const int units = a.nex * per_ex;
+template <int SRC>
+int launch_gemv(const GemvArgs& a, int rows_max, hipStream_t st) {
   if (a.tiles % WPB != 0) return CFH_E_UNSUPPORTED;
-  if (a.ksplit > 1 && (size_t)a.nl * a.tiles * a.ksplit > (size_t)MAX_UNITS) return CFH_E_UNSUPPORTED;
-  const size_t lds = lds_bytes(rows_max, a.K / a.ksplit);
-  if (lds > 160 * 1024) return CFH_E_UNSUPPORTED;
-  hipLaunchKernelGGL(k_phase<KIND>, dim3(units / WPB), dim3(WPB * 64), lds, st, a);
+  const size_t lds = lds_bytes(rows_max, a.K / a.ks);
+  if (lds > 64 * 1024) return CFH_E_UNSUPPORTED;
+  const long long units = (long long)a.nex * a.nl * a.ks * a.tiles;
+  hipLaunchKernelGGL(k_gemv<SRC>, dim3((unsigned)(units / WPB)), dim3(WPB * 64), lds, st, a);
+  CFH_LAUNCH_CHECK();
+  return CFH_OK;
+}
+
+int launch_attn(const AttnArgs& a, int nex, int sq_max, int sk_max, hipStream_t st) {
+  const size_t lds = (size_t)(sq_max + 2 * sk_max) * a.hd * 2;
+  if (lds > 120 * 1024 || sq_max > MAXR || sk_max > MAXR) return CFH_E_UNSUPPORTED;
+  hipLaunchKernelGGL(k_attn, dim3(nex * a.heads), dim3(1024), lds, st, a);
   CFH_LAUNCH_CHECK();
   return CFH_OK;
 }
@@ -549,183 +672,214 @@ extern "C" {
 
 int cfh_caps(const cfh_flow_dims* dims, int batch, int64_t* ws_bytes) {
   if (!cfh::flow_dims_ok(dims) || batch < 1) return CFH_E_UNSUPPORTED;
-  const WS w = carve(dims, nullptr);
+  if (dims->d > ROWT * ROWE) return CFH_E_UNSUPPORTED;
+  const Plan p = make_plan(dims);
+  const WS w = carve(p, nullptr);
   if (ws_bytes) *ws_bytes = (int64_t)w.total;
   return CFH_OK;
 }
 
 int cfh_flow_integrate(const cfh_flow_dims* dm, const void* const* experts, const void* ctx, void* z_out,
                        void* ws_ptr, int batch, void* stream) {
-  if (!cfh::flow_dims_ok(dm)) return CFH_E_UNSUPPORTED;
+  if (!cfh::flow_dims_ok(dm) || dm->d > ROWT * ROWE) return CFH_E_UNSUPPORTED;
   if (!experts || !ctx || !z_out || !ws_ptr || batch < 1) return CFH_E_INVALID;
-  const int nch = dm->draft_length / dm->chunk_size;
-  for (int c = 0; c < nch; ++c)
+  const Plan p = make_plan(dm);
+  for (int c = 0; c < p.nch; ++c)
     if (!experts[c]) return CFH_E_INVALID;
   hipStream_t st = (hipStream_t)stream;
   const cfh::ExpertLayout L = cfh::expert_layout(dm);
-  const WS w = carve(dm, (char*)ws_ptr);
-  const int d = dm->d, fd = dm->ffn_mult * dm->d, CS = dm->chunk_size, E = dm->flow_steps,
-            NL = dm->layers, C = dm->ctx_rows, KD = dm->draft_length, H = dm->heads;
-  const size_t gen_stride = (size_t)nch * MAXR * 2;
-  auto stats_of = [&](size_t gen, int c) { return w.stats + gen * gen_stride + (size_t)c * MAXR * 2; };
-  auto P = [&](int c, size_t off) { return (const char*)experts[c] + off; };
+  const WS w = carve(p, (char*)ws_ptr);
+  const int d = p.d, fd = p.fd, CS = p.CS, E = p.E, NL = p.NL, C = p.C, KD = p.KD, H = p.H, nch = p.nch;
+  auto PTR = [&](int c, size_t off) { return (const char*)experts[c] + off; };
+  auto BLK = [&](int l) { return L.blk0 + (size_t)l * L.blkstride; };
+  auto S_of = [&](int c) { return (c + 1) * CS; };
+  int rc;
 
   for (int b = 0; b < batch; ++b) {
     const h16* ctx_b = (const h16*)ctx + (size_t)b * C * d;
     h16* zo_b = (h16*)z_out + (size_t)b * KD * d;
 
-    // ---- cross K/V (once per draft) and time embeddings (once per draft)
+    // ---- per draft: time embeddings of every step, z0 + step-0 rows, cross K/V of every block
     {
-      PhaseArgs a = {};
-      a.nex = nch;
-      a.nl = NL;
-      a.wstride = (long long)L.blkstride;
-      a.vstride = (long long)L.blkstride;
-      a.d = d; a.N = 2 * d; a.K = d; a.tiles = 2 * d / 16; a.heads = H; a.hd = d / H; a.CS = CS; a.C = C;
-      a.E = E; a.FD = fd; a.ctx = ctx_b;
-      a.ksplit = 1;
+      GemvArgs a = {};
+      a.nex = nch; a.nl = 1; a.ks = p.ks_tau; a.tiles = d / 16; a.N = d; a.K = d; a.E = E;
       for (int c = 0; c < nch; ++c) {
-        PhaseEx& x = a.ex[c];
-        x.w = (const h16x8*)P(c, L.blk0 + L.kv);
-        x.bias = (const h16*)P(c, L.blk0 + L.kv_b);
-        x.lng = (const h16*)P(c, L.blk0 + L.cn_w);
-        x.lnb = (const h16*)P(c, L.blk0 + L.cn_b);
-        x.out = w.kvc[c];
-        x.rows = C;
-      }
-      int rc = launch_phase<K_KV>(a, C, st);
-      if (rc) return rc;
-    }
-    {
-      PhaseArgs a = {};
-      a.nex = nch; a.nl = 1;
-      a.d = d; a.N = d; a.K = d; a.tiles = d / 16; a.heads = H; a.hd = d / H; a.CS = CS; a.C = C; a.E = E;
-      a.FD = fd;
-      a.ksplit = ksplit_for(nch, a.tiles, d, E);
-      a.partials = w.partials; a.tile_ctr = w.tile_ctr;
-      for (int c = 0; c < nch; ++c) {
-        PhaseEx& x = a.ex[c];
-        x.w = (const h16x8*)P(c, L.tw2);
-        x.bias = (const h16*)P(c, L.tb2);
-        x.lng = (const h16*)P(c, L.tw0);
-        x.lnb = (const h16*)P(c, L.tb0);
-        x.out = w.tau[c];
+        GemvEx& x = a.ex[c];
+        x.w = (const h16x8*)PTR(c, L.tw2);
+        x.g0 = (const h16*)PTR(c, L.tw0);
+        x.b0 = (const h16*)PTR(c, L.tb0);
+        x.pout = w.Ptau + (size_t)c * p.ks_tau * E * d;
         x.rows = E;
       }
-      // counters must be zero before the tau phase: init clears them, so run init first
-      InitArgs ia = {};
-      ia.ctx = ctx_b; ia.z = w.z; ia.d = d; ia.C = C; ia.KD = KD; ia.CS = CS; ia.nch = nch; ia.init_mode = 0;
+      if ((rc = launch_gemv<SRC_TAU>(a, E, st))) return rc;
+      ReduceArgs r = {};
+      r.nex = nch; r.nl = 1; r.ks = p.ks_tau; r.rows = E; r.N = d; r.d = d; r.kv = 0;
       for (int c = 0; c < nch; ++c) {
-        ia.x[c] = w.x[c][0]; ia.x16[c] = w.x16[c][0]; ia.st0[c] = stats_of(0, c);
-        ia.pos[c] = (const h16*)P(c, L.pos); ia.tau0[c] = w.tau[c]; ia.srows[c] = (c + 1) * CS;
+        r.P[c] = a.ex[c].pout;
+        r.b[c] = (const h16*)PTR(c, L.tb2);
+        r.out[c] = w.tau[c];
       }
-      ia.zero_f = w.stats + gen_stride;
-      ia.nzero_f = w.stats_floats - gen_stride;
-      ia.zero_u = w.tile_ctr;
-      ia.nzero_u = (size_t)((char*)(w.head_ctr + w.n_head_ctr) - (char*)w.tile_ctr) / 4;
-      // tau needs clean counters; init needs tau.  Clear counters with a zero-only init pass
-      // (no rows), run tau, then run the real init.
-      InitArgs zc = ia;
-      zc.nch = 0;
-      hipLaunchKernelGGL(k_flow_init, dim3(KD), dim3(256), 0, st, zc);
+      hipLaunchKernelGGL(k_reduce, dim3(256), dim3(256), 0, st, r);
       CFH_LAUNCH_CHECK();
-      int rc = launch_phase<K_TAU>(a, E, st);
-      if (rc) return rc;
-      ia.zero_f = nullptr; ia.nzero_f = 0; ia.zero_u = nullptr; ia.nzero_u = 0;
-      hipLaunchKernelGGL(k_flow_init, dim3(KD), dim3(256), 0, st, ia);
+    }
+    // ---- z0 and the step-0 rows
+    {
+      RowsArgs r = {};
+      r.ctx = ctx_b; r.ctx_mom = w.ctx_mom; r.z = w.z; r.z_out = zo_b; r.euler = 0; r.last = 0; r.d = d; r.C = C; r.CS = CS;
+      r.nch = nch;
+      for (int c = 0; c < nch; ++c) {
+        r.x[c] = w.x[c]; r.pos[c] = (const h16*)PTR(c, L.pos); r.tau[c] = w.tau[c];
+        r.g[c] = (const h16*)PTR(c, BLK(0) + L.sn_w); r.b[c] = (const h16*)PTR(c, BLK(0) + L.sn_b);
+        r.a[c] = w.abuf[c];
+      }
+      hipLaunchKernelGGL(k_rows, dim3(KD), dim3(ROWT), 0, st, r);
       CFH_LAUNCH_CHECK();
     }
 
-    // ---- Euler steps
-    size_t gen = 0;
+    {
+      GemvArgs a = {};
+      a.nex = nch; a.nl = NL; a.ks = p.ks_kv; a.tiles = 2 * d / 16; a.N = 2 * d; a.K = d; a.E = E;
+      a.wstride = (long long)L.blkstride; a.vstride = (long long)L.blkstride;
+      for (int c = 0; c < nch; ++c) {
+        GemvEx& x = a.ex[c];
+        x.w = (const h16x8*)PTR(c, BLK(0) + L.kv);
+        x.a = ctx_b;
+        x.g0 = (const h16*)PTR(c, BLK(0) + L.cn_w);
+        x.b0 = (const h16*)PTR(c, BLK(0) + L.cn_b);
+        x.pout = w.Pkv + (size_t)c * NL * p.ks_kv * C * 2 * d;
+        x.mom = w.ctx_mom;
+        x.rows = C;
+      }
+      if ((rc = launch_gemv<SRC_CTX>(a, C, st))) return rc;
+      ReduceArgs r = {};
+      r.nex = nch; r.nl = NL; r.ks = p.ks_kv; r.rows = C; r.N = 2 * d; r.d = d; r.kv = 1;
+      r.vstride = (long long)L.blkstride;
+      for (int c = 0; c < nch; ++c) {
+        r.P[c] = a.ex[c].pout;
+        r.b[c] = (const h16*)PTR(c, BLK(0) + L.kv_b);
+        r.out[c] = w.kvc[c];
+      }
+      hipLaunchKernelGGL(k_reduce, dim3(1024), dim3(256), 0, st, r);
+      CFH_LAUNCH_CHECK();
+    }
     for (int s = 0; s < E; ++s) {
       for (int l = 0; l < NL; ++l) {
-        const size_t B = L.blk0 + (size_t)l * L.blkstride;
-        PhaseArgs a = {};
-        a.nex = nch; a.nl = 1; a.d = d; a.heads = H; a.hd = d / H; a.CS = CS; a.C = C; a.E = E; a.FD = fd;
-        a.partials = w.partials; a.tile_ctr = w.tile_ctr; a.head_ctr = w.head_ctr;
+        const size_t B = BLK(l);
+        // ---- QKV
+        GemvArgs a = {};
+        a.nex = nch; a.nl = 1; a.E = E;
+        a.ks = p.ks_qkv; a.tiles = 3 * d / 16; a.N = 3 * d; a.K = d;
         for (int c = 0; c < nch; ++c) {
-          PhaseEx& x = a.ex[c];
-          x.x = w.x[c][s & 1]; x.x16 = w.x16[c][s & 1]; x.qkv = w.qkv[c]; x.attn = w.attn[c]; x.g = w.g[c];
-          x.kv = w.kvc[c] + (size_t)l * 2 * C * d;
-          x.rows = (c + 1) * CS; x.row0 = 0; x.srows = x.rows;
+          GemvEx& x = a.ex[c];
+          x.w = (const h16x8*)PTR(c, B + L.qkv); x.a = w.abuf[c]; x.lda = d; x.pout = w.P[c]; x.rows = S_of(c);
         }
-        int rc;
-        // QKV
-        a.N = 3 * d; a.K = d; a.tiles = 3 * d / 16; a.ksplit = ksplit_for(nch, a.tiles, d, KD);
+        if ((rc = launch_gemv<SRC_BUF>(a, KD, st))) return rc;
+        AttnArgs at = {};
+        at.ks = p.ks_qkv; at.ldp = 3 * d; at.d = d; at.heads = H; at.hd = d / H; at.causal = 1;
         for (int c = 0; c < nch; ++c) {
-          PhaseEx& x = a.ex[c];
-          x.w = (const h16x8*)P(c, B + L.qkv); x.bias = (const h16*)P(c, B + L.qkv_b);
-          x.lng = (const h16*)P(c, B + L.sn_w); x.lnb = (const h16*)P(c, B + L.sn_b);
-          x.st_in = stats_of(gen, c);
+          at.P[c] = w.P[c]; at.bias[c] = (const h16*)PTR(c, B + L.qkv_b); at.kv[c] = nullptr;
+          at.out[c] = w.attn[c]; at.Sq[c] = at.Sk[c] = S_of(c);
         }
-        if ((rc = launch_phase<K_QKV>(a, KD, st))) return rc;
-        // O
-        a.N = d; a.K = d; a.tiles = d / 16; a.ksplit = ksplit_for(nch, a.tiles, d, KD);
+        if ((rc = launch_attn(at, nch, KD, KD, st))) return rc;
+        // ---- O + residual, LN_cross
+        a.ks = p.ks_o; a.tiles = d / 16; a.N = d; a.K = d;
         for (int c = 0; c < nch; ++c) {
-          PhaseEx& x = a.ex[c];
-          x.w = (const h16x8*)P(c, B + L.o); x.bias = (const h16*)P(c, B + L.o_b);
-          x.st_out = stats_of(gen + 1, c);
+          GemvEx& x = a.ex[c];
+          x.w = (const h16x8*)PTR(c, B + L.o); x.a = w.attn[c]; x.lda = d; x.pout = w.P[c];
         }
-        if ((rc = launch_phase<K_O>(a, KD, st))) return rc;
-        // QC
-        a.N = d; a.K = d; a.tiles = d / 16; a.ksplit = ksplit_for(nch, a.tiles, d, KD);
+        if ((rc = launch_gemv<SRC_BUF>(a, KD, st))) return rc;
+        NormArgs nm = {};
+        nm.nex = nch; nm.ks = p.ks_o; nm.d = d;
+        int nrows = 0;
         for (int c = 0; c < nch; ++c) {
-          PhaseEx& x = a.ex[c];
-          x.w = (const h16x8*)P(c, B + L.qc); x.bias = (const h16*)P(c, B + L.qc_b);
-          x.lng = (const h16*)P(c, B + L.xn_w); x.lnb = (const h16*)P(c, B + L.xn_b);
-          x.st_in = stats_of(gen + 1, c);
+          nm.x[c] = w.x[c]; nm.P[c] = w.P[c]; nm.bias[c] = (const h16*)PTR(c, B + L.o_b);
+          nm.g[c] = (const h16*)PTR(c, B + L.xn_w); nm.b[c] = (const h16*)PTR(c, B + L.xn_b);
+          nm.a[c] = w.abuf[c]; nm.rows[c] = S_of(c); nrows += S_of(c);
         }
-        if ((rc = launch_phase<K_QC>(a, KD, st))) return rc;
-        // OC
+        hipLaunchKernelGGL(k_norm, dim3(nrows), dim3(ROWT), 0, st, nm);
+        CFH_LAUNCH_CHECK();
+        // ---- QC + cross attention
+        a.ks = p.ks_o;
         for (int c = 0; c < nch; ++c) {
-          PhaseEx& x = a.ex[c];
-          x.w = (const h16x8*)P(c, B + L.oc); x.bias = (const h16*)P(c, B + L.oc_b);
-          x.st_out = stats_of(gen + 2, c);
+          GemvEx& x = a.ex[c];
+          x.w = (const h16x8*)PTR(c, B + L.qc); x.a = w.abuf[c]; x.lda = d; x.pout = w.P[c];
         }
-        if ((rc = launch_phase<K_OC>(a, KD, st))) return rc;
-        // W1
-        a.N = fd; a.K = d; a.tiles = fd / 16; a.ksplit = ksplit_for(nch, a.tiles, d, KD);
+        if ((rc = launch_gemv<SRC_BUF>(a, KD, st))) return rc;
+        at.ks = p.ks_o; at.ldp = d; at.causal = 0;
         for (int c = 0; c < nch; ++c) {
-          PhaseEx& x = a.ex[c];
-          x.w = (const h16x8*)P(c, B + L.w1); x.bias = (const h16*)P(c, B + L.w1_b);
-          x.lng = (const h16*)P(c, B + L.fn_w); x.lnb = (const h16*)P(c, B + L.fn_b);
-          x.st_in = stats_of(gen + 2, c);
+          at.P[c] = w.P[c]; at.bias[c] = (const h16*)PTR(c, B + L.qc_b);
+          at.kv[c] = w.kvc[c] + (size_t)l * 2 * C * d; at.Sk[c] = C;
         }
-        if ((rc = launch_phase<K_W1>(a, KD, st))) return rc;
-        // W2
-        a.N = d; a.K = fd; a.tiles = d / 16; a.ksplit = ksplit_for(nch, a.tiles, fd, KD);
+        if ((rc = launch_attn(at, nch, KD, C, st))) return rc;
+        // ---- OC + residual, LN_ffn
         for (int c = 0; c < nch; ++c) {
-          PhaseEx& x = a.ex[c];
-          x.w = (const h16x8*)P(c, B + L.w2); x.bias = (const h16*)P(c, B + L.w2_b);
-          x.st_out = stats_of(gen + 3, c);
+          GemvEx& x = a.ex[c];
+          x.w = (const h16x8*)PTR(c, B + L.oc); x.a = w.attn[c]; x.lda = d; x.pout = w.P[c];
         }
-        if ((rc = launch_phase<K_W2>(a, KD, st))) return rc;
-        gen += 3;
+        if ((rc = launch_gemv<SRC_BUF>(a, KD, st))) return rc;
+        for (int c = 0; c < nch; ++c) {
+          nm.bias[c] = (const h16*)PTR(c, B + L.oc_b);
+          nm.g[c] = (const h16*)PTR(c, B + L.fn_w); nm.b[c] = (const h16*)PTR(c, B + L.fn_b);
+        }
+        hipLaunchKernelGGL(k_norm, dim3(nrows), dim3(ROWT), 0, st, nm);
+        CFH_LAUNCH_CHECK();
+        // ---- W1, GELU
+        a.ks = p.ks_w1; a.tiles = fd / 16; a.N = fd; a.K = d;
+        for (int c = 0; c < nch; ++c) {
+          GemvEx& x = a.ex[c];
+          x.w = (const h16x8*)PTR(c, B + L.w1); x.a = w.abuf[c]; x.lda = d; x.pout = w.Pw1[c];
+        }
+        if ((rc = launch_gemv<SRC_BUF>(a, KD, st))) return rc;
+        GeluArgs ge = {};
+        ge.nex = nch; ge.ks = p.ks_w1; ge.N = fd;
+        for (int c = 0; c < nch; ++c) {
+          ge.P[c] = w.Pw1[c]; ge.b[c] = (const h16*)PTR(c, B + L.w1_b); ge.g[c] = w.g[c]; ge.rows[c] = S_of(c);
+        }
+        hipLaunchKernelGGL(k_gelu, dim3(384), dim3(256), 0, st, ge);
+        CFH_LAUNCH_CHECK();
+        // ---- W2 + residual, next LayerNorm
+        a.ks = p.ks_w2; a.tiles = d / 16; a.N = d; a.K = fd;
+        for (int c = 0; c < nch; ++c) {
+          GemvEx& x = a.ex[c];
+          x.w = (const h16x8*)PTR(c, B + L.w2); x.a = w.g[c]; x.lda = fd; x.pout = w.P[c];
+        }
+        if ((rc = launch_gemv<SRC_BUF>(a, KD, st))) return rc;
+        nm.ks = p.ks_w2;
+        for (int c = 0; c < nch; ++c) {
+          nm.bias[c] = (const h16*)PTR(c, B + L.w2_b);
+          if (l + 1 < NL) {
+            nm.g[c] = (const h16*)PTR(c, BLK(l + 1) + L.sn_w); nm.b[c] = (const h16*)PTR(c, BLK(l + 1) + L.sn_b);
+          } else {
+            nm.g[c] = (const h16*)PTR(c, L.on_w); nm.b[c] = (const h16*)PTR(c, L.on_b);
+          }
+        }
+        hipLaunchKernelGGL(k_norm, dim3(nrows), dim3(ROWT), 0, st, nm);
+        CFH_LAUNCH_CHECK();
       }
-      // OUT: velocity of the current chunk rows, Euler update, next step's pre_blocks rows
-      PhaseArgs a = {};
-      a.nex = nch; a.nl = 1; a.d = d; a.heads = H; a.hd = d / H; a.CS = CS; a.C = C; a.E = E; a.FD = fd;
-      a.N = d; a.K = d; a.tiles = d / 16; a.ksplit = ksplit_for(nch, a.tiles, d, CS);
-      a.partials = w.partials; a.tile_ctr = w.tile_ctr; a.head_ctr = w.head_ctr;
-      a.dt = 1.0f / (float)E;
-      a.has_next = (s + 1 < E);
-      a.z = w.z; a.z_out = zo_b;
-      for (int c = 0; c < nch; ++c) {
-        PhaseEx& x = a.ex[c];
-        x.w = (const h16x8*)P(c, L.out); x.bias = (const h16*)P(c, L.out_b);
-        x.lng = (const h16*)P(c, L.on_w); x.lnb = (const h16*)P(c, L.on_b);
-        x.st_in = stats_of(gen, c);
-        x.x = w.x[c][s & 1]; x.x16 = w.x16[c][s & 1];
-        x.x_next = w.x[c][(s + 1) & 1]; x.x16_next = w.x16[c][(s + 1) & 1];
-        x.rows = CS; x.row0 = c * CS; x.srows = (c + 1) * CS;
-        x.pos = (const h16*)P(c, L.pos);
-        x.tau_next = w.tau[c] + (size_t)(s + 1 < E ? s + 1 : s) * d;
-        x.st_next = stats_of(gen + 1, c);
+      // ---- OUT (current chunk rows) and the Euler update / next rows
+      {
+        GemvArgs a = {};
+        a.nex = nch; a.nl = 1; a.E = E; a.ks = p.ks_out; a.tiles = d / 16; a.N = d; a.K = d;
+        for (int c = 0; c < nch; ++c) {
+          GemvEx& x = a.ex[c];
+          x.w = (const h16x8*)PTR(c, L.out);
+          x.a = w.abuf[c] + (size_t)c * CS * d;   // out_norm rows of the current chunk
+          x.lda = d; x.pout = w.P[c]; x.rows = CS;
+        }
+        if ((rc = launch_gemv<SRC_BUF>(a, CS, st))) return rc;
+        RowsArgs r = {};
+        r.ctx = ctx_b; r.z = w.z; r.z_out = zo_b; r.euler = 1; r.last = (s + 1 == E); r.ks = p.ks_out;
+        r.dt = 1.0f / (float)E; r.d = d; r.C = C; r.CS = CS; r.nch = nch;
+        for (int c = 0; c < nch; ++c) {
+          r.Pout[c] = w.P[c]; r.bout[c] = (const h16*)PTR(c, L.out_b);
+          r.x[c] = w.x[c]; r.pos[c] = (const h16*)PTR(c, L.pos);
+          r.tau[c] = w.tau[c] + (size_t)(s + 1 < E ? s + 1 : s) * d;
+          r.g[c] = (const h16*)PTR(c, BLK(0) + L.sn_w); r.b[c] = (const h16*)PTR(c, BLK(0) + L.sn_b);
+          r.a[c] = w.abuf[c];
+        }
+        hipLaunchKernelGGL(k_rows, dim3(KD), dim3(ROWT), 0, st, r);
+        CFH_LAUNCH_CHECK();
       }
-      int rc = launch_phase<K_OUT>(a, CS, st);
-      if (rc) return rc;
-      gen += 1;
     }
   }
   return CFH_OK;

@@ -34,12 +34,15 @@ SIGNATURES = {
     "cfh_flow_expert_bytes": (_I64, [C.POINTER(FlowDims)]),
     "cfh_flow_pack_expert": (_I, [C.POINTER(FlowDims), C.POINTER(_VP), _I, _VP, _VP]),
     "cfh_flow_integrate": (_I, [C.POINTER(FlowDims), C.POINTER(_VP), _VP, _VP, _VP, _I, _VP]),
-    "cfh_head_logits": (_I, [_VP, _I, _I, _VP, _VP, _I, _VP, _I, _VP, _VP, _VP]),
+    "cfh_head_logits": (_I, [_VP, _I, _I, _VP, _VP, _I, _VP, _VP, _I, _I, _VP, _VP, _VP]),
     "cfh_row_topk": (_I, [_VP, _I, _I, _I, _VP, _VP, _VP, _VP]),
-    "cfh_head_topk": (_I, [_VP, _I, _I, _VP, _VP, _I, _VP, _I, _VP, _I, _VP, _VP, _VP, _VP, _VP]),
+    "cfh_head_topk": (_I, [_VP, _I, _I, _VP, _VP, _I, _VP, _VP, _I, _I, _VP, _I, _VP, _VP, _VP, _VP, _VP]),
     "cfh_head_gemm_topk": (_I, [_VP, _I, _I, _VP, _VP, _I, _I, _VP, _VP, _VP, _VP, _VP]),
     "cfh_path_ws_bytes": (_I64, [_I, _I, _I, _I]),
     "cfh_path_residual": (_I, [C.POINTER(_VP), _I, _I, _I, _VP, _I, _I, _VP, _VP, _VP, _VP, _VP]),
+    "cfh_beam_chain_step": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _VP]),
+    "cfh_beam_tree_step": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _I, _VP]),
+    "cfh_beam_backtrack": (_I, [_VP, _VP, _VP, _I, _I, _I, _VP, _VP]),
     "cfh_gdn_tree": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _VP, _VP, _VP]),
 }
 

@@ -1,0 +1,133 @@
+"""The drafting hot path on MI355X: one flow pass, then the beam over the shortlisted head.
+
+``Drafter`` holds what the proposer's ``_build`` assembles (``cf/vllm_plugin/flow_proposer.py:579-867``):
+the packed flow experts, the PathHead, the shortlisted lm_head with the markov bias, and the
+target's input embeddings.  ``beam_chains`` / ``beam_tree`` are the proposer's ``_draft_fn``
+(``:1187-1332``) with no host synchronisation until the caller reads the result.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from chain_flow_amd import _lib
+from chain_flow_amd.config import TreeFlowConfig
+from chain_flow_amd.flow import FusedFlow
+from chain_flow_amd.head import PathHead, ShortlistHead
+
+
+def front_pad(hidden: torch.Tensor, context_size: int) -> torch.Tensor:
+    """``TreeFlowDrafter._context`` (``cf/drafters/tree_flow.py:143-148``): the last C rows, front-padded
+    by repeating the oldest row."""
+    n = hidden.shape[1]
+    if n >= context_size:
+        return hidden[:, -context_size:]
+    pad = hidden[:, :1].expand(-1, context_size - n, -1)
+    return torch.cat([pad, hidden], dim=1)
+
+
+class Drafter:
+    def __init__(self, cfg: TreeFlowConfig, weights: dict, shortlist: torch.Tensor | None, device="cuda",
+                 path_trim: bool = True):
+        self.cfg = cfg
+        dev = torch.device(device)
+        if dev.type == "cuda" and dev.index is None:
+            dev = torch.device("cuda", torch.cuda.current_device())
+        self.device = dev
+        self.path_trim = path_trim
+        self.flow = FusedFlow(cfg, weights, device=dev)
+        self.path = PathHead(weights, weights["embed_tokens.weight"], cfg.path_order,
+                             cfg.path_ffn_multiplier, dev)
+        self.head = ShortlistHead(weights["lm_head.weight"].to(dev, torch.float16), shortlist,
+                                  weights["markov.w1.weight"], weights["markov.w2.weight"])
+        self.order = cfg.path_order
+
+    def _nlive(self, depth: int):
+        """``_nlive`` (``cf/vllm_plugin/flow_proposer.py:1030-1037``)."""
+        return depth if self.path_trim else None
+
+    def predict_hidden(self, ctx: torch.Tensor) -> torch.Tensor:
+        return self.flow.predict_hidden(ctx.to(self.device, torch.float16))
+
+    def beam_chains(self, ctx: torch.Tensor, known0: torch.Tensor, K: int, width: int = 4,
+                    pred: torch.Tensor | None = None) -> torch.Tensor:
+        """``_beam_chains`` with the one-pass head: ctx [B, C, d], known0 [B] -> [B, K'] int64 global ids,
+        K' = min(K, draft_length - 1).  ``pred`` (the flow output) may be passed in to skip the flow."""
+        dev = self.device
+        W, order = width, self.order
+        if pred is None:
+            pred = self.predict_hidden(ctx)
+        B, Kd, d = pred.shape
+        steps = min(K + 1, Kd)
+        if B * W > 8:
+            outs = [self.beam_chains(None, known0[i:i + 1], K, W, pred=pred[i:i + 1]) for i in range(B)]
+            return torch.cat(outs, 0)
+        lastp = torch.full((B, W, order), -1, dtype=torch.int32, device=dev)
+        lastp[:, :, 0] = known0.to(dev, torch.int32).view(B, 1)
+        cum = torch.full((B, W), float("-inf"), dtype=torch.float32, device=dev)
+        cum[:, 0] = 0.0
+        nst = steps - 1
+        toks = torch.empty(max(nst, 1), B, W, dtype=torch.int32, device=dev)
+        bps = torch.empty_like(toks)
+        hbuf = torch.empty(B * W, d, dtype=torch.float16, device=dev)
+        logits = torch.empty(B * W, self.head.n, dtype=torch.float16, device=dev)
+        L = _lib.lib()
+        st = _lib.stream_handle()
+        for step in range(1, steps):
+            for b in range(B):
+                self.path.hidden(lastp[b], self._nlive(step), pred[b, step], out=hbuf[b * W:(b + 1) * W])
+            vals, ids, _ = self.head.topk(hbuf, W, prev=lastp.view(B * W, order), prev_stride=order,
+                                          logits=logits)
+            _lib.check(L.cfh_beam_chain_step(vals.data_ptr(), ids.data_ptr(), cum.data_ptr(), lastp.data_ptr(),
+                                             _lib.ptr(self.head.sl), toks[step - 1].data_ptr(),
+                                             bps[step - 1].data_ptr(), B, W, order, st), "cfh_beam_chain_step")
+        out = torch.empty(B, nst, dtype=torch.int64, device=dev)
+        if nst > 0:
+            _lib.check(L.cfh_beam_backtrack(cum.data_ptr(), toks.data_ptr(), bps.data_ptr(), B, W, nst,
+                                            out.data_ptr(), st), "cfh_beam_backtrack")
+        return out
+
+    def beam_tree(self, ctx: torch.Tensor, known0: torch.Tensor, keep: int = 4, topb: int = 8, depth: int = 4,
+                  pred: torch.Tensor | None = None) -> torch.Tensor:
+        """``_beam_tree``: -> [B, 2N] int32-valued int64: N BFS-ordered tokens || parent node indices."""
+        dev = self.device
+        order = self.order
+        if pred is None:
+            pred = self.predict_hidden(ctx)
+        B, Kd, d = pred.shape
+        if B * keep > 8:
+            outs = [self.beam_tree(None, known0[i:i + 1], keep, topb, depth, pred=pred[i:i + 1])
+                    for i in range(B)]
+            return torch.cat(outs, 0)
+        nstep = min(depth, Kd - 1)
+        sizes, fr = [], 1
+        for _ in range(nstep):
+            k = min(keep, fr * topb)
+            sizes.append(k)
+            fr = k
+        N = sum(sizes)
+        out = torch.empty(B, 2 * N, dtype=torch.int32, device=dev)
+        lastp = torch.full((B, keep, order), -1, dtype=torch.int32, device=dev)
+        lastp[:, 0, 0] = known0.to(dev, torch.int32)
+        cum = torch.zeros(B, keep, dtype=torch.float32, device=dev)
+        prev_ids = torch.full((B, keep), -1, dtype=torch.int32, device=dev)
+        hbuf = torch.empty(B * keep, d, dtype=torch.float16, device=dev)
+        logits = torch.empty(B * keep, self.head.n, dtype=torch.float16, device=dev)
+        L = _lib.lib()
+        st = _lib.stream_handle()
+        fr, base = 1, 0
+        for step in range(1, nstep + 1):
+            rows = torch.empty(B * fr, d, dtype=torch.float16, device=dev) if fr != keep else hbuf
+            lp_rows = lastp[:, :fr].reshape(B * fr, order).contiguous()
+            for b in range(B):
+                self.path.hidden(lp_rows[b * fr:(b + 1) * fr], self._nlive(step), pred[b, step],
+                                 out=rows[b * fr:(b + 1) * fr])
+            vals, ids, _ = self.head.topk(rows, topb, prev=lp_rows, prev_stride=order,
+                                          logits=logits[:B * fr])
+            _lib.check(L.cfh_beam_tree_step(vals.data_ptr(), ids.data_ptr(), cum.data_ptr(), lastp.data_ptr(),
+                                            prev_ids.data_ptr(), _lib.ptr(self.head.sl), out.data_ptr(), 2 * N,
+                                            base, B, fr, topb, keep, order, st), "cfh_beam_tree_step")
+            base += sizes[step - 1]
+            fr = sizes[step - 1]
+        return out.long()

@@ -1,0 +1,140 @@
+"""Host side of the draft head: shortlisted lm_head + markov bias + top-k, and the PathHead residual.
+
+Mirrors the proposer's ``_head`` / ``_bias`` / ``_map`` (``cf/vllm_plugin/flow_proposer.py:1021-1028``)
+and the fused ``_residual_from_lastp`` (``cf/vllm_plugin/fused.py:25-37``) over libcfhip.so.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from chain_flow_amd import _lib
+
+
+def _i32(t: torch.Tensor) -> torch.Tensor:
+    return t.to(torch.int32).contiguous()
+
+
+class ShortlistHead:
+    """The target's lm_head restricted to a shortlist, read in place (row gather), plus the markov
+    logit bias ``markov.w2(markov.w1[prev])`` restricted to the same rows."""
+
+    def __init__(self, lm_w: torch.Tensor, shortlist: torch.Tensor | None, w1: torch.Tensor | None = None,
+                 w2: torch.Tensor | None = None):
+        if lm_w.dtype != torch.float16 or not lm_w.is_cuda:
+            raise ValueError("lm_w must be a CUDA fp16 [V, d] tensor")
+        self.lm_w = lm_w.contiguous()
+        self.V, self.d = self.lm_w.shape
+        self.sl = None if shortlist is None else _i32(shortlist.to(lm_w.device))
+        if self.sl is not None and self.sl.numel() and (int(self.sl.min()) < 0 or int(self.sl.max()) >= self.V):
+            raise ValueError("shortlist ids out of range of the lm_head")
+        self.n = self.V if self.sl is None else int(self.sl.numel())
+        self.w1 = None if w1 is None else w1.to(lm_w.device, torch.float16).contiguous()
+        self.w2 = None if w2 is None else w2.to(lm_w.device, torch.float16).contiguous()
+        if (self.w1 is None) != (self.w2 is None):
+            raise ValueError("markov w1 and w2 go together")
+        self.r = 0 if self.w1 is None else int(self.w1.shape[1])
+
+    def map(self, local: torch.Tensor) -> torch.Tensor:
+        """``_map``: shortlist-local column -> global token id."""
+        return local if self.sl is None else self.sl.long()[local.long()]
+
+    def logits(self, h: torch.Tensor, prev: torch.Tensor | None = None, prev_stride: int = 1,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+        """h [M, d] fp16, prev (global ids, int32) -> fp16 logits [M, n] (head + markov bias)."""
+        M = h.shape[0]
+        if out is None:
+            out = torch.empty(M, self.n, dtype=torch.float16, device=h.device)
+        use_m = self.w1 is not None and prev is not None
+        _lib.check(_lib.lib().cfh_head_logits(
+            h.data_ptr(), M, self.d, self.lm_w.data_ptr(), _lib.ptr(self.sl), self.n,
+            self.w1.data_ptr() if use_m else None, prev.data_ptr() if use_m else None, prev_stride,
+            self.r, self.w2.data_ptr() if use_m else None, out.data_ptr(), _lib.stream_handle()),
+            "cfh_head_logits")
+        return out
+
+    def topk(self, h: torch.Tensor, k: int, prev: torch.Tensor | None = None, prev_stride: int = 1,
+             logits: torch.Tensor | None = None):
+        """-> (log-prob values [M, k] f32, shortlist-local ids [M, k] int32, lse [M] f32)."""
+        M = h.shape[0]
+        dev = h.device
+        if logits is None:
+            logits = torch.empty(M, self.n, dtype=torch.float16, device=dev)
+        vals = torch.empty(M, k, dtype=torch.float32, device=dev)
+        ids = torch.empty(M, k, dtype=torch.int32, device=dev)
+        lse = torch.empty(M, dtype=torch.float32, device=dev)
+        use_m = self.w1 is not None and prev is not None
+        _lib.check(_lib.lib().cfh_head_topk(
+            h.data_ptr(), M, self.d, self.lm_w.data_ptr(), _lib.ptr(self.sl), self.n,
+            self.w1.data_ptr() if use_m else None, prev.data_ptr() if use_m else None, prev_stride,
+            self.r, self.w2.data_ptr() if use_m else None, k, logits.data_ptr(), vals.data_ptr(),
+            ids.data_ptr(), lse.data_ptr(), _lib.stream_handle()),
+            "cfh_head_topk")
+        return vals, ids, lse
+
+
+def row_topk(logits: torch.Tensor, k: int):
+    """Per-row log-softmax top-k of fp16 logits [M, n] -> (vals f32, ids int32, lse f32)."""
+    M, n = logits.shape
+    logits = logits.contiguous()
+    vals = torch.empty(M, k, dtype=torch.float32, device=logits.device)
+    ids = torch.empty(M, k, dtype=torch.int32, device=logits.device)
+    lse = torch.empty(M, dtype=torch.float32, device=logits.device)
+    _lib.check(_lib.lib().cfh_row_topk(logits.data_ptr(), M, n, k, vals.data_ptr(), ids.data_ptr(),
+                                       lse.data_ptr(), _lib.stream_handle()), "cfh_row_topk")
+    return vals, ids, lse
+
+
+def pack_linear(w: torch.Tensor) -> torch.Tensor:
+    """Row-major [n, k] 2-byte weight -> MFMA tile order (same shape, new storage)."""
+    w = w.contiguous()
+    out = torch.empty_like(w)
+    n, k = w.shape
+    _lib.check(_lib.lib().cfh_pack_linear(w.data_ptr(), n, k, out.data_ptr(), _lib.stream_handle()),
+               "cfh_pack_linear")
+    return out
+
+
+class PathHead:
+    """PathHead residual ``mlp(norm(sum_j mask_j (W_j emb(lastp_j) + b_j)))`` over packed weights."""
+
+    def __init__(self, weights: dict, embed_w: torch.Tensor, order: int, ffn_mult: int, device):
+        dev = torch.device(device)
+        f16 = dict(dtype=torch.float16, device=dev)
+        self.order, self.ffn, self.d = order, ffn_mult, int(embed_w.shape[1])
+        self.embed_w = embed_w.to(**f16).contiguous()
+        g = lambda n: weights[n].to(**f16).contiguous()
+        self.Wj = [pack_linear(g(f"path_head.offset_proj.{j}.weight")) for j in range(order)]
+        self.bj = [g(f"path_head.offset_proj.{j}.bias") for j in range(order)]
+        self.norm_w, self.norm_b = g("path_head.norm.weight"), g("path_head.norm.bias")
+        self.W0, self.b0 = pack_linear(g("path_head.mlp.0.weight")), g("path_head.mlp.0.bias")
+        self.W3, self.b3 = pack_linear(g("path_head.mlp.3.weight")), g("path_head.mlp.3.bias")
+        ptrs = [t.data_ptr() for t in self.Wj + self.bj] + [
+            self.norm_w.data_ptr(), self.norm_b.data_ptr(), self.W0.data_ptr(), self.b0.data_ptr(),
+            self.W3.data_ptr(), self.b3.data_ptr()]
+        self._ptrs = _lib.ptr_array(ptrs)
+        self._ws = {}
+
+    def _workspace(self, M: int, dev) -> torch.Tensor:
+        ws = self._ws.get(M)
+        if ws is None:
+            nbytes = int(_lib.lib().cfh_path_ws_bytes(M, self.d, self.ffn, self.order))
+            if nbytes < 0:
+                raise ValueError(f"path residual shape unsupported: M={M} d={self.d}")
+            ws = self._ws[M] = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        return ws
+
+    def hidden(self, lastp: torch.Tensor, nlive: int | None, pred: torch.Tensor,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+        """lastp [M, order] int32 (global ids, -1 = none), pred [d] fp16 ->
+        fp16(pred + residual) [M, d] (the head's input at this depth)."""
+        M = lastp.shape[0]
+        if out is None:
+            out = torch.empty(M, self.d, dtype=torch.float16, device=pred.device)
+        ws = self._workspace(M, pred.device)
+        _lib.check(_lib.lib().cfh_path_residual(
+            self._ptrs, self.order, self.ffn, self.d, lastp.data_ptr(), M,
+            -1 if nlive is None else int(nlive), self.embed_w.data_ptr(), pred.data_ptr(),
+            out.data_ptr(), ws.data_ptr(), _lib.stream_handle()), "cfh_path_residual")
+        return out

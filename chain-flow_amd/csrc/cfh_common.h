@@ -74,20 +74,30 @@ __host__ __device__ __forceinline__ size_t packed_index(int tile, int kstep, int
 // When nsteps is a multiple of PF the loads are issued unconditionally PF steps ahead, so the
 // compiler keeps PF fragment loads in flight per wave (vmcnt(PF-1) waits); other step counts
 // take a plain loop.
-template <int PF>
+// STRIDE = distance between consecutive k-steps of one lane, in 16-byte units (64 for the packed
+// layout; 4 for a row-major [rows][K] matrix read in place).  NT = non-temporal loads (packed
+// weights are read once; in-place rows use plain loads so the second half of each 128-byte line
+// is served from cache).
+template <int PF, int STRIDE = 64, bool NT = true>
 struct TileStream {
   h16x8 buf[PF];
   const h16x8* wp;
   int nsteps;
   bool piped;
 
+  __device__ __forceinline__ h16x8 ld(size_t s) const {
+    if constexpr (NT) return __builtin_nontemporal_load(wp + s * STRIDE);
+    else return wp[s * STRIDE];
+  }
+
+  // w: this lane's first fragment when STRIDE != 64; the tile base (lane offset added) when 64.
   __device__ __forceinline__ void begin(const h16x8* __restrict__ w, int n) {
-    wp = w + (threadIdx.x & 63);
+    wp = (STRIDE == 64) ? w + (threadIdx.x & 63) : w;
     nsteps = n;
     piped = (n >= PF) && (n % PF == 0);
     if (piped) {
 #pragma unroll
-      for (int p = 0; p < PF; ++p) buf[p] = __builtin_nontemporal_load(wp + (size_t)p * 64);
+      for (int p = 0; p < PF; ++p) buf[p] = ld(p);
     }
   }
 
@@ -104,7 +114,7 @@ struct TileStream {
 #pragma unroll
         for (int p = 0; p < PF; ++p) {
           const h16x8 b = buf[p];
-          buf[p] = __builtin_nontemporal_load(wp + (size_t)(s0 + PF + p) * 64);
+          buf[p] = ld((size_t)(s0 + PF + p));
           const h16x8 a = live ? *(const h16x8*)(arow + (s0 + p) * 32) : zero;
           acc = mfma_f16(a, b, acc);
         }
@@ -116,7 +126,7 @@ struct TileStream {
       }
     } else {
       for (int s = 0; s < nsteps; ++s) {
-        const h16x8 b = __builtin_nontemporal_load(wp + (size_t)s * 64);
+        const h16x8 b = ld((size_t)s);
         const h16x8 a = live ? *(const h16x8*)(arow + s * 32) : zero;
         acc = mfma_f16(a, b, acc);
       }

@@ -35,149 +35,11 @@
 #include <stdio.h>
 
 #include <algorithm>
+#include <mutex>
 
-#include "cfh_common.h"
-#include "cfh_host.h"
+#include "cfh_kernels.h"
 
 namespace {
-
-constexpr int WPB = 4;            // waves per GEMV workgroup
-constexpr int PF = 8;             // fragment loads in flight per wave
-constexpr int MAXR = 16;          // max activation rows per expert (draft_length, ctx rows, steps)
-constexpr int ROWT = 1024;        // threads of the row kernels (NORM / ROWS)
-constexpr int ROWE = 16;          // max elements per thread in the row kernels (d <= 16384)
-constexpr float LN_EPS = 1e-5f;
-
-enum Src { SRC_BUF = 0, SRC_CTX, SRC_TAU };
-
-// ---------------------------------------------------------------------------- GEMV
-struct GemvEx {
-  const h16x8* w;      // packed weight fragments (layer 0 when nl > 1)
-  const h16* a;        // SRC_BUF: activation rows [rows][lda]; SRC_CTX: context rows [rows][K]
-  int lda;
-  const h16* g0;       // SRC_CTX: context_norm weight (layer 0) | SRC_TAU: time_mlp.0.weight
-  const h16* b0;       // SRC_CTX: context_norm bias             | SRC_TAU: time_mlp.0.bias
-  float* pout;         // partial outputs [(l*ks + kc)][rows][N]
-  const float* mom;    // SRC_CTX: context row moments [rows][2] = (mean, rstd)
-  int rows;
-};
-
-struct GemvArgs {
-  GemvEx ex[4];
-  int nex, nl, ks, tiles, N, K, E;
-  long long wstride, vstride;   // bytes between consecutive layers (packed weights / vectors)
-};
-
-template <int SRC>
-__device__ void stage_A(const GemvArgs& a, const GemvEx& ep, int l, int kc, h16* As, int lda) {
-  const int KC = a.K / a.ks;
-  const int k0 = kc * KC;
-  const int rows = ep.rows;
-  const int nvec = KC / 8;
-  if constexpr (SRC == SRC_BUF) {
-    for (int idx = threadIdx.x; idx < rows * nvec; idx += blockDim.x) {
-      const int i = idx / nvec, kk = (idx - i * nvec) * 8;
-      *(h16x8*)(As + i * lda + kk) = *(const h16x8*)(ep.a + (size_t)i * ep.lda + k0 + kk);
-    }
-  } else if constexpr (SRC == SRC_CTX) {
-    // context_norm(ctx) of layer l; the row moments (mean, rstd) come precomputed in ep.mom
-    const h16* gw = (const h16*)((const char*)ep.g0 + (size_t)l * a.vstride);
-    const h16* gb = (const h16*)((const char*)ep.b0 + (size_t)l * a.vstride);
-    for (int idx = threadIdx.x; idx < rows * nvec; idx += blockDim.x) {
-      const int i = idx / nvec, kk = (idx - i * nvec) * 8;
-      const h16x8 xv = *(const h16x8*)(ep.a + (size_t)i * a.K + k0 + kk);
-      const h16x8 gv = *(const h16x8*)(gw + k0 + kk);
-      const h16x8 bv = *(const h16x8*)(gb + k0 + kk);
-      const float mu = ep.mom[2 * i], rs = ep.mom[2 * i + 1];
-      h16x8 o;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = (h16)(((float)xv[e] - mu) * rs * (float)gv[e] + (float)bv[e]);
-      *(h16x8*)(As + i * lda + kk) = o;
-    }
-  } else if constexpr (SRC == SRC_TAU) {
-    // rows = Euler steps: a_s = fp16(silu(fp16(tau_s * w0 + b0))), tau_s = fp16(s / E)
-    for (int idx = threadIdx.x; idx < rows * nvec; idx += blockDim.x) {
-      const int i = idx / nvec, kk = (idx - i * nvec) * 8;
-      const float tau = r16((float)i * (1.0f / (float)a.E));
-      h16x8 o;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float h = r16(tau * (float)ep.g0[k0 + kk + e] + (float)ep.b0[k0 + kk + e]);
-        o[e] = (h16)silu(h);
-      }
-      *(h16x8*)(As + i * lda + kk) = o;
-    }
-  }
-  __syncthreads();
-}
-
-template <int SRC>
-__global__ void __launch_bounds__(WPB * 64) k_gemv(GemvArgs a) {
-  extern __shared__ __align__(16) h16 As[];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int per_ex = a.nl * a.ks * a.tiles;
-  const int u0 = blockIdx.x * WPB;
-  const int e = u0 / per_ex;
-  int rem = u0 - e * per_ex;
-  const int l = rem / (a.ks * a.tiles);
-  rem -= l * a.ks * a.tiles;
-  const int kc = rem / a.tiles;
-  const int t = wave + (rem - kc * a.tiles);   // a workgroup never straddles (e, l, kc)
-  const GemvEx& ep = a.ex[e];
-  const int KC = a.K / a.ks;
-  const int lda = KC + 8;
-
-  // The weight stream does not depend on the activations: put its first PF fragment loads in
-  // flight before staging the activation chunk.
-  const h16x8* wbase = (const h16x8*)((const char*)ep.w + (size_t)l * a.wstride);
-  TileStream<PF> ts;
-  ts.begin(wbase + packed_index(t, kc * (KC / 32), a.K, 0), KC / 32);
-  stage_A<SRC>(a, ep, l, kc, As, lda);
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  acc = ts.run(As, lda, ep.rows, acc);
-
-  const int col = lane & 15, rbase = 4 * (lane >> 4);
-  float* po = ep.pout + ((size_t)(l * a.ks + kc) * ep.rows) * a.N + t * 16 + col;
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    if (rbase + j < ep.rows) po[(size_t)(rbase + j) * a.N] = acc[j];
-}
-
-// ---------------------------------------------------------------------------- partial reduce
-// out = fp16(sum_kc P[kc] + b), used for the per-draft cross K/V and time embeddings.
-struct ReduceArgs {
-  const float* P[4];
-  const h16* b[4];
-  h16* out[4];
-  int nex, nl, ks, rows, N, d, kv;   // kv: N = 2d split into [2][rows][d] per layer
-  long long vstride;
-};
-
-__global__ void __launch_bounds__(256) k_reduce(ReduceArgs a) {
-  const size_t per_l = (size_t)a.rows * a.N;
-  const size_t per_e = per_l * a.nl;
-  const size_t total = per_e * a.nex;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
-    const int e = (int)(i / per_e);
-    size_t r = i - e * per_e;
-    const int l = (int)(r / per_l);
-    r -= (size_t)l * per_l;
-    const int row = (int)(r / a.N), n = (int)(r - (size_t)row * a.N);
-    const float* P = a.P[e] + (size_t)l * a.ks * per_l + (size_t)row * a.N + n;
-    float s = 0.f;
-    for (int q = 0; q < a.ks; ++q) s += P[(size_t)q * per_l];
-    const h16* b = (const h16*)((const char*)a.b[e] + (size_t)l * a.vstride);
-    const float v = s + (float)b[n];
-    size_t o;
-    if (a.kv) {
-      const int part = n / a.d, nn = n - part * a.d;
-      o = (((size_t)l * 2 + part) * a.rows + row) * a.d + nn;
-    } else {
-      o = ((size_t)l * a.rows + row) * a.N + n;
-    }
-    a.out[e][o] = (h16)v;
-  }
-}
 
 // ---------------------------------------------------------------------------- attention
 // One workgroup per (expert, head): softmax(q k^T / sqrt(hd) [+ causal mask]) v for <= 16 query
@@ -279,91 +141,7 @@ __global__ void __launch_bounds__(1024) k_attn(AttnArgs a) {
   }
 }
 
-// ---------------------------------------------------------------------------- GELU
-// g = fp16(gelu(sum_kc P[kc] + b1)) for every row of every expert.
-struct GeluArgs {
-  const float* P[4];
-  const h16* b[4];
-  h16* g[4];
-  int rows[4];
-  int nex, ks, N;
-};
-
-__global__ void __launch_bounds__(256) k_gelu(GeluArgs a) {
-  size_t total = 0;
-  for (int e = 0; e < a.nex; ++e) total += (size_t)a.rows[e] * a.N / 4;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
-    int e = 0;
-    size_t j = i;
-    while (j >= (size_t)a.rows[e] * a.N / 4) j -= (size_t)a.rows[e++] * a.N / 4;
-    const size_t per_kc = (size_t)a.rows[e] * a.N;
-    const float* P = a.P[e] + j * 4;
-    float4 s4 = *(const float4*)P;
-    for (int q = 1; q < a.ks; ++q) {
-      const float4 t = *(const float4*)(P + q * per_kc);
-      s4.x += t.x; s4.y += t.y; s4.z += t.z; s4.w += t.w;
-    }
-    const int n = (int)((j * 4) % a.N);
-    const h16* bb = a.b[e] + n;
-    h16* g = a.g[e] + j * 4;
-    g[0] = (h16)gelu_erf(s4.x + (float)bb[0]);
-    g[1] = (h16)gelu_erf(s4.y + (float)bb[1]);
-    g[2] = (h16)gelu_erf(s4.z + (float)bb[2]);
-    g[3] = (h16)gelu_erf(s4.w + (float)bb[3]);
-  }
-}
-
 // ---------------------------------------------------------------------------- row kernels
-// Block-wide sum over the workgroup.
-__device__ __forceinline__ float block_sum(float v, float* red) {
-  v = wave_sum(v);
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  __syncthreads();
-  if (lane == 0) red[wave] = v;
-  __syncthreads();
-  float t = 0.f;
-  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t += red[w];
-  return t;
-}
-
-// LayerNorm of one row held as fp16-valued floats: thread t owns the float4 column groups
-// t, t + blockDim, ... (vals[k] = group k); two-pass moments; fp16 output.
-constexpr int ROWQ = ROWE / 4;   // float4 groups per thread
-
-__device__ void ln_row4(const float4* vals, int d, const h16* g, const h16* b, h16* out, float* red) {
-  const int nq = d / 4;
-  float s = 0.f;
-#pragma unroll
-  for (int k = 0; k < ROWQ; ++k) {
-    const int q = threadIdx.x + k * blockDim.x;
-    if (q < nq) s += (vals[k].x + vals[k].y) + (vals[k].z + vals[k].w);
-  }
-  const float mean = block_sum(s, red) / (float)d;
-  float v = 0.f;
-#pragma unroll
-  for (int k = 0; k < ROWQ; ++k) {
-    const int q = threadIdx.x + k * blockDim.x;
-    if (q < nq) {
-      const float a0 = vals[k].x - mean, a1 = vals[k].y - mean, a2 = vals[k].z - mean, a3 = vals[k].w - mean;
-      v += (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
-    }
-  }
-  const float rstd = 1.0f / sqrtf(block_sum(v, red) / (float)d + LN_EPS);
-#pragma unroll
-  for (int k = 0; k < ROWQ; ++k) {
-    const int q = threadIdx.x + k * blockDim.x;
-    if (q < nq) {
-      const int c = q * 4;
-      out[c + 0] = (h16)((vals[k].x - mean) * rstd * (float)g[c + 0] + (float)b[c + 0]);
-      out[c + 1] = (h16)((vals[k].y - mean) * rstd * (float)g[c + 1] + (float)b[c + 1]);
-      out[c + 2] = (h16)((vals[k].z - mean) * rstd * (float)g[c + 2] + (float)b[c + 2]);
-      out[c + 3] = (h16)((vals[k].w - mean) * rstd * (float)g[c + 3] + (float)b[c + 3]);
-    }
-  }
-}
-
-__device__ __forceinline__ float4 r16x4(float4 v) { return make_float4(r16(v.x), r16(v.y), r16(v.z), r16(v.w)); }
-
 // NORM: x[r] += sum_kc P[kc][r] + bias; a[r] = fp16(LN(fp16(x[r]))).  One workgroup per row.
 struct NormArgs {
   float* x[4];
@@ -558,27 +336,6 @@ __global__ void __launch_bounds__(ROWT) k_rows(RowsArgs a) {
 }
 
 // ---------------------------------------------------------------------------- host side
-size_t lds_bytes(int rows, int KC) { return (size_t)rows * (KC + 8) * 2; }
-
-// Split-K factor: the smallest divisor ks of the k-step count such that every unit streams a
-// whole number of PF-step prefetch blocks, the A chunk fits in 48 KiB of LDS (two or three
-// workgroups per CU) and the phase has >= 2048 wave units; else the largest valid one.
-int ksplit_for(int nex_units, int tiles, int K, int rows) {
-  const int steps = K / 32;
-  int best = -1;
-  for (int ks = 1; ks <= steps; ++ks) {
-    if (steps % ks) continue;
-    if ((steps / ks) % PF) continue;
-    if (lds_bytes(rows, K / ks) > 48 * 1024) continue;
-    best = ks;
-    if ((long long)nex_units * tiles * ks >= 2048) break;
-  }
-  if (best > 0) return best;
-  for (int ks = 1; ks <= steps; ++ks)
-    if (steps % ks == 0 && lds_bytes(rows, K / ks) <= 48 * 1024) return ks;
-  return steps;
-}
-
 struct Plan {
   int d, fd, CS, E, NL, C, KD, H, nch;
   int ks_qkv, ks_o, ks_w1, ks_w2, ks_out, ks_kv, ks_tau;
@@ -647,23 +404,144 @@ WS carve(const Plan& p, char* base) {
   return w;
 }
 
-template <int SRC>
-int launch_gemv(const GemvArgs& a, int rows_max, hipStream_t st) {
-  if (a.tiles % WPB != 0) return CFH_E_UNSUPPORTED;
-  const size_t lds = lds_bytes(rows_max, a.K / a.ks);
-  if (lds > 64 * 1024) return CFH_E_UNSUPPORTED;
-  const long long units = (long long)a.nex * a.nl * a.ks * a.tiles;
-  hipLaunchKernelGGL(k_gemv<SRC>, dim3((unsigned)(units / WPB)), dim3(WPB * 64), lds, st, a);
-  CFH_LAUNCH_CHECK();
-  return CFH_OK;
-}
-
 int launch_attn(const AttnArgs& a, int nex, int sq_max, int sk_max, hipStream_t st) {
   const size_t lds = (size_t)(sq_max + 2 * sk_max) * a.hd * 2;
   if (lds > 120 * 1024 || sq_max > MAXR || sk_max > MAXR) return CFH_E_UNSUPPORTED;
   hipLaunchKernelGGL(k_attn, dim3(nex * a.heads), dim3(1024), lds, st, a);
   CFH_LAUNCH_CHECK();
   return CFH_OK;
+}
+
+
+// One launch of one chunk expert's Euler step.  Kernel k of block l (k = 0..11):
+//   0 QKV, 1 self attention, 2 O, 3 NORM(LN_cross), 4 QC, 5 cross attention, 6 OC, 7 NORM(LN_ffn),
+//   8 W1, 9 GELU, 10 W2, 11 NORM(next LN);  l == NL, k == 0: out_proj on the current chunk rows.
+constexpr int KPB = 12;   // kernels per block and expert
+
+int expert_kernel(const Plan& p, const cfh::ExpertLayout& L, const WS& w, const void* expert, int c, int l,
+                  int k, hipStream_t st) {
+  const int d = p.d, fd = p.fd, CS = p.CS, NL = p.NL, C = p.C, H = p.H;
+  const int S = (c + 1) * CS;
+  auto PTR = [&](size_t off) { return (const char*)expert + off; };
+  auto BLK = [&](int ll) { return L.blk0 + (size_t)ll * L.blkstride; };
+  if (l == NL) {
+    GemvArgs a = {};
+    a.nex = 1; a.nl = 1; a.E = p.E; a.ks = p.ks_out; a.tiles = d / 16; a.N = d; a.K = d;
+    GemvEx& x = a.ex[0];
+    x.w = (const h16x8*)PTR(L.out);
+    x.a = w.abuf[c] + (size_t)c * CS * d;   // out_norm rows of the current chunk
+    x.lda = d; x.pout = w.P[c]; x.rows = CS;
+    return launch_gemv<SRC_BUF>(a, CS, st);
+  }
+  const size_t B = BLK(l);
+  GemvArgs a = {};
+  a.nex = 1; a.nl = 1; a.E = p.E;
+  GemvEx& x = a.ex[0];
+  x.lda = d; x.pout = w.P[c]; x.rows = S;
+  AttnArgs at = {};
+  at.d = d; at.heads = H; at.hd = d / H; at.P[0] = w.P[c]; at.out[0] = w.attn[c]; at.Sq[0] = S;
+  NormArgs nm = {};
+  nm.nex = 1; nm.d = d; nm.x[0] = w.x[c]; nm.P[0] = w.P[c]; nm.a[0] = w.abuf[c]; nm.rows[0] = S;
+  switch (k) {
+    case 0:  // QKV
+      a.ks = p.ks_qkv; a.tiles = 3 * d / 16; a.N = 3 * d; a.K = d;
+      x.w = (const h16x8*)PTR(B + L.qkv); x.a = w.abuf[c];
+      return launch_gemv<SRC_BUF>(a, S, st);
+    case 1:  // causal self attention
+      at.ks = p.ks_qkv; at.ldp = 3 * d; at.causal = 1; at.bias[0] = (const h16*)PTR(B + L.qkv_b);
+      at.kv[0] = nullptr; at.Sk[0] = S;
+      return launch_attn(at, 1, S, S, st);
+    case 2:  // O
+      a.ks = p.ks_o; a.tiles = d / 16; a.N = d; a.K = d;
+      x.w = (const h16x8*)PTR(B + L.o); x.a = w.attn[c];
+      return launch_gemv<SRC_BUF>(a, S, st);
+    case 3:  // residual + LN_cross
+      nm.ks = p.ks_o; nm.bias[0] = (const h16*)PTR(B + L.o_b);
+      nm.g[0] = (const h16*)PTR(B + L.xn_w); nm.b[0] = (const h16*)PTR(B + L.xn_b);
+      hipLaunchKernelGGL(k_norm, dim3(S), dim3(ROWT), 0, st, nm);
+      CFH_LAUNCH_CHECK();
+      return CFH_OK;
+    case 4:  // QC
+      a.ks = p.ks_o; a.tiles = d / 16; a.N = d; a.K = d;
+      x.w = (const h16x8*)PTR(B + L.qc); x.a = w.abuf[c];
+      return launch_gemv<SRC_BUF>(a, S, st);
+    case 5:  // cross attention over the hoisted context K/V
+      at.ks = p.ks_o; at.ldp = d; at.causal = 0; at.bias[0] = (const h16*)PTR(B + L.qc_b);
+      at.kv[0] = w.kvc[c] + (size_t)l * 2 * C * d; at.Sk[0] = C;
+      return launch_attn(at, 1, S, C, st);
+    case 6:  // OC
+      a.ks = p.ks_o; a.tiles = d / 16; a.N = d; a.K = d;
+      x.w = (const h16x8*)PTR(B + L.oc); x.a = w.attn[c];
+      return launch_gemv<SRC_BUF>(a, S, st);
+    case 7:  // residual + LN_ffn
+      nm.ks = p.ks_o; nm.bias[0] = (const h16*)PTR(B + L.oc_b);
+      nm.g[0] = (const h16*)PTR(B + L.fn_w); nm.b[0] = (const h16*)PTR(B + L.fn_b);
+      hipLaunchKernelGGL(k_norm, dim3(S), dim3(ROWT), 0, st, nm);
+      CFH_LAUNCH_CHECK();
+      return CFH_OK;
+    case 8:  // W1
+      a.ks = p.ks_w1; a.tiles = fd / 16; a.N = fd; a.K = d;
+      x.w = (const h16x8*)PTR(B + L.w1); x.a = w.abuf[c]; x.pout = w.Pw1[c];
+      return launch_gemv<SRC_BUF>(a, S, st);
+    case 9: {  // GELU
+      GeluArgs ge = {};
+      ge.nex = 1; ge.ks = p.ks_w1; ge.N = fd;
+      ge.P[0] = w.Pw1[c]; ge.b[0] = (const h16*)PTR(B + L.w1_b); ge.g[0] = w.g[c]; ge.rows[0] = S;
+      hipLaunchKernelGGL(k_gelu, dim3(192), dim3(256), 0, st, ge);
+      CFH_LAUNCH_CHECK();
+      return CFH_OK;
+    }
+    case 10:  // W2
+      a.ks = p.ks_w2; a.tiles = d / 16; a.N = d; a.K = fd;
+      x.w = (const h16x8*)PTR(B + L.w2); x.a = w.g[c]; x.lda = fd;
+      return launch_gemv<SRC_BUF>(a, S, st);
+    case 11:  // residual + LayerNorm of the next block (out_norm after the last block)
+      nm.ks = p.ks_w2; nm.bias[0] = (const h16*)PTR(B + L.w2_b);
+      if (l + 1 < NL) {
+        nm.g[0] = (const h16*)PTR(BLK(l + 1) + L.sn_w); nm.b[0] = (const h16*)PTR(BLK(l + 1) + L.sn_b);
+      } else {
+        nm.g[0] = (const h16*)PTR(L.on_w); nm.b[0] = (const h16*)PTR(L.on_b);
+      }
+      hipLaunchKernelGGL(k_norm, dim3(S), dim3(ROWT), 0, st, nm);
+      CFH_LAUNCH_CHECK();
+      return CFH_OK;
+  }
+  return CFH_E_INVALID;
+}
+
+// Side streams and fork/join events (one set per device, created on first use).
+struct SideStreams {
+  hipStream_t st[4];
+  hipEvent_t fork;
+  hipEvent_t join[4];
+};
+
+SideStreams* side_streams(int* status) {
+  static SideStreams cache[64];
+  static bool made[64];
+  static std::mutex mu;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= 64) {
+    *status = cfh::set_hip_error(e == hipSuccess ? hipErrorInvalidDevice : e);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  SideStreams& s = cache[dev];
+  if (!made[dev]) {
+    s.st[0] = nullptr;
+    for (int c = 1; c < 4; ++c)
+      if ((e = hipStreamCreateWithFlags(&s.st[c], hipStreamNonBlocking)) != hipSuccess) break;
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&s.fork, hipEventDisableTiming);
+    for (int c = 0; c < 4 && e == hipSuccess; ++c) e = hipEventCreateWithFlags(&s.join[c], hipEventDisableTiming);
+    if (e != hipSuccess) {
+      *status = cfh::set_hip_error(e);
+      return nullptr;
+    }
+    made[dev] = true;
+  }
+  *status = CFH_OK;
+  return &s;
 }
 
 }  // namespace
@@ -689,11 +567,12 @@ int cfh_flow_integrate(const cfh_flow_dims* dm, const void* const* experts, cons
   hipStream_t st = (hipStream_t)stream;
   const cfh::ExpertLayout L = cfh::expert_layout(dm);
   const WS w = carve(p, (char*)ws_ptr);
-  const int d = p.d, fd = p.fd, CS = p.CS, E = p.E, NL = p.NL, C = p.C, KD = p.KD, H = p.H, nch = p.nch;
+  const int d = p.d, CS = p.CS, E = p.E, NL = p.NL, C = p.C, KD = p.KD, nch = p.nch;
+  int rc = CFH_OK;
+  SideStreams* side = nullptr;
+  if (nch > 1 && !(side = side_streams(&rc))) return rc;
   auto PTR = [&](int c, size_t off) { return (const char*)experts[c] + off; };
   auto BLK = [&](int l) { return L.blk0 + (size_t)l * L.blkstride; };
-  auto S_of = [&](int c) { return (c + 1) * CS; };
-  int rc;
 
   for (int b = 0; b < batch; ++b) {
     const h16* ctx_b = (const h16*)ctx + (size_t)b * C * d;
@@ -763,123 +642,38 @@ int cfh_flow_integrate(const cfh_flow_dims* dm, const void* const* experts, cons
       CFH_LAUNCH_CHECK();
     }
     for (int s = 0; s < E; ++s) {
-      for (int l = 0; l < NL; ++l) {
-        const size_t B = BLK(l);
-        // ---- QKV
-        GemvArgs a = {};
-        a.nex = nch; a.nl = 1; a.E = E;
-        a.ks = p.ks_qkv; a.tiles = 3 * d / 16; a.N = 3 * d; a.K = d;
-        for (int c = 0; c < nch; ++c) {
-          GemvEx& x = a.ex[c];
-          x.w = (const h16x8*)PTR(c, B + L.qkv); x.a = w.abuf[c]; x.lda = d; x.pout = w.P[c]; x.rows = S_of(c);
-        }
-        if ((rc = launch_gemv<SRC_BUF>(a, KD, st))) return rc;
-        AttnArgs at = {};
-        at.ks = p.ks_qkv; at.ldp = 3 * d; at.d = d; at.heads = H; at.hd = d / H; at.causal = 1;
-        for (int c = 0; c < nch; ++c) {
-          at.P[c] = w.P[c]; at.bias[c] = (const h16*)PTR(c, B + L.qkv_b); at.kv[c] = nullptr;
-          at.out[c] = w.attn[c]; at.Sq[c] = at.Sk[c] = S_of(c);
-        }
-        if ((rc = launch_attn(at, nch, KD, KD, st))) return rc;
-        // ---- O + residual, LN_cross
-        a.ks = p.ks_o; a.tiles = d / 16; a.N = d; a.K = d;
-        for (int c = 0; c < nch; ++c) {
-          GemvEx& x = a.ex[c];
-          x.w = (const h16x8*)PTR(c, B + L.o); x.a = w.attn[c]; x.lda = d; x.pout = w.P[c];
-        }
-        if ((rc = launch_gemv<SRC_BUF>(a, KD, st))) return rc;
-        NormArgs nm = {};
-        nm.nex = nch; nm.ks = p.ks_o; nm.d = d;
-        int nrows = 0;
-        for (int c = 0; c < nch; ++c) {
-          nm.x[c] = w.x[c]; nm.P[c] = w.P[c]; nm.bias[c] = (const h16*)PTR(c, B + L.o_b);
-          nm.g[c] = (const h16*)PTR(c, B + L.xn_w); nm.b[c] = (const h16*)PTR(c, B + L.xn_b);
-          nm.a[c] = w.abuf[c]; nm.rows[c] = S_of(c); nrows += S_of(c);
-        }
-        hipLaunchKernelGGL(k_norm, dim3(nrows), dim3(ROWT), 0, st, nm);
-        CFH_LAUNCH_CHECK();
-        // ---- QC + cross attention
-        a.ks = p.ks_o;
-        for (int c = 0; c < nch; ++c) {
-          GemvEx& x = a.ex[c];
-          x.w = (const h16x8*)PTR(c, B + L.qc); x.a = w.abuf[c]; x.lda = d; x.pout = w.P[c];
-        }
-        if ((rc = launch_gemv<SRC_BUF>(a, KD, st))) return rc;
-        at.ks = p.ks_o; at.ldp = d; at.causal = 0;
-        for (int c = 0; c < nch; ++c) {
-          at.P[c] = w.P[c]; at.bias[c] = (const h16*)PTR(c, B + L.qc_b);
-          at.kv[c] = w.kvc[c] + (size_t)l * 2 * C * d; at.Sk[c] = C;
-        }
-        if ((rc = launch_attn(at, nch, KD, C, st))) return rc;
-        // ---- OC + residual, LN_ffn
-        for (int c = 0; c < nch; ++c) {
-          GemvEx& x = a.ex[c];
-          x.w = (const h16x8*)PTR(c, B + L.oc); x.a = w.attn[c]; x.lda = d; x.pout = w.P[c];
-        }
-        if ((rc = launch_gemv<SRC_BUF>(a, KD, st))) return rc;
-        for (int c = 0; c < nch; ++c) {
-          nm.bias[c] = (const h16*)PTR(c, B + L.oc_b);
-          nm.g[c] = (const h16*)PTR(c, B + L.fn_w); nm.b[c] = (const h16*)PTR(c, B + L.fn_b);
-        }
-        hipLaunchKernelGGL(k_norm, dim3(nrows), dim3(ROWT), 0, st, nm);
-        CFH_LAUNCH_CHECK();
-        // ---- W1, GELU
-        a.ks = p.ks_w1; a.tiles = fd / 16; a.N = fd; a.K = d;
-        for (int c = 0; c < nch; ++c) {
-          GemvEx& x = a.ex[c];
-          x.w = (const h16x8*)PTR(c, B + L.w1); x.a = w.abuf[c]; x.lda = d; x.pout = w.Pw1[c];
-        }
-        if ((rc = launch_gemv<SRC_BUF>(a, KD, st))) return rc;
-        GeluArgs ge = {};
-        ge.nex = nch; ge.ks = p.ks_w1; ge.N = fd;
-        for (int c = 0; c < nch; ++c) {
-          ge.P[c] = w.Pw1[c]; ge.b[c] = (const h16*)PTR(c, B + L.w1_b); ge.g[c] = w.g[c]; ge.rows[c] = S_of(c);
-        }
-        hipLaunchKernelGGL(k_gelu, dim3(384), dim3(256), 0, st, ge);
-        CFH_LAUNCH_CHECK();
-        // ---- W2 + residual, next LayerNorm
-        a.ks = p.ks_w2; a.tiles = d / 16; a.N = d; a.K = fd;
-        for (int c = 0; c < nch; ++c) {
-          GemvEx& x = a.ex[c];
-          x.w = (const h16x8*)PTR(c, B + L.w2); x.a = w.g[c]; x.lda = fd; x.pout = w.P[c];
-        }
-        if ((rc = launch_gemv<SRC_BUF>(a, KD, st))) return rc;
-        nm.ks = p.ks_w2;
-        for (int c = 0; c < nch; ++c) {
-          nm.bias[c] = (const h16*)PTR(c, B + L.w2_b);
-          if (l + 1 < NL) {
-            nm.g[c] = (const h16*)PTR(c, BLK(l + 1) + L.sn_w); nm.b[c] = (const h16*)PTR(c, BLK(l + 1) + L.sn_b);
-          } else {
-            nm.g[c] = (const h16*)PTR(c, L.on_w); nm.b[c] = (const h16*)PTR(c, L.on_b);
-          }
-        }
-        hipLaunchKernelGGL(k_norm, dim3(nrows), dim3(ROWT), 0, st, nm);
-        CFH_LAUNCH_CHECK();
+      // The chunk experts are independent within an Euler step (their inputs are slices of the
+      // step's z): expert 0 runs on the caller's stream, the others on side streams, so one
+      // expert's boundary kernels overlap the other's weight streaming.  Join before the update.
+      if (nch > 1) {
+        CFH_HIP(hipEventRecord(side->fork, st));
+        for (int c = 1; c < nch; ++c) CFH_HIP(hipStreamWaitEvent(side->st[c], side->fork, 0));
       }
-      // ---- OUT (current chunk rows) and the Euler update / next rows
-      {
-        GemvArgs a = {};
-        a.nex = nch; a.nl = 1; a.E = E; a.ks = p.ks_out; a.tiles = d / 16; a.N = d; a.K = d;
-        for (int c = 0; c < nch; ++c) {
-          GemvEx& x = a.ex[c];
-          x.w = (const h16x8*)PTR(c, L.out);
-          x.a = w.abuf[c] + (size_t)c * CS * d;   // out_norm rows of the current chunk
-          x.lda = d; x.pout = w.P[c]; x.rows = CS;
-        }
-        if ((rc = launch_gemv<SRC_BUF>(a, CS, st))) return rc;
-        RowsArgs r = {};
-        r.ctx = ctx_b; r.z = w.z; r.z_out = zo_b; r.euler = 1; r.last = (s + 1 == E); r.ks = p.ks_out;
-        r.dt = 1.0f / (float)E; r.d = d; r.C = C; r.CS = CS; r.nch = nch;
-        for (int c = 0; c < nch; ++c) {
-          r.Pout[c] = w.P[c]; r.bout[c] = (const h16*)PTR(c, L.out_b);
-          r.x[c] = w.x[c]; r.pos[c] = (const h16*)PTR(c, L.pos);
-          r.tau[c] = w.tau[c] + (size_t)(s + 1 < E ? s + 1 : s) * d;
-          r.g[c] = (const h16*)PTR(c, BLK(0) + L.sn_w); r.b[c] = (const h16*)PTR(c, BLK(0) + L.sn_b);
-          r.a[c] = w.abuf[c];
-        }
-        hipLaunchKernelGGL(k_rows, dim3(KD), dim3(ROWT), 0, st, r);
-        CFH_LAUNCH_CHECK();
+      // Launches alternate between the experts' streams, kernel by kernel.
+      for (int l = 0; l <= NL; ++l) {
+        const int nk = l < NL ? KPB : 1;
+        for (int k = 0; k < nk; ++k)
+          for (int c = 0; c < nch; ++c)
+            if ((rc = expert_kernel(p, L, w, experts[c], c, l, k, c == 0 ? st : side->st[c]))) return rc;
       }
+      if (nch > 1) {
+        for (int c = 1; c < nch; ++c) {
+          CFH_HIP(hipEventRecord(side->join[c], side->st[c]));
+          CFH_HIP(hipStreamWaitEvent(st, side->join[c], 0));
+        }
+      }
+      RowsArgs r = {};
+      r.ctx = ctx_b; r.z = w.z; r.z_out = zo_b; r.euler = 1; r.last = (s + 1 == E); r.ks = p.ks_out;
+      r.dt = 1.0f / (float)E; r.d = d; r.C = C; r.CS = CS; r.nch = nch;
+      for (int c = 0; c < nch; ++c) {
+        r.Pout[c] = w.P[c]; r.bout[c] = (const h16*)PTR(c, L.out_b);
+        r.x[c] = w.x[c]; r.pos[c] = (const h16*)PTR(c, L.pos);
+        r.tau[c] = w.tau[c] + (size_t)(s + 1 < E ? s + 1 : s) * d;
+        r.g[c] = (const h16*)PTR(c, BLK(0) + L.sn_w); r.b[c] = (const h16*)PTR(c, BLK(0) + L.sn_b);
+        r.a[c] = w.abuf[c];
+      }
+      hipLaunchKernelGGL(k_rows, dim3(KD), dim3(ROWT), 0, st, r);
+      CFH_LAUNCH_CHECK();
     }
   }
   return CFH_OK;

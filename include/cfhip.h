@@ -85,14 +85,15 @@ int cfh_flow_integrate(const cfh_flow_dims* dims, const void* const* experts, co
                        void* z_out, void* ws, int batch, void* stream);
 
 /* ---------------------------------------------------------------- shortlisted lm_head
- * logits[m][j] = fp16( fp16(h[m] . W[row_j]) + fp16(a[m] . W2[row_j]) ),  row_j = sl ? sl[j] : j
- *   h [M][d] fp16, W [V][d] fp16 (the target's full lm_head; rows gathered through sl),
- *   a [M][r] fp16 / W2 [V][r] fp16 optional markov bias (both NULL = none), M <= 16.
- *   logits [M][n] fp16.
- * Replaces FlowDrafterProposer._head + _bias (cf/vllm_plugin/flow_proposer.py:1021-1025) with a
- * row-gather GEMV over the int32 shortlist (no gathered copy of lm_w[sl]). */
+ * logits[m][j] = fp16( fp16(h[m] . W[row_j]) + fp16(A[m] . W2[row_j]) ),  row_j = sl ? sl[j] : j
+ *   h [M][d] fp16 (M <= 8, d % 256 == 0); W [V][d] fp16: the target's full lm_head, its shortlist
+ *   rows read in place through the int32 shortlist sl [n] (no gathered copy of lm_w[sl]);
+ *   markov bias (a, W2 NULL = none): A[m] = a[a_ids[m * a_ids_stride]] when a_ids is set (a = the
+ *   w1 table [V][r]) else a[m] ([M][r] fp16); W2 [V][r] fp16, r % 256 == 0.  logits [M][n] fp16.
+ * Replaces FlowDrafterProposer._head + _bias (cf/vllm_plugin/flow_proposer.py:1021-1025, 739-740). */
 int cfh_head_logits(const void* h, int M, int d, const void* W, const int32_t* sl, int n,
-                    const void* a, int r, const void* W2, void* logits, void* stream);
+                    const void* a, const int32_t* a_ids, int a_ids_stride, int r, const void* W2,
+                    void* logits, void* stream);
 
 /* Per-row log-softmax top-k of fp16 logits [M][n]: vals[m][i] = logit - logsumexp (fp32),
  * ids[m][i] = column, descending, ties to the lower column; lse[m] (may be NULL).  k <= 16.
@@ -102,8 +103,8 @@ int cfh_row_topk(const void* logits, int M, int n, int k, float* vals, int32_t* 
 
 /* cfh_head_logits followed by cfh_row_topk; `logits` is caller scratch [M][n] fp16. */
 int cfh_head_topk(const void* h, int M, int d, const void* W, const int32_t* sl, int n,
-                  const void* a, int r, const void* W2, int k, void* logits, float* vals,
-                  int32_t* ids, float* lse, void* stream);
+                  const void* a, const int32_t* a_ids, int a_ids_stride, int r, const void* W2, int k,
+                  void* logits, float* vals, int32_t* ids, float* lse, void* stream);
 
 /* Batched (M up to 256) bf16 skinny-GEMM head with per-row top-k: the two-pass candidate head's
  * pass A (cf/vllm_plugin/flow_proposer.py:1142-1165) as one MFMA kernel.
@@ -113,17 +114,40 @@ int cfh_head_gemm_topk(const void* x, int M, int d, const void* W, const int32_t
                        void* logits, float* vals, int32_t* ids, float* lse, void* stream);
 
 /* ---------------------------------------------------------------- draft search
- * Path-conditioned residual of the PathHead, fused form (cf/vllm_plugin/fused.py:25-37):
- *   hsum[m] = fp16( pred + MLP(LN( sum_{j<nlive} mask_j (W_j emb(lastp[m][j]) + b_j) )) )
- * with emb = embed_w rows of the global ids in lastp [M][order] (int32, -1 = no ancestor).
- * ph = path head fp16 parameters, device pointers in this order:
- *   offset_proj.{0..order-1}.weight (each [d][d]), offset_proj.{0..order-1}.bias,
- *   norm.weight, norm.bias, mlp.0.weight [f*d][d], mlp.0.bias, mlp.3.weight [d][f*d], mlp.3.bias
- * pred [d] fp16 (the marginal hidden of this depth, shared by the M rows). ws: cfh_path_ws_bytes. */
+ * Path-conditioned residual of the PathHead, fused form (cf/vllm_plugin/fused.py:25-37;
+ * un-fused twin cf/drafters/tree_flow.py:434-450):
+ *   hsum[m] = fp16( pred + MLP(LN( fp16(sum_{j<nlive} mask_j fp16(W_j emb(lastp[m][j]) + b_j)) )) )
+ * with emb = embed_w rows [V][d] of the global ids in lastp [M][order] (int32, -1 = no ancestor,
+ * mask_j = lastp[m][j] >= 0), nlive = live offsets at this depth (_nlive, :1030-1037).
+ * ph = path head fp16 parameters (2*order + 6 device pointers), matrices PACKED (cfh_pack_linear):
+ *   offset_proj.{0..order-1}.weight [d][d], offset_proj.{0..order-1}.bias [d], norm.weight,
+ *   norm.bias, mlp.0.weight [f*d][d], mlp.0.bias [f*d], mlp.3.weight [d][f*d], mlp.3.bias [d].
+ * pred [d] fp16 = the marginal hidden of this depth, shared by the M rows.  ws: cfh_path_ws_bytes. */
 int64_t cfh_path_ws_bytes(int M, int d, int ffn_mult, int order);
 int cfh_path_residual(const void* const* ph, int order, int ffn_mult, int d, const int32_t* lastp,
                       int M, int nlive, const void* embed_w, const void* pred, void* hsum, void* ws,
                       void* stream);
+
+/* One depth of _beam_chains (cf/vllm_plugin/flow_proposer.py:1250-1259) for B chains of width W
+ * (W*W <= 64): from the per-beam top-W rows vals/ids [B*W][W] (log-probs, shortlist-local ids),
+ * cand = cum[b][w] + vals; (cum, flat) = top-W(cand) (ties to the lower flat index);
+ * toks[b][w] = sl[ids[src][flat % W]] (global id), bps[b][w] = src = flat / W;
+ * lastp[b][w] = [toks, lastp[b][src][0..order-2]].  cum [B][W] and lastp [B][W][order] in place. */
+int cfh_beam_chain_step(const float* vals, const int32_t* ids, float* cum, int32_t* lastp,
+                        const int32_t* sl, int32_t* toks, int32_t* bps, int B, int W, int order,
+                        void* stream);
+
+/* One depth of _beam_tree (:1300-1330): F live frontier slots, topb children each, keep the best
+ * k = min(keep, F*topb); writes node tokens to out[b][base + i] and parent node indices to
+ * out[b][ld_out/2 + base + i]; cum/lastp/prev_ids are [B][keep](...) frontier arrays, updated. */
+int cfh_beam_tree_step(const float* vals, const int32_t* ids, float* cum, int32_t* lastp,
+                       int32_t* prev_ids, const int32_t* sl, int32_t* out, int ld_out, int base,
+                       int B, int F, int topb, int keep, int order, void* stream);
+
+/* Backtrack of _beam_chains (:1261-1267): idx = first arg-max of cum [B][W]; for each depth s from
+ * the last, out[b][s] = toks[s][b][idx], idx = bps[s][b][idx].  toks/bps [K][B][W]. */
+int cfh_beam_backtrack(const float* cum, const int32_t* toks, const int32_t* bps, int B, int W, int K,
+                       int64_t* out, void* stream);
 
 /* ---------------------------------------------------------------- tree gated delta net
  * tree_gated_delta_scan (cf/kernels/tree_scan.py:41-73): per node n (BFS order, parent[n] < n,

@@ -1,0 +1,201 @@
+"""GPU parity of the draft head: shortlisted lm_head + markov bias, top-k, path residual, beam steps.
+
+Contracts: fp16 logits equal to the oracle's within one fp16 ulp; top-k ids bit-exact on identical
+logits (ties to the lower index) and log-prob values within 1e-5; path residual within 2e-3
+norm-relative; beam steps bit-exact on identical inputs; end-to-end draft ids equal to the oracle's
+wherever the oracle's decision margin exceeds 1e-3.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_err, to64
+from chain_flow_amd.config import flownet
+from chain_flow_amd.head import PathHead, ShortlistHead, row_topk
+from chain_flow_amd.weights import make_weights, param_specs
+from oracle import beam as obeam
+from oracle import head as ohead
+
+MARGIN = 1e-3
+
+
+def _head_weights(d, V, seed=0, scale=8.0):
+    cfg = flownet(d, layers=1, flow_steps=1)
+    names = {n for n in param_specs(cfg, V) if n.startswith(("markov.", "path_head.", "lm_head", "embed_tokens"))}
+    W = make_weights(cfg, V, init="test", base_seed=seed, names=names)
+    W["lm_head.weight"] = (W["lm_head.weight"].float() * scale).half()
+    return cfg, W
+
+
+def _shortlist(V, n, seed=2):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randperm(V, generator=g)[:n].sort().values.to(torch.int32)
+
+
+def _ulp16(x):
+    x = np.abs(np.asarray(x, dtype=np.float64))
+    e = np.floor(np.log2(np.maximum(x, 2.0 ** -14)))
+    return 2.0 ** (e - 10)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M", [1, 4, 8])
+def test_head_logits_match_oracle(cuda, M):
+    d, V, n = 512, 4096, 1024
+    cfg, W = _head_weights(d, V)
+    sl = _shortlist(V, n)
+    g = torch.Generator().manual_seed(7)
+    h = torch.randn(M, d, generator=g).half()
+    prev = torch.randint(0, V, (M,), generator=g, dtype=torch.int32)
+    head = ShortlistHead(W["lm_head.weight"].to(cuda), sl.to(cuda), W["markov.w1.weight"].to(cuda),
+                         W["markov.w2.weight"].to(cuda))
+    got = to64(head.logits(h.to(cuda), prev.to(cuda)))
+    sl64 = sl.long().numpy()
+    ref = ohead.head_with_bias(to64(h), to64(W["lm_head.weight"])[sl64], to64(W["markov.w1.weight"]),
+                               to64(W["markov.w2.weight"])[sl64], prev.long().numpy())
+    diff = np.abs(got - ref)
+    assert (diff <= 2 * _ulp16(ref) + 1e-12).all(), diff.max()
+    assert (diff > 0).mean() < 0.02
+
+
+@pytest.mark.gpu
+def test_full_head_restricted_equals_shortlist_head(cuda):
+    """A full head restricted to the shortlist columns is the shortlist head (same rows, same sums)."""
+    d, V, n = 512, 4096, 1024
+    cfg, W = _head_weights(d, V)
+    sl = _shortlist(V, n)
+    h = torch.randn(4, d, generator=torch.Generator().manual_seed(3)).half().to(cuda)
+    full = ShortlistHead(W["lm_head.weight"].to(cuda), None).logits(h)
+    short = ShortlistHead(W["lm_head.weight"].to(cuda), sl.to(cuda)).logits(h)
+    assert torch.equal(full[:, sl.long().to(cuda)], short)
+
+
+@pytest.mark.gpu
+def test_identity_rows_give_coordinates(cuda):
+    """Head rows equal to unit vectors make the logits equal to h's coordinates."""
+    d = 512
+    lm = torch.zeros(d, d, dtype=torch.float16)
+    lm[torch.arange(d), torch.arange(d)] = 1.0
+    sl = torch.arange(0, d, 3, dtype=torch.int32)
+    h = torch.randn(2, d, generator=torch.Generator().manual_seed(4)).half()
+    got = ShortlistHead(lm.to(cuda), sl.to(cuda)).logits(h.to(cuda)).cpu()
+    assert torch.equal(got, h[:, sl.long()])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("k", [1, 4, 8, 16])
+def test_row_topk_bit_exact(cuda, k):
+    g = torch.Generator().manual_seed(11)
+    M, n = 6, 62642
+    logits = (torch.randn(M, n, generator=g) * 3).half()
+    logits[:, 100:140] = logits[:, 100:101]           # plant ties: equal values, lower index first
+    logits[2, :] = 1.0                                # a row made only of ties
+    vals, ids, lse = row_topk(logits.to(cuda), k)
+    L = to64(logits)
+    ref_lp = ohead.log_softmax(L)
+    rv, ri = ohead.topk(ref_lp, k)
+    assert np.array_equal(ids.cpu().numpy(), ri)
+    assert np.allclose(vals.cpu().numpy(), rv, atol=1e-5, rtol=0)
+    m = L.max(-1)
+    assert np.allclose(lse.cpu().numpy(), m + np.log(np.exp(L - m[:, None]).sum(-1)), atol=1e-5)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("nlive", [1, 2, 3, 4])
+def test_path_residual_matches_oracle(cuda, nlive):
+    d, V = 512, 4096
+    cfg, W = _head_weights(d, V)
+    ph = PathHead({k: v.to(cuda) for k, v in W.items()}, W["embed_tokens.weight"].to(cuda), cfg.path_order,
+                  cfg.path_ffn_multiplier, cuda)
+    g = torch.Generator().manual_seed(5)
+    M = 4
+    lastp = torch.randint(0, V, (M, cfg.path_order), generator=g, dtype=torch.int32)
+    lastp[1, 2:] = -1
+    lastp[3, 1:] = -1
+    pred = torch.randn(d, generator=g).half()
+    got = to64(ph.hidden(lastp.to(cuda), nlive, pred.to(cuda)))
+    W64 = {k: to64(v) for k, v in W.items() if k.startswith("path_head.")}
+    res = ohead.path_residual(W64, to64(W["embed_tokens.weight"]), lastp.long().numpy(), nlive, cfg.path_order)
+    ref = ohead.r16(to64(pred)[None] + res, "fp16")
+    assert rel_err(got, ref) < 2e-3
+
+
+def _np_chain_step(vals, ids, cum, lastp, sl, W):
+    B = cum.shape[0]
+    cand = (cum.reshape(B * W, 1) + vals).reshape(B, W * W)
+    ncum, flat = ohead.topk(cand, W)
+    src = flat // W
+    newtok = sl[np.take_along_axis(ids.reshape(B, W * W), flat, 1)]
+    lp = np.take_along_axis(lastp, src[:, :, None], 1)
+    lp = np.concatenate([newtok[:, :, None], lp[:, :, :-1]], -1)
+    return ncum, lp, newtok, src
+
+
+@pytest.mark.gpu
+def test_beam_chain_step_bit_exact(cuda):
+    from chain_flow_amd import _lib
+    rng = np.random.default_rng(0)
+    B, W, order, n = 3, 4, 4, 500
+    sl = np.sort(rng.choice(10000, n, replace=False)).astype(np.int32)
+    vals = np.round(rng.normal(size=(B * W, W)) * 4, 1).astype(np.float32)   # coarse -> ties
+    ids = rng.integers(0, n, size=(B * W, W)).astype(np.int32)
+    cum = np.round(rng.normal(size=(B, W)), 1).astype(np.float32)
+    cum[1, 1:] = -np.inf
+    lastp = rng.integers(-1, 10000, size=(B, W, order)).astype(np.int32)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+    # every device buffer stays referenced until the asynchronous kernel has run
+    vals_d, ids_d, sl_d, cum_d, lastp_d = t(vals), t(ids), t(sl), t(cum), t(lastp)
+    toks = torch.empty(B, W, dtype=torch.int32, device=cuda)
+    bps = torch.empty_like(toks)
+    _lib.check(_lib.lib().cfh_beam_chain_step(vals_d.data_ptr(), ids_d.data_ptr(), cum_d.data_ptr(),
+                                              lastp_d.data_ptr(), sl_d.data_ptr(), toks.data_ptr(), bps.data_ptr(),
+                                              B, W, order, _lib.stream_handle()), "step")
+    torch.cuda.synchronize()
+    ncum, nlp, ntok, nsrc = _np_chain_step(vals, ids, cum, lastp, sl, W)   # float32, as on the device
+    assert np.array_equal(cum_d.cpu().numpy(), ncum.astype(np.float32))
+    assert np.array_equal(lastp_d.cpu().numpy(), nlp)
+    assert np.array_equal(toks.cpu().numpy(), ntok)
+    assert np.array_equal(bps.cpu().numpy(), nsrc)
+
+
+def _near_tie(trace, W):
+    """True when any beam decision of the oracle (per-beam top-W of the log-probs, top-W over the
+    W*W candidates, or the final best-beam arg-max) had a margin <= MARGIN: the backtracked chain
+    depends on every one of them."""
+    for tr in trace:
+        if (ohead.margins(tr["lp"], W) <= MARGIN).any():
+            return True
+        if (ohead.margins(tr["cand"], W) <= MARGIN).any():
+            return True
+    if (ohead.margins(trace[-1]["cum"], 1) <= MARGIN).any():
+        return True
+    return False
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_beam_chains_match_oracle(cuda, seed):
+    from chain_flow_amd.drafter import Drafter
+    d, V, n, K, Wd = 512, 4096, 1024, 5, 4
+    cfg = flownet(d, layers=1, flow_steps=1)
+    W = make_weights(cfg, V, init="test", base_seed=seed)
+    W["lm_head.weight"] = (W["lm_head.weight"].float() * 8).half()
+    sl = _shortlist(V, n, seed=seed + 2)
+    dr = Drafter(cfg, {k: v.to(cuda) for k, v in W.items()}, sl.to(cuda), device=cuda)
+    g = torch.Generator().manual_seed(100 + seed)
+    pred = torch.randn(1, cfg.draft_length, d, generator=g).half()
+    known0 = torch.tensor([int(sl[7])])
+    got = dr.beam_chains(None, known0.to(cuda), K, Wd, pred=pred.to(cuda)).cpu().numpy()[0]
+    W64 = {k: to64(v) for k, v in W.items()}
+    sl64 = sl.long().numpy()
+    score = lambda h, prev: ohead.head_with_bias(h, W64["lm_head.weight"][sl64], W64["markov.w1.weight"],
+                                                 W64["markov.w2.weight"][sl64], prev)
+    resid = lambda lp, nl: ohead.path_residual(W64, W64["embed_tokens.weight"], lp, nl, cfg.path_order)
+    ref, trace = obeam.beam_chains(to64(pred), known0.numpy(), sl64, Wd, K, cfg.path_order, score, resid,
+                                   return_trace=True)
+    ref = ref[0]
+    print(f"[beam chains seed={seed}] gpu {got.tolist()} oracle {ref.tolist()}", flush=True)
+    if not np.array_equal(got, ref):
+        assert _near_tie(trace, Wd), (got, ref)

@@ -36,8 +36,9 @@ SIGNATURES = {
     "cfh_flow_integrate": (_I, [C.POINTER(FlowDims), C.POINTER(_VP), _VP, _VP, _VP, _I, _VP]),
     "cfh_head_logits": (_I, [_VP, _I, _I, _VP, _VP, _I, _VP, _VP, _I, _I, _VP, _VP, _VP]),
     "cfh_row_topk": (_I, [_VP, _I, _I, _I, _VP, _VP, _VP, _VP]),
-    "cfh_head_topk": (_I, [_VP, _I, _I, _VP, _VP, _I, _VP, _VP, _I, _I, _VP, _I, _VP, _VP, _VP, _VP, _VP]),
-    "cfh_head_gemm_topk": (_I, [_VP, _I, _I, _VP, _VP, _I, _I, _VP, _VP, _VP, _VP, _VP]),
+    "cfh_head_ws_bytes": (_I64, [_I, _I, _I]),
+    "cfh_head_topk": (_I, [_VP, _I, _I, _VP, _VP, _I, _VP, _VP, _I, _I, _VP, _I, _VP, _VP, _VP, _VP, _VP, _VP]),
+    "cfh_head_gemm_topk": (_I, [_VP, _I, _I, _VP, _VP, _I, _I, _VP, _VP, _VP, _VP, _VP, _VP]),
     "cfh_path_ws_bytes": (_I64, [_I, _I, _I, _I]),
     "cfh_path_residual": (_I, [C.POINTER(_VP), _I, _I, _I, _VP, _I, _I, _VP, _VP, _VP, _VP, _VP]),
     "cfh_beam_chain_step": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _VP]),

@@ -71,14 +71,12 @@ class Drafter:
         toks = torch.empty(max(nst, 1), B, W, dtype=torch.int32, device=dev)
         bps = torch.empty_like(toks)
         hbuf = torch.empty(B * W, d, dtype=torch.float16, device=dev)
-        logits = torch.empty(B * W, self.head.n, dtype=torch.float16, device=dev)
         L = _lib.lib()
         st = _lib.stream_handle()
         for step in range(1, steps):
             for b in range(B):
                 self.path.hidden(lastp[b], self._nlive(step), pred[b, step], out=hbuf[b * W:(b + 1) * W])
-            vals, ids, _ = self.head.topk(hbuf, W, prev=lastp.view(B * W, order), prev_stride=order,
-                                          logits=logits)
+            vals, ids, _ = self.head.topk(hbuf, W, prev=lastp.view(B * W, order), prev_stride=order)
             _lib.check(L.cfh_beam_chain_step(vals.data_ptr(), ids.data_ptr(), cum.data_ptr(), lastp.data_ptr(),
                                              _lib.ptr(self.head.sl), toks[step - 1].data_ptr(),
                                              bps[step - 1].data_ptr(), B, W, order, st), "cfh_beam_chain_step")
@@ -113,7 +111,6 @@ class Drafter:
         cum = torch.zeros(B, keep, dtype=torch.float32, device=dev)
         prev_ids = torch.full((B, keep), -1, dtype=torch.int32, device=dev)
         hbuf = torch.empty(B * keep, d, dtype=torch.float16, device=dev)
-        logits = torch.empty(B * keep, self.head.n, dtype=torch.float16, device=dev)
         L = _lib.lib()
         st = _lib.stream_handle()
         fr, base = 1, 0
@@ -123,8 +120,7 @@ class Drafter:
             for b in range(B):
                 self.path.hidden(lp_rows[b * fr:(b + 1) * fr], self._nlive(step), pred[b, step],
                                  out=rows[b * fr:(b + 1) * fr])
-            vals, ids, _ = self.head.topk(rows, topb, prev=lp_rows, prev_stride=order,
-                                          logits=logits[:B * fr])
+            vals, ids, _ = self.head.topk(rows, topb, prev=lp_rows, prev_stride=order)
             _lib.check(L.cfh_beam_tree_step(vals.data_ptr(), ids.data_ptr(), cum.data_ptr(), lastp.data_ptr(),
                                             prev_ids.data_ptr(), _lib.ptr(self.head.sl), out.data_ptr(), 2 * N,
                                             base, B, fr, topb, keep, order, st), "cfh_beam_tree_step")

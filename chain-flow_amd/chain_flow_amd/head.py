@@ -35,6 +35,7 @@ class ShortlistHead:
         if (self.w1 is None) != (self.w2 is None):
             raise ValueError("markov w1 and w2 go together")
         self.r = 0 if self.w1 is None else int(self.w1.shape[1])
+        self._ws = {}
 
     def map(self, local: torch.Tensor) -> torch.Tensor:
         """``_map``: shortlist-local column -> global token id."""
@@ -54,23 +55,76 @@ class ShortlistHead:
             "cfh_head_logits")
         return out
 
+    def workspace(self, M: int, k: int, device) -> torch.Tensor:
+        """Candidate workspace for M rows and top-k (kept per shape, reused across calls)."""
+        key = (M, k)
+        ws = self._ws.get(key)
+        if ws is None:
+            nbytes = int(_lib.lib().cfh_head_ws_bytes(M, self.n, k))
+            if nbytes < 0:
+                raise ValueError(f"head top-k shape unsupported: M={M} k={k}")
+            ws = self._ws[key] = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        return ws
+
     def topk(self, h: torch.Tensor, k: int, prev: torch.Tensor | None = None, prev_stride: int = 1,
-             logits: torch.Tensor | None = None):
-        """-> (log-prob values [M, k] f32, shortlist-local ids [M, k] int32, lse [M] f32)."""
+             logits: torch.Tensor | None = None, out=None):
+        """-> (log-prob values [M, k] f32, shortlist-local ids [M, k] int32, lse [M] f32).
+
+        The log-softmax top-k is fused into the head; ``logits`` (fp16 [M, n]) is written only when
+        given.  ``out`` = preallocated (vals, ids, lse) to fill."""
         M = h.shape[0]
         dev = h.device
-        if logits is None:
-            logits = torch.empty(M, self.n, dtype=torch.float16, device=dev)
-        vals = torch.empty(M, k, dtype=torch.float32, device=dev)
-        ids = torch.empty(M, k, dtype=torch.int32, device=dev)
-        lse = torch.empty(M, dtype=torch.float32, device=dev)
+        if out is None:
+            vals = torch.empty(M, k, dtype=torch.float32, device=dev)
+            ids = torch.empty(M, k, dtype=torch.int32, device=dev)
+            lse = torch.empty(M, dtype=torch.float32, device=dev)
+        else:
+            vals, ids, lse = out
         use_m = self.w1 is not None and prev is not None
+        ws = self.workspace(M, k, dev)
         _lib.check(_lib.lib().cfh_head_topk(
             h.data_ptr(), M, self.d, self.lm_w.data_ptr(), _lib.ptr(self.sl), self.n,
             self.w1.data_ptr() if use_m else None, prev.data_ptr() if use_m else None, prev_stride,
-            self.r, self.w2.data_ptr() if use_m else None, k, logits.data_ptr(), vals.data_ptr(),
-            ids.data_ptr(), lse.data_ptr(), _lib.stream_handle()),
+            self.r, self.w2.data_ptr() if use_m else None, k, _lib.ptr(logits), vals.data_ptr(),
+            ids.data_ptr(), lse.data_ptr(), ws.data_ptr(), _lib.stream_handle()),
             "cfh_head_topk")
+        return vals, ids, lse
+
+
+class GemmHead:
+    """Batched shortlisted head for many rows (M up to 256): bf16 MFMA skinny GEMM over the
+    shortlist rows of the lm_head, read in place, with the per-row log-softmax top-k fused in
+    (the two-pass candidate head's pass A, ``cf/vllm_plugin/flow_proposer.py:1142-1165``)."""
+
+    def __init__(self, lm_w: torch.Tensor, shortlist: torch.Tensor | None):
+        if lm_w.dtype != torch.bfloat16 or not lm_w.is_cuda:
+            raise ValueError("lm_w must be a CUDA bf16 [V, d] tensor")
+        self.lm_w = lm_w.contiguous()
+        self.V, self.d = self.lm_w.shape
+        self.sl = None if shortlist is None else _i32(shortlist.to(lm_w.device))
+        self.n = self.V if self.sl is None else int(self.sl.numel())
+        self._ws = {}
+
+    def topk(self, x: torch.Tensor, k: int, logits: torch.Tensor | None = None):
+        """x [M, d] bf16 -> (vals [M, k] f32 log-probs, ids [M, k] int32 local, lse [M] f32)."""
+        if x.dtype != torch.bfloat16 or x.shape[1] != self.d:
+            raise ValueError(f"x must be bf16 [M, {self.d}]")
+        x = x.contiguous()
+        M = x.shape[0]
+        dev = x.device
+        key = (M, k)
+        if key not in self._ws:
+            nbytes = int(_lib.lib().cfh_head_ws_bytes(M, self.n, k))
+            if nbytes < 0:
+                raise ValueError(f"gemm head shape unsupported: M={M} k={k}")
+            self._ws[key] = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        vals = torch.empty(M, k, dtype=torch.float32, device=dev)
+        ids = torch.empty(M, k, dtype=torch.int32, device=dev)
+        lse = torch.empty(M, dtype=torch.float32, device=dev)
+        _lib.check(_lib.lib().cfh_head_gemm_topk(
+            x.data_ptr(), M, self.d, self.lm_w.data_ptr(), _lib.ptr(self.sl), self.n, k, _lib.ptr(logits),
+            vals.data_ptr(), ids.data_ptr(), lse.data_ptr(), self._ws[key].data_ptr(), _lib.stream_handle()),
+            "cfh_head_gemm_topk")
         return vals, ids, lse
 
 

@@ -1,16 +1,22 @@
-// The draft head on MI355X: shortlisted lm_head (+ markov bias), per-row log-softmax top-k, the
-// path-conditioned residual and the beam-search steps of the proposer.
+// The draft head on MI355X: shortlisted lm_head (+ markov bias) with fused per-row log-softmax
+// top-k, the batched (MFMA skinny-GEMM) head, the path-conditioned residual and the beam-search
+// steps of the proposer.
 //
 // Reference semantics (cf/ = src/chain_flow/):
 //   _head  = h.to(fp16) @ lm_w[sl].T -> fp16 logits      cf/vllm_plugin/flow_proposer.py:1021-1022, 739
 //   _bias  = markov.w1(prev) @ markov.w2.weight[sl].T     :1024-1025, 740; cf/drafters/markov_flow.py:62-74
+//   lp = log_softmax(logits.float()); topk(lp, W)         :1249-1250
 //   _map   = sl[local]                                     :1027-1028
+//   two-pass head, pass A: one GEMM over the B*K marginal hiddens, then per-row top-M
+//                                                          :1142-1165
 //   fused path residual (one baddbmm over live offsets, masked sum, LN -> Linear -> GELU -> Linear)
 //                                                          cf/vllm_plugin/fused.py:25-37
 //   _beam_chains / _beam_tree depth steps and backtrack    :1187-1332
 //
-// The head reads the rows of the target's full lm_head in place through the int32 shortlist (a
-// row-gather GEMV), so no gathered copy of lm_w[sl] is needed.
+// The heads read the rows of the target's lm_head in place through the int32 shortlist (a row
+// gather), so no gathered copy of lm_w[sl] is needed.  The logits never have to reach HBM: each
+// workgroup reduces its column block to per-row (max, sum-exp) and a local top-k, and a merge
+// kernel combines the blocks into the row's log-sum-exp and top-k.
 #include <limits.h>
 
 #include "cfh_kernels.h"
@@ -18,10 +24,111 @@
 namespace {
 
 constexpr int HW = 8;       // waves per head workgroup (one 16-row vocabulary tile per wave)
-constexpr int HMAXM = 8;    // max activation rows of the in-place head
+constexpr int HCOLS = HW * 16;
+constexpr int HMAXM = 8;    // max activation rows of the in-place GEMV head
 constexpr int KMAX = 16;    // max top-k
 
-// ---------------------------------------------------------------------------- head GEMV
+// (value, index) order: larger value first, equal values by lower index.
+__device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
+  return va > vb || (va == vb && ia < ib);
+}
+
+// Arg-best of (v, i) over the lanes of an aligned group of W lanes (W a power of two <= 64).
+template <int W>
+__device__ __forceinline__ void group_best(float& v, int& i) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(v, o);
+    const int oi = __shfl_xor(i, o);
+    if (better(ov, oi, v, i)) { v = ov; i = oi; }
+  }
+}
+
+// Per-thread sorted list of the best KMAX (value, index) pairs seen.
+struct TopList {
+  float v[KMAX];
+  int i[KMAX];
+  __device__ __forceinline__ void init() {
+#pragma unroll
+    for (int q = 0; q < KMAX; ++q) { v[q] = -INFINITY; i[q] = INT_MAX; }
+  }
+  __device__ __forceinline__ void push(float x, int ix) {
+    if (!better(x, ix, v[KMAX - 1], i[KMAX - 1])) return;
+    v[KMAX - 1] = x;
+    i[KMAX - 1] = ix;
+#pragma unroll
+    for (int q = KMAX - 1; q > 0; --q) {
+      if (better(v[q], i[q], v[q - 1], i[q - 1])) {
+        const float tv = v[q]; v[q] = v[q - 1]; v[q - 1] = tv;
+        const int ti = i[q]; i[q] = i[q - 1]; i[q - 1] = ti;
+      }
+    }
+  }
+  __device__ __forceinline__ void pop() {
+#pragma unroll
+    for (int q = 0; q < KMAX - 1; ++q) { v[q] = v[q + 1]; i[q] = i[q + 1]; }
+    v[KMAX - 1] = -INFINITY;
+    i[KMAX - 1] = INT_MAX;
+  }
+};
+
+// k rounds of a block-wide arg-best over the heads of every thread's TopList; thread 0 receives
+// the winners in order through emit(r, v, i).  Uses red_v/red_i[nwaves].
+template <typename Emit>
+__device__ void block_select(TopList& L, int k, float* red_v, int* red_i, Emit emit) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+  for (int r = 0; r < k; ++r) {
+    float bv = L.v[0];
+    int bi = L.i[0];
+    group_best<64>(bv, bi);
+    __syncthreads();
+    if (lane == 0) { red_v[wave] = bv; red_i[wave] = bi; }
+    __syncthreads();
+    bv = red_v[0];
+    bi = red_i[0];
+    for (int w = 1; w < nw; ++w)
+      if (better(red_v[w], red_i[w], bv, bi)) { bv = red_v[w]; bi = red_i[w]; }
+    if (L.i[0] == bi && bi != INT_MAX) L.pop();   // the owner of the winner advances
+    if (threadIdx.x == 0) emit(r, bv, bi);
+  }
+}
+
+__device__ __forceinline__ float block_max(float v, float* red) {
+  v = wave_max(v);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = -INFINITY;
+  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t = fmaxf(t, red[w]);
+  return t;
+}
+
+// Candidate sets written by the head kernels: for row m and column block b,
+//   cv/ci [(m * nsets + b) * k + r]  the block's r-th best (fp16/bf16-rounded logit, column)
+//   cs    [(m * nsets + b) * 2]      the block's (max, sum of exp(logit - max))
+struct Cands {
+  float* cv;
+  int* ci;
+  float* cs;
+  int nsets, k;
+};
+
+__host__ __device__ __forceinline__ size_t cand_bytes(int M, int nsets, int k) {
+  return (size_t)M * nsets * ((size_t)k * 8 + 8);
+}
+
+__device__ __forceinline__ Cands carve_cands(void* ws, int M, int nsets, int k) {
+  Cands c;
+  c.cv = (float*)ws;
+  c.ci = (int*)(c.cv + (size_t)M * nsets * k);
+  c.cs = (float*)(c.ci + (size_t)M * nsets * k);
+  c.nsets = nsets;
+  c.k = k;
+  return c;
+}
+
+// ---------------------------------------------------------------------------- GEMV head
 struct HeadArgs {
   const h16* h;        // [M][d]
   const h16* W;        // [V][d]
@@ -29,12 +136,18 @@ struct HeadArgs {
   const h16* a;        // markov A: [M][r] rows, or the w1 table when a_ids is set
   const int* a_ids;    // row ids into a (a_ids[m * a_ids_stride]), or null
   const h16* W2;       // [V][r] markov w2 or null
-  h16* logits;         // [M][n]
-  int M, d, n, r, a_ids_stride;
+  h16* logits;         // [M][n] or null
+  void* ws;            // candidate sets (null: logits only)
+  int M, d, n, r, a_ids_stride, k, nsets;
 };
 
+// One wave per 16-row vocabulary tile, HW tiles per workgroup.  Each lane streams its vocabulary
+// row in place (row-major lm_head, 16 bytes per k-step) against the M activation rows in LDS with
+// v_mfma_f32_16x16x32_f16; the markov bias is a second, rank-r MFMA stream over w2.  Epilogue:
+// logit = fp16(fp16(h.W) + fp16(A.W2)); per row, the block's (max, sum-exp) and top-k.
 __global__ void __launch_bounds__(HW * 64) k_head(HeadArgs a) {
   extern __shared__ __align__(16) h16 sm[];
+  __shared__ float Lt[HMAXM][HCOLS];
   const int ldh = a.d + 8, ldm = a.r + 8;
   h16* Ah = sm;
   h16* Am = sm + a.M * ldh;
@@ -69,24 +182,105 @@ __global__ void __launch_bounds__(HW * 64) k_head(HeadArgs a) {
     tm.begin((const h16x8*)(a.W2 + row * a.r + 8 * (lane >> 4)), a.r / 32);
     accm = tm.run(Am, ldm, a.M, accm);
   }
-  if (!colv) return;
   const int rbase = 4 * (lane >> 4);
+  const int c = wave * 16 + (lane & 15);
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int rr = rbase + q;
     if (rr < a.M) {
-      const float v = a.W2 ? r16(acc[q]) + r16(accm[q]) : acc[q];
-      a.logits[(size_t)rr * a.n + j] = (h16)v;
+      const float v = a.W2 ? r16(r16(acc[q]) + r16(accm[q])) : r16(acc[q]);
+      if (a.logits && colv) a.logits[(size_t)rr * a.n + j] = (h16)v;
+      Lt[rr][c] = colv ? v : -INFINITY;
     }
   }
+  if (!a.ws) return;
+  __syncthreads();
+  if (wave >= a.M) return;
+  // wave `wave` reduces row `wave` of this block's HCOLS columns
+  const Cands cd = carve_cands(a.ws, a.M, a.nsets, a.k);
+  const int m = wave;
+  const int c0 = blockIdx.x * HCOLS + lane, c1 = c0 + 64;
+  float x0 = Lt[m][lane], x1 = Lt[m][lane + 64];
+  int i0 = x0 == -INFINITY ? INT_MAX : c0, i1 = x1 == -INFINITY ? INT_MAX : c1;
+  const float mx = wave_max(fmaxf(x0, x1));
+  const float se = mx == -INFINITY ? 0.f : wave_sum(expf(x0 - mx) + expf(x1 - mx));
+  if (better(x1, i1, x0, i0)) {
+    const float tv = x0; x0 = x1; x1 = tv;
+    const int ti = i0; i0 = i1; i1 = ti;
+  }
+  const size_t base = (size_t)m * a.nsets + blockIdx.x;
+  for (int r = 0; r < a.k; ++r) {
+    float bv = x0;
+    int bi = i0;
+    group_best<64>(bv, bi);
+    if (i0 == bi && bi != INT_MAX) { x0 = x1; i0 = i1; x1 = -INFINITY; i1 = INT_MAX; }
+    if (lane == 0) { cd.cv[base * a.k + r] = bv; cd.ci[base * a.k + r] = bi; }
+  }
+  if (lane == 0) { cd.cs[base * 2] = mx; cd.cs[base * 2 + 1] = se; }
 }
 
-// ---------------------------------------------------------------------------- top-k
-// (value, index) order: larger value first, equal values by lower index.
-__device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
-  return va > vb || (va == vb && ia < ib);
+// ---------------------------------------------------------------------------- merge
+// One workgroup per row: log-sum-exp from the blocks' (max, sum-exp) and the top-k over the
+// blocks' candidates.  vals = logit - lse, ids = column (-1 / -inf past the valid columns).
+struct MergeArgs {
+  const void* ws;
+  int M, nsets, k;
+  float* vals;
+  int* ids;
+  float* lse;
+};
+
+constexpr int MT_THREADS = 256;
+constexpr int MBATCH = 8;
+
+__global__ void __launch_bounds__(MT_THREADS) k_topk_merge(MergeArgs a) {
+  __shared__ float red[MT_THREADS / 64];
+  __shared__ float red_v[MT_THREADS / 64];
+  __shared__ int red_i[MT_THREADS / 64];
+  const Cands cd = carve_cands((void*)a.ws, a.M, a.nsets, a.k);
+  const int m = blockIdx.x;
+  const float* cs = cd.cs + (size_t)m * a.nsets * 2;
+  float mx = -INFINITY;
+  for (int b = threadIdx.x; b < a.nsets; b += blockDim.x) mx = fmaxf(mx, cs[b * 2]);
+  mx = block_max(mx, red);
+  float se = 0.f;
+  for (int b = threadIdx.x; b < a.nsets; b += blockDim.x) {
+    const float s = cs[b * 2 + 1];
+    if (s > 0.f) se += s * expf(cs[b * 2] - mx);
+  }
+  se = block_sum(se, red);
+  const float lse = mx + logf(se);
+  if (threadIdx.x == 0 && a.lse) a.lse[m] = lse;
+  const int total = a.nsets * a.k;
+  const float* cv = cd.cv + (size_t)m * total;
+  const int* ci = cd.ci + (size_t)m * total;
+  TopList L;
+  L.init();
+  for (int base = 0; base < total; base += MBATCH * MT_THREADS) {
+    float v[MBATCH];
+    int ix[MBATCH];
+#pragma unroll
+    for (int q = 0; q < MBATCH; ++q) {
+      const int e = base + q * MT_THREADS + threadIdx.x;
+      v[q] = e < total ? cv[e] : -INFINITY;
+      ix[q] = e < total ? ci[e] : INT_MAX;
+    }
+#pragma unroll
+    for (int q = 0; q < MBATCH; ++q) L.push(v[q], ix[q]);
+  }
+  float* vals = a.vals + (size_t)m * a.k;
+  int* ids = a.ids + (size_t)m * a.k;
+  block_select(L, a.k, red_v, red_i, [&](int r, float bv, int bi) {
+    const bool ok = bi != INT_MAX;
+    vals[r] = ok ? bv - lse : -INFINITY;
+    ids[r] = ok ? bi : -1;
+  });
 }
 
+// ---------------------------------------------------------------------------- row top-k
+// Standalone per-row log-softmax top-k of fp16 logits [M][n] (one workgroup per row): every
+// thread loads its columns in batches (all loads of a batch in flight together), keeps an online
+// (max, sum-exp) and a sorted top list, then the block selects the k best.
 struct TopkArgs {
   const h16* logits;   // [M][ld]
   int ld, M, n, k;
@@ -95,85 +289,266 @@ struct TopkArgs {
   float* lse;          // [M] or null
 };
 
-// One workgroup per row: running max / sum-exp and a per-thread sorted top-KMAX list, then k
-// rounds of a block-wide arg-max over the list heads.
-__global__ void __launch_bounds__(1024) k_topk(TopkArgs a) {
-  __shared__ float red_v[16];
-  __shared__ int red_i[16];
-  __shared__ float red[16];
+constexpr int TK_THREADS = 1024;
+
+__global__ void __launch_bounds__(TK_THREADS) k_topk(TopkArgs a) {
+  __shared__ float red[TK_THREADS / 64];
+  __shared__ float red_v[TK_THREADS / 64];
+  __shared__ int red_i[TK_THREADS / 64];
   const int row = blockIdx.x;
   const h16* L = a.logits + (size_t)row * a.ld;
-  float lv[KMAX];
-  int li[KMAX];
+  TopList T;
+  T.init();
+  float m = -INFINITY, s = 0.f;
+  for (int base = 0; base < a.n; base += MBATCH * TK_THREADS) {
+    float v[MBATCH];
 #pragma unroll
-  for (int q = 0; q < KMAX; ++q) {
-    lv[q] = -INFINITY;
-    li[q] = INT_MAX;
+    for (int q = 0; q < MBATCH; ++q) {
+      const int e = base + q * TK_THREADS + threadIdx.x;
+      v[q] = e < a.n ? (float)L[e] : -INFINITY;
+    }
+    float bm = m;
+#pragma unroll
+    for (int q = 0; q < MBATCH; ++q) bm = fmaxf(bm, v[q]);
+    if (bm != -INFINITY) {
+      s = (m == -INFINITY ? 0.f : s * expf(m - bm));
+#pragma unroll
+      for (int q = 0; q < MBATCH; ++q) s += expf(v[q] - bm);
+      m = bm;
+    }
+#pragma unroll
+    for (int q = 0; q < MBATCH; ++q) {
+      const int e = base + q * TK_THREADS + threadIdx.x;
+      if (e < a.n) T.push(v[q], e);
+    }
   }
-  float m = -INFINITY;
-  for (int i = threadIdx.x; i < a.n; i += blockDim.x) {
-    const float v = (float)L[i];
-    m = fmaxf(m, v);
-    if (better(v, i, lv[KMAX - 1], li[KMAX - 1])) {
-      lv[KMAX - 1] = v;
-      li[KMAX - 1] = i;
+  const float mx = block_max(m, red);
+  const float se = block_sum(m == -INFINITY ? 0.f : s * expf(m - mx), red);
+  const float lse = mx + logf(se);
+  if (threadIdx.x == 0 && a.lse) a.lse[row] = lse;
+  float* vals = a.vals + (size_t)row * a.k;
+  int* ids = a.ids + (size_t)row * a.k;
+  block_select(T, a.k, red_v, red_i, [&](int r, float bv, int bi) {
+    const bool ok = bi != INT_MAX;
+    vals[r] = ok ? bv - lse : -INFINITY;
+    ids[r] = ok ? bi : -1;
+  });
+}
+
+// ---------------------------------------------------------------------------- MFMA GEMM head
+// Batched head (M up to 256 rows, bf16): a workgroup of GW waves owns GW*NT*16 vocabulary rows;
+// each wave streams NT row tiles in place through the shortlist and multiplies every B fragment
+// against the MT 16-row tiles of the activations (v_mfma_f32_16x16x32_bf16), so one weight byte
+// feeds 16*MT rows.  The activations pass through LDS in 128-column chunks, double-buffered: the
+// next chunk's global loads are in flight while the current chunk is multiplied, and the weight
+// fragments of the next chunk are requested before the current chunk's MFMAs.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int GW = 4;             // waves per workgroup
+constexpr int GPF = 4;            // k-steps per LDS chunk = weight prefetch depth
+constexpr int GKC = 32 * GPF;     // 128 columns per chunk
+constexpr int GLD = GKC + 8;      // LDS row stride (elements)
+
+__device__ __forceinline__ float bf16_round(float x) {
+  return (float)(__bf16)x;
+}
+
+struct GemmArgs {
+  const uint16_t* x;   // [M][d] bf16
+  const uint16_t* W;   // [V][d] bf16
+  const int* sl;
+  uint16_t* logits;    // [M][n] bf16 or null
+  void* ws;
+  int M, d, n, k, nsets;
+};
+
+template <int MT, int NT>
+__global__ void __launch_bounds__(GW * 64) k_head_gemm(GemmArgs a) {
+  extern __shared__ __align__(16) uint16_t xs[];      // [2][MT*16][GLD]
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  constexpr int ROWS = MT * 16;
+  const int tile0 = (blockIdx.x * GW + wave) * NT;
+  const bf16x8* wp[NT];
 #pragma unroll
-      for (int q = KMAX - 1; q > 0; --q) {
-        if (better(lv[q], li[q], lv[q - 1], li[q - 1])) {
-          const float tv = lv[q]; lv[q] = lv[q - 1]; lv[q - 1] = tv;
-          const int ti = li[q]; li[q] = li[q - 1]; li[q - 1] = ti;
+  for (int t = 0; t < NT; ++t) {
+    const int j = (tile0 + t) * 16 + (lane & 15);
+    const int jc = j < a.n ? j : a.n - 1;
+    const size_t row = a.sl ? (size_t)a.sl[jc] : (size_t)jc;
+    wp[t] = (const bf16x8*)(a.W + row * a.d) + (lane >> 4);
+  }
+  const int nchunks = a.d / GKC;
+  bf16x8 bq[GPF][NT];
+#pragma unroll
+  for (int p = 0; p < GPF; ++p)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) bq[p][t] = wp[t][p * 4];
+  // x chunk loader: ROWS rows x GKC columns = ROWS*16 vectors of 8; MT per thread
+  auto load_x = [&](int c, bf16x8* xr) {
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const int idx = threadIdx.x + i * GW * 64;
+      const int r = idx >> 4, v = idx & 15;
+      if (r < a.M) {
+        xr[i] = *(const bf16x8*)(a.x + (size_t)r * a.d + c * GKC + v * 8);
+      } else {
+        xr[i] = (bf16x8){};
+      }
+    }
+  };
+  auto store_x = [&](int buf, const bf16x8* xr) {
+    uint16_t* xb = xs + (size_t)buf * ROWS * GLD;
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const int idx = threadIdx.x + i * GW * 64;
+      const int r = idx >> 4, v = idx & 15;
+      *(bf16x8*)(xb + r * GLD + v * 8) = xr[i];
+    }
+  };
+  {
+    bf16x8 xr[MT];
+    load_x(0, xr);
+    store_x(0, xr);
+  }
+  __syncthreads();
+  f32x4 acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[mt][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < nchunks; ++c) {
+    const bool more = c + 1 < nchunks;
+    bf16x8 xr[MT];
+    if (more) load_x(c + 1, xr);
+    const uint16_t* xb = xs + (size_t)(c & 1) * ROWS * GLD;
+#pragma unroll
+    for (int p = 0; p < GPF; ++p) {
+      bf16x8 b[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        b[t] = bq[p][t];
+        if (more) bq[p][t] = wp[t][((c + 1) * GPF + p) * 4];
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const bf16x8 av = *(const bf16x8*)(xb + (mt * 16 + (lane & 15)) * GLD + p * 32 + 8 * (lane >> 4));
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b[t], acc[mt][t], 0, 0, 0);
+      }
+    }
+    if (more) store_x((c + 1) & 1, xr);
+    __syncthreads();
+  }
+  // epilogue: bf16 logits; per wave and row, the top-k of the wave's NT*16 columns and its
+  // (max, sum-exp), parked in LDS; then per row the GW wave lists merge into the block's set.
+  const int g = lane >> 4, col = lane & 15;
+  float* wv = (float*)xs;                                   // [GW][ROWS][k]
+  int* wi = (int*)(wv + (size_t)GW * ROWS * a.k);           // [GW][ROWS][k]
+  float* ws2 = (float*)(wi + (size_t)GW * ROWS * a.k);      // [GW][ROWS][2]
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r = mt * 16 + 4 * g + q;
+      float v[NT];
+      int ix[NT];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const int j = (tile0 + t) * 16 + col;
+        const bool ok = j < a.n && r < a.M;
+        const float lv = bf16_round(acc[mt][t][q]);
+        if (ok && a.logits) a.logits[(size_t)r * a.n + j] = __builtin_bit_cast(uint16_t, (__bf16)lv);
+        v[t] = ok ? lv : -INFINITY;
+        ix[t] = ok ? j : INT_MAX;
+        mx = fmaxf(mx, v[t]);
+      }
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+      float se = 0.f;
+      if (mx != -INFINITY) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) se += expf(v[t] - mx);
+      }
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) se += __shfl_xor(se, o);
+      if (r < a.M && col == 0) {
+        ws2[((size_t)wave * ROWS + r) * 2] = mx;
+        ws2[((size_t)wave * ROWS + r) * 2 + 1] = se;
+      }
+      // selection inside the 16-lane group (columns of this row)
+      for (int rr = 0; rr < a.k; ++rr) {
+        float bv = -INFINITY;
+        int bi = INT_MAX, bt = -1;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+          if (better(v[t], ix[t], bv, bi)) { bv = v[t]; bi = ix[t]; bt = t; }
+        float gv = bv;
+        int gi = bi;
+        group_best<16>(gv, gi);
+        if (bi == gi && gi != INT_MAX) {
+#pragma unroll
+          for (int t = 0; t < NT; ++t)
+            if (t == bt) { v[t] = -INFINITY; ix[t] = INT_MAX; }
+        }
+        if (r < a.M && col == 0) {
+          wv[((size_t)wave * ROWS + r) * a.k + rr] = gv;
+          wi[((size_t)wave * ROWS + r) * a.k + rr] = gi;
         }
       }
     }
   }
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
-  // block max
-  float wm = wave_max(m);
-  if (lane == 0) red[wave] = wm;
   __syncthreads();
-  float mx = -INFINITY;
-  for (int w = 0; w < nw; ++w) mx = fmaxf(mx, red[w]);
-  __syncthreads();
-  // sum of exp(v - max)
-  float se = 0.f;
-  for (int i = threadIdx.x; i < a.n; i += blockDim.x) se += expf((float)L[i] - mx);
-  se = wave_sum(se);
-  if (lane == 0) red[wave] = se;
-  __syncthreads();
-  float tot = 0.f;
-  for (int w = 0; w < nw; ++w) tot += red[w];
-  const float lse = mx + logf(tot);
-  if (threadIdx.x == 0 && a.lse) a.lse[row] = lse;
-  // k rounds of arg-max over the list heads
-  for (int r = 0; r < a.k; ++r) {
-    float bv = lv[0];
-    int bi = li[0];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o);
-      const int oi = __shfl_xor(bi, o);
-      if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  const Cands cd = carve_cands(a.ws, a.M, a.nsets, a.k);
+  for (int r = threadIdx.x; r < a.M; r += blockDim.x) {
+    const size_t base = (size_t)r * a.nsets + blockIdx.x;
+    float mx = -INFINITY;
+    for (int w = 0; w < GW; ++w) mx = fmaxf(mx, ws2[((size_t)w * ROWS + r) * 2]);
+    float se = 0.f;
+    for (int w = 0; w < GW; ++w) {
+      const float s = ws2[((size_t)w * ROWS + r) * 2 + 1];
+      if (s > 0.f) se += s * expf(ws2[((size_t)w * ROWS + r) * 2] - mx);
     }
-    __syncthreads();
-    if (lane == 0) { red_v[wave] = bv; red_i[wave] = bi; }
-    __syncthreads();
-    bv = red_v[0];
-    bi = red_i[0];
-    for (int w = 1; w < nw; ++w)
-      if (better(red_v[w], red_i[w], bv, bi)) { bv = red_v[w]; bi = red_i[w]; }
-    if (li[0] == bi && bi != INT_MAX) {   // the owner pops its head
-#pragma unroll
-      for (int q = 0; q < KMAX - 1; ++q) { lv[q] = lv[q + 1]; li[q] = li[q + 1]; }
-      lv[KMAX - 1] = -INFINITY;
-      li[KMAX - 1] = INT_MAX;
-    }
-    if (threadIdx.x == 0) {
-      const bool ok = bi != INT_MAX;
-      a.vals[(size_t)row * a.k + r] = ok ? bv - lse : -INFINITY;
-      a.ids[(size_t)row * a.k + r] = ok ? bi : -1;
+    cd.cs[base * 2] = mx;
+    cd.cs[base * 2 + 1] = se;
+    int pos[GW];
+    for (int w = 0; w < GW; ++w) pos[w] = 0;
+    for (int rr = 0; rr < a.k; ++rr) {
+      float bv = -INFINITY;
+      int bi = INT_MAX, bw = 0;
+      for (int w = 0; w < GW; ++w) {
+        if (pos[w] >= a.k) continue;
+        const size_t o = ((size_t)w * ROWS + r) * a.k + pos[w];
+        if (better(wv[o], wi[o], bv, bi)) { bv = wv[o]; bi = wi[o]; bw = w; }
+      }
+      if (bi != INT_MAX) pos[bw]++;
+      cd.cv[base * a.k + rr] = bv;
+      cd.ci[base * a.k + rr] = bi;
     }
   }
 }
+
+template <int MT, int NT>
+size_t gemm_lds(int k) {
+  const size_t xbuf = 2 * (size_t)MT * 16 * GLD * 2;
+  const size_t cand = (size_t)GW * MT * 16 * ((size_t)k * 8 + 8);
+  return xbuf > cand ? xbuf : cand;
+}
+
+template <int MT, int NT>
+int launch_gemm(const GemmArgs& a0, hipStream_t st) {
+  GemmArgs a = a0;
+  const int cols = GW * NT * 16;
+  a.nsets = (a.n + cols - 1) / cols;
+  const size_t lds = gemm_lds<MT, NT>(a.k);
+  if (lds > 160 * 1024) return CFH_E_UNSUPPORTED;
+  CFH_HIP(hipFuncSetAttribute((const void*)k_head_gemm<MT, NT>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+  hipLaunchKernelGGL((k_head_gemm<MT, NT>), dim3(a.nsets), dim3(GW * 64), lds, st, a);
+  CFH_LAUNCH_CHECK();
+  return CFH_OK;
+}
+
+template <int MT, int NT>
+int gemm_nsets(int n) { return (n + GW * NT * 16 - 1) / (GW * NT * 16); }
 
 // ---------------------------------------------------------------------------- path residual
 struct PathSumArgs {
@@ -357,44 +732,108 @@ __global__ void k_backtrack(BacktrackArgs a) {
   }
 }
 
+
 size_t head_lds(int M, int d, int r) { return (size_t)M * (d + 8) * 2 + (size_t)M * (r + 8) * 2; }
+
+int launch_head(const HeadArgs& ha0, hipStream_t st) {
+  HeadArgs ha = ha0;
+  const size_t lds = head_lds(ha.M, ha.d, ha.r);
+  if (lds > 150 * 1024) return CFH_E_UNSUPPORTED;
+  CFH_HIP(hipFuncSetAttribute((const void*)k_head, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+  const int ntiles = (ha.n + 15) / 16;
+  hipLaunchKernelGGL(k_head, dim3((ntiles + HW - 1) / HW), dim3(HW * 64), lds, st, ha);
+  CFH_LAUNCH_CHECK();
+  return CFH_OK;
+}
+
+int launch_merge(const void* ws, int M, int nsets, int k, float* vals, int* ids, float* lse, hipStream_t st) {
+  MergeArgs m = {};
+  m.ws = ws; m.M = M; m.nsets = nsets; m.k = k; m.vals = vals; m.ids = ids; m.lse = lse;
+  hipLaunchKernelGGL(k_topk_merge, dim3(M), dim3(MT_THREADS), 0, st, m);
+  CFH_LAUNCH_CHECK();
+  return CFH_OK;
+}
+
+int head_args(HeadArgs& ha, const void* h, int M, int d, const void* W, const int32_t* sl, int n, const void* a,
+              const int32_t* a_ids, int a_ids_stride, int r, const void* W2) {
+  if (!h || !W || M < 1 || M > HMAXM || d < 32 || d % 256 || n < 1) return CFH_E_INVALID;
+  if (W2 && (!a || r < 32 || r % 256)) return CFH_E_INVALID;
+  ha = HeadArgs{};
+  ha.h = (const h16*)h; ha.W = (const h16*)W; ha.sl = sl; ha.a = (const h16*)a; ha.a_ids = a_ids;
+  ha.W2 = (const h16*)W2; ha.M = M; ha.d = d; ha.n = n; ha.r = W2 ? r : 0;
+  ha.a_ids_stride = a_ids_stride > 0 ? a_ids_stride : 1;
+  return CFH_OK;
+}
 
 }  // namespace
 
 extern "C" {
 
+int64_t cfh_head_ws_bytes(int M, int n, int k) {
+  if (M < 1 || n < 1 || k < 1 || k > KMAX) return -1;
+  const int nsets = (n + 127) / 128;    // the narrowest column block of any head kernel
+  return (int64_t)cand_bytes(M, nsets, k);
+}
+
 int cfh_head_logits(const void* h, int M, int d, const void* W, const int32_t* sl, int n, const void* a,
                     const int32_t* a_ids, int a_ids_stride, int r, const void* W2, void* logits, void* stream) {
-  if (!h || !W || !logits || M < 1 || M > HMAXM || d < 32 || d % 256 || n < 1) return CFH_E_INVALID;
-  if (W2 && (!a || r < 32 || r % 256)) return CFH_E_INVALID;
-  HeadArgs ha = {};
-  ha.h = (const h16*)h; ha.W = (const h16*)W; ha.sl = sl; ha.a = (const h16*)a; ha.a_ids = a_ids;
-  ha.W2 = (const h16*)W2; ha.logits = (h16*)logits; ha.M = M; ha.d = d; ha.n = n; ha.r = W2 ? r : 0;
-  ha.a_ids_stride = a_ids_stride > 0 ? a_ids_stride : 1;
-  const size_t lds = head_lds(M, d, ha.r);
-  if (lds > 160 * 1024) return CFH_E_UNSUPPORTED;
-  CFH_HIP(hipFuncSetAttribute((const void*)k_head, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-  const int ntiles = (n + 15) / 16;
-  hipLaunchKernelGGL(k_head, dim3((ntiles + HW - 1) / HW), dim3(HW * 64), lds, (hipStream_t)stream, ha);
-  CFH_LAUNCH_CHECK();
-  return CFH_OK;
+  if (!logits) return CFH_E_INVALID;
+  HeadArgs ha;
+  int rc = head_args(ha, h, M, d, W, sl, n, a, a_ids, a_ids_stride, r, W2);
+  if (rc) return rc;
+  ha.logits = (h16*)logits;
+  return launch_head(ha, (hipStream_t)stream);
 }
 
 int cfh_row_topk(const void* logits, int M, int n, int k, float* vals, int32_t* ids, float* lse, void* stream) {
   if (!logits || !vals || !ids || M < 1 || n < 1 || k < 1 || k > KMAX) return CFH_E_INVALID;
   TopkArgs ta = {};
   ta.logits = (const h16*)logits; ta.ld = n; ta.M = M; ta.n = n; ta.k = k; ta.vals = vals; ta.ids = ids; ta.lse = lse;
-  hipLaunchKernelGGL(k_topk, dim3(M), dim3(1024), 0, (hipStream_t)stream, ta);
+  hipLaunchKernelGGL(k_topk, dim3(M), dim3(TK_THREADS), 0, (hipStream_t)stream, ta);
   CFH_LAUNCH_CHECK();
   return CFH_OK;
 }
 
 int cfh_head_topk(const void* h, int M, int d, const void* W, const int32_t* sl, int n, const void* a,
                   const int32_t* a_ids, int a_ids_stride, int r, const void* W2, int k, void* logits, float* vals,
-                  int32_t* ids, float* lse, void* stream) {
-  int rc = cfh_head_logits(h, M, d, W, sl, n, a, a_ids, a_ids_stride, r, W2, logits, stream);
+                  int32_t* ids, float* lse, void* ws, void* stream) {
+  if (!vals || !ids || !ws || k < 1 || k > KMAX) return CFH_E_INVALID;
+  HeadArgs ha;
+  int rc = head_args(ha, h, M, d, W, sl, n, a, a_ids, a_ids_stride, r, W2);
   if (rc) return rc;
-  return cfh_row_topk(logits, M, n, k, vals, ids, lse, stream);
+  ha.logits = (h16*)logits;
+  ha.ws = ws;
+  ha.k = k;
+  ha.nsets = (n + HCOLS - 1) / HCOLS;
+  hipStream_t st = (hipStream_t)stream;
+  if ((rc = launch_head(ha, st))) return rc;
+  return launch_merge(ws, M, ha.nsets, k, vals, ids, lse, st);
+}
+
+int cfh_head_gemm_topk(const void* x, int M, int d, const void* W, const int32_t* sl, int n, int k, void* logits,
+                       float* vals, int32_t* ids, float* lse, void* ws, void* stream) {
+  if (!x || !W || !vals || !ids || !ws || M < 1 || M > 256 || d < GKC || d % GKC || n < 1 || k < 1 || k > KMAX)
+    return CFH_E_INVALID;
+  GemmArgs ga = {};
+  ga.x = (const uint16_t*)x; ga.W = (const uint16_t*)W; ga.sl = sl; ga.logits = (uint16_t*)logits; ga.ws = ws;
+  ga.M = M; ga.d = d; ga.n = n; ga.k = k;
+  hipStream_t st = (hipStream_t)stream;
+  int rc, nsets;
+  if (M <= 64) {
+    nsets = gemm_nsets<4, 4>(n);
+    ga.nsets = nsets;
+    rc = launch_gemm<4, 4>(ga, st);
+  } else if (M <= 160) {
+    nsets = gemm_nsets<10, 4>(n);
+    ga.nsets = nsets;
+    rc = launch_gemm<10, 4>(ga, st);
+  } else {
+    nsets = gemm_nsets<16, 2>(n);
+    ga.nsets = nsets;
+    rc = launch_gemm<16, 2>(ga, st);
+  }
+  if (rc) return rc;
+  return launch_merge(ws, M, nsets, k, vals, ids, lse, st);
 }
 
 int64_t cfh_path_ws_bytes(int M, int d, int ffn_mult, int order) {

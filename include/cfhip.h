@@ -101,17 +101,26 @@ int cfh_head_logits(const void* h, int M, int d, const void* W, const int32_t* s
 int cfh_row_topk(const void* logits, int M, int n, int k, float* vals, int32_t* ids, float* lse,
                  void* stream);
 
-/* cfh_head_logits followed by cfh_row_topk; `logits` is caller scratch [M][n] fp16. */
+/* Bytes of the candidate workspace `ws` that cfh_head_topk / cfh_head_gemm_topk need for M rows,
+ * n shortlist columns and top-k (-1 if out of range). */
+int64_t cfh_head_ws_bytes(int M, int n, int k);
+
+/* cfh_head_logits with the log-softmax top-k fused into the head: every workgroup reduces its
+ * column block to per-row (max, sum-exp) and a local top-k in `ws`, a merge kernel combines them.
+ * `logits` [M][n] fp16 is an optional output (NULL: the logits never reach memory).
+ * Same results as cfh_head_logits followed by cfh_row_topk. */
 int cfh_head_topk(const void* h, int M, int d, const void* W, const int32_t* sl, int n,
                   const void* a, const int32_t* a_ids, int a_ids_stride, int r, const void* W2, int k,
-                  void* logits, float* vals, int32_t* ids, float* lse, void* stream);
+                  void* logits, float* vals, int32_t* ids, float* lse, void* ws, void* stream);
 
-/* Batched (M up to 256) bf16 skinny-GEMM head with per-row top-k: the two-pass candidate head's
- * pass A (cf/vllm_plugin/flow_proposer.py:1142-1165) as one MFMA kernel.
- *   x [M][d] bf16, W [V][d] bf16 gathered through sl (or contiguous if sl == NULL),
- *   logits [M][n] bf16 scratch, vals/ids [M][k], lse [M] (may be NULL).  k <= 16. */
+/* Batched (M up to 256) bf16 skinny-GEMM head with per-row log-softmax top-k: the two-pass
+ * candidate head's pass A (cf/vllm_plugin/flow_proposer.py:1142-1165) as one MFMA kernel plus the
+ * candidate merge.  logits[m][j] = bf16(x[m] . W[row_j]), row_j = sl ? sl[j] : j.
+ *   x [M][d] bf16 (d % 128 == 0), W [V][d] bf16 read in place through sl,
+ *   logits [M][n] bf16 optional output (NULL: not written), vals/ids [M][k], lse [M] (may be NULL),
+ *   ws of cfh_head_ws_bytes(M, n, k) bytes.  k <= 16. */
 int cfh_head_gemm_topk(const void* x, int M, int d, const void* W, const int32_t* sl, int n, int k,
-                       void* logits, float* vals, int32_t* ids, float* lse, void* stream);
+                       void* logits, float* vals, int32_t* ids, float* lse, void* ws, void* stream);
 
 /* ---------------------------------------------------------------- draft search
  * Path-conditioned residual of the PathHead, fused form (cf/vllm_plugin/fused.py:25-37;

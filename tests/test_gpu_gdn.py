@@ -1,0 +1,97 @@
+"""GPU parity of the tree gated delta net (cfh_gdn_tree) against the float64 oracle.
+
+Contract (fp32 state): node outputs and node states within 1e-5 norm-relative of the oracle's
+tree_gated_delta_scan on the same bf16 q/k/v and fp32 g/beta/S0.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_err, to64
+from chain_flow_amd.gdn import L2_NORM_EPS, L2_SQRT_EPS, tree_gated_delta_scan
+from oracle import gdn as ogdn
+
+TOL = 1e-5
+
+
+def beam_tree_parents(keep=4, depth=5, topb=4):
+    """Parents of a width-`keep`, depth-`depth` beam tree in BFS order (first level: min(keep, topb)
+    children of the root; later levels: `keep` nodes spread over the previous level)."""
+    parents, prev = [], [-1]
+    base = 0
+    for lvl in range(depth):
+        k = min(keep, len(prev) * topb)
+        lvl_par = [prev[i % len(prev)] if lvl else -1 for i in range(k)]
+        parents += lvl_par
+        prev = list(range(base, base + k))
+        base += k
+    return np.array(parents)
+
+
+def _inputs(N, H, Dk, Dv, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(N, H, Dk, generator=g).to(torch.bfloat16)
+    k = torch.randn(N, H, Dk, generator=g).to(torch.bfloat16)
+    v = torch.randn(N, H, Dv, generator=g).to(torch.bfloat16)
+    gg = torch.nn.functional.logsigmoid(torch.randn(N, H, generator=g))
+    beta = torch.rand(N, H, generator=g)
+    S0 = torch.randn(H, Dk, Dv, generator=g) * 0.1
+    return q, k, v, gg, beta, S0
+
+
+def _run(cuda, parent, H=16, Dk=128, Dv=128, seed=5, l2mode=L2_NORM_EPS, states=True):
+    N = len(parent)
+    q, k, v, gg, beta, S0 = _inputs(N, H, Dk, Dv, seed)
+    out, st = tree_gated_delta_scan(q.to(cuda), k.to(cuda), v.to(cuda), gg, beta, torch.tensor(parent), S0,
+                                    l2mode=l2mode, write_states=states)
+    torch.cuda.synchronize()
+    mode = "norm_eps" if l2mode == L2_NORM_EPS else "sqrt_eps"
+    ro, rs = ogdn.tree_gated_delta_scan(to64(q), to64(k), to64(v), to64(gg), to64(beta), parent, to64(S0),
+                                        l2mode=mode)
+    return out, st, ro, rs, (q, k, v, gg, beta, S0)
+
+
+@pytest.mark.gpu
+def test_gdn_beam_tree_matches_oracle(cuda):
+    """Tree draft verification shape: beam width 4, depth 5 (plus a bushier variant), 16 heads,
+    dk = dv = 128, fp32 state."""
+    for parent in (beam_tree_parents(4, 5, 4), np.array([-1] + [0] * 4 + [1, 1, 2, 2, 3, 3, 4, 4] +
+                                                         list(range(5, 13)) + list(range(13, 21)) + [21, 22])):
+        out, st, ro, rs, _ = _run(cuda, parent)
+        print(f"[gdn] N={len(parent)} out err {rel_err(to64(out), ro):.2e} state err {rel_err(to64(st), rs):.2e}",
+              flush=True)
+        assert rel_err(to64(out), ro) < TOL
+        assert rel_err(to64(st), rs) < TOL
+
+
+@pytest.mark.gpu
+def test_gdn_chain_is_the_linear_recurrence(cuda):
+    parent = np.arange(-1, 11)
+    out, st, ro, rs, (q, k, v, gg, beta, S0) = _run(cuda, parent, H=4, Dv=64, seed=9)
+    seq = ogdn.sequential_path_output(to64(q), to64(k), to64(v), to64(gg), to64(beta), list(range(12)), to64(S0))
+    assert rel_err(to64(out)[-1], seq) < TOL
+    assert rel_err(to64(st), rs) < TOL
+
+
+@pytest.mark.gpu
+def test_gdn_forest_sqrt_eps_and_outputs_only(cuda):
+    parent = np.array([-1, -1, 0, 1, 2, 2, -1, 6, 3])
+    out, st, ro, rs, _ = _run(cuda, parent, H=3, Dv=192, seed=11, l2mode=L2_SQRT_EPS, states=False)
+    assert st is None
+    assert rel_err(to64(out), ro) < TOL
+
+
+@pytest.mark.gpu
+def test_gdn_refuses_non_bfs_order(cuda):
+    """A parent index at or after its node breaks the BFS contract: the kernel writes NaN for that
+    node instead of reading a state that does not exist yet."""
+    parent = np.array([-1, 0, 3, 1])
+    q, k, v, gg, beta, S0 = _inputs(4, 2, 128, 64, 3)
+    out, st = tree_gated_delta_scan(q.to(cuda), k.to(cuda), v.to(cuda), gg, beta, torch.tensor(parent), S0)
+    torch.cuda.synchronize()
+    assert np.isnan(to64(st)[2]).all()
+    o = to64(out)
+    assert np.isnan(o[2]).all()
+    assert np.isfinite(o[[0, 1, 3]]).all()

@@ -199,3 +199,30 @@ def test_beam_chains_match_oracle(cuda, seed):
     print(f"[beam chains seed={seed}] gpu {got.tolist()} oracle {ref.tolist()}", flush=True)
     if not np.array_equal(got, ref):
         assert _near_tie(trace, Wd), (got, ref)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,k,markov", [(1, 4, True), (4, 4, True), (4, 8, False), (8, 16, True)])
+def test_fused_head_topk_equals_logits_then_topk(cuda, M, k, markov):
+    """The fused head (per-block candidates + merge) returns exactly what the unfused pair
+    (fp16 logits, then per-row log-softmax top-k) returns on the same inputs."""
+    d, V, n = 512, 9000, 5003          # n not a multiple of the 128-column block
+    cfg, W = _head_weights(d, V)
+    sl = _shortlist(V, n)
+    g = torch.Generator().manual_seed(17)
+    h = torch.randn(M, d, generator=g).half().to(cuda)
+    prev = torch.randint(0, V, (M,), generator=g, dtype=torch.int32).to(cuda)
+    head = ShortlistHead(W["lm_head.weight"].to(cuda), sl.to(cuda),
+                         W["markov.w1.weight"].to(cuda) if markov else None,
+                         W["markov.w2.weight"].to(cuda) if markov else None)
+    logits = torch.empty(M, n, dtype=torch.float16, device=cuda)
+    vals, ids, lse = head.topk(h, k, prev=prev if markov else None, logits=logits)
+    rv, ri, rl = row_topk(logits, k)
+    torch.cuda.synchronize()
+    assert torch.equal(ids, ri)
+    assert torch.allclose(vals, rv, atol=2e-6, rtol=0)
+    assert torch.allclose(lse, rl, atol=2e-6, rtol=0)
+    L = to64(logits)
+    ov, oi = ohead.topk(ohead.log_softmax(L), k)
+    assert np.array_equal(ids.cpu().numpy(), oi)
+    assert np.allclose(vals.cpu().numpy(), ov, atol=1e-5, rtol=0)

@@ -6,98 +6,116 @@
 // numerics cf/csrc/fused_block.cu:280-325, 452-668, 674-722 (fp32 residual, fp16-parked LayerNorm
 // rows, fp16 q/k/v, attention and GELU outputs, cross K/V hoisted once per draft).
 //
-// Execution plan: one launch sequence per draft on the caller's stream, both chunk experts in
-// every launch.  Work that needs a whole row or a whole head sits at a kernel boundary; there is
-// no cross-workgroup synchronisation inside any kernel (no fences, no atomics, no spin-waits), so
-// every result is deterministic.
+// Execution plan.  One launch sequence per draft on the caller's stream; every launch covers both
+// chunk experts (they are independent within an Euler step), so each weight-streaming launch moves
+// the weights of two experts.  Work that needs a whole row sits in a small row kernel between two
+// streaming kernels; there is no cross-workgroup synchronisation inside any kernel (no fences, no
+// atomics, no spin-waits), so results are deterministic.  On MI355X a kernel boundary costs about
+// nothing on the stream, while a fenced grid barrier across the 8 XCDs costs ~12 us, which is why
+// this is a kernel pipeline and not one persistent launch.
 //
-//   per draft : KV  (cross K/V of every block) -> REDUCE ; TAU (time_mlp(tau_s), all s) -> REDUCE ;
-//               ROWS(init): z0 = init_latents(ctx), step-0 rows x, LN_self of block 0
-//   per step s, per block l:
-//     QKV  GEMV  A = LN_self(x)         -> fp32 partials
-//     ATTN       q,k,v = fp16(sum partials + b); causal self attention -> attn (fp16)
-//     O    GEMV  A = attn               -> partials
-//     NORM       x += sum + b_o; A = fp16(LN_cross(fp16(x)))
-//     QC   GEMV  A = LN_cross(x)        -> partials
-//     ATTN       q = fp16(sum + b); attention over the hoisted context K/V -> attn
-//     OC   GEMV  A = attn               -> partials
-//     NORM       x += sum + b_oc; A = LN_ffn(x)
-//     W1   GEMV  A = LN_ffn(x)          -> partials
-//     GELU       g = fp16(gelu(sum + b1))
-//     W2   GEMV  A = g                  -> partials
-//     NORM       x += sum + b2; A = LN_self of the next block (out_norm after the last block)
-//   OUT  GEMV  A = out_norm(x[current rows]) -> partials
-//   ROWS(euler): v = fp16(sum + b_out); z = fp16(z + fp16(dt v)); next step's rows and LN_self
+//   per draft : TAU  time_mlp(tau_s) for all E steps     (GEMV + reduce)
+//               ROWS init_latents(ctx), step-0 rows x, a = LN_self(x) of block 0
+//               KV   cross K/V of every block             (GEMV + reduce)
+//   per Euler step, per block l (both experts in every launch):
+//     QKV   stream  A = a (LN_self rows)          epilogue q,k,v = fp16(acc + b)      full-K tiles
+//     O     stream  A = causal self attention of head h, computed while staging    split-K by head
+//     RES   row     x += sum_h P + b_o ; a = LN_cross(fp16(x))
+//     QC    stream  A = a                         fp32 partials                     split-K
+//     OC    stream  A = cross attention of head h (q reduced from the QC partials, hoisted K/V)
+//     RES   row     x += sum_h P + b_oc ; a = LN_ffn(fp16(x))
+//     W1    stream  A = a                         epilogue g = fp16(gelu(acc + b1))  full-K tiles
+//     W2    stream  A = g                         fp32 partials                     split-K
+//     RES   row     x += sum P + b2 ; a = LN_self of block l+1 (out_norm after the last block)
+//   OUT   stream  A = out_norm rows of the current chunk                           split-K
+//   ROWS  row     v = fp16(sum P + b_out); z = fp16(z + fp16(dt v)); next step's rows and LN_self
 //
-// Every GEMV is split-K over workgroups: a wave owns one (n-tile of 16 outputs, k-chunk) unit,
-// streams the tile's packed fragments (cfh_common.h stream_tile) against the activation chunk held
-// in LDS, and stores its fp32 partial tile; the next kernel sums the partials in chunk order.
+// Streaming kernel: a wave owns TPW consecutive 16-column tiles of one (expert, k-chunk); it
+// streams their packed fragments (1 KiB per wave per k-step, contiguous per tile, non-temporal)
+// with PF fragment loads in flight, issued before the A operand is staged, and multiplies each
+// against the A rows held in LDS with v_mfma_f32_16x16x32_f16.
 #include <stdio.h>
 
 #include <algorithm>
-#include <mutex>
 
 #include "cfh_kernels.h"
 
 namespace {
 
-// ---------------------------------------------------------------------------- attention
-// One workgroup per (expert, head): softmax(q k^T / sqrt(hd) [+ causal mask]) v for <= 16 query
-// rows and <= 16 keys.  q (and k, v for self attention) are reduced from the projection's fp32
-// partials and rounded to fp16 as the reference materialises them; cross attention reads the
-// hoisted fp16 context K/V.  Causal mask = triu(-inf, 1) (cf/drafters/chunked_flow.py:273-275).
-struct AttnArgs {
-  const float* P[4];   // projection partials [ks][Sq][ldp]
-  const h16* bias[4];  // in_proj_bias (q at 0, k at d, v at 2d)
-  const h16* kv[4];    // cross: [2][Sk][d] of this block (null for self attention)
-  h16* out[4];         // [Sq][d]
-  int Sq[4], Sk[4];
-  int ks, ldp, d, heads, hd, causal;
+constexpr int SWMAX = 8;          // max waves per streaming workgroup
+constexpr int SPF = 16;           // fragment loads in flight per wave
+
+enum SrcKind { S_BUF = 0, S_SELF = 1, S_CROSS = 2 };
+enum EpiKind { E_PART = 0, E_BIAS16 = 1, E_GELU16 = 2 };
+
+struct SEx {
+  const h16x8* w;      // packed weights: fragment (tile t, k-step s) at ((t * K/32) + s) * 64
+  const h16* a;        // S_BUF: rows [S][lda] | S_SELF: q,k,v rows [S][3d] | S_CROSS: K/V [2][Ck][d]
+  int lda;
+  const float* pin;    // S_CROSS: cross-q partials [ks_in][S][d]
+  const h16* bin;      // S_CROSS: cross-q bias (in_proj_bias[0:d])
+  const h16* bias;     // E_BIAS16 / E_GELU16 bias [N]
+  void* out;           // E_PART: float [ks][S][N]; otherwise h16 [S][N]
+  int S;               // activation rows (<= 16)
 };
 
-__global__ void __launch_bounds__(1024) k_attn(AttnArgs a) {
-  extern __shared__ __align__(16) h16 sm[];
-  __shared__ float P[MAXR][MAXR + 1];
-  const int e = blockIdx.x / a.heads, h = blockIdx.x - e * a.heads;
-  const int Sq = a.Sq[e], Sk = a.Sk[e], hd = a.hd, d = a.d;
-  const int c0 = h * hd;
-  h16* sq = sm;
-  h16* sk = sm + (size_t)Sq * hd;
+struct SArgs {
+  SEx ex[4];
+  int nex, N, K, ks, wpb, tpw, wg_per_kc;
+  int d, hd, ks_in, Ck;
+};
+
+// Self / cross attention of head h for the S rows of one expert, written as fp16 into As
+// [S][lda] (lda >= hd + 8).  Causal mask = triu(-inf, 1) (cf/drafters/chunked_flow.py:273-275);
+// scores and the weighted sum in fp32 on fp16 q/k/v, output rounded to fp16.
+template <int SRC>
+__device__ void stage_attention(const SArgs& a, const SEx& ex, int h, h16* As, int lda, h16* scratch) {
+  const int S = ex.S, hd = a.hd, d = a.d;
+  const int Sk = SRC == S_SELF ? S : a.Ck;
+  h16* sq = scratch;
+  h16* sk = sq + (size_t)S * hd;
   h16* sv = sk + (size_t)Sk * hd;
-  const size_t pstride = (size_t)Sq * a.ldp;
-  // q (and k, v) = fp16(sum of partials + bias), four columns per thread-step
-  const int nsrc = a.kv[e] ? 1 : 3;
-  const int hq = hd / 4;
-  for (int idx = threadIdx.x; idx < nsrc * Sq * hq; idx += blockDim.x) {
-    const int part = idx / (Sq * hq);
-    const int r = idx - part * Sq * hq;
-    const int i = r / hq, c = (r - i * hq) * 4;
-    const int col = part * d + c0 + c;
-    const float* Pp = a.P[e] + (size_t)i * a.ldp + col;
-    float4 s4 = *(const float4*)Pp;
-    for (int q = 1; q < a.ks; ++q) {
-      const float4 t = *(const float4*)(Pp + q * pstride);
-      s4.x += t.x; s4.y += t.y; s4.z += t.z; s4.w += t.w;
+  float* P = (float*)(sv + (size_t)Sk * hd);   // [S][Sk]
+  const int nv = hd / 8;
+  const int c0 = h * hd;
+  if constexpr (SRC == S_SELF) {
+    const size_t ld = 3 * (size_t)d;
+    for (int idx = threadIdx.x; idx < 3 * S * nv; idx += blockDim.x) {
+      const int part = idx / (S * nv);
+      const int r = idx - part * S * nv;
+      const int i = r / nv, c = (r - i * nv) * 8;
+      h16* dst = (part == 0 ? sq : (part == 1 ? sk : sv)) + i * hd + c;
+      *(h16x8*)dst = *(const h16x8*)(ex.a + (size_t)i * ld + part * d + c0 + c);
     }
-    const h16* bb = a.bias[e] + col;
-    h16* dst = (part == 0 ? sq : (part == 1 ? sk : sv)) + i * hd + c;
-    dst[0] = (h16)(s4.x + (float)bb[0]);
-    dst[1] = (h16)(s4.y + (float)bb[1]);
-    dst[2] = (h16)(s4.z + (float)bb[2]);
-    dst[3] = (h16)(s4.w + (float)bb[3]);
-  }
-  if (a.kv[e]) {
-    const int nv = hd / 8;
+  } else {
+    // q = fp16(sum of the cross-q partials + bias), four columns per thread-step
+    const int nq = hd / 4;
+    const size_t pst = (size_t)S * d;
+    for (int idx = threadIdx.x; idx < S * nq; idx += blockDim.x) {
+      const int i = idx / nq, c = (idx - i * nq) * 4;
+      const float* Pp = ex.pin + (size_t)i * d + c0 + c;
+      float4 s4 = *(const float4*)Pp;
+      for (int q = 1; q < a.ks_in; ++q) {
+        const float4 t = *(const float4*)(Pp + q * pst);
+        s4.x += t.x; s4.y += t.y; s4.z += t.z; s4.w += t.w;
+      }
+      const h16* bb = ex.bin + c0 + c;
+      h16* dst = sq + i * hd + c;
+      dst[0] = (h16)(s4.x + (float)bb[0]);
+      dst[1] = (h16)(s4.y + (float)bb[1]);
+      dst[2] = (h16)(s4.z + (float)bb[2]);
+      dst[3] = (h16)(s4.w + (float)bb[3]);
+    }
     for (int idx = threadIdx.x; idx < Sk * nv; idx += blockDim.x) {
       const int j = idx / nv, c = (idx - j * nv) * 8;
-      *(h16x8*)(sk + j * hd + c) = *(const h16x8*)(a.kv[e] + (size_t)j * d + c0 + c);
-      *(h16x8*)(sv + j * hd + c) = *(const h16x8*)(a.kv[e] + (size_t)(Sk + j) * d + c0 + c);
+      *(h16x8*)(sk + j * hd + c) = *(const h16x8*)(ex.a + (size_t)j * d + c0 + c);
+      *(h16x8*)(sv + j * hd + c) = *(const h16x8*)(ex.a + (size_t)(Sk + j) * d + c0 + c);
     }
   }
   __syncthreads();
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
   const float scale = 1.0f / sqrtf((float)hd);
-  for (int pr = wave; pr < Sq * Sk; pr += nw) {
+  for (int pr = wave; pr < S * Sk; pr += nw) {
     const int i = pr / Sk, j = pr - i * Sk;
     float part = 0.f;
     for (int c = lane * 8; c < hd; c += 512) {
@@ -107,29 +125,28 @@ __global__ void __launch_bounds__(1024) k_attn(AttnArgs a) {
       for (int t = 0; t < 8; ++t) part += (float)qa[t] * (float)kb[t];
     }
     const float s = wave_sum(part) * scale;
-    if (lane == 0) P[i][j] = (a.causal && j > i) ? -INFINITY : s;
+    if (lane == 0) P[i * Sk + j] = (SRC == S_SELF && j > i) ? -INFINITY : s;
   }
   __syncthreads();
-  if ((int)threadIdx.x < Sq) {
+  if ((int)threadIdx.x < S) {
     const int i = threadIdx.x;
     float m = -INFINITY;
-    for (int j = 0; j < Sk; ++j) m = fmaxf(m, P[i][j]);
+    for (int j = 0; j < Sk; ++j) m = fmaxf(m, P[i * Sk + j]);
     float den = 0.f;
     for (int j = 0; j < Sk; ++j) {
-      const float ex = expf(P[i][j] - m);
-      P[i][j] = ex;
-      den += ex;
+      const float ex2 = expf(P[i * Sk + j] - m);
+      P[i * Sk + j] = ex2;
+      den += ex2;
     }
     const float inv = 1.0f / den;
-    for (int j = 0; j < Sk; ++j) P[i][j] *= inv;
+    for (int j = 0; j < Sk; ++j) P[i * Sk + j] *= inv;
   }
   __syncthreads();
-  const int nv = hd / 8;
-  for (int idx = threadIdx.x; idx < Sq * nv; idx += blockDim.x) {
+  for (int idx = threadIdx.x; idx < S * nv; idx += blockDim.x) {
     const int i = idx / nv, c = (idx - i * nv) * 8;
     float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     for (int j = 0; j < Sk; ++j) {
-      const float p = P[i][j];
+      const float p = P[i * Sk + j];
       const h16x8 vb = *(const h16x8*)(sv + j * hd + c);
 #pragma unroll
       for (int t = 0; t < 8; ++t) o[t] += p * (float)vb[t];
@@ -137,13 +154,132 @@ __global__ void __launch_bounds__(1024) k_attn(AttnArgs a) {
     h16x8 ov;
 #pragma unroll
     for (int t = 0; t < 8; ++t) ov[t] = (h16)o[t];
-    *(h16x8*)(a.out[e] + (size_t)i * d + c0 + c) = ov;
+    *(h16x8*)(As + i * lda + c) = ov;
   }
 }
 
+template <int SRC, int EPI>
+__global__ void __launch_bounds__(SWMAX * 64) k_stream(SArgs a) {
+  extern __shared__ __align__(16) h16 lds[];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  int b = blockIdx.x;
+  const int per_ex = a.ks * a.wg_per_kc;
+  const int e = b / per_ex;
+  b -= e * per_ex;
+  const int kc = b / a.wg_per_kc;
+  const int tg = b - kc * a.wg_per_kc;
+  const SEx& ex = a.ex[e];
+  const int ksteps = a.K / 32;
+  const int KC = a.K / a.ks, nsteps = KC / 32;
+  const int t0 = (tg * a.wpb + wave) * a.tpw;
+  const int nf = a.tpw * nsteps;
+  const int lda = KC + 8;
+  const h16x8* wbase = ex.w + ((size_t)t0 * ksteps + (size_t)kc * nsteps) * 64 + lane;
+  auto frag = [&](int f) -> h16x8 {
+    const int tt = f / nsteps, s = f - tt * nsteps;
+    return __builtin_nontemporal_load(wbase + ((size_t)tt * ksteps + s) * 64);
+  };
+  // the weight stream does not depend on the activations: put PF loads in flight first
+  h16x8 buf[SPF];
+#pragma unroll
+  for (int p = 0; p < SPF; ++p)
+    if (p < nf) buf[p] = frag(p);
+  h16* As = lds;
+  if constexpr (SRC == S_BUF) {
+    const int nv = KC / 8;
+    for (int idx = threadIdx.x; idx < ex.S * nv; idx += blockDim.x) {
+      const int i = idx / nv, kk = (idx - i * nv) * 8;
+      *(h16x8*)(As + i * lda + kk) = *(const h16x8*)(ex.a + (size_t)i * ex.lda + (size_t)kc * KC + kk);
+    }
+  } else {
+    stage_attention<SRC>(a, ex, kc, As, lda, As + (size_t)ex.S * lda);
+  }
+  __syncthreads();
+  const int row = lane & 15, kg = lane >> 4;
+  const bool live = row < ex.S;
+  const h16* arow = As + (live ? row : 0) * lda + kg * 8;
+  const h16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+  const int col = lane & 15, rbase = 4 * (lane >> 4);
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int f0 = 0; f0 < nf; f0 += SPF) {
+#pragma unroll
+    for (int p = 0; p < SPF; ++p) {
+      const int f = f0 + p;
+      if (f < nf) {
+        const h16x8 bf = buf[p];
+        if (f + SPF < nf) buf[p] = frag(f + SPF);
+        const int tt = f / nsteps, s = f - tt * nsteps;
+        const h16x8 av = live ? *(const h16x8*)(arow + s * 32) : zero;
+        acc = mfma_f16(av, bf, acc);
+        if (s == nsteps - 1) {
+          const int n = (t0 + tt) * 16 + col;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int r = rbase + q;
+            if (r < ex.S) {
+              if constexpr (EPI == E_PART) {
+                ((float*)ex.out)[((size_t)kc * ex.S + r) * a.N + n] = acc[q];
+              } else if constexpr (EPI == E_BIAS16) {
+                ((h16*)ex.out)[(size_t)r * a.N + n] = (h16)(acc[q] + (float)ex.bias[n]);
+              } else {
+                ((h16*)ex.out)[(size_t)r * a.N + n] = (h16)gelu_erf(acc[q] + (float)ex.bias[n]);
+              }
+            }
+          }
+          acc = (f32x4){0.f, 0.f, 0.f, 0.f};
+        }
+      }
+    }
+  }
+}
+
+size_t stream_lds(int SRC, int S, int KC, int hd, int Ck) {
+  size_t lds = (size_t)S * (KC + 8) * 2;
+  if (SRC != S_BUF) {
+    const int Sk = SRC == S_SELF ? S : Ck;
+    lds += (size_t)(S + 2 * Sk) * hd * 2 + (size_t)S * Sk * 4;
+  }
+  return lds;
+}
+
+template <int SRC, int EPI>
+int launch_stream(const SArgs& a, int S_max, hipStream_t st) {
+  const int tiles = a.N / 16;
+  if (a.K % a.ks || (a.K / a.ks) % 32 || tiles % (a.wpb * a.tpw) || a.wpb > SWMAX) return CFH_E_UNSUPPORTED;
+  const size_t lds = stream_lds(SRC, S_max, a.K / a.ks, a.hd, a.Ck);
+  if (lds > 150 * 1024) return CFH_E_UNSUPPORTED;
+  // allow more than 64 KiB of dynamic LDS, once per device
+  static unsigned long long attr_set = 0;
+  int dev = 0;
+  CFH_HIP(hipGetDevice(&dev));
+  if (dev < 64 && !(attr_set & (1ull << dev))) {
+    CFH_HIP(hipFuncSetAttribute((const void*)k_stream<SRC, EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                150 * 1024));
+    attr_set |= 1ull << dev;
+  }
+  const long long wgs = (long long)a.nex * a.ks * a.wg_per_kc;
+  hipLaunchKernelGGL((k_stream<SRC, EPI>), dim3((unsigned)wgs), dim3(a.wpb * 64), lds, st, a);
+  CFH_LAUNCH_CHECK();
+  return CFH_OK;
+}
+
 // ---------------------------------------------------------------------------- row kernels
-// NORM: x[r] += sum_kc P[kc][r] + bias; a[r] = fp16(LN(fp16(x[r]))).  One workgroup per row.
-struct NormArgs {
+// RES: x[r] += sum_kc P[kc][r] + bias; a[r] = fp16(LN(fp16(x[r]))).  One workgroup per (expert,
+// row) of d / (4 NQ) threads, NQ float4 column groups each; the partial rows are loaded RB at a
+// time with every load of a batch in flight together.
+constexpr int RQ = 16;            // max float4 groups per thread (d <= 16384)
+constexpr int RB = 8;             // partial rows loaded per batch
+
+// NQ for a row of d columns: the smallest group count giving a whole number of waves and at most
+// 1024 threads (0 if none), so the row's loads spread over as many lanes as possible.
+int res_nq(int d) {
+  const int nq = d / 4;
+  for (int q = 1; q <= RQ; ++q)
+    if (nq % q == 0 && (nq / q) % 64 == 0 && nq / q <= 1024) return q;
+  return 0;
+}
+
+struct ResArgs {
   float* x[4];
   const float* P[4];
   const h16* bias[4];
@@ -154,55 +290,110 @@ struct NormArgs {
   int nex, ks, d;
 };
 
-__global__ void __launch_bounds__(ROWT) k_norm(NormArgs a) {
-  __shared__ float red[ROWT / 64];
-  int e = 0, r = blockIdx.x;
-  while (e + 1 < a.nex && r >= a.rows[e]) r -= a.rows[e++];
-  const int d = a.d, nq = d / 4;
+__device__ __forceinline__ float block_sum_rt(float v, float* red) {  // red[blockDim/64]
+  v = wave_sum(v);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t += red[w];
+  return t;
+}
+
+template <int NQ>
+__device__ void res_row(const ResArgs& a, int e, int r) {
+  __shared__ float red[16];
+  const int RT = blockDim.x;
+  const int d = a.d;
   const size_t pst = (size_t)a.rows[e] * d;
   float* xr = a.x[e] + (size_t)r * d;
   const float* Pr = a.P[e] + (size_t)r * d;
-  float4 acc[ROWQ], xv[ROWQ];
+  float4 acc[NQ], xv[NQ];
 #pragma unroll
-  for (int k = 0; k < ROWQ; ++k) {
-    const int q = threadIdx.x + k * blockDim.x;
-    if (q < nq) {
-      xv[k] = *(const float4*)(xr + q * 4);
-      acc[k] = *(const float4*)(Pr + q * 4);
-    }
+  for (int k = 0; k < NQ; ++k) {
+    const int q = threadIdx.x + k * RT;
+    xv[k] = *(const float4*)(xr + q * 4);
+    acc[k] = *(const float4*)(Pr + q * 4);
   }
-#pragma unroll 4
-  for (int kc = 1; kc < a.ks; ++kc) {
+  for (int kc = 1; kc < a.ks; kc += RB) {
+    float4 t[RB][NQ];
 #pragma unroll
-    for (int k = 0; k < ROWQ; ++k) {
-      const int q = threadIdx.x + k * blockDim.x;
-      if (q < nq) {
-        const float4 t = *(const float4*)(Pr + kc * pst + q * 4);
-        acc[k].x += t.x; acc[k].y += t.y; acc[k].z += t.z; acc[k].w += t.w;
-      }
-    }
-  }
-  float4 vals[ROWQ];
+    for (int u = 0; u < RB; ++u)
 #pragma unroll
-  for (int k = 0; k < ROWQ; ++k) {
-    const int q = threadIdx.x + k * blockDim.x;
-    vals[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (q < nq) {
-      const h16* bb = a.bias[e] + q * 4;
-      float4 xn;
-      xn.x = xv[k].x + (acc[k].x + (float)bb[0]);
-      xn.y = xv[k].y + (acc[k].y + (float)bb[1]);
-      xn.z = xv[k].z + (acc[k].z + (float)bb[2]);
-      xn.w = xv[k].w + (acc[k].w + (float)bb[3]);
-      *(float4*)(xr + q * 4) = xn;
-      vals[k] = r16x4(xn);
-    }
+      for (int k = 0; k < NQ; ++k)
+        t[u][k] = kc + u < a.ks ? *(const float4*)(Pr + (kc + u) * pst + (threadIdx.x + k * RT) * 4)
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int u = 0; u < RB; ++u)
+#pragma unroll
+      for (int k = 0; k < NQ; ++k)
+        if (kc + u < a.ks) {
+          acc[k].x += t[u][k].x; acc[k].y += t[u][k].y; acc[k].z += t[u][k].z; acc[k].w += t[u][k].w;
+        }
   }
-  ln_row4(vals, d, a.g[e], a.b[e], a.a[e] + (size_t)r * d, red);
+  float4 vals[NQ];
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < NQ; ++k) {
+    const int q = threadIdx.x + k * RT;
+    const h16* bb = a.bias[e] + q * 4;
+    float4 xn;
+    xn.x = xv[k].x + (acc[k].x + (float)bb[0]);
+    xn.y = xv[k].y + (acc[k].y + (float)bb[1]);
+    xn.z = xv[k].z + (acc[k].z + (float)bb[2]);
+    xn.w = xv[k].w + (acc[k].w + (float)bb[3]);
+    *(float4*)(xr + q * 4) = xn;
+    vals[k] = r16x4(xn);
+    s += (vals[k].x + vals[k].y) + (vals[k].z + vals[k].w);
+  }
+  const float mean = block_sum_rt(s, red) / (float)d;
+  float v = 0.f;
+#pragma unroll
+  for (int k = 0; k < NQ; ++k) {
+    const float a0 = vals[k].x - mean, a1 = vals[k].y - mean, a2 = vals[k].z - mean, a3 = vals[k].w - mean;
+    v += (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
+  }
+  const float rstd = 1.0f / sqrtf(block_sum_rt(v, red) / (float)d + LN_EPS);
+  const h16* g = a.g[e];
+  const h16* bt = a.b[e];
+  h16* out = a.a[e] + (size_t)r * d;
+#pragma unroll
+  for (int k = 0; k < NQ; ++k) {
+    const int c = (threadIdx.x + k * RT) * 4;
+    out[c + 0] = (h16)((vals[k].x - mean) * rstd * (float)g[c + 0] + (float)bt[c + 0]);
+    out[c + 1] = (h16)((vals[k].y - mean) * rstd * (float)g[c + 1] + (float)bt[c + 1]);
+    out[c + 2] = (h16)((vals[k].z - mean) * rstd * (float)g[c + 2] + (float)bt[c + 2]);
+    out[c + 3] = (h16)((vals[k].w - mean) * rstd * (float)g[c + 3] + (float)bt[c + 3]);
+  }
+}
+
+template <int NQ>
+__global__ void __launch_bounds__(1024) k_res(ResArgs a) {
+  int e = 0, r = blockIdx.x;
+  while (e + 1 < a.nex && r >= a.rows[e]) r -= a.rows[e++];
+  res_row<NQ>(a, e, r);
+}
+
+int launch_res(const ResArgs& a, hipStream_t st) {
+  int total = 0;
+  for (int e = 0; e < a.nex; ++e) total += a.rows[e];
+  const int NQ = res_nq(a.d);
+  const int threads = NQ ? a.d / 4 / NQ : 0;
+  switch (NQ) {
+#define CFH_RES(N) \
+  case N: hipLaunchKernelGGL(k_res<N>, dim3(total), dim3(threads), 0, st, a); break;
+    CFH_RES(1) CFH_RES(2) CFH_RES(3) CFH_RES(4) CFH_RES(5) CFH_RES(6) CFH_RES(7) CFH_RES(8)
+    CFH_RES(9) CFH_RES(10) CFH_RES(11) CFH_RES(12) CFH_RES(13) CFH_RES(14) CFH_RES(15) CFH_RES(16)
+#undef CFH_RES
+    default: return CFH_E_UNSUPPORTED;
+  }
+  CFH_LAUNCH_CHECK();
+  return CFH_OK;
 }
 
 // ROWS: one workgroup per z row r.
-//   init  : z[r] = init_latents(ctx)[r] (delta mode, fp16 arithmetic)
+//   init  : z[r] = init_latents(ctx)[r] (delta mode, fp16 arithmetic); context row moments
 //   euler : v = fp16(sum_kc Pout[kc][i] + b_out) for the chunk c, row i owning z row r;
 //           z[r] = fp16(z[r] + fp16(dt v))   (z_out[r] = z[r] after the last step)
 // then, unless this was the last step, the next step's rows: for every expert c2 that reads z row
@@ -278,15 +469,21 @@ __global__ void __launch_bounds__(ROWT) k_rows(RowsArgs a) {
         zo[k] = *(const float4*)(a.z + (size_t)r * d + q * 4);
       }
     }
-    for (int kc = 1; kc < a.ks; ++kc) {
+    for (int kc = 1; kc < a.ks; kc += 2) {
+      float4 t[2][ROWQ];
 #pragma unroll
-      for (int k = 0; k < ROWQ; ++k) {
-        const int q = threadIdx.x + k * blockDim.x;
-        if (q < nq) {
-          const float4 t = *(const float4*)(Pr + kc * pst + q * 4);
-          acc[k].x += t.x; acc[k].y += t.y; acc[k].z += t.z; acc[k].w += t.w;
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int k = 0; k < ROWQ; ++k) {
+          const int q = threadIdx.x + k * blockDim.x;
+          t[u][k] = (q < nq && kc + u < a.ks) ? *(const float4*)(Pr + (kc + u) * pst + q * 4)
+                                              : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int k = 0; k < ROWQ; ++k)
+          if (kc + u < a.ks) { acc[k].x += t[u][k].x; acc[k].y += t[u][k].y; acc[k].z += t[u][k].z; acc[k].w += t[u][k].w; }
     }
 #pragma unroll
     for (int k = 0; k < ROWQ; ++k) {
@@ -336,23 +533,59 @@ __global__ void __launch_bounds__(ROWT) k_rows(RowsArgs a) {
 }
 
 // ---------------------------------------------------------------------------- host side
+// Split-K factor of a streaming GEMV: the smallest divisor of the k-step count that leaves at
+// least 8 k-steps per unit, keeps the A chunk within `lds_cap`, and gives >= `target` wave units;
+// else the largest valid one.
+int choose_ks(int nex, int tiles, int K, int S, int target, size_t lds_cap) {
+  const int steps = K / 32;
+  int best = -1;
+  for (int ks = 1; ks <= steps; ++ks) {
+    if (steps % ks || steps / ks < 8) continue;
+    if ((size_t)S * (K / ks + 8) * 2 > lds_cap) continue;
+    best = ks;
+    if ((long long)nex * ks * tiles >= target) break;
+  }
+  return best;
+}
+
 struct Plan {
-  int d, fd, CS, E, NL, C, KD, H, nch;
-  int ks_qkv, ks_o, ks_w1, ks_w2, ks_out, ks_kv, ks_tau;
+  int d, fd, CS, E, NL, C, KD, H, hd, nch, Smax;
+  int ks_qc, ks_w2, ks_out, ks_kv, ks_tau;
+  int wpb_qc, wpb_w2, wpb_out, tpw_att, wpb_att, wpb_full;
+  int pks;            // partial slots per expert
+  bool ok;
 };
 
+int pick_wpb(int tiles, int tpw) {
+  for (int w : {8, 4, 2, 1})
+    if (tiles % (w * tpw) == 0) return w;
+  return 1;
+}
+
 Plan make_plan(const cfh_flow_dims* dm) {
-  Plan p;
+  Plan p = {};
   p.d = dm->d; p.fd = dm->ffn_mult * dm->d; p.CS = dm->chunk_size; p.E = dm->flow_steps;
-  p.NL = dm->layers; p.C = dm->ctx_rows; p.KD = dm->draft_length; p.H = dm->heads;
+  p.NL = dm->layers; p.C = dm->ctx_rows; p.KD = dm->draft_length; p.H = dm->heads; p.hd = p.d / p.H;
   p.nch = p.KD / p.CS;
-  p.ks_qkv = ksplit_for(p.nch, 3 * p.d / 16, p.d, p.KD);
-  p.ks_o = ksplit_for(p.nch, p.d / 16, p.d, p.KD);
-  p.ks_w1 = ksplit_for(p.nch, p.fd / 16, p.d, p.KD);
-  p.ks_w2 = ksplit_for(p.nch, p.d / 16, p.fd, p.KD);
-  p.ks_out = ksplit_for(p.nch, p.d / 16, p.d, p.CS);
+  p.Smax = p.KD;
+  const int tiles_d = p.d / 16;
+  const size_t cap = 96 * 1024;
+  p.ks_qc = choose_ks(p.nch, tiles_d, p.d, p.Smax, 2048, cap);
+  p.ks_w2 = choose_ks(p.nch, tiles_d, p.fd, p.Smax, 4096, cap);
+  p.ks_out = choose_ks(p.nch, tiles_d, p.d, p.CS, 2048, cap);
   p.ks_kv = ksplit_for(p.nch * p.NL, 2 * p.d / 16, p.d, p.C);
   p.ks_tau = ksplit_for(p.nch, p.d / 16, p.d, p.E);
+  p.wpb_qc = pick_wpb(tiles_d, 1);
+  p.wpb_w2 = pick_wpb(tiles_d, 1);
+  p.wpb_out = pick_wpb(tiles_d, 1);
+  p.tpw_att = (tiles_d % 16 == 0) ? 2 : 1;
+  p.wpb_att = pick_wpb(tiles_d, p.tpw_att);
+  p.wpb_full = 8;
+  p.pks = std::max(std::max(p.H, p.ks_w2), p.ks_out);
+  p.ok = p.ks_qc > 0 && p.ks_w2 > 0 && p.ks_out > 0 && p.hd % 32 == 0 && (3 * tiles_d) % 8 == 0 &&
+         (p.fd / 16) % 8 == 0 && stream_lds(S_BUF, p.Smax, p.d, p.hd, p.C) <= 150 * 1024 &&
+         stream_lds(S_SELF, p.Smax, p.hd, p.hd, p.C) <= 150 * 1024 &&
+         stream_lds(S_CROSS, p.Smax, p.hd, p.hd, p.C) <= 150 * 1024 && res_nq(p.d) > 0;
   return p;
 }
 
@@ -360,10 +593,10 @@ struct WS {
   float* z;
   float* x[4];
   h16* abuf[4];
-  h16* attn[4];
+  h16* qkv[4];
   h16* g[4];
-  float* P[4];        // partials of the current GEMV
-  float* Pw1[4];      // W1 partials (read by GELU)
+  float* P[4];        // partials of the split-K kernels (O, OC, W2, OUT)
+  float* Pq[4];       // cross-q partials (QC), read by OC
   h16* tau[4];        // [E][d]
   h16* kvc[4];        // [L][2][C][d]
   float* Pkv;         // [nch][L][ks][C][2d]
@@ -386,14 +619,10 @@ WS carve(const Plan& p, char* base) {
     const size_t S = (size_t)(c + 1) * p.CS;
     w.x[c] = (float*)take(S * d * 4);
     w.abuf[c] = (h16*)take(S * d * 2);
-    w.attn[c] = (h16*)take(S * d * 2);
+    w.qkv[c] = (h16*)take(S * 3 * d * 2);
     w.g[c] = (h16*)take(S * fd * 2);
-    size_t pmax = (size_t)p.ks_qkv * S * 3 * d;
-    pmax = std::max(pmax, (size_t)p.ks_o * S * d);
-    pmax = std::max(pmax, (size_t)p.ks_w2 * S * d);
-    pmax = std::max(pmax, (size_t)p.ks_out * p.CS * d);
-    w.P[c] = (float*)take(pmax * 4);
-    w.Pw1[c] = (float*)take((size_t)p.ks_w1 * S * fd * 4);
+    w.P[c] = (float*)take((size_t)p.pks * S * d * 4);
+    w.Pq[c] = (float*)take((size_t)p.ks_qc * S * d * 4);
     w.tau[c] = (h16*)take((size_t)p.E * d * 2);
     w.kvc[c] = (h16*)take((size_t)p.NL * 2 * p.C * d * 2);
   }
@@ -404,144 +633,112 @@ WS carve(const Plan& p, char* base) {
   return w;
 }
 
-int launch_attn(const AttnArgs& a, int nex, int sq_max, int sk_max, hipStream_t st) {
-  const size_t lds = (size_t)(sq_max + 2 * sk_max) * a.hd * 2;
-  if (lds > 120 * 1024 || sq_max > MAXR || sk_max > MAXR) return CFH_E_UNSUPPORTED;
-  hipLaunchKernelGGL(k_attn, dim3(nex * a.heads), dim3(1024), lds, st, a);
-  CFH_LAUNCH_CHECK();
-  return CFH_OK;
-}
-
-
-// One launch of one chunk expert's Euler step.  Kernel k of block l (k = 0..11):
-//   0 QKV, 1 self attention, 2 O, 3 NORM(LN_cross), 4 QC, 5 cross attention, 6 OC, 7 NORM(LN_ffn),
-//   8 W1, 9 GELU, 10 W2, 11 NORM(next LN);  l == NL, k == 0: out_proj on the current chunk rows.
-constexpr int KPB = 12;   // kernels per block and expert
-
-int expert_kernel(const Plan& p, const cfh::ExpertLayout& L, const WS& w, const void* expert, int c, int l,
-                  int k, hipStream_t st) {
-  const int d = p.d, fd = p.fd, CS = p.CS, NL = p.NL, C = p.C, H = p.H;
-  const int S = (c + 1) * CS;
-  auto PTR = [&](size_t off) { return (const char*)expert + off; };
-  auto BLK = [&](int ll) { return L.blk0 + (size_t)ll * L.blkstride; };
-  if (l == NL) {
-    GemvArgs a = {};
-    a.nex = 1; a.nl = 1; a.E = p.E; a.ks = p.ks_out; a.tiles = d / 16; a.N = d; a.K = d;
-    GemvEx& x = a.ex[0];
-    x.w = (const h16x8*)PTR(L.out);
-    x.a = w.abuf[c] + (size_t)c * CS * d;   // out_norm rows of the current chunk
-    x.lda = d; x.pout = w.P[c]; x.rows = CS;
-    return launch_gemv<SRC_BUF>(a, CS, st);
-  }
-  const size_t B = BLK(l);
-  GemvArgs a = {};
-  a.nex = 1; a.nl = 1; a.E = p.E;
-  GemvEx& x = a.ex[0];
-  x.lda = d; x.pout = w.P[c]; x.rows = S;
-  AttnArgs at = {};
-  at.d = d; at.heads = H; at.hd = d / H; at.P[0] = w.P[c]; at.out[0] = w.attn[c]; at.Sq[0] = S;
-  NormArgs nm = {};
-  nm.nex = 1; nm.d = d; nm.x[0] = w.x[c]; nm.P[0] = w.P[c]; nm.a[0] = w.abuf[c]; nm.rows[0] = S;
-  switch (k) {
-    case 0:  // QKV
-      a.ks = p.ks_qkv; a.tiles = 3 * d / 16; a.N = 3 * d; a.K = d;
-      x.w = (const h16x8*)PTR(B + L.qkv); x.a = w.abuf[c];
-      return launch_gemv<SRC_BUF>(a, S, st);
-    case 1:  // causal self attention
-      at.ks = p.ks_qkv; at.ldp = 3 * d; at.causal = 1; at.bias[0] = (const h16*)PTR(B + L.qkv_b);
-      at.kv[0] = nullptr; at.Sk[0] = S;
-      return launch_attn(at, 1, S, S, st);
-    case 2:  // O
-      a.ks = p.ks_o; a.tiles = d / 16; a.N = d; a.K = d;
-      x.w = (const h16x8*)PTR(B + L.o); x.a = w.attn[c];
-      return launch_gemv<SRC_BUF>(a, S, st);
-    case 3:  // residual + LN_cross
-      nm.ks = p.ks_o; nm.bias[0] = (const h16*)PTR(B + L.o_b);
-      nm.g[0] = (const h16*)PTR(B + L.xn_w); nm.b[0] = (const h16*)PTR(B + L.xn_b);
-      hipLaunchKernelGGL(k_norm, dim3(S), dim3(ROWT), 0, st, nm);
-      CFH_LAUNCH_CHECK();
-      return CFH_OK;
-    case 4:  // QC
-      a.ks = p.ks_o; a.tiles = d / 16; a.N = d; a.K = d;
-      x.w = (const h16x8*)PTR(B + L.qc); x.a = w.abuf[c];
-      return launch_gemv<SRC_BUF>(a, S, st);
-    case 5:  // cross attention over the hoisted context K/V
-      at.ks = p.ks_o; at.ldp = d; at.causal = 0; at.bias[0] = (const h16*)PTR(B + L.qc_b);
-      at.kv[0] = w.kvc[c] + (size_t)l * 2 * C * d; at.Sk[0] = C;
-      return launch_attn(at, 1, S, C, st);
-    case 6:  // OC
-      a.ks = p.ks_o; a.tiles = d / 16; a.N = d; a.K = d;
-      x.w = (const h16x8*)PTR(B + L.oc); x.a = w.attn[c];
-      return launch_gemv<SRC_BUF>(a, S, st);
-    case 7:  // residual + LN_ffn
-      nm.ks = p.ks_o; nm.bias[0] = (const h16*)PTR(B + L.oc_b);
-      nm.g[0] = (const h16*)PTR(B + L.fn_w); nm.b[0] = (const h16*)PTR(B + L.fn_b);
-      hipLaunchKernelGGL(k_norm, dim3(S), dim3(ROWT), 0, st, nm);
-      CFH_LAUNCH_CHECK();
-      return CFH_OK;
-    case 8:  // W1
-      a.ks = p.ks_w1; a.tiles = fd / 16; a.N = fd; a.K = d;
-      x.w = (const h16x8*)PTR(B + L.w1); x.a = w.abuf[c]; x.pout = w.Pw1[c];
-      return launch_gemv<SRC_BUF>(a, S, st);
-    case 9: {  // GELU
-      GeluArgs ge = {};
-      ge.nex = 1; ge.ks = p.ks_w1; ge.N = fd;
-      ge.P[0] = w.Pw1[c]; ge.b[0] = (const h16*)PTR(B + L.w1_b); ge.g[0] = w.g[c]; ge.rows[0] = S;
-      hipLaunchKernelGGL(k_gelu, dim3(192), dim3(256), 0, st, ge);
-      CFH_LAUNCH_CHECK();
-      return CFH_OK;
+// The nine launches of block l (both experts in each).
+int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w, const void* const* experts, int l,
+               hipStream_t st) {
+  const int d = p.d, fd = p.fd, NL = p.NL, nch = p.nch;
+  auto PTR = [&](int c, size_t off) { return (const char*)experts[c] + off; };
+  const size_t B = L.blk0 + (size_t)l * L.blkstride;
+  auto S_of = [&](int c) { return (c + 1) * p.CS; };
+  int rc;
+  // QKV: q, k, v = fp16(LN_self(x) W_in^T + b_in), full-K tiles
+  {
+    SArgs a = {};
+    a.nex = nch; a.N = 3 * d; a.K = d; a.ks = 1; a.wpb = p.wpb_full; a.tpw = 1; a.d = d; a.hd = p.hd;
+    a.wg_per_kc = (3 * d / 16) / (a.wpb * a.tpw);
+    for (int c = 0; c < nch; ++c) {
+      SEx& x = a.ex[c];
+      x.w = (const h16x8*)PTR(c, B + L.qkv); x.a = w.abuf[c]; x.lda = d; x.bias = (const h16*)PTR(c, B + L.qkv_b);
+      x.out = w.qkv[c]; x.S = S_of(c);
     }
-    case 10:  // W2
-      a.ks = p.ks_w2; a.tiles = d / 16; a.N = d; a.K = fd;
-      x.w = (const h16x8*)PTR(B + L.w2); x.a = w.g[c]; x.lda = fd;
-      return launch_gemv<SRC_BUF>(a, S, st);
-    case 11:  // residual + LayerNorm of the next block (out_norm after the last block)
-      nm.ks = p.ks_w2; nm.bias[0] = (const h16*)PTR(B + L.w2_b);
-      if (l + 1 < NL) {
-        nm.g[0] = (const h16*)PTR(BLK(l + 1) + L.sn_w); nm.b[0] = (const h16*)PTR(BLK(l + 1) + L.sn_b);
-      } else {
-        nm.g[0] = (const h16*)PTR(L.on_w); nm.b[0] = (const h16*)PTR(L.on_b);
-      }
-      hipLaunchKernelGGL(k_norm, dim3(S), dim3(ROWT), 0, st, nm);
-      CFH_LAUNCH_CHECK();
-      return CFH_OK;
+    if ((rc = launch_stream<S_BUF, E_BIAS16>(a, p.Smax, st))) return rc;
   }
-  return CFH_E_INVALID;
-}
-
-// Side streams and fork/join events (one set per device, created on first use).
-struct SideStreams {
-  hipStream_t st[4];
-  hipEvent_t fork;
-  hipEvent_t join[4];
-};
-
-SideStreams* side_streams(int* status) {
-  static SideStreams cache[64];
-  static bool made[64];
-  static std::mutex mu;
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess || dev < 0 || dev >= 64) {
-    *status = cfh::set_hip_error(e == hipSuccess ? hipErrorInvalidDevice : e);
-    return nullptr;
-  }
-  std::lock_guard<std::mutex> lock(mu);
-  SideStreams& s = cache[dev];
-  if (!made[dev]) {
-    s.st[0] = nullptr;
-    for (int c = 1; c < 4; ++c)
-      if ((e = hipStreamCreateWithFlags(&s.st[c], hipStreamNonBlocking)) != hipSuccess) break;
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&s.fork, hipEventDisableTiming);
-    for (int c = 0; c < 4 && e == hipSuccess; ++c) e = hipEventCreateWithFlags(&s.join[c], hipEventDisableTiming);
-    if (e != hipSuccess) {
-      *status = cfh::set_hip_error(e);
-      return nullptr;
+  // O: causal self attention per head, staged, then out_proj split-K by head
+  {
+    SArgs a = {};
+    a.nex = nch; a.N = d; a.K = d; a.ks = p.H; a.wpb = p.wpb_att; a.tpw = p.tpw_att; a.d = d; a.hd = p.hd;
+    a.wg_per_kc = (d / 16) / (a.wpb * a.tpw);
+    for (int c = 0; c < nch; ++c) {
+      SEx& x = a.ex[c];
+      x.w = (const h16x8*)PTR(c, B + L.o); x.a = w.qkv[c]; x.out = w.P[c]; x.S = S_of(c);
     }
-    made[dev] = true;
+    if ((rc = launch_stream<S_SELF, E_PART>(a, p.Smax, st))) return rc;
   }
-  *status = CFH_OK;
-  return &s;
+  ResArgs r = {};
+  r.nex = nch; r.d = d;
+  for (int c = 0; c < nch; ++c) { r.x[c] = w.x[c]; r.P[c] = w.P[c]; r.a[c] = w.abuf[c]; r.rows[c] = S_of(c); }
+  // residual + LN_cross
+  r.ks = p.H;
+  for (int c = 0; c < nch; ++c) {
+    r.bias[c] = (const h16*)PTR(c, B + L.o_b);
+    r.g[c] = (const h16*)PTR(c, B + L.xn_w); r.b[c] = (const h16*)PTR(c, B + L.xn_b);
+  }
+  if ((rc = launch_res(r, st))) return rc;
+  // QC: cross-attention query projection, split-K partials
+  {
+    SArgs a = {};
+    a.nex = nch; a.N = d; a.K = d; a.ks = p.ks_qc; a.wpb = p.wpb_qc; a.tpw = 1; a.d = d; a.hd = p.hd;
+    a.wg_per_kc = (d / 16) / (a.wpb * a.tpw);
+    for (int c = 0; c < nch; ++c) {
+      SEx& x = a.ex[c];
+      x.w = (const h16x8*)PTR(c, B + L.qc); x.a = w.abuf[c]; x.lda = d; x.out = w.Pq[c]; x.S = S_of(c);
+    }
+    if ((rc = launch_stream<S_BUF, E_PART>(a, p.Smax, st))) return rc;
+  }
+  // OC: cross attention per head over the hoisted context K/V, staged, then out_proj split-K by head
+  {
+    SArgs a = {};
+    a.nex = nch; a.N = d; a.K = d; a.ks = p.H; a.wpb = p.wpb_att; a.tpw = p.tpw_att; a.d = d; a.hd = p.hd;
+    a.ks_in = p.ks_qc; a.Ck = p.C;
+    a.wg_per_kc = (d / 16) / (a.wpb * a.tpw);
+    for (int c = 0; c < nch; ++c) {
+      SEx& x = a.ex[c];
+      x.w = (const h16x8*)PTR(c, B + L.oc); x.a = w.kvc[c] + (size_t)l * 2 * p.C * d; x.pin = w.Pq[c];
+      x.bin = (const h16*)PTR(c, B + L.qc_b); x.out = w.P[c]; x.S = S_of(c);
+    }
+    if ((rc = launch_stream<S_CROSS, E_PART>(a, p.Smax, st))) return rc;
+  }
+  // residual + LN_ffn
+  for (int c = 0; c < nch; ++c) {
+    r.bias[c] = (const h16*)PTR(c, B + L.oc_b);
+    r.g[c] = (const h16*)PTR(c, B + L.fn_w); r.b[c] = (const h16*)PTR(c, B + L.fn_b);
+  }
+  if ((rc = launch_res(r, st))) return rc;
+  // W1: g = fp16(gelu(LN_ffn(x) W1^T + b1)), full-K tiles
+  {
+    SArgs a = {};
+    a.nex = nch; a.N = fd; a.K = d; a.ks = 1; a.wpb = p.wpb_full; a.tpw = 1; a.d = d; a.hd = p.hd;
+    a.wg_per_kc = (fd / 16) / (a.wpb * a.tpw);
+    for (int c = 0; c < nch; ++c) {
+      SEx& x = a.ex[c];
+      x.w = (const h16x8*)PTR(c, B + L.w1); x.a = w.abuf[c]; x.lda = d; x.bias = (const h16*)PTR(c, B + L.w1_b);
+      x.out = w.g[c]; x.S = S_of(c);
+    }
+    if ((rc = launch_stream<S_BUF, E_GELU16>(a, p.Smax, st))) return rc;
+  }
+  // W2: split-K partials
+  {
+    SArgs a = {};
+    a.nex = nch; a.N = d; a.K = fd; a.ks = p.ks_w2; a.wpb = p.wpb_w2; a.tpw = 1; a.d = d; a.hd = p.hd;
+    a.wg_per_kc = (d / 16) / (a.wpb * a.tpw);
+    for (int c = 0; c < nch; ++c) {
+      SEx& x = a.ex[c];
+      x.w = (const h16x8*)PTR(c, B + L.w2); x.a = w.g[c]; x.lda = fd; x.out = w.P[c]; x.S = S_of(c);
+    }
+    if ((rc = launch_stream<S_BUF, E_PART>(a, p.Smax, st))) return rc;
+  }
+  // residual + LayerNorm of the next block (out_norm after the last block)
+  r.ks = p.ks_w2;
+  for (int c = 0; c < nch; ++c) {
+    r.bias[c] = (const h16*)PTR(c, B + L.w2_b);
+    if (l + 1 < NL) {
+      const size_t Bn = L.blk0 + (size_t)(l + 1) * L.blkstride;
+      r.g[c] = (const h16*)PTR(c, Bn + L.sn_w); r.b[c] = (const h16*)PTR(c, Bn + L.sn_b);
+    } else {
+      r.g[c] = (const h16*)PTR(c, L.on_w); r.b[c] = (const h16*)PTR(c, L.on_b);
+    }
+  }
+  return launch_res(r, st);
 }
 
 }  // namespace
@@ -550,8 +747,9 @@ extern "C" {
 
 int cfh_caps(const cfh_flow_dims* dims, int batch, int64_t* ws_bytes) {
   if (!cfh::flow_dims_ok(dims) || batch < 1) return CFH_E_UNSUPPORTED;
-  if (dims->d > ROWT * ROWE) return CFH_E_UNSUPPORTED;
+  if (dims->d > ROWT * ROWE || dims->draft_length > MAXR) return CFH_E_UNSUPPORTED;
   const Plan p = make_plan(dims);
+  if (!p.ok) return CFH_E_UNSUPPORTED;
   const WS w = carve(p, nullptr);
   if (ws_bytes) *ws_bytes = (int64_t)w.total;
   return CFH_OK;
@@ -559,9 +757,10 @@ int cfh_caps(const cfh_flow_dims* dims, int batch, int64_t* ws_bytes) {
 
 int cfh_flow_integrate(const cfh_flow_dims* dm, const void* const* experts, const void* ctx, void* z_out,
                        void* ws_ptr, int batch, void* stream) {
-  if (!cfh::flow_dims_ok(dm) || dm->d > ROWT * ROWE) return CFH_E_UNSUPPORTED;
+  if (!cfh::flow_dims_ok(dm) || dm->d > ROWT * ROWE || dm->draft_length > MAXR) return CFH_E_UNSUPPORTED;
   if (!experts || !ctx || !z_out || !ws_ptr || batch < 1) return CFH_E_INVALID;
   const Plan p = make_plan(dm);
+  if (!p.ok) return CFH_E_UNSUPPORTED;
   for (int c = 0; c < p.nch; ++c)
     if (!experts[c]) return CFH_E_INVALID;
   hipStream_t st = (hipStream_t)stream;
@@ -569,8 +768,6 @@ int cfh_flow_integrate(const cfh_flow_dims* dm, const void* const* experts, cons
   const WS w = carve(p, (char*)ws_ptr);
   const int d = p.d, CS = p.CS, E = p.E, NL = p.NL, C = p.C, KD = p.KD, nch = p.nch;
   int rc = CFH_OK;
-  SideStreams* side = nullptr;
-  if (nch > 1 && !(side = side_streams(&rc))) return rc;
   auto PTR = [&](int c, size_t off) { return (const char*)experts[c] + off; };
   auto BLK = [&](int l) { return L.blk0 + (size_t)l * L.blkstride; };
 
@@ -578,7 +775,7 @@ int cfh_flow_integrate(const cfh_flow_dims* dm, const void* const* experts, cons
     const h16* ctx_b = (const h16*)ctx + (size_t)b * C * d;
     h16* zo_b = (h16*)z_out + (size_t)b * KD * d;
 
-    // ---- per draft: time embeddings of every step, z0 + step-0 rows, cross K/V of every block
+    // ---- per draft: time embeddings of every step
     {
       GemvArgs a = {};
       a.nex = nch; a.nl = 1; a.ks = p.ks_tau; a.tiles = d / 16; a.N = d; a.K = d; a.E = E;
@@ -604,8 +801,8 @@ int cfh_flow_integrate(const cfh_flow_dims* dm, const void* const* experts, cons
     // ---- z0 and the step-0 rows
     {
       RowsArgs r = {};
-      r.ctx = ctx_b; r.ctx_mom = w.ctx_mom; r.z = w.z; r.z_out = zo_b; r.euler = 0; r.last = 0; r.d = d; r.C = C; r.CS = CS;
-      r.nch = nch;
+      r.ctx = ctx_b; r.ctx_mom = w.ctx_mom; r.z = w.z; r.z_out = zo_b; r.euler = 0; r.last = 0; r.d = d; r.C = C;
+      r.CS = CS; r.nch = nch;
       for (int c = 0; c < nch; ++c) {
         r.x[c] = w.x[c]; r.pos[c] = (const h16*)PTR(c, L.pos); r.tau[c] = w.tau[c];
         r.g[c] = (const h16*)PTR(c, BLK(0) + L.sn_w); r.b[c] = (const h16*)PTR(c, BLK(0) + L.sn_b);
@@ -614,7 +811,7 @@ int cfh_flow_integrate(const cfh_flow_dims* dm, const void* const* experts, cons
       hipLaunchKernelGGL(k_rows, dim3(KD), dim3(ROWT), 0, st, r);
       CFH_LAUNCH_CHECK();
     }
-
+    // ---- cross K/V of every block (once per draft)
     {
       GemvArgs a = {};
       a.nex = nch; a.nl = NL; a.ks = p.ks_kv; a.tiles = 2 * d / 16; a.N = 2 * d; a.K = d; a.E = E;
@@ -642,25 +839,19 @@ int cfh_flow_integrate(const cfh_flow_dims* dm, const void* const* experts, cons
       CFH_LAUNCH_CHECK();
     }
     for (int s = 0; s < E; ++s) {
-      // The chunk experts are independent within an Euler step (their inputs are slices of the
-      // step's z): expert 0 runs on the caller's stream, the others on side streams, so one
-      // expert's boundary kernels overlap the other's weight streaming.  Join before the update.
-      if (nch > 1) {
-        CFH_HIP(hipEventRecord(side->fork, st));
-        for (int c = 1; c < nch; ++c) CFH_HIP(hipStreamWaitEvent(side->st[c], side->fork, 0));
-      }
-      // Launches alternate between the experts' streams, kernel by kernel.
-      for (int l = 0; l <= NL; ++l) {
-        const int nk = l < NL ? KPB : 1;
-        for (int k = 0; k < nk; ++k)
-          for (int c = 0; c < nch; ++c)
-            if ((rc = expert_kernel(p, L, w, experts[c], c, l, k, c == 0 ? st : side->st[c]))) return rc;
-      }
-      if (nch > 1) {
-        for (int c = 1; c < nch; ++c) {
-          CFH_HIP(hipEventRecord(side->join[c], side->st[c]));
-          CFH_HIP(hipStreamWaitEvent(st, side->join[c], 0));
+      for (int l = 0; l < NL; ++l)
+        if ((rc = block_pass(p, L, w, experts, l, st))) return rc;
+      // OUT: out_proj on the out_norm rows of each expert's current chunk
+      {
+        SArgs a = {};
+        a.nex = nch; a.N = d; a.K = d; a.ks = p.ks_out; a.wpb = p.wpb_out; a.tpw = 1; a.d = d; a.hd = p.hd;
+        a.wg_per_kc = (d / 16) / (a.wpb * a.tpw);
+        for (int c = 0; c < nch; ++c) {
+          SEx& x = a.ex[c];
+          x.w = (const h16x8*)PTR(c, L.out); x.a = w.abuf[c] + (size_t)c * CS * d; x.lda = d; x.out = w.P[c];
+          x.S = CS;
         }
+        if ((rc = launch_stream<S_BUF, E_PART>(a, CS, st))) return rc;
       }
       RowsArgs r = {};
       r.ctx = ctx_b; r.z = w.z; r.z_out = zo_b; r.euler = 1; r.last = (s + 1 == E); r.ks = p.ks_out;

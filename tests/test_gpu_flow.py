@@ -31,7 +31,7 @@ def _flow_weights(cfg, init="test", seed=0):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("d,layers,steps", [(512, 1, 1), (512, 2, 2), (1024, 2, 3)])
+@pytest.mark.parametrize("d,layers,steps", [(512, 1, 1), (512, 2, 2), (1024, 2, 3), (2560, 1, 2)])
 def test_flow_matches_oracle(cuda, d, layers, steps):
     cfg = flownet(d, layers=layers, flow_steps=steps)
     W = _flow_weights(cfg)

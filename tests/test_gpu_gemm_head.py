@@ -1,10 +1,12 @@
 """GPU parity of the batched MFMA head (cfh_head_gemm_topk): bf16 skinny GEMM over the shortlist
 rows of the lm_head with the per-row log-softmax top-k fused in.
 
-Contract: bf16 logits within one bf16 ulp of the float64 product of the bf16 inputs; top-k ids
-equal to the oracle's top-k of the float64 logits wherever the oracle's margin exceeds 1e-3, and
-bit-exact against the top-k of the kernel's own logits; log-probs within 1e-5 of the log-softmax
-of the kernel's logits.
+Contract: bf16 logits within one bf16 ulp (plus the fp32 accumulation error, which matters only
+where the dot product cancels to a tiny value) of the float64 product of the bf16 inputs.  The
+logits the reference ranks are bf16 themselves, so the oracle's logits are the float64 products
+rounded to bf16: top-k ids must equal the oracle's wherever the oracle's (rounded) margin exceeds
+1e-3, and equal the top-k of the kernel's own logits everywhere; log-probs within 1e-5 of the
+log-softmax of the kernel's logits.
 """
 from __future__ import annotations
 
@@ -23,6 +25,15 @@ def _bf16_ulp(x):
     x = np.abs(np.asarray(x, dtype=np.float64))
     e = np.floor(np.log2(np.maximum(x, 2.0 ** -126)))
     return 2.0 ** (e - 7)
+
+
+def _bf16(x):
+    return torch.from_numpy(np.asarray(x, dtype=np.float32)).to(torch.bfloat16).double().numpy()
+
+
+def _acc_err(x, Wsl):
+    """Bound of the fp32 accumulation error of each dot product: 2^-20 sum_i |x_i w_i|."""
+    return 2.0 ** -20 * (np.abs(x) @ np.abs(Wsl).T)
 
 
 def _case(cuda, M, d, V, n, k, seed, scale):
@@ -44,18 +55,20 @@ def test_gemm_head_matches_oracle(cuda, M, d, n, k):
     V = 2 * n + 17
     print(f"[gemm head] M={M} d={d} n={n} k={k}", flush=True)
     W, sl, x, logits, vals, ids, lse = _case(cuda, M, d, V, n, k, seed=M + d, scale=4.0)
-    ref = to64(x) @ to64(W)[sl.long().numpy()].T                      # float64 of the bf16 inputs
+    Wsl = to64(W)[sl.long().numpy()]
+    ref = to64(x) @ Wsl.T                                             # float64 of the bf16 inputs
     got = to64(logits)
-    assert (np.abs(got - ref) <= _bf16_ulp(ref) + 1e-30).all()
+    assert (np.abs(got - ref) <= _bf16_ulp(ref) + _acc_err(to64(x), Wsl)).all()
     # top-k of the kernel's own logits: bit-exact ids, values to 1e-5
     lp = ohead.log_softmax(got)
     ov, oi = ohead.topk(lp, k)
     assert np.array_equal(ids.cpu().numpy(), oi)
     assert np.allclose(vals.cpu().numpy(), ov, atol=1e-5, rtol=0)
     # against the float64 oracle wherever the decision margin is clear
-    rv, ri = ohead.topk(ohead.log_softmax(ref), k)
-    mg = ohead.margins(ref, k)
-    clear = mg > MARGIN
+    ref16 = _bf16(ref)
+    rv, ri = ohead.topk(ohead.log_softmax(ref16), k)
+    clear = ohead.margins(ref16, k) > MARGIN
+    assert clear.mean() > 0.5
     assert np.array_equal(ids.cpu().numpy()[clear], ri[clear])
 
 
@@ -73,8 +86,10 @@ def test_gemm_head_batched_drafting_shape(cuda):
     torch.cuda.synchronize()
     rows = np.arange(0, M, 7)
     Wsl = to64(W[sl.long().to(cuda)])
-    ref = to64(x)[rows] @ Wsl.T
-    rv, ri = ohead.topk(ohead.log_softmax(ref), k)
-    clear = ohead.margins(ref, k) > MARGIN
+    ref16 = _bf16(to64(x)[rows] @ Wsl.T)
+    rv, ri = ohead.topk(ohead.log_softmax(ref16), k)
+    clear = ohead.margins(ref16, k) > MARGIN
+    assert clear.mean() > 0.5
     assert np.array_equal(ids.cpu().numpy()[rows][clear], ri[clear])
-    assert np.allclose(vals.cpu().numpy()[rows], rv, atol=2e-2, rtol=0)   # bf16 logits vs float64
+    # log-probs: equal up to the rare one-ulp rounding differences of single logits
+    assert np.allclose(vals.cpu().numpy()[rows][clear], rv[clear], atol=5e-2, rtol=0)

@@ -43,7 +43,8 @@
 namespace {
 
 constexpr int SWMAX = 8;          // max waves per streaming workgroup
-constexpr int SPF = 16;           // fragment loads in flight per wave
+constexpr int PF_FULL = 16;       // fragment loads in flight per wave: full-K kernels
+constexpr int PF_SPLIT = 8;       //                                   split-K kernels
 
 enum SrcKind { S_BUF = 0, S_SELF = 1, S_CROSS = 2 };
 enum EpiKind { E_PART = 0, E_BIAS16 = 1, E_GELU16 = 2 };
@@ -158,7 +159,7 @@ __device__ void stage_attention(const SArgs& a, const SEx& ex, int h, h16* As, i
   }
 }
 
-template <int SRC, int EPI>
+template <int SRC, int EPI, int SPF>
 __global__ void __launch_bounds__(SWMAX * 64) k_stream(SArgs a) {
   extern __shared__ __align__(16) h16 lds[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -242,8 +243,8 @@ size_t stream_lds(int SRC, int S, int KC, int hd, int Ck) {
   return lds;
 }
 
-template <int SRC, int EPI>
-int launch_stream(const SArgs& a, int S_max, hipStream_t st) {
+template <int SRC, int EPI, int SPF>
+int launch_stream_pf(const SArgs& a, int S_max, hipStream_t st) {
   const int tiles = a.N / 16;
   if (a.K % a.ks || (a.K / a.ks) % 32 || tiles % (a.wpb * a.tpw) || a.wpb > SWMAX) return CFH_E_UNSUPPORTED;
   const size_t lds = stream_lds(SRC, S_max, a.K / a.ks, a.hd, a.Ck);
@@ -253,14 +254,22 @@ int launch_stream(const SArgs& a, int S_max, hipStream_t st) {
   int dev = 0;
   CFH_HIP(hipGetDevice(&dev));
   if (dev < 64 && !(attr_set & (1ull << dev))) {
-    CFH_HIP(hipFuncSetAttribute((const void*)k_stream<SRC, EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    CFH_HIP(hipFuncSetAttribute((const void*)k_stream<SRC, EPI, SPF>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 150 * 1024));
     attr_set |= 1ull << dev;
   }
   const long long wgs = (long long)a.nex * a.ks * a.wg_per_kc;
-  hipLaunchKernelGGL((k_stream<SRC, EPI>), dim3((unsigned)wgs), dim3(a.wpb * 64), lds, st, a);
+  hipLaunchKernelGGL((k_stream<SRC, EPI, SPF>), dim3((unsigned)wgs), dim3(a.wpb * 64), lds, st, a);
   CFH_LAUNCH_CHECK();
   return CFH_OK;
+}
+
+// Full-K units stream 160+ fragments per wave and want a deep prefetch; split-K units are short
+// and many, and a shallower one keeps fewer requests queued at the HBM controllers (measured).
+template <int SRC, int EPI>
+int launch_stream(const SArgs& a, int S_max, hipStream_t st) {
+  return a.ks == 1 ? launch_stream_pf<SRC, EPI, PF_FULL>(a, S_max, st)
+                   : launch_stream_pf<SRC, EPI, PF_SPLIT>(a, S_max, st);
 }
 
 // ---------------------------------------------------------------------------- row kernels
@@ -575,8 +584,8 @@ Plan make_plan(const cfh_flow_dims* dm) {
   p.ks_out = choose_ks(p.nch, tiles_d, p.d, p.CS, 2048, cap);
   p.ks_kv = ksplit_for(p.nch * p.NL, 2 * p.d / 16, p.d, p.C);
   p.ks_tau = ksplit_for(p.nch, p.d / 16, p.d, p.E);
-  p.wpb_qc = pick_wpb(tiles_d, 1);
-  p.wpb_w2 = pick_wpb(tiles_d, 1);
+  p.wpb_qc = std::min(4, pick_wpb(tiles_d, 1));
+  p.wpb_w2 = std::min(4, pick_wpb(tiles_d, 1));
   p.wpb_out = pick_wpb(tiles_d, 1);
   p.tpw_att = (tiles_d % 16 == 0) ? 2 : 1;
   p.wpb_att = pick_wpb(tiles_d, p.tpw_att);

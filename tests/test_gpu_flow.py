@@ -45,3 +45,17 @@ def test_flow_matches_oracle(cuda, d, layers, steps):
     print(f"  rel err {err:.3e}", flush=True)
     assert np.isfinite(to64(z)).all()
     assert err < TOL_FP16
+
+
+@pytest.mark.gpu
+def test_flow_is_bit_reproducible(cuda):
+    """Every reduction runs in a fixed order (no atomics): repeated drafts give bit-identical
+    hidden states."""
+    cfg = flownet(1024, layers=2, flow_steps=2)
+    W = {k: v.to(cuda) for k, v in _flow_weights(cfg, seed=4).items()}
+    ctx = synthetic_context(1, cfg.context_size, 1024, seed=2).to(cuda)
+    ff = FusedFlow(cfg, W, device=cuda)
+    a = ff.predict_hidden(ctx).clone()
+    b = ff.predict_hidden(ctx).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)

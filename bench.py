@@ -136,6 +136,9 @@ def main():
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--flow-steps", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="after timing, copy one 1 GiB buffer (a kernel of known traffic for calibrating "
+                         "the profiler's FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py measures one GPU: the draft step is a single-GPU, batch-1 path and this "
@@ -204,6 +207,13 @@ def main():
                      "frac": round(flow_gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "flow pass (cfh_flow_integrate)"},
     }
+    if args.calib_copy:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if not args.no_cpu:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline(W, cfg, dr.head.sl, d)

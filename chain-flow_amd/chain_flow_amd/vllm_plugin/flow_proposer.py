@@ -1,0 +1,258 @@
+"""``FlowDrafterProposer``: the ``custom_class`` speculative proposer surface, over the MI355X kernels.
+
+Mirrors ``chain_flow.vllm_plugin.flow_proposer.FlowDrafterProposer`` (``cf/vllm_plugin/flow_proposer.py``):
+
+* constructor ``FlowDrafterProposer(vllm_config)`` reads ``speculative_config.num_speculative_tokens``,
+  ``scheduler_config.max_num_seqs`` and the same ``CF_*`` / ``VLLM_SPEC_TREE`` environment with the
+  same validation and messages (``:330-389``);
+* ``_build`` loads the drafter checkpoint directory -- ``chained_flow_tree_config.json``
+  (``model_args``) and ``model.safetensors`` (keys prefixed ``drafter.``), applies ``CF_FLOW_STEPS``,
+  checks the chain / tree emit limits, and resolves the shortlist with the same order, vocabulary
+  guard and declared-identity check (``:579-765``, ``:1006-1016``; ``cf/defaults.py:210-244``);
+* ``_draft_fn(ctx [B, C, d], known0 [B])`` is ``_beam_chains`` -> ``[B, K]`` or ``_beam_tree`` ->
+  ``[B, 2N]`` (``:1187-1332``), run by ``chain_flow_amd.drafter.Drafter`` on the HIP kernels;
+* ``propose(sampled_token_ids, num_tokens_no_spec, token_ids_cpu, slot_mappings=None, **kw)`` returns
+  ``list[list[int]]`` (``:1698``, ``:2494-2569``).
+
+What differs, by design: the drafter is the target-width ``TreeFlowDrafter`` (``architecture
+"tree_flow"``); a VAE-latent checkpoint (``TreeVAEFlowConfig``) is refused with a message.  There
+is no Hugging Face download (``CF_DRAFTER_DIR`` must be a local directory) and no torch.compile.
+The target's final hidden states reach the proposer through :meth:`stash_hidden_states` (the
+reference monkeypatches ``GPUModelRunner.propose_draft_token_ids`` to stash
+``sample_hidden_states``, ``:40-59``) and the target's input embeddings and ``lm_head`` weight
+through :meth:`bind_target` (the reference reads them off ``runner.model``, ``:585-590``).
+"""
+from __future__ import annotations
+
+import dataclasses
+import json
+import os
+from pathlib import Path
+
+import torch
+
+from chain_flow_amd import shortlist as _sl
+from chain_flow_amd.config import TreeFlowConfig
+from chain_flow_amd.drafter import Drafter, front_pad
+
+CONFIG_NAME = "chained_flow_tree_config.json"
+WEIGHTS_NAME = "model.safetensors"
+PACKAGED_SHORTLIST = Path(__file__).resolve().parents[1] / "data" / "shortlist_qwen3_5.pt"
+
+
+def shortlist_candidates(drafter_dir: str | None) -> list[tuple[str, str]]:
+    """Shortlists to try, best first, as (path, provenance) (``cf/defaults.py:210-244``): the
+    drafter checkpoint's own ``shortlist.pt``, then the packaged list (if installed)."""
+    out: list[tuple[str, str]] = []
+    if drafter_dir and os.path.isdir(drafter_dir):
+        p = Path(drafter_dir) / "shortlist.pt"
+        if p.is_file():
+            out.append((str(p), "drafter checkpoint"))
+    if PACKAGED_SHORTLIST.is_file():
+        out.append((str(PACKAGED_SHORTLIST), "packaged"))
+    return out
+
+
+def load_drafter_config(ckd: str) -> TreeFlowConfig:
+    """``model_args`` of ``chained_flow_tree_config.json`` -> TreeFlowConfig, with the
+    ``CF_FLOW_STEPS`` inference override (``flow_proposer.py:616-631``)."""
+    with open(os.path.join(ckd, CONFIG_NAME)) as f:
+        margs = json.load(f)["model_args"]
+    arch = margs.get("architecture", "tree_flow")
+    if arch != "tree_flow":
+        raise ValueError(f"drafter architecture {arch!r} is not supported by this build: it runs the "
+                         f"target-width TreeFlowDrafter ('tree_flow'); VAE-latent drafters are not built")
+    fields = {f.name for f in dataclasses.fields(TreeFlowConfig)}
+    cfg = TreeFlowConfig(**{k: v for k, v in margs.items() if k in fields})
+    fs = os.environ.get("CF_FLOW_STEPS")
+    if fs:
+        n = int(fs)
+        if n < 1:
+            raise ValueError(f"CF_FLOW_STEPS must be >= 1, got {n}")
+        cfg.num_flow_steps = n
+    return cfg
+
+
+def load_drafter_weights(ckd: str, dtype=torch.float16, device="cpu") -> dict:
+    """``drafter.``-prefixed tensors of ``model.safetensors``, prefix stripped (``:638-640``)."""
+    from safetensors.torch import load_file
+    sd = load_file(os.path.join(ckd, WEIGHTS_NAME), device="cpu")
+    return {k[len("drafter."):]: v.to(device, dtype) for k, v in sd.items() if k.startswith("drafter.")}
+
+
+def declared_shortlist(ckd: str) -> dict:
+    """The optional ``shortlist`` block {rows, ids_sha256} of the drafter config (``:1006-1016``)."""
+    try:
+        with open(os.path.join(ckd, CONFIG_NAME)) as f:
+            return json.load(f).get("shortlist") or {}
+    except Exception:
+        return {}
+
+
+def resolve_shortlist(ckd: str, vocab_size: int, explicit: str | None):
+    """(ids int32 | None, provenance) -- ``_build``'s resolution (``:680-765``).
+
+    ``explicit`` = the value of ``CF_SHORTLIST`` when it is set: a path (must exist) or "" (full
+    head by request).  Candidates built for another vocabulary are refused and the next is tried;
+    a list whose content differs from the drafter's declared identity raises."""
+    if explicit is not None and explicit != "":
+        if not os.path.exists(explicit):
+            raise FileNotFoundError(f"CF_SHORTLIST={explicit} does not exist")
+        cands = [(explicit, "CF_SHORTLIST")]
+    elif explicit == "":
+        return None, "explicit CF_SHORTLIST='' -- FULL HEAD by request"
+    else:
+        cands = shortlist_candidates(ckd)
+    rejected = []
+    for path, src in cands:
+        ids, meta = _sl.load(path)
+        bad = _sl.check(ids, meta, vocab_size)
+        if bad:
+            rejected.append(f"{src} {path}: {bad}")
+            continue
+        sl = _sl.resolve(ids, vocab_size)
+        decl = declared_shortlist(ckd)
+        if decl:
+            got = _sl.ids_content_sha(sl)
+            want_rows, want_sha = decl.get("rows"), decl.get("ids_sha256")
+            if (want_rows and int(want_rows) != sl.numel()) or (want_sha and want_sha != got):
+                raise RuntimeError(
+                    "shortlist does not match what this drafter declares.\n"
+                    f"  resolved : {path}  [{src}]\n"
+                    f"             {sl.numel()} rows, ids-sha256 {got}\n"
+                    f"  declared : {want_rows} rows, ids-sha256 {want_sha}")
+        return sl, f"{src} {os.path.basename(path)}"
+    why = "FULL HEAD -- every candidate refused: " + " | ".join(rejected) if rejected else "FULL HEAD"
+    return None, why
+
+
+class FlowDrafterProposer:
+    def __init__(self, vllm_config):
+        spec = vllm_config.speculative_config
+        self.tree = os.environ.get("VLLM_SPEC_TREE", "0") == "1"
+        self.tree_keep = int(os.environ.get("CF_TREE_KEEP", "4"))
+        self.tree_topb = int(os.environ.get("CF_TREE_TOPB", "8"))
+        self.tree_depth = int(os.environ.get("CF_TREE_DEPTH", "4"))
+        self.branching = self.tree and os.environ.get("CF_TREE_BRANCH", "1") == "1"
+        if self.branching and self.tree_keep > self.tree_topb:
+            raise ValueError(
+                f"CF_TREE_KEEP={self.tree_keep} > CF_TREE_TOPB={self.tree_topb}: depth 1 expands "
+                f"a single node, so it can hold at most {self.tree_topb} children while "
+                f"N=keep*depth assumes {self.tree_keep}. Raise CF_TREE_TOPB to >= CF_TREE_KEEP.")
+        self.N = self.tree_keep * self.tree_depth
+        if self.branching:
+            if int(spec.num_speculative_tokens) != self.N + 1:
+                raise AssertionError(
+                    f"set num_speculative_tokens={self.N + 1} for "
+                    f"CF_TREE_KEEP={self.tree_keep} x CF_TREE_DEPTH={self.tree_depth}")
+        self.K = int(spec.num_speculative_tokens) - (1 if self.tree else 0)
+        self.draft_width = self.N if self.branching else self.K
+        self.width = int(os.environ.get("CF_WIDTH", "4"))
+        self.ckd = os.environ.get("CF_DRAFTER_DIR")
+        if not self.ckd:
+            raise ValueError("set CF_DRAFTER_DIR to the drafter checkpoint dir")
+        if not os.path.isdir(self.ckd):
+            raise ValueError(f"CF_DRAFTER_DIR={self.ckd} is not a directory (this build loads local "
+                             f"checkpoints only; download the repo first)")
+        self.shortlist_path = os.environ.get("CF_SHORTLIST")
+        self.max_reqs = int(vllm_config.scheduler_config.max_num_seqs)
+        self.path_trim = os.environ.get("CF_PATH_TRIM", "1") != "0"
+        self.drafter: Drafter | None = None
+        self._target = None
+        self._hidden = None
+        self.ctx_hist: dict[int, torch.Tensor] = {}
+
+    # ---- what the reference reads off the engine ------------------------------------------
+    def bind_target(self, embed_w: torch.Tensor, lm_w: torch.Tensor) -> None:
+        """The target's input embeddings [V, d] and lm_head weight [V, d] (device tensors)."""
+        if embed_w.shape != lm_w.shape:
+            raise ValueError("embed_tokens and lm_head must both be [V, d]")
+        self._target = (embed_w, lm_w)
+
+    def stash_hidden_states(self, hidden: torch.Tensor) -> None:
+        """Final hidden states of the tokens just sampled, one row per entry of the next
+        ``propose`` call's flattened ``sampled_token_ids`` (the reference's stash hook)."""
+        self._hidden = hidden
+
+    # ---- build -----------------------------------------------------------------------------
+    def _build(self):
+        if self._target is None:
+            raise RuntimeError("bind_target(embed_w, lm_w) before the first propose")
+        embed_w, lm_w = self._target
+        self.dev = embed_w.device
+        V, H = lm_w.shape
+        cfg = load_drafter_config(self.ckd)
+        if cfg.expert_dim != H:
+            raise ValueError(f"drafter expert_dim={cfg.expert_dim} but the target hidden size is {H}")
+        if self.branching:
+            emit = min(self.tree_depth, cfg.draft_length - 1)
+            if emit != self.tree_depth:
+                raise ValueError(
+                    f"CF_TREE_DEPTH={self.tree_depth} but the drafter can only emit "
+                    f"{emit} levels (draft_length={cfg.draft_length}). Set CF_TREE_DEPTH<={emit} and "
+                    f"num_speculative_tokens={self.tree_keep * emit + 1}.")
+        else:
+            emit = cfg.draft_length - 1
+            if self.K > emit:
+                raise ValueError(
+                    f"num_speculative_tokens={self.K} but this drafter can only emit {emit} "
+                    f"chain tokens (draft_length={cfg.draft_length}; depth 0 reconstructs the "
+                    f"token that was already committed). Set num_speculative_tokens<={emit}.")
+        weights = load_drafter_weights(self.ckd, torch.float16, self.dev)
+        weights["lm_head.weight"] = lm_w.to(torch.float16)
+        weights["embed_tokens.weight"] = embed_w.to(torch.float16)
+        explicit = self.shortlist_path if "CF_SHORTLIST" in os.environ else None
+        sl, self.shortlist_source = resolve_shortlist(self.ckd, V, explicit)
+        self.cfg = cfg
+        self.drafter = Drafter(cfg, weights, None if sl is None else sl.to(self.dev), device=self.dev,
+                               path_trim=self.path_trim)
+        self.ctx_size = cfg.context_size
+
+    # ---- drafting --------------------------------------------------------------------------
+    def _draft_fn(self, ctx: torch.Tensor, known0: torch.Tensor) -> torch.Tensor:
+        if self.branching:
+            return self.drafter.beam_tree(ctx, known0, keep=self.tree_keep, topb=self.tree_topb,
+                                          depth=self.tree_depth)
+        return self.drafter.beam_chains(ctx, known0, self.K, width=self.width)
+
+    @torch.inference_mode()
+    def propose(self, sampled_token_ids, num_tokens_no_spec=None, token_ids_cpu=None, slot_mappings=None,
+                **kw):
+        """sampled_token_ids: per request, the tokens committed this step (list of lists).  The
+        stashed hidden states hold one row per committed token, requests in order.  Returns the
+        next draft per request: K chain tokens, or the N tree tokens (their parents are kept in
+        ``self.last_parents``)."""
+        if self.drafter is None:
+            self._build()
+        hidden = kw.get("hidden_states", self._hidden)
+        if hidden is None:
+            raise RuntimeError("no hidden states: stash_hidden_states() before propose()")
+        rows, ctxs, known = [], [], []
+        off = 0
+        for i, toks in enumerate(sampled_token_ids):
+            n = len(toks)
+            if n == 0:
+                continue
+            h = hidden[off:off + n].to(self.dev, torch.float16)
+            off += n
+            prev = self.ctx_hist.get(i)
+            hist = h if prev is None else torch.cat([prev, h], 0)
+            self.ctx_hist[i] = hist[-self.ctx_size:]
+            rows.append(i)
+            ctxs.append(front_pad(self.ctx_hist[i][None], self.ctx_size)[0])
+            known.append(int(toks[-1]))
+        out = [[] for _ in sampled_token_ids]
+        if not rows:
+            return out
+        ctx = torch.stack(ctxs, 0)
+        known0 = torch.tensor(known, device=self.dev, dtype=torch.long)
+        draft = self._draft_fn(ctx, known0).cpu().tolist()       # the one device -> host sync
+        self.last_parents = {}
+        for j, i in enumerate(rows):
+            if self.branching:
+                Nn = len(draft[j]) // 2
+                out[i] = draft[j][:Nn]
+                self.last_parents[i] = draft[j][Nn:]
+            else:
+                out[i] = draft[j]
+        return out

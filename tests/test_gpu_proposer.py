@@ -1,0 +1,66 @@
+"""FlowDrafterProposer end to end on the GPU: a tiny checkpoint directory, the target's embeddings
+and lm_head bound, hidden states stashed, then propose() -- compared with the oracle's chain on the
+same context (ids equal wherever the oracle's decisions are not near ties)."""
+from __future__ import annotations
+
+import json
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import to64
+from chain_flow_amd import shortlist as slmod
+from chain_flow_amd.config import flownet
+from chain_flow_amd.vllm_plugin import flow_proposer as fp
+from chain_flow_amd.weights import make_weights, param_specs
+from oracle import beam as obeam
+from oracle import flow as oflow
+from oracle import head as ohead
+
+
+@pytest.mark.gpu
+def test_proposer_chain_draft_matches_oracle(cuda, tmp_path, monkeypatch):
+    from safetensors.torch import save_file
+    d, V, n = 512, 4096, 1024
+    cfg = flownet(d, layers=1, flow_steps=2)
+    W = make_weights(cfg, V, init="test", base_seed=7)
+    W["lm_head.weight"] = (W["lm_head.weight"].float() * 8).half()
+    drafter = {k: v for k, v in W.items() if k not in ("lm_head.weight", "embed_tokens.weight")}
+    save_file({"drafter." + k: v.contiguous() for k, v in drafter.items()}, str(tmp_path / fp.WEIGHTS_NAME))
+    (tmp_path / fp.CONFIG_NAME).write_text(json.dumps({"model_args": cfg.to_dict()}))
+    sl = torch.randperm(V, generator=torch.Generator().manual_seed(3))[:n]
+    slmod.save(tmp_path / "shortlist.pt", sl, vocab_size=V)
+    for k in ("VLLM_SPEC_TREE", "CF_SHORTLIST", "CF_FLOW_STEPS"):
+        monkeypatch.delenv(k, raising=False)
+    monkeypatch.setenv("CF_DRAFTER_DIR", str(tmp_path))
+    vc = SimpleNamespace(speculative_config=SimpleNamespace(num_speculative_tokens=5),
+                         scheduler_config=SimpleNamespace(max_num_seqs=4))
+    p = fp.FlowDrafterProposer(vc)
+    p.bind_target(W["embed_tokens.weight"].to(cuda), W["lm_head.weight"].to(cuda))
+    g = torch.Generator().manual_seed(11)
+    hid = torch.randn(3, d, generator=g)
+    hid = (hid / hid.pow(2).mean(-1, keepdim=True).sqrt()).half()
+    slv = torch.unique(sl.long())
+    toks = [int(slv[10]), int(slv[20]), int(slv[30])]
+    p.stash_hidden_states(hid.to(cuda))
+    out = p.propose([toks])
+    assert len(out) == 1 and len(out[0]) == 5
+    # oracle on the same context: 3 hiddens front-padded to 8, known0 = last committed token
+    ctx = oflow.front_pad_context(to64(hid)[None], cfg.context_size)
+    W64 = {k: to64(v) for k, v in W.items()}
+    ocfg = dict(draft_length=cfg.draft_length, chunk_size=cfg.chunk_size, num_layers=1, num_heads=cfg.num_heads,
+                num_flow_steps=2, init_mode="delta")
+    pred = oflow.predict_hidden(W64, ctx, ocfg, numerics="fp16")
+    s64 = slv.numpy()
+    score = lambda h, prev: ohead.head_with_bias(h, W64["lm_head.weight"][s64], W64["markov.w1.weight"],
+                                                 W64["markov.w2.weight"][s64], prev)
+    resid = lambda lp, nl: ohead.path_residual(W64, W64["embed_tokens.weight"], lp, nl, cfg.path_order)
+    ref, trace = obeam.beam_chains(pred, np.array([toks[-1]]), s64, 4, 5, cfg.path_order, score, resid,
+                                   return_trace=True)
+    print(f"[proposer] gpu {out[0]} oracle {ref[0].tolist()}", flush=True)
+    if out[0] != ref[0].tolist():
+        near = any((ohead.margins(t["lp"], 4) <= 1e-3).any() or (ohead.margins(t["cand"], 4) <= 1e-3).any()
+                   for t in trace)
+        assert near, (out[0], ref[0].tolist())

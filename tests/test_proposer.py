@@ -1,0 +1,115 @@
+"""The FlowDrafterProposer surface (host logic, no GPU): constructor validation, checkpoint
+loading, shortlist resolution order / vocabulary guard / declared identity.
+
+Mirrors the reference's behaviour in cf/vllm_plugin/flow_proposer.py:330-389, 579-765, 1006-1016
+and cf/defaults.py:210-244 (its own tests cover the shortlist guard, tests/test_shortlist.py:69-121).
+"""
+from __future__ import annotations
+
+import json
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+from chain_flow_amd import shortlist as slmod
+from chain_flow_amd.config import flownet
+from chain_flow_amd.vllm_plugin import flow_proposer as fp
+from chain_flow_amd.weights import make_weights, param_specs
+
+
+def _vcfg(k=5, seqs=8):
+    return SimpleNamespace(speculative_config=SimpleNamespace(num_speculative_tokens=k),
+                           scheduler_config=SimpleNamespace(max_num_seqs=seqs))
+
+
+@pytest.fixture
+def ckpt(tmp_path):
+    from safetensors.torch import save_file
+    cfg = flownet(512, layers=1, flow_steps=2)
+    names = {n for n in param_specs(cfg, 64, target=False)}
+    W = make_weights(cfg, 64, init="test", names=names, target=False, dtype=torch.float32)
+    save_file({"drafter." + k: v.contiguous() for k, v in W.items()} | {"other.x": torch.zeros(2)},
+              str(tmp_path / fp.WEIGHTS_NAME))
+    margs = {k: v for k, v in cfg.to_dict().items()}
+    (tmp_path / fp.CONFIG_NAME).write_text(json.dumps({"model_args": margs, "data_args": {}, "loss_args": {}}))
+    return tmp_path, cfg, W
+
+
+def _env(monkeypatch, **kv):
+    for k in ("VLLM_SPEC_TREE", "CF_TREE_KEEP", "CF_TREE_TOPB", "CF_TREE_DEPTH", "CF_TREE_BRANCH",
+              "CF_DRAFTER_DIR", "CF_SHORTLIST", "CF_FLOW_STEPS", "CF_WIDTH"):
+        monkeypatch.delenv(k, raising=False)
+    for k, v in kv.items():
+        monkeypatch.setenv(k, str(v))
+
+
+def test_requires_a_drafter_dir(monkeypatch):
+    _env(monkeypatch)
+    with pytest.raises(ValueError, match="CF_DRAFTER_DIR"):
+        fp.FlowDrafterProposer(_vcfg())
+
+
+def test_chain_mode_widths(monkeypatch, ckpt):
+    _env(monkeypatch, CF_DRAFTER_DIR=ckpt[0], CF_WIDTH=3)
+    p = fp.FlowDrafterProposer(_vcfg(k=5))
+    assert (p.K, p.draft_width, p.width, p.branching) == (5, 5, 3, False)
+
+
+def test_tree_mode_sizes_and_checks(monkeypatch, ckpt):
+    _env(monkeypatch, CF_DRAFTER_DIR=ckpt[0], VLLM_SPEC_TREE=1, CF_TREE_KEEP=4, CF_TREE_TOPB=8, CF_TREE_DEPTH=5)
+    p = fp.FlowDrafterProposer(_vcfg(k=21))
+    assert (p.N, p.K, p.draft_width) == (20, 20, 20)
+    with pytest.raises(AssertionError, match="num_speculative_tokens=21"):
+        fp.FlowDrafterProposer(_vcfg(k=20))
+    _env(monkeypatch, CF_DRAFTER_DIR=ckpt[0], VLLM_SPEC_TREE=1, CF_TREE_KEEP=8, CF_TREE_TOPB=4)
+    with pytest.raises(ValueError, match="CF_TREE_KEEP=8 > CF_TREE_TOPB=4"):
+        fp.FlowDrafterProposer(_vcfg(k=33))
+
+
+def test_checkpoint_config_and_weights(monkeypatch, ckpt):
+    d, cfg, W = ckpt
+    _env(monkeypatch, CF_FLOW_STEPS=8)
+    got = fp.load_drafter_config(str(d))
+    assert got.expert_dim == 512 and got.num_flow_steps == 8 and got.draft_length == cfg.draft_length
+    w = fp.load_drafter_weights(str(d), torch.float32)
+    assert set(w) == set(W)                                   # prefix stripped, foreign keys dropped
+    assert torch.equal(w["expert.out_proj.weight"], W["expert.out_proj.weight"])
+    _env(monkeypatch, CF_FLOW_STEPS=0)
+    with pytest.raises(ValueError, match="CF_FLOW_STEPS must be >= 1"):
+        fp.load_drafter_config(str(d))
+
+
+def test_vae_checkpoints_are_refused(tmp_path):
+    (tmp_path / fp.CONFIG_NAME).write_text(json.dumps({"model_args": {"architecture": "tree_vae_flow"}}))
+    with pytest.raises(ValueError, match="not supported"):
+        fp.load_drafter_config(str(tmp_path))
+
+
+def test_shortlist_resolution_order_and_guard(tmp_path):
+    V = 1000
+    # no candidates -> full head
+    sl, why = fp.resolve_shortlist(str(tmp_path), V, None)
+    assert sl is None
+    # the drafter's own list wins
+    slmod.save(tmp_path / "shortlist.pt", [5, 3, 900], vocab_size=V)
+    sl, why = fp.resolve_shortlist(str(tmp_path), V, None)
+    assert sl.tolist() == [3, 5, 900] and why.startswith("drafter checkpoint")
+    # a list built for another vocabulary is refused, not clamped
+    sl, why = fp.resolve_shortlist(str(tmp_path), 2000, None)
+    assert sl is None and "refused" in why and "vocab_size=1000" in why
+    # explicit "" = full head; explicit missing path fails loudly
+    assert fp.resolve_shortlist(str(tmp_path), V, "")[0] is None
+    with pytest.raises(FileNotFoundError):
+        fp.resolve_shortlist(str(tmp_path), V, str(tmp_path / "nope.pt"))
+
+
+def test_declared_identity_mismatch_raises(tmp_path):
+    V = 1000
+    slmod.save(tmp_path / "shortlist.pt", [1, 2, 3], vocab_size=V)
+    good = slmod.ids_content_sha(torch.tensor([1, 2, 3]))
+    (tmp_path / fp.CONFIG_NAME).write_text(json.dumps({"model_args": {}, "shortlist": {"rows": 3, "ids_sha256": good}}))
+    assert fp.resolve_shortlist(str(tmp_path), V, None)[0].tolist() == [1, 2, 3]
+    (tmp_path / fp.CONFIG_NAME).write_text(json.dumps({"model_args": {}, "shortlist": {"rows": 4}}))
+    with pytest.raises(RuntimeError, match="does not match what this drafter declares"):
+        fp.resolve_shortlist(str(tmp_path), V, None)

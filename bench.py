@@ -54,6 +54,15 @@ def head_bytes(d, K, W, n_rows, rank=256, order=4, path_ffn=2):
     return total
 
 
+def measured_traffic(d, L, E):
+    """HBM bytes per flow pass from the committed counter profile of this workload (FETCH_SIZE and
+    WRITE_SIZE, calibrated with a 1 GiB copy), or None for a workload without one."""
+    p = ROOT / "profiles" / f"flow_d{d}_L{L}_E{E}_traffic.json"
+    if not p.exists():
+        return None
+    return int(json.loads(p.read_text())["traffic_bytes"])
+
+
 def build_workload(d, L, E, device):
     import torch
     from chain_flow_amd.config import flownet
@@ -204,7 +213,7 @@ def main():
                          "step_event": round(med(step_ms), 4)},
         "algorithmic_bytes": {"flow": fb, "head": hb, "draft_gbs": round((fb + hb) / (ms * 1e-3) / 1e9, 1)},
         "roofline": {"bound": "hbm", "achieved": round(flow_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(flow_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(flow_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(d, L, E),
                      "kernel": "flow pass (cfh_flow_integrate)"},
     }
     if args.calib_copy:

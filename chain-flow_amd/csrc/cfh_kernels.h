@@ -9,6 +9,28 @@
 
 namespace {
 
+// Copy rows x 8-half vectors from global to LDS with SB loads in flight per thread: every load of a
+// batch is issued before the first LDS store, so the staging costs one memory round trip per batch
+// instead of one per vector.
+constexpr int SB = 8;
+
+template <typename Src, typename Dst>
+__device__ __forceinline__ void batched_copy(int total, Src src, Dst dst) {
+  for (int base = 0; base < total; base += SB * (int)blockDim.x) {
+    h16x8 t[SB];
+#pragma unroll
+    for (int u = 0; u < SB; ++u) {
+      const int idx = base + u * (int)blockDim.x + (int)threadIdx.x;
+      if (idx < total) t[u] = src(idx);
+    }
+#pragma unroll
+    for (int u = 0; u < SB; ++u) {
+      const int idx = base + u * (int)blockDim.x + (int)threadIdx.x;
+      if (idx < total) dst(idx, t[u]);
+    }
+  }
+}
+
 constexpr int WPB = 4;            // waves per GEMV workgroup
 constexpr int PF = 8;             // fragment loads in flight per wave
 constexpr int MAXR = 16;          // max activation rows per expert (draft_length, ctx rows, steps)
@@ -47,16 +69,26 @@ __device__ void stage_A(const GemvArgs& a, const GemvEx& ep, int l, int kc, h16*
   const int rows = ep.rows;
   const int nvec = KC / 8;
   if constexpr (SRC == SRC_BUF) {
-    for (int idx = threadIdx.x; idx < rows * nvec; idx += blockDim.x) {
-      const int i = idx / nvec, kk = (idx - i * nvec) * 8;
-      *(h16x8*)(As + i * lda + kk) = *(const h16x8*)(ep.a + (size_t)i * ep.lda + k0 + kk);
-    }
+    batched_copy(rows * nvec,
+                 [&](int idx) {
+                   const int i = idx / nvec, kk = (idx - i * nvec) * 8;
+                   return *(const h16x8*)(ep.a + (size_t)i * ep.lda + k0 + kk);
+                 },
+                 [&](int idx, h16x8 v) {
+                   const int i = idx / nvec, kk = (idx - i * nvec) * 8;
+                   *(h16x8*)(As + i * lda + kk) = v;
+                 });
   } else if constexpr (SRC == SRC_GATHER) {
-    for (int idx = threadIdx.x; idx < rows * nvec; idx += blockDim.x) {
-      const int i = idx / nvec, kk = (idx - i * nvec) * 8;
-      const int id = max(ep.ids[i * ep.ids_stride], 0);
-      *(h16x8*)(As + i * lda + kk) = *(const h16x8*)(ep.a + (size_t)id * ep.lda + k0 + kk);
-    }
+    batched_copy(rows * nvec,
+                 [&](int idx) {
+                   const int i = idx / nvec, kk = (idx - i * nvec) * 8;
+                   const int id = max(ep.ids[i * ep.ids_stride], 0);
+                   return *(const h16x8*)(ep.a + (size_t)id * ep.lda + k0 + kk);
+                 },
+                 [&](int idx, h16x8 v) {
+                   const int i = idx / nvec, kk = (idx - i * nvec) * 8;
+                   *(h16x8*)(As + i * lda + kk) = v;
+                 });
   } else if constexpr (SRC == SRC_CTX) {
     // context_norm(ctx) of layer l; the row moments (mean, rstd) come precomputed in ep.mom
     const h16* gw = (const h16*)((const char*)ep.g0 + (size_t)l * a.vstride);

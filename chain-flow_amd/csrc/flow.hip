@@ -80,14 +80,16 @@ __device__ void stage_attention(const SArgs& a, const SEx& ex, int h, h16* As, i
   const int nv = hd / 8;
   const int c0 = h * hd;
   if constexpr (SRC == S_SELF) {
+    // sq, sk, sv are consecutive [S][hd] blocks: vector idx -> (part, row, col)
     const size_t ld = 3 * (size_t)d;
-    for (int idx = threadIdx.x; idx < 3 * S * nv; idx += blockDim.x) {
-      const int part = idx / (S * nv);
-      const int r = idx - part * S * nv;
-      const int i = r / nv, c = (r - i * nv) * 8;
-      h16* dst = (part == 0 ? sq : (part == 1 ? sk : sv)) + i * hd + c;
-      *(h16x8*)dst = *(const h16x8*)(ex.a + (size_t)i * ld + part * d + c0 + c);
-    }
+    batched_copy(3 * S * nv,
+                 [&](int idx) {
+                   const int part = idx / (S * nv);
+                   const int r = idx - part * S * nv;
+                   const int i = r / nv, c = (r - i * nv) * 8;
+                   return *(const h16x8*)(ex.a + (size_t)i * ld + part * d + c0 + c);
+                 },
+                 [&](int idx, h16x8 v) { *(h16x8*)(sq + (size_t)idx * 8) = v; });
   } else {
     // q = fp16(sum of the cross-q partials + bias), four columns per thread-step
     const int nq = hd / 4;
@@ -95,11 +97,14 @@ __device__ void stage_attention(const SArgs& a, const SEx& ex, int h, h16* As, i
     for (int idx = threadIdx.x; idx < S * nq; idx += blockDim.x) {
       const int i = idx / nq, c = (idx - i * nq) * 4;
       const float* Pp = ex.pin + (size_t)i * d + c0 + c;
-      float4 s4 = *(const float4*)Pp;
-      for (int q = 1; q < a.ks_in; ++q) {
-        const float4 t = *(const float4*)(Pp + q * pst);
-        s4.x += t.x; s4.y += t.y; s4.z += t.z; s4.w += t.w;
-      }
+      float4 t[8];                                  // every partial of the group in flight at once
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (q < a.ks_in) t[q] = *(const float4*)(Pp + q * pst);
+      float4 s4 = t[0];
+#pragma unroll
+      for (int q = 1; q < 8; ++q)
+        if (q < a.ks_in) { s4.x += t[q].x; s4.y += t[q].y; s4.z += t[q].z; s4.w += t[q].w; }
       const h16* bb = ex.bin + c0 + c;
       h16* dst = sq + i * hd + c;
       dst[0] = (h16)(s4.x + (float)bb[0]);
@@ -107,11 +112,13 @@ __device__ void stage_attention(const SArgs& a, const SEx& ex, int h, h16* As, i
       dst[2] = (h16)(s4.z + (float)bb[2]);
       dst[3] = (h16)(s4.w + (float)bb[3]);
     }
-    for (int idx = threadIdx.x; idx < Sk * nv; idx += blockDim.x) {
-      const int j = idx / nv, c = (idx - j * nv) * 8;
-      *(h16x8*)(sk + j * hd + c) = *(const h16x8*)(ex.a + (size_t)j * d + c0 + c);
-      *(h16x8*)(sv + j * hd + c) = *(const h16x8*)(ex.a + (size_t)(Sk + j) * d + c0 + c);
-    }
+    // sk, sv are consecutive [Sk][hd] blocks fed from the K and V rows of the hoisted context
+    batched_copy(2 * Sk * nv,
+                 [&](int idx) {
+                   const int j = idx / nv, c = (idx - j * nv) * 8;   // j < 2 Sk: K rows then V rows
+                   return *(const h16x8*)(ex.a + (size_t)j * d + c0 + c);
+                 },
+                 [&](int idx, h16x8 v) { *(h16x8*)(sk + (size_t)idx * 8) = v; });
   }
   __syncthreads();
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
@@ -188,10 +195,15 @@ __global__ void __launch_bounds__(SWMAX * 64) k_stream(SArgs a) {
   h16* As = lds;
   if constexpr (SRC == S_BUF) {
     const int nv = KC / 8;
-    for (int idx = threadIdx.x; idx < ex.S * nv; idx += blockDim.x) {
-      const int i = idx / nv, kk = (idx - i * nv) * 8;
-      *(h16x8*)(As + i * lda + kk) = *(const h16x8*)(ex.a + (size_t)i * ex.lda + (size_t)kc * KC + kk);
-    }
+    batched_copy(ex.S * nv,
+                 [&](int idx) {
+                   const int i = idx / nv, kk = (idx - i * nv) * 8;
+                   return *(const h16x8*)(ex.a + (size_t)i * ex.lda + (size_t)kc * KC + kk);
+                 },
+                 [&](int idx, h16x8 v) {
+                   const int i = idx / nv, kk = (idx - i * nv) * 8;
+                   *(h16x8*)(As + i * lda + kk) = v;
+                 });
   } else {
     stage_attention<SRC>(a, ex, kc, As, lda, As + (size_t)ex.S * lda);
   }
@@ -591,7 +603,7 @@ Plan make_plan(const cfh_flow_dims* dm) {
   p.wpb_att = pick_wpb(tiles_d, p.tpw_att);
   p.wpb_full = 8;
   p.pks = std::max(std::max(p.H, p.ks_w2), p.ks_out);
-  p.ok = p.ks_qc > 0 && p.ks_w2 > 0 && p.ks_out > 0 && p.hd % 32 == 0 && (3 * tiles_d) % 8 == 0 &&
+  p.ok = p.ks_qc > 0 && p.ks_qc <= 8 && p.ks_w2 > 0 && p.ks_out > 0 && p.hd % 32 == 0 && (3 * tiles_d) % 8 == 0 &&
          (p.fd / 16) % 8 == 0 && stream_lds(S_BUF, p.Smax, p.d, p.hd, p.C) <= 150 * 1024 &&
          stream_lds(S_SELF, p.Smax, p.hd, p.hd, p.C) <= 150 * 1024 &&
          stream_lds(S_CROSS, p.Smax, p.hd, p.hd, p.C) <= 150 * 1024 && res_nq(p.d) > 0;

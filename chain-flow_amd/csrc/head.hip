@@ -161,17 +161,27 @@ __global__ void __launch_bounds__(HW * 64) k_head(HeadArgs a) {
   TileStream<PF, 4, false> ts;
   ts.begin((const h16x8*)(a.W + row * a.d + 8 * (lane >> 4)), a.d / 32);
   const int nh = a.d / 8;
-  for (int idx = threadIdx.x; idx < a.M * nh; idx += blockDim.x) {
-    const int i = idx / nh, kk = (idx - i * nh) * 8;
-    *(h16x8*)(Ah + i * ldh + kk) = *(const h16x8*)(a.h + (size_t)i * a.d + kk);
-  }
+  batched_copy(a.M * nh,
+               [&](int idx) {
+                 const int i = idx / nh, kk = (idx - i * nh) * 8;
+                 return *(const h16x8*)(a.h + (size_t)i * a.d + kk);
+               },
+               [&](int idx, h16x8 v) {
+                 const int i = idx / nh, kk = (idx - i * nh) * 8;
+                 *(h16x8*)(Ah + i * ldh + kk) = v;
+               });
   if (a.W2) {
     const int nm = a.r / 8;
-    for (int idx = threadIdx.x; idx < a.M * nm; idx += blockDim.x) {
-      const int i = idx / nm, kk = (idx - i * nm) * 8;
-      const size_t src = a.a_ids ? (size_t)max(a.a_ids[i * a.a_ids_stride], 0) : (size_t)i;
-      *(h16x8*)(Am + i * ldm + kk) = *(const h16x8*)(a.a + src * a.r + kk);
-    }
+    batched_copy(a.M * nm,
+                 [&](int idx) {
+                   const int i = idx / nm, kk = (idx - i * nm) * 8;
+                   const size_t src = a.a_ids ? (size_t)max(a.a_ids[i * a.a_ids_stride], 0) : (size_t)i;
+                   return *(const h16x8*)(a.a + src * a.r + kk);
+                 },
+                 [&](int idx, h16x8 v) {
+                   const int i = idx / nm, kk = (idx - i * nm) * 8;
+                   *(h16x8*)(Am + i * ldm + kk) = v;
+                 });
   }
   __syncthreads();
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};

@@ -9,6 +9,15 @@
 
 namespace {
 
+// Workgroup barrier that orders LDS accesses only.  __syncthreads() also waits for every global
+// load the wave has in flight (its release fence covers global memory), which would drain a
+// weight prefetch issued before the barrier; this one waits for the LDS queue alone.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Copy rows x 8-half vectors from global to LDS with SB loads in flight per thread: every load of a
 // batch is issued before the first LDS store, so the staging costs one memory round trip per batch
 // instead of one per vector.

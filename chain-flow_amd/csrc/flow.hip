@@ -42,7 +42,7 @@
 
 namespace {
 
-constexpr int SWMAX = 8;          // max waves per streaming workgroup
+constexpr int SWMAX = 16;         // max waves per streaming workgroup
 constexpr int PF_FULL = 16;       // fragment loads in flight per wave: full-K kernels
 constexpr int PF_SPLIT = 8;       //                                   split-K kernels
 
@@ -66,61 +66,12 @@ struct SArgs {
   int d, hd, ks_in, Ck;
 };
 
-// Self / cross attention of head h for the S rows of one expert, written as fp16 into As
-// [S][lda] (lda >= hd + 8).  Causal mask = triu(-inf, 1) (cf/drafters/chunked_flow.py:273-275);
-// scores and the weighted sum in fp32 on fp16 q/k/v, output rounded to fp16.
-template <int SRC>
-__device__ void stage_attention(const SArgs& a, const SEx& ex, int h, h16* As, int lda, h16* scratch) {
-  const int S = ex.S, hd = a.hd, d = a.d;
-  const int Sk = SRC == S_SELF ? S : a.Ck;
-  h16* sq = scratch;
-  h16* sk = sq + (size_t)S * hd;
-  h16* sv = sk + (size_t)Sk * hd;
-  float* P = (float*)(sv + (size_t)Sk * hd);   // [S][Sk]
-  const int nv = hd / 8;
-  const int c0 = h * hd;
-  if constexpr (SRC == S_SELF) {
-    // sq, sk, sv are consecutive [S][hd] blocks: vector idx -> (part, row, col)
-    const size_t ld = 3 * (size_t)d;
-    batched_copy(3 * S * nv,
-                 [&](int idx) {
-                   const int part = idx / (S * nv);
-                   const int r = idx - part * S * nv;
-                   const int i = r / nv, c = (r - i * nv) * 8;
-                   return *(const h16x8*)(ex.a + (size_t)i * ld + part * d + c0 + c);
-                 },
-                 [&](int idx, h16x8 v) { *(h16x8*)(sq + (size_t)idx * 8) = v; });
-  } else {
-    // q = fp16(sum of the cross-q partials + bias), four columns per thread-step
-    const int nq = hd / 4;
-    const size_t pst = (size_t)S * d;
-    for (int idx = threadIdx.x; idx < S * nq; idx += blockDim.x) {
-      const int i = idx / nq, c = (idx - i * nq) * 4;
-      const float* Pp = ex.pin + (size_t)i * d + c0 + c;
-      float4 t[8];                                  // every partial of the group in flight at once
-#pragma unroll
-      for (int q = 0; q < 8; ++q)
-        if (q < a.ks_in) t[q] = *(const float4*)(Pp + q * pst);
-      float4 s4 = t[0];
-#pragma unroll
-      for (int q = 1; q < 8; ++q)
-        if (q < a.ks_in) { s4.x += t[q].x; s4.y += t[q].y; s4.z += t[q].z; s4.w += t[q].w; }
-      const h16* bb = ex.bin + c0 + c;
-      h16* dst = sq + i * hd + c;
-      dst[0] = (h16)(s4.x + (float)bb[0]);
-      dst[1] = (h16)(s4.y + (float)bb[1]);
-      dst[2] = (h16)(s4.z + (float)bb[2]);
-      dst[3] = (h16)(s4.w + (float)bb[3]);
-    }
-    // sk, sv are consecutive [Sk][hd] blocks fed from the K and V rows of the hoisted context
-    batched_copy(2 * Sk * nv,
-                 [&](int idx) {
-                   const int j = idx / nv, c = (idx - j * nv) * 8;   // j < 2 Sk: K rows then V rows
-                   return *(const h16x8*)(ex.a + (size_t)j * d + c0 + c);
-                 },
-                 [&](int idx, h16x8 v) { *(h16x8*)(sk + (size_t)idx * 8) = v; });
-  }
-  __syncthreads();
+// Attention of head h for the S rows of one expert from q, k, v already in LDS (sq [S][hd], sk and
+// sv [Sk][hd]), written as fp16 into As [S][lda].  Causal mask = triu(-inf, 1)
+// (cf/drafters/chunked_flow.py:273-275); scores and the weighted sum in fp32 on fp16 q/k/v, output
+// rounded to fp16.
+__device__ void attend(int S, int Sk, int hd, bool causal, const h16* sq, const h16* sk, const h16* sv,
+                       float* P, h16* As, int lda) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
   const float scale = 1.0f / sqrtf((float)hd);
   for (int pr = wave; pr < S * Sk; pr += nw) {
@@ -132,10 +83,10 @@ __device__ void stage_attention(const SArgs& a, const SEx& ex, int h, h16* As, i
 #pragma unroll
       for (int t = 0; t < 8; ++t) part += (float)qa[t] * (float)kb[t];
     }
-    const float s = wave_sum(part) * scale;
-    if (lane == 0) P[i * Sk + j] = (SRC == S_SELF && j > i) ? -INFINITY : s;
+    const float sc = wave_sum(part) * scale;
+    if (lane == 0) P[i * Sk + j] = (causal && j > i) ? -INFINITY : sc;
   }
-  __syncthreads();
+  lds_barrier();
   if ((int)threadIdx.x < S) {
     const int i = threadIdx.x;
     float m = -INFINITY;
@@ -149,7 +100,8 @@ __device__ void stage_attention(const SArgs& a, const SEx& ex, int h, h16* As, i
     const float inv = 1.0f / den;
     for (int j = 0; j < Sk; ++j) P[i * Sk + j] *= inv;
   }
-  __syncthreads();
+  lds_barrier();
+  const int nv = hd / 8;
   for (int idx = threadIdx.x; idx < S * nv; idx += blockDim.x) {
     const int i = idx / nv, c = (idx - i * nv) * 8;
     float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -166,8 +118,143 @@ __device__ void stage_attention(const SArgs& a, const SEx& ex, int h, h16* As, i
   }
 }
 
-template <int SRC, int EPI, int SPF>
-__global__ void __launch_bounds__(SWMAX * 64) k_stream(SArgs a) {
+// Operand staging in two phases around the weight prefetch.  A wave's vector loads complete in
+// issue order, so operand loads issued after the prefetch burst would wait for all of it; instead
+// `load` issues every operand load of the thread (at most NS, which the launcher guarantees) into
+// registers, the kernel then puts the weight prefetch in flight, and `place` writes the registers
+// to LDS.  There is deliberately no slower path for operands that do not fit: its loads would
+// make the compiler's wait before the first multiply cover the whole prefetch.
+// Every slot load and store is unconditional, its index clamped into range (a clamped slot
+// rewrites the last vector with the value it holds), so that the compiler cannot sink a load past
+// the prefetch into a conditional store, where the wait before the store would cover the prefetch.
+//   S_BUF  : vectors idx = u * nt + t of the A chunk [S][KC] -> As [S][lda]
+//   S_SELF : vectors of q | k | v of head h (each [S][hd]) -> consecutive LDS blocks sq, sk, sv
+//   S_CROSS: the ks_in fp32 partials of each 4-column q group g = t + j * nt the thread owns
+//            (slot q * gj + j; summed in the order q = 0, 1, ...) and then the vectors of the
+//            hoisted context K and V rows of head h
+template <int SRC, int NS>
+struct Stage {
+  h16x8 st[NS];
+  int nqs;   // S_CROSS: q-partial slots (ks_in * gj)
+  int gj;    // S_CROSS: q groups per thread (<= 4)
+  uint2 qb[4];   // S_CROSS: the 4 fp16 q-bias values of each q group
+
+  __device__ __forceinline__ static const h16x8* buf_src(const SEx& ex, int kc, int KC, int nv, int idx) {
+    const int i = idx / nv, kk = (idx - i * nv) * 8;
+    return (const h16x8*)(ex.a + (size_t)i * ex.lda + (size_t)kc * KC + kk);
+  }
+  __device__ __forceinline__ static const h16x8* self_src(const SArgs& a, const SEx& ex, int h, int nv, int idx) {
+    const int part = idx / (ex.S * nv);
+    const int r = idx - part * ex.S * nv;
+    const int i = r / nv, c = (r - i * nv) * 8;
+    return (const h16x8*)(ex.a + (size_t)i * 3 * a.d + part * a.d + h * a.hd + c);
+  }
+  __device__ __forceinline__ static const h16x8* kv_src(const SArgs& a, const SEx& ex, int h, int nv, int idx) {
+    const int j = idx / nv, c = (idx - j * nv) * 8;   // j < 2 Ck: K rows then V rows
+    return (const h16x8*)(ex.a + (size_t)j * a.d + h * a.hd + c);
+  }
+  __device__ __forceinline__ static const h16x8* q_src(const SArgs& a, const SEx& ex, int h, int g, int q) {
+    const int nq = a.hd / 4;
+    const int i = g / nq, c = (g - i * nq) * 4;
+    return (const h16x8*)(ex.pin + (size_t)q * ex.S * a.d + (size_t)i * a.d + h * a.hd + c);
+  }
+
+  __device__ __forceinline__ void load(const SArgs& a, const SEx& ex, int kc, int KC) {
+    const int t = threadIdx.x, nt = blockDim.x;
+    if constexpr (SRC == S_BUF) {
+      const int nv = KC / 8, total = ex.S * nv;
+#pragma unroll
+      for (int u = 0; u < NS; ++u) st[u] = *buf_src(ex, kc, KC, nv, min(u * nt + t, total - 1));
+    } else if constexpr (SRC == S_SELF) {
+      const int nv = a.hd / 8, total = 3 * ex.S * nv;
+#pragma unroll
+      for (int u = 0; u < NS; ++u) st[u] = *self_src(a, ex, kc, nv, min(u * nt + t, total - 1));
+    } else {
+      const int G = ex.S * (a.hd / 4), nv = a.hd / 8, nkv = 2 * a.Ck * nv;
+      gj = (G + nt - 1) / nt;
+      nqs = a.ks_in * gj;
+      const int nq = a.hd / 4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int g = min(t + j * nt, G - 1);
+        qb[j] = *(const uint2*)(ex.bin + kc * a.hd + (g - (g / nq) * nq) * 4);
+      }
+#pragma unroll
+      for (int u = 0; u < NS; ++u) {
+        if (u < nqs) {
+          const int q = u / gj, j = u - q * gj;
+          st[u] = *q_src(a, ex, kc, min(t + j * nt, G - 1), q);
+        } else {
+          st[u] = *kv_src(a, ex, kc, nv, min((u - nqs) * nt + t, nkv - 1));
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ void place(const SArgs& a, const SEx& ex, int kc, int KC, h16* As, int lda) {
+    const int t = threadIdx.x, nt = blockDim.x;
+    if constexpr (SRC == S_BUF) {
+      const int nv = KC / 8, total = ex.S * nv;
+      auto put = [&](int idx, h16x8 v) {
+        const int i = idx / nv, kk = (idx - i * nv) * 8;
+        *(h16x8*)(As + i * lda + kk) = v;
+      };
+#pragma unroll
+      for (int u = 0; u < NS; ++u) put(min(u * nt + t, total - 1), st[u]);
+      lds_barrier();
+    } else {
+      const int S = ex.S, hd = a.hd, nv = hd / 8;
+      const int Sk = SRC == S_SELF ? S : a.Ck;
+      h16* sq = As + (size_t)S * lda;
+      h16* sk = sq + (size_t)S * hd;
+      h16* sv = sk + (size_t)Sk * hd;
+      float* P = (float*)(sv + (size_t)Sk * hd);   // [S][Sk]
+      if constexpr (SRC == S_SELF) {
+        const int total = 3 * S * nv;
+#pragma unroll
+        for (int u = 0; u < NS; ++u) *(h16x8*)(sq + (size_t)min(u * nt + t, total - 1) * 8) = st[u];
+      } else {
+        const int nq = hd / 4, G = S * nq, nkv = 2 * Sk * nv;
+        // q = fp16(sum of the cross-q partials + bias) for the 4-column group g
+        auto put_q = [&](int g, float4 s4, uint2 bw) {
+          const int i = g / nq, c = (g - i * nq) * 4;
+          const h16x4 bb = __builtin_bit_cast(h16x4, bw);
+          h16* dst = sq + i * hd + c;
+          dst[0] = (h16)(s4.x + (float)bb[0]);
+          dst[1] = (h16)(s4.y + (float)bb[1]);
+          dst[2] = (h16)(s4.z + (float)bb[2]);
+          dst[3] = (h16)(s4.w + (float)bb[3]);
+        };
+        auto add4 = [](float4& s4, float4 v) { s4.x += v.x; s4.y += v.y; s4.z += v.z; s4.w += v.w; };
+        float4 qs[4] = {};
+#pragma unroll
+        for (int u = 0; u < NS; ++u) {
+          if (u < nqs) {
+            const int q = u / gj, j = u - q * gj;
+            const float4 v = __builtin_bit_cast(float4, st[u]);
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+              if (jj == j) {
+                if (q == 0) qs[jj] = v;
+                else add4(qs[jj], v);
+              }
+          } else {
+            *(h16x8*)(sk + (size_t)min((u - nqs) * nt + t, nkv - 1) * 8) = st[u];
+          }
+        }
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+          if (jj < gj && t + jj * nt < G) put_q(t + jj * nt, qs[jj], qb[jj]);
+      }
+      lds_barrier();
+      attend(S, Sk, hd, SRC == S_SELF, sq, sk, sv, P, As, lda);
+      lds_barrier();
+    }
+  }
+};
+
+template <int SRC, int EPI, int SPF, int NS, int WV>
+__global__ void __launch_bounds__(WV * 64) k_stream(SArgs a) {
   extern __shared__ __align__(16) h16 lds[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   int b = blockIdx.x;
@@ -187,61 +274,55 @@ __global__ void __launch_bounds__(SWMAX * 64) k_stream(SArgs a) {
     const int tt = f / nsteps, s = f - tt * nsteps;
     return __builtin_nontemporal_load(wbase + ((size_t)tt * ksteps + s) * 64);
   };
-  // the weight stream does not depend on the activations: put PF loads in flight first
+  // operand loads first, then the weight prefetch (independent of the operand), then LDS
+  // (the scheduling barriers keep the three groups in this order)
+  Stage<SRC, NS> sg;
+  sg.load(a, ex, kc, KC);
+  __builtin_amdgcn_sched_barrier(0);
   h16x8 buf[SPF];
 #pragma unroll
-  for (int p = 0; p < SPF; ++p)
-    if (p < nf) buf[p] = frag(p);
+  for (int p = 0; p < SPF; ++p) buf[p] = frag(min(p, nf - 1));
+  __builtin_amdgcn_sched_barrier(0);
   h16* As = lds;
-  if constexpr (SRC == S_BUF) {
-    const int nv = KC / 8;
-    batched_copy(ex.S * nv,
-                 [&](int idx) {
-                   const int i = idx / nv, kk = (idx - i * nv) * 8;
-                   return *(const h16x8*)(ex.a + (size_t)i * ex.lda + (size_t)kc * KC + kk);
-                 },
-                 [&](int idx, h16x8 v) {
-                   const int i = idx / nv, kk = (idx - i * nv) * 8;
-                   *(h16x8*)(As + i * lda + kk) = v;
-                 });
-  } else {
-    stage_attention<SRC>(a, ex, kc, As, lda, As + (size_t)ex.S * lda);
-  }
-  __syncthreads();
+  sg.place(a, ex, kc, KC, As, lda);
   const int row = lane & 15, kg = lane >> 4;
   const bool live = row < ex.S;
   const h16* arow = As + (live ? row : 0) * lda + kg * 8;
   const h16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
   const int col = lane & 15, rbase = 4 * (lane >> 4);
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  // fragment f: multiply, and store the tile after its last k-step
+  auto step = [&](int f, h16x8 bf) {
+    const int tt = f / nsteps, s = f - tt * nsteps;
+    const h16x8 av = live ? *(const h16x8*)(arow + s * 32) : zero;
+    acc = mfma_f16(av, bf, acc);
+    if (s == nsteps - 1) {
+      const int n = (t0 + tt) * 16 + col;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = rbase + q;
+        if (r < ex.S) {
+          if constexpr (EPI == E_PART) {
+            ((float*)ex.out)[((size_t)kc * ex.S + r) * a.N + n] = acc[q];
+          } else if constexpr (EPI == E_BIAS16) {
+            ((h16*)ex.out)[(size_t)r * a.N + n] = (h16)(acc[q] + (float)ex.bias[n]);
+          } else {
+            ((h16*)ex.out)[(size_t)r * a.N + n] = (h16)gelu_erf(acc[q] + (float)ex.bias[n]);
+          }
+        }
+      }
+      acc = (f32x4){0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  // Slot p is consumed and then refilled with the fragment SPF ahead, always (past the end the
+  // index is clamped to the last fragment, which re-reads a line just fetched), so the ring's
+  // registers stay fixed across iterations and each multiply waits only for its own fragment.
+  // A conditional refill would make the wait before every multiply cover all loads in flight.
   for (int f0 = 0; f0 < nf; f0 += SPF) {
 #pragma unroll
     for (int p = 0; p < SPF; ++p) {
-      const int f = f0 + p;
-      if (f < nf) {
-        const h16x8 bf = buf[p];
-        if (f + SPF < nf) buf[p] = frag(f + SPF);
-        const int tt = f / nsteps, s = f - tt * nsteps;
-        const h16x8 av = live ? *(const h16x8*)(arow + s * 32) : zero;
-        acc = mfma_f16(av, bf, acc);
-        if (s == nsteps - 1) {
-          const int n = (t0 + tt) * 16 + col;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int r = rbase + q;
-            if (r < ex.S) {
-              if constexpr (EPI == E_PART) {
-                ((float*)ex.out)[((size_t)kc * ex.S + r) * a.N + n] = acc[q];
-              } else if constexpr (EPI == E_BIAS16) {
-                ((h16*)ex.out)[(size_t)r * a.N + n] = (h16)(acc[q] + (float)ex.bias[n]);
-              } else {
-                ((h16*)ex.out)[(size_t)r * a.N + n] = (h16)gelu_erf(acc[q] + (float)ex.bias[n]);
-              }
-            }
-          }
-          acc = (f32x4){0.f, 0.f, 0.f, 0.f};
-        }
-      }
+      if (f0 + p < nf) step(f0 + p, buf[p]);
+      buf[p] = frag(min(f0 + p + SPF, nf - 1));
     }
   }
 }
@@ -255,41 +336,76 @@ size_t stream_lds(int SRC, int S, int KC, int hd, int Ck) {
   return lds;
 }
 
-template <int SRC, int EPI, int SPF>
-int launch_stream_pf(const SArgs& a, int S_max, hipStream_t st) {
-  const int tiles = a.N / 16;
-  if (a.K % a.ks || (a.K / a.ks) % 32 || tiles % (a.wpb * a.tpw) || a.wpb > SWMAX) return CFH_E_UNSUPPORTED;
-  const size_t lds = stream_lds(SRC, S_max, a.K / a.ks, a.hd, a.Ck);
-  if (lds > 150 * 1024) return CFH_E_UNSUPPORTED;
+template <int SRC, int EPI, int SPF, int NS, int WV>
+int launch_stream_k(const SArgs& a, size_t lds, hipStream_t st) {
   // allow more than 64 KiB of dynamic LDS, once per device
   static unsigned long long attr_set = 0;
   int dev = 0;
   CFH_HIP(hipGetDevice(&dev));
   if (dev < 64 && !(attr_set & (1ull << dev))) {
-    CFH_HIP(hipFuncSetAttribute((const void*)k_stream<SRC, EPI, SPF>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                150 * 1024));
+    CFH_HIP(hipFuncSetAttribute((const void*)k_stream<SRC, EPI, SPF, NS, WV>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024));
     attr_set |= 1ull << dev;
   }
   const long long wgs = (long long)a.nex * a.ks * a.wg_per_kc;
-  hipLaunchKernelGGL((k_stream<SRC, EPI, SPF>), dim3((unsigned)wgs), dim3(a.wpb * 64), lds, st, a);
+  hipLaunchKernelGGL((k_stream<SRC, EPI, SPF, NS, WV>), dim3((unsigned)wgs), dim3(a.wpb * 64), lds, st, a);
   CFH_LAUNCH_CHECK();
   return CFH_OK;
 }
 
-// Full-K units stream 160+ fragments per wave and want a deep prefetch; split-K units are short
-// and many, and a shallower one keeps fewer requests queued at the HBM controllers (measured).
+// Operand loads per thread of an expert with S_max rows (16-byte vectors); more than 16 (or, for
+// the cross attention, more than 4 q groups per thread) is not supported.
+int stage_need(int SRC, const SArgs& a, int S_max) {
+  const int nt = a.wpb * 64;
+  auto up = [](int x, int y) { return (x + y - 1) / y; };
+  if (SRC == S_BUF) return up(S_max * (a.K / a.ks / 8), nt);
+  if (SRC == S_SELF) return up(3 * S_max * (a.hd / 8), nt);
+  const int gj = up(S_max * (a.hd / 4), nt);
+  return gj > 4 ? 1 << 20 : a.ks_in * gj + up(2 * a.Ck * (a.hd / 8), nt);
+}
+
+template <int SRC, int EPI, int SPF, int WV>
+int launch_stream_ns(const SArgs& a, size_t lds, int need, hipStream_t st) {
+  if (need <= 4) return launch_stream_k<SRC, EPI, SPF, 4, WV>(a, lds, st);
+  if (need <= 8) return launch_stream_k<SRC, EPI, SPF, 8, WV>(a, lds, st);
+  return launch_stream_k<SRC, EPI, SPF, 16, WV>(a, lds, st);
+}
+
+// Full-K units of 8-wave workgroups stream 160+ fragments per wave and want a deep prefetch;
+// split-K units are short and many, and a shallower one keeps fewer requests queued at the HBM
+// controllers; 16-wave workgroups already hold twice the waves per CU and take the shallower one
+// (measured).  The operand slots (4, 8 or 16) cover every operand load of a thread.
+// Operand slots of the kernel for a workgroup of wpb waves (the 16-wave kernels have 128 VGPRs).
+int stage_slots(int wpb) { return wpb > 8 ? 8 : 16; }
+
+int stream_check(int SRC, const SArgs& a, int S_max) {
+  if (a.ks <= 0 || a.wpb <= 0 || a.tpw <= 0 || a.N % 16 || a.K % a.ks || (a.K / a.ks) % 32) return CFH_E_UNSUPPORTED;
+  if ((a.N / 16) % (a.wpb * a.tpw) || a.wpb > SWMAX || stage_need(SRC, a, S_max) > stage_slots(a.wpb) ||
+      stream_lds(SRC, S_max, a.K / a.ks, a.hd, a.Ck) > 150 * 1024)
+    return CFH_E_UNSUPPORTED;
+  return CFH_OK;
+}
+
 template <int SRC, int EPI>
 int launch_stream(const SArgs& a, int S_max, hipStream_t st) {
-  return a.ks == 1 ? launch_stream_pf<SRC, EPI, PF_FULL>(a, S_max, st)
-                   : launch_stream_pf<SRC, EPI, PF_SPLIT>(a, S_max, st);
+  if (stream_check(SRC, a, S_max)) return CFH_E_UNSUPPORTED;
+  const size_t lds = stream_lds(SRC, S_max, a.K / a.ks, a.hd, a.Ck);
+  const int need = stage_need(SRC, a, S_max);
+  if (a.wpb > 8) {   // the 16-wave kernels have 128 VGPRs: at most 8 operand slots
+    if (need <= 4) return launch_stream_k<SRC, EPI, PF_SPLIT, 4, 16>(a, lds, st);
+    return launch_stream_k<SRC, EPI, PF_SPLIT, 8, 16>(a, lds, st);
+  }
+  if (a.ks == 1) return launch_stream_ns<SRC, EPI, PF_FULL, 8>(a, lds, need, st);
+  return launch_stream_ns<SRC, EPI, PF_SPLIT, 8>(a, lds, need, st);
 }
 
 // ---------------------------------------------------------------------------- row kernels
 // RES: x[r] += sum_kc P[kc][r] + bias; a[r] = fp16(LN(fp16(x[r]))).  One workgroup per (expert,
-// row) of d / (4 NQ) threads, NQ float4 column groups each; the partial rows are loaded RB at a
+// row) of d / (4 NQ) threads, NQ float4 column groups each; the partial rows are loaded RB(NQ) at a
 // time with every load of a batch in flight together.
 constexpr int RQ = 16;            // max float4 groups per thread (d <= 16384)
-constexpr int RB = 8;             // partial rows loaded per batch
+// partial rows loaded per batch: 16 float4 loads per thread in flight, at least 2 rows
+constexpr int rb_for(int nq) { return nq <= 2 ? 8 : nq <= 4 ? 4 : 2; }
 
 // NQ for a row of d columns: the smallest group count giving a whole number of waves and at most
 // 1024 threads (0 if none), so the row's loads spread over as many lanes as possible.
@@ -337,6 +453,7 @@ __device__ void res_row(const ResArgs& a, int e, int r) {
     xv[k] = *(const float4*)(xr + q * 4);
     acc[k] = *(const float4*)(Pr + q * 4);
   }
+  constexpr int RB = rb_for(NQ);
   for (int kc = 1; kc < a.ks; kc += RB) {
     float4 t[RB][NQ];
 #pragma unroll
@@ -572,7 +689,7 @@ int choose_ks(int nex, int tiles, int K, int S, int target, size_t lds_cap) {
 struct Plan {
   int d, fd, CS, E, NL, C, KD, H, hd, nch, Smax;
   int ks_qc, ks_w2, ks_out, ks_kv, ks_tau;
-  int wpb_qc, wpb_w2, wpb_out, tpw_att, wpb_att, wpb_full;
+  int wpb_qc, wpb_w2, wpb_out, tpw_att, wpb_att, wpb_full, wpb_w1;
   int pks;            // partial slots per expert
   bool ok;
 };
@@ -581,6 +698,22 @@ int pick_wpb(int tiles, int tpw) {
   for (int w : {8, 4, 2, 1})
     if (tiles % (w * tpw) == 0) return w;
   return 1;
+}
+
+// Waves per workgroup (and, if tpw is given, tiles per wave: 1 or 2) that cut T tiles of each of U
+// (expert, k-chunk) units into exactly one workgroup per CU of the 256, so the launch runs as one
+// round; false (nothing changed) if no split of at most 16 waves does.
+bool fit_grid(int T, int U, int* wpb, int* tpw) {
+  constexpr int CUS = 256;
+  if ((long long)T * U % CUS) return false;
+  const int wt = (int)((long long)T * U / CUS);
+  for (int tp : {2, 1}) {
+    if ((tp == 2 && !tpw) || wt % tp || wt / tp > SWMAX || T % wt) continue;
+    *wpb = wt / tp;
+    if (tpw) *tpw = tp;
+    return true;
+  }
+  return false;
 }
 
 Plan make_plan(const cfh_flow_dims* dm) {
@@ -592,21 +725,47 @@ Plan make_plan(const cfh_flow_dims* dm) {
   const int tiles_d = p.d / 16;
   const size_t cap = 96 * 1024;
   p.ks_qc = choose_ks(p.nch, tiles_d, p.d, p.Smax, 2048, cap);
-  p.ks_w2 = choose_ks(p.nch, tiles_d, p.fd, p.Smax, 4096, cap);
+  // W2: one d-wide k-chunk per ffn slice (ks = ffn_mult) in 16-wave workgroups, so that W1 and W2
+  // both run as one round of ~240 workgroups at one workgroup per CU; else split-K by wave count
+  const bool w2_wide = tiles_d % 16 == 0 && stream_lds(S_BUF, p.Smax, p.d, p.hd, p.C) <= 150 * 1024;
+  p.ks_w2 = w2_wide ? dm->ffn_mult : choose_ks(p.nch, tiles_d, p.fd, p.Smax, 4096, cap);
   p.ks_out = choose_ks(p.nch, tiles_d, p.d, p.CS, 2048, cap);
   p.ks_kv = ksplit_for(p.nch * p.NL, 2 * p.d / 16, p.d, p.C);
   p.ks_tau = ksplit_for(p.nch, p.d / 16, p.d, p.E);
   p.wpb_qc = std::min(4, pick_wpb(tiles_d, 1));
-  p.wpb_w2 = std::min(4, pick_wpb(tiles_d, 1));
+  p.wpb_w2 = w2_wide ? 16 : std::min(4, pick_wpb(tiles_d, 1));
   p.wpb_out = pick_wpb(tiles_d, 1);
   p.tpw_att = (tiles_d % 16 == 0) ? 2 : 1;
   p.wpb_att = pick_wpb(tiles_d, p.tpw_att);
+  fit_grid(tiles_d, p.nch * p.H, &p.wpb_att, &p.tpw_att);
   p.wpb_full = 8;
+  p.wpb_w1 = (p.fd / 16) % 16 == 0 ? 16 : 8;
+  // the cross attention holds every q partial of its groups in registers: fewer QC splits if needed
+  for (int ks = p.ks_qc; ks > 1; --ks) {
+    SArgs a = {};
+    a.N = p.d; a.K = p.d; a.ks = p.H; a.wpb = p.wpb_att; a.tpw = p.tpw_att; a.hd = p.hd; a.ks_in = ks; a.Ck = p.C;
+    if ((p.d / 32) % ks || stage_need(S_CROSS, a, p.Smax) > stage_slots(a.wpb)) continue;
+    p.ks_qc = ks;
+    break;
+  }
+  fit_grid(tiles_d, p.nch * p.ks_qc, &p.wpb_qc, nullptr);
   p.pks = std::max(std::max(p.H, p.ks_w2), p.ks_out);
-  p.ok = p.ks_qc > 0 && p.ks_qc <= 8 && p.ks_w2 > 0 && p.ks_out > 0 && p.hd % 32 == 0 && (3 * tiles_d) % 8 == 0 &&
-         (p.fd / 16) % 8 == 0 && stream_lds(S_BUF, p.Smax, p.d, p.hd, p.C) <= 150 * 1024 &&
-         stream_lds(S_SELF, p.Smax, p.hd, p.hd, p.C) <= 150 * 1024 &&
-         stream_lds(S_CROSS, p.Smax, p.hd, p.hd, p.C) <= 150 * 1024 && res_nq(p.d) > 0;
+  p.ok = p.ks_qc > 0 && p.ks_qc <= 8 && p.ks_w2 > 0 && p.ks_out > 0 && p.hd % 32 == 0 && res_nq(p.d) > 0;
+  if (!p.ok) return p;
+  // every streaming launch of a draft, as block_pass and the OUT step issue them
+  auto sa = [&](int N, int K, int ks, int wpb, int tpw) {
+    SArgs a = {};
+    a.nex = p.nch; a.N = N; a.K = K; a.ks = ks; a.wpb = wpb; a.tpw = tpw; a.d = p.d; a.hd = p.hd;
+    a.ks_in = p.ks_qc; a.Ck = p.C;
+    return a;
+  };
+  p.ok = !stream_check(S_BUF, sa(3 * p.d, p.d, 1, p.wpb_full, 1), p.Smax) &&
+         !stream_check(S_SELF, sa(p.d, p.d, p.H, p.wpb_att, p.tpw_att), p.Smax) &&
+         !stream_check(S_BUF, sa(p.d, p.d, p.ks_qc, p.wpb_qc, 1), p.Smax) &&
+         !stream_check(S_CROSS, sa(p.d, p.d, p.H, p.wpb_att, p.tpw_att), p.Smax) &&
+         !stream_check(S_BUF, sa(p.fd, p.d, 1, p.wpb_w1, 1), p.Smax) &&
+         !stream_check(S_BUF, sa(p.d, p.fd, p.ks_w2, p.wpb_w2, 1), p.Smax) &&
+         !stream_check(S_BUF, sa(p.d, p.d, p.ks_out, p.wpb_out, 1), p.CS);
   return p;
 }
 
@@ -728,7 +887,7 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w, const voi
   // W1: g = fp16(gelu(LN_ffn(x) W1^T + b1)), full-K tiles
   {
     SArgs a = {};
-    a.nex = nch; a.N = fd; a.K = d; a.ks = 1; a.wpb = p.wpb_full; a.tpw = 1; a.d = d; a.hd = p.hd;
+    a.nex = nch; a.N = fd; a.K = d; a.ks = 1; a.wpb = p.wpb_w1; a.tpw = 1; a.d = d; a.hd = p.hd;
     a.wg_per_kc = (fd / 16) / (a.wpb * a.tpw);
     for (int c = 0; c < nch; ++c) {
       SEx& x = a.ex[c];

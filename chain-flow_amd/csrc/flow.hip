@@ -269,19 +269,34 @@ __global__ void __launch_bounds__(WV * 64) k_stream(SArgs a) {
   const int t0 = (tg * a.wpb + wave) * a.tpw;
   const int nf = a.tpw * nsteps;
   const int lda = KC + 8;
-  const h16x8* wbase = ex.w + ((size_t)t0 * ksteps + (size_t)kc * nsteps) * 64 + lane;
-  auto frag = [&](int f) -> h16x8 {
-    const int tt = f / nsteps, s = f - tt * nsteps;
-    return __builtin_nontemporal_load(wbase + ((size_t)tt * ksteps + s) * 64);
+  // Fragment loader: a wave-uniform pointer walked one fragment at a time (the next tile of the
+  // wave starts ksteps - nsteps fragments further on); past the last fragment it stays there, so
+  // the ring's surplus refills re-read a line just fetched.  Walking the pointer, rather than
+  // deriving each address from the fragment index, keeps integer divisions out of the loop
+  // (measured: they cost ~5% of the streaming rate).
+  const h16x8* lw = ex.w + ((size_t)t0 * ksteps + (size_t)kc * nsteps) * 64;
+  const size_t jump = (size_t)(ksteps - nsteps + 1) * 64;
+  int ls = 0, lleft = nf;
+  auto issue = [&]() -> h16x8 {
+    const h16x8 v = __builtin_nontemporal_load(lw + lane);
+    const bool adv = lleft > 1, wrap = ls == nsteps - 1;
+    lw += adv ? (wrap ? jump : 64) : 0;
+    ls = adv ? (wrap ? 0 : ls + 1) : ls;
+    lleft -= adv;
+    return v;
   };
   // operand loads first, then the weight prefetch (independent of the operand), then LDS
   // (the scheduling barriers keep the three groups in this order)
   Stage<SRC, NS> sg;
   sg.load(a, ex, kc, KC);
+  // the bias of the wave's first tile comes with the operand: an epilogue load issued after the
+  // weight loads would wait for every one of them
+  float bias0 = 0.f;
+  if constexpr (EPI != E_PART) bias0 = (float)ex.bias[t0 * 16 + (lane & 15)];
   __builtin_amdgcn_sched_barrier(0);
   h16x8 buf[SPF];
 #pragma unroll
-  for (int p = 0; p < SPF; ++p) buf[p] = frag(min(p, nf - 1));
+  for (int p = 0; p < SPF; ++p) buf[p] = issue();
   __builtin_amdgcn_sched_barrier(0);
   h16* As = lds;
   sg.place(a, ex, kc, KC, As, lda);
@@ -291,38 +306,46 @@ __global__ void __launch_bounds__(WV * 64) k_stream(SArgs a) {
   const h16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
   const int col = lane & 15, rbase = 4 * (lane >> 4);
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  // fragment f: multiply, and store the tile after its last k-step
-  auto step = [&](int f, h16x8 bf) {
-    const int tt = f / nsteps, s = f - tt * nsteps;
-    const h16x8 av = live ? *(const h16x8*)(arow + s * 32) : zero;
+  // the next fragment to multiply is k-step cs of the wave's tile ct; the tile is stored after its
+  // last k-step
+  int cs = 0, ct = 0;
+  auto step = [&](h16x8 bf) {
+    const h16x8 av = live ? *(const h16x8*)(arow + cs * 32) : zero;
     acc = mfma_f16(av, bf, acc);
-    if (s == nsteps - 1) {
-      const int n = (t0 + tt) * 16 + col;
+    if (cs == nsteps - 1) {
+      const int n = (t0 + ct) * 16 + col;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int r = rbase + q;
         if (r < ex.S) {
           if constexpr (EPI == E_PART) {
             ((float*)ex.out)[((size_t)kc * ex.S + r) * a.N + n] = acc[q];
-          } else if constexpr (EPI == E_BIAS16) {
-            ((h16*)ex.out)[(size_t)r * a.N + n] = (h16)(acc[q] + (float)ex.bias[n]);
           } else {
-            ((h16*)ex.out)[(size_t)r * a.N + n] = (h16)gelu_erf(acc[q] + (float)ex.bias[n]);
+            float bv;
+            if (ct == 0) bv = bias0;
+            else bv = (float)ex.bias[n];
+            if constexpr (EPI == E_BIAS16) ((h16*)ex.out)[(size_t)r * a.N + n] = (h16)(acc[q] + bv);
+            else ((h16*)ex.out)[(size_t)r * a.N + n] = (h16)gelu_erf(acc[q] + bv);
           }
         }
       }
       acc = (f32x4){0.f, 0.f, 0.f, 0.f};
+      ++ct;
+      cs = 0;
+    } else {
+      ++cs;
     }
   };
-  // Slot p is consumed and then refilled with the fragment SPF ahead, always (past the end the
-  // index is clamped to the last fragment, which re-reads a line just fetched), so the ring's
+  // Slot p is consumed and then refilled with the fragment SPF ahead, always, so the ring's
   // registers stay fixed across iterations and each multiply waits only for its own fragment.
-  // A conditional refill would make the wait before every multiply cover all loads in flight.
+  // A conditional refill would make the wait before every multiply cover all loads in flight, and
+  // a separate drain after the loop makes the compiler copy the ring between registers at the
+  // loop entry, which waits for the whole prefetch (both measured in the generated code).
   for (int f0 = 0; f0 < nf; f0 += SPF) {
 #pragma unroll
     for (int p = 0; p < SPF; ++p) {
-      if (f0 + p < nf) step(f0 + p, buf[p]);
-      buf[p] = frag(min(f0 + p + SPF, nf - 1));
+      if (f0 + p < nf) step(buf[p]);
+      buf[p] = issue();
     }
   }
 }

@@ -110,14 +110,16 @@ struct TileStream {
     const h16* arow = As + (live ? row : 0) * lda + kg * 8;
     const h16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
     if (piped) {
+      // slot p is consumed and only then refilled PF steps ahead: the ring keeps its registers
+      // across iterations (a refill issued before the multiply needs a second register, and the
+      // copy back at the loop edge waits for every load in flight)
       int s0 = 0;
       for (; s0 < nsteps - PF; s0 += PF) {
 #pragma unroll
         for (int p = 0; p < PF; ++p) {
-          const h16x8 b = buf[p];
-          buf[p] = ld((size_t)(s0 + PF + p));
           const h16x8 a = live ? *(const h16x8*)(arow + (s0 + p) * 32) : zero;
-          acc = mfma_f16(a, b, acc);
+          acc = mfma_f16(a, buf[p], acc);
+          buf[p] = ld((size_t)(s0 + PF + p));
         }
       }
 #pragma unroll

@@ -237,9 +237,9 @@ __global__ void __launch_bounds__(256) k_gelu(GeluArgs a) {
 __device__ __forceinline__ float block_sum(float v, float* red) {
   v = wave_sum(v);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  __syncthreads();
+  lds_barrier();   // (not __syncthreads: no wait for the row's global stores in flight)
   if (lane == 0) red[wave] = v;
-  __syncthreads();
+  lds_barrier();
   float t = 0.f;
   for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t += red[w];
   return t;
@@ -251,6 +251,16 @@ constexpr int ROWQ = ROWE / 4;   // float4 groups per thread
 
 __device__ void ln_row4(const float4* vals, int d, const h16* g, const h16* b, h16* out, float* red) {
   const int nq = d / 4;
+  // gamma and beta are loaded before the statistics, not after them
+  h16x4 gq[ROWQ], bq[ROWQ];
+#pragma unroll
+  for (int k = 0; k < ROWQ; ++k) {
+    const int q = threadIdx.x + k * blockDim.x;
+    if (q < nq) {
+      gq[k] = *(const h16x4*)(g + q * 4);
+      bq[k] = *(const h16x4*)(b + q * 4);
+    }
+  }
   float s = 0.f;
 #pragma unroll
   for (int k = 0; k < ROWQ; ++k) {
@@ -272,11 +282,12 @@ __device__ void ln_row4(const float4* vals, int d, const h16* g, const h16* b, h
   for (int k = 0; k < ROWQ; ++k) {
     const int q = threadIdx.x + k * blockDim.x;
     if (q < nq) {
-      const int c = q * 4;
-      out[c + 0] = (h16)((vals[k].x - mean) * rstd * (float)g[c + 0] + (float)b[c + 0]);
-      out[c + 1] = (h16)((vals[k].y - mean) * rstd * (float)g[c + 1] + (float)b[c + 1]);
-      out[c + 2] = (h16)((vals[k].z - mean) * rstd * (float)g[c + 2] + (float)b[c + 2]);
-      out[c + 3] = (h16)((vals[k].w - mean) * rstd * (float)g[c + 3] + (float)b[c + 3]);
+      h16x4 o;
+      o[0] = (h16)((vals[k].x - mean) * rstd * (float)gq[k][0] + (float)bq[k][0]);
+      o[1] = (h16)((vals[k].y - mean) * rstd * (float)gq[k][1] + (float)bq[k][1]);
+      o[2] = (h16)((vals[k].z - mean) * rstd * (float)gq[k][2] + (float)bq[k][2]);
+      o[3] = (h16)((vals[k].w - mean) * rstd * (float)gq[k][3] + (float)bq[k][3]);
+      *(h16x4*)(out + q * 4) = o;
     }
   }
 }

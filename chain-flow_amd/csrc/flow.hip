@@ -453,9 +453,9 @@ struct ResArgs {
 __device__ __forceinline__ float block_sum_rt(float v, float* red) {  // red[blockDim/64]
   v = wave_sum(v);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  __syncthreads();
+  lds_barrier();   // (not __syncthreads: no wait for the row's global stores in flight)
   if (lane == 0) red[wave] = v;
-  __syncthreads();
+  lds_barrier();
   float t = 0.f;
   for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t += red[w];
   return t;
@@ -469,12 +469,18 @@ __device__ void res_row(const ResArgs& a, int e, int r) {
   const size_t pst = (size_t)a.rows[e] * d;
   float* xr = a.x[e] + (size_t)r * d;
   const float* Pr = a.P[e] + (size_t)r * d;
+  // every load of the row is issued up front (the bias, gamma and beta too, so that the LayerNorm
+  // does not pay a second memory round trip after the statistics)
   float4 acc[NQ], xv[NQ];
+  h16x4 bq[NQ], gq[NQ], btq[NQ];
 #pragma unroll
   for (int k = 0; k < NQ; ++k) {
     const int q = threadIdx.x + k * RT;
     xv[k] = *(const float4*)(xr + q * 4);
     acc[k] = *(const float4*)(Pr + q * 4);
+    bq[k] = *(const h16x4*)(a.bias[e] + q * 4);
+    gq[k] = *(const h16x4*)(a.g[e] + q * 4);
+    btq[k] = *(const h16x4*)(a.b[e] + q * 4);
   }
   constexpr int RB = rb_for(NQ);
   for (int kc = 1; kc < a.ks; kc += RB) {
@@ -498,12 +504,11 @@ __device__ void res_row(const ResArgs& a, int e, int r) {
 #pragma unroll
   for (int k = 0; k < NQ; ++k) {
     const int q = threadIdx.x + k * RT;
-    const h16* bb = a.bias[e] + q * 4;
     float4 xn;
-    xn.x = xv[k].x + (acc[k].x + (float)bb[0]);
-    xn.y = xv[k].y + (acc[k].y + (float)bb[1]);
-    xn.z = xv[k].z + (acc[k].z + (float)bb[2]);
-    xn.w = xv[k].w + (acc[k].w + (float)bb[3]);
+    xn.x = xv[k].x + (acc[k].x + (float)bq[k][0]);
+    xn.y = xv[k].y + (acc[k].y + (float)bq[k][1]);
+    xn.z = xv[k].z + (acc[k].z + (float)bq[k][2]);
+    xn.w = xv[k].w + (acc[k].w + (float)bq[k][3]);
     *(float4*)(xr + q * 4) = xn;
     vals[k] = r16x4(xn);
     s += (vals[k].x + vals[k].y) + (vals[k].z + vals[k].w);
@@ -516,16 +521,16 @@ __device__ void res_row(const ResArgs& a, int e, int r) {
     v += (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
   }
   const float rstd = 1.0f / sqrtf(block_sum_rt(v, red) / (float)d + LN_EPS);
-  const h16* g = a.g[e];
-  const h16* bt = a.b[e];
   h16* out = a.a[e] + (size_t)r * d;
 #pragma unroll
   for (int k = 0; k < NQ; ++k) {
     const int c = (threadIdx.x + k * RT) * 4;
-    out[c + 0] = (h16)((vals[k].x - mean) * rstd * (float)g[c + 0] + (float)bt[c + 0]);
-    out[c + 1] = (h16)((vals[k].y - mean) * rstd * (float)g[c + 1] + (float)bt[c + 1]);
-    out[c + 2] = (h16)((vals[k].z - mean) * rstd * (float)g[c + 2] + (float)bt[c + 2]);
-    out[c + 3] = (h16)((vals[k].w - mean) * rstd * (float)g[c + 3] + (float)bt[c + 3]);
+    h16x4 o;
+    o[0] = (h16)((vals[k].x - mean) * rstd * (float)gq[k][0] + (float)btq[k][0]);
+    o[1] = (h16)((vals[k].y - mean) * rstd * (float)gq[k][1] + (float)btq[k][1]);
+    o[2] = (h16)((vals[k].z - mean) * rstd * (float)gq[k][2] + (float)btq[k][2]);
+    o[3] = (h16)((vals[k].w - mean) * rstd * (float)gq[k][3] + (float)btq[k][3]);
+    *(h16x4*)(out + c) = o;
   }
 }
 
@@ -772,6 +777,7 @@ Plan make_plan(const cfh_flow_dims* dm) {
     break;
   }
   fit_grid(tiles_d, p.nch * p.ks_qc, &p.wpb_qc, nullptr);
+  fit_grid(tiles_d, p.nch * p.ks_out, &p.wpb_out, nullptr);
   p.pks = std::max(std::max(p.H, p.ks_w2), p.ks_out);
   p.ok = p.ks_qc > 0 && p.ks_qc <= 8 && p.ks_w2 > 0 && p.ks_out > 0 && p.hd % 32 == 0 && res_nq(p.d) > 0;
   if (!p.ok) return p;

@@ -38,6 +38,9 @@ SIGNATURES = {
     "cfh_row_topk": (_I, [_VP, _I, _I, _I, _VP, _VP, _VP, _VP]),
     "cfh_head_ws_bytes": (_I64, [_I, _I, _I]),
     "cfh_head_topk": (_I, [_VP, _I, _I, _VP, _VP, _I, _VP, _VP, _I, _I, _VP, _I, _VP, _VP, _VP, _VP, _VP, _VP]),
+    "cfh_head_packed_bytes": (_I64, [_I, _I, _I]),
+    "cfh_head_pack": (_I, [_VP, _VP, _VP, _I, _I, _I, _VP, _VP]),
+    "cfh_head_topk_packed": (_I, [_VP, _I, _I, _VP, _I, _VP, _VP, _I, _I, _I, _VP, _VP, _VP, _VP, _VP, _VP]),
     "cfh_head_gemm_topk": (_I, [_VP, _I, _I, _VP, _VP, _I, _I, _VP, _VP, _VP, _VP, _VP, _VP]),
     "cfh_path_ws_bytes": (_I64, [_I, _I, _I, _I]),
     "cfh_path_residual": (_I, [C.POINTER(_VP), _I, _I, _I, _VP, _I, _I, _VP, _VP, _VP, _VP, _VP]),

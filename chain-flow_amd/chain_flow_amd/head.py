@@ -17,11 +17,16 @@ def _i32(t: torch.Tensor) -> torch.Tensor:
 
 
 class ShortlistHead:
-    """The target's lm_head restricted to a shortlist, read in place (row gather), plus the markov
-    logit bias ``markov.w2(markov.w1[prev])`` restricted to the same rows."""
+    """The target's lm_head restricted to a shortlist, plus the markov logit bias
+    ``markov.w2(markov.w1[prev])`` restricted to the same rows.
+
+    ``packed=True`` (default) gathers the shortlisted rows of lm_head and markov.w2 once into the
+    MFMA fragment order (``cfh_head_pack``: n * (d + r) * 2 bytes of HBM, 673 MB for the 62,642-row
+    shortlist at d=5120, r=256), so ``topk`` streams contiguous fragments; ``packed=False`` reads
+    the rows in place through the shortlist on every call.  Both give the same results."""
 
     def __init__(self, lm_w: torch.Tensor, shortlist: torch.Tensor | None, w1: torch.Tensor | None = None,
-                 w2: torch.Tensor | None = None):
+                 w2: torch.Tensor | None = None, packed: bool = True):
         if lm_w.dtype != torch.float16 or not lm_w.is_cuda:
             raise ValueError("lm_w must be a CUDA fp16 [V, d] tensor")
         self.lm_w = lm_w.contiguous()
@@ -36,6 +41,16 @@ class ShortlistHead:
             raise ValueError("markov w1 and w2 go together")
         self.r = 0 if self.w1 is None else int(self.w1.shape[1])
         self._ws = {}
+        self.image = None
+        if packed:
+            L = _lib.lib()
+            nbytes = int(L.cfh_head_packed_bytes(self.n, self.d, self.r))
+            if nbytes < 0:
+                raise ValueError(f"head shape unsupported for packing: n={self.n} d={self.d} r={self.r}")
+            self.image = torch.empty(nbytes, dtype=torch.uint8, device=lm_w.device)
+            _lib.check(L.cfh_head_pack(self.lm_w.data_ptr(), None if self.w2 is None else self.w2.data_ptr(),
+                                       _lib.ptr(self.sl), self.n, self.d, self.r, self.image.data_ptr(),
+                                       _lib.stream_handle()), "cfh_head_pack")
 
     def map(self, local: torch.Tensor) -> torch.Tensor:
         """``_map``: shortlist-local column -> global token id."""
@@ -82,6 +97,13 @@ class ShortlistHead:
             vals, ids, lse = out
         use_m = self.w1 is not None and prev is not None
         ws = self.workspace(M, k, dev)
+        if self.image is not None:
+            _lib.check(_lib.lib().cfh_head_topk_packed(
+                h.data_ptr(), M, self.d, self.image.data_ptr(), self.n,
+                self.w1.data_ptr() if use_m else None, prev.data_ptr() if use_m else None, prev_stride,
+                self.r if use_m else 0, k, _lib.ptr(logits), vals.data_ptr(), ids.data_ptr(), lse.data_ptr(),
+                ws.data_ptr(), _lib.stream_handle()), "cfh_head_topk_packed")
+            return vals, ids, lse
         _lib.check(_lib.lib().cfh_head_topk(
             h.data_ptr(), M, self.d, self.lm_w.data_ptr(), _lib.ptr(self.sl), self.n,
             self.w1.data_ptr() if use_m else None, prev.data_ptr() if use_m else None, prev_stride,

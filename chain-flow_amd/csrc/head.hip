@@ -141,10 +141,22 @@ struct HeadArgs {
   int M, d, n, r, a_ids_stride, k, nsets;
 };
 
+// Packed head image (cfh_head_pack): the shortlisted rows of W, then those of the markov w2, in
+// the MFMA fragment order -- fragment (tile t, k-step s) = 1 KiB at (t * K/32 + s) * 64 vectors,
+// lane l holding row sl[16 t + l % 16], columns 32 s + 8 (l / 16) .. +7.  Columns past n repeat
+// the last shortlisted row.
+__host__ __device__ __forceinline__ size_t head_packed_w_bytes(int n, int d) {
+  return (size_t)((n + 15) / 16) * 16 * d * 2;
+}
+
 // One wave per 16-row vocabulary tile, HW tiles per workgroup.  Each lane streams its vocabulary
 // row in place (row-major lm_head, 16 bytes per k-step) against the M activation rows in LDS with
 // v_mfma_f32_16x16x32_f16; the markov bias is a second, rank-r MFMA stream over w2.  Epilogue:
 // logit = fp16(fp16(h.W) + fp16(A.W2)); per row, the block's (max, sum-exp) and top-k.
+//
+// PACKED: W and W2 point at a cfh_head_pack image instead (same results): each wave then streams
+// one contiguous 1 KiB fragment per k-step rather than 16 rows 64 bytes at a time.
+template <bool PACKED>
 __global__ void __launch_bounds__(HW * 64) k_head(HeadArgs a) {
   extern __shared__ __align__(16) h16 sm[];
   __shared__ float Lt[HMAXM][HCOLS];
@@ -157,9 +169,17 @@ __global__ void __launch_bounds__(HW * 64) k_head(HeadArgs a) {
   const int j = t * 16 + (lane & 15);
   const bool colv = (t < ntiles) && (j < a.n);
   const int jc = colv ? j : a.n - 1;                 // padding lanes load a valid row
-  const size_t row = a.sl ? (size_t)a.sl[jc] : (size_t)jc;
-  TileStream<PF, 4, false> ts;
-  ts.begin((const h16x8*)(a.W + row * a.d + 8 * (lane >> 4)), a.d / 32);
+  const size_t row = PACKED ? 0 : (a.sl ? (size_t)a.sl[jc] : (size_t)jc);
+  const size_t tp = (size_t)min(t, ntiles - 1);      // packed: padding waves stream the last tile
+  // the markov fragments (r/32 per lane) are put in flight first: they are few and are used last
+  TileStream<PF, PACKED ? 64 : 4, PACKED> tm;
+  if (a.W2) {
+    if constexpr (PACKED) tm.begin((const h16x8*)a.W2 + tp * (a.r / 32) * 64, a.r / 32);
+    else tm.begin((const h16x8*)(a.W2 + row * a.r + 8 * (lane >> 4)), a.r / 32);
+  }
+  TileStream<PF, PACKED ? 64 : 4, PACKED> ts;
+  if constexpr (PACKED) ts.begin((const h16x8*)a.W + tp * (a.d / 32) * 64, a.d / 32);
+  else ts.begin((const h16x8*)(a.W + row * a.d + 8 * (lane >> 4)), a.d / 32);
   const int nh = a.d / 8;
   batched_copy(a.M * nh,
                [&](int idx) {
@@ -187,11 +207,7 @@ __global__ void __launch_bounds__(HW * 64) k_head(HeadArgs a) {
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   acc = ts.run(Ah, ldh, a.M, acc);
   f32x4 accm = {0.f, 0.f, 0.f, 0.f};
-  if (a.W2) {
-    TileStream<PF, 4, false> tm;
-    tm.begin((const h16x8*)(a.W2 + row * a.r + 8 * (lane >> 4)), a.r / 32);
-    accm = tm.run(Am, ldm, a.M, accm);
-  }
+  if (a.W2) accm = tm.run(Am, ldm, a.M, accm);
   const int rbase = 4 * (lane >> 4);
   const int c = wave * 16 + (lane & 15);
 #pragma unroll
@@ -745,13 +761,40 @@ __global__ void k_backtrack(BacktrackArgs a) {
 
 size_t head_lds(int M, int d, int r) { return (size_t)M * (d + 8) * 2 + (size_t)M * (r + 8) * 2; }
 
-int launch_head(const HeadArgs& ha0, hipStream_t st) {
+int launch_head(const HeadArgs& ha0, hipStream_t st, bool packed = false) {
   HeadArgs ha = ha0;
   const size_t lds = head_lds(ha.M, ha.d, ha.r);
   if (lds > 150 * 1024) return CFH_E_UNSUPPORTED;
-  CFH_HIP(hipFuncSetAttribute((const void*)k_head, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+  const void* fn = packed ? (const void*)k_head<true> : (const void*)k_head<false>;
+  CFH_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
   const int ntiles = (ha.n + 15) / 16;
-  hipLaunchKernelGGL(k_head, dim3((ntiles + HW - 1) / HW), dim3(HW * 64), lds, st, ha);
+  if (packed) hipLaunchKernelGGL(k_head<true>, dim3((ntiles + HW - 1) / HW), dim3(HW * 64), lds, st, ha);
+  else hipLaunchKernelGGL(k_head<false>, dim3((ntiles + HW - 1) / HW), dim3(HW * 64), lds, st, ha);
+  CFH_LAUNCH_CHECK();
+  return CFH_OK;
+}
+
+// out[i] (16-byte vectors) of the packed image of rows sl[0..n) of w [.][K]; i < ntiles * 16 * K / 8
+__global__ void k_pack_rows(const uint4* __restrict__ w, const int* __restrict__ sl, int n, int K,
+                            uint4* __restrict__ out) {
+  const int ntiles = (n + 15) / 16;
+  const size_t total = (size_t)ntiles * 16 * K / 8;
+  const int ks = K / 32;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    const int lane = (int)(i & 63);
+    const size_t ts = i >> 6;
+    const int s = (int)(ts % ks);
+    const int t = (int)(ts / ks);
+    const int j = min(t * 16 + (lane & 15), n - 1);
+    const size_t row = sl ? (size_t)sl[j] : (size_t)j;
+    out[i] = w[(row * K + (size_t)s * 32 + 8 * (lane >> 4)) / 8];
+  }
+}
+
+int launch_pack_rows(const void* w, const int32_t* sl, int n, int K, void* out, hipStream_t st) {
+  const size_t total = (size_t)((n + 15) / 16) * 16 * K / 8;
+  const int grid = (int)std::min<size_t>((total + 255) / 256, 65536);
+  hipLaunchKernelGGL(k_pack_rows, dim3(grid), dim3(256), 0, st, (const uint4*)w, sl, n, K, (uint4*)out);
   CFH_LAUNCH_CHECK();
   return CFH_OK;
 }
@@ -817,6 +860,37 @@ int cfh_head_topk(const void* h, int M, int d, const void* W, const int32_t* sl,
   ha.nsets = (n + HCOLS - 1) / HCOLS;
   hipStream_t st = (hipStream_t)stream;
   if ((rc = launch_head(ha, st))) return rc;
+  return launch_merge(ws, M, ha.nsets, k, vals, ids, lse, st);
+}
+
+int64_t cfh_head_packed_bytes(int n, int d, int r) {
+  if (n < 1 || d < 32 || d % 256 || r < 0 || (r > 0 && (r < 32 || r % 256))) return -1;
+  return (int64_t)(head_packed_w_bytes(n, d) + (r > 0 ? head_packed_w_bytes(n, r) : 0));
+}
+
+int cfh_head_pack(const void* W, const void* W2, const int32_t* sl, int n, int d, int r, void* packed,
+                  void* stream) {
+  if (!W || !packed || cfh_head_packed_bytes(n, d, r) < 0 || (r > 0 && !W2)) return CFH_E_INVALID;
+  hipStream_t st = (hipStream_t)stream;
+  int rc = launch_pack_rows(W, sl, n, d, packed, st);
+  if (rc || r == 0) return rc;
+  return launch_pack_rows(W2, sl, n, r, (char*)packed + head_packed_w_bytes(n, d), st);
+}
+
+int cfh_head_topk_packed(const void* h, int M, int d, const void* packed, int n, const void* a,
+                         const int32_t* a_ids, int a_ids_stride, int r, int k, void* logits, float* vals,
+                         int32_t* ids, float* lse, void* ws, void* stream) {
+  if (!packed || !vals || !ids || !ws || k < 1 || k > KMAX || cfh_head_packed_bytes(n, d, r) < 0) return CFH_E_INVALID;
+  const void* W2 = r > 0 ? (const char*)packed + head_packed_w_bytes(n, d) : nullptr;
+  HeadArgs ha;
+  int rc = head_args(ha, h, M, d, packed, nullptr, n, a, a_ids, a_ids_stride, r, W2);
+  if (rc) return rc;
+  ha.logits = (h16*)logits;
+  ha.ws = ws;
+  ha.k = k;
+  ha.nsets = (n + HCOLS - 1) / HCOLS;
+  hipStream_t st = (hipStream_t)stream;
+  if ((rc = launch_head(ha, st, true))) return rc;
   return launch_merge(ws, M, ha.nsets, k, vals, ids, lse, st);
 }
 

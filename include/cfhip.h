@@ -113,6 +113,22 @@ int cfh_head_topk(const void* h, int M, int d, const void* W, const int32_t* sl,
                   const void* a, const int32_t* a_ids, int a_ids_stride, int r, const void* W2, int k,
                   void* logits, float* vals, int32_t* ids, float* lse, void* ws, void* stream);
 
+/* Bytes of the packed shortlist head image for n shortlist columns, dimension d and markov rank r
+ * (0: no markov table); -1 if out of range. */
+int64_t cfh_head_packed_bytes(int n, int d, int r);
+
+/* Gathers the shortlisted rows W[sl[j]] (and W2[sl[j]] when r > 0) into one image in the MFMA
+ * fragment order, once per shortlist: the layout-for-bandwidth form of the in-place row gather of
+ * cfh_head_topk (cf/vllm_plugin/flow_proposer.py:1021-1025 reads lm_head[shortlist] per call).
+ * packed: cfh_head_packed_bytes(n, d, r) bytes.  sl NULL = rows 0..n-1. */
+int cfh_head_pack(const void* W, const void* W2, const int32_t* sl, int n, int d, int r, void* packed,
+                  void* stream);
+
+/* cfh_head_topk over a cfh_head_pack image (no sl, W, W2: the image holds them).  Same results. */
+int cfh_head_topk_packed(const void* h, int M, int d, const void* packed, int n, const void* a,
+                         const int32_t* a_ids, int a_ids_stride, int r, int k, void* logits, float* vals,
+                         int32_t* ids, float* lse, void* ws, void* stream);
+
 /* Batched (M up to 256) bf16 skinny-GEMM head with per-row log-softmax top-k: the two-pass
  * candidate head's pass A (cf/vllm_plugin/flow_proposer.py:1142-1165) as one MFMA kernel plus the
  * candidate merge.  logits[m][j] = bf16(x[m] . W[row_j]), row_j = sl ? sl[j] : j.

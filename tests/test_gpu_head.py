@@ -226,3 +226,30 @@ def test_fused_head_topk_equals_logits_then_topk(cuda, M, k, markov):
     ov, oi = ohead.topk(ohead.log_softmax(L), k)
     assert np.array_equal(ids.cpu().numpy(), oi)
     assert np.allclose(vals.cpu().numpy(), ov, atol=1e-5, rtol=0)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,k,markov,n", [(1, 4, True, 5003), (4, 4, True, 62642 // 8), (8, 16, False, 1000)])
+def test_packed_head_equals_in_place(cuda, M, k, markov, n):
+    """The packed shortlist image (rows gathered once into the fragment order) gives bit-identical
+    logits and the same top-k as the in-place row gather; n not a multiple of 16 exercises the
+    padded last tile."""
+    d, V = 512, 9000
+    cfg, W = _head_weights(d, V)
+    sl = _shortlist(V, n)
+    g = torch.Generator().manual_seed(29)
+    h = torch.randn(M, d, generator=g).half().to(cuda)
+    prev = torch.randint(0, V, (M,), generator=g, dtype=torch.int32).to(cuda)
+    args = (W["lm_head.weight"].to(cuda), sl.to(cuda), W["markov.w1.weight"].to(cuda) if markov else None,
+            W["markov.w2.weight"].to(cuda) if markov else None)
+    packed, in_place = ShortlistHead(*args, packed=True), ShortlistHead(*args, packed=False)
+    assert packed.image is not None and in_place.image is None
+    out = []
+    for head in (packed, in_place):
+        logits = torch.empty(M, n, dtype=torch.float16, device=cuda)
+        vals, ids, lse = head.topk(h, k, prev=prev if markov else None, logits=logits)
+        out.append((logits, vals, ids, lse))
+    torch.cuda.synchronize()
+    print(f"[packed head M={M} k={k} markov={markov} n={n}]", flush=True)
+    for a, b in zip(out[0], out[1]):
+        assert torch.equal(a, b)

@@ -71,7 +71,7 @@ __host__ __device__ __forceinline__ size_t packed_index(int tile, int kstep, int
 //   TileStream<PF> ts; ts.begin(wp, nsteps);  ...stage A, __syncthreads()...;  acc = ts.run(...)
 //   wp   : packed fragments of this tile at the first k-step of the chunk (lane offset added here)
 //   As   : LDS rows [rows][lda] (halves); lane reads row (lane&15), k-offset 8*(lane>>4) + 32*s
-//   rows : number of valid A rows (<= 16); lanes on padding rows feed zeros
+//   rows : number of valid A rows (<= 16); output rows >= rows hold garbage and must not be stored
 // When nsteps is a multiple of PF the loads are issued unconditionally PF steps ahead, so the
 // compiler keeps PF fragment loads in flight per wave (vmcnt(PF-1) waits); other step counts
 // take a plain loop.
@@ -106,9 +106,8 @@ struct TileStream {
     const int lane = threadIdx.x & 63;
     const int row = lane & 15;
     const int kg = lane >> 4;
-    const bool live = row < rows;
-    const h16* arow = As + (live ? row : 0) * lda + kg * 8;
-    const h16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+    // padding-row lanes read row 0; their products only reach output rows that are never stored
+    const h16* arow = As + (row < rows ? row : 0) * lda + kg * 8;
     if (piped) {
       // slot p is consumed and only then refilled PF steps ahead: the ring keeps its registers
       // across iterations (a refill issued before the multiply needs a second register, and the
@@ -117,20 +116,20 @@ struct TileStream {
       for (; s0 < nsteps - PF; s0 += PF) {
 #pragma unroll
         for (int p = 0; p < PF; ++p) {
-          const h16x8 a = live ? *(const h16x8*)(arow + (s0 + p) * 32) : zero;
+          const h16x8 a = *(const h16x8*)(arow + (s0 + p) * 32);
           acc = mfma_f16(a, buf[p], acc);
           buf[p] = ld((size_t)(s0 + PF + p));
         }
       }
 #pragma unroll
       for (int p = 0; p < PF; ++p) {
-        const h16x8 a = live ? *(const h16x8*)(arow + (s0 + p) * 32) : zero;
+        const h16x8 a = *(const h16x8*)(arow + (s0 + p) * 32);
         acc = mfma_f16(a, buf[p], acc);
       }
     } else {
       for (int s = 0; s < nsteps; ++s) {
         const h16x8 b = ld((size_t)s);
-        const h16x8 a = live ? *(const h16x8*)(arow + s * 32) : zero;
+        const h16x8 a = *(const h16x8*)(arow + s * 32);
         acc = mfma_f16(a, b, acc);
       }
     }

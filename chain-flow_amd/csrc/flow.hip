@@ -301,16 +301,16 @@ __global__ void __launch_bounds__(WV * 64) k_stream(SArgs a) {
   h16* As = lds;
   sg.place(a, ex, kc, KC, As, lda);
   const int row = lane & 15, kg = lane >> 4;
-  const bool live = row < ex.S;
-  const h16* arow = As + (live ? row : 0) * lda + kg * 8;
-  const h16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+  // lanes of padding rows (row >= S) read row 0: their products land only in output rows that
+  // are never stored, so no zeroing is needed
+  const h16* arow = As + (row < ex.S ? row : 0) * lda + kg * 8;
   const int col = lane & 15, rbase = 4 * (lane >> 4);
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   // the next fragment to multiply is k-step cs of the wave's tile ct; the tile is stored after its
   // last k-step
   int cs = 0, ct = 0;
   auto step = [&](h16x8 bf) {
-    const h16x8 av = live ? *(const h16x8*)(arow + cs * 32) : zero;
+    const h16x8 av = *(const h16x8*)(arow + cs * 32);
     acc = mfma_f16(av, bf, acc);
     if (cs == nsteps - 1) {
       const int n = (t0 + ct) * 16 + col;

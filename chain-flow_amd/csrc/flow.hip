@@ -45,6 +45,7 @@ namespace {
 constexpr int SWMAX = 16;         // max waves per streaming workgroup
 constexpr int PF_FULL = 16;       // fragment loads in flight per wave: full-K kernels
 constexpr int PF_SPLIT = 8;       //                                   split-K kernels
+constexpr int STREAM_SYNC = 4;    // fragment groups between workgroup barriers in the stream (measured: 4 best of 0-4)
 
 enum SrcKind { S_BUF = 0, S_SELF = 1, S_CROSS = 2 };
 enum EpiKind { E_PART = 0, E_BIAS16 = 1, E_GELU16 = 2 };
@@ -64,6 +65,7 @@ struct SArgs {
   SEx ex[4];
   int nex, N, K, ks, wpb, tpw, wg_per_kc;
   int d, hd, ks_in, Ck;
+  int sync;            // fragment groups between workgroup barriers in the stream (0: none)
 };
 
 // Attention of head h for the S rows of one expert from q, k, v already in LDS (sq [S][hd], sk and
@@ -341,11 +343,21 @@ __global__ void __launch_bounds__(WV * 64) k_stream(SArgs a) {
   // A conditional refill would make the wait before every multiply cover all loads in flight, and
   // a separate drain after the loop makes the compiler copy the ring between registers at the
   // loop entry, which waits for the whole prefetch (both measured in the generated code).
+  // Every a.sync groups the waves of the workgroup meet at a barrier (no memory fence: the rings
+  // stay in flight).  Left alone, the oldest wave on each SIMD wins the issue arbitration and
+  // finishes far ahead of the youngest (measured: 16-wave workgroups end spread over 35 us of a
+  // 95 us stream), and the last third of the stream then runs with a fraction of the loads in
+  // flight; in step, all waves finish together.
+  int g = 0;
   for (int f0 = 0; f0 < nf; f0 += SPF) {
 #pragma unroll
     for (int p = 0; p < SPF; ++p) {
       if (f0 + p < nf) step(buf[p]);
       buf[p] = issue();
+    }
+    if (++g == a.sync) {
+      g = 0;
+      __builtin_amdgcn_s_barrier();
     }
   }
 }
@@ -410,7 +422,9 @@ int stream_check(int SRC, const SArgs& a, int S_max) {
 }
 
 template <int SRC, int EPI>
-int launch_stream(const SArgs& a, int S_max, hipStream_t st) {
+int launch_stream(const SArgs& a0, int S_max, hipStream_t st) {
+  SArgs a = a0;
+  a.sync = STREAM_SYNC;
   if (stream_check(SRC, a, S_max)) return CFH_E_UNSUPPORTED;
   const size_t lds = stream_lds(SRC, S_max, a.K / a.ks, a.hd, a.Ck);
   const int need = stage_need(SRC, a, S_max);

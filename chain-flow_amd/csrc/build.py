@@ -41,12 +41,26 @@ def sources():
 
 def compile_one(src: Path) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [hipcc(), *HIPFLAGS, "-c", str(src), "-o", str(obj)]
+    # the resource-usage remarks name every kernel that spills registers to scratch memory
+    cmd = [hipcc(), *HIPFLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{r.stdout}\n{r.stderr}")
     noise = "is not a recognized feature for this target"
-    warn = "\n".join(line for line in r.stderr.splitlines() if noise not in line and line.strip())
+    lines = r.stderr.splitlines()
+    spills, name = [], None
+    for line in lines:
+        if "remark: Function Name:" in line:
+            name = line.split("Function Name:")[1].split("[")[0].strip()
+        elif "remark:" in line and "ScratchSize [bytes/lane]:" in line:
+            n = int(line.split("ScratchSize [bytes/lane]:")[1].split("[")[0])
+            if n > 0 and name:
+                spills.append(f"{name} ({n} B/lane)")
+    if spills:
+        print(f"{src.name}: {len(spills)} kernel(s) use scratch (register spills): " + "; ".join(spills[:6]),
+              file=sys.stderr)
+    warn = "\n".join(line for line in lines if noise not in line and "remark:" not in line and line.strip()
+                     and not line.lstrip().startswith(("|", "^")) and "kernel-resource-usage" not in line)
     if warn.strip():
         print(warn, file=sys.stderr)
     return obj

@@ -33,32 +33,48 @@ __device__ __forceinline__ float gelu_erf(float x) {
 
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+// Cross-lane steps by DPP (a VALU operand modifier, a few cycles) rather than __shfl_xor, which
+// lowers to ds_bpermute through the LDS unit (~100+ cycles per step, measured to dominate the
+// per-head attention staged by the flow's out-projection kernels).
+//   XOR1 / XOR2   quad_perm [1,0,3,2] / [2,3,0,1]   lane ^ 1 / lane ^ 2
+//   HMIRROR       row_half_mirror                   lane 7 - i within each 8 lanes
+//   MIRROR        row_mirror                        lane 15 - i within each 16 lanes
+// After XOR1, XOR2, HMIRROR, MIRROR with a commutative, associative combine, every lane of a
+// 16-lane row holds the row's result; the four rows are then combined through readlane.
+enum DppCtrl { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HMIRROR = 0x141, DPP_MIRROR = 0x140 };
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i32(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float readlane_f32(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+// Sum over the 16 lanes of each row, in every lane of the row.
+__device__ __forceinline__ float row_sum(float v) {
+  v += dpp_f32<DPP_XOR1>(v);
+  v += dpp_f32<DPP_XOR2>(v);
+  v += dpp_f32<DPP_HMIRROR>(v);
+  v += dpp_f32<DPP_MIRROR>(v);
   return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {   // every lane receives the total
+  v = row_sum(v);
+  return (readlane_f32(v, 0) + readlane_f32(v, 16)) + (readlane_f32(v, 32) + readlane_f32(v, 48));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
-}
-
-// Agent-scope release/acquire around the "last arriver" counters used for split-K fixups and
-// per-head attention.  All lanes execute the fences; lane 0 performs the RMW.
-__device__ __forceinline__ unsigned arrive_count(unsigned* ctr) {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  unsigned old = 0;
-  if ((threadIdx.x & 63) == 0) old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  old = __shfl(old, 0);
-  return old;
-}
-
-__device__ __forceinline__ void acquire_fence() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
-
-__device__ __forceinline__ void reset_count(unsigned* ctr) {
-  if ((threadIdx.x & 63) == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  v = fmaxf(v, dpp_f32<DPP_XOR1>(v));
+  v = fmaxf(v, dpp_f32<DPP_XOR2>(v));
+  v = fmaxf(v, dpp_f32<DPP_HMIRROR>(v));
+  v = fmaxf(v, dpp_f32<DPP_MIRROR>(v));
+  return fmaxf(fmaxf(readlane_f32(v, 0), readlane_f32(v, 16)), fmaxf(readlane_f32(v, 32), readlane_f32(v, 48)));
 }
 
 // Packed index (in h16x8 units) of the B fragment for (tile, kstep) of a layer with K inputs.

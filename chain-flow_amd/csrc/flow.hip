@@ -69,49 +69,55 @@ struct SArgs {
 };
 
 // Attention of head h for the S rows of one expert from q, k, v already in LDS (sq [S][hd], sk and
-// sv [Sk][hd]), written as fp16 into As [S][lda].  Causal mask = triu(-inf, 1)
+// sv [Sk][hd], Sk <= 16), written as fp16 into As [S][lda].  Causal mask = triu(-inf, 1)
 // (cf/drafters/chunked_flow.py:273-275); scores and the weighted sum in fp32 on fp16 q/k/v, output
 // rounded to fp16.
+// One wave per query row: lane group j (LP lanes) holds key j, so the dot products, the row max,
+// exp and sum stay in registers (DPP reductions); every LDS read of a phase is issued before the
+// first is used.  (A wave per (i, j) pair with a serial softmax thread per row spent 2-4 us here,
+// almost all of it in dependent LDS round trips.)
 __device__ void attend(int S, int Sk, int hd, bool causal, const h16* sq, const h16* sk, const h16* sv,
                        float* P, h16* As, int lda) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
   const float scale = 1.0f / sqrtf((float)hd);
-  for (int pr = wave; pr < S * Sk; pr += nw) {
-    const int i = pr / Sk, j = pr - i * Sk;
+  const bool l8 = Sk <= 8;                 // 8 lanes per key (else 4)
+  const int j = l8 ? lane >> 3 : lane >> 2, sub = l8 ? lane & 7 : lane & 3;
+  const int step = l8 ? 64 : 32;           // halves between a lane's 8-half chunks
+  const int jr = min(j, Sk - 1);           // lanes of keys >= Sk read a valid row, result masked
+  for (int i = wave; i < S; i += nw) {
+    const h16* qr = sq + i * hd + sub * 8;
+    const h16* kr = sk + jr * hd + sub * 8;
     float part = 0.f;
-    for (int c = lane * 8; c < hd; c += 512) {
-      const h16x8 qa = *(const h16x8*)(sq + i * hd + c);
-      const h16x8 kb = *(const h16x8*)(sk + j * hd + c);
+    for (int c = 0; c < hd; c += step) {
+      const h16x8 qa = *(const h16x8*)(qr + c);
+      const h16x8 kb = *(const h16x8*)(kr + c);
 #pragma unroll
       for (int t = 0; t < 8; ++t) part += (float)qa[t] * (float)kb[t];
     }
-    const float sc = wave_sum(part) * scale;
-    if (lane == 0) P[i * Sk + j] = (causal && j > i) ? -INFINITY : sc;
-  }
-  lds_barrier();
-  if ((int)threadIdx.x < S) {
-    const int i = threadIdx.x;
-    float m = -INFINITY;
-    for (int j = 0; j < Sk; ++j) m = fmaxf(m, P[i * Sk + j]);
-    float den = 0.f;
-    for (int j = 0; j < Sk; ++j) {
-      const float ex2 = expf(P[i * Sk + j] - m);
-      P[i * Sk + j] = ex2;
-      den += ex2;
-    }
-    const float inv = 1.0f / den;
-    for (int j = 0; j < Sk; ++j) P[i * Sk + j] *= inv;
+    part += dpp_f32<DPP_XOR1>(part);
+    part += dpp_f32<DPP_XOR2>(part);
+    if (l8) part += dpp_f32<DPP_HMIRROR>(part);
+    const bool valid = j < Sk && !(causal && j > i);
+    const float sc = valid ? part * scale : -INFINITY;
+    const float m = wave_max(sc);
+    const float e = valid ? expf(sc - m) : 0.f;
+    const float inv = 1.0f / wave_sum(sub == 0 ? e : 0.f);
+    if (sub == 0 && j < Sk) P[i * Sk + j] = e * inv;
   }
   lds_barrier();
   const int nv = hd / 8;
   for (int idx = threadIdx.x; idx < S * nv; idx += blockDim.x) {
     const int i = idx / nv, c = (idx - i * nv) * 8;
     float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int j = 0; j < Sk; ++j) {
-      const float p = P[i * Sk + j];
-      const h16x8 vb = *(const h16x8*)(sv + j * hd + c);
+    for (int j0 = 0; j0 < Sk; j0 += 8) {   // 8 keys at a time; keys past Sk: a valid row, weight 0
 #pragma unroll
-      for (int t = 0; t < 8; ++t) o[t] += p * (float)vb[t];
+      for (int jj = 0; jj < 8; ++jj) {
+        const int jc = min(j0 + jj, Sk - 1);
+        const float p = j0 + jj < Sk ? P[i * Sk + jc] : 0.f;
+        const h16x8 vb = *(const h16x8*)(sv + jc * hd + c);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) o[t] += p * (float)vb[t];
+      }
     }
     h16x8 ov;
 #pragma unroll
@@ -415,6 +421,7 @@ int stage_slots(int wpb) { return wpb > 8 ? 8 : 16; }
 
 int stream_check(int SRC, const SArgs& a, int S_max) {
   if (a.ks <= 0 || a.wpb <= 0 || a.tpw <= 0 || a.N % 16 || a.K % a.ks || (a.K / a.ks) % 32) return CFH_E_UNSUPPORTED;
+  if (SRC != S_BUF && ((SRC == S_SELF ? S_max : a.Ck) > 16 || a.hd % 64)) return CFH_E_UNSUPPORTED;
   if ((a.N / 16) % (a.wpb * a.tpw) || a.wpb > SWMAX || stage_need(SRC, a, S_max) > stage_slots(a.wpb) ||
       stream_lds(SRC, S_max, a.K / a.ks, a.hd, a.Ck) > 150 * 1024)
     return CFH_E_UNSUPPORTED;
@@ -441,8 +448,11 @@ int launch_stream(const SArgs& a0, int S_max, hipStream_t st) {
 // row) of d / (4 NQ) threads, NQ float4 column groups each; the partial rows are loaded RB(NQ) at a
 // time with every load of a batch in flight together.
 constexpr int RQ = 16;            // max float4 groups per thread (d <= 16384)
-// partial rows loaded per batch: 16 float4 loads per thread in flight, at least 2 rows
-constexpr int rb_for(int nq) { return nq <= 2 ? 8 : nq <= 4 ? 4 : 2; }
+// partial rows loaded per batch: as many as fit the registers of a launch bound of mt threads
+// (mt 768: 168 VGPRs, mt 1024: 128)
+constexpr int rb_for(int nq, int mt) {
+  return mt <= 768 ? (nq <= 2 ? 8 : nq <= 4 ? 4 : nq <= 8 ? 2 : 1) : (nq <= 1 ? 8 : nq <= 2 ? 4 : nq <= 4 ? 2 : 1);
+}
 
 // NQ for a row of d columns: the smallest group count giving a whole number of waves and at most
 // 1024 threads (0 if none), so the row's loads spread over as many lanes as possible.
@@ -475,7 +485,7 @@ __device__ __forceinline__ float block_sum_rt(float v, float* red) {  // red[blo
   return t;
 }
 
-template <int NQ>
+template <int NQ, int MT>
 __device__ void res_row(const ResArgs& a, int e, int r) {
   __shared__ float red[16];
   const int RT = blockDim.x;
@@ -496,7 +506,7 @@ __device__ void res_row(const ResArgs& a, int e, int r) {
     gq[k] = *(const h16x4*)(a.g[e] + q * 4);
     btq[k] = *(const h16x4*)(a.b[e] + q * 4);
   }
-  constexpr int RB = rb_for(NQ);
+  constexpr int RB = rb_for(NQ, MT);
   for (int kc = 1; kc < a.ks; kc += RB) {
     float4 t[RB][NQ];
 #pragma unroll
@@ -548,11 +558,13 @@ __device__ void res_row(const ResArgs& a, int e, int r) {
   }
 }
 
-template <int NQ>
-__global__ void __launch_bounds__(1024) k_res(ResArgs a) {
+// MT = the launch bound: 768 threads (12 waves, up to 168 VGPRs) when the row fits, else 1024
+// (128 VGPRs); the all-loads-up-front row needs more than 128 at NQ = 2.
+template <int NQ, int MT>
+__global__ void __launch_bounds__(MT) k_res(ResArgs a) {
   int e = 0, r = blockIdx.x;
   while (e + 1 < a.nex && r >= a.rows[e]) r -= a.rows[e++];
-  res_row<NQ>(a, e, r);
+  res_row<NQ, MT>(a, e, r);
 }
 
 int launch_res(const ResArgs& a, hipStream_t st) {
@@ -560,9 +572,13 @@ int launch_res(const ResArgs& a, hipStream_t st) {
   for (int e = 0; e < a.nex; ++e) total += a.rows[e];
   const int NQ = res_nq(a.d);
   const int threads = NQ ? a.d / 4 / NQ : 0;
+  const bool small = threads <= 768;
   switch (NQ) {
 #define CFH_RES(N) \
-  case N: hipLaunchKernelGGL(k_res<N>, dim3(total), dim3(threads), 0, st, a); break;
+  case N:                                                                             \
+    if (small) hipLaunchKernelGGL((k_res<N, 768>), dim3(total), dim3(threads), 0, st, a); \
+    else hipLaunchKernelGGL((k_res<N, 1024>), dim3(total), dim3(threads), 0, st, a);      \
+    break;
     CFH_RES(1) CFH_RES(2) CFH_RES(3) CFH_RES(4) CFH_RES(5) CFH_RES(6) CFH_RES(7) CFH_RES(8)
     CFH_RES(9) CFH_RES(10) CFH_RES(11) CFH_RES(12) CFH_RES(13) CFH_RES(14) CFH_RES(15) CFH_RES(16)
 #undef CFH_RES

@@ -33,14 +33,33 @@ __device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
   return va > vb || (va == vb && ia < ib);
 }
 
-// Arg-best of (v, i) over the lanes of an aligned group of W lanes (W a power of two <= 64).
+// Arg-best of (v, i) over the lanes of an aligned group of W lanes (W = 16 or 64), in every lane
+// of the group.  `better` is a total order, so the result does not depend on the pairing.
+template <int CTRL>
+__device__ __forceinline__ void best_step(float& v, int& i) {
+  const float ov = dpp_f32<CTRL>(v);
+  const int oi = dpp_i32<CTRL>(i);
+  if (better(ov, oi, v, i)) { v = ov; i = oi; }
+}
+
 template <int W>
 __device__ __forceinline__ void group_best(float& v, int& i) {
+  static_assert(W == 16 || W == 64, "group_best: 16 or 64 lanes");
+  best_step<DPP_XOR1>(v, i);
+  best_step<DPP_XOR2>(v, i);
+  best_step<DPP_HMIRROR>(v, i);
+  best_step<DPP_MIRROR>(v, i);
+  if constexpr (W == 64) {
+    float bv = readlane_f32(v, 0);
+    int bi = __builtin_amdgcn_readlane(i, 0);
 #pragma unroll
-  for (int o = W / 2; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(v, o);
-    const int oi = __shfl_xor(i, o);
-    if (better(ov, oi, v, i)) { v = ov; i = oi; }
+    for (int r = 16; r < 64; r += 16) {
+      const float rv = readlane_f32(v, r);
+      const int ri = __builtin_amdgcn_readlane(i, r);
+      if (better(rv, ri, bv, bi)) { bv = rv; bi = ri; }
+    }
+    v = bv;
+    i = bi;
   }
 }
 
@@ -488,15 +507,16 @@ __global__ void __launch_bounds__(GW * 64) k_head_gemm(GemmArgs a) {
         ix[t] = ok ? j : INT_MAX;
         mx = fmaxf(mx, v[t]);
       }
-#pragma unroll
-      for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+      mx = fmaxf(mx, dpp_f32<DPP_XOR1>(mx));
+      mx = fmaxf(mx, dpp_f32<DPP_XOR2>(mx));
+      mx = fmaxf(mx, dpp_f32<DPP_HMIRROR>(mx));
+      mx = fmaxf(mx, dpp_f32<DPP_MIRROR>(mx));
       float se = 0.f;
       if (mx != -INFINITY) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) se += expf(v[t] - mx);
       }
-#pragma unroll
-      for (int o = 8; o > 0; o >>= 1) se += __shfl_xor(se, o);
+      se = row_sum(se);
       if (r < a.M && col == 0) {
         ws2[((size_t)wave * ROWS + r) * 2] = mx;
         ws2[((size_t)wave * ROWS + r) * 2 + 1] = se;
@@ -705,12 +725,7 @@ __global__ void __launch_bounds__(64) k_beam_step(BeamArgs a) {
   for (int r = 0; r < k; ++r) {
     float bv = cv;
     int bi = ci;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o);
-      const int oi = __shfl_xor(bi, o);
-      if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-    }
+    group_best<64>(bv, bi);
     if (ci == bi) { cv = -INFINITY; ci = INT_MAX; }
     if (lane == 0) { win_val[r] = bv; win_flat[r] = bi; }
   }

@@ -48,6 +48,8 @@ SIGNATURES = {
     "cfh_beam_tree_step": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _I, _VP]),
     "cfh_beam_backtrack": (_I, [_VP, _VP, _VP, _I, _I, _I, _VP, _VP]),
     "cfh_gdn_tree": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _VP, _VP, _VP]),
+    "cfh_gdn_tree_vllm": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _I, _VP, _VP, _I, _I, _I, _I, _I, _I, _I,
+                               C.c_float, _VP, _VP]),
 }
 
 

@@ -43,3 +43,44 @@ def tree_gated_delta_scan(q, k, v, g, beta, parent, S0, *, use_qk_l2norm: bool =
                                        int(l2mode), out.data_ptr(), _lib.ptr(states), _lib.stream_handle()),
                "cfh_gdn_tree")
     return out, states
+
+
+def tree_gdn_vllm(mixed_qkv, a, b, A_log, dt_bias, ssm_state, node_slots, parent, *, num_q_heads: int,
+                  prefix_slot: int = 1, scale: float | None = None, use_qk_l2norm: bool = True):
+    """The serving form of the tree GDN (``tree_scan_gdn_recurrence_path``,
+    ``cf/vllm_tree/tree_ssm.py:256-351``; bit-identical by construction to the per-node slot form
+    ``:34-96``): one launch of ``cfh_gdn_tree_vllm``.
+
+    mixed_qkv [N, 2 H K + HV V] bf16 (q heads | k heads | value heads), a, b [N, HV] bf16, A_log,
+    dt_bias [HV], ssm_state [slots, HV, V, K] bf16 or fp32 (updated in place: node n's state goes to
+    slot node_slots[n]; every node starts from slot ``prefix_slot``), parent [N] (BFS, -1 = root).
+    -> o [N, HV, V] bf16."""
+    N, conv = mixed_qkv.shape
+    _, HV, V, K = ssm_state.shape
+    H = int(num_q_heads)
+    if conv != 2 * H * K + HV * V:
+        raise ValueError(f"mixed_qkv width {conv} != 2*{H}*{K} + {HV}*{V}")
+    if mixed_qkv.dtype != torch.bfloat16 or a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+        raise ValueError("mixed_qkv, a, b must be bf16")
+    if ssm_state.dtype not in (torch.bfloat16, torch.float32) or not ssm_state.is_contiguous():
+        raise ValueError("ssm_state must be a contiguous bf16 or fp32 [slots, HV, V, K] tensor")
+    if a.shape != (N, HV) or b.shape != (N, HV):
+        raise ValueError("a, b must be [N, HV]")
+    dev = mixed_qkv.device
+    slots = node_slots.to(dev, torch.int32).contiguous()
+    nslots = ssm_state.shape[0]
+    if int(slots.min()) < 0 or int(slots.max()) >= nslots or not 0 <= prefix_slot < nslots:
+        raise ValueError("slot index out of range of ssm_state")
+    if len(set(slots.tolist())) != N or prefix_slot in set(slots.tolist()):
+        raise ValueError("node slots must be distinct from each other and from the prefix slot")
+    x, a, b = mixed_qkv.contiguous(), a.contiguous(), b.contiguous()
+    A_log = A_log.to(dev, torch.float32).contiguous()
+    dt_bias = dt_bias.to(dev, torch.float32).contiguous()
+    parent = parent.to(dev, torch.int32).contiguous()
+    out = torch.empty(N, HV, V, dtype=torch.bfloat16, device=dev)
+    _lib.check(_lib.lib().cfh_gdn_tree_vllm(
+        x.data_ptr(), a.data_ptr(), b.data_ptr(), A_log.data_ptr(), dt_bias.data_ptr(), ssm_state.data_ptr(),
+        int(ssm_state.dtype == torch.bfloat16), slots.data_ptr(), parent.data_ptr(), int(prefix_slot), N, H, HV,
+        K, V, int(bool(use_qk_l2norm)), float(K ** -0.5 if scale is None else scale), out.data_ptr(),
+        _lib.stream_handle()), "cfh_gdn_tree_vllm")
+    return out

@@ -10,6 +10,7 @@ from __future__ import annotations
 import argparse
 import concurrent.futures as cf
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -59,8 +60,10 @@ def compile_one(src: Path) -> Path:
     if spills:
         print(f"{src.name}: {len(spills)} kernel(s) use scratch (register spills): " + "; ".join(spills[:6]),
               file=sys.stderr)
+    # drop the remarks and the source-context lines that follow them
+    ctx = re.compile(r"^\s*(\d+\s*)?[|^]|^In file included from")
     warn = "\n".join(line for line in lines if noise not in line and "remark:" not in line and line.strip()
-                     and not line.lstrip().startswith(("|", "^")) and "kernel-resource-usage" not in line)
+                     and not ctx.match(line) and "kernel-resource-usage" not in line)
     if warn.strip():
         print(warn, file=sys.stderr)
     return obj

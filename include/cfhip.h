@@ -186,6 +186,23 @@ int cfh_gdn_tree(const void* q, const void* k, const void* v, const float* g, co
                  const float* S0, const int32_t* parent, int N, int H, int Dk, int Dv,
                  int use_l2norm, int l2mode, float* out, float* states, void* stream);
 
+/* The serving (vLLM) form of the tree GDN (cf/vllm_tree/tree_ssm.py:256-311, path-parallel;
+ * bit-identical by construction to the per-node slot form :34-77 that stores each node's state and
+ * has its children read it back):
+ *   mixed_qkv [N][2 H K + HV V] bf16 (q heads | k heads | HV value heads; value head hv uses q/k
+ *   head hv / (HV / H)); a, b [N][HV] bf16; A_log, dt_bias [HV] fp32;
+ *   g = -exp(A_log) softplus(a + dt_bias) (softplus = identity above 20), beta = bf16(sigmoid(b));
+ *   q, k l2-normalised as x / sqrt(|x|^2 + 1e-6) (use_l2norm), q scaled by `scale`;
+ *   ssm_state [slots][HV][V][K], bf16 (state_bf16 = 1) or fp32: every node starts from slot
+ *   prefix_slot, replays its root->node path with each ancestor's state rounded to the storage
+ *   type, writes its state to slot node_slots[n] and o [N][HV][V] bf16.
+ * parent [N] int32 (BFS order, -1 = root).  K == 128, V % 64 == 0, N <= 256; node slots must be
+ * distinct from each other and from prefix_slot.  Replaces tree_scan_gdn_recurrence[_path]. */
+int cfh_gdn_tree_vllm(const void* mixed_qkv, const void* a, const void* b, const float* A_log,
+                      const float* dt_bias, void* ssm_state, int state_bf16, const int32_t* node_slots,
+                      const int32_t* parent, int prefix_slot, int N, int H, int HV, int K, int V,
+                      int use_l2norm, float scale, void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -95,3 +95,76 @@ def test_gdn_refuses_non_bfs_order(cuda):
     o = to64(out)
     assert np.isnan(o[2]).all()
     assert np.isfinite(o[[0, 1, 3]]).all()
+
+
+# ---------------------------------------------------------------- serving (vLLM) form, row a18
+def _vllm_inputs(N, H, HV, K, V, seed, state_dtype):
+    g = torch.Generator().manual_seed(seed)
+    X = torch.randn(N, 2 * H * K + HV * V, generator=g).to(torch.bfloat16)
+    a = torch.randn(N, HV, generator=g).to(torch.bfloat16)
+    b = torch.randn(N, HV, generator=g).to(torch.bfloat16)
+    A_log = torch.randn(HV, generator=g) * 0.5
+    dt_bias = torch.randn(HV, generator=g) * 0.5
+    st = torch.zeros(N + 3, HV, V, K)
+    st[1] = torch.randn(HV, V, K, generator=g) * 0.1
+    st[N + 2] = 7.0                                  # a slot nobody may touch
+    return X, a, b, A_log, dt_bias, st.to(state_dtype)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("H,HV,state_dtype", [(16, 16, torch.bfloat16), (16, 16, torch.float32),
+                                              (4, 16, torch.bfloat16)])
+def test_gdn_vllm_form_matches_oracle(cuda, H, HV, state_dtype):
+    """cfh_gdn_tree_vllm on the C5 beam tree (31 nodes, 16 value heads, K = V = 128) against the
+    float32 slot-form oracle: fp32 states within 1e-5 norm-relative; bf16 states within 5e-4 (a
+    storage rounding can land on the other side of a tie when the sums run in another order)."""
+    from chain_flow_amd.gdn import tree_gdn_vllm
+    parent = beam_tree_parents()
+    N, K, V = len(parent), 128, 128
+    X, a, b, A_log, dt_bias, st = _vllm_inputs(N, H, HV, K, V, 11, state_dtype)
+    slots = torch.arange(2, N + 2, dtype=torch.int32)
+    st_d = st.to(cuda)
+    o = tree_gdn_vllm(X.to(cuda), a.to(cuda), b.to(cuda), A_log, dt_bias, st_d, slots, torch.tensor(parent),
+                      num_q_heads=H, prefix_slot=1)
+    torch.cuda.synchronize()
+    bf = state_dtype == torch.bfloat16
+    ro, rs = ogdn.tree_gdn_vllm(X.float().numpy(), a.float().numpy(), b.float().numpy(), A_log.numpy(),
+                                dt_bias.numpy(), st.float().numpy(), slots.numpy(), parent, 1, H, HV, K, V,
+                                K ** -0.5, state_bf16=bf, form="slots")
+    got_o = o.float().cpu().numpy()
+    got_s = st_d.float().cpu().numpy()
+    eo = rel_err(got_o, ogdn._round_bf16(ro))
+    es = rel_err(got_s, rs)
+    print(f"[gdn vllm H={H} HV={HV} {state_dtype}] out err {eo:.2e} state err {es:.2e}", flush=True)
+    # bf16 slots: storing the states in bf16 instead of fp32 moves them by ~2e-3 on this tree, so
+    # 5e-4 also catches a kernel that skipped the storage rounding of an ancestor's state
+    assert es < (5e-4 if bf else 1e-5)
+    assert eo < 2e-3                             # output rounded to bf16 on both sides
+    assert np.array_equal(got_s[N + 2], st[N + 2].float().numpy())   # untouched slot
+    assert np.array_equal(got_s[1], st[1].float().numpy())           # the prefix slot is only read
+
+
+@pytest.mark.gpu
+def test_gdn_vllm_fp32_states_equal_research_kernel(cuda):
+    """With fp32 slots and one q/k head per value head the serving kernel is the research kernel
+    (cfh_gdn_tree, l2mode sqrt-eps) fed the same gates: same per-path recurrence."""
+    from chain_flow_amd.gdn import tree_gdn_vllm
+    parent = beam_tree_parents()
+    N, H, K, V = len(parent), 16, 128, 128
+    X, a, b, A_log, dt_bias, st = _vllm_inputs(N, H, H, K, V, 12, torch.float32)
+    slots = torch.arange(2, N + 2, dtype=torch.int32)
+    st_d = st.to(cuda)
+    o = tree_gdn_vllm(X.to(cuda), a.to(cuda), b.to(cuda), A_log, dt_bias, st_d, slots, torch.tensor(parent),
+                      num_q_heads=H)
+    g, beta = ogdn.vllm_gates_f32(a.float().numpy(), b.float().numpy(), A_log.numpy(), dt_bias.numpy())
+    q = X[:, :H * K].reshape(N, H, K)
+    k = X[:, H * K:2 * H * K].reshape(N, H, K)
+    v = X[:, 2 * H * K:].reshape(N, H, V)
+    S0 = st[1].transpose(1, 2).contiguous()
+    out, states = tree_gated_delta_scan(q.to(cuda), k.to(cuda), v.to(cuda), torch.from_numpy(g),
+                                        torch.from_numpy(beta), torch.tensor(parent), S0, l2mode=L2_SQRT_EPS)
+    torch.cuda.synchronize()
+    ref_o = out.to(torch.bfloat16).float()
+    assert rel_err(o.float().cpu().numpy(), ref_o.cpu().numpy()) < 4e-3
+    got = st_d[2:N + 2].transpose(2, 3).cpu().numpy()
+    assert rel_err(got, states.cpu().numpy()) < 1e-6

@@ -59,3 +59,23 @@ def test_flow_is_bit_reproducible(cuda):
     b = ff.predict_hidden(ctx).clone()
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+@pytest.mark.gpu
+def test_flow_full_width_matches_oracle(cuda):
+    """The benchmark's width (d = 5120: head_dim 640, ffn 30720, the 16-wave and one-round grids,
+    the deep operand staging) against the oracle: one block, two Euler steps."""
+    d = 5120
+    cfg = flownet(d, layers=1, flow_steps=2)
+    print(f"[flow parity] d={d} L=1 E=2 (full width)", flush=True)
+    W = _flow_weights(cfg, seed=7)
+    ctx = synthetic_context(1, cfg.context_size, d, seed=3)
+    ff = FusedFlow(cfg, {k: v.to(cuda) for k, v in W.items()}, device=cuda)
+    z = ff.predict_hidden(ctx.to(cuda))
+    torch.cuda.synchronize()
+    del ff
+    ref = oflow.predict_hidden(weights64(W), to64(ctx), _ocfg(cfg), numerics="fp16")
+    err = rel_err(to64(z), ref)
+    print(f"  rel err {err:.3e}", flush=True)
+    assert np.isfinite(to64(z)).all()
+    assert err < TOL_FP16

@@ -253,3 +253,46 @@ def test_packed_head_equals_in_place(cuda, M, k, markov, n):
     print(f"[packed head M={M} k={k} markov={markov} n={n}]", flush=True)
     for a, b in zip(out[0], out[1]):
         assert torch.equal(a, b)
+
+
+@pytest.mark.gpu
+def test_packed_head_full_width_matches_oracle(cuda):
+    """The benchmark's head shape: 62,642 shortlist rows x d = 5120 with the rank-256 markov bias,
+    4 beam rows, top-8, through the packed image.  Logits within 2 fp16 ulp of the oracle; top-8
+    ids equal to the oracle's wherever the oracle's adjacent margins exceed 1e-3."""
+    d, V, n, M, k = 5120, 70000, 62642, 4, 8
+    cfg = flownet(d, layers=1, flow_steps=1)
+    names = {x for x in param_specs(cfg, V) if x.startswith(("markov.", "lm_head"))}
+    W = make_weights(cfg, V, init="test", base_seed=3, names=names)
+    W["lm_head.weight"] = (W["lm_head.weight"].float() * 8.0).half()
+    sl = _shortlist(V, n, seed=5)
+    g = torch.Generator().manual_seed(13)
+    h = torch.randn(M, d, generator=g).half()
+    prev = torch.randint(0, V, (M,), generator=g, dtype=torch.int32)
+    print(f"[head parity] n={n} d={d} M={M} k={k} (full width, packed)", flush=True)
+    head = ShortlistHead(W["lm_head.weight"].to(cuda), sl.to(cuda), W["markov.w1.weight"].to(cuda),
+                         W["markov.w2.weight"].to(cuda))
+    logits = torch.empty(M, n, dtype=torch.float16, device=cuda)
+    vals, ids, lse = head.topk(h.to(cuda), k, prev=prev.to(cuda), logits=logits)
+    torch.cuda.synchronize()
+    got = to64(logits)
+    gid = ids.cpu().numpy()
+    del head, logits
+    sl64 = sl.long().numpy()
+    hw = ohead.head_logits(to64(h), to64(W["lm_head.weight"][sl64]))
+    mb = ohead.markov_bias(to64(W["markov.w1.weight"]), to64(W["markov.w2.weight"][sl64]), prev.long().numpy())
+    ref = ohead.r16(hw + mb, "fp16")
+    diff = np.abs(got - ref)
+    print(f"  max logit diff {diff.max():.3e}, fraction differing {(diff > 0).mean():.4f}", flush=True)
+    # each fp16 rounding point (h.W, A.W2 and their sum) may land one ulp apart when the fp32
+    # accumulation order differs: the bound is one ulp of each, at its own magnitude
+    assert (diff <= _ulp16(hw) + _ulp16(mb) + _ulp16(ref) + 1e-12).all()
+    assert (diff > 0).mean() < 0.01
+    order = np.argsort(-ref, axis=1, kind="stable")[:, :k + 1]
+    for m in range(M):
+        rv = ref[m, order[m]]
+        for r in range(k):
+            lo = rv[r] - rv[r + 1]
+            hi = np.inf if r == 0 else rv[r - 1] - rv[r]
+            if min(lo, hi) > MARGIN:
+                assert gid[m, r] == order[m, r], (m, r)

@@ -34,6 +34,9 @@ struct ExpertLayout {
 };
 
 bool flow_dims_ok(const cfh_flow_dims* d);
+// Heads per attention k-chunk: the fewest whole heads (1, 2 or 4, dividing H) whose columns make
+// a multiple of 32, the MFMA k-step; 0 if none (head widths must be multiples of 8).
+int heads_per_chunk(int hd, int H);
 ExpertLayout expert_layout(const cfh_flow_dims* d);
 
 }  // namespace cfh

@@ -14,10 +14,17 @@ int set_hip_error(hipError_t e) {
 }
 int last_hip_error() { return g_last_hip; }
 
+int heads_per_chunk(int hd, int H) {
+  if (hd <= 0 || hd % 8 || H <= 0) return 0;
+  for (int h : {1, 2, 4})
+    if ((h * hd) % 32 == 0 && H % h == 0) return h;
+  return 0;
+}
+
 bool flow_dims_ok(const cfh_flow_dims* d) {
   if (!d) return false;
-  if (d->d <= 0 || d->d % 512 != 0 || d->d > 16384) return false;
-  if (d->heads <= 0 || d->d % d->heads != 0 || (d->d / d->heads) % 64 != 0) return false;
+  if (d->d <= 0 || d->d % 64 != 0 || d->d > 16384) return false;
+  if (d->heads <= 0 || d->d % d->heads != 0 || !heads_per_chunk(d->d / d->heads, d->heads)) return false;
   if ((d->d / d->heads) > 1024) return false;
   if (d->ffn_mult < 1 || d->ffn_mult > 8) return false;
   if (d->layers < 1 || d->layers > 64) return false;

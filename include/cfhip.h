@@ -44,9 +44,11 @@ int cfh_pack_linear(const void* w, int n, int k, void* out, void* stream);
  * Shape of one TreeFlowDrafter flow: HiddenKVFlowExpert chunk experts
  * (cf/drafters/tree_flow.py:40-77, cf/drafters/chunked_flow.py:205-414). */
 typedef struct cfh_flow_dims {
-  int d;             /* hidden size (expert_dim == target hidden size); d % 512 == 0       */
+  int d;             /* expert_dim: the target hidden size, or the VAE latent size (640 /  */
+                     /* 1024) in the latent drafters; d % 64 == 0, d <= 16384             */
   int ffn_mult;      /* ffn multiplier (6)                                                 */
-  int heads;         /* attention heads (8); (d / heads) % 64 == 0                         */
+  int heads;         /* attention heads (8); head width d / heads a multiple of 8 (80 at  */
+                     /* d = 640: two heads share an MFMA k-chunk)                          */
   int layers;        /* HiddenKVFlowBlocks per expert (num_drafter_layers)                 */
   int ctx_rows;      /* context_size (8); 2 <= ctx_rows <= 16                              */
   int draft_length;  /* draft_length (8); <= 16                                            */
@@ -83,6 +85,50 @@ int cfh_flow_pack_expert(const cfh_flow_dims* dims, const void* const* raw, int 
  * (cf/cuda_block.py:407-431 / pybind `expert`, `cross_kv`, cf/csrc/fused_block.cu:793-862). */
 int cfh_flow_integrate(const cfh_flow_dims* dims, const void* const* experts, const void* ctx,
                        void* z_out, void* ws, int batch, void* stream);
+
+/* ---------------------------------------------------------------- hidden-state VAE
+ * TransformerHiddenVAE (cf/vae/transformer_hidden.py:9-79; config cf/vae/base.py:9-17): the frozen
+ * VAE the latent drafters run the flow inside (cf/drafters/tree_vae_flow.py:163-175).  Each half is
+ * input Linear + position embedding, `layers` pre-LN nn.TransformerEncoderLayers (bidirectional
+ * self-attention, GELU FFN of 4*inter, LayerNorm eps 1e-5), a final LayerNorm and an output
+ * Linear, in fp16 with the rounding points of torch's fp16 modules (fp16 residual stream). */
+typedef struct cfh_vae_dims {
+  int hidden;        /* target hidden size (encoder input, decoder output); % 64 == 0     */
+  int latent;        /* latent_size (640 / 1024); % 64 == 0                               */
+  int inter;         /* intermediate_size (1920): transformer width; % 64 == 0            */
+  int layers;        /* num_layers of each half (2)                                       */
+  int heads;         /* num_heads (8); 1 when inter % num_heads != 0, as the module does  */
+  int max_rows;      /* max_sequence_length (16): rows of the position tables             */
+} cfh_vae_dims;
+
+/* Bytes of the packed VAE image (-1 if `dims` is unsupported). */
+int64_t cfh_vae_bytes(const cfh_vae_dims* dims);
+
+/* Pack the VAE.  raw[] = device pointers to its fp16 parameters in state_dict order, logvar
+ * omitted (n_raw = 14 + 24*layers):
+ *   encoder_in.{weight,bias}, encoder_pos.weight, per encoder layer l:
+ *   encoder.layers.l.self_attn.in_proj_{weight,bias}, .self_attn.out_proj.{weight,bias},
+ *   .linear1.{weight,bias}, .linear2.{weight,bias}, .norm1.{weight,bias}, .norm2.{weight,bias},
+ *   then encoder_norm.{weight,bias}, mu.{weight,bias}, decoder_in.{weight,bias},
+ *   decoder_pos.weight, the decoder layers in the same order, decoder_norm.{weight,bias},
+ *   decoder_out.{weight,bias}.
+ * Replaces _load_frozen_vae's module build (cf/drafters/tree_vae_flow.py:50-87). */
+int cfh_vae_pack(const cfh_vae_dims* dims, const void* const* raw, int n_raw, void* packed, void* stream);
+
+/* 0 if this build runs `dims` on sequences of `rows` rows (rows <= 16 and <= max_rows), with the
+ * workspace size in *ws_bytes; CFH_E_UNSUPPORTED otherwise. */
+int cfh_vae_caps(const cfh_vae_dims* dims, int rows, int64_t* ws_bytes);
+
+/* encode_sequence(hidden).mu (cf/vae/transformer_hidden.py:52-59): hidden [batch][rows][hidden]
+ * fp16 -> mu [batch][rows][latent] fp16.  Replaces TreeVAEFlowDrafter._encode (tree_vae_flow.py:
+ * 163-165). */
+int cfh_vae_encode(const cfh_vae_dims* dims, const void* packed, const void* hidden, void* mu, int batch,
+                   int rows, void* ws, void* stream);
+
+/* decode_sequence(z) (cf/vae/transformer_hidden.py:61-68): z [batch][rows][latent] fp16 ->
+ * out [batch][rows][hidden] fp16.  Replaces TreeVAEFlowDrafter._decode (tree_vae_flow.py:167-169). */
+int cfh_vae_decode(const cfh_vae_dims* dims, const void* packed, const void* z, void* out, int batch,
+                   int rows, void* ws, void* stream);
 
 /* ---------------------------------------------------------------- shortlisted lm_head
  * logits[m][j] = fp16( fp16(h[m] . W[row_j]) + fp16(A[m] . W2[row_j]) ),  row_j = sl ? sl[j] : j

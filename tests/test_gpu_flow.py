@@ -79,3 +79,24 @@ def test_flow_full_width_matches_oracle(cuda):
     print(f"  rel err {err:.3e}", flush=True)
     assert np.isfinite(to64(z)).all()
     assert err < TOL_FP16
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("d,heads,layers,steps", [(640, 8, 2, 2), (640, 16, 1, 2), (768, 12, 1, 1), (1920, 8, 1, 1)])
+def test_flow_latent_widths_match_oracle(cuda, d, heads, layers, steps):
+    """Widths whose heads do not fill an MFMA k-step (head_dim 80 and 240: two heads per attention
+    k-chunk; 40: four) and rows that do not fill whole waves of the residual kernel (d = 640 and
+    1920: 160 and 480 four-column groups).  d = 640 with 8 heads is the latent width of the
+    shipped VAE drafters."""
+    cfg = flownet(d, layers=layers, flow_steps=steps, num_heads=heads)
+    W = _flow_weights(cfg, seed=11)
+    ctx = synthetic_context(1, cfg.context_size, d, seed=5)
+    print(f"[flow parity] d={d} H={heads} L={layers} E={steps}", flush=True)
+    ff = FusedFlow(cfg, {k: v.to(cuda) for k, v in W.items()}, device=cuda)
+    z = ff.predict_hidden(ctx.to(cuda))
+    torch.cuda.synchronize()
+    ref = oflow.predict_hidden(weights64(W), to64(ctx), _ocfg(cfg), numerics="fp16")
+    err = rel_err(to64(z), ref)
+    print(f"  rel err {err:.3e}", flush=True)
+    assert np.isfinite(to64(z)).all()
+    assert err < TOL_FP16

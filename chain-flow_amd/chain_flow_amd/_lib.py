@@ -20,6 +20,11 @@ class FlowDims(C.Structure):
                 ("flow_steps", C.c_int)]
 
 
+class VaeDims(C.Structure):
+    _fields_ = [("hidden", C.c_int), ("latent", C.c_int), ("inter", C.c_int), ("layers", C.c_int),
+                ("heads", C.c_int), ("max_rows", C.c_int)]
+
+
 _VP = C.c_void_p
 _I = C.c_int
 _I64 = C.c_int64
@@ -34,6 +39,11 @@ SIGNATURES = {
     "cfh_flow_expert_bytes": (_I64, [C.POINTER(FlowDims)]),
     "cfh_flow_pack_expert": (_I, [C.POINTER(FlowDims), C.POINTER(_VP), _I, _VP, _VP]),
     "cfh_flow_integrate": (_I, [C.POINTER(FlowDims), C.POINTER(_VP), _VP, _VP, _VP, _I, _VP]),
+    "cfh_vae_bytes": (_I64, [C.POINTER(VaeDims)]),
+    "cfh_vae_pack": (_I, [C.POINTER(VaeDims), C.POINTER(_VP), _I, _VP, _VP]),
+    "cfh_vae_caps": (_I, [C.POINTER(VaeDims), _I, C.POINTER(_I64)]),
+    "cfh_vae_encode": (_I, [C.POINTER(VaeDims), _VP, _VP, _VP, _I, _I, _VP, _VP]),
+    "cfh_vae_decode": (_I, [C.POINTER(VaeDims), _VP, _VP, _VP, _I, _I, _VP, _VP]),
     "cfh_head_logits": (_I, [_VP, _I, _I, _VP, _VP, _I, _VP, _VP, _I, _I, _VP, _VP, _VP]),
     "cfh_row_topk": (_I, [_VP, _I, _I, _I, _VP, _VP, _VP, _VP]),
     "cfh_head_ws_bytes": (_I64, [_I, _I, _I]),

@@ -41,8 +41,62 @@ class TreeFlowConfig:
     def num_chunks(self) -> int:
         return self.draft_length // self.chunk_size
 
+    @property
+    def flow_dim(self) -> int:
+        """Width the chunk experts run at: the target hidden size here, the latent size in the VAE
+        drafter."""
+        return self.expert_dim
+
     def to_dict(self) -> dict:
         return asdict(self)
+
+
+@dataclass
+class TreeVAEFlowConfig(TreeFlowConfig):
+    """The latent drafter's config (``cf/drafters/tree_vae_flow.py:32-47``): the flow runs at
+    ``latent_size`` inside a frozen ``TransformerHiddenVAE``; the path head, markov bias and lm_head
+    stay at the target hidden size.  The serving proposer builds every drafter with this class
+    (``cf/vllm_plugin/flow_proposer.py:616-632``)."""
+    vae_dir: str | None = None
+    latent_size: int = 640
+    vae_type: str = "transformer_hidden"
+    vae_intermediate_size: int = 1920
+    vae_num_layers: int = 2
+    vae_num_heads: int = 8
+    vae_max_sequence_length: int = 16
+    train_vae: bool = False
+    lambda_vae_recon: float = 0.5
+    lag_context: bool = False
+    lag_extend: bool = False
+    anchor_token: bool = False
+    sched_sampling_p: float = 0.0
+    prev_token_cond: bool = True
+
+    @property
+    def flow_dim(self) -> int:
+        return self.latent_size
+
+    @property
+    def vae_heads(self) -> int:
+        """``num_heads if intermediate_size % num_heads == 0 else 1``
+        (``cf/vae/transformer_hidden.py:13``)."""
+        h = self.vae_num_heads
+        return h if self.vae_intermediate_size % h == 0 else 1
+
+    def vae_config(self, hidden_size: int) -> dict:
+        """``HiddenVAEConfig`` fields (``cf/vae/base.py:9-17``) as ``_load_frozen_vae`` fills them
+        (``cf/drafters/tree_vae_flow.py:50-55``)."""
+        return dict(hidden_size=hidden_size, latent_size=self.latent_size,
+                    intermediate_size=self.vae_intermediate_size, num_layers=self.vae_num_layers,
+                    num_heads=self.vae_num_heads, max_sequence_length=self.vae_max_sequence_length)
+
+
+def config_from_model_args(model_args: dict) -> TreeVAEFlowConfig:
+    """``chained_flow_tree_config.json["model_args"]`` -> config, keeping only the known fields, as
+    the proposer does (``cf/vllm_plugin/flow_proposer.py:616-618``)."""
+    from dataclasses import fields
+    known = {f.name for f in fields(TreeVAEFlowConfig)}
+    return TreeVAEFlowConfig(**{k: v for k, v in model_args.items() if k in known})
 
 
 def flownet(d: int, layers: int = 8, flow_steps: int = 8, **kw) -> TreeFlowConfig:

@@ -1,8 +1,9 @@
 """The drafting hot path on MI355X: one flow pass, then the beam over the shortlisted head.
 
 ``Drafter`` holds what the proposer's ``_build`` assembles (``cf/vllm_plugin/flow_proposer.py:579-867``):
-the packed flow experts, the PathHead, the shortlisted lm_head with the markov bias, and the
-target's input embeddings.  ``beam_chains`` / ``beam_tree`` are the proposer's ``_draft_fn``
+the packed flow experts, the PathHead, the shortlisted lm_head with the markov bias, the target's
+input embeddings and, for the latent drafter (``TreeVAEFlowConfig``), the packed VAE the flow runs
+inside (``cf/drafters/tree_vae_flow.py:163-175``).  ``beam_chains`` / ``beam_tree`` are the proposer's ``_draft_fn``
 (``:1187-1332``) with no host synchronisation until the caller reads the result.
 """
 from __future__ import annotations
@@ -12,9 +13,10 @@ import ctypes as C
 import torch
 
 from chain_flow_amd import _lib
-from chain_flow_amd.config import TreeFlowConfig
+from chain_flow_amd.config import TreeFlowConfig, TreeVAEFlowConfig
 from chain_flow_amd.flow import FusedFlow
 from chain_flow_amd.head import PathHead, ShortlistHead
+from chain_flow_amd.vae import HiddenVAE
 
 
 def front_pad(hidden: torch.Tensor, context_size: int) -> torch.Tensor:
@@ -36,6 +38,14 @@ class Drafter:
             dev = torch.device("cuda", torch.cuda.current_device())
         self.device = dev
         self.path_trim = path_trim
+        self.vae = None
+        if isinstance(cfg, TreeVAEFlowConfig):
+            for flag in ("lag_context", "anchor_token"):
+                if getattr(cfg, flag):
+                    raise ValueError(f"{flag}=True is not built: this build runs the latent drafter "
+                                     f"without the lag slot / token anchor (the shipped default)")
+            hidden = weights["lm_head.weight"].shape[1]
+            self.vae = HiddenVAE(cfg, hidden, weights, device=dev)
         self.flow = FusedFlow(cfg, weights, device=dev)
         self.path = PathHead(weights, weights["embed_tokens.weight"], cfg.path_order,
                              cfg.path_ffn_multiplier, dev)
@@ -48,7 +58,12 @@ class Drafter:
         return depth if self.path_trim else None
 
     def predict_hidden(self, ctx: torch.Tensor) -> torch.Tensor:
-        return self.flow.predict_hidden(ctx.to(self.device, torch.float16))
+        """ctx [B, C, hidden] (front-padded) -> marginal hiddens [B, draft_length, hidden]
+        (``TreeFlowDrafter.predict_hidden``; latent drafter: decode(integrate(encode(ctx).mu)))."""
+        ctx = ctx.to(self.device, torch.float16)
+        if self.vae is None:
+            return self.flow.predict_hidden(ctx)
+        return self.vae.decode(self.flow.predict_hidden(self.vae.encode(ctx)))
 
     def beam_chains(self, ctx: torch.Tensor, known0: torch.Tensor, K: int, width: int = 4,
                     pred: torch.Tensor | None = None) -> torch.Tensor:

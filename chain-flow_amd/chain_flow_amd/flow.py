@@ -17,7 +17,7 @@ from chain_flow_amd.weights import expert_param_names, expert_prefixes
 
 
 def flow_dims(cfg: TreeFlowConfig) -> _lib.FlowDims:
-    return _lib.FlowDims(cfg.expert_dim, cfg.ffn_multiplier, cfg.num_heads, cfg.num_drafter_layers,
+    return _lib.FlowDims(cfg.flow_dim, cfg.ffn_multiplier, cfg.num_heads, cfg.num_drafter_layers,
                          cfg.context_size, cfg.draft_length, cfg.chunk_size, cfg.num_flow_steps)
 
 
@@ -64,16 +64,18 @@ class FusedFlow:
         return sum(b.numel() for b in self.packed)
 
     def predict_hidden(self, ctx: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-        """ctx [B, context_size, d] fp16 (already front-padded) -> [B, draft_length, d] fp16."""
+        """ctx [B, context_size, d] fp16 (already front-padded; d = cfg.flow_dim) -> [B, draft_length, d]
+        fp16."""
         cfg = self.cfg
-        if ctx.dim() != 3 or ctx.shape[1] != cfg.context_size or ctx.shape[2] != cfg.expert_dim:
-            raise ValueError(f"ctx must be [B, {cfg.context_size}, {cfg.expert_dim}], got {tuple(ctx.shape)}")
+        d = cfg.flow_dim
+        if ctx.dim() != 3 or ctx.shape[1] != cfg.context_size or ctx.shape[2] != d:
+            raise ValueError(f"ctx must be [B, {cfg.context_size}, {d}], got {tuple(ctx.shape)}")
         if ctx.dtype != torch.float16 or ctx.device != self.device:
             raise ValueError("ctx must be fp16 on the flow's device")
         ctx = ctx.contiguous()
         B = ctx.shape[0]
         if out is None:
-            out = torch.empty(B, cfg.draft_length, cfg.expert_dim, dtype=torch.float16, device=self.device)
+            out = torch.empty(B, cfg.draft_length, d, dtype=torch.float16, device=self.device)
         _lib.check(_lib.lib().cfh_flow_integrate(C.byref(self.dims), self._experts, ctx.data_ptr(),
                                                  out.data_ptr(), self.ws.data_ptr(), B,
                                                  _lib.stream_handle()),

@@ -14,9 +14,14 @@ Mirrors ``chain_flow.vllm_plugin.flow_proposer.FlowDrafterProposer`` (``cf/vllm_
 * ``propose(sampled_token_ids, num_tokens_no_spec, token_ids_cpu, slot_mappings=None, **kw)`` returns
   ``list[list[int]]`` (``:1698``, ``:2494-2569``).
 
-What differs, by design: the drafter is the target-width ``TreeFlowDrafter`` (``architecture
-"tree_flow"``); a VAE-latent checkpoint (``TreeVAEFlowConfig``) is refused with a message.  There
-is no Hugging Face download (``CF_DRAFTER_DIR`` must be a local directory) and no torch.compile.
+Drafters: the reference builds every checkpoint as the latent ``TreeVAEFlowDrafter``
+(``:583, 616-632``), with the VAE from ``CF_VAE_DIR`` / the config's ``vae_dir`` overlaid by the
+checkpoint's own ``drafter.vae.*`` tensors; so does this proposer for any checkpoint that carries
+VAE fields or tensors.  A checkpoint with neither is served as the target-width ``TreeFlowDrafter``
+(``expert_dim`` = target hidden size), the form the synthetic d = 2560 / 5120 workloads use.
+What differs, by design: no Hugging Face download (``CF_DRAFTER_DIR`` must be a local directory),
+no torch.compile, and the latent drafter's ``lag_context`` / ``anchor_token`` options are refused
+with a message (not built).
 The target's final hidden states reach the proposer through :meth:`stash_hidden_states` (the
 reference monkeypatches ``GPUModelRunner.propose_draft_token_ids`` to stash
 ``sample_hidden_states``, ``:40-59``) and the target's input embeddings and ``lm_head`` weight
@@ -32,8 +37,9 @@ from pathlib import Path
 import torch
 
 from chain_flow_amd import shortlist as _sl
-from chain_flow_amd.config import TreeFlowConfig
+from chain_flow_amd.config import TreeFlowConfig, TreeVAEFlowConfig
 from chain_flow_amd.drafter import Drafter, front_pad
+from chain_flow_amd.vae import load_vae_dir
 
 CONFIG_NAME = "chained_flow_tree_config.json"
 WEIGHTS_NAME = "model.safetensors"
@@ -53,17 +59,32 @@ def shortlist_candidates(drafter_dir: str | None) -> list[tuple[str, str]]:
     return out
 
 
+VAE_FIELDS = {f.name for f in dataclasses.fields(TreeVAEFlowConfig)} - {
+    f.name for f in dataclasses.fields(TreeFlowConfig)}
+
+
+def _checkpoint_has_vae(ckd: str) -> bool:
+    from safetensors import safe_open
+    path = os.path.join(ckd, WEIGHTS_NAME)
+    if not os.path.exists(path):
+        return False
+    with safe_open(path, framework="pt") as f:
+        return any(k.startswith("drafter.vae.") for k in f.keys())
+
+
 def load_drafter_config(ckd: str) -> TreeFlowConfig:
-    """``model_args`` of ``chained_flow_tree_config.json`` -> TreeFlowConfig, with the
-    ``CF_FLOW_STEPS`` inference override (``flow_proposer.py:616-631``)."""
+    """``model_args`` of ``chained_flow_tree_config.json`` -> config, with the ``CF_FLOW_STEPS``
+    inference override (``flow_proposer.py:616-631``): ``TreeVAEFlowConfig`` when the checkpoint
+    carries VAE fields or ``drafter.vae.*`` tensors, else the target-width ``TreeFlowConfig``."""
     with open(os.path.join(ckd, CONFIG_NAME)) as f:
         margs = json.load(f)["model_args"]
     arch = margs.get("architecture", "tree_flow")
     if arch != "tree_flow":
-        raise ValueError(f"drafter architecture {arch!r} is not supported by this build: it runs the "
-                         f"target-width TreeFlowDrafter ('tree_flow'); VAE-latent drafters are not built")
-    fields = {f.name for f in dataclasses.fields(TreeFlowConfig)}
-    cfg = TreeFlowConfig(**{k: v for k, v in margs.items() if k in fields})
+        raise ValueError(f"drafter architecture {arch!r} is not supported (TreeFlowConfig.architecture "
+                         f"must be 'tree_flow')")
+    kind = TreeVAEFlowConfig if (VAE_FIELDS & set(margs) or _checkpoint_has_vae(ckd)) else TreeFlowConfig
+    fields = {f.name for f in dataclasses.fields(kind)}
+    cfg = kind(**{k: v for k, v in margs.items() if k in fields})
     fs = os.environ.get("CF_FLOW_STEPS")
     if fs:
         n = int(fs)
@@ -182,8 +203,10 @@ class FlowDrafterProposer:
         self.dev = embed_w.device
         V, H = lm_w.shape
         cfg = load_drafter_config(self.ckd)
-        if cfg.expert_dim != H:
+        latent = isinstance(cfg, TreeVAEFlowConfig)
+        if not latent and cfg.expert_dim != H:
             raise ValueError(f"drafter expert_dim={cfg.expert_dim} but the target hidden size is {H}")
+        vae_sd = load_vae_dir(cfg) if latent else None     # raises as _load_frozen_vae does
         if self.branching:
             emit = min(self.tree_depth, cfg.draft_length - 1)
             if emit != self.tree_depth:
@@ -199,6 +222,10 @@ class FlowDrafterProposer:
                     f"chain tokens (draft_length={cfg.draft_length}; depth 0 reconstructs the "
                     f"token that was already committed). Set num_speculative_tokens<={emit}.")
         weights = load_drafter_weights(self.ckd, torch.float16, self.dev)
+        if vae_sd:
+            # the drafter checkpoint's own vae.* tensors win (load_state_dict after the VAE load)
+            for k, v in vae_sd.items():
+                weights.setdefault(k, v.to(self.dev, torch.float16))
         weights["lm_head.weight"] = lm_w.to(torch.float16)
         weights["embed_tokens.weight"] = embed_w.to(torch.float16)
         explicit = self.shortlist_path if "CF_SHORTLIST" in os.environ else None

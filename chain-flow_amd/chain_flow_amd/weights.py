@@ -5,8 +5,9 @@ sha256(name) mod 2^63 (mixed with a base seed), so any subset can be regenerated
 in another process, on the CPU or the GPU generator.  Names follow the reference's
 ``TreeFlowDrafter`` (``cf/drafters/tree_flow.py:107-131``), ``HiddenKVFlowExpert``
 (``cf/drafters/chunked_flow.py:205-262``), ``HiddenKVFlowBlock`` (``:168-183``), ``MarkovHead``
-(``cf/drafters/markov_flow.py:62-70``) and ``PathHead`` (``cf/drafters/tree_flow.py:80-96``), plus
-the target model's ``lm_head.weight`` and ``embed_tokens.weight``.
+(``cf/drafters/markov_flow.py:62-70``) and ``PathHead`` (``cf/drafters/tree_flow.py:80-96``), the
+latent drafter's ``vae.`` module (``TransformerHiddenVAE``, ``cf/vae/transformer_hidden.py:9-42``),
+plus the target model's ``lm_head.weight`` and ``embed_tokens.weight``.
 
 Two initialisations:
 * ``"baseline"`` -- Linear/Embedding weights ~N(0, 0.02), biases 0, LayerNorm weight 1 / bias 0
@@ -20,7 +21,7 @@ import hashlib
 
 import torch
 
-from chain_flow_amd.config import TreeFlowConfig
+from chain_flow_amd.config import TreeFlowConfig, TreeVAEFlowConfig
 
 
 def param_seed(name: str, base_seed: int = 0) -> int:
@@ -52,9 +53,62 @@ def expert_param_names(cfg: TreeFlowConfig, prefix: str):
     return names
 
 
-def param_specs(cfg: TreeFlowConfig, vocab: int, target: bool = True):
-    """name -> (shape, kind, fan_in) for every drafter parameter (and the target's head/embedding)."""
-    d, fd = cfg.expert_dim, cfg.expert_dim * cfg.ffn_multiplier
+def vae_half_names(cfg: TreeVAEFlowConfig, side: str):
+    """State-dict names (``vae.`` prefix) of one VAE half, ``side`` = "encoder" or "decoder", in
+    the order cfh_vae_pack expects."""
+    out_name = "vae.mu" if side == "encoder" else "vae.decoder_out"
+    names = [f"vae.{side}_in.weight", f"vae.{side}_in.bias", f"vae.{side}_pos.weight"]
+    for l in range(cfg.vae_num_layers):
+        b = f"vae.{side}.layers.{l}."
+        names += [b + "self_attn.in_proj_weight", b + "self_attn.in_proj_bias",
+                  b + "self_attn.out_proj.weight", b + "self_attn.out_proj.bias",
+                  b + "linear1.weight", b + "linear1.bias", b + "linear2.weight", b + "linear2.bias",
+                  b + "norm1.weight", b + "norm1.bias", b + "norm2.weight", b + "norm2.bias"]
+    names += [f"vae.{side}_norm.weight", f"vae.{side}_norm.bias", out_name + ".weight", out_name + ".bias"]
+    return names
+
+
+def vae_param_names(cfg: TreeVAEFlowConfig):
+    """Every VAE parameter cfh_vae_pack reads (encoder half then decoder half; logvar is unused)."""
+    return vae_half_names(cfg, "encoder") + vae_half_names(cfg, "decoder")
+
+
+def _vae_specs(cfg: TreeVAEFlowConfig, hidden: int):
+    I, Z, T = cfg.vae_intermediate_size, cfg.latent_size, cfg.vae_max_sequence_length
+    specs = {}
+    for side, kin, nout, out_name in (("encoder", hidden, Z, "vae.mu"), ("decoder", Z, hidden, "vae.decoder_out")):
+        specs[f"vae.{side}_in.weight"] = ((I, kin), "linear", kin)
+        specs[f"vae.{side}_in.bias"] = ((I,), "bias", kin)
+        specs[f"vae.{side}_pos.weight"] = ((T, I), "embedding", I)
+        for l in range(cfg.vae_num_layers):
+            b = f"vae.{side}.layers.{l}."
+            specs[b + "self_attn.in_proj_weight"] = ((3 * I, I), "linear", I)
+            specs[b + "self_attn.in_proj_bias"] = ((3 * I,), "bias", I)
+            specs[b + "self_attn.out_proj.weight"] = ((I, I), "linear", I)
+            specs[b + "self_attn.out_proj.bias"] = ((I,), "bias", I)
+            specs[b + "linear1.weight"] = ((4 * I, I), "linear", I)
+            specs[b + "linear1.bias"] = ((4 * I,), "bias", I)
+            specs[b + "linear2.weight"] = ((I, 4 * I), "linear", 4 * I)
+            specs[b + "linear2.bias"] = ((I,), "bias", 4 * I)
+            for n in ("norm1", "norm2"):
+                specs[b + n + ".weight"] = ((I,), "ln_w", I)
+                specs[b + n + ".bias"] = ((I,), "ln_b", I)
+        specs[f"vae.{side}_norm.weight"] = ((I,), "ln_w", I)
+        specs[f"vae.{side}_norm.bias"] = ((I,), "ln_b", I)
+        specs[out_name + ".weight"] = ((nout, I), "linear", I)
+        specs[out_name + ".bias"] = ((nout,), "bias", I)
+        if side == "encoder":
+            specs["vae.logvar.weight"] = ((Z, I), "linear", I)
+            specs["vae.logvar.bias"] = ((Z,), "bias", I)
+    return specs
+
+
+def param_specs(cfg: TreeFlowConfig, vocab: int, target: bool = True, hidden: int | None = None):
+    """name -> (shape, kind, fan_in) for every drafter parameter (and the target's head/embedding).
+    The chunk experts run at ``cfg.flow_dim``; the path head, markov bias, VAE ends and target
+    tensors at ``hidden`` (default ``cfg.expert_dim``: the target hidden size)."""
+    d, fd = cfg.flow_dim, cfg.flow_dim * cfg.ffn_multiplier
+    hidden = cfg.expert_dim if hidden is None else hidden
     specs = {}
     for p in expert_prefixes(cfg):
         for n in expert_param_names(cfg, p):
@@ -86,6 +140,7 @@ def param_specs(cfg: TreeFlowConfig, vocab: int, target: bool = True):
     r = cfg.markov_rank
     specs["markov.w1.weight"] = ((vocab, r), "embedding_rank", r)
     specs["markov.w2.weight"] = ((vocab, r), "linear", r)
+    d = hidden
     pf = cfg.path_ffn_multiplier * d
     for j in range(cfg.path_order):
         specs[f"path_head.offset_proj.{j}.weight"] = ((d, d), "linear", d)
@@ -96,6 +151,8 @@ def param_specs(cfg: TreeFlowConfig, vocab: int, target: bool = True):
     specs["path_head.mlp.0.bias"] = ((pf,), "bias", d)
     specs["path_head.mlp.3.weight"] = ((d, pf), "linear", pf)
     specs["path_head.mlp.3.bias"] = ((d,), "bias", pf)
+    if isinstance(cfg, TreeVAEFlowConfig):
+        specs.update(_vae_specs(cfg, hidden))
     if target:
         specs["lm_head.weight"] = ((vocab, d), "linear", d)
         specs["embed_tokens.weight"] = ((vocab, d), "embedding_tok", d)
@@ -130,9 +187,9 @@ def _draw(shape, kind, fan_in, init, gen, device):
 
 
 def make_weights(cfg: TreeFlowConfig, vocab: int, *, init: str = "test", dtype=torch.float16,
-                 device="cpu", base_seed: int = 0, names=None, target: bool = True):
+                 device="cpu", base_seed: int = 0, names=None, target: bool = True, hidden: int | None = None):
     """name -> tensor (dtype, device) for every parameter (or only ``names``)."""
-    specs = param_specs(cfg, vocab, target=target)
+    specs = param_specs(cfg, vocab, target=target, hidden=hidden)
     out = {}
     for name, (shape, kind, fan_in) in specs.items():
         if names is not None and name not in names:

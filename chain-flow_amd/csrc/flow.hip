@@ -196,12 +196,13 @@ Plan make_plan(const cfh_flow_dims* dm) {
   p.Smax = p.KD;
   const int tiles_d = p.d / 16;
   const size_t cap = 96 * 1024;
-  p.ks_qc = choose_ks(p.nch, tiles_d, p.d, p.Smax, 2048, cap);
+  // (one k-chunk when K has fewer than 8 k-steps: small latent widths)
+  p.ks_qc = std::max(choose_ks(p.nch, tiles_d, p.d, p.Smax, 2048, cap), 1);
   // W2: one d-wide k-chunk per ffn slice (ks = ffn_mult) in 16-wave workgroups, so that W1 and W2
   // both run as one round of ~240 workgroups at one workgroup per CU; else split-K by wave count
   const bool w2_wide = tiles_d % 16 == 0 && stream_lds(S_BUF, p.Smax, p.d, p.hd, p.C) <= 150 * 1024;
-  p.ks_w2 = w2_wide ? dm->ffn_mult : choose_ks(p.nch, tiles_d, p.fd, p.Smax, 4096, cap);
-  p.ks_out = choose_ks(p.nch, tiles_d, p.d, p.CS, 2048, cap);
+  p.ks_w2 = w2_wide ? dm->ffn_mult : std::max(choose_ks(p.nch, tiles_d, p.fd, p.Smax, 4096, cap), 1);
+  p.ks_out = std::max(choose_ks(p.nch, tiles_d, p.d, p.CS, 2048, cap), 1);
   p.ks_kv = ksplit_for(p.nch * p.NL, 2 * p.d / 16, p.d, p.C);
   p.ks_tau = ksplit_for(p.nch, p.d / 16, p.d, p.E);
   p.wpb_qc = std::min(4, pick_wpb(tiles_d, 1));
@@ -210,8 +211,8 @@ Plan make_plan(const cfh_flow_dims* dm) {
   p.tpw_att = (tiles_d % 16 == 0) ? 2 : 1;
   p.wpb_att = pick_wpb(tiles_d, p.tpw_att);
   fit_grid(tiles_d, p.nch * p.ks_att, &p.wpb_att, &p.tpw_att);
-  p.wpb_full = 8;
-  p.wpb_w1 = (p.fd / 16) % 16 == 0 ? 16 : 8;
+  p.wpb_full = pick_wpb(3 * tiles_d, 1);
+  p.wpb_w1 = (p.fd / 16) % 16 == 0 ? 16 : pick_wpb(p.fd / 16, 1);
   // the cross attention holds every q partial of its groups in registers: fewer QC splits if needed
   for (int ks = p.ks_qc; ks > 1; --ks) {
     SArgs a = {};

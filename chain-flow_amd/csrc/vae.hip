@@ -110,9 +110,9 @@ struct VaePlan {
 };
 
 // Split-K launch shape of an N x K streaming product over T rows: as many k-chunks as reach ~2048
-// wave units (at least 8 k-steps each), 8-wave (or smaller) workgroups.
+// wave units (at least 8 k-steps each; one chunk when K has fewer), 8-wave (or smaller) workgroups.
 void split_shape(int N, int K, int T, int* ks, int* wpb) {
-  *ks = choose_ks(1, N / 16, K, T, 2048, 96 * 1024);
+  *ks = std::max(choose_ks(1, N / 16, K, T, 2048, 96 * 1024), 1);
   *wpb = pick_wpb(N / 16, 1);
 }
 

@@ -82,12 +82,13 @@ def test_flow_full_width_matches_oracle(cuda):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("d,heads,layers,steps", [(640, 8, 2, 2), (640, 16, 1, 2), (768, 12, 1, 1), (1920, 8, 1, 1)])
+@pytest.mark.parametrize("d,heads,layers,steps", [(640, 8, 2, 2), (640, 16, 1, 2), (768, 12, 1, 1), (1920, 8, 1, 1),
+                                                  (128, 8, 1, 2), (64, 8, 1, 1), (192, 4, 1, 1)])
 def test_flow_latent_widths_match_oracle(cuda, d, heads, layers, steps):
-    """Widths whose heads do not fill an MFMA k-step (head_dim 80 and 240: two heads per attention
-    k-chunk; 40: four) and rows that do not fill whole waves of the residual kernel (d = 640 and
-    1920: 160 and 480 four-column groups).  d = 640 with 8 heads is the latent width of the
-    shipped VAE drafters."""
+    """Widths whose heads do not fill an MFMA k-step (head_dim 80, 240, 16 and 48: two heads per
+    attention k-chunk; 40 and 8: four), rows that do not fill whole waves of the residual kernel
+    (d = 640 and 1920: 160 and 480 four-column groups) and widths too short to split K (d <= 256).
+    d = 640 with 8 heads is the latent width of the shipped VAE drafters."""
     cfg = flownet(d, layers=layers, flow_steps=steps, num_heads=heads)
     W = _flow_weights(cfg, seed=11)
     ctx = synthetic_context(1, cfg.context_size, d, seed=5)

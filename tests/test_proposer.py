@@ -38,7 +38,7 @@ def ckpt(tmp_path):
 
 def _env(monkeypatch, **kv):
     for k in ("VLLM_SPEC_TREE", "CF_TREE_KEEP", "CF_TREE_TOPB", "CF_TREE_DEPTH", "CF_TREE_BRANCH",
-              "CF_DRAFTER_DIR", "CF_SHORTLIST", "CF_FLOW_STEPS", "CF_WIDTH"):
+              "CF_DRAFTER_DIR", "CF_SHORTLIST", "CF_FLOW_STEPS", "CF_WIDTH", "CF_VAE_DIR"):
         monkeypatch.delenv(k, raising=False)
     for k, v in kv.items():
         monkeypatch.setenv(k, str(v))
@@ -113,3 +113,54 @@ def test_declared_identity_mismatch_raises(tmp_path):
     (tmp_path / fp.CONFIG_NAME).write_text(json.dumps({"model_args": {}, "shortlist": {"rows": 4}}))
     with pytest.raises(RuntimeError, match="does not match what this drafter declares"):
         fp.resolve_shortlist(str(tmp_path), V, None)
+
+
+def _latent_cfg(**kw):
+    from chain_flow_amd.config import TreeVAEFlowConfig
+    base = dict(context_size=8, draft_length=8, chunk_size=4, expert_dim=1024, num_heads=8, ffn_multiplier=6,
+                num_drafter_layers=1, num_flow_steps=2, latent_size=64, vae_intermediate_size=64,
+                vae_num_layers=1, vae_num_heads=4, vae_max_sequence_length=16)
+    base.update(kw)
+    return TreeVAEFlowConfig(**base)
+
+
+def test_latent_checkpoint_is_a_vae_drafter(monkeypatch, tmp_path):
+    """VAE fields in model_args (or drafter.vae.* tensors) select TreeVAEFlowConfig, as every
+    checkpoint the reference proposer serves is built (cf/vllm_plugin/flow_proposer.py:616-632)."""
+    from safetensors.torch import save_file
+    from chain_flow_amd.config import TreeVAEFlowConfig
+    _env(monkeypatch)
+    cfg = _latent_cfg()
+    W = make_weights(cfg, 64, init="test", target=False, dtype=torch.float32, hidden=128)
+    save_file({"drafter." + k: v.contiguous() for k, v in W.items()}, str(tmp_path / fp.WEIGHTS_NAME))
+    (tmp_path / fp.CONFIG_NAME).write_text(json.dumps({"model_args": cfg.to_dict()}))
+    got = fp.load_drafter_config(str(tmp_path))
+    assert isinstance(got, TreeVAEFlowConfig) and got.flow_dim == 64 and got.latent_size == 64
+    assert W["expert.out_proj.weight"].shape == (64, 64) and W["path_head.norm.weight"].shape == (128,)
+    # tensors alone (model_args without VAE fields) still mean a latent drafter
+    margs = {k: v for k, v in cfg.to_dict().items() if k not in fp.VAE_FIELDS}
+    (tmp_path / fp.CONFIG_NAME).write_text(json.dumps({"model_args": margs}))
+    assert isinstance(fp.load_drafter_config(str(tmp_path)), TreeVAEFlowConfig)
+
+
+def test_vae_dir_resolution(monkeypatch, tmp_path):
+    """_load_frozen_vae's lookup (cf/drafters/tree_vae_flow.py:57-87): CF_VAE_DIR over vae_dir,
+    model.safetensors else the newest checkpoint-N, vae.-prefixed or bare keys, named errors."""
+    from safetensors.torch import save_file
+    from chain_flow_amd.vae import load_vae_dir
+    _env(monkeypatch)
+    assert load_vae_dir(_latent_cfg()) is None
+    for n, val in ((3, 1.0), (10, 2.0)):
+        (tmp_path / f"checkpoint-{n}").mkdir()
+        save_file({"encoder_in.bias": torch.full((4,), val)}, str(tmp_path / f"checkpoint-{n}" / "model.safetensors"))
+    got = load_vae_dir(_latent_cfg(vae_dir=str(tmp_path)))
+    assert set(got) == {"vae.encoder_in.bias"} and float(got["vae.encoder_in.bias"][0]) == 2.0
+    save_file({"vae.mu.bias": torch.ones(2), "other": torch.ones(1)}, str(tmp_path / "model.safetensors"))
+    assert set(load_vae_dir(_latent_cfg(vae_dir=str(tmp_path)))) == {"vae.mu.bias"}
+    with pytest.raises(FileNotFoundError, match="vae_dir in the checkpoint config"):
+        load_vae_dir(_latent_cfg(vae_dir=str(tmp_path / "absent")))
+    monkeypatch.setenv("CF_VAE_DIR", str(tmp_path / "empty"))
+    (tmp_path / "empty").mkdir()
+    with pytest.raises(FileNotFoundError, match="CF_VAE_DIR") as e:
+        load_vae_dir(_latent_cfg(vae_dir=str(tmp_path)))
+    assert "neither of the above" in str(e.value)

@@ -44,6 +44,7 @@ SIGNATURES = {
     "cfh_vae_caps": (_I, [C.POINTER(VaeDims), _I, C.POINTER(_I64)]),
     "cfh_vae_encode": (_I, [C.POINTER(VaeDims), _VP, _VP, _VP, _I, _I, _VP, _VP]),
     "cfh_vae_decode": (_I, [C.POINTER(VaeDims), _VP, _VP, _VP, _I, _I, _VP, _VP]),
+    "cfh_ring_step": (_I, [_VP, _VP, _VP, _I, _I, _VP, _I, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _VP, _VP]),
     "cfh_head_logits": (_I, [_VP, _I, _I, _VP, _VP, _I, _VP, _VP, _I, _I, _VP, _VP, _VP]),
     "cfh_row_topk": (_I, [_VP, _I, _I, _I, _VP, _VP, _VP, _VP]),
     "cfh_head_ws_bytes": (_I64, [_I, _I, _I]),

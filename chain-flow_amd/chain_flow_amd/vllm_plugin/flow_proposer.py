@@ -12,7 +12,14 @@ Mirrors ``chain_flow.vllm_plugin.flow_proposer.FlowDrafterProposer`` (``cf/vllm_
 * ``_draft_fn(ctx [B, C, d], known0 [B])`` is ``_beam_chains`` -> ``[B, K]`` or ``_beam_tree`` ->
   ``[B, 2N]`` (``:1187-1332``), run by ``chain_flow_amd.drafter.Drafter`` on the HIP kernels;
 * ``propose(sampled_token_ids, num_tokens_no_spec, token_ids_cpu, slot_mappings=None, **kw)`` returns
-  ``list[list[int]]`` (``:1698``, ``:2494-2569``).
+  ``list[list[int]]`` (``:1698``, ``:2494-2569``), or with ``CF_ASYNC_SPEC=1`` the GPU int32 tensor
+  ``[num_reqs, draft_width]`` indexed by batch row with no host read (``_async_draft_tensor``,
+  ``:2326-2357``);
+* the context lives in a device ring per batch slot (``_ring_write`` / ``_ring_gather``,
+  ``:916-961``; ``cfh_ring_step``), with the slot lifecycle of ``_ctx_gpu`` (``:2045-2105``: a new
+  request resets or seeds its slot, a request moved by vLLM's batch condense carries its history),
+  and the ring step + draft run as one captured graph per batch bucket (``CF_CUDAGRAPH``,
+  ``CF_DRAFT_BUCKETS``; ``:1342-1365, 1511-1589``).
 
 Drafters: the reference builds every checkpoint as the latent ``TreeVAEFlowDrafter``
 (``:583, 616-632``), with the VAE from ``CF_VAE_DIR`` / the config's ``vae_dir`` overlaid by the
@@ -38,7 +45,9 @@ import torch
 
 from chain_flow_amd import shortlist as _sl
 from chain_flow_amd.config import TreeFlowConfig, TreeVAEFlowConfig
-from chain_flow_amd.drafter import Drafter, front_pad
+from chain_flow_amd.drafter import Drafter
+from chain_flow_amd.graph import DraftGraphs, bucket_ladder
+from chain_flow_amd.ring import ContextRing
 from chain_flow_amd.vae import load_vae_dir
 
 CONFIG_NAME = "chained_flow_tree_config.json"
@@ -178,10 +187,14 @@ class FlowDrafterProposer:
         self.shortlist_path = os.environ.get("CF_SHORTLIST")
         self.max_reqs = int(vllm_config.scheduler_config.max_num_seqs)
         self.path_trim = os.environ.get("CF_PATH_TRIM", "1") != "0"
+        self.use_cg = os.environ.get("CF_CUDAGRAPH", "1") == "1"
+        self.async_spec = os.environ.get("CF_ASYNC_SPEC", "0") == "1"
         self.drafter: Drafter | None = None
         self._target = None
         self._hidden = None
-        self.ctx_hist: dict[int, torch.Tensor] = {}
+        self._slot_req: list = [None] * self.max_reqs       # request id held by each batch slot
+        self._req_slot: dict = {}
+        self._dtok = None
 
     # ---- what the reference reads off the engine ------------------------------------------
     def bind_target(self, embed_w: torch.Tensor, lm_w: torch.Tensor) -> None:
@@ -234,6 +247,11 @@ class FlowDrafterProposer:
         self.drafter = Drafter(cfg, weights, None if sl is None else sl.to(self.dev), device=self.dev,
                                path_trim=self.path_trim)
         self.ctx_size = cfg.context_size
+        # rows one request can append per step: the committed token plus every accepted draft
+        self.kmax = (self.tree_depth + 1) if self.branching else (self.K + 1)
+        self.ring = ContextRing(self.max_reqs, self.ctx_size, H, device=self.dev)
+        self.graphs = (DraftGraphs(self.ring, self._draft_fn, self.kmax, bucket_ladder(self.max_reqs))
+                       if self.use_cg else None)
 
     # ---- drafting --------------------------------------------------------------------------
     def _draft_fn(self, ctx: torch.Tensor, known0: torch.Tensor) -> torch.Tensor:
@@ -242,38 +260,96 @@ class FlowDrafterProposer:
                                           depth=self.tree_depth)
         return self.drafter.beam_chains(ctx, known0, self.K, width=self.width)
 
+    def _lifecycle(self, rows, req_ids) -> list[int]:
+        """Slot bookkeeping of ``_ctx_gpu`` (``:2045-2080``): returns the slots that hold a NEW request
+        (reset, then seeded or started empty); a live request found in another slot is moved with
+        its history.  Without request ids every slot is taken to keep its request."""
+        if req_ids is None:
+            return []
+        fresh, migrate = [], []
+        for i in rows:
+            rid = req_ids[i] if i < len(req_ids) else str(i)
+            if self._slot_req[i] == rid:
+                continue
+            old = self._req_slot.get(rid)
+            if old is not None and old != i and self._slot_req[old] == rid:
+                migrate.append((i, old))
+            else:
+                fresh.append(i)
+            self._slot_req[i] = rid
+            self._req_slot[rid] = i
+        live = set(req_ids)
+        for k in [k for k in self._req_slot if k not in live]:
+            self._req_slot.pop(k, None)
+        self.ring.migrate(migrate)
+        if fresh:
+            self.ring.reset(fresh)
+        return fresh
+
+    def _async_draft_tensor(self, ch: torch.Tensor, rows, nreq: int) -> torch.Tensor:
+        """[nreq, draft_width] int32 on the device, one row per batch slot (zeros where no draft),
+        in a persistent buffer (``:2326-2357``)."""
+        N = self.draft_width
+        if int(ch.shape[1]) < N:
+            raise AssertionError(f"draft is {tuple(ch.shape)} but {N} columns were declared to vLLM")
+        if self._dtok is None:
+            self._dtok = torch.zeros((self.max_reqs, N), dtype=torch.int32, device=ch.device)
+        v = self._dtok[:nreq]
+        v.zero_()
+        v.index_copy_(0, torch.tensor(rows, device=ch.device), ch[:len(rows), :N].to(v.dtype))
+        return v
+
     @torch.inference_mode()
     def propose(self, sampled_token_ids, num_tokens_no_spec=None, token_ids_cpu=None, slot_mappings=None,
                 **kw):
-        """sampled_token_ids: per request, the tokens committed this step (list of lists).  The
-        stashed hidden states hold one row per committed token, requests in order.  Returns the
+        """sampled_token_ids: per request (batch slot), the tokens committed this step (list of lists).
+        The stashed hidden states hold one row per committed token, requests in order.  Returns the
         next draft per request: K chain tokens, or the N tree tokens (their parents are kept in
-        ``self.last_parents``)."""
+        ``self.last_parents``); with ``CF_ASYNC_SPEC=1`` the device tensor instead.
+        kw: ``hidden_states`` (instead of the stash), ``req_ids`` (slot lifecycle)."""
         if self.drafter is None:
             self._build()
         hidden = kw.get("hidden_states", self._hidden)
         if hidden is None:
             raise RuntimeError("no hidden states: stash_hidden_states() before propose()")
-        rows, ctxs, known = [], [], []
+        hidden = hidden.to(self.dev, torch.float16)
+        nreq = len(sampled_token_ids)
+        if nreq > self.max_reqs:
+            raise ValueError(f"{nreq} requests exceed max_num_seqs={self.max_reqs}")
+        rows, starts, cnt, known, wmask = [], [], [], [], []
         off = 0
         for i, toks in enumerate(sampled_token_ids):
             n = len(toks)
             if n == 0:
                 continue
-            h = hidden[off:off + n].to(self.dev, torch.float16)
-            off += n
-            prev = self.ctx_hist.get(i)
-            hist = h if prev is None else torch.cat([prev, h], 0)
-            self.ctx_hist[i] = hist[-self.ctx_size:]
             rows.append(i)
-            ctxs.append(front_pad(self.ctx_hist[i][None], self.ctx_size)[0])
+            starts.append(off)
+            cnt.append(n)
+            wmask.append(1)
             known.append(int(toks[-1]))
-        out = [[] for _ in sampled_token_ids]
+            off += n
+        fresh = set(self._lifecycle(rows, kw.get("req_ids")))
+        for j, i in enumerate(rows):
+            if cnt[j] > self.kmax:
+                # more rows than one step appends (a prefill): they seed the slot, as the
+                # reference's _seed_prompt_ctx does, and are not appended again
+                self.ring.seed(i, hidden[starts[j]:starts[j] + cnt[j]])
+                wmask[j], cnt[j] = 0, 0
+            elif i in fresh:
+                pass                    # reset above: this step's rows start the history
         if not rows:
-            return out
-        ctx = torch.stack(ctxs, 0)
-        known0 = torch.tensor(known, device=self.dev, dtype=torch.long)
-        draft = self._draft_fn(ctx, known0).cpu().tolist()       # the one device -> host sync
+            return torch.zeros(nreq, self.draft_width, dtype=torch.int32, device=self.dev) \
+                if self.async_spec else [[] for _ in sampled_token_ids]
+        sh = hidden[:off]
+        if self.graphs is not None and self.graphs.bucket_for(len(rows)) is not None:
+            draft = self.graphs.run(sh, rows, starts, cnt, known, wmask)
+        else:
+            ctx = self.ring.step(sh, rows, starts, cnt, wmask, kmax=self.kmax)
+            draft = self._draft_fn(ctx, torch.tensor(known, device=self.dev, dtype=torch.long))
+        if self.async_spec:
+            return self._async_draft_tensor(draft, rows, nreq)
+        draft = draft.cpu().tolist()                 # the one device -> host sync
+        out = [[] for _ in sampled_token_ids]
         self.last_parents = {}
         for j, i in enumerate(rows):
             if self.branching:

@@ -130,6 +130,20 @@ int cfh_vae_encode(const cfh_vae_dims* dims, const void* packed, const void* hid
 int cfh_vae_decode(const cfh_vae_dims* dims, const void* packed, const void* z, void* out, int batch,
                    int rows, void* ws, void* stream);
 
+/* ---------------------------------------------------------------- context ring
+ * FlowDrafterProposer._ring_write + _ring_gather (cf/vllm_plugin/flow_proposer.py:916-961) as one
+ * launch, one workgroup per request.  ring [R][C+1][H] (2-byte elements; row C is the reference's
+ * trash row, unused), rpos / nval [R] int32 = next write position / valid rows per slot.
+ * For request b (slot rows[b]): rows j < min(cnt[b], Kmax) of sh [T][H] (same element type as the
+ * ring) at starts[b] + j -- or, with a tree's accepted path [R][path_ld], at starts[b] + 0 and
+ * starts[b] + 1 + path[slot][j-1] -- are appended unless wmask[b] == 0 (wmask NULL = all 1);
+ * rpos/nval advance; then, if ctx [B][C][H] is set, the slot's window is read back oldest first,
+ * front-padded by repeating the oldest row (TreeFlowDrafter._context, tree_flow.py:143-148).
+ * cnt NULL = gather only.  H % 8 == 0. */
+int cfh_ring_step(void* ring, int32_t* rpos, int32_t* nval, int C, int H, const void* sh, int T,
+                  const int32_t* rows, const int32_t* starts, const int32_t* cnt, const int32_t* wmask,
+                  const int32_t* path, int path_ld, int Kmax, int B, void* ctx, void* stream);
+
 /* ---------------------------------------------------------------- shortlisted lm_head
  * logits[m][j] = fp16( fp16(h[m] . W[row_j]) + fp16(A[m] . W2[row_j]) ),  row_j = sl ? sl[j] : j
  *   h [M][d] fp16 (M <= 8, d % 256 == 0); W [V][d] fp16: the target's full lm_head, its shortlist

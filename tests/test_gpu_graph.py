@@ -1,0 +1,61 @@
+"""GPU: the whole-draft graph (ring step -> predict_hidden -> beam) replays bit-identically to the
+same steps run eagerly, step after step as the rings evolve, with unrelated eager work between
+replays and batches that pad up to a bucket; for the target-width and the latent drafter."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from chain_flow_amd.config import TreeVAEFlowConfig, flownet
+from chain_flow_amd.drafter import Drafter
+from chain_flow_amd.graph import DraftGraphs, bucket_ladder
+from chain_flow_amd.ring import ContextRing
+from chain_flow_amd.weights import make_weights
+
+
+def _drafter(kind, cuda):
+    d, V, n = 512, 4096, 1024
+    if kind == "latent":
+        cfg = TreeVAEFlowConfig(context_size=8, draft_length=8, chunk_size=4, expert_dim=d, num_heads=8,
+                                ffn_multiplier=6, num_drafter_layers=1, num_flow_steps=2, latent_size=128,
+                                vae_intermediate_size=256, vae_num_layers=1, vae_num_heads=4,
+                                vae_max_sequence_length=16)
+    else:
+        cfg = flownet(d, layers=1, flow_steps=2)
+    W = make_weights(cfg, V, init="test", base_seed=5, hidden=d)
+    W["lm_head.weight"] = (W["lm_head.weight"].float() * 8).half()
+    sl = torch.randperm(V, generator=torch.Generator().manual_seed(3))[:n].sort().values
+    return Drafter(cfg, {k: v.to(cuda) for k, v in W.items()}, sl.to(torch.int32).to(cuda), device=cuda), d, sl
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind", ["target", "latent"])
+def test_draft_graph_replays_equal_eager(cuda, kind):
+    dr, d, sl = _drafter(kind, cuda)
+    R, C, kmax = 4, 8, 6
+    eager_ring = ContextRing(R, C, d, device=cuda)
+    graph_ring = ContextRing(R, C, d, device=cuda)
+    draft = lambda ctx, k0: dr.beam_chains(ctx, k0, 5, 4)
+    graphs = DraftGraphs(graph_ring, draft, kmax, bucket_ladder(R))
+    assert graphs.buckets == [1, 2, 4]
+    rng = np.random.default_rng(9)
+    print(f"[graph] {kind}", flush=True)
+    for step in range(6):
+        B = int(rng.integers(1, R))                      # 1..3: pads to buckets 1, 2 and 4
+        rows = rng.permutation(R)[:B].tolist()
+        cnt = rng.integers(1, kmax + 1, size=B).tolist()
+        starts = np.concatenate([[0], np.cumsum(cnt)[:-1]]).tolist()
+        sh = torch.randn(sum(cnt), d, generator=torch.Generator().manual_seed(100 + step)).half().to(cuda)
+        k0 = sl[rng.integers(0, len(sl), size=B)].long().tolist()
+        ctx = eager_ring.step(sh, rows, starts, cnt, kmax=kmax)
+        want = draft(ctx, torch.tensor(k0, device=cuda)).clone()
+        torch.cuda.synchronize()
+        junk = torch.randn(256, 256, device=cuda) @ torch.randn(256, 256, device=cuda)   # eager work between
+        got = graphs.run(sh, rows, starts, cnt, k0).clone()
+        torch.cuda.synchronize()
+        del junk
+        print(f"  step {step} B={B} graph {got.tolist()} eager {want.tolist()}", flush=True)
+        assert torch.equal(got, want), step
+        assert torch.equal(graph_ring.ring[:, :C], eager_ring.ring[:, :C])
+        assert torch.equal(graph_ring.rpos, eager_ring.rpos) and torch.equal(graph_ring.nval, eager_ring.nval)

@@ -64,3 +64,67 @@ def test_proposer_chain_draft_matches_oracle(cuda, tmp_path, monkeypatch):
         near = any((ohead.margins(t["lp"], 4) <= 1e-3).any() or (ohead.margins(t["cand"], 4) <= 1e-3).any()
                    for t in trace)
         assert near, (out[0], ref[0].tolist())
+
+
+def _ckpt(tmp_path, d=512, V=4096, n=1024, seed=7):
+    from safetensors.torch import save_file
+    cfg = flownet(d, layers=1, flow_steps=2)
+    W = make_weights(cfg, V, init="test", base_seed=seed)
+    W["lm_head.weight"] = (W["lm_head.weight"].float() * 8).half()
+    drafter = {k: v for k, v in W.items() if k not in ("lm_head.weight", "embed_tokens.weight")}
+    save_file({"drafter." + k: v.contiguous() for k, v in drafter.items()}, str(tmp_path / fp.WEIGHTS_NAME))
+    (tmp_path / fp.CONFIG_NAME).write_text(json.dumps({"model_args": cfg.to_dict()}))
+    sl = torch.randperm(V, generator=torch.Generator().manual_seed(3))[:n]
+    slmod.save(tmp_path / "shortlist.pt", sl, vocab_size=V)
+    return cfg, W, torch.unique(sl.long())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("graph", ["1", "0"])
+def test_proposer_ring_steps_and_async(cuda, tmp_path, monkeypatch, graph):
+    """Several propose() steps for two requests (one recycled for a new request id half way): the
+    device ring (+ the draft graph when CF_CUDAGRAPH=1) gives exactly the drafts of the eager
+    Drafter on the front-padded true history, and CF_ASYNC_SPEC=1 returns the same drafts as the
+    [num_reqs, K] int32 device tensor, rows by batch slot, zeros for a request with no tokens."""
+    from chain_flow_amd.drafter import front_pad
+    d = 512
+    cfg, W, slv = _ckpt(tmp_path)
+    for k in ("VLLM_SPEC_TREE", "CF_SHORTLIST", "CF_FLOW_STEPS", "CF_DRAFT_BUCKETS"):
+        monkeypatch.delenv(k, raising=False)
+    monkeypatch.setenv("CF_DRAFTER_DIR", str(tmp_path))
+    monkeypatch.setenv("CF_CUDAGRAPH", graph)
+    vc = SimpleNamespace(speculative_config=SimpleNamespace(num_speculative_tokens=5),
+                         scheduler_config=SimpleNamespace(max_num_seqs=4))
+    p = fp.FlowDrafterProposer(vc)
+    monkeypatch.setenv("CF_ASYNC_SPEC", "1")
+    pa = fp.FlowDrafterProposer(vc)
+    for q in (p, pa):
+        q.bind_target(W["embed_tokens.weight"].to(cuda), W["lm_head.weight"].to(cuda))
+    rng = np.random.default_rng(4)
+    hist = {0: [], 1: []}
+    ids = ["a", "b"]
+    for step in range(4):
+        if step == 2:
+            ids = ["a", "c"]              # slot 1 now holds a new request: its history restarts
+            hist[1] = []
+        toks = [[int(t) for t in slv[rng.integers(0, len(slv), size=int(rng.integers(1, 4)))]] for _ in range(2)]
+        if step == 3:
+            toks[1] = []                  # no tokens for slot 1 this step
+        n = sum(len(t) for t in toks)
+        hid = torch.randn(n, d, generator=torch.Generator().manual_seed(50 + step)).half()
+        off = 0
+        for i, t in enumerate(toks):
+            hist[i] += [hid[off + j] for j in range(len(t))]
+            off += len(t)
+        out = p.propose(toks, hidden_states=hid.to(cuda), req_ids=ids)
+        outa = pa.propose(toks, hidden_states=hid.to(cuda), req_ids=ids)
+        torch.cuda.synchronize()
+        rows = [i for i in range(2) if toks[i]]
+        ctx = torch.stack([front_pad(torch.stack(hist[i])[None], cfg.context_size)[0] for i in rows]).to(cuda)
+        want = p.drafter.beam_chains(ctx, torch.tensor([toks[i][-1] for i in rows], device=cuda), 5, 4).cpu()
+        print(f"[proposer ring] step {step} graph={graph} {out} eager {want.tolist()}", flush=True)
+        for j, i in enumerate(rows):
+            assert out[i] == want[j].tolist(), (step, i)
+        assert outa.dtype == torch.int32 and outa.is_cuda and outa.shape == (2, 5)
+        for i in range(2):
+            assert outa[i].cpu().tolist() == (out[i] if toks[i] else [0] * 5), (step, i)

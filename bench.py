@@ -2,6 +2,7 @@
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--d 5120] [--layers 8] [--no-cpu]
     python bench.py --workload latent        # the shipped 4B latent drafter (see below)
+    python bench.py --workload verify        # the tree-verify kernels at the tree-draft shapes
 
 A step is one whole FlowDrafterProposer chain draft over inputs already resident in HBM:
 ``predict_hidden`` (init_latents + 8 Euler steps of both chunk experts, every block) followed by the
@@ -15,6 +16,14 @@ E=8 Euler steps, path order 4, markov rank 256) on a 248,320-row target head res
 the flow at the VAE latent width 640 (8 blocks, 2 Euler steps) between the TransformerHiddenVAE
 encoder and decoder (intermediate 1920, 2 layers each, 8 heads), same head and beam; its
 ``roofline`` covers the whole predict_hidden pass (encode, flow, decode).
+
+``--workload verify`` times the tree-verify kernels at the tree-draft shapes, each launch alone on
+resident inputs: the tree GDN state update with every node's state written (16
+heads, dk = dv = 128, bf16 q/k/v, fp32 states; a 31-node tree of depth 5) -- its time is ``value`` and its bytes the
+``roofline`` -- and, in ``breakdown_us``, the serving GDN (bf16 slots), the width-4 tree conv
+(6144 channels), the tree attention + prefix merge (40 nodes: 8 per level over 5 levels, 16 heads
+over 4 kv heads, D 256, bf16) and the greedy accept on the same tree (41 rows of a 248,320-token
+vocabulary).
 
 Prints one JSON line.  ``roofline`` covers the flow pass (the dominant part, ~96% of the bytes),
 timed with HIP events on the stream it runs on; ``cpu_baseline`` is the CPU oracle timed on a
@@ -204,12 +213,113 @@ def cpu_baseline(W, cfg, sl, d):
                        f"({t_head * 1e3:.0f} ms); scaled by E*L={E * L}, L={L}, K={K}")}
 
 
+def verify_bench(dev, iters=200, warmup=20):
+    """Per-launch times (us, HIP events over `iters` back-to-back launches) of the tree-verify kernels."""
+    import ctypes as C
+    import numpy as np
+    import torch
+    from chain_flow_amd import _lib
+    L = _lib.lib()
+    st = _lib.stream_handle()
+    g = torch.Generator(device="cpu").manual_seed(5)
+    bf = lambda *sh: torch.randn(*sh, generator=g).to(torch.bfloat16).to(dev)
+
+    parent = np.array([-1] + [(i - 1) // 2 for i in range(1, 31)])   # 31 nodes: depth 5, two children each
+    N, H, Dk, Dv = len(parent), 16, 128, 128
+    par_d = torch.as_tensor(parent).to(dev, torch.int32)
+    q, k, v = bf(N, H, Dk), bf(N, H, Dk), bf(N, H, Dv)
+    gg = torch.nn.functional.logsigmoid(torch.randn(N, H, generator=g)).to(dev)
+    beta = torch.rand(N, H, generator=g).to(dev)
+    S0 = (torch.randn(H, Dk, Dv, generator=g) * 0.1).to(dev)
+    out = torch.empty(N, H, Dv, device=dev)
+    states = torch.empty(N, H, Dk, Dv, device=dev)
+    # serving form: mixed_qkv rows, bf16 value-major slots
+    HV = H
+    mixed = bf(N, 2 * H * Dk + HV * Dv)
+    a_, b_ = bf(N, HV), bf(N, HV)
+    A_log, dt_bias = torch.randn(HV, generator=g).to(dev), torch.randn(HV, generator=g).to(dev)
+    slots = torch.zeros(N + 2, HV, Dv, Dk, dtype=torch.bfloat16, device=dev)
+    node_slots = torch.arange(2, N + 2, dtype=torch.int32, device=dev)
+    o_vllm = torch.empty(N, HV, Dv, dtype=torch.bfloat16, device=dev)
+    # tree conv over the GDN input channels
+    dim = 2 * H * Dk + HV * Dv
+    cx, cw, cb = bf(N, dim), bf(dim, 4), bf(dim)
+    cst = bf(N + 2, dim, 4)
+    cout = torch.empty(N, dim, dtype=torch.bfloat16, device=dev)
+    # tree attention: one request, 40 nodes, 16 q heads over 4 kv heads, D 256
+    TN, TH, THk, TD = 40, 16, 4, 256
+    tq, tk, tv = bf(TN, TH, TD), bf(TN, THk, TD), bf(TN, THk, TD)
+    tout, tpo = bf(TN, TH, TD), bf(TN, TH, TD)
+    tpl = (torch.randn(TH, TN, generator=g) + 3).to(dev)
+    # the shipped tree shape: keep 8 x depth 5 in BFS order, 8 roots, each later level's parents drawn
+    # from the level above (at most 5 tree columns per row)
+    trng = np.random.default_rng(1)
+    tpar = np.array([-1] * 8 + [int(8 * (i // 8 - 1) + trng.integers(0, 8)) for i in range(8, TN)])
+    nanc = np.ones((1, TN, TN), dtype=np.uint8)
+    for n in range(TN):
+        m = n
+        while m >= 0:
+            nanc[0, n, m] = 0
+            m = tpar[m]
+    tidx = torch.arange(TN, dtype=torch.int32, device=dev)
+    tmask = torch.as_tensor(nanc).to(dev)
+    # greedy accept: 41 rows of the full vocabulary
+    V = VOCAB
+    logits = bf(TN + 1, V)
+    cu_d = torch.tensor([TN], dtype=torch.int32, device=dev)
+    cu_s = torch.tensor([TN + 1], dtype=torch.int32, device=dev)
+    dids = torch.randint(0, V, (TN,), generator=g).to(dev, torch.int32)
+    dpar = torch.as_tensor(tpar).to(dev, torch.int32)
+    otok = torch.empty(1, TN + 1, dtype=torch.int32, device=dev)
+    opath = torch.empty(1, TN, dtype=torch.int32, device=dev)
+    olen = torch.empty(1, dtype=torch.int32, device=dev)
+    ra = torch.empty(TN + 1, dtype=torch.int32, device=dev)
+    aws = torch.empty(int(L.cfh_tree_accept_ws_bytes(TN + 1)), dtype=torch.uint8, device=dev)
+    kern = {
+        "gdn_tree_with_states": lambda: L.cfh_gdn_tree(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), gg.data_ptr(), beta.data_ptr(), S0.data_ptr(),
+            par_d.data_ptr(), N, H, Dk, Dv, 1, 0, out.data_ptr(), states.data_ptr(), st),
+        "gdn_tree_outputs_only": lambda: L.cfh_gdn_tree(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), gg.data_ptr(), beta.data_ptr(), S0.data_ptr(),
+            par_d.data_ptr(), N, H, Dk, Dv, 1, 0, out.data_ptr(), None, st),
+        "gdn_serving_bf16_slots": lambda: L.cfh_gdn_tree_vllm(
+            mixed.data_ptr(), a_.data_ptr(), b_.data_ptr(), A_log.data_ptr(), dt_bias.data_ptr(), slots.data_ptr(), 1,
+            node_slots.data_ptr(), par_d.data_ptr(), 1, N, H, HV, Dk, Dv, 1, C.c_float(Dk ** -0.5), o_vllm.data_ptr(),
+            st),
+        "tree_conv": lambda: L.cfh_tree_conv(
+            cx.data_ptr(), dim, cst.data_ptr(), cw.data_ptr(), cb.data_ptr(), node_slots.data_ptr(), par_d.data_ptr(),
+            1, N, dim, 1, cout.data_ptr(), dim, st),
+        "tree_attn_merge": lambda: L.cfh_tree_attn_merge(
+            tq.data_ptr(), TH * TD, tk.data_ptr(), THk * TD, tv.data_ptr(), THk * TD, tout.data_ptr(), TH * TD,
+            tpo.data_ptr(), tpl.data_ptr(), tidx.data_ptr(), tmask.data_ptr(), C.c_float(TD ** -0.5), 1, TN, TH, THk,
+            TD, 1, st),
+        "tree_greedy_accept": lambda: L.cfh_tree_greedy_accept(
+            logits.data_ptr(), V, V, TN + 1, 1, cu_d.data_ptr(), cu_s.data_ptr(), dids.data_ptr(), dpar.data_ptr(), 1,
+            TN, otok.data_ptr(), opath.data_ptr(), olen.data_ptr(), ra.data_ptr(), aws.data_ptr(), st),
+    }
+    res = {}
+    for name, fn in kern.items():
+        for _ in range(warmup):
+            _lib.check(fn(), name)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        res[name] = e0.elapsed_time(e1) * 1e3 / iters
+    gdn_bytes = (H * Dk * Dv * 4 + 3 * N * H * Dk * 2 + 2 * N * H * 4 + N * H * Dv * 4 + N * H * Dk * Dv * 4
+                 + N * 4)
+    return res, gdn_bytes, N
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["target", "latent"], default="target",
+    ap.add_argument("--workload", choices=["target", "latent", "verify"], default="target",
                     help="target: the flow at the target width d (default); latent: the shipped 4B "
                          "latent drafter (hidden 2560, VAE latent 640, 8 blocks, 2 Euler steps)")
     ap.add_argument("--d", type=int, default=None, help="target hidden size (5120; latent: 2560)")
@@ -231,6 +341,24 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.workload == "verify":
+        res, gb, N = verify_bench(dev)
+        t = res["gdn_tree_with_states"]
+        out = {
+            "metric": "us per tree GDN state update with states (31-node tree, 16 heads, dk=dv=128)",
+            "value": round(t, 2), "unit": "us per launch", "n_gpus": 1, "steps": 200, "warmup": 20,
+            "ms_per_step": round(t / 1e3, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+            "dtype": "fp32 state, bf16 q/k/v", "data": "synthetic (seeded)",
+            "config": {"workload": f"tree verify kernels: {N}-node tree GDN (16 heads, dk=dv=128), serving "
+                                   f"GDN bf16 slots, tree conv 6144 channels, tree attention 40 nodes x 16/4 heads "
+                                   f"D 256 bf16, greedy accept 41 x {VOCAB}"},
+            "breakdown_us": {k: round(v, 2) for k, v in res.items()},
+            "roofline": {"bound": "hbm", "achieved": round(gb / (t * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gb / (t * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                         "kernel": "cfh_gdn_tree (states written)", "algorithmic_bytes": gb},
+        }
+        print(json.dumps(out), flush=True)
+        return
     latent = args.workload == "latent"
     d = args.d or (2560 if latent else 5120)
     L = args.layers

@@ -45,6 +45,12 @@ SIGNATURES = {
     "cfh_vae_encode": (_I, [C.POINTER(VaeDims), _VP, _VP, _VP, _I, _I, _VP, _VP]),
     "cfh_vae_decode": (_I, [C.POINTER(VaeDims), _VP, _VP, _VP, _I, _I, _VP, _VP]),
     "cfh_ring_step": (_I, [_VP, _VP, _VP, _I, _I, _VP, _I, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _VP, _VP]),
+    "cfh_tree_conv": (_I, [_VP, _I, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _VP, _I, _VP]),
+    "cfh_tree_attn_merge": (_I, [_VP, _I, _VP, _I, _VP, _I, _VP, _I, _VP, _VP, _VP, _VP, C.c_float, _I, _I, _I, _I,
+                                 _I, _I, _VP]),
+    "cfh_tree_accept_ws_bytes": (_I64, [_I]),
+    "cfh_tree_greedy_accept": (_I, [_VP, C.c_longlong, _I, _I, _I, _VP, _VP, _VP, _VP, _I, _I, _VP, _VP, _VP, _VP,
+                                    _VP, _VP]),
     "cfh_head_logits": (_I, [_VP, _I, _I, _VP, _VP, _I, _VP, _VP, _I, _I, _VP, _VP, _VP]),
     "cfh_row_topk": (_I, [_VP, _I, _I, _I, _VP, _VP, _VP, _VP]),
     "cfh_head_ws_bytes": (_I64, [_I, _I, _I]),

@@ -263,6 +263,44 @@ int cfh_gdn_tree_vllm(const void* mixed_qkv, const void* a, const void* b, const
                       const int32_t* parent, int prefix_slot, int N, int H, int HV, int K, int V,
                       int use_l2norm, float scale, void* out, void* stream);
 
+/* ---------------------------------------------------------------- rest of the tree verify
+ * Tree causal conv1d, width 4 (cf/vllm_tree/tree_ssm.py:393-438; depth form :189-253): node n
+ * (BFS order, parent [N] node index, -1 = root) sees the last three inputs of its root->node path,
+ * the prefix slot's state before the root; out = act(bias + bf16(s0 w0) + bf16(s1 w1) +
+ * bf16(s2 w2) + bf16(x w3)) with fp32 accumulation left to right, act = SiLU (silu = 1) or none;
+ * the node's state (s1, s2, x, s3) goes to slot node_slots[n].  x [N][x_ld], out [N][out_ld],
+ * conv_state [slots][dim][4], weight [dim][4], bias [dim] (or NULL): all bf16. */
+int cfh_tree_conv(const void* x, int x_ld, void* conv_state, const void* weight, const void* bias,
+                  const int32_t* node_slots, const int32_t* parent, int prefix_slot, int N, int dim, int silu,
+                  void* out, int out_ld, void* stream);
+
+/* The draft-tree rows' ancestor-masked attention merged with the shared-prefix half
+ * (_tree_suffix_eager + merge_attn_states, patch lines 529-575; fused form tree_attn_fused.cu):
+ * per request s, node n, head h: softmax over the nodes m with not_anc[s][n][m] == 0 of
+ * scale * q[idx[s][n]][h] . k[idx[s][m]][h / (H/Hkv)] (fp32), P.V in fp32 rounded to the element
+ * type, lse_s = max + log(sum); then merged with prefix_out [S*N][H][D] / prefix_lse [H][S*N]
+ * (fp32) by the log-sum-exp rule and written to out[idx[s][n]][h].  q/k/v/out rows are [.][heads][D]
+ * with row strides q_ld/k_ld/v_ld/o_ld (elements); bf16 (is_bf16) or fp16; D in {64, 128, 256};
+ * N <= 128; pointers and strides aligned to D/32 bytes (each lane reads D/64 elements at once). */
+int cfh_tree_attn_merge(const void* q, int q_ld, const void* k, int k_ld, const void* v, int v_ld, void* out,
+                        int o_ld, const void* prefix_out, const float* prefix_lse, const int32_t* idx,
+                        const uint8_t* not_anc, float scale, int S, int N, int H, int Hkv, int D, int is_bf16,
+                        void* stream);
+
+/* Greedy tree verify (tree_rejection_sample + tree_greedy_descent_kernel, patch lines 433-550):
+ * row_argmax[r] = first arg-max of logits row r (n_rows rows of V, row stride ld, bf16 or fp16);
+ * then per request b (its rows s0 = cu_sampled[b] - n - 1 .. with n = its draft count from
+ * cu_draft, inclusive cumulative counts): from the root row, emit the target's token, step to the
+ * first child (parents: local parent, -1 = root) whose draft token equals it, repeat.
+ * out_tokens [B][max_spec+1] (accepted drafts + the bonus, -1 padded), accepted_path
+ * [B][max_spec] (node per depth, -1 padded), accepted_len [B]; row_argmax [n_rows] receives the
+ * arg-max of every row of the B requests; ws: cfh_tree_accept_ws_bytes(n_rows) bytes. */
+int64_t cfh_tree_accept_ws_bytes(int n_rows);
+int cfh_tree_greedy_accept(const void* logits, long long ld, int V, int n_rows, int is_bf16, const int32_t* cu_draft,
+                           const int32_t* cu_sampled, const int32_t* draft_ids, const int32_t* parents, int B,
+                           int max_spec, int32_t* out_tokens, int32_t* accepted_path, int32_t* accepted_len,
+                           int32_t* row_argmax, void* ws, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -69,6 +69,18 @@ def head_bytes(d, K, W, n_rows, rank=256, order=4, path_ffn=2):
     return total
 
 
+def head_bytes_twopass(d, K, M, n_rows, rank=256, order=4, path_ffn=2):
+    """Two-pass head over K depths: pass A reads the shortlist rows of lm_head once (the K marginal
+    hiddens together); each depth reads its M candidate rows of lm_head and markov w2 in place, plus
+    the PathHead weights as in the one-pass head."""
+    total = n_rows * d * 2
+    for s in range(1, K + 1):
+        nlive = min(s, order)
+        total += M * d * 2 + M * rank * 2
+        total += (nlive * d * d + 2 * path_ffn * d * d) * 2
+    return total
+
+
 def measured_traffic(d, L, E):
     """HBM bytes per flow pass from the committed counter profile of this workload (FETCH_SIZE and
     WRITE_SIZE, calibrated with a 1 GiB copy), or None for a workload without one."""
@@ -90,7 +102,7 @@ def vae_bytes(hidden, latent=LATENT, inter=VAE_INTER, layers=VAE_LAYERS, rows=8)
     return 2 * (half(hidden, latent) + half(latent, hidden)) + 2 * rows * (hidden + latent) * 2
 
 
-def build_workload(d, L, E, device, latent=False):
+def build_workload(d, L, E, device, latent=False, twopass=0):
     import torch
     from chain_flow_amd.config import TreeVAEFlowConfig, flownet
     from chain_flow_amd.drafter import Drafter
@@ -106,7 +118,7 @@ def build_workload(d, L, E, device, latent=False):
         cfg = flownet(d, layers=L, flow_steps=E)
     W = make_weights(cfg, VOCAB, init="baseline", dtype=torch.float16, device=device, base_seed=0, hidden=d)
     sl = synthetic(VOCAB, SHORTLIST_ROWS, seed=2)
-    dr = Drafter(cfg, W, sl.to(device), device=device)
+    dr = Drafter(cfg, W, sl.to(device), device=device, twopass_m=twopass)
     ctx = synthetic_context(1, cfg.context_size, d, seed=1).to(device)
     known0 = sl[1234:1235].long().to(device)
     return cfg, W, dr, ctx, known0
@@ -325,6 +337,8 @@ def main():
     ap.add_argument("--d", type=int, default=None, help="target hidden size (5120; latent: 2560)")
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--flow-steps", type=int, default=None, help="Euler steps (8; latent: 2)")
+    ap.add_argument("--twopass", type=int, default=0,
+                    help="two-pass candidate head with M candidates (0: the one-pass head of the metric)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calib-copy", action="store_true",
                     help="after timing, copy one 1 GiB buffer (a kernel of known traffic for calibrating "
@@ -365,7 +379,7 @@ def main():
     E = args.flow_steps or (2 if latent else 8)
     K, Wd = 5, 4
     print(f"[bench] building workload {args.workload} d={d} L={L} E={E}", file=sys.stderr, flush=True)
-    cfg, W, dr, ctx, known0 = build_workload(d, L, E, dev, latent=latent)
+    cfg, W, dr, ctx, known0 = build_workload(d, L, E, dev, latent=latent, twopass=args.twopass)
     torch.cuda.synchronize()
 
     def step():
@@ -406,7 +420,10 @@ def main():
         workload = (f"chain draft d={d} fp16 bs1 K={K} width {Wd}, flow L={L} E={E} "
                     f"2 chunk experts, shortlisted head {SHORTLIST_ROWS}x{d}")
         metric = "us per 5-token draft step (d=5120, bs1) + achieved HBM GB/s vs roofline"
-    hb = head_bytes(d, K, Wd, SHORTLIST_ROWS)
+    hb = (head_bytes_twopass(d, K, args.twopass, SHORTLIST_ROWS) if args.twopass
+          else head_bytes(d, K, Wd, SHORTLIST_ROWS))
+    if args.twopass:
+        workload += f", two-pass head M={args.twopass} shared"
     flow_gbs = fb / (med(flow_ms) * 1e-3) / 1e9
     out = {
         "metric": metric,

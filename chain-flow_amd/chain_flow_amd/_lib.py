@@ -51,6 +51,8 @@ SIGNATURES = {
     "cfh_tree_accept_ws_bytes": (_I64, [_I]),
     "cfh_tree_greedy_accept": (_I, [_VP, C.c_longlong, _I, _I, _I, _VP, _VP, _VP, _VP, _I, _I, _VP, _VP, _VP, _VP,
                                     _VP, _VP]),
+    "cfh_cand_ws_bytes": (_I64, [_I, _I]),
+    "cfh_cand_topm": (_I, [_VP, C.c_longlong, _VP, _I, _I, _I, _I, _VP, _VP, _VP, _VP, _VP]),
     "cfh_head_logits": (_I, [_VP, _I, _I, _VP, _VP, _I, _VP, _VP, _I, _I, _VP, _VP, _VP]),
     "cfh_row_topk": (_I, [_VP, _I, _I, _I, _VP, _VP, _VP, _VP]),
     "cfh_head_ws_bytes": (_I64, [_I, _I, _I]),

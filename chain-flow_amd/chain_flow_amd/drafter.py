@@ -30,8 +30,15 @@ def front_pad(hidden: torch.Tensor, context_size: int) -> torch.Tensor:
 
 
 class Drafter:
+    """``twopass_m`` > 0 switches the beam searches to the two-pass candidate head
+    (``cf/vllm_plugin/flow_proposer.py:1113-1184``): one head pass over the marginal hiddens of every
+    depth picks M shortlist rows (``twopass_shared``: one set for all depths, else one per depth;
+    ``twopass_seed``: scored with the seed path's residual and markov bias), and each depth
+    rescores only those rows, renormalised over them."""
+
     def __init__(self, cfg: TreeFlowConfig, weights: dict, shortlist: torch.Tensor | None, device="cuda",
-                 path_trim: bool = True):
+                 path_trim: bool = True, twopass_m: int = 0, twopass_shared: bool = True,
+                 twopass_seed: bool = False):
         self.cfg = cfg
         dev = torch.device(device)
         if dev.type == "cuda" and dev.index is None:
@@ -52,6 +59,56 @@ class Drafter:
         self.head = ShortlistHead(weights["lm_head.weight"].to(dev, torch.float16), shortlist,
                                   weights["markov.w1.weight"], weights["markov.w2.weight"])
         self.order = cfg.path_order
+        if twopass_m and not 0 < twopass_m < self.head.n:
+            raise ValueError(f"two-pass M={twopass_m} must be below the head's {self.head.n} rows")
+        self.twopass_m, self.twopass_shared, self.twopass_seed = int(twopass_m), bool(twopass_shared), \
+            bool(twopass_seed)
+
+    def _pass_a(self, pred: torch.Tensor, lastp: torch.Tensor, n0: int, n1: int, width: int):
+        """Candidate rows of depths n0..n1-1: global ids [B, n1-n0, M] (a shared set repeated)."""
+        B = pred.shape[0]
+        sr = sp = None
+        if self.twopass_seed:
+            res0 = torch.empty(B * width, pred.shape[-1], dtype=torch.float16, device=self.device)
+            for b in range(B):
+                self.path.hidden(lastp[b], self._nlive(1), torch.zeros_like(pred[b, 0]),
+                                 out=res0[b * width:(b + 1) * width])
+            sr = res0.view(B, width, -1)[:, 0]
+            sp = lastp[:, 0, 0]
+        _, glob = self.head.candidates(pred[:, n0:n1].contiguous(), self.twopass_m, self.twopass_shared, sr, sp)
+        if self.twopass_shared:
+            glob = glob[:, None].expand(B, n1 - n0, self.twopass_m)
+        return glob
+
+    def _candidate_image(self, cands, B):
+        """One request with a shared candidate set: its rows packed once for every depth."""
+        if cands is None or B != 1 or not self.twopass_shared:
+            return None
+        self._cimg = self.head.pack_rows(cands[0, 0].contiguous(), getattr(self, "_cimg", None))
+        return self._cimg
+
+    def _scores(self, rows: torch.Tensor, k: int, prev: torch.Tensor, order: int, cand: torch.Tensor | None, B: int,
+                image: torch.Tensor | None = None):
+        """Per-depth top-k of rows [B*F, d]: (vals [B*F, k], ids [B*F, k] int32, map) -- one-pass over the
+        shortlist (ids shortlist-local, map = the shortlist), two-pass over one request's packed
+        candidate image (ids local to the candidates, map = their global ids), or over each
+        request's candidate rows read in place (ids already global, map None)."""
+        if cand is None:
+            vals, ids, _ = self.head.topk(rows, k, prev=prev, prev_stride=order)
+            return vals, ids, self.head.sl
+        if image is not None:
+            vals, ids, _ = self.head.topk_image(rows, k, image, cand.shape[-1], prev=prev, prev_stride=order)
+            return vals, ids, cand[0]
+        F = rows.shape[0] // B
+        vals = torch.empty(B * F, k, dtype=torch.float32, device=rows.device)
+        ids = torch.empty(B * F, k, dtype=torch.int32, device=rows.device)
+        for b in range(B):
+            cb = cand[b].contiguous()
+            v, i, _ = self.head.topk_rows(rows[b * F:(b + 1) * F], k, cb, prev=prev[b * F * order:],
+                                          prev_stride=order)
+            vals[b * F:(b + 1) * F] = v
+            ids[b * F:(b + 1) * F] = cb[i.long()]
+        return vals, ids, None
 
     def _nlive(self, depth: int):
         """``_nlive`` (``cf/vllm_plugin/flow_proposer.py:1030-1037``)."""
@@ -88,12 +145,15 @@ class Drafter:
         hbuf = torch.empty(B * W, d, dtype=torch.float16, device=dev)
         L = _lib.lib()
         st = _lib.stream_handle()
+        cands = self._pass_a(pred, lastp, 1, steps, W) if self.twopass_m and steps > 1 else None
+        image = self._candidate_image(cands, B)
         for step in range(1, steps):
             for b in range(B):
                 self.path.hidden(lastp[b], self._nlive(step), pred[b, step], out=hbuf[b * W:(b + 1) * W])
-            vals, ids, _ = self.head.topk(hbuf, W, prev=lastp.view(B * W, order), prev_stride=order)
+            vals, ids, smap = self._scores(hbuf, W, lastp.view(-1), order,
+                                           None if cands is None else cands[:, step - 1], B, image)
             _lib.check(L.cfh_beam_chain_step(vals.data_ptr(), ids.data_ptr(), cum.data_ptr(), lastp.data_ptr(),
-                                             _lib.ptr(self.head.sl), toks[step - 1].data_ptr(),
+                                             _lib.ptr(smap), toks[step - 1].data_ptr(),
                                              bps[step - 1].data_ptr(), B, W, order, st), "cfh_beam_chain_step")
         out = torch.empty(B, nst, dtype=torch.int64, device=dev)
         if nst > 0:
@@ -128,6 +188,8 @@ class Drafter:
         hbuf = torch.empty(B * keep, d, dtype=torch.float16, device=dev)
         L = _lib.lib()
         st = _lib.stream_handle()
+        cands = self._pass_a(pred, lastp, 1, nstep + 1, keep) if self.twopass_m and nstep > 0 else None
+        image = self._candidate_image(cands, B)
         fr, base = 1, 0
         for step in range(1, nstep + 1):
             rows = torch.empty(B * fr, d, dtype=torch.float16, device=dev) if fr != keep else hbuf
@@ -135,9 +197,10 @@ class Drafter:
             for b in range(B):
                 self.path.hidden(lp_rows[b * fr:(b + 1) * fr], self._nlive(step), pred[b, step],
                                  out=rows[b * fr:(b + 1) * fr])
-            vals, ids, _ = self.head.topk(rows, topb, prev=lp_rows, prev_stride=order)
+            vals, ids, smap = self._scores(rows, topb, lp_rows.view(-1), order,
+                                           None if cands is None else cands[:, step - 1], B, image)
             _lib.check(L.cfh_beam_tree_step(vals.data_ptr(), ids.data_ptr(), cum.data_ptr(), lastp.data_ptr(),
-                                            prev_ids.data_ptr(), _lib.ptr(self.head.sl), out.data_ptr(), 2 * N,
+                                            prev_ids.data_ptr(), _lib.ptr(smap), out.data_ptr(), 2 * N,
                                             base, B, fr, topb, keep, order, st), "cfh_beam_tree_step")
             base += sizes[step - 1]
             fr = sizes[step - 1]

@@ -112,6 +112,96 @@ class ShortlistHead:
             "cfh_head_topk")
         return vals, ids, lse
 
+    def candidates(self, hm: torch.Tensor, M: int, shared: bool = True, seed_res: torch.Tensor | None = None,
+                   seed_prev: torch.Tensor | None = None):
+        """Pass A of the two-pass head (``_candidates``, ``cf/vllm_plugin/flow_proposer.py:1142-1165``):
+        hm [B, n, d] fp16 marginal hiddens of n depths -> (local [B, M] or [B, n, M] int32 ascending
+        shortlist columns, global ids of the same shape).  shared: one set per request by the best
+        per-depth log-prob; else one set per depth.  seed_res [B, d] / seed_prev [B] (global ids):
+        the seed path's residual and markov parent added to every row."""
+        B, n, d = hm.shape
+        dev = hm.device
+        if not 0 < M < self.n:
+            raise ValueError(f"two-pass M={M} must be in (0, {self.n})")
+        rows = hm if seed_res is None else (hm.float() + seed_res.float()[:, None]).to(torch.float16)
+        rows = rows.reshape(B * n, d).contiguous()
+        prev = None if seed_prev is None else seed_prev.to(dev, torch.int32).repeat_interleave(n).contiguous()
+        logits = torch.empty(B * n, self.n, dtype=torch.float16, device=dev)
+        lse = torch.empty(B * n, dtype=torch.float32, device=dev)
+        for r0 in range(0, B * n, 8):                      # the head takes at most 8 rows a launch
+            r1 = min(B * n, r0 + 8)
+            self.topk(rows[r0:r1], 1, prev=None if prev is None else prev[r0:r1], logits=logits[r0:r1],
+                      out=(torch.empty(r1 - r0, 1, device=dev), torch.empty(r1 - r0, 1, dtype=torch.int32,
+                                                                               device=dev), lse[r0:r1]))
+        nreq, nrow = (B, n) if shared else (B * n, 1)
+        local = torch.empty(nreq, M, dtype=torch.int32, device=dev)
+        glob = torch.empty(nreq, M, dtype=torch.int32, device=dev)
+        L = _lib.lib()
+        ws = torch.empty(int(L.cfh_cand_ws_bytes(nreq, self.n)), dtype=torch.uint8, device=dev)
+        _lib.check(L.cfh_cand_topm(logits.data_ptr(), self.n, lse.data_ptr(), nreq, nrow, self.n, M,
+                                   _lib.ptr(self.sl), local.data_ptr(), glob.data_ptr(), ws.data_ptr(),
+                                   _lib.stream_handle()), "cfh_cand_topm")
+        if not shared:
+            local, glob = local.view(B, n, M), glob.view(B, n, M)
+        return local, glob
+
+    def pack_rows(self, rows: torch.Tensor, image: torch.Tensor | None = None) -> torch.Tensor:
+        """The given global rows of lm_head and markov w2 (int32 [M]) gathered once into the MFMA
+        fragment order (``cfh_head_pack``): the two-pass head's shared candidate image, read by
+        ``topk_image`` at every depth (``_gather_cand``, ``flow_proposer.py:1167-1172``)."""
+        n = rows.numel()
+        L = _lib.lib()
+        nbytes = int(L.cfh_head_packed_bytes(n, self.d, self.r))
+        if image is None or image.numel() < nbytes:
+            image = torch.empty(nbytes, dtype=torch.uint8, device=self.lm_w.device)
+        _lib.check(L.cfh_head_pack(self.lm_w.data_ptr(), None if self.w2 is None else self.w2.data_ptr(),
+                                   rows.data_ptr(), n, self.d, self.r, image.data_ptr(), _lib.stream_handle()),
+                   "cfh_head_pack")
+        return image
+
+    def topk_image(self, h: torch.Tensor, k: int, image: torch.Tensor, n: int, prev: torch.Tensor | None = None,
+                   prev_stride: int = 1):
+        """``topk`` over a ``pack_rows`` image of n rows: ids are positions in those rows."""
+        Mh = h.shape[0]
+        dev = h.device
+        vals = torch.empty(Mh, k, dtype=torch.float32, device=dev)
+        ids = torch.empty(Mh, k, dtype=torch.int32, device=dev)
+        lse = torch.empty(Mh, dtype=torch.float32, device=dev)
+        key = ("image", Mh, n, k)
+        ws = self._ws.get(key)
+        if ws is None:
+            ws = self._ws[key] = torch.empty(int(_lib.lib().cfh_head_ws_bytes(Mh, n, k)), dtype=torch.uint8,
+                                             device=dev)
+        use_m = self.w1 is not None and prev is not None
+        _lib.check(_lib.lib().cfh_head_topk_packed(
+            h.data_ptr(), Mh, self.d, image.data_ptr(), n, self.w1.data_ptr() if use_m else None,
+            prev.data_ptr() if use_m else None, prev_stride, self.r if use_m else 0, k, None, vals.data_ptr(),
+            ids.data_ptr(), lse.data_ptr(), ws.data_ptr(), _lib.stream_handle()), "cfh_head_topk_packed")
+        return vals, ids, lse
+
+    def topk_rows(self, h: torch.Tensor, k: int, rows: torch.Tensor, prev: torch.Tensor | None = None,
+                  prev_stride: int = 1):
+        """Pass B (``_rescore`` + topk): the head and markov bias over the given global rows only
+        (int32 [M], read in place), log-softmax over those M columns, top-k.
+        -> (vals [Mh, k] f32, ids [Mh, k] int32 positions in ``rows``, lse [Mh])."""
+        Mh, n = h.shape[0], rows.numel()
+        dev = h.device
+        vals = torch.empty(Mh, k, dtype=torch.float32, device=dev)
+        ids = torch.empty(Mh, k, dtype=torch.int32, device=dev)
+        lse = torch.empty(Mh, dtype=torch.float32, device=dev)
+        key = ("rows", Mh, n, k)
+        ws = self._ws.get(key)
+        if ws is None:
+            ws = self._ws[key] = torch.empty(int(_lib.lib().cfh_head_ws_bytes(Mh, n, k)), dtype=torch.uint8,
+                                             device=dev)
+        use_m = self.w1 is not None and prev is not None
+        _lib.check(_lib.lib().cfh_head_topk(
+            h.data_ptr(), Mh, self.d, self.lm_w.data_ptr(), rows.data_ptr(), n,
+            self.w1.data_ptr() if use_m else None, prev.data_ptr() if use_m else None, prev_stride,
+            self.r, self.w2.data_ptr() if use_m else None, k, None, vals.data_ptr(), ids.data_ptr(),
+            lse.data_ptr(), ws.data_ptr(), _lib.stream_handle()), "cfh_head_topk")
+        return vals, ids, lse
+
 
 class GemmHead:
     """Batched shortlisted head for many rows (M up to 256): bf16 MFMA skinny GEMM over the

@@ -15,6 +15,9 @@ Mirrors ``chain_flow.vllm_plugin.flow_proposer.FlowDrafterProposer`` (``cf/vllm_
   ``list[list[int]]`` (``:1698``, ``:2494-2569``), or with ``CF_ASYNC_SPEC=1`` the GPU int32 tensor
   ``[num_reqs, draft_width]`` indexed by batch row with no host read (``_async_draft_tensor``,
   ``:2326-2357``);
+* the head is the two-pass candidate head by default (``CF_TWOPASS_M=8192``, ``CF_TWOPASS_SHARED=1``,
+  ``CF_TWOPASS_SEED=0``; ``:1113-1184``, ``cf/defaults.py:123-127``), dropped when M does not fit
+  the head unless it was asked for;
 * the context lives in a device ring per batch slot (``_ring_write`` / ``_ring_gather``,
   ``:916-961``; ``cfh_ring_step``), with the slot lifecycle of ``_ctx_gpu`` (``:2045-2105``: a new
   request resets or seeds its slot, a request moved by vLLM's batch condense carries its history),
@@ -188,6 +191,13 @@ class FlowDrafterProposer:
         self.max_reqs = int(vllm_config.scheduler_config.max_num_seqs)
         self.path_trim = os.environ.get("CF_PATH_TRIM", "1") != "0"
         self.use_cg = os.environ.get("CF_CUDAGRAPH", "1") == "1"
+        # two-pass candidate head, on by default as in the reference's defaults table
+        # (cf/defaults.py:123-127): M = CF_TWOPASS_M (8192), one candidate set for all depths
+        # (CF_TWOPASS_SHARED=1), pass A on the bare marginals (CF_TWOPASS_SEED=0)
+        self._twopass_explicit = "CF_TWOPASS_M" in os.environ
+        self.twopass_m = int(os.environ.get("CF_TWOPASS_M", "8192") or 0)
+        self.twopass_shared = os.environ.get("CF_TWOPASS_SHARED", "1") == "1"
+        self.twopass_seed = os.environ.get("CF_TWOPASS_SEED", "0") == "1"
         self.async_spec = os.environ.get("CF_ASYNC_SPEC", "0") == "1"
         self.drafter: Drafter | None = None
         self._target = None
@@ -244,8 +254,16 @@ class FlowDrafterProposer:
         explicit = self.shortlist_path if "CF_SHORTLIST" in os.environ else None
         sl, self.shortlist_source = resolve_shortlist(self.ckd, V, explicit)
         self.cfg = cfg
+        rows = V if sl is None else int(sl.numel())
+        if self.twopass_m >= rows:
+            # a two-pass head as wide as the head it narrows buys nothing: refuse an explicit
+            # request, quietly drop the default (flow_proposer.py:766-775)
+            if self._twopass_explicit:
+                raise ValueError(f"CF_TWOPASS_M={self.twopass_m} >= head rows {rows}")
+            self.twopass_m, self.twopass_shared = 0, False
         self.drafter = Drafter(cfg, weights, None if sl is None else sl.to(self.dev), device=self.dev,
-                               path_trim=self.path_trim)
+                               path_trim=self.path_trim, twopass_m=self.twopass_m,
+                               twopass_shared=self.twopass_shared, twopass_seed=self.twopass_seed)
         self.ctx_size = cfg.context_size
         # rows one request can append per step: the committed token plus every accepted draft
         self.kmax = (self.tree_depth + 1) if self.branching else (self.K + 1)

@@ -189,6 +189,16 @@ int cfh_head_topk_packed(const void* h, int M, int d, const void* packed, int n,
                          const int32_t* a_ids, int a_ids_stride, int r, int k, void* logits, float* vals,
                          int32_t* ids, float* lse, void* ws, void* stream);
 
+/* Pass A of the two-pass candidate head (FlowDrafterProposer._candidates, flow_proposer.py:
+ * 1142-1165): for each of B requests owning n consecutive rows of fp16 logits [B*n][ld] (over Vs
+ * shortlist columns) with their log-sum-exp lse [B*n], value[j] = max_d (logits[d][j] - lse[d]);
+ * the M columns of largest value (ties to the lower column), ascending, into cand_local [B][M] and,
+ * mapped through the shortlist sl (NULL = identity), cand_global [B][M] (may be NULL).  n = 1
+ * selects per row (the per-depth sets).  ws: cfh_cand_ws_bytes(B, Vs) bytes. */
+int64_t cfh_cand_ws_bytes(int B, int Vs);
+int cfh_cand_topm(const void* logits, long long ld, const float* lse, int B, int n, int Vs, int M, const int32_t* sl,
+                  int32_t* cand_local, int32_t* cand_global, void* ws, void* stream);
+
 /* Batched (M up to 256) bf16 skinny-GEMM head with per-row log-softmax top-k: the two-pass
  * candidate head's pass A (cf/vllm_plugin/flow_proposer.py:1142-1165) as one MFMA kernel plus the
  * candidate merge.  logits[m][j] = bf16(x[m] . W[row_j]), row_j = sl ? sl[j] : j.

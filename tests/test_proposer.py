@@ -164,3 +164,22 @@ def test_vae_dir_resolution(monkeypatch, tmp_path):
     with pytest.raises(FileNotFoundError, match="CF_VAE_DIR") as e:
         load_vae_dir(_latent_cfg(vae_dir=str(tmp_path)))
     assert "neither of the above" in str(e.value)
+
+
+def test_twopass_default_and_explicit_width(monkeypatch, ckpt):
+    """CF_TWOPASS_M defaults to 8192 shared (the reference's defaults table); a default wider than
+    the head is dropped, an explicit one is refused (cf/vllm_plugin/flow_proposer.py:766-775)."""
+    d, cfg, W = ckpt
+    _env(monkeypatch, CF_DRAFTER_DIR=d)
+    for k in ("CF_TWOPASS_M", "CF_TWOPASS_SHARED", "CF_TWOPASS_SEED"):
+        monkeypatch.delenv(k, raising=False)
+    p = fp.FlowDrafterProposer(_vcfg())
+    assert (p.twopass_m, p.twopass_shared, p.twopass_seed) == (8192, True, False)
+    V = 64
+    emb = torch.zeros(V, 512, dtype=torch.float16)
+    monkeypatch.setenv("CF_TWOPASS_M", "100")
+    monkeypatch.setenv("CF_SHORTLIST", "")               # full head: 64 rows
+    q = fp.FlowDrafterProposer(_vcfg())
+    q.bind_target(emb, emb.clone())
+    with pytest.raises(ValueError, match="CF_TWOPASS_M=100 >= head rows 64"):
+        q._build()

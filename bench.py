@@ -3,6 +3,7 @@
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--d 5120] [--layers 8] [--no-cpu]
     python bench.py --workload latent        # the shipped 4B latent drafter (see below)
     python bench.py --workload verify        # the tree-verify kernels at the tree-draft shapes
+    python bench.py --workload gemm          # the batched head: 32 seqs x 5 depths, d=4096 bf16
 
 A step is one whole FlowDrafterProposer chain draft over inputs already resident in HBM:
 ``predict_hidden`` (init_latents + 8 Euler steps of both chunk experts, every block) followed by the
@@ -24,6 +25,11 @@ heads, dk = dv = 128, bf16 q/k/v, fp32 states; a 31-node tree of depth 5) -- its
 (6144 channels), the tree attention + prefix merge (40 nodes: 8 per level over 5 levels, 16 heads
 over 4 kv heads, D 256, bf16) and the greedy accept on the same tree (41 rows of a 248,320-token
 vocabulary).
+
+``--workload gemm`` times the batched-drafting head: 32 sequences x 5 depths = 160 rows at d=4096
+bf16 against the 62,642-row shortlist of a 248,320-row head, MFMA skinny GEMM with the per-row
+log-softmax top-8 fused in (`cfh_head_gemm_topk`); ``roofline`` is HBM (513 MB of head rows) and the
+line also states the MFMA rate against the 2.5 PFLOP/s bf16 dense peak.
 
 Prints one JSON line.  ``roofline`` covers the flow pass (the dominant part, ~96% of the bytes),
 timed with HIP events on the stream it runs on; ``cpu_baseline`` is the CPU oracle timed on a
@@ -326,12 +332,37 @@ def verify_bench(dev, iters=200, warmup=20):
     return res, gdn_bytes, N
 
 
+def gemm_bench(dev, iters=100, warmup=10):
+    import torch
+    from chain_flow_amd.head import GemmHead
+    M, d, V, n, k = 160, 4096, VOCAB, SHORTLIST_ROWS, 8
+    g = torch.Generator(device=dev).manual_seed(4)
+    W = (torch.randn(V, d, generator=g, device=dev) * (4.0 / d ** 0.5)).to(torch.bfloat16)
+    from chain_flow_amd.shortlist import synthetic
+    sl = synthetic(V, n, seed=2).to(dev)
+    x = torch.randn(M, d, generator=g, device=dev).to(torch.bfloat16)
+    head = GemmHead(W, sl)
+    for _ in range(warmup):
+        head.topk(x, k)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        head.topk(x, k)
+    e1.record()
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) * 1e-3 / iters
+    nbytes = n * d * 2 + M * d * 2 + M * k * 8
+    flops = 2.0 * M * n * d
+    return t, nbytes, flops, (M, d, n, k)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["target", "latent", "verify"], default="target",
+    ap.add_argument("--workload", choices=["target", "latent", "verify", "gemm"], default="target",
                     help="target: the flow at the target width d (default); latent: the shipped 4B "
                          "latent drafter (hidden 2560, VAE latent 640, 8 blocks, 2 Euler steps)")
     ap.add_argument("--d", type=int, default=None, help="target hidden size (5120; latent: 2560)")
@@ -355,6 +386,24 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.workload == "gemm":
+        t, nb, fl, (M, d_, n_, k_) = gemm_bench(dev)
+        gbs = nb / t / 1e9
+        out = {
+            "metric": "us per batched head step (32 seqs x 5 depths = 160 rows, d=4096 bf16, shortlist top-8)",
+            "value": round(t * 1e6, 2), "unit": "us per launch", "n_gpus": 1, "steps": 100, "warmup": 10,
+            "ms_per_step": round(t * 1e3, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+            "dtype": "bf16", "data": "synthetic (seeded)",
+            "config": {"workload": f"batched shortlisted head: M={M} rows x {n_}-row shortlist of a {VOCAB}-row "
+                                   f"head, d={d_} bf16, fused log-softmax top-{k_}"},
+            "mfma": {"achieved_tflops": round(fl / t / 1e12, 1), "peak_tflops": 2500.0,
+                     "frac": round(fl / t / 1e12 / 2500.0, 4), "gflop": round(fl / 1e9, 1)},
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "cfh_head_gemm_topk",
+                         "algorithmic_bytes": nb},
+        }
+        print(json.dumps(out), flush=True)
+        return
     if args.workload == "verify":
         res, gb, N = verify_bench(dev)
         t = res["gdn_tree_with_states"]

@@ -385,14 +385,14 @@ __global__ void __launch_bounds__(TK_THREADS) k_topk(TopkArgs a) {
 // each wave streams NT row tiles in place through the shortlist and multiplies every B fragment
 // against the MT 16-row tiles of the activations (v_mfma_f32_16x16x32_bf16), so one weight byte
 // feeds 16*MT rows.  The activations pass through LDS in 128-column chunks, double-buffered: the
-// next chunk's global loads are in flight while the current chunk is multiplied, and the weight
-// fragments of the next chunk are requested before the current chunk's MFMAs.
+// next chunk's loads are in flight while the current one is multiplied.  The weight fragments
+// alternate between two register sets by chunk parity, so each chunk's weights are requested a
+// whole chunk of multiplies ahead.  Two waves a SIMD (GW = 8) keep the accumulators and both sets
+// in registers, and one wave's multiplies run while the other waits.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int GW = 4;             // waves per workgroup
-constexpr int GPF = 4;            // k-steps per LDS chunk = weight prefetch depth
-constexpr int GKC = 32 * GPF;     // 128 columns per chunk
-constexpr int GLD = GKC + 8;      // LDS row stride (elements)
+constexpr int GPF = 4;            // k-steps per LDS chunk
+constexpr int GKC = 32 * GPF;     // 128 columns per chunk: a row is 16 slots of 16 bytes
 
 __device__ __forceinline__ float bf16_round(float x) {
   return (float)(__bf16)x;
@@ -407,9 +407,11 @@ struct GemmArgs {
   int M, d, n, k, nsets;
 };
 
-template <int MT, int NT>
+template <int MT, int NT, int GW>
 __global__ void __launch_bounds__(GW * 64) k_head_gemm(GemmArgs a) {
-  extern __shared__ __align__(16) uint16_t xs[];      // [2][MT*16][GLD]
+  // [2][MT*16][GKC], each row's 16-byte slots XOR-swizzled by the row's low 4 bits: the 16 rows
+  // an MFMA operand read touches then fall on 16 different bank groups
+  extern __shared__ __align__(16) uint16_t xs[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   constexpr int ROWS = MT * 16;
   const int tile0 = (blockIdx.x * GW + wave) * NT;
@@ -422,178 +424,184 @@ __global__ void __launch_bounds__(GW * 64) k_head_gemm(GemmArgs a) {
     wp[t] = (const bf16x8*)(a.W + row * a.d) + (lane >> 4);
   }
   const int nchunks = a.d / GKC;
-  bf16x8 bq[GPF][NT];
+  // two register sets of weight fragments, for even and odd chunks: while chunk c is multiplied
+  // from one set, the other holds chunk c+1 in flight, and each k-step's fragments are reloaded
+  // with chunk c+2's right after their last multiply, in the same registers (nothing is copied at
+  // the loop edge, so no wait drains the loads)
+  bf16x8 bqa[GPF][NT], bqb[GPF][NT];
 #pragma unroll
   for (int p = 0; p < GPF; ++p)
 #pragma unroll
-    for (int t = 0; t < NT; ++t) bq[p][t] = wp[t][p * 4];
-  // x chunk loader: ROWS rows x GKC columns = ROWS*16 vectors of 8; MT per thread
+    for (int t = 0; t < NT; ++t) {
+      bqa[p][t] = wp[t][p * 4];
+      bqb[p][t] = wp[t][(min(1, nchunks - 1) * GPF + p) * 4];
+    }
+  // x chunk: ROWS x 16 vectors of 8, XV a thread (vector idx = row*16 + v); branch-free, rows past
+  // M repeat row M-1 (their products are never read), so the wait counts before the multiplies
+  // count these loads exactly and leave the weight loads in flight
+  constexpr int XV = ROWS * 16 / (GW * 64);
+  static_assert(XV * GW * 64 == ROWS * 16, "x chunk must split evenly over the workgroup");
   auto load_x = [&](int c, bf16x8* xr) {
 #pragma unroll
-    for (int i = 0; i < MT; ++i) {
+    for (int i = 0; i < XV; ++i) {
       const int idx = threadIdx.x + i * GW * 64;
-      const int r = idx >> 4, v = idx & 15;
-      if (r < a.M) {
-        xr[i] = *(const bf16x8*)(a.x + (size_t)r * a.d + c * GKC + v * 8);
-      } else {
-        xr[i] = (bf16x8){};
-      }
+      xr[i] = *(const bf16x8*)(a.x + (size_t)min(idx >> 4, a.M - 1) * a.d + c * GKC + (idx & 15) * 8);
     }
   };
   auto store_x = [&](int buf, const bf16x8* xr) {
-    uint16_t* xb = xs + (size_t)buf * ROWS * GLD;
+    uint16_t* xb = xs + (size_t)buf * ROWS * GKC;
 #pragma unroll
-    for (int i = 0; i < MT; ++i) {
+    for (int i = 0; i < XV; ++i) {
       const int idx = threadIdx.x + i * GW * 64;
-      const int r = idx >> 4, v = idx & 15;
-      *(bf16x8*)(xb + r * GLD + v * 8) = xr[i];
+      const int r = idx >> 4;
+      *(bf16x8*)(xb + r * GKC + ((idx & 15) ^ (r & 15)) * 8) = xr[i];
     }
   };
   {
-    bf16x8 xr[MT];
+    bf16x8 xr[XV];
     load_x(0, xr);
     store_x(0, xr);
   }
-  __syncthreads();
+  lds_barrier();
   f32x4 acc[MT][NT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[mt][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  for (int c = 0; c < nchunks; ++c) {
-    const bool more = c + 1 < nchunks;
-    bf16x8 xr[MT];
-    if (more) load_x(c + 1, xr);
-    const uint16_t* xb = xs + (size_t)(c & 1) * ROWS * GLD;
+  auto step = [&](int c, bf16x8 (&bq)[GPF][NT]) {
+    // chunks past the end are clamped to the last: the x re-read lands in the idle LDS buffer,
+    // which nothing reads again, and the weight re-read is never multiplied
+    bf16x8 xr[XV];
+    load_x(min(c + 1, nchunks - 1), xr);
+    const int cw = min(c + 2, nchunks - 1);
+    const uint16_t* xb = xs + (size_t)(c & 1) * ROWS * GKC + (lane & 15) * GKC;
 #pragma unroll
     for (int p = 0; p < GPF; ++p) {
-      bf16x8 b[NT];
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        b[t] = bq[p][t];
-        if (more) bq[p][t] = wp[t][((c + 1) * GPF + p) * 4];
-      }
+      const int slot = (p * 4 + (lane >> 4)) ^ (lane & 15);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const bf16x8 av = *(const bf16x8*)(xb + (mt * 16 + (lane & 15)) * GLD + p * 32 + 8 * (lane >> 4));
-#pragma unroll
-        for (int t = 0; t < NT; ++t) acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b[t], acc[mt][t], 0, 0, 0);
-      }
-    }
-    if (more) store_x((c + 1) & 1, xr);
-    __syncthreads();
-  }
-  // epilogue: bf16 logits; per wave and row, the top-k of the wave's NT*16 columns and its
-  // (max, sum-exp), parked in LDS; then per row the GW wave lists merge into the block's set.
-  const int g = lane >> 4, col = lane & 15;
-  float* wv = (float*)xs;                                   // [GW][ROWS][k]
-  int* wi = (int*)(wv + (size_t)GW * ROWS * a.k);           // [GW][ROWS][k]
-  float* ws2 = (float*)(wi + (size_t)GW * ROWS * a.k);      // [GW][ROWS][2]
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int r = mt * 16 + 4 * g + q;
-      float v[NT];
-      int ix[NT];
-      float mx = -INFINITY;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const int j = (tile0 + t) * 16 + col;
-        const bool ok = j < a.n && r < a.M;
-        const float lv = bf16_round(acc[mt][t][q]);
-        if (ok && a.logits) a.logits[(size_t)r * a.n + j] = __builtin_bit_cast(uint16_t, (__bf16)lv);
-        v[t] = ok ? lv : -INFINITY;
-        ix[t] = ok ? j : INT_MAX;
-        mx = fmaxf(mx, v[t]);
-      }
-      mx = fmaxf(mx, dpp_f32<DPP_XOR1>(mx));
-      mx = fmaxf(mx, dpp_f32<DPP_XOR2>(mx));
-      mx = fmaxf(mx, dpp_f32<DPP_HMIRROR>(mx));
-      mx = fmaxf(mx, dpp_f32<DPP_MIRROR>(mx));
-      float se = 0.f;
-      if (mx != -INFINITY) {
-#pragma unroll
-        for (int t = 0; t < NT; ++t) se += expf(v[t] - mx);
-      }
-      se = row_sum(se);
-      if (r < a.M && col == 0) {
-        ws2[((size_t)wave * ROWS + r) * 2] = mx;
-        ws2[((size_t)wave * ROWS + r) * 2 + 1] = se;
-      }
-      // selection inside the 16-lane group (columns of this row)
-      for (int rr = 0; rr < a.k; ++rr) {
-        float bv = -INFINITY;
-        int bi = INT_MAX, bt = -1;
+        const bf16x8 av = *(const bf16x8*)(xb + mt * 16 * GKC + slot * 8);
 #pragma unroll
         for (int t = 0; t < NT; ++t)
-          if (better(v[t], ix[t], bv, bi)) { bv = v[t]; bi = ix[t]; bt = t; }
-        float gv = bv;
-        int gi = bi;
-        group_best<16>(gv, gi);
-        if (bi == gi && gi != INT_MAX) {
+          acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bq[p][t], acc[mt][t], 0, 0, 0);
+      }
+      // keep the reloads here: the scheduler would otherwise sink them to the end of the chunk
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int t = 0; t < NT; ++t)
-            if (t == bt) { v[t] = -INFINITY; ix[t] = INT_MAX; }
-        }
-        if (r < a.M && col == 0) {
-          wv[((size_t)wave * ROWS + r) * a.k + rr] = gv;
-          wi[((size_t)wave * ROWS + r) * a.k + rr] = gi;
-        }
-      }
+      for (int t = 0; t < NT; ++t) bq[p][t] = wp[t][(cw * GPF + p) * 4];
+      __builtin_amdgcn_sched_barrier(0);
     }
+    store_x((c + 1) & 1, xr);
+    // LDS-only barrier: __syncthreads() would also wait for every weight fragment in flight
+    lds_barrier();
+  };
+  for (int c = 0; c < nchunks; c += 2) {
+    step(c, bqa);
+    if (c + 1 < nchunks) step(c + 1, bqb);
   }
-  __syncthreads();
+  // epilogue.  The block's bf16 logits (the values the top-k ranks) are parked in LDS, [ROWS][LST]
+  // over the x buffers; then one 16-lane group a row ranks all COLS columns of the block: lane l
+  // holds columns l*CPL .. l*CPL+CPL-1 as 32-bit keys (order-preserving bf16 bits << 16 |
+  // 0xFFFF - column), so one integer max picks the larger logit and, on a tie, the lower column;
+  // a round is CPL-1 maxes, 4 DPP steps and the winner's removal.  Key 0 = no column.
+  constexpr int COLS = GW * NT * 16, LST = COLS + 8, CPL = COLS / 16;
+  static_assert(CPL % 8 == 0, "a lane's columns are read as 16-byte vectors");
+  uint16_t* lg = xs;
+  {
+    const int g = lane >> 4, col = lane & 15;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int r = mt * 16 + 4 * g + q;
+          const int c = (wave * NT + t) * 16 + col;
+          const uint16_t b = __builtin_bit_cast(uint16_t, (__bf16)acc[mt][t][q]);
+          lg[r * LST + c] = b;
+          const int j = blockIdx.x * COLS + c;
+          if (a.logits && r < a.M && j < a.n) a.logits[(size_t)r * a.n + j] = b;
+        }
+  }
+  lds_barrier();
   const Cands cd = carve_cands(a.ws, a.M, a.nsets, a.k);
-  for (int r = threadIdx.x; r < a.M; r += blockDim.x) {
-    const size_t base = (size_t)r * a.nsets + blockIdx.x;
-    float mx = -INFINITY;
-    for (int w = 0; w < GW; ++w) mx = fmaxf(mx, ws2[((size_t)w * ROWS + r) * 2]);
-    float se = 0.f;
-    for (int w = 0; w < GW; ++w) {
-      const float s = ws2[((size_t)w * ROWS + r) * 2 + 1];
-      if (s > 0.f) se += s * expf(ws2[((size_t)w * ROWS + r) * 2] - mx);
-    }
-    cd.cs[base * 2] = mx;
-    cd.cs[base * 2 + 1] = se;
-    int pos[GW];
-    for (int w = 0; w < GW; ++w) pos[w] = 0;
-    for (int rr = 0; rr < a.k; ++rr) {
-      float bv = -INFINITY;
-      int bi = INT_MAX, bw = 0;
-      for (int w = 0; w < GW; ++w) {
-        if (pos[w] >= a.k) continue;
-        const size_t o = ((size_t)w * ROWS + r) * a.k + pos[w];
-        if (better(wv[o], wi[o], bv, bi)) { bv = wv[o]; bi = wi[o]; bw = w; }
+  const int col = lane & 15;
+  for (int r = threadIdx.x >> 4; r < a.M; r += GW * 4) {
+    unsigned key[CPL];
+    float v[CPL];
+#pragma unroll
+    for (int h = 0; h < CPL / 8; ++h) {
+      const uint4 u = *(const uint4*)(lg + r * LST + col * CPL + h * 8);
+      const unsigned w4[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int i = h * 8 + e, c = col * CPL + i;
+        unsigned b = (w4[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+        if (b == 0x8000u) b = 0;                           // -0 ranks as +0
+        const bool ok = blockIdx.x * COLS + c < a.n;
+        v[i] = ok ? __uint_as_float(b << 16) : -INFINITY;
+        const unsigned o = (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
+        key[i] = ok ? (o << 16) | (0xFFFFu - (unsigned)c) : 0u;
       }
-      if (bi != INT_MAX) pos[bw]++;
-      cd.cv[base * a.k + rr] = bv;
-      cd.ci[base * a.k + rr] = bi;
+    }
+    float mx = -INFINITY;
+    const size_t base = (size_t)r * a.nsets + blockIdx.x;
+    for (int rr = 0; rr < a.k; ++rr) {
+      unsigned m = key[0];
+#pragma unroll
+      for (int i = 1; i < CPL; ++i) m = max(m, key[i]);
+      m = max(m, (unsigned)dpp_i32<DPP_XOR1>((int)m));
+      m = max(m, (unsigned)dpp_i32<DPP_XOR2>((int)m));
+      m = max(m, (unsigned)dpp_i32<DPP_HMIRROR>((int)m));
+      m = max(m, (unsigned)dpp_i32<DPP_MIRROR>((int)m));
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) key[i] = key[i] == m ? 0u : key[i];
+      const unsigned o = m >> 16;
+      const unsigned b = (o & 0x8000u) ? (o & 0x7FFFu) : (~o & 0xFFFFu);
+      const float bv = m ? __uint_as_float(b << 16) : -INFINITY;
+      if (rr == 0) mx = bv;
+      if (col == 0) {
+        cd.cv[base * a.k + rr] = bv;
+        cd.ci[base * a.k + rr] = m ? blockIdx.x * COLS + (int)(0xFFFFu - (m & 0xFFFFu)) : INT_MAX;
+      }
+    }
+    float se = 0.f;
+    if (mx != -INFINITY) {
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) se += expf(v[i] - mx);
+    }
+    se = row_sum(se);
+    if (col == 0) {
+      cd.cs[base * 2] = mx;
+      cd.cs[base * 2 + 1] = se;
     }
   }
 }
 
-template <int MT, int NT>
-size_t gemm_lds(int k) {
-  const size_t xbuf = 2 * (size_t)MT * 16 * GLD * 2;
-  const size_t cand = (size_t)GW * MT * 16 * ((size_t)k * 8 + 8);
-  return xbuf > cand ? xbuf : cand;
+template <int MT, int NT, int GW>
+size_t gemm_lds() {
+  const size_t xbuf = 2 * (size_t)MT * 16 * GKC * 2;               // x double buffer
+  const size_t lgt = (size_t)MT * 16 * (GW * NT * 16 + 8) * 2;     // the block's logits
+  return xbuf > lgt ? xbuf : lgt;
 }
 
-template <int MT, int NT>
+template <int MT, int NT, int GW>
 int launch_gemm(const GemmArgs& a0, hipStream_t st) {
+  // cfh_head_ws_bytes sizes the candidate lists for blocks of at least 128 columns
+  static_assert(GW * NT * 16 >= 128, "a GEMM block must cover at least 128 shortlist columns");
   GemmArgs a = a0;
   const int cols = GW * NT * 16;
   a.nsets = (a.n + cols - 1) / cols;
-  const size_t lds = gemm_lds<MT, NT>(a.k);
+  const size_t lds = gemm_lds<MT, NT, GW>();
   if (lds > 160 * 1024) return CFH_E_UNSUPPORTED;
-  CFH_HIP(hipFuncSetAttribute((const void*)k_head_gemm<MT, NT>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-  hipLaunchKernelGGL((k_head_gemm<MT, NT>), dim3(a.nsets), dim3(GW * 64), lds, st, a);
+  CFH_HIP(hipFuncSetAttribute((const void*)k_head_gemm<MT, NT, GW>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)lds));
+  hipLaunchKernelGGL((k_head_gemm<MT, NT, GW>), dim3(a.nsets), dim3(GW * 64), lds, st, a);
   CFH_LAUNCH_CHECK();
   return CFH_OK;
 }
 
-template <int MT, int NT>
+template <int MT, int NT, int GW>
 int gemm_nsets(int n) { return (n + GW * NT * 16 - 1) / (GW * NT * 16); }
 
 // ---------------------------------------------------------------------------- path residual
@@ -919,17 +927,17 @@ int cfh_head_gemm_topk(const void* x, int M, int d, const void* W, const int32_t
   hipStream_t st = (hipStream_t)stream;
   int rc, nsets;
   if (M <= 64) {
-    nsets = gemm_nsets<4, 4>(n);
+    nsets = gemm_nsets<4, 2, 8>(n);
     ga.nsets = nsets;
-    rc = launch_gemm<4, 4>(ga, st);
+    rc = launch_gemm<4, 2, 8>(ga, st);
   } else if (M <= 160) {
-    nsets = gemm_nsets<10, 4>(n);
+    nsets = gemm_nsets<10, 2, 8>(n);
     ga.nsets = nsets;
-    rc = launch_gemm<10, 4>(ga, st);
+    rc = launch_gemm<10, 2, 8>(ga, st);
   } else {
-    nsets = gemm_nsets<16, 2>(n);
+    nsets = gemm_nsets<16, 1, 8>(n);
     ga.nsets = nsets;
-    rc = launch_gemm<16, 2>(ga, st);
+    rc = launch_gemm<16, 1, 8>(ga, st);
   }
   if (rc) return rc;
   return launch_merge(ws, M, nsets, k, vals, ids, lse, st);

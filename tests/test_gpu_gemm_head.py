@@ -50,7 +50,7 @@ def _case(cuda, M, d, V, n, k, seed, scale):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("M,d,n,k", [(1, 256, 1000, 4), (40, 512, 3001, 8), (160, 1024, 5000, 8),
-                                     (256, 512, 2000, 16)])
+                                     (200, 640, 3000, 8), (256, 512, 2000, 16)])
 def test_gemm_head_matches_oracle(cuda, M, d, n, k):
     V = 2 * n + 17
     print(f"[gemm head] M={M} d={d} n={n} k={k}", flush=True)

@@ -205,10 +205,12 @@ class ShortlistHead:
 
 class GemmHead:
     """Batched shortlisted head for many rows (M up to 256): bf16 MFMA skinny GEMM over the
-    shortlist rows of the lm_head, read in place, with the per-row log-softmax top-k fused in
-    (the two-pass candidate head's pass A, ``cf/vllm_plugin/flow_proposer.py:1142-1165``)."""
+    shortlist rows of the lm_head, with the per-row log-softmax top-k fused in (the two-pass
+    candidate head's pass A, ``cf/vllm_plugin/flow_proposer.py:1142-1165``).  ``packed=True`` gathers
+    the shortlist rows once into the MFMA fragment image (``cfh_head_pack``; d % 256 == 0) so every
+    weight load is contiguous; otherwise the rows are read in place through the shortlist."""
 
-    def __init__(self, lm_w: torch.Tensor, shortlist: torch.Tensor | None):
+    def __init__(self, lm_w: torch.Tensor, shortlist: torch.Tensor | None, packed: bool = False):
         if lm_w.dtype != torch.bfloat16 or not lm_w.is_cuda:
             raise ValueError("lm_w must be a CUDA bf16 [V, d] tensor")
         self.lm_w = lm_w.contiguous()
@@ -216,6 +218,14 @@ class GemmHead:
         self.sl = None if shortlist is None else _i32(shortlist.to(lm_w.device))
         self.n = self.V if self.sl is None else int(self.sl.numel())
         self._ws = {}
+        self.image = None
+        if packed:
+            nbytes = int(_lib.lib().cfh_head_packed_bytes(self.n, self.d, 0))
+            if nbytes < 0:
+                raise ValueError(f"packed gemm head needs d % 256 == 0 (d={self.d})")
+            self.image = torch.empty(nbytes, dtype=torch.uint8, device=lm_w.device)
+            _lib.check(_lib.lib().cfh_head_pack(self.lm_w.data_ptr(), None, _lib.ptr(self.sl), self.n, self.d, 0,
+                                                self.image.data_ptr(), _lib.stream_handle()), "cfh_head_pack")
 
     def topk(self, x: torch.Tensor, k: int, logits: torch.Tensor | None = None):
         """x [M, d] bf16 -> (vals [M, k] f32 log-probs, ids [M, k] int32 local, lse [M] f32)."""
@@ -233,10 +243,16 @@ class GemmHead:
         vals = torch.empty(M, k, dtype=torch.float32, device=dev)
         ids = torch.empty(M, k, dtype=torch.int32, device=dev)
         lse = torch.empty(M, dtype=torch.float32, device=dev)
-        _lib.check(_lib.lib().cfh_head_gemm_topk(
-            x.data_ptr(), M, self.d, self.lm_w.data_ptr(), _lib.ptr(self.sl), self.n, k, _lib.ptr(logits),
-            vals.data_ptr(), ids.data_ptr(), lse.data_ptr(), self._ws[key].data_ptr(), _lib.stream_handle()),
-            "cfh_head_gemm_topk")
+        if self.image is not None:
+            _lib.check(_lib.lib().cfh_head_gemm_topk_packed(
+                x.data_ptr(), M, self.d, self.image.data_ptr(), self.n, k, _lib.ptr(logits), vals.data_ptr(),
+                ids.data_ptr(), lse.data_ptr(), self._ws[key].data_ptr(), _lib.stream_handle()),
+                "cfh_head_gemm_topk_packed")
+        else:
+            _lib.check(_lib.lib().cfh_head_gemm_topk(
+                x.data_ptr(), M, self.d, self.lm_w.data_ptr(), _lib.ptr(self.sl), self.n, k, _lib.ptr(logits),
+                vals.data_ptr(), ids.data_ptr(), lse.data_ptr(), self._ws[key].data_ptr(), _lib.stream_handle()),
+                "cfh_head_gemm_topk")
         return vals, ids, lse
 
 

@@ -388,7 +388,9 @@ __global__ void __launch_bounds__(TK_THREADS) k_topk(TopkArgs a) {
 // next chunk's loads are in flight while the current one is multiplied.  The weight fragments
 // alternate between two register sets by chunk parity, so each chunk's weights are requested a
 // whole chunk of multiplies ahead.  Two waves a SIMD (GW = 8) keep the accumulators and both sets
-// in registers, and one wave's multiplies run while the other waits.
+// in registers, and one wave's multiplies run while the other waits.  PK: the weights come from a
+// cfh_head_pack image, whose 16-row x 32-column fragments are the MFMA B operands in lane order,
+// so every wave load is 1 KB contiguous (in place: 16 rows x 64 bytes).
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int GPF = 4;            // k-steps per LDS chunk
@@ -407,7 +409,7 @@ struct GemmArgs {
   int M, d, n, k, nsets;
 };
 
-template <int MT, int NT, int GW>
+template <int MT, int NT, int GW, bool PK>
 __global__ void __launch_bounds__(GW * 64) k_head_gemm(GemmArgs a) {
   // [2][MT*16][GKC], each row's 16-byte slots XOR-swizzled by the row's low 4 bits: the 16 rows
   // an MFMA operand read touches then fall on 16 different bank groups
@@ -415,13 +417,20 @@ __global__ void __launch_bounds__(GW * 64) k_head_gemm(GemmArgs a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   constexpr int ROWS = MT * 16;
   const int tile0 = (blockIdx.x * GW + wave) * NT;
+  // fragment (tile, k-step s) of lane: wp[t][s * KS]; tiles past the shortlist re-read its last one
+  constexpr int KS = PK ? 64 : 4;
   const bf16x8* wp[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    const int j = (tile0 + t) * 16 + (lane & 15);
-    const int jc = j < a.n ? j : a.n - 1;
-    const size_t row = a.sl ? (size_t)a.sl[jc] : (size_t)jc;
-    wp[t] = (const bf16x8*)(a.W + row * a.d) + (lane >> 4);
+    if constexpr (PK) {
+      const int tile = min(tile0 + t, (a.n + 15) / 16 - 1);
+      wp[t] = (const bf16x8*)a.W + (size_t)tile * (a.d / 32) * 64 + lane;
+    } else {
+      const int j = (tile0 + t) * 16 + (lane & 15);
+      const int jc = j < a.n ? j : a.n - 1;
+      const size_t row = a.sl ? (size_t)a.sl[jc] : (size_t)jc;
+      wp[t] = (const bf16x8*)(a.W + row * a.d) + (lane >> 4);
+    }
   }
   const int nchunks = a.d / GKC;
   // two register sets of weight fragments, for even and odd chunks: while chunk c is multiplied
@@ -433,8 +442,8 @@ __global__ void __launch_bounds__(GW * 64) k_head_gemm(GemmArgs a) {
   for (int p = 0; p < GPF; ++p)
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      bqa[p][t] = wp[t][p * 4];
-      bqb[p][t] = wp[t][(min(1, nchunks - 1) * GPF + p) * 4];
+      bqa[p][t] = wp[t][p * KS];
+      bqb[p][t] = wp[t][(min(1, nchunks - 1) * GPF + p) * KS];
     }
   // x chunk: ROWS x 16 vectors of 8, XV a thread (vector idx = row*16 + v); branch-free, rows past
   // M repeat row M-1 (their products are never read), so the wait counts before the multiplies
@@ -488,7 +497,7 @@ __global__ void __launch_bounds__(GW * 64) k_head_gemm(GemmArgs a) {
       // keep the reloads here: the scheduler would otherwise sink them to the end of the chunk
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int t = 0; t < NT; ++t) bq[p][t] = wp[t][(cw * GPF + p) * 4];
+      for (int t = 0; t < NT; ++t) bq[p][t] = wp[t][(cw * GPF + p) * KS];
       __builtin_amdgcn_sched_barrier(0);
     }
     store_x((c + 1) & 1, xr);
@@ -585,7 +594,7 @@ size_t gemm_lds() {
   return xbuf > lgt ? xbuf : lgt;
 }
 
-template <int MT, int NT, int GW>
+template <int MT, int NT, int GW, bool PK>
 int launch_gemm(const GemmArgs& a0, hipStream_t st) {
   // cfh_head_ws_bytes sizes the candidate lists for blocks of at least 128 columns
   static_assert(GW * NT * 16 >= 128, "a GEMM block must cover at least 128 shortlist columns");
@@ -594,9 +603,9 @@ int launch_gemm(const GemmArgs& a0, hipStream_t st) {
   a.nsets = (a.n + cols - 1) / cols;
   const size_t lds = gemm_lds<MT, NT, GW>();
   if (lds > 160 * 1024) return CFH_E_UNSUPPORTED;
-  CFH_HIP(hipFuncSetAttribute((const void*)k_head_gemm<MT, NT, GW>, hipFuncAttributeMaxDynamicSharedMemorySize,
+  CFH_HIP(hipFuncSetAttribute((const void*)k_head_gemm<MT, NT, GW, PK>, hipFuncAttributeMaxDynamicSharedMemorySize,
                               (int)lds));
-  hipLaunchKernelGGL((k_head_gemm<MT, NT, GW>), dim3(a.nsets), dim3(GW * 64), lds, st, a);
+  hipLaunchKernelGGL((k_head_gemm<MT, NT, GW, PK>), dim3(a.nsets), dim3(GW * 64), lds, st, a);
   CFH_LAUNCH_CHECK();
   return CFH_OK;
 }
@@ -830,6 +839,32 @@ int launch_merge(const void* ws, int M, int nsets, int k, float* vals, int* ids,
   return CFH_OK;
 }
 
+template <bool PK>
+int gemm_topk(const void* x, int M, int d, const void* W, const int32_t* sl, int n, int k, void* logits,
+              float* vals, int32_t* ids, float* lse, void* ws, hipStream_t st) {
+  if (!x || !W || !vals || !ids || !ws || M < 1 || M > 256 || d < GKC || d % GKC || n < 1 || k < 1 || k > KMAX)
+    return CFH_E_INVALID;
+  GemmArgs ga = {};
+  ga.x = (const uint16_t*)x; ga.W = (const uint16_t*)W; ga.sl = sl; ga.logits = (uint16_t*)logits; ga.ws = ws;
+  ga.M = M; ga.d = d; ga.n = n; ga.k = k;
+  int rc, nsets;
+  if (M <= 64) {
+    nsets = gemm_nsets<4, 2, 8>(n);
+    ga.nsets = nsets;
+    rc = launch_gemm<4, 2, 8, PK>(ga, st);
+  } else if (M <= 160) {
+    nsets = gemm_nsets<10, 2, 8>(n);
+    ga.nsets = nsets;
+    rc = launch_gemm<10, 2, 8, PK>(ga, st);
+  } else {
+    nsets = gemm_nsets<16, 1, 8>(n);
+    ga.nsets = nsets;
+    rc = launch_gemm<16, 1, 8, PK>(ga, st);
+  }
+  if (rc) return rc;
+  return launch_merge(ws, M, nsets, k, vals, ids, lse, st);
+}
+
 int head_args(HeadArgs& ha, const void* h, int M, int d, const void* W, const int32_t* sl, int n, const void* a,
               const int32_t* a_ids, int a_ids_stride, int r, const void* W2) {
   if (!h || !W || M < 1 || M > HMAXM || d < 32 || d % 256 || n < 1) return CFH_E_INVALID;
@@ -919,28 +954,13 @@ int cfh_head_topk_packed(const void* h, int M, int d, const void* packed, int n,
 
 int cfh_head_gemm_topk(const void* x, int M, int d, const void* W, const int32_t* sl, int n, int k, void* logits,
                        float* vals, int32_t* ids, float* lse, void* ws, void* stream) {
-  if (!x || !W || !vals || !ids || !ws || M < 1 || M > 256 || d < GKC || d % GKC || n < 1 || k < 1 || k > KMAX)
-    return CFH_E_INVALID;
-  GemmArgs ga = {};
-  ga.x = (const uint16_t*)x; ga.W = (const uint16_t*)W; ga.sl = sl; ga.logits = (uint16_t*)logits; ga.ws = ws;
-  ga.M = M; ga.d = d; ga.n = n; ga.k = k;
-  hipStream_t st = (hipStream_t)stream;
-  int rc, nsets;
-  if (M <= 64) {
-    nsets = gemm_nsets<4, 2, 8>(n);
-    ga.nsets = nsets;
-    rc = launch_gemm<4, 2, 8>(ga, st);
-  } else if (M <= 160) {
-    nsets = gemm_nsets<10, 2, 8>(n);
-    ga.nsets = nsets;
-    rc = launch_gemm<10, 2, 8>(ga, st);
-  } else {
-    nsets = gemm_nsets<16, 1, 8>(n);
-    ga.nsets = nsets;
-    rc = launch_gemm<16, 1, 8>(ga, st);
-  }
-  if (rc) return rc;
-  return launch_merge(ws, M, nsets, k, vals, ids, lse, st);
+  return gemm_topk<false>(x, M, d, W, sl, n, k, logits, vals, ids, lse, ws, (hipStream_t)stream);
+}
+
+int cfh_head_gemm_topk_packed(const void* x, int M, int d, const void* packed, int n, int k, void* logits,
+                              float* vals, int32_t* ids, float* lse, void* ws, void* stream) {
+  if (cfh_head_packed_bytes(n, d, 0) < 0) return CFH_E_INVALID;
+  return gemm_topk<true>(x, M, d, packed, nullptr, n, k, logits, vals, ids, lse, ws, (hipStream_t)stream);
 }
 
 int64_t cfh_path_ws_bytes(int M, int d, int ffn_mult, int order) {

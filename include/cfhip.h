@@ -208,6 +208,11 @@ int cfh_cand_topm(const void* logits, long long ld, const float* lse, int B, int
 int cfh_head_gemm_topk(const void* x, int M, int d, const void* W, const int32_t* sl, int n, int k,
                        void* logits, float* vals, int32_t* ids, float* lse, void* ws, void* stream);
 
+/* cfh_head_gemm_topk over a cfh_head_pack image of W (r = 0; the image holds the shortlist rows,
+ * d % 256 == 0): every weight load is a contiguous MFMA fragment.  Same results. */
+int cfh_head_gemm_topk_packed(const void* x, int M, int d, const void* packed, int n, int k, void* logits,
+                              float* vals, int32_t* ids, float* lse, void* ws, void* stream);
+
 /* ---------------------------------------------------------------- draft search
  * Path-conditioned residual of the PathHead, fused form (cf/vllm_plugin/fused.py:25-37;
  * un-fused twin cf/drafters/tree_flow.py:434-450):

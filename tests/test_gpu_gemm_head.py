@@ -36,12 +36,12 @@ def _acc_err(x, Wsl):
     return 2.0 ** -20 * (np.abs(x) @ np.abs(Wsl).T)
 
 
-def _case(cuda, M, d, V, n, k, seed, scale):
+def _case(cuda, M, d, V, n, k, seed, scale, packed=False):
     g = torch.Generator().manual_seed(seed)
     W = (torch.randn(V, d, generator=g) * (scale / d ** 0.5)).to(torch.bfloat16)
     sl = torch.randperm(V, generator=g)[:n].sort().values.to(torch.int32)
     x = torch.randn(M, d, generator=g).to(torch.bfloat16)
-    head = GemmHead(W.to(cuda), sl.to(cuda))
+    head = GemmHead(W.to(cuda), sl.to(cuda), packed=packed)
     logits = torch.empty(M, n, dtype=torch.bfloat16, device=cuda)
     vals, ids, lse = head.topk(x.to(cuda), k, logits=logits)
     torch.cuda.synchronize()
@@ -49,12 +49,15 @@ def _case(cuda, M, d, V, n, k, seed, scale):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("packed", [False, True])
 @pytest.mark.parametrize("M,d,n,k", [(1, 256, 1000, 4), (40, 512, 3001, 8), (160, 1024, 5000, 8),
-                                     (200, 640, 3000, 8), (256, 512, 2000, 16)])
-def test_gemm_head_matches_oracle(cuda, M, d, n, k):
+                                     (200, 640, 3000, 8), (256, 512, 2000, 16), (97, 768, 2049, 5)])
+def test_gemm_head_matches_oracle(cuda, M, d, n, k, packed):
+    if packed and d % 256:
+        pytest.skip("the packed image needs d % 256 == 0")
     V = 2 * n + 17
-    print(f"[gemm head] M={M} d={d} n={n} k={k}", flush=True)
-    W, sl, x, logits, vals, ids, lse = _case(cuda, M, d, V, n, k, seed=M + d, scale=4.0)
+    print(f"[gemm head] M={M} d={d} n={n} k={k} packed={packed}", flush=True)
+    W, sl, x, logits, vals, ids, lse = _case(cuda, M, d, V, n, k, seed=M + d, scale=4.0, packed=packed)
     Wsl = to64(W)[sl.long().numpy()]
     ref = to64(x) @ Wsl.T                                             # float64 of the bf16 inputs
     got = to64(logits)
@@ -73,7 +76,8 @@ def test_gemm_head_matches_oracle(cuda, M, d, n, k):
 
 
 @pytest.mark.gpu
-def test_gemm_head_batched_drafting_shape(cuda):
+@pytest.mark.parametrize("packed", [False, True])
+def test_gemm_head_batched_drafting_shape(cuda, packed):
     """32 sequences x 5 depths = 160 rows, d=4096, the 62,642-row shortlist of a 248,320-row head,
     top-8 per row (checked on a sample of rows against float64)."""
     M, d, V, n, k = 160, 4096, 248320, 62642, 8
@@ -81,7 +85,7 @@ def test_gemm_head_batched_drafting_shape(cuda):
     W = (torch.randn(V, d, generator=g, device=cuda) * (4.0 / d ** 0.5)).to(torch.bfloat16)
     sl = torch.randperm(V, generator=torch.Generator().manual_seed(2))[:n].sort().values.to(torch.int32)
     x = torch.randn(M, d, generator=g, device=cuda).to(torch.bfloat16)
-    head = GemmHead(W, sl.to(cuda))
+    head = GemmHead(W, sl.to(cuda), packed=packed)
     vals, ids, lse = head.topk(x, k)
     torch.cuda.synchronize()
     rows = np.arange(0, M, 7)

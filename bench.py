@@ -97,6 +97,26 @@ def measured_traffic(d, L, E):
     return int(json.loads(p.read_text())["traffic_bytes"])
 
 
+def measured_gemm_traffic(M, d):
+    """HBM bytes per launch of the packed batched head kernel from its committed counter profile
+    (FETCH_SIZE and WRITE_SIZE, calibrated with a 1 GiB copy), or None without one."""
+    p = ROOT / "profiles" / f"head_gemm_M{M}_d{d}_traffic.json"
+    if not p.exists():
+        return None
+    return int(json.loads(p.read_text())["traffic_bytes"])
+
+
+def calib_copy(dev):
+    """One 1 GiB device copy: a kernel of known traffic for calibrating FETCH_SIZE / WRITE_SIZE."""
+    import torch
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 LATENT, VAE_INTER, VAE_LAYERS = 640, 1920, 2
 
 
@@ -406,10 +426,12 @@ def main():
             "mfma": {"achieved_tflops": round(fl / t / 1e12, 1), "peak_tflops": 2500.0,
                      "frac": round(fl / t / 1e12 / 2500.0, 4), "gflop": round(fl / 1e9, 1)},
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_gemm_traffic(M, d_),
                          "kernel": "cfh_head_gemm_topk_packed",
                          "algorithmic_bytes": nb},
         }
+        if args.calib_copy:
+            calib_copy(dev)
         print(json.dumps(out), flush=True)
         return
     if args.workload == "verify":
@@ -505,12 +527,7 @@ def main():
     if latent:
         out["config"].update({"latent": LATENT, "vae_intermediate": VAE_INTER, "vae_layers": VAE_LAYERS})
     if args.calib_copy:
-        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+        calib_copy(dev)
     if not args.no_cpu:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
         out["cpu_baseline"] = (cpu_baseline_latent(W, cfg, dr.head.sl, d, ctx) if latent

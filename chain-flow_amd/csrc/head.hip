@@ -322,6 +322,128 @@ __global__ void __launch_bounds__(MT_THREADS) k_topk_merge(MergeArgs a) {
   });
 }
 
+// The same merge with one wave per row and no workgroup barriers, for rows whose candidates fit in
+// LDS (nsets * k * 8 bytes <= MW_LDS): every block's list is sorted best first, so the row's top-k
+// is a k-way merge of the lists.  The wave stages the row's lists in LDS; lane l caches the heads
+// of the blocks b = l + 64 s (s < S); each round is a lane argmax over S heads, a wave argmax (DPP),
+// and the winning lane moves to its list's next entry.  Same results as k_topk_merge.
+constexpr int MW_LDS = 64 * 1024;
+
+template <int S>
+__global__ void __launch_bounds__(256) k_merge_wave(MergeArgs a) {
+  extern __shared__ __align__(16) float mw[];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int m = blockIdx.x * (blockDim.x >> 6) + wave;
+  if (m >= a.M) return;                                  // (no workgroup barrier below)
+  const Cands cd = carve_cands((void*)a.ws, a.M, a.nsets, a.k);
+  const int k = a.k, total = a.nsets * k;
+  float* sv = mw + (size_t)wave * total * 2;
+  int* si = (int*)(sv + total);
+  const float* cv = cd.cv + (size_t)m * total;
+  const int* ci = cd.ci + (size_t)m * total;
+  // the lane's blocks' (max, sum-exp) first: loads complete in issue order, so the log-sum-exp
+  // below does not wait for the staging loads
+  const float2* cs = (const float2*)(cd.cs + (size_t)m * a.nsets * 2);
+  float2 cq[S];
+#pragma unroll
+  for (int q = 0; q < S; ++q) {
+    const int b = lane + 64 * q;
+    cq[q] = b < a.nsets ? cs[b] : make_float2(-INFINITY, 0.f);
+  }
+  // staging: batches of 8 loads a lane issued before their LDS writes, 16 bytes each when the
+  // row's lists start 16-byte aligned (total % 4 == 0)
+  if ((total & 3) == 0) {
+    const int nv = total / 4;
+    for (int e0 = lane; e0 < nv; e0 += 64 * 8) {
+      uint4 tv[8], ti[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int e = e0 + 64 * j;
+        if (e < nv) {
+          tv[j] = ((const uint4*)cv)[e];
+          ti[j] = ((const uint4*)ci)[e];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int e = e0 + 64 * j;
+        if (e < nv) {
+          ((uint4*)sv)[e] = tv[j];
+          ((uint4*)si)[e] = ti[j];
+        }
+      }
+    }
+  } else {
+    for (int e0 = lane; e0 < total; e0 += 64 * 8) {
+      float tv[8];
+      int ti[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int e = e0 + 64 * j;
+        if (e < total) { tv[j] = cv[e]; ti[j] = ci[e]; }
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int e = e0 + 64 * j;
+        if (e < total) { sv[e] = tv[j]; si[e] = ti[j]; }
+      }
+    }
+  }
+  // log-sum-exp over the blocks' (max, sum-exp)
+  float mx = -INFINITY;
+#pragma unroll
+  for (int q = 0; q < S; ++q) mx = fmaxf(mx, cq[q].x);
+  mx = wave_max(mx);
+  float se = 0.f;
+#pragma unroll
+  for (int q = 0; q < S; ++q)
+    if (cq[q].y > 0.f) se += cq[q].y * expf(cq[q].x - mx);
+  se = wave_sum(se);
+  const float lse = mx + logf(se);
+  if (lane == 0 && a.lse) a.lse[m] = lse;
+  // the staged lists are read by other lanes of this wave: LDS accesses of one wave complete in
+  // order, the fence keeps the compiler from moving the reads above the writes
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+  float hv[S];
+  int hi[S], pos[S];
+#pragma unroll
+  for (int q = 0; q < S; ++q) {
+    const int b = lane + 64 * q;
+    pos[q] = 0;
+    hv[q] = b < a.nsets ? sv[b * k] : -INFINITY;
+    hi[q] = b < a.nsets ? si[b * k] : INT_MAX;
+  }
+  float* vals = a.vals + (size_t)m * k;
+  int* ids = a.ids + (size_t)m * k;
+  for (int r = 0; r < k; ++r) {
+    float bv = hv[0];
+    int bi = hi[0], bq = 0;
+#pragma unroll
+    for (int q = 1; q < S; ++q)
+      if (better(hv[q], hi[q], bv, bi)) { bv = hv[q]; bi = hi[q]; bq = q; }
+    float gv = bv;
+    int gi = bi;
+    group_best<64>(gv, gi);
+    if (bi == gi && gi != INT_MAX) {                     // the owner of the winner advances
+#pragma unroll
+      for (int q = 0; q < S; ++q)
+        if (q == bq) {
+          const int b = lane + 64 * q;
+          const int p = ++pos[q];
+          hv[q] = p < k ? sv[b * k + p] : -INFINITY;
+          hi[q] = p < k ? si[b * k + p] : INT_MAX;
+        }
+    }
+    if (lane == 0) {
+      const bool ok = gi != INT_MAX;
+      vals[r] = ok ? gv - lse : -INFINITY;
+      ids[r] = ok ? gi : -1;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------- row top-k
 // Standalone per-row log-softmax top-k of fp16 logits [M][n] (one workgroup per row): every
 // thread loads its columns in batches (all loads of a batch in flight together), keeps an online
@@ -831,9 +953,28 @@ int launch_pack_rows(const void* w, const int32_t* sl, int n, int K, void* out, 
   return CFH_OK;
 }
 
+template <int S>
+int launch_merge_wave(const MergeArgs& m, size_t row_bytes, hipStream_t st) {
+  // one row (one wave) a workgroup, so the rows spread over the CUs (measured: 11.7 us for 160
+  // rows against 13.4 us at four rows a workgroup)
+  CFH_HIP(hipFuncSetAttribute((const void*)k_merge_wave<S>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)row_bytes));
+  hipLaunchKernelGGL(k_merge_wave<S>, dim3(m.M), dim3(64), row_bytes, st, m);
+  CFH_LAUNCH_CHECK();
+  return CFH_OK;
+}
+
 int launch_merge(const void* ws, int M, int nsets, int k, float* vals, int* ids, float* lse, hipStream_t st) {
   MergeArgs m = {};
   m.ws = ws; m.M = M; m.nsets = nsets; m.k = k; m.vals = vals; m.ids = ids; m.lse = lse;
+  const size_t row_bytes = (size_t)nsets * k * 8;
+  if (row_bytes <= MW_LDS) {
+    const int S = (nsets + 63) / 64;
+    if (S <= 1) return launch_merge_wave<1>(m, row_bytes, st);
+    if (S <= 2) return launch_merge_wave<2>(m, row_bytes, st);
+    if (S <= 4) return launch_merge_wave<4>(m, row_bytes, st);
+    if (S <= 8) return launch_merge_wave<8>(m, row_bytes, st);
+  }
   hipLaunchKernelGGL(k_topk_merge, dim3(M), dim3(MT_THREADS), 0, st, m);
   CFH_LAUNCH_CHECK();
   return CFH_OK;

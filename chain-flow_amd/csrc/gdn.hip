@@ -9,9 +9,10 @@
 // Execution plan (path-parallel): one wave per (node, head, 64-column value slice).  Lane j owns
 // state column j (all Dk = 128 rows) in registers and replays the node's ancestor chain from the
 // root, so every node's state and output come from the same sequential per-path recurrence
-// (tree_scan.py:78-90) and no wave waits for another.  q/k of each path step are normalised by the
-// wave and broadcast through LDS.  The recompute costs depth x (3 Dk FMAs per lane) per node,
-// which is far below the state traffic (S0 read, node state written).
+// (tree_scan.py:78-90) and no wave waits for another.  k of each path step is normalised by the
+// wave and broadcast through LDS; q only for the node itself (the output).  The recompute costs
+// depth x 3 Dk FMA-class operations per lane per node, below the state traffic (S0 read, node
+// state written).
 #include "cfh_common.h"
 #include "cfh_host.h"
 
@@ -36,10 +37,68 @@ struct GdnArgs {
 
 __device__ __forceinline__ float bf16f(uint16_t b) { return __uint_as_float((unsigned)b << 16); }
 
+// The ancestor chain comes from the parents staged in LDS by one coalesced load; each batch of up to
+// GDN_LB path steps issues all its loads (k, v, gates) before any math, and the step scalars wait
+// in LDS for the sequential replay.  The dot products over Dk run as four partial sums.
+constexpr int GDN_LB = 8;
+
+// Lane 0 walks n, parent(n), ..., root through the staged parents; *len = path length, returns
+// nonzero if a parent does not precede its child (not BFS-ordered).
+__device__ int gdn_path(const int* __restrict__ parent, int n, int* par, int* path, int* plen_s, int* bad_s) {
+  const int lane = threadIdx.x;
+  for (int i = lane; i <= n; i += 64) par[i] = parent[i];
+  __syncthreads();
+  if (lane == 0) {
+    int len = 0, bad = 0, cur = n;
+    while (true) {
+      path[len++] = cur;
+      const int p = par[cur];
+      if (p < 0) break;
+      if (p >= cur) { bad = 1; break; }
+      cur = p;
+    }
+    *plen_s = len;
+    *bad_s = bad;
+  }
+  __syncthreads();
+  return *bad_s;
+}
+
+// kv = S^T k after S *= e (S in registers, k broadcast from LDS), four partial sums
+__device__ __forceinline__ float gdn_decay_dot(float* S, const float* kk, float e) {
+  float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
+#pragma unroll
+  for (int i = 0; i < GDN_DK; i += 4) {
+    const float4 k4 = *(const float4*)(kk + i);
+    S[i] *= e; S[i + 1] *= e; S[i + 2] *= e; S[i + 3] *= e;
+    p0 += S[i] * k4.x; p1 += S[i + 1] * k4.y; p2 += S[i + 2] * k4.z; p3 += S[i + 3] * k4.w;
+  }
+  return (p0 + p1) + (p2 + p3);
+}
+
+__device__ __forceinline__ float gdn_dot(const float* S, const float* qq) {
+  float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
+#pragma unroll
+  for (int i = 0; i < GDN_DK; i += 4) {
+    const float4 q4 = *(const float4*)(qq + i);
+    p0 += S[i] * q4.x; p1 += S[i + 1] * q4.y; p2 += S[i + 2] * q4.z; p3 += S[i + 3] * q4.w;
+  }
+  return (p0 + p1) + (p2 + p3);
+}
+
+__device__ __forceinline__ void gdn_rank1(float* S, const float* kk, float delta) {
+#pragma unroll
+  for (int i = 0; i < GDN_DK; i += 4) {
+    const float4 k4 = *(const float4*)(kk + i);
+    S[i] += k4.x * delta; S[i + 1] += k4.y * delta; S[i + 2] += k4.z * delta; S[i + 3] += k4.w * delta;
+  }
+}
+
 __global__ void __launch_bounds__(64) k_gdn_tree(GdnArgs a) {
-  __shared__ float qs[GDN_DK];
-  __shared__ float ks[GDN_DK];
-  __shared__ int path[GDN_MAXN];
+  __shared__ __align__(16) float qs[GDN_DK];
+  __shared__ __align__(16) float ks[GDN_LB][GDN_DK];
+  __shared__ float egs[GDN_LB], bts[GDN_LB], vjs[GDN_LB][64];
+  __shared__ int par[GDN_MAXN], path[GDN_MAXN];
   __shared__ int plen_s, bad_s;
   const int nvs = a.Dv / 64;
   int u = blockIdx.x;
@@ -50,71 +109,66 @@ __global__ void __launch_bounds__(64) k_gdn_tree(GdnArgs a) {
   const int lane = threadIdx.x;
   const int j = vs * 64 + lane;
 
-  if (lane == 0) {
-    // ancestor chain n, parent(n), ..., root; indices strictly decrease, so at most n + 1 entries
-    int len = 0, bad = 0, cur = n;
-    while (true) {
-      path[len++] = cur;
-      const int p = a.parent[cur];
-      if (p < 0) break;
-      if (p >= cur) { bad = 1; break; }
-      cur = p;
-    }
-    plen_s = len;
-    bad_s = bad;
-  }
-  __syncthreads();
-  const int len = plen_s;
-  if (bad_s) {   // not BFS-ordered: refuse with NaN outputs rather than read a later node
+  // the node's own q (for the output) and the initial state do not depend on the path: issued
+  // before the parents, they share its memory round trip
+  const size_t qn = ((size_t)n * a.H + h) * GDN_DK;
+  float q0 = bf16f(a.q[qn + lane]), q1 = bf16f(a.q[qn + 64 + lane]);
+  float S[GDN_DK];
+  const float* s0 = a.S0 + (size_t)h * GDN_DK * a.Dv + j;
+#pragma unroll
+  for (int i = 0; i < GDN_DK; ++i) S[i] = s0[(size_t)i * a.Dv];
+  if (gdn_path(a.parent, n, par, path, &plen_s, &bad_s)) {   // not BFS-ordered: NaN outputs
     const float nan = __builtin_nanf("");
     a.out[((size_t)n * a.H + h) * a.Dv + j] = nan;
     if (a.states)
       for (int i = 0; i < GDN_DK; ++i) a.states[(((size_t)n * a.H + h) * GDN_DK + i) * a.Dv + j] = nan;
     return;
   }
+  const int len = plen_s;
 
-  float S[GDN_DK];
-  const float* s0 = a.S0 + (size_t)h * GDN_DK * a.Dv + j;
+  for (int t0 = len - 1; t0 >= 0; t0 -= GDN_LB) {
+    const int nb = min(GDN_LB, t0 + 1);                      // steps t0, t0 - 1, ..., t0 - nb + 1
+    float k0[GDN_LB], k1[GDN_LB], vj[GDN_LB], gg[GDN_LB], bb[GDN_LB];
 #pragma unroll
-  for (int i = 0; i < GDN_DK; ++i) S[i] = s0[(size_t)i * a.Dv];
-
-  float o = 0.f;
-  for (int t = len - 1; t >= 0; --t) {
-    const int m = path[t];
-    const size_t qk = ((size_t)m * a.H + h) * GDN_DK;
-    float q0 = bf16f(a.q[qk + lane]), q1 = bf16f(a.q[qk + 64 + lane]);
-    float k0 = bf16f(a.k[qk + lane]), k1 = bf16f(a.k[qk + 64 + lane]);
-    if (a.l2norm) {
-      const float sq = wave_sum(q0 * q0 + q1 * q1);
-      const float sk = wave_sum(k0 * k0 + k1 * k1);
-      const float iq = a.l2mode ? 1.0f / sqrtf(sq + 1e-6f) : 1.0f / (sqrtf(sq) + 1e-6f);
-      const float ik = a.l2mode ? 1.0f / sqrtf(sk + 1e-6f) : 1.0f / (sqrtf(sk) + 1e-6f);
-      q0 *= iq; q1 *= iq; k0 *= ik; k1 *= ik;
+    for (int b = 0; b < GDN_LB; ++b) {
+      const int m = path[t0 - min(b, nb - 1)];               // past nb: a repeat, never used
+      const size_t qk = ((size_t)m * a.H + h) * GDN_DK;
+      k0[b] = bf16f(a.k[qk + lane]);
+      k1[b] = bf16f(a.k[qk + 64 + lane]);
+      vj[b] = bf16f(a.v[((size_t)m * a.H + h) * a.Dv + j]);
+      gg[b] = a.g[(size_t)m * a.H + h];
+      bb[b] = a.beta[(size_t)m * a.H + h];
     }
-    __syncthreads();   // the previous step's reads of qs/ks are done
-    qs[lane] = q0 * a.scale;
-    qs[lane + 64] = q1 * a.scale;
-    ks[lane] = k0;
-    ks[lane + 64] = k1;
+#pragma unroll
+    for (int b = 0; b < GDN_LB; ++b) {
+      if (b < nb) {
+        float ik = 1.0f;
+        if (a.l2norm) {
+          const float sk = wave_sum(k0[b] * k0[b] + k1[b] * k1[b]);
+          ik = a.l2mode ? 1.0f / sqrtf(sk + 1e-6f) : 1.0f / (sqrtf(sk) + 1e-6f);
+        }
+        ks[b][lane] = k0[b] * ik;
+        ks[b][lane + 64] = k1[b] * ik;
+        vjs[b][lane] = vj[b];
+        if (lane == 0) { egs[b] = expf(gg[b]); bts[b] = bb[b]; }
+      }
+    }
     __syncthreads();
-    const float eg = expf(a.g[(size_t)m * a.H + h]);
-    const float bt = a.beta[(size_t)m * a.H + h];
-    const float vj = bf16f(a.v[((size_t)m * a.H + h) * a.Dv + j]);
-    float kv = 0.f;
-#pragma unroll
-    for (int i = 0; i < GDN_DK; ++i) {
-      S[i] *= eg;
-      kv += S[i] * ks[i];
+    for (int b = 0; b < nb; ++b) {
+      const float kv = gdn_decay_dot(S, ks[b], egs[b]);
+      gdn_rank1(S, ks[b], (vjs[b][lane] - kv) * bts[b]);
     }
-    const float delta = (vj - kv) * bt;
-    o = 0.f;
-#pragma unroll
-    for (int i = 0; i < GDN_DK; ++i) {
-      S[i] += ks[i] * delta;
-      o += S[i] * qs[i];
-    }
+    __syncthreads();   // the batch's reads of ks / vjs are done before the next batch writes them
   }
-  a.out[((size_t)n * a.H + h) * a.Dv + j] = o;
+  if (a.l2norm) {
+    const float sq = wave_sum(q0 * q0 + q1 * q1);
+    const float iq = a.l2mode ? 1.0f / sqrtf(sq + 1e-6f) : 1.0f / (sqrtf(sq) + 1e-6f);
+    q0 *= iq; q1 *= iq;
+  }
+  qs[lane] = q0 * a.scale;
+  qs[lane + 64] = q1 * a.scale;
+  __syncthreads();
+  a.out[((size_t)n * a.H + h) * a.Dv + j] = gdn_dot(S, qs);
   if (a.states) {
     float* st = a.states + ((size_t)n * a.H + h) * GDN_DK * a.Dv + j;
 #pragma unroll
@@ -148,19 +202,92 @@ struct GdnVArgs {
   float scale;
 };
 
-__device__ __forceinline__ float round_bf16(float x) {   // round to nearest even, as the cast does
-  unsigned u = __float_as_uint(x);
-  if ((u & 0x7f800000u) == 0x7f800000u) return x;        // inf / nan unchanged
-  u = (u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u;
-  return __uint_as_float(u);
+// round to nearest even, as torch's cast does: gfx950 converts in hardware (v_cvt_pk_bf16_f32, two
+// values an instruction), inf unchanged, NaN stays NaN
+__device__ __forceinline__ float round_bf16(float x) { return (float)(__bf16)x; }
+__device__ __forceinline__ uint16_t to_bf16(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
+
+// The serving form's state rows (one value row of K = 128 contiguous elements per lane) pass
+// through LDS so that global memory sees the wave's 64 rows as one contiguous block of 16-byte
+// chunks; rows are padded by 16 bytes in LDS (row stride RB + 16), which keeps the lanes' row reads
+// on different banks.
+template <typename T>
+__device__ __forceinline__ void rows_in(const T* __restrict__ src, float* S, unsigned char* lds) {
+  constexpr int RB = GDN_DK * (int)sizeof(T), RS = RB + 16, NC = 64 * RB / 1024;
+  const int lane = threadIdx.x;
+#pragma unroll
+  for (int c0 = 0; c0 < NC; c0 += 16) {
+    uint4 t[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) t[c] = ((const uint4*)src)[lane + 64 * (c0 + c)];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      const int e = (lane + 64 * (c0 + c)) * 16;
+      *(uint4*)(lds + (e / RB) * RS + e % RB) = t[c];
+    }
+  }
+  __syncthreads();
+  const unsigned char* row = lds + lane * RS;
+#pragma unroll
+  for (int q = 0; q < RB / 16; ++q) {
+    const uint4 u = *(const uint4*)(row + 16 * q);
+    const unsigned w[4] = {u.x, u.y, u.z, u.w};
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) S[8 * q + e] = __uint_as_float((w[e >> 1] >> (16 * (e & 1))) << 16);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) S[4 * q + e] = __uint_as_float(w[e]);
+    }
+  }
+  __syncthreads();   // the rows are read before the buffer is reused
 }
-__device__ __forceinline__ uint16_t to_bf16(float x) { return (uint16_t)(__float_as_uint(round_bf16(x)) >> 16); }
+
+template <typename T>
+__device__ __forceinline__ void rows_out(T* __restrict__ dst, const float* S, unsigned char* lds) {
+  constexpr int RB = GDN_DK * (int)sizeof(T), RS = RB + 16, NC = 64 * RB / 1024;
+  const int lane = threadIdx.x;
+  unsigned char* row = lds + lane * RS;
+#pragma unroll
+  for (int q = 0; q < RB / 16; ++q) {
+    uint4 u;
+    if constexpr (sizeof(T) == 2) {
+      unsigned w[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        w[e] = (unsigned)to_bf16(S[8 * q + 2 * e]) | ((unsigned)to_bf16(S[8 * q + 2 * e + 1]) << 16);
+      u = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+      u = make_uint4(__float_as_uint(S[4 * q]), __float_as_uint(S[4 * q + 1]), __float_as_uint(S[4 * q + 2]),
+                     __float_as_uint(S[4 * q + 3]));
+    }
+    *(uint4*)(row + 16 * q) = u;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int e = (lane + 64 * c) * 16;
+    ((uint4*)dst)[lane + 64 * c] = *(const uint4*)(lds + (e / RB) * RS + e % RB);
+  }
+}
 
 __global__ void __launch_bounds__(64) k_gdn_tree_vllm(GdnVArgs a) {
-  __shared__ float qs[GDN_DK];
-  __shared__ float ks[GDN_DK];
-  __shared__ int path[GDN_MAXN];
+  __shared__ __align__(16) float qs[GDN_DK];
+  __shared__ int par[GDN_MAXN], path[GDN_MAXN];
   __shared__ int plen_s, bad_s;
+  // the state rows (before the replay and after it) share their buffer with the replay's staging
+  struct Stage {
+    float ks[GDN_LB][GDN_DK];
+    float egs[GDN_LB], bts[GDN_LB], vjs[GDN_LB][64];
+  };
+  constexpr int ROWS_BYTES = 64 * (GDN_DK * 4 + 16);
+  static_assert(sizeof(Stage) <= ROWS_BYTES, "staging fits in the row buffer");
+  __shared__ __align__(16) unsigned char rows[ROWS_BYTES];
+  Stage& sg = *(Stage*)rows;
+  float (*ks)[GDN_DK] = sg.ks;
+  float* egs = sg.egs;
+  float* bts = sg.bts;
+  float (*vjs)[64] = sg.vjs;
   const int nvs = a.V / 64;
   int u = blockIdx.x;
   const int vs = u % nvs;
@@ -171,96 +298,79 @@ __global__ void __launch_bounds__(64) k_gdn_tree_vllm(GdnVArgs a) {
   const int lane = threadIdx.x;
   const int j = vs * 64 + lane;
   const size_t srow = (size_t)a.HV * a.V * GDN_DK;                 // elements per slot
-  const size_t sofs = ((size_t)hv * a.V + j) * GDN_DK;             // this lane's state row in a slot
+  const size_t sblk = ((size_t)hv * a.V + vs * 64) * GDN_DK;       // the wave's 64 rows in a slot
 
-  if (lane == 0) {
-    int len = 0, bad = 0, cur = n;
-    while (true) {
-      path[len++] = cur;
-      const int p = a.parent[cur];
-      if (p < 0) break;
-      if (p >= cur) { bad = 1; break; }
-      cur = p;
-    }
-    plen_s = len;
-    bad_s = bad;
-  }
-  __syncthreads();
-  const int len = plen_s;
-  if (bad_s) {   // not BFS-ordered: NaN outputs, state slot untouched
+  // the node's own q (for the output) and the prefix state do not depend on the path: issued
+  // before the parents, they share its memory round trip
+  const uint16_t* rown = a.qkv + (size_t)n * a.ld;
+  float q0 = bf16f(rown[(size_t)h * GDN_DK + lane]), q1 = bf16f(rown[(size_t)h * GDN_DK + 64 + lane]);
+  float S[GDN_DK];
+  if (a.bf16_state)
+    rows_in((const uint16_t*)a.state + (size_t)a.prefix * srow + sblk, S, rows);
+  else
+    rows_in((const float*)a.state + (size_t)a.prefix * srow + sblk, S, rows);
+  const float Aexp = expf(a.A_log[hv]), dtb = a.dt_bias[hv];
+  if (gdn_path(a.parent, n, par, path, &plen_s, &bad_s)) {   // not BFS-ordered: NaN outputs, slot untouched
     a.out[((size_t)n * a.HV + hv) * a.V + j] = 0x7fc0;
     return;
   }
-
-  float S[GDN_DK];
-  if (a.bf16_state) {
-    const uint16_t* s0 = (const uint16_t*)a.state + (size_t)a.prefix * srow + sofs;
-#pragma unroll
-    for (int i = 0; i < GDN_DK; ++i) S[i] = bf16f(s0[i]);
-  } else {
-    const float* s0 = (const float*)a.state + (size_t)a.prefix * srow + sofs;
-#pragma unroll
-    for (int i = 0; i < GDN_DK; ++i) S[i] = s0[i];
-  }
-  const float Aexp = expf(a.A_log[hv]), dtb = a.dt_bias[hv];
+  const int len = plen_s;
   const size_t koff = (size_t)a.H * GDN_DK + (size_t)h * GDN_DK;
   const size_t voff = 2 * (size_t)a.H * GDN_DK + (size_t)hv * a.V + j;
-  for (int t = len - 1; t >= 0; --t) {
-    const int m = path[t];
-    const uint16_t* row = a.qkv + (size_t)m * a.ld;
-    float k0 = bf16f(row[koff + lane]), k1 = bf16f(row[koff + 64 + lane]);
-    if (a.l2norm) {
-      const float ik = 1.0f / sqrtf(wave_sum(k0 * k0 + k1 * k1) + 1e-6f);
-      k0 *= ik; k1 *= ik;
+  for (int t0 = len - 1; t0 >= 0; t0 -= GDN_LB) {
+    const int nb = min(GDN_LB, t0 + 1);                      // steps t0, t0 - 1, ..., t0 - nb + 1
+    float k0[GDN_LB], k1[GDN_LB], vj[GDN_LB], xa[GDN_LB], xb[GDN_LB];
+#pragma unroll
+    for (int b = 0; b < GDN_LB; ++b) {
+      const int m = path[t0 - min(b, nb - 1)];               // past nb: a repeat, never used
+      const uint16_t* row = a.qkv + (size_t)m * a.ld;
+      k0[b] = bf16f(row[koff + lane]);
+      k1[b] = bf16f(row[koff + 64 + lane]);
+      vj[b] = bf16f(row[voff]);
+      xa[b] = bf16f(a.ga[(size_t)m * a.HV + hv]);
+      xb[b] = bf16f(a.gb[(size_t)m * a.HV + hv]);
     }
-    __syncthreads();   // the previous step's reads of ks are done
-    ks[lane] = k0;
-    ks[lane + 64] = k1;
+#pragma unroll
+    for (int b = 0; b < GDN_LB; ++b) {
+      if (b < nb) {
+        float ik = 1.0f;
+        if (a.l2norm) ik = 1.0f / sqrtf(wave_sum(k0[b] * k0[b] + k1[b] * k1[b]) + 1e-6f);
+        ks[b][lane] = k0[b] * ik;
+        ks[b][lane + 64] = k1[b] * ik;
+        vjs[b][lane] = vj[b];
+        if (lane == 0) {
+          const float x = xa[b] + dtb;
+          const float sp = x <= 20.0f ? logf(1.0f + expf(x)) : x;
+          egs[b] = expf(-Aexp * sp);
+          bts[b] = round_bf16(1.0f / (1.0f + expf(-xb[b])));
+        }
+      }
+    }
     __syncthreads();
-    const float x = bf16f(a.ga[(size_t)m * a.HV + hv]) + dtb;
-    const float sp = x <= 20.0f ? logf(1.0f + expf(x)) : x;
-    const float eg = expf(-Aexp * sp);
-    const float bt = round_bf16(1.0f / (1.0f + expf(-bf16f(a.gb[(size_t)m * a.HV + hv]))));
-    const float vj = bf16f(row[voff]);
-    float kv = 0.f;
+    for (int b = 0; b < nb; ++b) {
+      const float kv = gdn_decay_dot(S, ks[b], egs[b]);
+      gdn_rank1(S, ks[b], (vjs[b][lane] - kv) * bts[b]);
+      if (t0 - b > 0 && a.bf16_state) {   // an ancestor: its stored (bf16) state is what the child reads
 #pragma unroll
-    for (int i = 0; i < GDN_DK; ++i) {
-      S[i] *= eg;
-      kv += S[i] * ks[i];
+        for (int i = 0; i < GDN_DK; ++i) S[i] = round_bf16(S[i]);
+      }
     }
-    const float delta = (vj - kv) * bt;
-#pragma unroll
-    for (int i = 0; i < GDN_DK; ++i) S[i] += delta * ks[i];
-    if (t > 0 && a.bf16_state) {   // an ancestor: its stored (bf16) state is what the child reads
-#pragma unroll
-      for (int i = 0; i < GDN_DK; ++i) S[i] = round_bf16(S[i]);
-    }
+    __syncthreads();   // the batch's reads of ks / vjs are done before the next batch writes them
   }
   // output with the node's own q
-  const uint16_t* row = a.qkv + (size_t)n * a.ld;
-  float q0 = bf16f(row[(size_t)h * GDN_DK + lane]), q1 = bf16f(row[(size_t)h * GDN_DK + 64 + lane]);
   if (a.l2norm) {
     const float iq = 1.0f / sqrtf(wave_sum(q0 * q0 + q1 * q1) + 1e-6f);
     q0 *= iq; q1 *= iq;
   }
-  __syncthreads();
   qs[lane] = q0 * a.scale;
   qs[lane + 64] = q1 * a.scale;
   __syncthreads();
-  float o = 0.f;
-#pragma unroll
-  for (int i = 0; i < GDN_DK; ++i) o += S[i] * qs[i];
-  a.out[((size_t)n * a.HV + hv) * a.V + j] = to_bf16(o);
-  const size_t dst = (size_t)a.slots[n] * srow + sofs;
-  if (a.bf16_state) {
-    uint16_t* st = (uint16_t*)a.state + dst;
-#pragma unroll
-    for (int i = 0; i < GDN_DK; ++i) st[i] = to_bf16(S[i]);
-  } else {
-    float* st = (float*)a.state + dst;
-#pragma unroll
-    for (int i = 0; i < GDN_DK; ++i) st[i] = S[i];
-  }
+  a.out[((size_t)n * a.HV + hv) * a.V + j] = to_bf16(gdn_dot(S, qs));
+  const size_t dst = (size_t)a.slots[n] * srow + sblk;
+  if (a.bf16_state)
+    rows_out((uint16_t*)a.state + dst, S, rows);
+  else
+    rows_out((float*)a.state + dst, S, rows);
 }
 
 }  // namespace

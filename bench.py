@@ -106,6 +106,35 @@ def measured_gemm_traffic(M, d):
     return int(json.loads(p.read_text())["traffic_bytes"])
 
 
+def head_compare(W, sl, d, dev, rows=4, k=8, iters=50):
+    """One head top-k launch (rows x d fp16 hiddens, top-k per row, no markov bias) over the packed
+    shortlist image (the drafter's path), the shortlist rows read in place, and the full vocabulary
+    read in place: microseconds per call and the rows' bytes."""
+    import torch
+    from chain_flow_amd.head import ShortlistHead
+    lm_w = W["lm_head.weight"]
+    h = torch.randn(rows, d, generator=torch.Generator(device=dev).manual_seed(9), device=dev).half()
+    res = {"rows": rows, "k": k, "shortlist_rows": int(sl.numel()), "full_rows": int(lm_w.shape[0])}
+    for name, head in (("shortlist_packed", lambda: ShortlistHead(lm_w, sl, packed=True)),
+                       ("shortlist_in_place", lambda: ShortlistHead(lm_w, sl, packed=False)),
+                       ("full_in_place", lambda: ShortlistHead(lm_w, None, packed=False))):
+        hd = head()
+        for _ in range(5):
+            hd.topk(h, k)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            hd.topk(h, k)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / iters
+        nb = hd.n * d * 2
+        res[name] = {"us": round(us, 2), "bytes": nb, "gbs": round(nb / (us * 1e-6) / 1e9, 1)}
+        del hd
+    return res
+
+
 def calib_copy(dev):
     """One 1 GiB device copy: a kernel of known traffic for calibrating FETCH_SIZE / WRITE_SIZE."""
     import torch
@@ -498,7 +527,7 @@ def main():
         traffic, kern = measured_traffic(d, L, E), "flow pass (cfh_flow_integrate)"
         workload = (f"chain draft d={d} fp16 bs1 K={K} width {Wd}, flow L={L} E={E} "
                     f"2 chunk experts, shortlisted head {SHORTLIST_ROWS}x{d}")
-        metric = "us per 5-token draft step (d=5120, bs1) + achieved HBM GB/s vs roofline"
+        metric = f"us per 5-token draft step (d={d}, bs1) + achieved HBM GB/s vs roofline"
     hb = (head_bytes_twopass(d, K, args.twopass, SHORTLIST_ROWS) if args.twopass
           else head_bytes(d, K, Wd, SHORTLIST_ROWS))
     if args.twopass:
@@ -526,6 +555,9 @@ def main():
     }
     if latent:
         out["config"].update({"latent": LATENT, "vae_intermediate": VAE_INTER, "vae_layers": VAE_LAYERS})
+    else:
+        print("[bench] head comparison", file=sys.stderr, flush=True)
+        out["head_compare"] = head_compare(W, dr.head.sl, d, dev)
     if args.calib_copy:
         calib_copy(dev)
     if not args.no_cpu:

@@ -202,11 +202,15 @@ def test_beam_chains_match_oracle(cuda, seed):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("M,k,markov", [(1, 4, True), (4, 4, True), (4, 8, False), (8, 16, True)])
-def test_fused_head_topk_equals_logits_then_topk(cuda, M, k, markov):
+@pytest.mark.parametrize("M,k,markov,n,V", [(1, 4, True, 5003, 9000), (4, 4, True, 5003, 9000),
+                                             (4, 8, False, 5003, 9000), (8, 16, True, 5003, 9000),
+                                             (2, 16, True, 65000, 70000), (4, 8, False, 80003, 90000)])
+def test_fused_head_topk_equals_logits_then_topk(cuda, M, k, markov, n, V):
     """The fused head (per-block candidates + merge) returns exactly what the unfused pair
-    (fp16 logits, then per-row log-softmax top-k) returns on the same inputs."""
-    d, V, n = 512, 9000, 5003          # n not a multiple of the 128-column block
+    (fp16 logits, then per-row log-softmax top-k) returns on the same inputs.  n not a multiple
+    of the 128-column block; 65,000 columns at k=16 fill the wave merge's 64 KB of LDS, 80,003
+    columns (626 blocks) take the block-wide merge."""
+    d = 512
     cfg, W = _head_weights(d, V)
     sl = _shortlist(V, n)
     g = torch.Generator().manual_seed(17)
@@ -216,6 +220,7 @@ def test_fused_head_topk_equals_logits_then_topk(cuda, M, k, markov):
                          W["markov.w1.weight"].to(cuda) if markov else None,
                          W["markov.w2.weight"].to(cuda) if markov else None)
     logits = torch.empty(M, n, dtype=torch.float16, device=cuda)
+    print(f"[fused head] M={M} k={k} markov={markov} n={n}", flush=True)
     vals, ids, lse = head.topk(h, k, prev=prev if markov else None, logits=logits)
     rv, ri, rl = row_topk(logits, k)
     torch.cuda.synchronize()

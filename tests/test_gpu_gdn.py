@@ -76,6 +76,26 @@ def test_gdn_chain_is_the_linear_recurrence(cuda):
 
 
 @pytest.mark.gpu
+def test_gdn_strong_decay_matches_oracle(cuda):
+    """Gates of -30 (decay ~1e-13) and -inf (decay 0) along a chain and a tree: the running decay
+    scale falls below its floor and is folded into the state; outputs and states stay within TOL."""
+    for parent in (np.arange(-1, 9), np.array([-1, 0, 0, 1, 1, 2, 2, 3, 4, 5])):
+        N = len(parent)
+        q, k, v, gg, beta, S0 = _inputs(N, 4, 128, 64, 21)
+        gg[2] = -30.0
+        gg[5, :2] = float("-inf")
+        gg[6] = -12.0
+        out, st = tree_gated_delta_scan(q.to(cuda), k.to(cuda), v.to(cuda), gg, beta, torch.tensor(parent), S0)
+        torch.cuda.synchronize()
+        ro, rs = ogdn.tree_gated_delta_scan(to64(q), to64(k), to64(v), to64(gg), to64(beta), parent, to64(S0))
+        print(f"[gdn strong decay] N={N} out err {rel_err(to64(out), ro):.2e} state err {rel_err(to64(st), rs):.2e}",
+              flush=True)
+        assert np.isfinite(to64(out)).all() and np.isfinite(to64(st)).all()
+        assert rel_err(to64(out), ro) < TOL
+        assert rel_err(to64(st), rs) < TOL
+
+
+@pytest.mark.gpu
 def test_gdn_forest_sqrt_eps_and_outputs_only(cuda):
     parent = np.array([-1, -1, 0, 1, 2, 2, -1, 6, 3])
     out, st, ro, rs, _ = _run(cuda, parent, H=3, Dv=192, seed=11, l2mode=L2_SQRT_EPS, states=False)

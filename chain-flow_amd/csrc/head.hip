@@ -355,14 +355,14 @@ __global__ void __launch_bounds__(256) k_merge_wave(MergeArgs a) {
   if ((total & 3) == 0) {
     const int nv = total / 4;
     for (int e0 = lane; e0 < nv; e0 += 64 * 8) {
+      // loads unconditional (index clamped; the surplus is never stored), so the batch stays in
+      // registers: a conditionally written array would live in scratch memory
       uint4 tv[8], ti[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int e = e0 + 64 * j;
-        if (e < nv) {
-          tv[j] = ((const uint4*)cv)[e];
-          ti[j] = ((const uint4*)ci)[e];
-        }
+        const int e = min(e0 + 64 * j, nv - 1);
+        tv[j] = ((const uint4*)cv)[e];
+        ti[j] = ((const uint4*)ci)[e];
       }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -379,8 +379,9 @@ __global__ void __launch_bounds__(256) k_merge_wave(MergeArgs a) {
       int ti[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int e = e0 + 64 * j;
-        if (e < total) { tv[j] = cv[e]; ti[j] = ci[e]; }
+        const int e = min(e0 + 64 * j, total - 1);
+        tv[j] = cv[e];
+        ti[j] = ci[e];
       }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {

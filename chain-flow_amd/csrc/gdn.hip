@@ -45,10 +45,9 @@ constexpr int GDN_LB = 8;
 // Lane 0 walks n, parent(n), ..., root through the staged parents; *len = path length, returns
 // nonzero if a parent does not precede its child (not BFS-ordered).
 __device__ int gdn_path(const int* __restrict__ parent, int n, int* par, int* path, int* plen_s, int* bad_s) {
-  const int lane = threadIdx.x;
-  for (int i = lane; i <= n; i += 64) par[i] = parent[i];
+  for (int i = threadIdx.x; i <= n; i += blockDim.x) par[i] = parent[i];
   __syncthreads();
-  if (lane == 0) {
+  if (threadIdx.x == 0) {
     int len = 0, bad = 0, cur = n;
     while (true) {
       path[len++] = cur;
@@ -94,10 +93,47 @@ __device__ __forceinline__ void gdn_rank1(float* S, const float* kk, float delta
   }
 }
 
-__global__ void __launch_bounds__(64) k_gdn_tree(GdnArgs a) {
+// GDN_NW waves per (node, head, 64-column value slice): wave w holds state rows
+// [GDN_HK w, GDN_HK (w + 1)) of the slice's columns, so the deepest nodes' replays (the critical
+// path) spread over GDN_NW times the SIMDs.  Each step's dot product is the sum of the waves'
+// partials, exchanged through LDS (one barrier a step, buffers alternating by step).
+constexpr int GDN_NW = 4;                  // waves per (node, head, value slice)
+constexpr int GDN_HK = GDN_DK / GDN_NW;    // state rows a wave holds
+
+__device__ __forceinline__ float gdn_decay_dot_h(float* S, const float* kk, float e) {
+  float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
+#pragma unroll
+  for (int i = 0; i < GDN_HK; i += 4) {
+    const float4 k4 = *(const float4*)(kk + i);
+    S[i] *= e; S[i + 1] *= e; S[i + 2] *= e; S[i + 3] *= e;
+    p0 += S[i] * k4.x; p1 += S[i + 1] * k4.y; p2 += S[i + 2] * k4.z; p3 += S[i + 3] * k4.w;
+  }
+  return (p0 + p1) + (p2 + p3);
+}
+
+__device__ __forceinline__ float gdn_dot_h(const float* S, const float* qq) {
+  float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
+#pragma unroll
+  for (int i = 0; i < GDN_HK; i += 4) {
+    const float4 q4 = *(const float4*)(qq + i);
+    p0 += S[i] * q4.x; p1 += S[i + 1] * q4.y; p2 += S[i + 2] * q4.z; p3 += S[i + 3] * q4.w;
+  }
+  return (p0 + p1) + (p2 + p3);
+}
+
+__device__ __forceinline__ void gdn_rank1_h(float* S, const float* kk, float delta) {
+#pragma unroll
+  for (int i = 0; i < GDN_HK; i += 4) {
+    const float4 k4 = *(const float4*)(kk + i);
+    S[i] += k4.x * delta; S[i + 1] += k4.y * delta; S[i + 2] += k4.z * delta; S[i + 3] += k4.w * delta;
+  }
+}
+
+__global__ void __launch_bounds__(64 * GDN_NW) k_gdn_tree(GdnArgs a) {
   __shared__ __align__(16) float qs[GDN_DK];
   __shared__ __align__(16) float ks[GDN_LB][GDN_DK];
   __shared__ float egs[GDN_LB], bts[GDN_LB], vjs[GDN_LB][64];
+  __shared__ float red[2][GDN_NW][64];                       // [step parity][wave][lane]
   __shared__ int par[GDN_MAXN], path[GDN_MAXN];
   __shared__ int plen_s, bad_s;
   const int nvs = a.Dv / 64;
@@ -106,73 +142,92 @@ __global__ void __launch_bounds__(64) k_gdn_tree(GdnArgs a) {
   u /= nvs;
   const int h = u % a.H;
   const int n = u / a.H;
-  const int lane = threadIdx.x;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int j = vs * 64 + lane;
+  const int i0 = wave * GDN_HK;                              // this wave's state rows
 
   // the node's own q (for the output) and the initial state do not depend on the path: issued
   // before the parents, they share its memory round trip
   const size_t qn = ((size_t)n * a.H + h) * GDN_DK;
   float q0 = bf16f(a.q[qn + lane]), q1 = bf16f(a.q[qn + 64 + lane]);
-  float S[GDN_DK];
-  const float* s0 = a.S0 + (size_t)h * GDN_DK * a.Dv + j;
+  float S[GDN_HK];
+  const float* s0 = a.S0 + ((size_t)h * GDN_DK + i0) * a.Dv + j;
 #pragma unroll
-  for (int i = 0; i < GDN_DK; ++i) S[i] = s0[(size_t)i * a.Dv];
+  for (int i = 0; i < GDN_HK; ++i) S[i] = s0[(size_t)i * a.Dv];
   if (gdn_path(a.parent, n, par, path, &plen_s, &bad_s)) {   // not BFS-ordered: NaN outputs
     const float nan = __builtin_nanf("");
-    a.out[((size_t)n * a.H + h) * a.Dv + j] = nan;
+    if (wave == 0) a.out[((size_t)n * a.H + h) * a.Dv + j] = nan;
     if (a.states)
-      for (int i = 0; i < GDN_DK; ++i) a.states[(((size_t)n * a.H + h) * GDN_DK + i) * a.Dv + j] = nan;
+      for (int i = 0; i < GDN_HK; ++i)
+        a.states[(((size_t)n * a.H + h) * GDN_DK + i0 + i) * a.Dv + j] = nan;
     return;
   }
   const int len = plen_s;
+  int rb = 0;                                                // red buffer of the next exchange
 
   for (int t0 = len - 1; t0 >= 0; t0 -= GDN_LB) {
     const int nb = min(GDN_LB, t0 + 1);                      // steps t0, t0 - 1, ..., t0 - nb + 1
-    float k0[GDN_LB], k1[GDN_LB], vj[GDN_LB], gg[GDN_LB], bb[GDN_LB];
+    if (wave == 0) {                                         // wave 0 stages the batch for both
+      float k0[GDN_LB], k1[GDN_LB], vj[GDN_LB], gg[GDN_LB], bb[GDN_LB];
 #pragma unroll
-    for (int b = 0; b < GDN_LB; ++b) {
-      const int m = path[t0 - min(b, nb - 1)];               // past nb: a repeat, never used
-      const size_t qk = ((size_t)m * a.H + h) * GDN_DK;
-      k0[b] = bf16f(a.k[qk + lane]);
-      k1[b] = bf16f(a.k[qk + 64 + lane]);
-      vj[b] = bf16f(a.v[((size_t)m * a.H + h) * a.Dv + j]);
-      gg[b] = a.g[(size_t)m * a.H + h];
-      bb[b] = a.beta[(size_t)m * a.H + h];
-    }
+      for (int b = 0; b < GDN_LB; ++b) {
+        const int m = path[t0 - min(b, nb - 1)];             // past nb: a repeat, never used
+        const size_t qk = ((size_t)m * a.H + h) * GDN_DK;
+        k0[b] = bf16f(a.k[qk + lane]);
+        k1[b] = bf16f(a.k[qk + 64 + lane]);
+        vj[b] = bf16f(a.v[((size_t)m * a.H + h) * a.Dv + j]);
+        gg[b] = a.g[(size_t)m * a.H + h];
+        bb[b] = a.beta[(size_t)m * a.H + h];
+      }
 #pragma unroll
-    for (int b = 0; b < GDN_LB; ++b) {
-      if (b < nb) {
-        float ik = 1.0f;
-        if (a.l2norm) {
-          const float sk = wave_sum(k0[b] * k0[b] + k1[b] * k1[b]);
-          ik = a.l2mode ? 1.0f / sqrtf(sk + 1e-6f) : 1.0f / (sqrtf(sk) + 1e-6f);
+      for (int b = 0; b < GDN_LB; ++b) {
+        if (b < nb) {
+          float ik = 1.0f;
+          if (a.l2norm) {
+            const float sk = wave_sum(k0[b] * k0[b] + k1[b] * k1[b]);
+            ik = a.l2mode ? 1.0f / sqrtf(sk + 1e-6f) : 1.0f / (sqrtf(sk) + 1e-6f);
+          }
+          ks[b][lane] = k0[b] * ik;
+          ks[b][lane + 64] = k1[b] * ik;
+          vjs[b][lane] = vj[b];
+          if (lane == 0) { egs[b] = expf(gg[b]); bts[b] = bb[b]; }
         }
-        ks[b][lane] = k0[b] * ik;
-        ks[b][lane + 64] = k1[b] * ik;
-        vjs[b][lane] = vj[b];
-        if (lane == 0) { egs[b] = expf(gg[b]); bts[b] = bb[b]; }
       }
     }
     __syncthreads();
     for (int b = 0; b < nb; ++b) {
-      const float kv = gdn_decay_dot(S, ks[b], egs[b]);
-      gdn_rank1(S, ks[b], (vjs[b][lane] - kv) * bts[b]);
+      red[rb][wave][lane] = gdn_decay_dot_h(S, ks[b] + i0, egs[b]);
+      __syncthreads();
+      float kv = 0.f;
+#pragma unroll
+      for (int w = 0; w < GDN_NW; ++w) kv += red[rb][w][lane];
+      rb ^= 1;
+      gdn_rank1_h(S, ks[b] + i0, (vjs[b][lane] - kv) * bts[b]);
     }
     __syncthreads();   // the batch's reads of ks / vjs are done before the next batch writes them
   }
-  if (a.l2norm) {
-    const float sq = wave_sum(q0 * q0 + q1 * q1);
-    const float iq = a.l2mode ? 1.0f / sqrtf(sq + 1e-6f) : 1.0f / (sqrtf(sq) + 1e-6f);
-    q0 *= iq; q1 *= iq;
+  if (wave == 0) {
+    if (a.l2norm) {
+      const float sq = wave_sum(q0 * q0 + q1 * q1);
+      const float iq = a.l2mode ? 1.0f / sqrtf(sq + 1e-6f) : 1.0f / (sqrtf(sq) + 1e-6f);
+      q0 *= iq; q1 *= iq;
+    }
+    qs[lane] = q0 * a.scale;
+    qs[lane + 64] = q1 * a.scale;
   }
-  qs[lane] = q0 * a.scale;
-  qs[lane + 64] = q1 * a.scale;
   __syncthreads();
-  a.out[((size_t)n * a.H + h) * a.Dv + j] = gdn_dot(S, qs);
-  if (a.states) {
-    float* st = a.states + ((size_t)n * a.H + h) * GDN_DK * a.Dv + j;
+  red[rb][wave][lane] = gdn_dot_h(S, qs + i0);
+  __syncthreads();
+  if (wave == 0) {
+    float o = 0.f;
 #pragma unroll
-    for (int i = 0; i < GDN_DK; ++i) st[(size_t)i * a.Dv] = S[i];
+    for (int w = 0; w < GDN_NW; ++w) o += red[rb][w][lane];
+    a.out[((size_t)n * a.H + h) * a.Dv + j] = o;
+  }
+  if (a.states) {
+    float* st = a.states + (((size_t)n * a.H + h) * GDN_DK + i0) * a.Dv + j;
+#pragma unroll
+    for (int i = 0; i < GDN_HK; ++i) st[(size_t)i * a.Dv] = S[i];
   }
 }
 
@@ -207,29 +262,31 @@ struct GdnVArgs {
 __device__ __forceinline__ float round_bf16(float x) { return (float)(__bf16)x; }
 __device__ __forceinline__ uint16_t to_bf16(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
 
-// The serving form's state rows (one value row of K = 128 contiguous elements per lane) pass
-// through LDS so that global memory sees the wave's 64 rows as one contiguous block of 16-byte
-// chunks; rows are padded by 16 bytes in LDS (row stride RB + 16), which keeps the lanes' row reads
-// on different banks.
+// The serving form's state rows (one value row of K = 128 contiguous elements per lane; wave w
+// holds K elements [GDN_HK w, GDN_HK (w + 1))) pass through LDS so that global memory sees the workgroup's
+// 64 rows as one contiguous block of 16-byte chunks; rows are padded by 16 bytes in LDS (row stride
+// RB + 16), which keeps the lanes' row reads on different banks.
 template <typename T>
 __device__ __forceinline__ void rows_in(const T* __restrict__ src, float* S, unsigned char* lds) {
-  constexpr int RB = GDN_DK * (int)sizeof(T), RS = RB + 16, NC = 64 * RB / 1024;
-  const int lane = threadIdx.x;
+  constexpr int RB = GDN_DK * (int)sizeof(T), RS = RB + 16, NC = 64 * RB / 16;   // 1024 or 2048 chunks
+  const int t = threadIdx.x;
+  constexpr int NT = 64 * GDN_NW, NB = NC / NT < 8 ? NC / NT : 8;   // threads; chunks a batch
+  static_assert(NC % (NT * NB) == 0, "the block splits into whole batches");
 #pragma unroll
-  for (int c0 = 0; c0 < NC; c0 += 16) {
-    uint4 t[16];
+  for (int c0 = 0; c0 < NC; c0 += NT * NB) {
+    uint4 v[NB];
 #pragma unroll
-    for (int c = 0; c < 16; ++c) t[c] = ((const uint4*)src)[lane + 64 * (c0 + c)];
+    for (int q = 0; q < NB; ++q) v[q] = ((const uint4*)src)[c0 + t + NT * q];
 #pragma unroll
-    for (int c = 0; c < 16; ++c) {
-      const int e = (lane + 64 * (c0 + c)) * 16;
-      *(uint4*)(lds + (e / RB) * RS + e % RB) = t[c];
+    for (int q = 0; q < NB; ++q) {
+      const int e = (c0 + t + NT * q) * 16;
+      *(uint4*)(lds + (e / RB) * RS + e % RB) = v[q];
     }
   }
   __syncthreads();
-  const unsigned char* row = lds + lane * RS;
+  const unsigned char* row = lds + (t & 63) * RS + (t >> 6) * (RB / GDN_NW);
 #pragma unroll
-  for (int q = 0; q < RB / 16; ++q) {
+  for (int q = 0; q < RB / (16 * GDN_NW); ++q) {
     const uint4 u = *(const uint4*)(row + 16 * q);
     const unsigned w[4] = {u.x, u.y, u.z, u.w};
     if constexpr (sizeof(T) == 2) {
@@ -245,11 +302,11 @@ __device__ __forceinline__ void rows_in(const T* __restrict__ src, float* S, uns
 
 template <typename T>
 __device__ __forceinline__ void rows_out(T* __restrict__ dst, const float* S, unsigned char* lds) {
-  constexpr int RB = GDN_DK * (int)sizeof(T), RS = RB + 16, NC = 64 * RB / 1024;
-  const int lane = threadIdx.x;
-  unsigned char* row = lds + lane * RS;
+  constexpr int RB = GDN_DK * (int)sizeof(T), RS = RB + 16, NC = 64 * RB / 16;
+  const int t = threadIdx.x;
+  unsigned char* row = lds + (t & 63) * RS + (t >> 6) * (RB / GDN_NW);
 #pragma unroll
-  for (int q = 0; q < RB / 16; ++q) {
+  for (int q = 0; q < RB / (16 * GDN_NW); ++q) {
     uint4 u;
     if constexpr (sizeof(T) == 2) {
       unsigned w[4];
@@ -265,14 +322,15 @@ __device__ __forceinline__ void rows_out(T* __restrict__ dst, const float* S, un
   }
   __syncthreads();
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const int e = (lane + 64 * c) * 16;
-    ((uint4*)dst)[lane + 64 * c] = *(const uint4*)(lds + (e / RB) * RS + e % RB);
+  for (int c0 = 0; c0 < NC; c0 += 64 * GDN_NW) {
+    const int c = c0 + t, e = c * 16;
+    ((uint4*)dst)[c] = *(const uint4*)(lds + (e / RB) * RS + e % RB);
   }
 }
 
-__global__ void __launch_bounds__(64) k_gdn_tree_vllm(GdnVArgs a) {
+__global__ void __launch_bounds__(64 * GDN_NW) k_gdn_tree_vllm(GdnVArgs a) {
   __shared__ __align__(16) float qs[GDN_DK];
+  __shared__ float red[2][GDN_NW][64];                       // [step parity][wave][lane]
   __shared__ int par[GDN_MAXN], path[GDN_MAXN];
   __shared__ int plen_s, bad_s;
   // the state rows (before the replay and after it) share their buffer with the replay's staging
@@ -295,77 +353,95 @@ __global__ void __launch_bounds__(64) k_gdn_tree_vllm(GdnVArgs a) {
   const int hv = u % a.HV;
   const int n = u / a.HV;
   const int h = hv / (a.HV / a.H);
-  const int lane = threadIdx.x;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int j = vs * 64 + lane;
+  const int i0 = wave * GDN_HK;                              // this wave's K elements
   const size_t srow = (size_t)a.HV * a.V * GDN_DK;                 // elements per slot
-  const size_t sblk = ((size_t)hv * a.V + vs * 64) * GDN_DK;       // the wave's 64 rows in a slot
+  const size_t sblk = ((size_t)hv * a.V + vs * 64) * GDN_DK;       // the workgroup's 64 rows in a slot
 
   // the node's own q (for the output) and the prefix state do not depend on the path: issued
   // before the parents, they share its memory round trip
   const uint16_t* rown = a.qkv + (size_t)n * a.ld;
   float q0 = bf16f(rown[(size_t)h * GDN_DK + lane]), q1 = bf16f(rown[(size_t)h * GDN_DK + 64 + lane]);
-  float S[GDN_DK];
+  float S[GDN_HK];
   if (a.bf16_state)
     rows_in((const uint16_t*)a.state + (size_t)a.prefix * srow + sblk, S, rows);
   else
     rows_in((const float*)a.state + (size_t)a.prefix * srow + sblk, S, rows);
   const float Aexp = expf(a.A_log[hv]), dtb = a.dt_bias[hv];
   if (gdn_path(a.parent, n, par, path, &plen_s, &bad_s)) {   // not BFS-ordered: NaN outputs, slot untouched
-    a.out[((size_t)n * a.HV + hv) * a.V + j] = 0x7fc0;
+    if (wave == 0) a.out[((size_t)n * a.HV + hv) * a.V + j] = 0x7fc0;
     return;
   }
   const int len = plen_s;
+  int rb = 0;                                                // red buffer of the next exchange
   const size_t koff = (size_t)a.H * GDN_DK + (size_t)h * GDN_DK;
   const size_t voff = 2 * (size_t)a.H * GDN_DK + (size_t)hv * a.V + j;
   for (int t0 = len - 1; t0 >= 0; t0 -= GDN_LB) {
     const int nb = min(GDN_LB, t0 + 1);                      // steps t0, t0 - 1, ..., t0 - nb + 1
-    float k0[GDN_LB], k1[GDN_LB], vj[GDN_LB], xa[GDN_LB], xb[GDN_LB];
+    if (wave == 0) {                                         // wave 0 stages the batch for both
+      float k0[GDN_LB], k1[GDN_LB], vj[GDN_LB], xa[GDN_LB], xb[GDN_LB];
 #pragma unroll
-    for (int b = 0; b < GDN_LB; ++b) {
-      const int m = path[t0 - min(b, nb - 1)];               // past nb: a repeat, never used
-      const uint16_t* row = a.qkv + (size_t)m * a.ld;
-      k0[b] = bf16f(row[koff + lane]);
-      k1[b] = bf16f(row[koff + 64 + lane]);
-      vj[b] = bf16f(row[voff]);
-      xa[b] = bf16f(a.ga[(size_t)m * a.HV + hv]);
-      xb[b] = bf16f(a.gb[(size_t)m * a.HV + hv]);
-    }
+      for (int b = 0; b < GDN_LB; ++b) {
+        const int m = path[t0 - min(b, nb - 1)];             // past nb: a repeat, never used
+        const uint16_t* row = a.qkv + (size_t)m * a.ld;
+        k0[b] = bf16f(row[koff + lane]);
+        k1[b] = bf16f(row[koff + 64 + lane]);
+        vj[b] = bf16f(row[voff]);
+        xa[b] = bf16f(a.ga[(size_t)m * a.HV + hv]);
+        xb[b] = bf16f(a.gb[(size_t)m * a.HV + hv]);
+      }
 #pragma unroll
-    for (int b = 0; b < GDN_LB; ++b) {
-      if (b < nb) {
-        float ik = 1.0f;
-        if (a.l2norm) ik = 1.0f / sqrtf(wave_sum(k0[b] * k0[b] + k1[b] * k1[b]) + 1e-6f);
-        ks[b][lane] = k0[b] * ik;
-        ks[b][lane + 64] = k1[b] * ik;
-        vjs[b][lane] = vj[b];
-        if (lane == 0) {
-          const float x = xa[b] + dtb;
-          const float sp = x <= 20.0f ? logf(1.0f + expf(x)) : x;
-          egs[b] = expf(-Aexp * sp);
-          bts[b] = round_bf16(1.0f / (1.0f + expf(-xb[b])));
+      for (int b = 0; b < GDN_LB; ++b) {
+        if (b < nb) {
+          float ik = 1.0f;
+          if (a.l2norm) ik = 1.0f / sqrtf(wave_sum(k0[b] * k0[b] + k1[b] * k1[b]) + 1e-6f);
+          ks[b][lane] = k0[b] * ik;
+          ks[b][lane + 64] = k1[b] * ik;
+          vjs[b][lane] = vj[b];
+          if (lane == 0) {
+            const float x = xa[b] + dtb;
+            const float sp = x <= 20.0f ? logf(1.0f + expf(x)) : x;
+            egs[b] = expf(-Aexp * sp);
+            bts[b] = round_bf16(1.0f / (1.0f + expf(-xb[b])));
+          }
         }
       }
     }
     __syncthreads();
     for (int b = 0; b < nb; ++b) {
-      const float kv = gdn_decay_dot(S, ks[b], egs[b]);
-      gdn_rank1(S, ks[b], (vjs[b][lane] - kv) * bts[b]);
+      red[rb][wave][lane] = gdn_decay_dot_h(S, ks[b] + i0, egs[b]);
+      __syncthreads();
+      float kv = 0.f;
+#pragma unroll
+      for (int w = 0; w < GDN_NW; ++w) kv += red[rb][w][lane];
+      rb ^= 1;
+      gdn_rank1_h(S, ks[b] + i0, (vjs[b][lane] - kv) * bts[b]);
       if (t0 - b > 0 && a.bf16_state) {   // an ancestor: its stored (bf16) state is what the child reads
 #pragma unroll
-        for (int i = 0; i < GDN_DK; ++i) S[i] = round_bf16(S[i]);
+        for (int i = 0; i < GDN_HK; ++i) S[i] = round_bf16(S[i]);
       }
     }
     __syncthreads();   // the batch's reads of ks / vjs are done before the next batch writes them
   }
   // output with the node's own q
-  if (a.l2norm) {
-    const float iq = 1.0f / sqrtf(wave_sum(q0 * q0 + q1 * q1) + 1e-6f);
-    q0 *= iq; q1 *= iq;
+  if (wave == 0) {
+    if (a.l2norm) {
+      const float iq = 1.0f / sqrtf(wave_sum(q0 * q0 + q1 * q1) + 1e-6f);
+      q0 *= iq; q1 *= iq;
+    }
+    qs[lane] = q0 * a.scale;
+    qs[lane + 64] = q1 * a.scale;
   }
-  qs[lane] = q0 * a.scale;
-  qs[lane + 64] = q1 * a.scale;
   __syncthreads();
-  a.out[((size_t)n * a.HV + hv) * a.V + j] = to_bf16(gdn_dot(S, qs));
+  red[rb][wave][lane] = gdn_dot_h(S, qs + i0);
+  __syncthreads();
+  if (wave == 0) {
+    float o = 0.f;
+#pragma unroll
+    for (int w = 0; w < GDN_NW; ++w) o += red[rb][w][lane];
+    a.out[((size_t)n * a.HV + hv) * a.V + j] = to_bf16(o);
+  }
   const size_t dst = (size_t)a.slots[n] * srow + sblk;
   if (a.bf16_state)
     rows_out((uint16_t*)a.state + dst, S, rows);
@@ -388,7 +464,7 @@ int cfh_gdn_tree(const void* q, const void* k, const void* v, const float* g, co
   a.S0 = S0; a.parent = parent; a.out = out; a.states = states; a.N = N; a.H = H; a.Dv = Dv;
   a.l2norm = use_l2norm ? 1 : 0; a.l2mode = l2mode ? 1 : 0; a.scale = 1.0f / sqrtf((float)Dk);
   const long long blocks = (long long)N * H * (Dv / 64);
-  hipLaunchKernelGGL(k_gdn_tree, dim3((unsigned)blocks), dim3(64), 0, (hipStream_t)stream, a);
+  hipLaunchKernelGGL(k_gdn_tree, dim3((unsigned)blocks), dim3(64 * GDN_NW), 0, (hipStream_t)stream, a);
   CFH_LAUNCH_CHECK();
   return CFH_OK;
 }
@@ -408,7 +484,7 @@ int cfh_gdn_tree_vllm(const void* mixed_qkv, const void* a, const void* b, const
   g.out = (uint16_t*)out; g.N = N; g.H = H; g.HV = HV; g.V = V; g.ld = 2 * H * K + HV * V;
   g.prefix = prefix_slot; g.bf16_state = state_bf16 ? 1 : 0; g.l2norm = use_l2norm ? 1 : 0; g.scale = scale;
   const long long blocks = (long long)N * HV * (V / 64);
-  hipLaunchKernelGGL(k_gdn_tree_vllm, dim3((unsigned)blocks), dim3(64), 0, (hipStream_t)stream, g);
+  hipLaunchKernelGGL(k_gdn_tree_vllm, dim3((unsigned)blocks), dim3(64 * GDN_NW), 0, (hipStream_t)stream, g);
   CFH_LAUNCH_CHECK();
   return CFH_OK;
 }

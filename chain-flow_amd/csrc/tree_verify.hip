@@ -311,9 +311,10 @@ __global__ void __launch_bounds__(256) k_argmax_part(const u16* logits, int V, l
 }
 
 // Per request r (one workgroup): its rows s0 .. s0 + n of the flat logits (row 0 = the last
-// committed token, row 1 + i = tree node i) get their arg-max from the slices; then one thread
+// committed token, row 1 + i = tree node i) get their arg-max from the slices; then the wave
 // walks the tree: from the root row, emit the target's token at the current row; move to the first
-// child whose draft token equals it; stop when none does.  Output tokens (accepted drafts + the
+// child whose draft token equals it (64 nodes tested at a time, a ballot picks the lowest); stop
+// when none does.  Output tokens (accepted drafts + the
 // bonus) [B][max_spec + 1] (-1 padded), accepted path (node per depth, -1 padded) [B][max_spec],
 // accepted length [B].
 struct DescentArgs {
@@ -355,23 +356,36 @@ __global__ void __launch_bounds__(64) k_tree_descent(DescentArgs a) {
   for (int i = threadIdx.x; i <= a.max_spec; i += blockDim.x) ot[i] = -1;
   for (int i = threadIdx.x; i < a.max_spec; i += blockDim.x) pt[i] = -1;
   __syncthreads();
-  if (threadIdx.x != 0) return;
+  // the walk: at each level the wave tests 64 nodes at a time for (parent == cur, token == the
+  // row's argmax); the lowest matching index is the first child in draft order
+  const int lane = threadIdx.x;
   int cur = -1, pos = 0;
   for (int step = 0; step <= a.max_spec; ++step) {
     const int tok = lds ? s_arg[cur + 1] : a.row_argmax[s0 + cur + 1];
-    ot[pos] = tok;
+    if (lane == 0) ot[pos] = tok;
     int nxt = -1;
-    for (int i = 0; i < n && pos < a.max_spec; ++i) {
-      const int pi = lds ? s_par[i] : a.parents[d0 + i];
-      const int ti = lds ? s_tok[i] : a.draft[d0 + i];
-      if (pi == cur && ti == tok) { nxt = i; break; }
+    if (pos < a.max_spec) {
+      for (int i0 = 0; i0 < n; i0 += 64) {
+        const int i = i0 + lane;
+        bool hit = false;
+        if (i < n) {
+          const int pi = lds ? s_par[i] : a.parents[d0 + i];
+          const int ti = lds ? s_tok[i] : a.draft[d0 + i];
+          hit = pi == cur && ti == tok;
+        }
+        const unsigned long long m = __ballot(hit);
+        if (m) {
+          nxt = i0 + __ffsll((long long)m) - 1;
+          break;
+        }
+      }
     }
     if (nxt < 0) break;
-    pt[pos] = nxt;
+    if (lane == 0) pt[pos] = nxt;
     cur = nxt;
     ++pos;
   }
-  a.len[r] = pos;
+  if (lane == 0) a.len[r] = pos;
 }
 
 }  // namespace

@@ -6,13 +6,14 @@
 // with q, k l2-normalised (x / (|x| + 1e-6), or x / sqrt(|x|^2 + 1e-6) as in the Triton kernels of
 // cf/vllm_tree/tree_ssm.py:60-62) and q scaled by Dk^-1/2.  State layout [H][Dk][Dv].
 //
-// Execution plan (path-parallel): one wave per (node, head, 64-column value slice).  Lane j owns
-// state column j (all Dk = 128 rows) in registers and replays the node's ancestor chain from the
-// root, so every node's state and output come from the same sequential per-path recurrence
-// (tree_scan.py:78-90) and no wave waits for another.  k of each path step is normalised by the
-// wave and broadcast through LDS; q only for the node itself (the output).  The recompute costs
-// depth x 3 Dk FMA-class operations per lane per node, below the state traffic (S0 read, node
-// state written).
+// Execution plan (path-parallel): one workgroup per (node, head, 64-column value slice), four
+// waves of it each holding 32 of the Dk = 128 state rows (lane j: column j) in registers.  The
+// workgroup replays the node's ancestor chain from the root, so every node's state and output come
+// from the same sequential per-path recurrence (tree_scan.py:78-90) and no workgroup waits for
+// another; each step's dot products are summed over the four waves through LDS.  k of each path
+// step is normalised once and broadcast through LDS; q only for the node itself (the output).
+// The recompute costs depth x 3 Dk FMA-class operations per column per node, below the state
+// traffic (S0 read, node state written).
 #include "cfh_common.h"
 #include "cfh_host.h"
 
@@ -63,36 +64,6 @@ __device__ int gdn_path(const int* __restrict__ parent, int n, int* par, int* pa
   return *bad_s;
 }
 
-// kv = S^T k after S *= e (S in registers, k broadcast from LDS), four partial sums
-__device__ __forceinline__ float gdn_decay_dot(float* S, const float* kk, float e) {
-  float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
-#pragma unroll
-  for (int i = 0; i < GDN_DK; i += 4) {
-    const float4 k4 = *(const float4*)(kk + i);
-    S[i] *= e; S[i + 1] *= e; S[i + 2] *= e; S[i + 3] *= e;
-    p0 += S[i] * k4.x; p1 += S[i + 1] * k4.y; p2 += S[i + 2] * k4.z; p3 += S[i + 3] * k4.w;
-  }
-  return (p0 + p1) + (p2 + p3);
-}
-
-__device__ __forceinline__ float gdn_dot(const float* S, const float* qq) {
-  float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
-#pragma unroll
-  for (int i = 0; i < GDN_DK; i += 4) {
-    const float4 q4 = *(const float4*)(qq + i);
-    p0 += S[i] * q4.x; p1 += S[i + 1] * q4.y; p2 += S[i + 2] * q4.z; p3 += S[i + 3] * q4.w;
-  }
-  return (p0 + p1) + (p2 + p3);
-}
-
-__device__ __forceinline__ void gdn_rank1(float* S, const float* kk, float delta) {
-#pragma unroll
-  for (int i = 0; i < GDN_DK; i += 4) {
-    const float4 k4 = *(const float4*)(kk + i);
-    S[i] += k4.x * delta; S[i + 1] += k4.y * delta; S[i + 2] += k4.z * delta; S[i + 3] += k4.w * delta;
-  }
-}
-
 // GDN_NW waves per (node, head, 64-column value slice): wave w holds state rows
 // [GDN_HK w, GDN_HK (w + 1)) of the slice's columns, so the deepest nodes' replays (the critical
 // path) spread over GDN_NW times the SIMDs.  Each step's dot product is the sum of the waves'
@@ -100,6 +71,7 @@ __device__ __forceinline__ void gdn_rank1(float* S, const float* kk, float delta
 constexpr int GDN_NW = 4;                  // waves per (node, head, value slice)
 constexpr int GDN_HK = GDN_DK / GDN_NW;    // state rows a wave holds
 
+// kv partial = S^T k over the wave's rows after S *= e (k broadcast from LDS), four partial sums
 __device__ __forceinline__ float gdn_decay_dot_h(float* S, const float* kk, float e) {
   float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
 #pragma unroll

@@ -519,10 +519,6 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 constexpr int GPF = 4;            // k-steps per LDS chunk
 constexpr int GKC = 32 * GPF;     // 128 columns per chunk: a row is 16 slots of 16 bytes
 
-__device__ __forceinline__ float bf16_round(float x) {
-  return (float)(__bf16)x;
-}
-
 struct GemmArgs {
   const uint16_t* x;   // [M][d] bf16
   const uint16_t* W;   // [V][d] bf16

@@ -615,6 +615,15 @@ int choose_ks(int nex, int tiles, int K, int S, int target, size_t lds_cap) {
   return best;
 }
 
+// Waves per workgroup for a launch of nunits (expert, k-chunk) units of `tiles` column tiles: the
+// most (at most maxw, a power of two dividing tiles) that still gives about one workgroup per CU
+// (nunits * tiles / w >= 240); narrow widths take fewer waves so that the launch spans the chip.
+int wpb_for_grid(int tiles, int nunits, int maxw) {
+  int best = 1;
+  for (int w = 2; w <= maxw && tiles % w == 0 && (long long)nunits * tiles / w >= 240; w *= 2) best = w;
+  return best;
+}
+
 int pick_wpb(int tiles, int tpw) {
   for (int w : {8, 4, 2, 1})
     if (tiles % (w * tpw) == 0) return w;

@@ -206,13 +206,15 @@ Plan make_plan(const cfh_flow_dims* dm) {
   p.ks_kv = ksplit_for(p.nch * p.NL, 2 * p.d / 16, p.d, p.C);
   p.ks_tau = ksplit_for(p.nch, p.d / 16, p.d, p.E);
   p.wpb_qc = std::min(4, pick_wpb(tiles_d, 1));
-  p.wpb_w2 = w2_wide ? 16 : std::min(4, pick_wpb(tiles_d, 1));
+  p.wpb_w2 = w2_wide ? wpb_for_grid(tiles_d, p.nch * p.ks_w2, 16) : std::min(4, pick_wpb(tiles_d, 1));
   p.wpb_out = pick_wpb(tiles_d, 1);
   p.tpw_att = (tiles_d % 16 == 0) ? 2 : 1;
   p.wpb_att = pick_wpb(tiles_d, p.tpw_att);
   fit_grid(tiles_d, p.nch * p.ks_att, &p.wpb_att, &p.tpw_att);
-  p.wpb_full = pick_wpb(3 * tiles_d, 1);
-  p.wpb_w1 = (p.fd / 16) % 16 == 0 ? 16 : pick_wpb(p.fd / 16, 1);
+  // full-K launches (QKV, W1): one workgroup per CU at any width (16 waves for W1 and 8 for QKV
+  // at d = 5120, fewer at narrow widths, where those would leave most CUs idle)
+  p.wpb_full = wpb_for_grid(3 * tiles_d, p.nch, 8);
+  p.wpb_w1 = wpb_for_grid(p.fd / 16, p.nch, 16);
   // the cross attention holds every q partial of its groups in registers: fewer QC splits if needed
   for (int ks = p.ks_qc; ks > 1; --ks) {
     SArgs a = {};

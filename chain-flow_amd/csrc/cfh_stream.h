@@ -618,9 +618,13 @@ int choose_ks(int nex, int tiles, int K, int S, int target, size_t lds_cap) {
 // Waves per workgroup for a launch of nunits (expert, k-chunk) units of `tiles` column tiles: the
 // most (at most maxw, a power of two dividing tiles) that still gives about one workgroup per CU
 // (nunits * tiles / w >= 240); narrow widths take fewer waves so that the launch spans the chip.
-int wpb_for_grid(int tiles, int nunits, int maxw) {
+// `vecs` (the operand's 8-half vectors, S rows x K-chunk / 8) raises the count again until every
+// thread's operand loads fit its slots (16 up to 8 waves, 8 above).
+int wpb_for_grid(int tiles, int nunits, int maxw, int vecs) {
+  auto fits = [&](int w) { return (vecs + 64 * w - 1) / (64 * w) <= (w > 8 ? 8 : 16); };
   int best = 1;
   for (int w = 2; w <= maxw && tiles % w == 0 && (long long)nunits * tiles / w >= 240; w *= 2) best = w;
+  while (!fits(best) && best * 2 <= maxw && tiles % (best * 2) == 0) best *= 2;
   return best;
 }
 

@@ -205,16 +205,16 @@ Plan make_plan(const cfh_flow_dims* dm) {
   p.ks_out = std::max(choose_ks(p.nch, tiles_d, p.d, p.CS, 2048, cap), 1);
   p.ks_kv = ksplit_for(p.nch * p.NL, 2 * p.d / 16, p.d, p.C);
   p.ks_tau = ksplit_for(p.nch, p.d / 16, p.d, p.E);
-  p.wpb_qc = std::min(4, pick_wpb(tiles_d, 1));
-  p.wpb_w2 = w2_wide ? wpb_for_grid(tiles_d, p.nch * p.ks_w2, 16) : std::min(4, pick_wpb(tiles_d, 1));
-  p.wpb_out = pick_wpb(tiles_d, 1);
+  p.wpb_w2 = w2_wide ? wpb_for_grid(tiles_d, p.nch * p.ks_w2, 16, p.Smax * (p.fd / p.ks_w2) / 8)
+                     : std::min(4, pick_wpb(tiles_d, 1));
+  p.wpb_out = wpb_for_grid(tiles_d, p.nch * p.ks_out, 8, p.CS * (p.d / p.ks_out) / 8);
   p.tpw_att = (tiles_d % 16 == 0) ? 2 : 1;
-  p.wpb_att = pick_wpb(tiles_d, p.tpw_att);
+  p.wpb_att = pick_wpb(tiles_d, p.tpw_att);   // (the attention staging needs the waves' slots)
   fit_grid(tiles_d, p.nch * p.ks_att, &p.wpb_att, &p.tpw_att);
   // full-K launches (QKV, W1): one workgroup per CU at any width (16 waves for W1 and 8 for QKV
   // at d = 5120, fewer at narrow widths, where those would leave most CUs idle)
-  p.wpb_full = wpb_for_grid(3 * tiles_d, p.nch, 8);
-  p.wpb_w1 = wpb_for_grid(p.fd / 16, p.nch, 16);
+  p.wpb_full = wpb_for_grid(3 * tiles_d, p.nch, 8, p.Smax * p.d / 8);
+  p.wpb_w1 = wpb_for_grid(p.fd / 16, p.nch, 16, p.Smax * p.d / 8);
   // the cross attention holds every q partial of its groups in registers: fewer QC splits if needed
   for (int ks = p.ks_qc; ks > 1; --ks) {
     SArgs a = {};
@@ -223,6 +223,7 @@ Plan make_plan(const cfh_flow_dims* dm) {
     p.ks_qc = ks;
     break;
   }
+  p.wpb_qc = wpb_for_grid(tiles_d, p.nch * p.ks_qc, 4, p.Smax * (p.d / p.ks_qc) / 8);
   fit_grid(tiles_d, p.nch * p.ks_qc, &p.wpb_qc, nullptr);
   fit_grid(tiles_d, p.nch * p.ks_out, &p.wpb_out, nullptr);
   p.pks = std::max(std::max(p.ks_att, p.ks_w2), p.ks_out);

@@ -110,10 +110,11 @@ struct VaePlan {
 };
 
 // Split-K launch shape of an N x K streaming product over T rows: as many k-chunks as reach ~2048
-// wave units (at least 8 k-steps each; one chunk when K has fewer), 8-wave (or smaller) workgroups.
+// wave units (at least 8 k-steps each; one chunk when K has fewer), workgroups of up to 8 waves
+// that still fill one workgroup per CU.
 void split_shape(int N, int K, int T, int* ks, int* wpb) {
   *ks = std::max(choose_ks(1, N / 16, K, T, 2048, 96 * 1024), 1);
-  *wpb = pick_wpb(N / 16, 1);
+  *wpb = wpb_for_grid(N / 16, *ks, 8, T * (K / *ks) / 8);
 }
 
 VaePlan vae_plan(const cfh_vae_dims* dm, int T) {
@@ -124,10 +125,10 @@ VaePlan vae_plan(const cfh_vae_dims* dm, int T) {
   auto half = [&](HalfPlan& h, int kin, int nout) {
     h.Kin = kin; h.Nout = nout;
     split_shape(p.I, kin, T, &h.ks_in, &h.wpb_in);
-    h.wpb_qkv = pick_wpb(3 * p.I / 16, 1);
+    h.wpb_qkv = wpb_for_grid(3 * p.I / 16, 1, 8, T * p.I / 8);
     h.ks_att = p.H / hpk;
-    h.wpb_att = pick_wpb(p.I / 16, 1);
-    h.wpb_w1 = pick_wpb(p.F / 16, 1);
+    h.wpb_att = pick_wpb(p.I / 16, 1);   // (the attention staging needs the waves' slots)
+    h.wpb_w1 = wpb_for_grid(p.F / 16, 1, 8, T * p.I / 8);
     split_shape(p.I, p.F, T, &h.ks_w2, &h.wpb_w2);
     split_shape(nout, p.I, T, &h.ks_out, &h.wpb_out);
   };

@@ -48,6 +48,24 @@ def test_flow_matches_oracle(cuda, d, layers, steps):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("d,kd,cs", [(1024, 16, 8), (640, 16, 8)])
+def test_flow_long_draft_matches_oracle(cuda, d, kd, cs):
+    """Draft length 16 in two chunks of 8 (16 rows in the second chunk's launches)."""
+    cfg = flownet(d, layers=1, flow_steps=2, draft_length=kd, chunk_size=cs)
+    W = _flow_weights(cfg)
+    ctx = synthetic_context(1, cfg.context_size, d, seed=3)
+    print(f"[flow parity] d={d} draft_length={kd} chunk={cs}", flush=True)
+    ff = FusedFlow(cfg, {k: v.to(cuda) for k, v in W.items()}, device=cuda)
+    z = ff.predict_hidden(ctx.to(cuda))
+    torch.cuda.synchronize()
+    ref = oflow.predict_hidden(weights64(W), to64(ctx), _ocfg(cfg), numerics="fp16")
+    err = rel_err(to64(z), ref)
+    print(f"  rel err {err:.3e}", flush=True)
+    assert np.isfinite(to64(z)).all()
+    assert err < TOL_FP16
+
+
+@pytest.mark.gpu
 def test_flow_is_bit_reproducible(cuda):
     """Every reduction runs in a fixed order (no atomics): repeated drafts give bit-identical
     hidden states."""

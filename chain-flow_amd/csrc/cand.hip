@@ -22,21 +22,27 @@ __device__ __forceinline__ unsigned order_key(float v) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Exclusive scan of one int per thread over the workgroup (LDS, Hillis-Steele); *total = the sum.
+// Exclusive scan of one int per thread over the workgroup; *total = the sum.  Each wave scans its
+// lanes with shuffles, the 16 wave totals go through LDS: two barriers, not two per doubling step.
 __device__ int block_exscan(int v, int* buf, int* total) {
-  const int t = threadIdx.x;
-  buf[t] = v;
-  __syncthreads();
-  for (int off = 1; off < CT; off <<= 1) {
-    const int add = t >= off ? buf[t - off] : 0;
-    __syncthreads();
-    buf[t] += add;
-    __syncthreads();
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  int incl = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int u = __shfl_up(incl, off);
+    if (lane >= off) incl += u;
   }
-  const int incl = buf[t];
-  *total = buf[CT - 1];
+  if (lane == 63) buf[wave] = incl;
   __syncthreads();
-  return incl - v;
+  int base = 0, sum = 0;
+  for (int w = 0; w < CT / 64; ++w) {
+    const int x = buf[w];
+    base += w < wave ? x : 0;
+    sum += x;
+  }
+  *total = sum;
+  __syncthreads();   // buf is reused by the next scan
+  return base + incl - v;
 }
 
 struct CandArgs {
@@ -45,10 +51,12 @@ struct CandArgs {
   const int* sl;                  // [Vs] or null
   int* cand_local;                // [B][M]
   int* cand_global;               // [B][M] or null
-  unsigned* keys;                 // ws [B][Vs]
+  unsigned* keys;                 // ws [B][Vp], Vp = Vs rounded up to 4 (16-byte rows)
   long long ld;
   int n, Vs, M;
 };
+
+__host__ __device__ constexpr int padded_vs(int Vs) { return (Vs + 3) & ~3; }
 
 // keys[b][j] for 4 columns a thread, grid (B, column blocks): coalesced and spread over the chip
 __global__ void __launch_bounds__(256) k_cand_keys(CandArgs a) {
@@ -61,26 +69,26 @@ __global__ void __launch_bounds__(256) k_cand_keys(CandArgs a) {
       const size_t r = (size_t)b * a.n + d;
       v = fmaxf(v, (float)__builtin_bit_cast(_Float16, a.logits[r * a.ld + j]) - a.lse[r]);
     }
-    a.keys[(size_t)b * a.Vs + j] = order_key(v);
+    a.keys[(size_t)b * padded_vs(a.Vs) + j] = order_key(v);
   }
 }
 
-// Radix select in three digits of the 32-bit key -- bits 31..20, 19..8, 7..0 (4096 / 4096 / 256
-// bins): the wide first digit spreads the log-probabilities, whose top bits (sign and exponent)
-// take only a few values, over many bins instead of serialising the histogram atomics on one.
-// Each pass counts only the keys that match the digits chosen so far; the digit holding the M-th
-// largest key is found by a workgroup scan over the bins (thread t owns bins 4t .. 4t+3 from the
-// top).
-__device__ void select_digit(const unsigned* keys, int Vs, unsigned prefix, unsigned pmask, int shift, int bins,
-                             int* hist, int* scan, unsigned* s_prefix, int* s_rem) {
+// Radix select over the bits below the keys' common prefix, 12 bits a pass (4096 bins; the last
+// pass takes what is left): the bits every key shares (the sign and most of the exponent of the
+// log-probabilities) would put all keys in a few bins and serialise the histogram atomics on
+// them.  Each pass counts only the keys that match the digits chosen so far; the digit holding the
+// M-th largest key is found by a workgroup scan over the bins (thread t owns bins 4t .. 4t+3 from
+// the top).  `each` visits the thread's keys.
+template <typename Each>
+__device__ void select_digit(Each& each, unsigned prefix, unsigned pmask, int shift, int bins, int* hist, int* scan,
+                             unsigned* s_prefix, int* s_rem) {
   const int t = threadIdx.x;
   for (int i = t; i < bins; i += CT) hist[i] = 0;
   __syncthreads();
   const unsigned dmask = (unsigned)bins - 1;
-  for (int j = t; j < Vs; j += CT) {
-    const unsigned k = keys[j];
+  each([&](unsigned k) {
     if ((k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & dmask], 1);
-  }
+  });
   __syncthreads();
   const int per = bins / CT > 0 ? bins / CT : 1;            // 4 bins a thread at 4096, else 1
   int cnt[4] = {0, 0, 0, 0}, sum = 0;
@@ -104,46 +112,161 @@ __device__ void select_digit(const unsigned* keys, int Vs, unsigned prefix, unsi
   __syncthreads();
 }
 
+// Every pass reads the keys as 16-byte vectors (4 columns a lane; consecutive lanes, consecutive
+// vectors) in batches of KB loads a thread issues together: one workgroup per request is bound by
+// the loads it keeps in flight.  The compaction works on 256-column segments, one wave each: ballot
+// counts per segment, then segment offsets by two workgroup scans, then each column's output slot
+// from the ballots of the lanes below it.  The shortlist ids are loaded with the keys, ahead of any
+// store (a load issued after a store to memory it may alias waits for a full round trip).
+constexpr int KB = 8;         // vectors in flight per thread per batch
+constexpr int SEGB = 4;       // segments in flight per wave
+constexpr int MAXSEG = 1024;  // 256-column segments: Vs <= 262,144
+
 __global__ void __launch_bounds__(CT) k_cand_select(CandArgs a) {
   __shared__ int hist[4096];
   __shared__ int scan[CT];
+  __shared__ int sg_a[MAXSEG], sg_b[MAXSEG];
   __shared__ unsigned s_prefix;
   __shared__ int s_rem;
-  const int b = blockIdx.x, t = threadIdx.x;
-  const unsigned* keys = a.keys + (size_t)b * a.Vs;
-  if (t == 0) { s_prefix = 0; s_rem = a.M; }
+  const int b = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int nv = padded_vs(a.Vs) / 4;
+  const uint4* keys = (const uint4*)(a.keys + (size_t)b * padded_vs(a.Vs));
+  auto each = [&](auto&& f) {
+    for (int v0 = t; v0 < nv; v0 += CT * KB) {
+      uint4 kb[KB];
+#pragma unroll
+      for (int u = 0; u < KB; ++u) kb[u] = keys[min(v0 + u * CT, nv - 1)];   // (past nv: never used)
+#pragma unroll
+      for (int u = 0; u < KB; ++u) {
+        const int j = 4 * (v0 + u * CT);
+        if (j < a.Vs) f(kb[u].x);
+        if (j + 1 < a.Vs) f(kb[u].y);
+        if (j + 2 < a.Vs) f(kb[u].z);
+        if (j + 3 < a.Vs) f(kb[u].w);
+      }
+    }
+  };
+  // the keys' common prefix: bits where the AND and the OR of every key agree
+  unsigned kand = ~0u, kor = 0u;
+  each([&](unsigned k) {
+    kand &= k;
+    kor |= k;
+  });
+  for (int off = 32; off > 0; off >>= 1) {
+    kand &= (unsigned)__shfl_xor((int)kand, off);
+    kor |= (unsigned)__shfl_xor((int)kor, off);
+  }
+  if (lane == 0) {
+    scan[wave] = (int)kand;
+    scan[CT / 64 + wave] = (int)kor;
+  }
   __syncthreads();
-  select_digit(keys, a.Vs, 0u, 0u, 20, 4096, hist, scan, &s_prefix, &s_rem);
-  select_digit(keys, a.Vs, s_prefix, 0xFFF00000u, 8, 4096, hist, scan, &s_prefix, &s_rem);
-  select_digit(keys, a.Vs, s_prefix, 0xFFFFFF00u, 0, 256, hist, scan, &s_prefix, &s_rem);
+  kand = ~0u;
+  kor = 0u;
+  for (int w = 0; w < CT / 64; ++w) {
+    kand &= (unsigned)scan[w];
+    kor |= (unsigned)scan[CT / 64 + w];
+  }
+  __syncthreads();
+  const unsigned diff = kand ^ kor;
+  // bits [lo, 32) are fixed; lo = 0 when every key is equal (then all M come from the ties)
+  int lo = diff ? 32 - __clz(diff) : 0;
+  unsigned pmask = lo >= 32 ? 0u : ~((1u << lo) - 1u);
+  if (t == 0) { s_prefix = kand & pmask; s_rem = a.M; }
+  __syncthreads();
+  while (lo > 0) {
+    const int w = min(12, lo), shift = lo - w;
+    select_digit(each, s_prefix, pmask, shift, 1 << w, hist, scan, &s_prefix, &s_rem);
+    pmask |= ((1u << w) - 1u) << shift;
+    lo = shift;
+  }
   const unsigned T = s_prefix;
   const int need = s_rem;   // ties at T that belong to the M (lowest columns first)
-  // compaction in column order: thread t owns the contiguous columns [c0, c1)
-  const int per = (a.Vs + CT - 1) / CT;
-  const int c0 = min(t * per, a.Vs), c1 = min(c0 + per, a.Vs);
-  int gt = 0, eq = 0;
-  for (int j = c0; j < c1; ++j) {
-    const unsigned k = keys[j];
-    gt += k > T;
-    eq += k == T;
-  }
+  // compaction in column order by 256-column segments (lane l holds columns 4l .. 4l+3)
+  const int nseg = (nv + 63) / 64;
+  const unsigned long long below = (1ull << lane) - 1ull;
+  const bool gather = a.sl && a.cand_global;
+  auto segments = [&](bool ids, auto&& f) {   // f(segment, first column, keys, ids) on every lane
+    for (int s0 = wave; s0 < nseg; s0 += (CT / 64) * SEGB) {
+      uint4 kk[SEGB];
+      int4 ii[SEGB];
+#pragma unroll
+      for (int u = 0; u < SEGB; ++u) kk[u] = keys[min((s0 + u * (CT / 64)) * 64 + lane, nv - 1)];
+      if (ids) {
+#pragma unroll
+        for (int u = 0; u < SEGB; ++u) {
+          const int j = ((s0 + u * (CT / 64)) * 64 + lane) * 4;
+          ii[u] = make_int4(a.sl[min(j, a.Vs - 1)], a.sl[min(j + 1, a.Vs - 1)], a.sl[min(j + 2, a.Vs - 1)],
+                            a.sl[min(j + 3, a.Vs - 1)]);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < SEGB; ++u) {
+        const int sg = s0 + u * (CT / 64);
+        if (sg < nseg) f(sg, (sg * 64 + lane) * 4, kk[u], ii[u]);   // (wave-uniform)
+      }
+    }
+  };
+  segments(false, [&](int sg, int j, uint4 k4, int4) {
+    const unsigned k[4] = {k4.x, k4.y, k4.z, k4.w};
+    int gt = 0, eq = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const bool ok = j + q < a.Vs;
+      gt += __popcll(__ballot(ok && k[q] > T));
+      eq += __popcll(__ballot(ok && k[q] == T));
+    }
+    if (lane == 0) { sg_a[sg] = gt; sg_b[sg] = eq; }
+  });
+  __syncthreads();
+  // segment offsets: thread t owns segments [g0, g1); sg_b becomes the ties before the segment,
+  // sg_a the output slot of its first column
+  const int sp = (nseg + CT - 1) / CT;
+  const int g0 = min(t * sp, nseg), g1 = min(g0 + sp, nseg);
+  int eq_own = 0;
+  for (int g = g0; g < g1; ++g) eq_own += sg_b[g];
   int tot;
-  const int eq_before = block_exscan(eq, scan, &tot);
-  const int take_eq = min(max(need - eq_before, 0), eq);
-  int out = block_exscan(gt + take_eq, scan, &tot);
-  int eq_seen = 0;
+  int eq_run = block_exscan(eq_own, scan, &tot);
+  int out_own = 0;
+  for (int g = g0; g < g1; ++g) out_own += sg_a[g] + min(max(need - eq_run, 0), sg_b[g]), eq_run += sg_b[g];
+  int out_run = block_exscan(out_own, scan, &tot);
+  eq_run -= eq_own;
+  for (int g = g0; g < g1; ++g) {
+    const int gt = sg_a[g], eq = sg_b[g];
+    sg_a[g] = out_run;
+    sg_b[g] = eq_run;
+    out_run += gt + min(max(need - eq_run, 0), eq);
+    eq_run += eq;
+  }
+  __syncthreads();
   int* cl = a.cand_local + (size_t)b * a.M;
   int* cg = a.cand_global ? a.cand_global + (size_t)b * a.M : nullptr;
-  for (int j = c0; j < c1; ++j) {
-    const unsigned k = keys[j];
-    bool take = k > T;
-    if (k == T) take = eq_seen++ < take_eq;
-    if (take) {
-      cl[out] = j;
-      if (cg) cg[out] = a.sl ? a.sl[j] : j;
-      ++out;
+  segments(gather, [&](int sg, int j, uint4 k4, int4 i4) {
+    const unsigned k[4] = {k4.x, k4.y, k4.z, k4.w};
+    const int id[4] = {i4.x, i4.y, i4.z, i4.w};
+    bool eqb[4], take[4];
+    int eq_rank = sg_b[sg];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      eqb[q] = j + q < a.Vs && k[q] == T;
+      eq_rank += __popcll(__ballot(eqb[q]) & below);
     }
-  }
+    int pos = sg_a[sg];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      take[q] = (j + q < a.Vs && k[q] > T) || (eqb[q] && eq_rank < need);
+      eq_rank += eqb[q];
+      pos += __popcll(__ballot(take[q]) & below);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (take[q]) {
+        cl[pos] = j + q;
+        if (cg) cg[pos] = gather ? id[q] : j + q;
+        ++pos;
+      }
+    }
+  });
 }
 
 }  // namespace
@@ -152,7 +275,7 @@ extern "C" {
 
 int64_t cfh_cand_ws_bytes(int B, int Vs) {
   if (B < 0 || Vs < 0) return -1;
-  return (int64_t)B * Vs * 4;
+  return (int64_t)B * padded_vs(Vs) * 4;
 }
 
 int cfh_cand_topm(const void* logits, long long ld, const float* lse, int B, int n, int Vs, int M, const int32_t* sl,
@@ -160,6 +283,8 @@ int cfh_cand_topm(const void* logits, long long ld, const float* lse, int B, int
   if (B == 0) return CFH_OK;
   if (!logits || !lse || !cand_local || !ws || B < 0 || n < 1 || Vs < 1 || M < 1 || M > Vs || ld < Vs)
     return CFH_E_INVALID;
+  if ((uintptr_t)ws & 15) return CFH_E_INVALID;
+  if (Vs > 256 * MAXSEG) return CFH_E_UNSUPPORTED;
   CandArgs a = {(const unsigned short*)logits, lse, sl, cand_local, cand_global, (unsigned*)ws, ld, n, Vs, M};
   hipStream_t st = (hipStream_t)stream;
   hipLaunchKernelGGL(k_cand_keys, dim3(B, (Vs + 1023) / 1024), dim3(256), 0, st, a);

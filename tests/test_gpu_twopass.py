@@ -14,6 +14,7 @@ import pytest
 import torch
 
 from conftest import to64
+from chain_flow_amd import _lib
 from chain_flow_amd.config import flownet
 from chain_flow_amd.drafter import Drafter
 from chain_flow_amd.weights import make_weights, synthetic_context
@@ -53,6 +54,44 @@ def test_candidate_selection_is_exact(cuda, shared):
             assert np.array_equal(got, want), (b, dd)
             gg = (glob[b] if shared else glob[b, dd]).cpu().numpy()
             assert np.array_equal(gg, sl.numpy()[want])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,n,Vs,M,ld,kind", [
+    (3, 5, 1001, 77, 1003, "ties"),          # ragged width (not a multiple of 4), heavy ties
+    (2, 1, 62642, 8192, 62642, "randn"),     # the shortlist width of the d=5120 head
+    (1, 3, 70001, 70001, 70001, "randn"),    # M = every column
+    (2, 2, 5, 3, 8, "equal"),                # every value equal: all M from the ties
+    (1, 2, 262144, 1000, 262144, "ties"),    # the largest supported width
+])
+def test_candidate_select_edges(cuda, B, n, Vs, M, ld, kind):
+    """cfh_cand_topm through the C-ABI against numpy's stable top-M of
+    max_d(float(logit) - lse) in fp32 (ties to the lower column), output in column order."""
+    g = np.random.default_rng(Vs + M)
+    if kind == "ties":
+        lg = (g.integers(-40, 8, size=(B * n, ld)) * 0.25).astype(np.float16)
+    elif kind == "equal":
+        lg = np.full((B * n, ld), -1.5, np.float16)
+    else:
+        lg = (g.standard_normal((B * n, ld)) * 3).astype(np.float16)
+    lse = (g.integers(0, 4, size=B * n) * 0.5 + 10).astype(np.float32)
+    if kind == "equal":
+        lse[:] = 10
+    sl = np.sort(g.choice(4 * Vs, Vs, replace=False)).astype(np.int32)
+    L = _lib.lib()
+    dl, dlse, dsl = torch.from_numpy(lg).to(cuda), torch.from_numpy(lse).to(cuda), torch.from_numpy(sl).to(cuda)
+    local = torch.full((B, M), -1, dtype=torch.int32, device=cuda)
+    glob = torch.full((B, M), -1, dtype=torch.int32, device=cuda)
+    ws = torch.empty(int(L.cfh_cand_ws_bytes(B, Vs)), dtype=torch.uint8, device=cuda)
+    print(f"[cand edges] B={B} n={n} Vs={Vs} M={M} ld={ld} {kind}", flush=True)
+    _lib.check(L.cfh_cand_topm(dl.data_ptr(), ld, dlse.data_ptr(), B, n, Vs, M, dsl.data_ptr(), local.data_ptr(),
+                               glob.data_ptr(), ws.data_ptr(), _lib.stream_handle()), "cfh_cand_topm")
+    torch.cuda.synchronize()
+    vals = (lg[:, :Vs].astype(np.float32) - lse[:, None]).reshape(B, n, Vs).max(1)
+    for b in range(B):
+        want = np.sort(np.argsort(-vals[b], kind="stable")[:M])
+        assert np.array_equal(local[b].cpu().numpy(), want), b
+        assert np.array_equal(glob[b].cpu().numpy(), sl[want]), b
 
 
 @pytest.mark.gpu

@@ -23,7 +23,7 @@ def pytest_configure(config):
 
 def pytest_collection_modifyitems(config, items):
     # A GPU test on a host without a GPU fails loudly rather than silently skipping: the GPU
-    # tier is only selected (-m gpu) on GPU boxes.
+    # tier is only selected (-m gpu) on machines that have a GPU.
     return None
 
 

@@ -116,10 +116,11 @@ __device__ void select_digit(Each& each, unsigned prefix, unsigned pmask, int sh
 // vectors) in batches of KB loads a thread issues together: one workgroup per request is bound by
 // the loads it keeps in flight.  The compaction works on 256-column segments, one wave each: ballot
 // counts per segment, then segment offsets by two workgroup scans, then each column's output slot
-// from the ballots of the lanes below it.  The shortlist ids are loaded with the keys, ahead of any
-// store (a load issued after a store to memory it may alias waits for a full round trip).
+// from the ballots of the lanes below it.  A wave loads all its segments' keys in one batch (up to
+// 65,536 columns), and the shortlist ids are gathered in a last pass over the M outputs: a load
+// issued after stores waits for them (the wave's memory counter is in order).
 constexpr int KB = 8;         // vectors in flight per thread per batch
-constexpr int SEGB = 4;       // segments in flight per wave
+constexpr int SEGB = 16;      // segments in flight per wave
 constexpr int MAXSEG = 1024;  // 256-column segments: Vs <= 262,144
 
 __global__ void __launch_bounds__(CT) k_cand_select(CandArgs a) {
@@ -185,29 +186,19 @@ __global__ void __launch_bounds__(CT) k_cand_select(CandArgs a) {
   // compaction in column order by 256-column segments (lane l holds columns 4l .. 4l+3)
   const int nseg = (nv + 63) / 64;
   const unsigned long long below = (1ull << lane) - 1ull;
-  const bool gather = a.sl && a.cand_global;
-  auto segments = [&](bool ids, auto&& f) {   // f(segment, first column, keys, ids) on every lane
+  auto segments = [&](auto&& f) {   // f(segment, first column, keys) on every lane of the wave
     for (int s0 = wave; s0 < nseg; s0 += (CT / 64) * SEGB) {
       uint4 kk[SEGB];
-      int4 ii[SEGB];
 #pragma unroll
       for (int u = 0; u < SEGB; ++u) kk[u] = keys[min((s0 + u * (CT / 64)) * 64 + lane, nv - 1)];
-      if (ids) {
-#pragma unroll
-        for (int u = 0; u < SEGB; ++u) {
-          const int j = ((s0 + u * (CT / 64)) * 64 + lane) * 4;
-          ii[u] = make_int4(a.sl[min(j, a.Vs - 1)], a.sl[min(j + 1, a.Vs - 1)], a.sl[min(j + 2, a.Vs - 1)],
-                            a.sl[min(j + 3, a.Vs - 1)]);
-        }
-      }
 #pragma unroll
       for (int u = 0; u < SEGB; ++u) {
         const int sg = s0 + u * (CT / 64);
-        if (sg < nseg) f(sg, (sg * 64 + lane) * 4, kk[u], ii[u]);   // (wave-uniform)
+        if (sg < nseg) f(sg, (sg * 64 + lane) * 4, kk[u]);   // (wave-uniform)
       }
     }
   };
-  segments(false, [&](int sg, int j, uint4 k4, int4) {
+  segments([&](int sg, int j, uint4 k4) {
     const unsigned k[4] = {k4.x, k4.y, k4.z, k4.w};
     int gt = 0, eq = 0;
 #pragma unroll
@@ -241,9 +232,8 @@ __global__ void __launch_bounds__(CT) k_cand_select(CandArgs a) {
   __syncthreads();
   int* cl = a.cand_local + (size_t)b * a.M;
   int* cg = a.cand_global ? a.cand_global + (size_t)b * a.M : nullptr;
-  segments(gather, [&](int sg, int j, uint4 k4, int4 i4) {
+  segments([&](int sg, int j, uint4 k4) {
     const unsigned k[4] = {k4.x, k4.y, k4.z, k4.w};
-    const int id[4] = {i4.x, i4.y, i4.z, i4.w};
     bool eqb[4], take[4];
     int eq_rank = sg_b[sg];
 #pragma unroll
@@ -260,13 +250,16 @@ __global__ void __launch_bounds__(CT) k_cand_select(CandArgs a) {
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      if (take[q]) {
-        cl[pos] = j + q;
-        if (cg) cg[pos] = gather ? id[q] : j + q;
-        ++pos;
-      }
+      if (take[q]) cl[pos++] = j + q;
     }
   });
+  if (cg) {   // global ids of the candidates (the barrier makes the workgroup's stores visible)
+    __syncthreads();
+    for (int i = t; i < a.M; i += CT) {
+      const int c = cl[i];
+      cg[i] = a.sl ? a.sl[c] : c;
+    }
+  }
 }
 
 }  // namespace

@@ -194,8 +194,8 @@ int cfh_head_topk_packed(const void* h, int M, int d, const void* packed, int n,
  * shortlist columns) with their log-sum-exp lse [B*n], value[j] = max_d (logits[d][j] - lse[d]);
  * the M columns of largest value (ties to the lower column), ascending, into cand_local [B][M] and,
  * mapped through the shortlist sl (NULL = identity), cand_global [B][M] (may be NULL).  n = 1
- * selects per row (the per-depth sets).  ws: cfh_cand_ws_bytes(B, Vs) bytes.  Vs <= 262,144
- * (CFH_E_UNSUPPORTED above). */
+ * selects per row (the per-depth sets).  ws: cfh_cand_ws_bytes(B, Vs) bytes, 16-byte aligned
+ * (CFH_E_INVALID otherwise).  Vs <= 262,144 (CFH_E_UNSUPPORTED above). */
 int64_t cfh_cand_ws_bytes(int B, int Vs);
 int cfh_cand_topm(const void* logits, long long ld, const float* lse, int B, int n, int Vs, int M, const int32_t* sl,
                   int32_t* cand_local, int32_t* cand_global, void* ws, void* stream);

@@ -28,3 +28,18 @@ def test_status_strings_without_a_device():
     assert L.cfh_version() >= 100
     assert L.cfh_error_string(0) == b"ok"
     assert L.cfh_error_string(2) == b"unsupported shape"
+
+
+def test_candidate_select_argument_checks_without_a_device():
+    """cfh_cand_topm's host-side checks return before any launch: keys rows padded to 4 columns,
+    a 16-byte aligned workspace, widths up to 262,144 columns."""
+    L = _lib.lib()
+    assert L.cfh_cand_ws_bytes(2, 5) == 2 * 8 * 4
+    assert L.cfh_cand_ws_bytes(3, 62642) == 3 * 62644 * 4
+    p = 4096   # stand-in addresses: never dereferenced, the checks fail first
+    # (logits, ld, lse, B, n, Vs, M, sl, cand_local, cand_global, ws, stream)
+    assert L.cfh_cand_topm(p, 1003, p, 3, 5, 1001, 77, None, p, None, p + 8, None) == 1      # misaligned ws
+    assert L.cfh_cand_topm(p, 1003, p, 3, 5, 1001, 1002, None, p, None, p, None) == 1       # M > Vs
+    assert L.cfh_cand_topm(p, 1000, p, 3, 5, 1001, 77, None, p, None, p, None) == 1         # ld < Vs
+    assert L.cfh_cand_topm(p, 262145, p, 1, 1, 262145, 8, None, p, None, p, None) == 2      # too wide
+    assert L.cfh_cand_topm(p, 1003, p, 0, 5, 1001, 77, None, p, None, p, None) == 0         # nothing to do

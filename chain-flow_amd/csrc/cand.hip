@@ -5,10 +5,12 @@
 //   value[j] = max over the request's n rows d of (logits[d][j] - lse[d])   (fp32)
 // (shared: the best per-depth log-prob; n = 1 gives the per-depth set, the order of the raw logits),
 // the M largest values with ties to the lower column, written in ascending column order.
-// The values become order-preserving 32-bit keys in `ws` (a wide grid); then one 1024-thread
-// workgroup per request runs a most-significant-digit-first radix select (histograms in LDS) that
-// finds the M-th largest key and how many ties at it belong to the M, and a workgroup scan in
-// column order compacts.  No sort and no atomics on global memory; deterministic.
+// The values become order-preserving 32-bit keys in `ws` (a wide grid; rows padded to 4 keys);
+// then one 1024-thread workgroup per request finds the bits every key shares, runs a
+// most-significant-digit-first radix select over the rest (12-bit digits, histograms in LDS) that
+// finds the M-th largest key and how many ties at it belong to the M, and compacts in column order
+// by 256-column segments (ballot counts, workgroup scans of the segment counts, ballot ranks).
+// No sort and no atomics on global memory; deterministic.
 #include <math.h>
 
 #include "cfh_kernels.h"

@@ -55,23 +55,46 @@ struct CandArgs {
   int* cand_global;               // [B][M] or null
   unsigned* keys;                 // ws [B][Vp], Vp = Vs rounded up to 4 (16-byte rows)
   long long ld;
-  int n, Vs, M;
+  int n, Vs, M, B;
 };
 
 __host__ __device__ constexpr int padded_vs(int Vs) { return (Vs + 3) & ~3; }
+// column blocks of k_cand_keys (1024 columns each); after the keys, ws holds each block's AND and
+// OR of its keys: masks [B][key_blocks][2]
+__host__ __device__ constexpr int key_blocks(int Vs) { return (Vs + 1023) / 1024; }
 
-// keys[b][j] for 4 columns a thread, grid (B, column blocks): coalesced and spread over the chip
+// keys[b][j] for 4 columns a thread, grid (B, column blocks): coalesced and spread over the chip;
+// each block also writes the AND and the OR of its keys (order-free, so still deterministic)
 __global__ void __launch_bounds__(256) k_cand_keys(CandArgs a) {
+  __shared__ unsigned red[2][4];
   const int b = blockIdx.x;
+  unsigned kand = ~0u, kor = 0u;
   for (int q = 0; q < 4; ++q) {
     const int j = (blockIdx.y * 4 + q) * 256 + threadIdx.x;
-    if (j >= a.Vs) return;
+    if (j >= a.Vs) break;
     float v = -INFINITY;
     for (int d = 0; d < a.n; ++d) {
       const size_t r = (size_t)b * a.n + d;
       v = fmaxf(v, (float)__builtin_bit_cast(_Float16, a.logits[r * a.ld + j]) - a.lse[r]);
     }
-    a.keys[(size_t)b * padded_vs(a.Vs) + j] = order_key(v);
+    const unsigned k = order_key(v);
+    a.keys[(size_t)b * padded_vs(a.Vs) + j] = k;
+    kand &= k;
+    kor |= k;
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    kand &= (unsigned)__shfl_xor((int)kand, off);
+    kor |= (unsigned)__shfl_xor((int)kor, off);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    red[0][threadIdx.x >> 6] = kand;
+    red[1][threadIdx.x >> 6] = kor;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned* m = a.keys + (size_t)a.B * padded_vs(a.Vs) + ((size_t)b * key_blocks(a.Vs) + blockIdx.y) * 2;
+    m[0] = red[0][0] & red[0][1] & red[0][2] & red[0][3];
+    m[1] = red[1][0] | red[1][1] | red[1][2] | red[1][3];
   }
 }
 
@@ -149,12 +172,14 @@ __global__ void __launch_bounds__(CT) k_cand_select(CandArgs a) {
       }
     }
   };
-  // the keys' common prefix: bits where the AND and the OR of every key agree
+  // the keys' common prefix: bits where the AND and the OR of every key agree (from the key
+  // blocks' masks)
   unsigned kand = ~0u, kor = 0u;
-  each([&](unsigned k) {
-    kand &= k;
-    kor |= k;
-  });
+  const unsigned* masks = a.keys + (size_t)a.B * padded_vs(a.Vs) + (size_t)b * key_blocks(a.Vs) * 2;
+  for (int i = t; i < key_blocks(a.Vs); i += CT) {
+    kand &= masks[2 * i];
+    kor |= masks[2 * i + 1];
+  }
   for (int off = 32; off > 0; off >>= 1) {
     kand &= (unsigned)__shfl_xor((int)kand, off);
     kor |= (unsigned)__shfl_xor((int)kor, off);
@@ -270,7 +295,7 @@ extern "C" {
 
 int64_t cfh_cand_ws_bytes(int B, int Vs) {
   if (B < 0 || Vs < 0) return -1;
-  return (int64_t)B * padded_vs(Vs) * 4;
+  return (int64_t)B * padded_vs(Vs) * 4 + (int64_t)B * key_blocks(Vs) * 8;
 }
 
 int cfh_cand_topm(const void* logits, long long ld, const float* lse, int B, int n, int Vs, int M, const int32_t* sl,
@@ -280,9 +305,9 @@ int cfh_cand_topm(const void* logits, long long ld, const float* lse, int B, int
     return CFH_E_INVALID;
   if ((uintptr_t)ws & 15) return CFH_E_INVALID;
   if (Vs > 256 * MAXSEG) return CFH_E_UNSUPPORTED;
-  CandArgs a = {(const unsigned short*)logits, lse, sl, cand_local, cand_global, (unsigned*)ws, ld, n, Vs, M};
+  CandArgs a = {(const unsigned short*)logits, lse, sl, cand_local, cand_global, (unsigned*)ws, ld, n, Vs, M, B};
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(k_cand_keys, dim3(B, (Vs + 1023) / 1024), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(k_cand_keys, dim3(B, key_blocks(Vs)), dim3(256), 0, st, a);
   CFH_LAUNCH_CHECK();
   hipLaunchKernelGGL(k_cand_select, dim3(B), dim3(CT), 0, st, a);
   CFH_LAUNCH_CHECK();

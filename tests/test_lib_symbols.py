@@ -31,11 +31,12 @@ def test_status_strings_without_a_device():
 
 
 def test_candidate_select_argument_checks_without_a_device():
-    """cfh_cand_topm's host-side checks return before any launch: keys rows padded to 4 columns,
-    a 16-byte aligned workspace, widths up to 262,144 columns."""
+    """cfh_cand_topm's host-side checks return before any launch: keys rows padded to 4 columns
+    plus each 1024-column block's AND/OR masks, a 16-byte aligned workspace, widths up to 262,144
+    columns."""
     L = _lib.lib()
-    assert L.cfh_cand_ws_bytes(2, 5) == 2 * 8 * 4
-    assert L.cfh_cand_ws_bytes(3, 62642) == 3 * 62644 * 4
+    assert L.cfh_cand_ws_bytes(2, 5) == 2 * 8 * 4 + 2 * 1 * 8            # keys + one block's AND/OR
+    assert L.cfh_cand_ws_bytes(3, 62642) == 3 * 62644 * 4 + 3 * 62 * 8
     p = 4096   # stand-in addresses: never dereferenced, the checks fail first
     # (logits, ld, lse, B, n, Vs, M, sl, cand_local, cand_global, ws, stream)
     assert L.cfh_cand_topm(p, 1003, p, 3, 5, 1001, 77, None, p, None, p + 8, None) == 1      # misaligned ws

@@ -104,6 +104,21 @@ def test_shortlist_resolution_order_and_guard(tmp_path):
         fp.resolve_shortlist(str(tmp_path), V, str(tmp_path / "nope.pt"))
 
 
+def test_packaged_shortlist_is_the_last_resort(tmp_path):
+    """Step 4 of the resolution order (``cf/defaults.py:205-244``): with no list beside the checkpoint,
+    the packaged Qwen3.5 list is found for its own vocabulary, and the checkpoint's list still wins."""
+    assert fp.PACKAGED_SHORTLIST.is_file()
+    V = slmod.PACKAGED_VOCAB
+    sl, why = fp.resolve_shortlist(str(tmp_path), V, None)
+    assert sl is not None and sl.numel() == slmod.PACKAGED_ROWS and why == "packaged shortlist_qwen3_5.pt"
+    assert slmod.ids_content_sha(sl) == "42fb98262c247aaf79c860da979b048c96408c885416161c6e83c2a93cc6dbfb"
+    assert [p for _, p in fp.shortlist_candidates(str(tmp_path))] == ["packaged"]
+    slmod.save(tmp_path / "shortlist.pt", [5, 3, 900], vocab_size=V)
+    sl, why = fp.resolve_shortlist(str(tmp_path), V, None)
+    assert sl.tolist() == [3, 5, 900] and why.startswith("drafter checkpoint")
+    assert [p for _, p in fp.shortlist_candidates(str(tmp_path))] == ["drafter checkpoint", "packaged"]
+
+
 def test_declared_identity_mismatch_raises(tmp_path):
     V = 1000
     slmod.save(tmp_path / "shortlist.pt", [1, 2, 3], vocab_size=V)

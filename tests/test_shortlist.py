@@ -1,7 +1,8 @@
 """The shortlist file format and the vocabulary guard (host logic, no GPU).
 
 Mirrors the reference's own tests of ``cf/shortlist.py`` (tests/test_shortlist.py:28-87) on the
-reference's packaged shortlist, kept here as a data fixture (tests/golden/shortlist_qwen3_5.pt).
+reference's packaged shortlist, which ships inside the package (chain_flow_amd/data/shortlist_qwen3_5.pt)
+as the proposer's last-resort list.
 """
 from __future__ import annotations
 
@@ -12,7 +13,7 @@ import torch
 
 from chain_flow_amd import shortlist
 
-FIXTURE = Path(__file__).parent / "golden" / "shortlist_qwen3_5.pt"
+FIXTURE = Path(__file__).resolve().parents[1] / "chain-flow_amd" / "chain_flow_amd" / "data" / "shortlist_qwen3_5.pt"
 # content identity recorded for the reference's packaged list (sorted int32 ids)
 PACKAGED_SHA = "42fb98262c247aaf79c860da979b048c96408c885416161c6e83c2a93cc6dbfb"
 

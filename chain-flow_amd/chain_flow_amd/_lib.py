@@ -39,6 +39,7 @@ SIGNATURES = {
     "cfh_flow_expert_bytes": (_I64, [C.POINTER(FlowDims)]),
     "cfh_flow_pack_expert": (_I, [C.POINTER(FlowDims), C.POINTER(_VP), _I, _VP, _VP]),
     "cfh_flow_integrate": (_I, [C.POINTER(FlowDims), C.POINTER(_VP), _VP, _VP, _VP, _I, _VP]),
+    "cfh_flow_integrate_noalloc": (_I, [C.POINTER(FlowDims), C.POINTER(_VP), _VP, _VP, _I, _VP]),
     "cfh_vae_bytes": (_I64, [C.POINTER(VaeDims)]),
     "cfh_vae_pack": (_I, [C.POINTER(VaeDims), C.POINTER(_VP), _I, _VP, _VP]),
     "cfh_vae_caps": (_I, [C.POINTER(VaeDims), _I, C.POINTER(_I64)]),

@@ -33,6 +33,7 @@
 #include <stdio.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "cfh_stream.h"
 
@@ -399,29 +400,10 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w, const voi
   return launch_res(r, st);
 }
 
-}  // namespace
-
-extern "C" {
-
-int cfh_caps(const cfh_flow_dims* dims, int batch, int64_t* ws_bytes) {
-  if (!cfh::flow_dims_ok(dims) || batch < 1) return CFH_E_UNSUPPORTED;
-  if (dims->d > ROWT * ROWE || dims->draft_length > MAXR) return CFH_E_UNSUPPORTED;
-  const Plan p = make_plan(dims);
-  if (!p.ok) return CFH_E_UNSUPPORTED;
-  const WS w = carve(p, nullptr);
-  if (ws_bytes) *ws_bytes = (int64_t)w.total;
-  return CFH_OK;
-}
-
-int cfh_flow_integrate(const cfh_flow_dims* dm, const void* const* experts, const void* ctx, void* z_out,
-                       void* ws_ptr, int batch, void* stream) {
-  if (!cfh::flow_dims_ok(dm) || dm->d > ROWT * ROWE || dm->draft_length > MAXR) return CFH_E_UNSUPPORTED;
-  if (!experts || !ctx || !z_out || !ws_ptr || batch < 1) return CFH_E_INVALID;
-  const Plan p = make_plan(dm);
-  if (!p.ok) return CFH_E_UNSUPPORTED;
-  for (int c = 0; c < p.nch; ++c)
-    if (!experts[c]) return CFH_E_INVALID;
-  hipStream_t st = (hipStream_t)stream;
+// The whole draft of `batch` requests on workspace ws (the plan's carve() layout): per request the
+// per-draft launches, then E Euler steps of L block passes and the OUT / ROWS step.
+int integrate(const Plan& p, const cfh_flow_dims* dm, const void* const* experts, const void* ctx, void* z_out,
+              void* ws_ptr, int batch, hipStream_t st) {
   const cfh::ExpertLayout L = cfh::expert_layout(dm);
   const WS w = carve(p, (char*)ws_ptr);
   const int d = p.d, CS = p.CS, E = p.E, NL = p.NL, C = p.C, KD = p.KD, nch = p.nch;
@@ -526,6 +508,71 @@ int cfh_flow_integrate(const cfh_flow_dims* dm, const void* const* experts, cons
     }
   }
   return CFH_OK;
+}
+
+// The no-allocation entry point's workspace: one array per device, resolved to its device address
+// on the first call on each device (the array's name in host code is a host-side stand-in, never a
+// device address).  Its contents persist between calls; the flow writes every workspace element
+// before it reads it, so nothing needs clearing.
+__device__ __align__(256) unsigned char scratch[CFH_NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[MAX_DEVICES];
+
+int scratch_address(void** out) {
+  int dev = 0;
+  CFH_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= MAX_DEVICES) return CFH_E_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    CFH_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    if (!ptr) return CFH_E_HIP;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return CFH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cfh_caps(const cfh_flow_dims* dims, int batch, int64_t* ws_bytes) {
+  if (!cfh::flow_dims_ok(dims) || batch < 1) return CFH_E_UNSUPPORTED;
+  if (dims->d > ROWT * ROWE || dims->draft_length > MAXR) return CFH_E_UNSUPPORTED;
+  const Plan p = make_plan(dims);
+  if (!p.ok) return CFH_E_UNSUPPORTED;
+  const WS w = carve(p, nullptr);
+  if (ws_bytes) *ws_bytes = (int64_t)w.total;
+  return CFH_OK;
+}
+
+int cfh_flow_integrate(const cfh_flow_dims* dm, const void* const* experts, const void* ctx, void* z_out,
+                       void* ws_ptr, int batch, void* stream) {
+  if (!cfh::flow_dims_ok(dm) || dm->d > ROWT * ROWE || dm->draft_length > MAXR) return CFH_E_UNSUPPORTED;
+  if (!experts || !ctx || !z_out || !ws_ptr || batch < 1) return CFH_E_INVALID;
+  const Plan p = make_plan(dm);
+  if (!p.ok) return CFH_E_UNSUPPORTED;
+  for (int c = 0; c < p.nch; ++c)
+    if (!experts[c]) return CFH_E_INVALID;
+  return integrate(p, dm, experts, ctx, z_out, ws_ptr, batch, (hipStream_t)stream);
+}
+
+int cfh_flow_integrate_noalloc(const cfh_flow_dims* dm, const void* const* experts, const void* ctx, void* z_out,
+                               int batch, void* stream) {
+  if (!cfh::flow_dims_ok(dm) || dm->d > ROWT * ROWE || dm->draft_length > MAXR) return CFH_E_UNSUPPORTED;
+  if (!experts || !ctx || !z_out || batch < 1) return CFH_E_INVALID;
+  const Plan p = make_plan(dm);
+  if (!p.ok) return CFH_E_UNSUPPORTED;
+  for (int c = 0; c < p.nch; ++c)
+    if (!experts[c]) return CFH_E_INVALID;
+  if (carve(p, nullptr).total > (size_t)CFH_NOALLOC_SCRATCH_BYTES) return CFH_E_SCRATCH;
+  void* ws = nullptr;
+  int rc = scratch_address(&ws);
+  if (rc) return rc;
+  return integrate(p, dm, experts, ctx, z_out, ws, batch, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -118,6 +118,7 @@ const char* cfh_error_string(int status) {
     case CFH_E_INVALID: return "invalid argument";
     case CFH_E_UNSUPPORTED: return "unsupported shape";
     case CFH_E_HIP: return "HIP runtime error";
+    case CFH_E_SCRATCH: return "workspace exceeds the no-allocation scratch (CFH_NOALLOC_SCRATCH_BYTES)";
     default: return "unknown status";
   }
 }

@@ -25,6 +25,11 @@ extern "C" {
 #define CFH_E_INVALID 1          /* bad argument (null pointer, size out of range)        */
 #define CFH_E_UNSUPPORTED 2      /* shape this build does not support                     */
 #define CFH_E_HIP 3              /* a HIP runtime call failed (cfh_last_hip_error)        */
+#define CFH_E_SCRATCH 4          /* the no-allocation entry point's workspace is too small */
+
+/* Size of the library's per-device scratch array behind cfh_flow_integrate_noalloc (32 MiB:
+ * the flow workspace of d <= 5120 at 8 layers needs 18.7 MB). */
+#define CFH_NOALLOC_SCRATCH_BYTES (32ll << 20)
 
 /* Library version (major*10000 + minor*100 + patch). */
 int cfh_version(void);
@@ -85,6 +90,16 @@ int cfh_flow_pack_expert(const cfh_flow_dims* dims, const void* const* raw, int 
  * (cf/cuda_block.py:407-431 / pybind `expert`, `cross_kv`, cf/csrc/fused_block.cu:793-862). */
 int cfh_flow_integrate(const cfh_flow_dims* dims, const void* const* experts, const void* ctx,
                        void* z_out, void* ws, int batch, void* stream);
+
+/* cfh_flow_integrate without a caller workspace, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  It has no
+ * counterpart in the reference.  The workspace is the library's file-scope device array of
+ * CFH_NOALLOC_SCRATCH_BYTES, one per device, resolved on the first call on each device; nothing
+ * is allocated or freed.  Shapes whose workspace (cfh_caps) exceeds it return CFH_E_SCRATCH.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (two streams, two
+ * host threads) race and must be serialised by the caller.  Same results as cfh_flow_integrate. */
+int cfh_flow_integrate_noalloc(const cfh_flow_dims* dims, const void* const* experts, const void* ctx,
+                               void* z_out, int batch, void* stream);
 
 /* ---------------------------------------------------------------- hidden-state VAE
  * TransformerHiddenVAE (cf/vae/transformer_hidden.py:9-79; config cf/vae/base.py:9-17): the frozen

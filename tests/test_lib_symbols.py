@@ -44,3 +44,22 @@ def test_candidate_select_argument_checks_without_a_device():
     assert L.cfh_cand_topm(p, 1000, p, 3, 5, 1001, 77, None, p, None, p, None) == 1         # ld < Vs
     assert L.cfh_cand_topm(p, 262145, p, 1, 1, 262145, 8, None, p, None, p, None) == 2      # too wide
     assert L.cfh_cand_topm(p, 1003, p, 0, 5, 1001, 77, None, p, None, p, None) == 0         # nothing to do
+
+
+def test_noalloc_flow_rejects_a_workspace_beyond_the_scratch_without_a_device():
+    """cfh_flow_integrate_noalloc refuses, before any HIP call, a shape whose flow workspace exceeds
+    the 32 MiB scratch array (d = 8192 at 8 layers needs 46.7 MB), with its own status."""
+    import ctypes as C
+
+    from chain_flow_amd.config import flownet
+    from chain_flow_amd.flow import caps, flow_dims
+    L = _lib.lib()
+    assert L.cfh_error_string(4).startswith(b"workspace exceeds the no-allocation scratch")
+    cfg = flownet(8192, layers=8, flow_steps=8)
+    assert caps(cfg) > 32 << 20
+    assert caps(flownet(5120, layers=8, flow_steps=8)) <= 32 << 20
+    dims = flow_dims(cfg)
+    p = 4096   # stand-in addresses: never dereferenced, the size check fails first
+    experts = _lib.ptr_array([p, p])
+    assert L.cfh_flow_integrate_noalloc(C.byref(dims), experts, p, p, 1, None) == 4
+    assert L.cfh_flow_integrate_noalloc(C.byref(dims), experts, p, p, 0, None) == 1    # batch < 1

@@ -33,8 +33,11 @@ in-place gather `cfh_head_gemm_topk` is reported beside it); ``roofline`` is HBM
 rows) and the line also states the MFMA rate against the 2.5 PFLOP/s bf16 dense peak.
 
 Prints one JSON line.  ``roofline`` covers the flow pass (the dominant part, ~96% of the bytes),
-timed with HIP events on the stream it runs on; ``cpu_baseline`` is the CPU oracle timed on a
-bounded sample of the same workload on this host and scaled to one draft step (rank 0, N=1 only).
+timed with HIP events on the stream it runs on.  ``cpu_baseline`` is the CPU reference plumbing run
+measured whole on this host (rank 0, N=1 only): chain drafts at d=2560 in fp32 (L=8, E=8, the
+width-4 beam over the 62,642-row restriction of a 248,320-row fp32 head) by the numpy oracle in
+float32, 1 warm-up and the median of 3; ``cpu_baseline_d5120_extrapolated`` scales a bounded
+float32 sample of the metric's own d=5120 workload to one draft.
 """
 from __future__ import annotations
 
@@ -223,38 +226,128 @@ def cpu_baseline_latent(W, cfg, sl, d, ctx):
                        f"d={d} ({t_head * 1e3:.0f} ms) scaled by K={K}")}
 
 
+def host_threads():
+    """The CPUs this process may run on (its affinity set), capped by OMP_NUM_THREADS when set: the
+    host's share that the CPU baseline's BLAS threads use."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(n, 1)
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline_c1(dev, reps=3):
+    """The CPU reference plumbing run (C1), measured whole: a chain draft at d = 2560 in fp32 on the
+    host -- TreeFlowDrafter.predict_hidden (L = 8 blocks, E = 8 Euler steps, 2 chunk experts,
+    seeded N(0, 0.02) weights, N(0, 1) RMS-1 context) and the 5-token width-4 beam over a
+    248,320 x 2560 fp32 head restricted to the seeded 62,642-id shortlist (path residual, markov
+    bias, log-softmax top-k), plus the greedy (width-1) chain, timed apart.  The numpy oracle in
+    float32 arithmetic with BLAS on this process's CPU share; 1 warm-up, median of ``reps``.  The
+    weights are drawn on the GPU with the same per-parameter seeds and copied to the host (setup,
+    not timed)."""
+    import numpy as np
+    import torch
+    from threadpoolctl import threadpool_limits
+    from chain_flow_amd.config import flownet
+    from chain_flow_amd.shortlist import synthetic
+    from chain_flow_amd.weights import make_weights, synthetic_context
+    from oracle import beam as obeam
+    from oracle import flow as oflow
+    from oracle import head as ohead
+    d, K, Wd = 2560, 5, 4
+    cfg = flownet(d, layers=8, flow_steps=8)
+    W = make_weights(cfg, VOCAB, init="baseline", dtype=torch.float32, device=dev, base_seed=0)
+    sl = synthetic(VOCAB, SHORTLIST_ROWS, seed=2)
+    sld = sl.long().to(dev)
+    host = lambda t: t.detach().cpu().numpy()
+    Wf = {k: host(v) for k, v in W.items() if k.startswith(("expert.", "extra_experts.", "path_head."))}
+    w_sl = host(W["lm_head.weight"][sld])            # lm_w[sl], built once (flow_proposer.py:739)
+    w2_sl = host(W["markov.w2.weight"][sld])
+    w1 = host(W["markov.w1.weight"])
+    emb = host(W["embed_tokens.weight"])
+    del W, sld
+    torch.cuda.empty_cache()
+    ctx = synthetic_context(1, cfg.context_size, d, seed=1, dtype=torch.float32).numpy()
+    known0 = np.array([int(sl[1234])])
+    s64 = sl.long().numpy()
+    ocfg = dict(draft_length=cfg.draft_length, chunk_size=cfg.chunk_size, num_layers=cfg.num_drafter_layers,
+                num_heads=cfg.num_heads, num_flow_steps=cfg.num_flow_steps, init_mode=cfg.init_mode)
+    score = lambda h, prev: ohead.head_with_bias(h, w_sl, w1, w2_sl, prev, numerics="fp32")
+    resid = lambda lp, nl: ohead.path_residual(Wf, emb, lp, nl, cfg.path_order, numerics="fp32")
+
+    def chain(pred, width):
+        return obeam.beam_chains(pred, known0, s64, width, K, cfg.path_order, score, resid, numerics="fp32")
+
+    n = host_threads()
+    with threadpool_limits(limits=n):
+        pred = oflow.predict_hidden(Wf, ctx, ocfg, numerics="fp32")       # warm-up
+        chain(pred, Wd)
+        ts, tg = [], []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            pred = oflow.predict_hidden(Wf, ctx, ocfg, numerics="fp32")
+            ids = chain(pred, Wd)
+            t1 = time.perf_counter()
+            greedy = chain(pred, 1)
+            ts.append(t1 - t0)
+            tg.append(time.perf_counter() - t1)
+    assert pred.dtype == np.float32
+    med = lambda v: sorted(v)[len(v) // 2]
+    return {"value": round(med(ts) * 1e6, 1), "unit": "us per draft step", "cores": n, "kind": "port",
+            "sample": (f"whole C1 drafts: numpy oracle in float32 at d={d}, L=8, E=8 (predict_hidden) + the "
+                       f"{K}-token width-{Wd} beam over the {SHORTLIST_ROWS}-row restriction of a {VOCAB}x{d} "
+                       f"fp32 head; median of {reps} after 1 warm-up; {n} BLAS threads on a "
+                       f"{cpu_model()} host (os.cpu_count() {os.cpu_count()})"),
+            "runs_s": [round(t, 3) for t in ts],
+            "greedy_chain_us": round(med(tg) * 1e6, 1),
+            "chain_ids": [int(x) for x in ids[0]], "greedy_ids": [int(x) for x in greedy[0]]}
+
+
 def cpu_baseline(W, cfg, sl, d):
-    """The CPU oracle on a bounded sample of the same workload, scaled to one draft step.
+    """The CPU oracle on a bounded sample of the metric's own workload (d = 5120), scaled to one
+    draft step: an extrapolation, reported beside the whole C1 run.
 
     Sample: one HiddenKVFlowBlock pass of each chunk expert (S = 4 and 8 rows), the cross K/V of
     one block of each expert, and one head depth (4 beams: fused path residual with 4 live offsets,
-    62,642-row shortlist GEMV + markov bias, log-softmax).  One draft = E*L block passes of each
-    expert + L cross K/V per expert + K head depths."""
+    62,642-row shortlist GEMV + markov bias, log-softmax), in float32.  One draft = E*L block passes
+    of each expert + L cross K/V per expert + K head depths."""
     import numpy as np
-    import torch
+    from threadpoolctl import threadpool_limits
     from oracle import flow as oflow
     from oracle import head as ohead
-    try:
-        from threadpoolctl import threadpool_info
-        cores = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:
-        cores = os.cpu_count() or 1
-    f64 = lambda t: t.detach().float().cpu().double().numpy()
+    cores = host_threads()
+    f64 = lambda t: t.detach().float().cpu().numpy()
     rng = np.random.default_rng(0)
+    lim = threadpool_limits(limits=cores)
     t_blocks = 0.0
     t_kv = 0.0
     for ci, p in enumerate(oflow.expert_prefixes(cfg.num_chunks)):
         bp = f"{p}blocks.0."
         Wb = {k: f64(v) for k, v in W.items() if k.startswith(bp)}
         S = (ci + 1) * cfg.chunk_size
-        ctx = rng.standard_normal((1, cfg.context_size, d))
+        ctx = rng.standard_normal((1, cfg.context_size, d)).astype(np.float32)
         t0 = time.perf_counter()
-        kv = oflow.cross_kv(Wb, bp, ctx, "fp16")
+        kv = oflow.cross_kv(Wb, bp, ctx, "fp32")
         t_kv += time.perf_counter() - t0
-        res = rng.standard_normal((1, S, d))
+        res = rng.standard_normal((1, S, d)).astype(np.float32)
         mask = oflow.causal_mask(S)
         t0 = time.perf_counter()
-        oflow.block_forward(Wb, bp, res, kv, mask, cfg.num_heads, "fp16")
+        oflow.block_forward(Wb, bp, res, kv, mask, cfg.num_heads, "fp32")
         t_blocks += time.perf_counter() - t0
         del Wb
     slt = sl.long().cpu()
@@ -264,18 +357,19 @@ def cpu_baseline(W, cfg, sl, d):
     w_sl = f64(W["lm_head.weight"][slt.to(W["lm_head.weight"].device)])
     w1 = f64(W["markov.w1.weight"][slt[:4096].to(W["markov.w1.weight"].device)])
     w2_sl = f64(W["markov.w2.weight"][slt.to(W["markov.w2.weight"].device)])
-    pred = rng.standard_normal((d,))
+    pred = rng.standard_normal((d,)).astype(np.float32)
     t0 = time.perf_counter()
-    res = ohead.path_residual(Wh, emb, lastp, 4, cfg.path_order, "fp16")
-    h = ohead.r16(pred[None] + res, "fp16")
+    res = ohead.path_residual(Wh, emb, lastp, 4, cfg.path_order, "fp32")
+    h = ohead.r16(pred[None] + res, "fp32")
     logits = ohead.head_with_bias(h, w_sl, w1, w2_sl, lastp[:, 0])
     lp = ohead.log_softmax(logits)
     ohead.topk(lp, 4)
     t_head = time.perf_counter() - t0
+    lim.unregister()
     E, L, K = cfg.num_flow_steps, cfg.num_drafter_layers, 5
     us = (E * L * t_blocks + L * t_kv + K * t_head) * 1e6
     return {"value": us, "unit": "us per draft step", "cores": int(cores), "kind": "port",
-            "sample": (f"numpy oracle (float64 math, fp16 rounding points) at d={d}: one block pass of "
+            "sample": (f"extrapolated: numpy oracle in float32 at d={d}: one block pass of "
                        f"each chunk expert ({t_blocks * 1e3:.0f} ms), one block's cross K/V per expert "
                        f"({t_kv * 1e3:.0f} ms), one 4-beam head depth over {SHORTLIST_ROWS} rows "
                        f"({t_head * 1e3:.0f} ms); scaled by E*L={E * L}, L={L}, K={K}")}
@@ -562,8 +656,13 @@ def main():
         calib_copy(dev)
     if not args.no_cpu:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
-        out["cpu_baseline"] = (cpu_baseline_latent(W, cfg, dr.head.sl, d, ctx) if latent
-                               else cpu_baseline(W, cfg, dr.head.sl, d))
+        if latent:
+            out["cpu_baseline"] = cpu_baseline_latent(W, cfg, dr.head.sl, d, ctx)
+        else:
+            out[f"cpu_baseline_d{d}_extrapolated"] = cpu_baseline(W, cfg, dr.head.sl, d)
+            del W, dr
+            torch.cuda.empty_cache()
+            out["cpu_baseline"] = cpu_baseline_c1(dev)
     print(json.dumps(out), flush=True)
 
 

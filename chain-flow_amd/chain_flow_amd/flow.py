@@ -8,6 +8,7 @@ and every Euler step of every chunk expert -- on the current stream.
 from __future__ import annotations
 
 import ctypes as C
+import os
 
 import torch
 
@@ -16,9 +17,31 @@ from chain_flow_amd.config import TreeFlowConfig
 from chain_flow_amd.weights import expert_param_names, expert_prefixes
 
 
-def flow_dims(cfg: TreeFlowConfig) -> _lib.FlowDims:
+# the shapes the reference's fused block kernel is built for (cf/cuda_block.py:46-51)
+_FUSED_D, _FUSED_FM, _FUSED_HEADS, _FUSED_S, _FUSED_MAX_C = (640, 1024), (6,), 8, (4, 8), 16
+
+
+def reference_numerics(cfg: TreeFlowConfig, batch: int = 1) -> int:
+    """The fp16 numerics the reference runs this flow in: its fused block kernel
+    (``_lib.FLOW_FUSED``) when ``cuda_block.supported`` takes every chunk expert's shape and the
+    batch is 1 or ``CF_CUDA_BLOCK_BATCH`` is set (``cf/cuda_block.py:95-117, 474-481``,
+    ``cf/drafters/chunked_flow.py:295-331``), else torch's fp16 modules (``_lib.FLOW_MODULES``), as
+    also with ``CF_CUDA_BLOCK=0``."""
+    off = ("0", "", "false", "False")
+    if os.environ.get("CF_CUDA_BLOCK", "1") in off:                  # the reference's kill switch
+        return _lib.FLOW_MODULES
+    batch_ok = batch == 1 or os.environ.get("CF_CUDA_BLOCK_BATCH", "0") not in off
+    rows = [(c + 1) * cfg.chunk_size for c in range(cfg.draft_length // cfg.chunk_size)]
+    fused = (cfg.flow_dim in _FUSED_D and cfg.ffn_multiplier in _FUSED_FM and cfg.num_heads == _FUSED_HEADS
+             and all(s in _FUSED_S for s in rows) and 0 < cfg.context_size <= _FUSED_MAX_C and batch_ok)
+    return _lib.FLOW_FUSED if fused else _lib.FLOW_MODULES
+
+
+def flow_dims(cfg: TreeFlowConfig, numerics: int | None = None) -> _lib.FlowDims:
+    """cfh_flow_dims of ``cfg``; ``numerics`` defaults to the reference's at batch 1."""
+    num = reference_numerics(cfg) if numerics is None else int(numerics)
     return _lib.FlowDims(cfg.flow_dim, cfg.ffn_multiplier, cfg.num_heads, cfg.num_drafter_layers,
-                         cfg.context_size, cfg.draft_length, cfg.chunk_size, cfg.num_flow_steps)
+                         cfg.context_size, cfg.draft_length, cfg.chunk_size, cfg.num_flow_steps, num)
 
 
 def caps(cfg: TreeFlowConfig, batch: int = 1):
@@ -63,9 +86,11 @@ class FusedFlow:
     def weight_bytes(self) -> int:
         return sum(b.numel() for b in self.packed)
 
-    def predict_hidden(self, ctx: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    def predict_hidden(self, ctx: torch.Tensor, out: torch.Tensor | None = None,
+                       numerics: int | None = None) -> torch.Tensor:
         """ctx [B, context_size, d] fp16 (already front-padded; d = cfg.flow_dim) -> [B, draft_length, d]
-        fp16."""
+        fp16, in the numerics the reference uses for this shape and batch (``reference_numerics``)
+        unless ``numerics`` names one."""
         cfg = self.cfg
         d = cfg.flow_dim
         if ctx.dim() != 3 or ctx.shape[1] != cfg.context_size or ctx.shape[2] != d:
@@ -76,6 +101,7 @@ class FusedFlow:
         B = ctx.shape[0]
         if out is None:
             out = torch.empty(B, cfg.draft_length, d, dtype=torch.float16, device=self.device)
+        self.dims.numerics = reference_numerics(cfg, B) if numerics is None else int(numerics)
         _lib.check(_lib.lib().cfh_flow_integrate(C.byref(self.dims), self._experts, ctx.data_ptr(),
                                                  out.data_ptr(), self.ws.data_ptr(), B,
                                                  _lib.stream_handle()),

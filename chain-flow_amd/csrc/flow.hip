@@ -6,6 +6,10 @@
 // numerics cf/csrc/fused_block.cu:280-325, 452-668, 674-722 (fp32 residual, fp16-parked LayerNorm
 // rows, fp16 q/k/v, attention and GELU outputs, cross K/V hoisted once per draft).
 //
+// Numerics: the fused kernel's (fp32 residual x += sublayer; GELU of the fp32 pre-activation) or
+// torch's fp16 modules' (x = fp16(x + fp16(sublayer)); GELU of the fp16-rounded up-projection), as
+// cfh_flow_dims.numerics says; only the residual row kernel and the W1 epilogue differ.
+//
 // Execution plan.  One launch sequence per draft on the caller's stream; every launch covers both
 // chunk experts (they are independent within an Euler step), so each weight-streaming launch moves
 // the weights of two experts.  Work that needs a whole row sits in a small row kernel between two
@@ -185,6 +189,7 @@ struct Plan {
   int ks_qc, ks_w2, ks_out, ks_kv, ks_tau;
   int wpb_qc, wpb_w2, wpb_out, tpw_att, wpb_att, wpb_full, wpb_w1;
   int pks;            // partial slots per expert
+  int res_mode;       // RES_ADD32 (fused-kernel numerics) or RES_ADD16 (torch fp16 modules)
   bool ok;
 };
 
@@ -195,6 +200,7 @@ Plan make_plan(const cfh_flow_dims* dm) {
   p.ks_att = cfh::heads_per_chunk(p.hd, p.H) ? p.H / cfh::heads_per_chunk(p.hd, p.H) : 0;
   p.nch = p.KD / p.CS;
   p.Smax = p.KD;
+  p.res_mode = dm->numerics == CFH_FLOW_MODULES ? RES_ADD16 : RES_ADD32;
   const int tiles_d = p.d / 16;
   const size_t cap = 96 * 1024;
   // (one k-chunk when K has fewer than 8 k-steps: small latent widths)
@@ -324,7 +330,7 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w, const voi
     if ((rc = launch_stream<S_SELF, E_PART>(a, p.Smax, st))) return rc;
   }
   ResArgs r = {};
-  r.nex = nch; r.d = d;
+  r.nex = nch; r.d = d; r.mode = p.res_mode;
   for (int c = 0; c < nch; ++c) { r.x[c] = w.x[c]; r.P[c] = w.P[c]; r.a[c] = w.abuf[c]; r.rows[c] = S_of(c); }
   // residual + LN_cross
   r.ks = p.ks_att;
@@ -367,6 +373,7 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w, const voi
   {
     SArgs a = {};
     a.nex = nch; a.N = fd; a.K = d; a.ks = 1; a.wpb = p.wpb_w1; a.tpw = 1; a.d = d; a.hd = p.hd;
+    a.gelu_r16 = p.res_mode == RES_ADD16;   // torch's Linear rounds before its GELU module
     a.wg_per_kc = (fd / 16) / (a.wpb * a.tpw);
     for (int c = 0; c < nch; ++c) {
       SEx& x = a.ex[c];

@@ -33,6 +33,7 @@ bool flow_dims_ok(const cfh_flow_dims* d) {
   if (d->draft_length % d->chunk_size != 0) return false;
   if (d->draft_length / d->chunk_size > 4) return false;
   if (d->flow_steps < 1 || d->flow_steps > 16) return false;
+  if (d->numerics != CFH_FLOW_FUSED && d->numerics != CFH_FLOW_MODULES) return false;
   return true;
 }
 

@@ -59,7 +59,20 @@ typedef struct cfh_flow_dims {
   int draft_length;  /* draft_length (8); <= 16                                            */
   int chunk_size;    /* chunk_size (4); draft_length % chunk_size == 0                     */
   int flow_steps;    /* num_flow_steps E (Euler steps); 1 <= E <= 16                       */
+  int numerics;      /* CFH_FLOW_FUSED or CFH_FLOW_MODULES: the rounding points to follow      */
 } cfh_flow_dims;
+
+/* The two fp16 numerics the reference runs its flow blocks in (both with fp32 accumulation, fp16
+ * q/k/v, attention and LayerNorm outputs):
+ *   CFH_FLOW_FUSED   its fused block kernel (cf/csrc/fused_block.cu:280-325, 452-668), engaged
+ *                    for D in {640, 1024}, ffn x6, 8 heads, chunk rows in {4, 8}, <= 16 context
+ *                    rows, batch 1 (cf/cuda_block.py:95-102, cf/drafters/chunked_flow.py:
+ *                    295-331): fp32 residual stream, GELU of the fp32 pre-activation;
+ *   CFH_FLOW_MODULES torch's fp16 modules, every other shape (cf/drafters/chunked_flow.py:185-202):
+ *                    fp16 residual stream x = fp16(x + fp16(sublayer)), GELU of the
+ *                    fp16-rounded up-projection. */
+#define CFH_FLOW_FUSED 0
+#define CFH_FLOW_MODULES 1
 
 /* Capability/shape gate: 0 (CFH_OK) if this build runs `dims` at `batch`, with the workspace
  * size in *ws_bytes; CFH_E_UNSUPPORTED otherwise.  Replaces cuda_block.supported()/max_grid()

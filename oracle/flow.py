@@ -15,11 +15,25 @@ Follows, in the reference (``cf/`` = ``src/chain_flow/``):
   fp16-parked LayerNorm rows, fp16 q/k/v, attention output and GELU output; cross K/V from
   ``context_norm(ctx)`` computed once per draft.
 
+Numerics (``numerics=``):
+
+* ``"fp16"`` -- the reference's fused block kernel, which it engages only for D in {640, 1024},
+  ffn x6, 8 heads, chunk rows in {4, 8}, at most 16 context rows and batch 1
+  (``cf/cuda_block.py:95-102``, ``cf/drafters/chunked_flow.py:295-331``): fp32 residual stream,
+  GELU of the unrounded pre-activation.
+* ``"fp16_modules"`` -- torch's fp16 modules, what the reference runs for every other shape
+  (``cf/drafters/chunked_flow.py:185-202`` with ``.half()`` weights): the residual stream is fp16,
+  every sublayer output (out_proj, FFN down-projection) is rounded to fp16 before the add and the
+  sum rounded again, and the FFN up-projection is rounded to fp16 before the GELU.
+* ``"fp32"`` -- no rounding (the fp32 CPU plumbing).
+
 Weights come in as a dict keyed by the reference's ``state_dict`` names
 (``expert.blocks.{l}.self_attn.in_proj_weight`` ...), values float arrays already holding the exact
 values the device path uses (fp16-representable for the fp16 path).
 """
 from __future__ import annotations
+
+import math
 
 import numpy as np
 from scipy.special import erf
@@ -27,11 +41,18 @@ from scipy.special import erf
 LN_EPS = 1e-5
 
 
+FP16_MODES = ("fp16", "fp16_modules")
+
+
 def r16(x, numerics):
-    """Round to fp16 when the fp16 path materialises this tensor; identity for fp32 numerics."""
-    if numerics == "fp16":
-        return np.asarray(x, dtype=np.float64).astype(np.float16).astype(np.float64)
-    return np.asarray(x, dtype=np.float64)
+    """Round to fp16 when the fp16 path materialises this tensor; identity for fp32 numerics.
+    The arithmetic type is kept: float32 arrays stay float32 (the fp32 CPU timing runs), anything
+    else becomes float64."""
+    x = np.asarray(x)
+    ft = np.float32 if x.dtype == np.float32 else np.float64
+    if numerics in FP16_MODES:
+        return x.astype(np.float16).astype(ft)
+    return x.astype(ft, copy=False)
 
 
 def layer_norm(x, w, b, numerics, eps=LN_EPS):
@@ -46,7 +67,7 @@ def layer_norm(x, w, b, numerics, eps=LN_EPS):
 
 def gelu(x):
     """``nn.GELU()`` default (approximate='none'): 0.5 x (1 + erf(x / sqrt 2))."""
-    return 0.5 * x * (1.0 + erf(x / np.sqrt(2.0)))
+    return 0.5 * x * (1.0 + erf(x * (1.0 / math.sqrt(2.0))))
 
 
 def silu(x):
@@ -64,9 +85,9 @@ def attention(q, k, v, heads, mask=None):
     qh = q.reshape(B, Sq, heads, hd).transpose(0, 2, 1, 3)
     kh = k.reshape(B, Sk, heads, hd).transpose(0, 2, 1, 3)
     vh = v.reshape(B, Sk, heads, hd).transpose(0, 2, 1, 3)
-    s = qh @ kh.transpose(0, 1, 3, 2) / np.sqrt(hd)
+    s = qh @ kh.transpose(0, 1, 3, 2) * (1.0 / math.sqrt(hd))
     if mask is not None:
-        s = s + mask
+        s = s + mask.astype(s.dtype)
     s = s - s.max(-1, keepdims=True)
     p = np.exp(s)
     p = p / p.sum(-1, keepdims=True)
@@ -103,7 +124,7 @@ def init_latents(context, draft_length, numerics, mode="delta"):
         delta = r16(context[:, -1:, :] - context[:, -2:-1, :], numerics)
     else:
         delta = np.zeros_like(last)
-    steps = np.arange(1, draft_length + 1, dtype=np.float64).reshape(1, draft_length, 1)
+    steps = np.arange(1, draft_length + 1, dtype=last.dtype).reshape(1, draft_length, 1)
     return r16(last + r16(steps * delta, numerics), numerics)
 
 
@@ -134,26 +155,41 @@ def cross_kv(W, bp, ctx, numerics):
 
 
 def block_forward(W, bp, res, kv, mask, heads, numerics):
-    """One ``HiddenKVFlowBlock`` on the fp32 residual ``res`` [B, S, d]
+    """One ``HiddenKVFlowBlock`` on the residual ``res`` [B, S, d]
     (``cf/drafters/chunked_flow.py:185-202``; stage structure of ``cf/csrc/fused_block.cu:528-662``)."""
     d = res.shape[-1]
+    modules = numerics == "fp16_modules"
+
+    def add(res, y):
+        # fused kernel: fp32 residual += fp32 sublayer output; torch modules: fp16(res + fp16(y))
+        return r16(res + r16(y, numerics), numerics) if modules else res + y
+
     # 1-2: self attention
     a = r16(layer_norm(res, W[bp + "self_norm.weight"], W[bp + "self_norm.bias"], numerics), numerics)
     w, b = W[bp + "self_attn.in_proj_weight"], W[bp + "self_attn.in_proj_bias"]
     qkv = r16(_lin(a, w, b), numerics)
     o = r16(attention(qkv[..., :d], qkv[..., d:2 * d], qkv[..., 2 * d:], heads, mask), numerics)
-    res = res + _lin(o, W[bp + "self_attn.out_proj.weight"], W[bp + "self_attn.out_proj.bias"])
+    res = add(res, _lin(o, W[bp + "self_attn.out_proj.weight"], W[bp + "self_attn.out_proj.bias"]))
     # 3-4: cross attention over the (hoisted) context K/V
     a = r16(layer_norm(res, W[bp + "cross_norm.weight"], W[bp + "cross_norm.bias"], numerics), numerics)
     w, b = W[bp + "cross_attn.in_proj_weight"], W[bp + "cross_attn.in_proj_bias"]
     q = r16(_lin(a, w[:d], b[:d]), numerics)
     o = r16(attention(q, kv[0], kv[1], heads, None), numerics)
-    res = res + _lin(o, W[bp + "cross_attn.out_proj.weight"], W[bp + "cross_attn.out_proj.bias"])
-    # 5-6: feed-forward
+    res = add(res, _lin(o, W[bp + "cross_attn.out_proj.weight"], W[bp + "cross_attn.out_proj.bias"]))
+    # 5-6: feed-forward (the modules round the up-projection before the GELU)
     a = r16(layer_norm(res, W[bp + "ffn.0.weight"], W[bp + "ffn.0.bias"], numerics), numerics)
     u = _lin(a, W[bp + "ffn.1.weight"], W[bp + "ffn.1.bias"])
-    g = r16(gelu(u), numerics)
-    return res + _lin(g, W[bp + "ffn.4.weight"], W[bp + "ffn.4.bias"])
+    g = r16(gelu(r16(u, numerics) if modules else u), numerics)
+    return add(res, _lin(g, W[bp + "ffn.4.weight"], W[bp + "ffn.4.bias"]))
+
+
+def fused_kernel_shape(d, ffn_mult, heads, chunk_rows, ctx_rows, batch):
+    """Whether the reference runs this flow shape on its fused block kernel (``"fp16"`` numerics)
+    rather than on torch's fp16 modules (``"fp16_modules"``): ``cuda_block.supported`` plus the
+    batch-1 gate of ``_cf_fused_runner`` (``cf/cuda_block.py:95-102``,
+    ``cf/drafters/chunked_flow.py:295-331``; ``CF_CUDA_BLOCK_BATCH`` is off by default)."""
+    return (d in (640, 1024) and ffn_mult == 6 and heads == 8 and all(s in (4, 8) for s in chunk_rows)
+            and 0 < ctx_rows <= 16 and batch == 1)
 
 
 def expert_velocity(W, pfx, prev, cur, tau_add, chunk_start, kvs, cfg, numerics):
@@ -194,7 +230,7 @@ def predict_hidden(W, context, cfg, numerics="fp16", return_trace=False):
     trace = [z.copy()]
     dt = 1.0 / E
     for s in range(E):
-        tau = r16(np.float64(s * dt), numerics)
+        tau = float(r16(s * dt, numerics))
         vels = []
         for ci, p in enumerate(pfxs):
             start = ci * cs

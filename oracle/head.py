@@ -26,7 +26,8 @@ def path_residual(W, embed_w, lastp, nlive, order, numerics="fp16"):
     depth (``_nlive``) or None for all.  -> residual [N, d]."""
     o = order if nlive is None else min(nlive, order)
     lp = np.asarray(lastp)[:, :o]
-    mask = (lp >= 0).astype(np.float64)
+    ft = np.float32 if W["path_head.norm.weight"].dtype == np.float32 else np.float64
+    mask = (lp >= 0).astype(ft)
     emb = embed_w[np.maximum(lp, 0)]                                    # [N, o, d]
     terms = []
     for j in range(o):

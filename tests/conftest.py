@@ -43,6 +43,15 @@ def weights64(W: dict) -> dict:
     return {k: to64(v) for k, v in W.items()}
 
 
+def oracle_numerics(cfg, batch: int = 1) -> str:
+    """The oracle mode matching the numerics the reference runs this flow shape in: its fused
+    kernel's ("fp16") or torch's fp16 modules' ("fp16_modules")."""
+    from oracle import flow as oflow
+    rows = [(c + 1) * cfg.chunk_size for c in range(cfg.draft_length // cfg.chunk_size)]
+    fused = oflow.fused_kernel_shape(cfg.flow_dim, cfg.ffn_multiplier, cfg.num_heads, rows, cfg.context_size, batch)
+    return "fp16" if fused else "fp16_modules"
+
+
 @pytest.fixture(scope="session")
 def cuda():
     import torch

@@ -127,3 +127,58 @@ def test_tree_gdn_matches_reference():
     assert rel_err(out, f("out")) < TOL
     assert rel_err(states, f("states")) < TOL
     assert rel_err(out, G["gdn_seq"]) < TOL
+
+
+# ---- fp16: the reference's own drafter cast to fp16 and run on the CPU (tests/golden/make_golden_fp16.py),
+# i.e. torch's fp16 modules -- the numerics the reference uses at every width its fused kernel does not take.
+G16 = np.load(Path(__file__).parent / "golden" / "reference_tiny_fp16.npz")
+
+
+def _weights16(E):
+    assert G16[f"weights_sha_E{E}"].tobytes() == G[f"weights_sha_E{E}"].tobytes()
+    return {k: v.astype(np.float16).astype(np.float64) for k, v in _weights(E).items()}
+
+
+@pytest.mark.parametrize("E", [1, 3])
+def test_fp16_modules_numerics_pinned_by_the_reference_fp16_drafter(E):
+    """The oracle's "fp16_modules" mode (fp16 residual x = fp16(x + fp16(sublayer)), GELU of the
+    rounded up-projection) agrees with the reference's fp16 predict_hidden to ~1.1e-4 norm-relative:
+    one-ulp flips from torch's fp16 GEMM accumulation order.  The fused-kernel mode (fp32 residual)
+    and fp32 math are measurably further (1.5-2.3e-4 and 3.7-4.5e-4), so a dropped residual or
+    GELU rounding fails here."""
+    W = _weights16(E)
+    ctx = G16["ctx16"].astype(np.float64)
+    err = {num: rel_err(oflow.predict_hidden(W, ctx, _ocfg(E), numerics=num), G16[f"pred16_E{E}"])
+           for num in ("fp16_modules", "fp16", "fp32")}
+    assert err["fp16_modules"] < 1.3e-4, err
+    assert err["fp16_modules"] < err["fp16"] and 2.5 * err["fp16_modules"] < err["fp32"], err
+
+
+def test_fp16_modules_velocity_pinned_by_the_reference():
+    W = _weights16(3)
+    ctx = G16["ctx16"].astype(np.float64)
+    err = {}
+    for num in ("fp16_modules", "fp16", "fp32"):
+        z0 = oflow.init_latents(ctx, 8, "fp16")
+        kvs = [[oflow.cross_kv(W, f"{p}blocks.{l}.", ctx, num) for l in range(LAYERS)]
+               for p in oflow.expert_prefixes(2)]
+        vels = []
+        for ci, p in enumerate(oflow.expert_prefixes(2)):
+            tau_add = oflow.tau_embedding(W, p, 0.25, num)
+            vels.append(oflow.expert_velocity(W, p, z0[:, :4 * ci], z0[:, 4 * ci:4 * ci + 4], tau_add, 4 * ci,
+                                              kvs[ci], _ocfg(3), num))
+        err[num] = rel_err(np.concatenate(vels, 1), G16["vel16_tau025"])
+    assert err["fp16_modules"] < 6.5e-4, err
+    assert err["fp16_modules"] < min(err["fp16"], err["fp32"]), err
+
+
+@pytest.mark.parametrize("nl", [1, 2, 4])
+def test_fp16_path_residual_pinned_by_the_reference(nl):
+    """The fused path residual's fp16 rounding points (one rounding per offset projection, the
+    masked sum, LayerNorm, the MLP's up-projection and GELU) reproduce the reference's fp16 output to
+    2e-5 (bit for bit at 2 and 4 live offsets); fp32 math is 4.5e-4 away."""
+    W = _weights16(3)
+    got = ohead.path_residual(W, W["embed_tokens.weight"], G16["lastp"], nl, 4, numerics="fp16")
+    assert rel_err(got, G16[f"res16_fused_n{nl}"]) < 2e-5
+    got32 = ohead.path_residual(W, W["embed_tokens.weight"], G16["lastp"], nl, 4, numerics="fp32")
+    assert rel_err(got32, G16[f"res16_fused_n{nl}"]) > 2e-4

@@ -1,7 +1,9 @@
 """GPU parity of the fused flow (cfh_flow_integrate) against the CPU oracle.
 
-Contract: predicted hiddens within 2e-3 norm-relative of the oracle's fp16-path restatement of
-``TreeFlowDrafter.predict_hidden`` on the same seeded weights and context.
+Contract: predicted hiddens within 2e-3 norm-relative of the oracle's fp16 restatement of
+``TreeFlowDrafter.predict_hidden`` on the same seeded weights and context, in the numerics the
+reference runs that shape in (its fused kernel's at d in {640, 1024}, torch's fp16 modules'
+elsewhere).
 """
 from __future__ import annotations
 
@@ -9,7 +11,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import rel_err, to64, weights64
+from conftest import oracle_numerics, rel_err, to64, weights64
 from chain_flow_amd.config import flownet
 from chain_flow_amd.flow import FusedFlow
 from chain_flow_amd.weights import make_weights, synthetic_context
@@ -40,7 +42,7 @@ def test_flow_matches_oracle(cuda, d, layers, steps):
     ff = FusedFlow(cfg, {k: v.to(cuda) for k, v in W.items()}, device=cuda)
     z = ff.predict_hidden(ctx.to(cuda))
     torch.cuda.synchronize()
-    ref = oflow.predict_hidden(weights64(W), to64(ctx), _ocfg(cfg), numerics="fp16")
+    ref = oflow.predict_hidden(weights64(W), to64(ctx), _ocfg(cfg), numerics=oracle_numerics(cfg))
     err = rel_err(to64(z), ref)
     print(f"  rel err {err:.3e}", flush=True)
     assert np.isfinite(to64(z)).all()
@@ -58,7 +60,7 @@ def test_flow_long_draft_matches_oracle(cuda, d, kd, cs):
     ff = FusedFlow(cfg, {k: v.to(cuda) for k, v in W.items()}, device=cuda)
     z = ff.predict_hidden(ctx.to(cuda))
     torch.cuda.synchronize()
-    ref = oflow.predict_hidden(weights64(W), to64(ctx), _ocfg(cfg), numerics="fp16")
+    ref = oflow.predict_hidden(weights64(W), to64(ctx), _ocfg(cfg), numerics=oracle_numerics(cfg))
     err = rel_err(to64(z), ref)
     print(f"  rel err {err:.3e}", flush=True)
     assert np.isfinite(to64(z)).all()
@@ -92,7 +94,7 @@ def test_flow_full_width_matches_oracle(cuda):
     z = ff.predict_hidden(ctx.to(cuda))
     torch.cuda.synchronize()
     del ff
-    ref = oflow.predict_hidden(weights64(W), to64(ctx), _ocfg(cfg), numerics="fp16")
+    ref = oflow.predict_hidden(weights64(W), to64(ctx), _ocfg(cfg), numerics=oracle_numerics(cfg))
     err = rel_err(to64(z), ref)
     print(f"  rel err {err:.3e}", flush=True)
     assert np.isfinite(to64(z)).all()
@@ -114,7 +116,7 @@ def test_flow_latent_widths_match_oracle(cuda, d, heads, layers, steps):
     ff = FusedFlow(cfg, {k: v.to(cuda) for k, v in W.items()}, device=cuda)
     z = ff.predict_hidden(ctx.to(cuda))
     torch.cuda.synchronize()
-    ref = oflow.predict_hidden(weights64(W), to64(ctx), _ocfg(cfg), numerics="fp16")
+    ref = oflow.predict_hidden(weights64(W), to64(ctx), _ocfg(cfg), numerics=oracle_numerics(cfg))
     err = rel_err(to64(z), ref)
     print(f"  rel err {err:.3e}", flush=True)
     assert np.isfinite(to64(z)).all()

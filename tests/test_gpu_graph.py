@@ -14,7 +14,7 @@ from chain_flow_amd.ring import ContextRing
 from chain_flow_amd.weights import make_weights
 
 
-def _drafter(kind, cuda):
+def _drafter(kind, cuda, twopass_m=0, shared=True):
     d, V, n = 512, 4096, 1024
     if kind == "latent":
         cfg = TreeVAEFlowConfig(context_size=8, draft_length=8, chunk_size=4, expert_dim=d, num_heads=8,
@@ -26,21 +26,30 @@ def _drafter(kind, cuda):
     W = make_weights(cfg, V, init="test", base_seed=5, hidden=d)
     W["lm_head.weight"] = (W["lm_head.weight"].float() * 8).half()
     sl = torch.randperm(V, generator=torch.Generator().manual_seed(3))[:n].sort().values
-    return Drafter(cfg, {k: v.to(cuda) for k, v in W.items()}, sl.to(torch.int32).to(cuda), device=cuda), d, sl
+    return Drafter(cfg, {k: v.to(cuda) for k, v in W.items()}, sl.to(torch.int32).to(cuda), device=cuda,
+                   twopass_m=twopass_m, twopass_shared=shared), d, sl
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("kind", ["target", "latent"])
-def test_draft_graph_replays_equal_eager(cuda, kind):
-    dr, d, sl = _drafter(kind, cuda)
+@pytest.mark.parametrize("kind,search,twopass", [
+    ("target", "chain", None), ("latent", "chain", None),
+    # the proposer's default head: two-pass (shared candidate image at B = 1, per-request candidate
+    # rows read in place at B > 1), and per-depth candidate sets
+    ("target", "chain", "shared"), ("target", "chain", "per_depth"),
+    ("target", "tree", None), ("target", "tree", "shared"), ("latent", "tree", "per_depth")])
+def test_draft_graph_replays_equal_eager(cuda, kind, search, twopass):
+    dr, d, sl = _drafter(kind, cuda, twopass_m=256 if twopass else 0, shared=twopass != "per_depth")
     R, C, kmax = 4, 8, 6
     eager_ring = ContextRing(R, C, d, device=cuda)
     graph_ring = ContextRing(R, C, d, device=cuda)
-    draft = lambda ctx, k0: dr.beam_chains(ctx, k0, 5, 4)
+    if search == "chain":
+        draft = lambda ctx, k0: dr.beam_chains(ctx, k0, 5, 4)
+    else:
+        draft = lambda ctx, k0: dr.beam_tree(ctx, k0, keep=4, topb=8, depth=4)
     graphs = DraftGraphs(graph_ring, draft, kmax, bucket_ladder(R))
     assert graphs.buckets == [1, 2, 4]
     rng = np.random.default_rng(9)
-    print(f"[graph] {kind}", flush=True)
+    print(f"[graph] {kind} {search} twopass={twopass}", flush=True)
     for step in range(6):
         B = int(rng.integers(1, R))                      # 1..3: pads to buckets 1, 2 and 4
         rows = rng.permutation(R)[:B].tolist()

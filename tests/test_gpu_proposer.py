@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import to64
+from conftest import oracle_numerics, to64
 from chain_flow_amd import shortlist as slmod
 from chain_flow_amd.config import flownet
 from chain_flow_amd.vllm_plugin import flow_proposer as fp
@@ -52,7 +52,7 @@ def test_proposer_chain_draft_matches_oracle(cuda, tmp_path, monkeypatch):
     W64 = {k: to64(v) for k, v in W.items()}
     ocfg = dict(draft_length=cfg.draft_length, chunk_size=cfg.chunk_size, num_layers=1, num_heads=cfg.num_heads,
                 num_flow_steps=2, init_mode="delta")
-    pred = oflow.predict_hidden(W64, ctx, ocfg, numerics="fp16")
+    pred = oflow.predict_hidden(W64, ctx, ocfg, numerics=oracle_numerics(cfg))
     s64 = slv.numpy()
     score = lambda h, prev: ohead.head_with_bias(h, W64["lm_head.weight"][s64], W64["markov.w1.weight"],
                                                  W64["markov.w2.weight"][s64], prev)

@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import rel_err, to64
+from conftest import oracle_numerics, rel_err, to64
 from chain_flow_amd import shortlist as slmod
 from chain_flow_amd.config import TreeVAEFlowConfig
 from chain_flow_amd.drafter import Drafter
@@ -110,7 +110,8 @@ def test_latent_drafter_predict_hidden_matches_oracle(cuda):
     ctx = synthetic_context(1, 8, hidden, seed=8)
     pred = dr.predict_hidden(ctx.to(cuda))
     torch.cuda.synchronize()
-    ref = ovae.predict_hidden({k: to64(v) for k, v in W.items()}, to64(ctx), _vcfg(cfg), _fcfg(cfg), "fp16")
+    ref = ovae.predict_hidden({k: to64(v) for k, v in W.items()}, to64(ctx), _vcfg(cfg), _fcfg(cfg), "fp16",
+                              oracle_numerics(cfg))
     err = rel_err(to64(pred), ref)
     print(f"  rel err {err:.3e}", flush=True)
     assert pred.shape == (1, 8, hidden) and np.isfinite(to64(pred)).all()
@@ -149,7 +150,7 @@ def test_latent_proposer_chain_matches_oracle(cuda, tmp_path, monkeypatch):
     assert len(out) == 1 and len(out[0]) == 5
     ctx = oflow.front_pad_context(to64(hid)[None], cfg.context_size)
     W64 = {k: to64(v) for k, v in W.items()}
-    pred = ovae.predict_hidden(W64, ctx, _vcfg(cfg), _fcfg(cfg), "fp16")
+    pred = ovae.predict_hidden(W64, ctx, _vcfg(cfg), _fcfg(cfg), "fp16", oracle_numerics(cfg))
     s64 = slv.numpy()
     score = lambda h, prev: ohead.head_with_bias(h, W64["lm_head.weight"][s64], W64["markov.w1.weight"],
                                                  W64["markov.w2.weight"][s64], prev)

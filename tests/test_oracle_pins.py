@@ -302,3 +302,57 @@ def test_ancestor_chain():
     assert depth.tolist() == [0, 1, 1, 2, 3]
     assert chain[4].tolist() == [4, 3, 1, 0]
     assert chain[2].tolist() == [2, 0, 0, 0]
+
+
+def test_product_and_oracle_agree_on_the_reference_numerics(monkeypatch):
+    """The flow's numerics switch (chain_flow_amd.flow.reference_numerics) and the oracle's copy of
+    the reference's fused-kernel gate (oracle.flow.fused_kernel_shape) pick the same mode over a
+    grid of shapes and batches, and follow the reference's CF_CUDA_BLOCK / CF_CUDA_BLOCK_BATCH."""
+    from chain_flow_amd import _lib
+    from chain_flow_amd.config import flownet
+    from chain_flow_amd.flow import reference_numerics
+    from conftest import oracle_numerics
+    monkeypatch.delenv("CF_CUDA_BLOCK", raising=False)
+    monkeypatch.delenv("CF_CUDA_BLOCK_BATCH", raising=False)
+    seen = set()
+    for d in (512, 640, 1024, 2560, 5120):
+        for heads in (8, 16):
+            for (kd, cs) in ((8, 4), (16, 8), (12, 4)):
+                for batch in (1, 2):
+                    cfg = flownet(d, layers=1, flow_steps=2, num_heads=heads, draft_length=kd, chunk_size=cs)
+                    got = reference_numerics(cfg, batch)
+                    want = oracle_numerics(cfg, batch)
+                    assert (got == _lib.FLOW_FUSED) == (want == "fp16"), (d, heads, kd, cs, batch)
+                    seen.add(want)
+    assert seen == {"fp16", "fp16_modules"}
+    cfg = flownet(640, layers=1, flow_steps=2)
+    assert reference_numerics(cfg, 1) == _lib.FLOW_FUSED and reference_numerics(cfg, 2) == _lib.FLOW_MODULES
+    monkeypatch.setenv("CF_CUDA_BLOCK_BATCH", "1")
+    assert reference_numerics(cfg, 2) == _lib.FLOW_FUSED
+    monkeypatch.setenv("CF_CUDA_BLOCK", "0")
+    assert reference_numerics(cfg, 1) == _lib.FLOW_MODULES
+
+
+def test_oracle_runs_in_float32_for_the_cpu_timing():
+    """Given float32 weights and context, the oracle's fp32 path stays in float32 end to end (the
+    arithmetic the CPU baseline times) and agrees with its float64 run to float32 precision."""
+    import torch
+    from chain_flow_amd.config import flownet
+    from chain_flow_amd.weights import make_weights, param_specs, synthetic_context
+    cfg = flownet(128, layers=2, flow_steps=3)
+    names = {n for n in param_specs(cfg, 64) if not n.startswith(("lm_head", "embed_tokens", "markov"))}
+    W = make_weights(cfg, 64, init="test", base_seed=2, names=names, dtype=torch.float32)
+    W32 = {k: v.numpy() for k, v in W.items()}
+    W64 = {k: v.double().numpy() for k, v in W.items()}
+    ctx = synthetic_context(1, 8, 128, seed=3, dtype=torch.float32).numpy()
+    ocfg = dict(draft_length=8, chunk_size=4, num_layers=2, num_heads=8, num_flow_steps=3, init_mode="delta")
+    z32 = oflow.predict_hidden(W32, ctx, ocfg, numerics="fp32")
+    z64 = oflow.predict_hidden(W64, ctx.astype(np.float64), ocfg, numerics="fp32")
+    assert z32.dtype == np.float32 and z64.dtype == np.float64
+    assert np.linalg.norm(z32 - z64) / np.linalg.norm(z64) < 1e-5
+    lastp = np.array([[3, 5, -1, -1], [7, 1, 2, 9]])
+    emb32 = np.random.default_rng(0).standard_normal((64, 128)).astype(np.float32)
+    r32 = ohead.path_residual(W32, emb32, lastp, 2, 4, numerics="fp32")
+    r64 = ohead.path_residual(W64, emb32.astype(np.float64), lastp, 2, 4, numerics="fp32")
+    assert r32.dtype == np.float32
+    assert np.linalg.norm(r32 - r64) / np.linalg.norm(r64) < 1e-5

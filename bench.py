@@ -57,14 +57,22 @@ SHORTLIST_ROWS = 62642
 VOCAB = 248320
 
 
-def flow_bytes(d, L, E, C, ffn=6):
+def flow_bytes(d, L, E, C, ffn=6, heads=8, ctx=8, fold=True):
     """Algorithmic HBM bytes of one predict_hidden: every fp16 weight byte once per time it is
-    needed (block weights per Euler step per chunk expert, cross K/V projection once per draft,
-    time_mlp[2] + out_norm/out_proj per step per expert) plus context in and hiddens out."""
-    blk = (3 + 1 + 1 + 1 + 2 * ffn) * d * d + (3 + 1 + 1 + 1 + ffn + 1 + 6) * d   # 18d^2 + 19d at ffn=6
+    needed plus context in and hiddens out.  Per Euler step per chunk expert: the block weights
+    (QKV, O, W1, W2 and the vectors; with the cross attention folded, the per-draft factors A and B
+    of H x C rows instead of the cross q / out projections) and time_mlp[2] + out_norm/out_proj;
+    once per draft: the cross K/V projection (and, folded, the cross q and out projections that
+    build A and B, which are written once)."""
+    vec = (3 + 1 + 1 + 1 + ffn + 1 + 6) * d                                        # 19d at ffn=6
+    if fold:
+        blk = (3 + 1 + 2 * ffn) * d * d + vec + 2 * heads * ctx * d                # 16d^2 + A, B
+        per_draft = L * (4 * d * d + 4 * d + 2 * heads * ctx * d)
+    else:
+        blk = (3 + 1 + 1 + 1 + 2 * ffn) * d * d + vec                              # 18d^2 + 19d
+        per_draft = L * (2 * d * d + 4 * d)
     per_step = L * blk + 2 * d * d + 5 * d
-    per_draft_kv = L * (2 * d * d + 4 * d)
-    halves = E * C * per_step + C * per_draft_kv
+    halves = E * C * per_step + C * per_draft
     return 2 * halves + 2 * (8 * d) + 2 * (8 * d)
 
 
@@ -610,14 +618,14 @@ def main():
     med = lambda v: v[len(v) // 2]
     ms = wall * 1e3 / args.steps
     if latent:
-        fb = flow_bytes(LATENT, L, E, cfg.num_chunks) + vae_bytes(d)
+        fb = flow_bytes(LATENT, L, E, cfg.num_chunks, fold=(LATENT // cfg.num_heads) % 32 == 0) + vae_bytes(d)
         traffic, kern = None, "predict_hidden pass (cfh_vae_encode + cfh_flow_integrate + cfh_vae_decode)"
         workload = (f"latent chain draft: hidden {d} fp16 bs1 K={K} width {Wd}; TransformerHiddenVAE latent "
                     f"{LATENT} (intermediate {VAE_INTER}, {VAE_LAYERS}+{VAE_LAYERS} layers); flow at {LATENT}, "
                     f"L={L} E={E} 2 chunk experts; shortlisted head {SHORTLIST_ROWS}x{d}")
         metric = "us per 5-token draft step (latent drafter: hidden 2560, VAE latent 640, bs1)"
     else:
-        fb = flow_bytes(d, L, E, cfg.num_chunks)
+        fb = flow_bytes(d, L, E, cfg.num_chunks, fold=(d // cfg.num_heads) % 32 == 0)
         traffic, kern = measured_traffic(d, L, E), "flow pass (cfh_flow_integrate)"
         workload = (f"chain draft d={d} fp16 bs1 K={K} width {Wd}, flow L={L} E={E} "
                     f"2 chunk experts, shortlisted head {SHORTLIST_ROWS}x{d}")

@@ -31,6 +31,7 @@ struct ExpertLayout {
       fn_w, fn_b, w1, w1_b, w2, w2_b;
   size_t on_w, on_b, out, out_b;           // out_norm, out_proj
   size_t total;
+  bool fold;                               // cross attention folded (xattn_fold): qc holds Wq^T
 };
 
 bool flow_dims_ok(const cfh_flow_dims* d);
@@ -38,5 +39,10 @@ bool flow_dims_ok(const cfh_flow_dims* d);
 // a multiple of 32, the MFMA k-step; 0 if none (head widths must be multiples of 8).
 int heads_per_chunk(int hd, int H);
 ExpertLayout expert_layout(const cfh_flow_dims* d);
+// Whether the flow folds the cross attention's query and output projections into per-draft
+// factors of the context K/V (one head per k-chunk: head width a multiple of 32).  The packed
+// layout depends on it (the query weight is stored transposed), so packing and the flow plan both
+// decide by this one function of the shape.
+bool xattn_fold(const cfh_flow_dims* d);
 
 }  // namespace cfh

@@ -20,7 +20,7 @@ constexpr int PF_SPLIT = 8;       //                                   split-K k
 constexpr int STREAM_SYNC = 4;    // fragment groups between workgroup barriers in the stream (measured: 4 best of 0-4)
 
 enum SrcKind { S_BUF = 0, S_SELF = 1, S_CROSS = 2 };
-enum EpiKind { E_PART = 0, E_BIAS16 = 1, E_GELU16 = 2 };
+enum EpiKind { E_PART = 0, E_BIAS16 = 1, E_GELU16 = 2, E_PART16 = 3 };
 
 struct SEx {
   const h16x8* w;      // packed weights: fragment (tile t, k-step s) at ((t * K/32) + s) * 64
@@ -29,7 +29,7 @@ struct SEx {
   const float* pin;    // S_CROSS: cross-q partials [ks_in][S][d]
   const h16* bin;      // S_CROSS: cross-q bias (in_proj_bias[0:d])
   const h16* bias;     // E_BIAS16 / E_GELU16 bias [N]
-  void* out;           // E_PART: float [ks][S][N]; otherwise h16 [S][N]
+  void* out;           // E_PART: float [ks][S][N]; E_PART16: h16 [ks][S][N]; otherwise h16 [S][N]
   int S;               // activation rows (<= 16)
 };
 
@@ -283,7 +283,7 @@ __global__ void __launch_bounds__(WV * 64) k_stream(SArgs a) {
   // the bias of the wave's first tile comes with the operand: an epilogue load issued after the
   // weight loads would wait for every one of them
   float bias0 = 0.f;
-  if constexpr (EPI != E_PART) bias0 = (float)ex.bias[t0 * 16 + (lane & 15)];
+  if constexpr (EPI == E_BIAS16 || EPI == E_GELU16) bias0 = (float)ex.bias[t0 * 16 + (lane & 15)];
   __builtin_amdgcn_sched_barrier(0);
   h16x8 buf[SPF];
 #pragma unroll
@@ -311,6 +311,8 @@ __global__ void __launch_bounds__(WV * 64) k_stream(SArgs a) {
         if (r < ex.S) {
           if constexpr (EPI == E_PART) {
             ((float*)ex.out)[((size_t)kc * ex.S + r) * a.N + n] = acc[q];
+          } else if constexpr (EPI == E_PART16) {
+            ((h16*)ex.out)[((size_t)kc * ex.S + r) * a.N + n] = (h16)acc[q];
           } else {
             float bv;
             if (ct == 0) bv = bias0;

@@ -21,18 +21,26 @@
 //   per draft : TAU  time_mlp(tau_s) for all E steps     (GEMV + reduce)
 //               ROWS init_latents(ctx), step-0 rows x, a = LN_self(x) of block 0
 //               KV   cross K/V of every block             (GEMV + reduce)
+//               FOLD per block: A_h = Wq_h^T K_h^T, B_h = Wo_h V_h   (stream, split-K by head)
 //   per Euler step, per block l (both experts in every launch):
 //     QKV   stream  A = a (LN_self rows)          epilogue q,k,v = fp16(acc + b)      full-K tiles
 //     O     stream  A = causal self attention of head h, computed while staging    split-K by head
 //     RES   row     x += sum_h P + b_o ; a = LN_cross(fp16(x))
-//     QC    stream  A = a                         fp32 partials                     split-K
-//     OC    stream  A = cross attention of head h (q reduced from the QC partials, hoisted K/V)
+//     XATT  small   scores_h = a A_h + bq_h K_h^T, softmax, P_h B_h per head (fp32 partials)
 //     RES   row     x += sum_h P + b_oc ; a = LN_ffn(fp16(x))
 //     W1    stream  A = a                         epilogue g = fp16(gelu(acc + b1))  full-K tiles
 //     W2    stream  A = g                         fp32 partials                     split-K
 //     RES   row     x += sum P + b2 ; a = LN_self of block l+1 (out_norm after the last block)
 //   OUT   stream  A = out_norm rows of the current chunk                           split-K
 //   ROWS  row     v = fp16(sum P + b_out); z = fp16(z + fp16(dt v)); next step's rows and LN_self
+//
+// The cross attention's query and output projections are folded into the context: the context is
+// fixed for the whole draft, so q_h . K_h = LN(x) . (Wq_h^T K_h^T) + bq_h . K_h and
+// Wo (P V) = sum_h P_h (Wo_h V_h); the two d x (H C) factors are built once per draft from Wq and
+// Wo, and no block pass streams those two d x d matrices again (2 d^2 of the 18 d^2 halves a block
+// pass reads).  Same products in exact arithmetic; q and the attention output are not rounded to
+// fp16 on the way.  Shapes with several heads per MFMA k-chunk (head width not a multiple of 32)
+// keep the unfolded QC / OC streaming launches.
 //
 #include <stdio.h>
 
@@ -183,6 +191,159 @@ __global__ void __launch_bounds__(ROWT) k_rows(RowsArgs a) {
   }
 }
 
+// XATT: the cross attention of one block pass from the per-draft factors A_h = Wq_h^T K_h^T and
+// B_h = Wo_h V_h (both [H][C][d] fp16) and sb_h[c] = bq_h . K_h[c] (fp32): for every row r,
+//   scores[r][c] = (LN(x)[r] . A_h[c] + sb_h[c]) / sqrt(hd),  P = softmax_c(scores),
+//   out_h[r][n] = sum_c P[r][c] B_h[c][n]
+// (exactly q_h . K_h with q = Wq LN(x) + bq, and Wo_h (P V_h); A and B are rounded to fp16 where
+// the reference rounds q and P V_h).  One workgroup per (expert, head, column block of n).  The
+// workgroup first puts its block of B_h in flight (it does not depend on the scores), then the
+// scores: one 16 x 16 MFMA tile (rows x context rows) over d with the k-steps split over the waves,
+// each wave issuing all its loads before its MFMAs, the wave tiles summed through LDS; the softmax;
+// and its column block of P_h B_h, written as the head's fp32 partial [H][S][d] that the residual
+// row kernel sums with the other heads and the out_proj bias, as for any split-K sublayer.
+struct XattArgs {
+  const h16* xn[4];      // LN_cross(x) rows [S][d]
+  const h16* A[4];       // this layer's A [H][C][d]
+  const h16* Bf[4];      // this layer's B [H][C][d]
+  const float* sb[4];    // this layer's sb [H][C]
+  float* out[4];         // partials [H][S][d]
+  int S[4];
+  int nex, d, H, C, nb;
+  float scale;
+};
+
+constexpr int XT = 512;        // threads of an XATT workgroup
+
+template <int CM>              // context rows, padded to 8 or 16
+__global__ void __launch_bounds__(XT) k_xattn(XattArgs a) {
+  constexpr int NW = XT / 64;
+  constexpr int XRS = CM == 8 ? 20 : 10;     // k-steps a wave loads in one round (registers)
+  __shared__ float red[NW][256];
+  __shared__ float P[MAXR][16];
+  int b = blockIdx.x;
+  const int cb = b % a.nb;
+  b /= a.nb;
+  const int h = b % a.H, e = b / a.H;
+  const int S = a.S[e], C = a.C, d = a.d;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  // this thread's 8 columns of B_h (every context row), in flight before the scores
+  const int gpb = d / 8 / a.nb, g = cb * gpb + min(t, gpb - 1);
+  const h16* Bh = a.Bf[e] + (size_t)h * C * d + 8 * g;
+  h16x8 bv[CM];
+#pragma unroll
+  for (int c = 0; c < CM; ++c) bv[c] = *(const h16x8*)(Bh + (size_t)min(c, C - 1) * d);
+  // scores: lane row = lane % 16 (rows past S repeat row S-1: their products are never read),
+  // context row = lane % 16 of the B operand (rows past C read row C-1, zeroed)
+  const h16* Ah = a.A[e] + (size_t)h * C * d;
+  const int ns = d / 32, per = (ns + NW - 1) / NW, s0 = wave * per, s1 = min(ns, s0 + per);
+  const int ci = lane & 15;
+  const h16* xrow = a.xn[e] + (size_t)min(lane & 15, S - 1) * d + 8 * (lane >> 4);
+  const h16* arow = Ah + (size_t)min(ci, C - 1) * d + 8 * (lane >> 4);
+  const h16x8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int r0 = s0; r0 < s1; r0 += XRS) {
+    h16x8 xv[XRS], av[XRS];
+#pragma unroll
+    for (int u = 0; u < XRS; ++u) {
+      const int st = min(r0 + u, s1 - 1);
+      xv[u] = *(const h16x8*)(xrow + st * 32);
+      av[u] = *(const h16x8*)(arow + st * 32);
+    }
+#pragma unroll
+    for (int u = 0; u < XRS; ++u)
+      if (r0 + u < s1) acc = mfma_f16(xv[u], ci < C ? av[u] : zero8, acc);
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) red[wave][(4 * (lane >> 4) + q) * 16 + (lane & 15)] = acc[q];
+  __syncthreads();
+  if (t < 256) {
+    const int r = t >> 4, c = t & 15;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) v += red[w][t];
+    if (r < S) P[r][c] = c < C ? (v + a.sb[e][h * C + c]) * a.scale : -INFINITY;
+  }
+  __syncthreads();
+  // softmax over the C context rows, one thread per row
+  if (t < S) {
+    float m = -INFINITY;
+    for (int c = 0; c < C; ++c) m = fmaxf(m, P[t][c]);
+    float z[16], sum = 0.f;
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      z[c] = c < C ? expf(P[t][c] - m) : 0.f;
+      sum += z[c];
+    }
+    const float inv = 1.0f / sum;
+#pragma unroll
+    for (int c = 0; c < 16; ++c) P[t][c] = z[c] * inv;
+  }
+  __syncthreads();
+  // this workgroup's columns of P_h B_h
+  if (t < gpb) {
+    float* oh = a.out[e] + (size_t)h * S * d + 8 * g;
+    for (int r = 0; r < S; ++r) {
+      float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < CM; ++c) {
+        const float pw = P[r][c];   // 0 for the padding rows c >= C
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] += pw * (float)bv[c][j];
+      }
+      *(float4*)(oh + (size_t)r * d) = make_float4(o[0], o[1], o[2], o[3]);
+      *(float4*)(oh + (size_t)r * d + 4) = make_float4(o[4], o[5], o[6], o[7]);
+    }
+  }
+}
+
+// The query bias's share of every block's scores, sb[l][h][c] = bq_h . K_h[c], once per draft:
+// one workgroup per (expert, block), one wave per (head, context row) pair at a time.
+struct XbiasArgs {
+  const h16* K[4];       // block 0's context K rows [C][d]; block l at + l * kstride halves
+  const h16* bq[4];      // block 0's cross_attn.in_proj_bias[0:d]; block l at + l * bstride bytes
+  float* sb[4];          // [L][H][C]
+  long long kstride, bstride;
+  int nex, nl, d, H, C;
+};
+
+__global__ void __launch_bounds__(1024) k_xbias(XbiasArgs a) {
+  const int e = blockIdx.x / a.nl, l = blockIdx.x - e * a.nl;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int hd = a.d / a.H;
+  const h16* K = a.K[e] + (size_t)l * a.kstride;
+  const h16* bq = (const h16*)((const char*)a.bq[e] + (size_t)l * a.bstride);
+  for (int p = wave; p < a.H * a.C; p += nw) {
+    const int h = p / a.C, c = p - h * a.C;
+    float s = 0.f;
+    for (int j = lane; j < hd; j += 64) s += (float)bq[h * hd + j] * (float)K[(size_t)c * a.d + h * hd + j];
+    s = wave_sum(s);
+    if (lane == 0) a.sb[e][((size_t)l * a.H + h) * a.C + c] = s;
+  }
+}
+
+// Column blocks per (expert, head) of XATT: at least 64 workgroups in all, each block a whole
+// number of 8-column groups, at most one group per thread; 0 if d / 8 has no such split.
+int xattn_blocks(int d, int units) {
+  const int ng = d / 8;
+  for (int nb = 1; nb <= ng; ++nb)
+    if (ng % nb == 0 && ng / nb <= XT && units * nb >= 64) return nb;
+  for (int nb = 1; nb <= ng; ++nb)
+    if (ng % nb == 0 && ng / nb <= XT) return nb;
+  return 0;
+}
+
+int launch_xattn(const XattArgs& a, hipStream_t st) {
+  if (a.C > 16 || a.nb <= 0) return CFH_E_UNSUPPORTED;
+  for (int e = 0; e < a.nex; ++e)
+    if (a.S[e] > MAXR) return CFH_E_UNSUPPORTED;
+  const dim3 grid((unsigned)(a.nex * a.H * a.nb));
+  if (a.C <= 8) hipLaunchKernelGGL(k_xattn<8>, grid, dim3(XT), 0, st, a);
+  else hipLaunchKernelGGL(k_xattn<16>, grid, dim3(XT), 0, st, a);
+  CFH_LAUNCH_CHECK();
+  return CFH_OK;
+}
+
 struct Plan {
   int d, fd, CS, E, NL, C, KD, H, hd, nch, Smax;
   int ks_att;         // k-chunks of the attention launches: H / heads per chunk
@@ -190,6 +351,8 @@ struct Plan {
   int wpb_qc, wpb_w2, wpb_out, tpw_att, wpb_att, wpb_full, wpb_w1;
   int pks;            // partial slots per expert
   int res_mode;       // RES_ADD32 (fused-kernel numerics) or RES_ADD16 (torch fp16 modules)
+  bool fold;          // cross attention folded into per-draft factors (cfh::xattn_fold)
+  int wpb_fold, xnb;  // fold hoist launch waves / XATT column blocks per (expert, head)
   bool ok;
 };
 
@@ -201,6 +364,7 @@ Plan make_plan(const cfh_flow_dims* dm) {
   p.nch = p.KD / p.CS;
   p.Smax = p.KD;
   p.res_mode = dm->numerics == CFH_FLOW_MODULES ? RES_ADD16 : RES_ADD32;
+  p.fold = cfh::xattn_fold(dm);
   const int tiles_d = p.d / 16;
   const size_t cap = 96 * 1024;
   // (one k-chunk when K has fewer than 8 k-steps: small latent widths)
@@ -234,6 +398,10 @@ Plan make_plan(const cfh_flow_dims* dm) {
   fit_grid(tiles_d, p.nch * p.ks_qc, &p.wpb_qc, nullptr);
   fit_grid(tiles_d, p.nch * p.ks_out, &p.wpb_out, nullptr);
   p.pks = std::max(std::max(p.ks_att, p.ks_w2), p.ks_out);
+  if (p.fold) {
+    p.wpb_fold = wpb_for_grid(tiles_d, 2 * p.nch * p.H, 8, p.C * p.hd / 8);
+    p.xnb = xattn_blocks(p.d, p.nch * p.H);
+  }
   p.ok = p.ks_qc > 0 && p.ks_qc <= 8 && p.ks_w2 > 0 && p.ks_out > 0 && p.ks_att > 0 && res_nq(p.d) > 0;
   if (!p.ok) return p;
   // every streaming launch of a draft, as block_pass and the OUT step issue them
@@ -243,10 +411,11 @@ Plan make_plan(const cfh_flow_dims* dm) {
     a.ks_in = p.ks_qc; a.Ck = p.C;
     return a;
   };
+  const bool cross_ok = p.fold ? !stream_check(S_BUF, sa(p.d, p.d, p.H, p.wpb_fold, 1), p.C) && p.xnb > 0
+                              : !stream_check(S_BUF, sa(p.d, p.d, p.ks_qc, p.wpb_qc, 1), p.Smax) &&
+                                    !stream_check(S_CROSS, sa(p.d, p.d, p.ks_att, p.wpb_att, p.tpw_att), p.Smax);
   p.ok = !stream_check(S_BUF, sa(3 * p.d, p.d, 1, p.wpb_full, 1), p.Smax) &&
-         !stream_check(S_SELF, sa(p.d, p.d, p.ks_att, p.wpb_att, p.tpw_att), p.Smax) &&
-         !stream_check(S_BUF, sa(p.d, p.d, p.ks_qc, p.wpb_qc, 1), p.Smax) &&
-         !stream_check(S_CROSS, sa(p.d, p.d, p.ks_att, p.wpb_att, p.tpw_att), p.Smax) &&
+         !stream_check(S_SELF, sa(p.d, p.d, p.ks_att, p.wpb_att, p.tpw_att), p.Smax) && cross_ok &&
          !stream_check(S_BUF, sa(p.fd, p.d, 1, p.wpb_w1, 1), p.Smax) &&
          !stream_check(S_BUF, sa(p.d, p.fd, p.ks_w2, p.wpb_w2, 1), p.Smax) &&
          !stream_check(S_BUF, sa(p.d, p.d, p.ks_out, p.wpb_out, 1), p.CS);
@@ -260,9 +429,12 @@ struct WS {
   h16* qkv[4];
   h16* g[4];
   float* P[4];        // partials of the split-K kernels (O, OC, W2, OUT)
-  float* Pq[4];       // cross-q partials (QC), read by OC
+  float* Pq[4];       // cross-q partials (QC), read by OC (unfolded shapes)
   h16* tau[4];        // [E][d]
   h16* kvc[4];        // [L][2][C][d]
+  h16* fa[4];         // folded shapes: A [L][H][C][d] = Wq_h^T K_h^T
+  h16* fb[4];         //                B [L][H][C][d] = Wo_h V_h
+  float* fsb[4];      //                sb [L][H][C] = bq_h . K_h
   float* Pkv;         // [nch][L][ks][C][2d]
   float* Ptau;        // [nch][ks][E][d]
   float* ctx_mom;     // [C][2]
@@ -286,9 +458,14 @@ WS carve(const Plan& p, char* base) {
     w.qkv[c] = (h16*)take(S * 3 * d * 2);
     w.g[c] = (h16*)take(S * fd * 2);
     w.P[c] = (float*)take((size_t)p.pks * S * d * 4);
-    w.Pq[c] = (float*)take((size_t)p.ks_qc * S * d * 4);
+    if (!p.fold) w.Pq[c] = (float*)take((size_t)p.ks_qc * S * d * 4);
     w.tau[c] = (h16*)take((size_t)p.E * d * 2);
     w.kvc[c] = (h16*)take((size_t)p.NL * 2 * p.C * d * 2);
+    if (p.fold) {
+      w.fa[c] = (h16*)take((size_t)p.NL * p.H * p.C * d * 2);
+      w.fb[c] = (h16*)take((size_t)p.NL * p.H * p.C * d * 2);
+      w.fsb[c] = (float*)take((size_t)p.NL * p.H * p.C * 4);
+    }
   }
   w.Pkv = (float*)take((size_t)p.nch * p.NL * p.ks_kv * p.C * 2 * d * 4);
   w.Ptau = (float*)take((size_t)p.nch * p.ks_tau * p.E * d * 4);
@@ -339,8 +516,19 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w, const voi
     r.g[c] = (const h16*)PTR(c, B + L.xn_w); r.b[c] = (const h16*)PTR(c, B + L.xn_b);
   }
   if ((rc = launch_res(r, st))) return rc;
+  if (p.fold) {
+    XattArgs x = {};
+    x.nex = nch; x.d = d; x.H = p.H; x.C = p.C; x.nb = p.xnb; x.scale = 1.0f / sqrtf((float)p.hd);
+    const size_t per_l = (size_t)p.H * p.C * d;
+    for (int c = 0; c < nch; ++c) {
+      x.xn[c] = w.abuf[c]; x.A[c] = w.fa[c] + (size_t)l * per_l; x.Bf[c] = w.fb[c] + (size_t)l * per_l;
+      x.sb[c] = w.fsb[c] + (size_t)l * p.H * p.C;
+      x.out[c] = w.P[c]; x.S[c] = S_of(c);
+    }
+    if ((rc = launch_xattn(x, st))) return rc;
+  }
   // QC: cross-attention query projection, split-K partials
-  {
+  if (!p.fold) {
     SArgs a = {};
     a.nex = nch; a.N = d; a.K = d; a.ks = p.ks_qc; a.wpb = p.wpb_qc; a.tpw = 1; a.d = d; a.hd = p.hd;
     a.wg_per_kc = (d / 16) / (a.wpb * a.tpw);
@@ -351,7 +539,7 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w, const voi
     if ((rc = launch_stream<S_BUF, E_PART>(a, p.Smax, st))) return rc;
   }
   // OC: cross attention per head over the hoisted context K/V, staged, then out_proj split-K by head
-  {
+  if (!p.fold) {
     SArgs a = {};
     a.nex = nch; a.N = d; a.K = d; a.ks = p.ks_att; a.wpb = p.wpb_att; a.tpw = p.tpw_att; a.d = d; a.hd = p.hd;
     a.ks_in = p.ks_qc; a.Ck = p.C;
@@ -484,6 +672,42 @@ int integrate(const Plan& p, const cfh_flow_dims* dm, const void* const* experts
       }
       hipLaunchKernelGGL(k_reduce, dim3(1024), dim3(256), 0, st, r);
       CFH_LAUNCH_CHECK();
+    }
+    // ---- the folded cross attention's factors of every block: A_h = Wq_h^T K_h^T from the
+    // transposed query weight against the K rows, B_h = Wo_h V_h from the out-projection against
+    // the V rows, each split-K by head (the partial of head h, rounded to fp16, is the factor)
+    if (p.fold) {
+      XbiasArgs xb = {};
+      xb.nex = nch; xb.nl = NL; xb.d = d; xb.H = p.H; xb.C = C;
+      xb.kstride = (long long)2 * C * d; xb.bstride = (long long)L.blkstride;
+      for (int c = 0; c < nch; ++c) {
+        xb.K[c] = w.kvc[c]; xb.bq[c] = (const h16*)PTR(c, BLK(0) + L.qc_b); xb.sb[c] = w.fsb[c];
+      }
+      hipLaunchKernelGGL(k_xbias, dim3(nch * NL), dim3(1024), 0, st, xb);
+      CFH_LAUNCH_CHECK();
+      for (int l = 0; l < NL; ++l) {
+        const size_t per_l = (size_t)p.H * C * d;
+        for (int half = 0; half < 2; ++half) {
+          // A and B of every expert in one launch when they fit the launch's four weight sets
+          if (half == 1 && 2 * nch <= 4) break;
+          SArgs a = {};
+          a.N = d; a.K = d; a.ks = p.H; a.wpb = p.wpb_fold; a.tpw = 1; a.d = d; a.hd = p.hd;
+          a.wg_per_kc = (d / 16) / a.wpb;
+          for (int part = 0; part < 2; ++part) {
+            if (2 * nch > 4 && part != half) continue;
+            for (int c = 0; c < nch; ++c) {
+              SEx& x = a.ex[a.nex++];
+              const h16* kv = w.kvc[c] + (size_t)l * 2 * C * d;
+              x.w = (const h16x8*)PTR(c, BLK(l) + (part == 0 ? L.qc : L.oc));
+              x.a = part == 0 ? kv : kv + (size_t)C * d;
+              x.lda = d;
+              x.out = (part == 0 ? w.fa[c] : w.fb[c]) + (size_t)l * per_l;
+              x.S = C;
+            }
+          }
+          if ((rc = launch_stream<S_BUF, E_PART16>(a, C, st))) return rc;
+        }
+      }
     }
     for (int s = 0; s < E; ++s) {
       for (int l = 0; l < NL; ++l)

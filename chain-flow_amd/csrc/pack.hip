@@ -37,6 +37,11 @@ bool flow_dims_ok(const cfh_flow_dims* d) {
   return true;
 }
 
+bool xattn_fold(const cfh_flow_dims* d) {
+  const int hd = d->d / d->heads;
+  return heads_per_chunk(hd, d->heads) == 1 && d->ctx_rows <= 16;
+}
+
 ExpertLayout expert_layout(const cfh_flow_dims* dm) {
   const size_t d = dm->d, fd = (size_t)dm->ffn_mult * dm->d, H = 2;  // 2 bytes per element
   ExpertLayout L;
@@ -88,10 +93,33 @@ ExpertLayout expert_layout(const cfh_flow_dims* dm) {
   L.out_b = take(d * H);
   L.out = take(d * d * H);
   L.total = off;
+  L.fold = xattn_fold(dm);
   return L;
 }
 
 }  // namespace cfh
+
+// The transpose of a row-major W[k][n] in the same tile order: out holds W^T [n][k] packed, i.e.
+// out[(t*(K/32)+s)*64 + lane][j] = W[32s + 8*(lane/16) + j][16t + lane%16] (K = k).  Used once per
+// weight, so the strided reads do not matter.
+__global__ void k_pack_linear_t(const uint16_t* __restrict__ w, int n, int k, uint4* __restrict__ out) {
+  const size_t total = (size_t)n * k / 8;    // output vectors: n rows of W^T x k/8
+  const int ks = k / 32;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const int lane = (int)(i & 63);
+    const size_t ts = i >> 6;
+    const int s = (int)(ts % ks);
+    const int t = (int)(ts / ks);
+    const size_t col = (size_t)t * 16 + (lane & 15);          // row of W^T = column of W
+    const size_t row0 = (size_t)s * 32 + 8 * (lane >> 4);     // first of 8 rows of W
+    uint16_t v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = w[(row0 + j) * n + col];
+    out[i] = make_uint4(v[0] | (unsigned)v[1] << 16, v[2] | (unsigned)v[3] << 16, v[4] | (unsigned)v[5] << 16,
+                        v[6] | (unsigned)v[7] << 16);
+  }
+}
 
 // out[(t*(K/32)+s)*64 + lane] = W[16t + lane%16][32s + 8*(lane/16) .. +7]
 __global__ void k_pack_linear(const uint4* __restrict__ w, int n, int k, uint4* __restrict__ out) {
@@ -180,7 +208,14 @@ int cfh_flow_pack_expert(const cfh_flow_dims* dims, const void* const* raw, int 
     CFH_TRY(cp(B + L.xn_b, r[7], d));
     CFH_TRY(cp(B + L.cn_w, r[8], d));
     CFH_TRY(cp(B + L.cn_b, r[9], d));
-    CFH_TRY(pk(B + L.qc, r[10], (int)d, (int)d));
+    if (L.fold) {
+      // the query weight transposed: the per-draft fold computes Wq_h^T K_h^T from it
+      hipLaunchKernelGGL(k_pack_linear_t, dim3(1024), dim3(256), 0, st, (const uint16_t*)r[10], (int)d, (int)d,
+                         (uint4*)(base + B + L.qc));
+      CFH_HIP(hipGetLastError());
+    } else {
+      CFH_TRY(pk(B + L.qc, r[10], (int)d, (int)d));
+    }
     CFH_TRY(pk(B + L.kv, (const char*)r[10] + d * d * 2, (int)(2 * d), (int)d));
     CFH_TRY(cp(B + L.qc_b, r[11], d));
     CFH_TRY(cp(B + L.kv_b, (const char*)r[11] + d * 2, 2 * d));

@@ -27,9 +27,9 @@ extern "C" {
 #define CFH_E_HIP 3              /* a HIP runtime call failed (cfh_last_hip_error)        */
 #define CFH_E_SCRATCH 4          /* the no-allocation entry point's workspace is too small */
 
-/* Size of the library's per-device scratch array behind cfh_flow_integrate_noalloc (32 MiB:
- * the flow workspace of d <= 5120 at 8 layers needs 18.7 MB). */
-#define CFH_NOALLOC_SCRATCH_BYTES (32ll << 20)
+/* Size of the library's per-device scratch array behind cfh_flow_integrate_noalloc (64 MiB:
+ * the flow workspace of d <= 5120 at 8 layers needs 57.3 MiB). */
+#define CFH_NOALLOC_SCRATCH_BYTES (64ll << 20)
 
 /* Library version (major*10000 + minor*100 + patch). */
 int cfh_version(void);

@@ -48,7 +48,7 @@ def test_candidate_select_argument_checks_without_a_device():
 
 def test_noalloc_flow_rejects_a_workspace_beyond_the_scratch_without_a_device():
     """cfh_flow_integrate_noalloc refuses, before any HIP call, a shape whose flow workspace exceeds
-    the 32 MiB scratch array (d = 8192 at 8 layers needs 46.7 MB), with its own status."""
+    the 64 MiB scratch array (d = 8192 at 8 layers needs 108 MiB), with its own status."""
     import ctypes as C
 
     from chain_flow_amd.config import flownet
@@ -56,8 +56,8 @@ def test_noalloc_flow_rejects_a_workspace_beyond_the_scratch_without_a_device():
     L = _lib.lib()
     assert L.cfh_error_string(4).startswith(b"workspace exceeds the no-allocation scratch")
     cfg = flownet(8192, layers=8, flow_steps=8)
-    assert caps(cfg) > 32 << 20
-    assert caps(flownet(5120, layers=8, flow_steps=8)) <= 32 << 20
+    assert caps(cfg) > 64 << 20
+    assert caps(flownet(5120, layers=8, flow_steps=8)) <= 64 << 20
     dims = flow_dims(cfg)
     p = 4096   # stand-in addresses: never dereferenced, the size check fails first
     experts = _lib.ptr_array([p, p])

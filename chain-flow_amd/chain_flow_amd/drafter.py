@@ -91,24 +91,20 @@ class Drafter:
                 image: torch.Tensor | None = None):
         """Per-depth top-k of rows [B*F, d]: (vals [B*F, k], ids [B*F, k] int32, map) -- one-pass over the
         shortlist (ids shortlist-local, map = the shortlist), two-pass over one request's packed
-        candidate image (ids local to the candidates, map = their global ids), or over each
-        request's candidate rows read in place (ids already global, map None)."""
+        candidate image (ids local to the candidates, map = their global ids), or over every
+        request's own candidate rows read in place, all requests in one launch (ids already global,
+        map None)."""
         if cand is None:
             vals, ids, _ = self.head.topk(rows, k, prev=prev, prev_stride=order)
             return vals, ids, self.head.sl
         if image is not None:
             vals, ids, _ = self.head.topk_image(rows, k, image, cand.shape[-1], prev=prev, prev_stride=order)
             return vals, ids, cand[0]
+        cb = cand.contiguous()                                          # [B, M]
+        vals, ids, _ = self.head.topk_groups(rows, k, cb, prev=prev, prev_stride=order)
         F = rows.shape[0] // B
-        vals = torch.empty(B * F, k, dtype=torch.float32, device=rows.device)
-        ids = torch.empty(B * F, k, dtype=torch.int32, device=rows.device)
-        for b in range(B):
-            cb = cand[b].contiguous()
-            v, i, _ = self.head.topk_rows(rows[b * F:(b + 1) * F], k, cb, prev=prev[b * F * order:],
-                                          prev_stride=order)
-            vals[b * F:(b + 1) * F] = v
-            ids[b * F:(b + 1) * F] = cb[i.long()]
-        return vals, ids, None
+        glob = torch.gather(cb, 1, ids.view(B, F * k).long()).view(B * F, k)
+        return vals, glob, None
 
     def _nlive(self, depth: int):
         """``_nlive`` (``cf/vllm_plugin/flow_proposer.py:1030-1037``)."""
@@ -128,13 +124,13 @@ class Drafter:
         K' = min(K, draft_length - 1).  ``pred`` (the flow output) may be passed in to skip the flow."""
         dev = self.device
         W, order = width, self.order
+        if not 1 <= W <= 8:
+            raise ValueError(f"beam width {W} is not supported: the beam step keeps W*W <= 64 candidates "
+                             f"per chain (width 1..8)")
         if pred is None:
             pred = self.predict_hidden(ctx)
         B, Kd, d = pred.shape
         steps = min(K + 1, Kd)
-        if B * W > 8:
-            outs = [self.beam_chains(None, known0[i:i + 1], K, W, pred=pred[i:i + 1]) for i in range(B)]
-            return torch.cat(outs, 0)
         lastp = torch.full((B, W, order), -1, dtype=torch.int32, device=dev)
         lastp[:, :, 0] = known0.to(dev, torch.int32).view(B, 1)
         cum = torch.full((B, W), float("-inf"), dtype=torch.float32, device=dev)
@@ -148,8 +144,8 @@ class Drafter:
         cands = self._pass_a(pred, lastp, 1, steps, W) if self.twopass_m and steps > 1 else None
         image = self._candidate_image(cands, B)
         for step in range(1, steps):
-            for b in range(B):
-                self.path.hidden(lastp[b], self._nlive(step), pred[b, step], out=hbuf[b * W:(b + 1) * W])
+            # every request's W beams in one call, each request's rows with its own marginal hidden
+            self.path.hidden(lastp.view(B * W, order), self._nlive(step), pred[:, step], out=hbuf)
             vals, ids, smap = self._scores(hbuf, W, lastp.view(-1), order,
                                            None if cands is None else cands[:, step - 1], B, image)
             _lib.check(L.cfh_beam_chain_step(vals.data_ptr(), ids.data_ptr(), cum.data_ptr(), lastp.data_ptr(),
@@ -166,13 +162,12 @@ class Drafter:
         """``_beam_tree``: -> [B, 2N] int32-valued int64: N BFS-ordered tokens || parent node indices."""
         dev = self.device
         order = self.order
+        if keep < 1 or topb < 1 or keep * topb > 64:
+            raise ValueError(f"tree keep {keep} x top-b {topb} is not supported: a tree step ranks at most 64 "
+                             f"children per request (keep * topb <= 64)")
         if pred is None:
             pred = self.predict_hidden(ctx)
         B, Kd, d = pred.shape
-        if B * keep > 8:
-            outs = [self.beam_tree(None, known0[i:i + 1], keep, topb, depth, pred=pred[i:i + 1])
-                    for i in range(B)]
-            return torch.cat(outs, 0)
         nstep = min(depth, Kd - 1)
         sizes, fr = [], 1
         for _ in range(nstep):
@@ -194,9 +189,7 @@ class Drafter:
         for step in range(1, nstep + 1):
             rows = torch.empty(B * fr, d, dtype=torch.float16, device=dev) if fr != keep else hbuf
             lp_rows = lastp[:, :fr].reshape(B * fr, order).contiguous()
-            for b in range(B):
-                self.path.hidden(lp_rows[b * fr:(b + 1) * fr], self._nlive(step), pred[b, step],
-                                 out=rows[b * fr:(b + 1) * fr])
+            self.path.hidden(lp_rows, self._nlive(step), pred[:, step], out=rows)
             vals, ids, smap = self._scores(rows, topb, lp_rows.view(-1), order,
                                            None if cands is None else cands[:, step - 1], B, image)
             _lib.check(L.cfh_beam_tree_step(vals.data_ptr(), ids.data_ptr(), cum.data_ptr(), lastp.data_ptr(),

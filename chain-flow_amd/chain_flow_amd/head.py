@@ -16,6 +16,10 @@ def _i32(t: torch.Tensor) -> torch.Tensor:
     return t.to(torch.int32).contiguous()
 
 
+GEMV_ROWS = 8        # rows the GEMV head takes per launch; more go through the MFMA GEMM head
+GEMM_ROWS = 256      # rows of one GEMM head launch
+
+
 class ShortlistHead:
     """The target's lm_head restricted to a shortlist, plus the markov logit bias
     ``markov.w2(markov.w1[prev])`` restricted to the same rows.
@@ -86,7 +90,9 @@ class ShortlistHead:
         """-> (log-prob values [M, k] f32, shortlist-local ids [M, k] int32, lse [M] f32).
 
         The log-softmax top-k is fused into the head; ``logits`` (fp16 [M, n]) is written only when
-        given.  ``out`` = preallocated (vals, ids, lse) to fill."""
+        given.  ``out`` = preallocated (vals, ids, lse) to fill.  Up to 8 rows run on the GEMV head;
+        more (the batched and tree searches, pass A over many requests) on the MFMA GEMM head over
+        the packed image, 256 rows a launch, with the same rounding points."""
         M = h.shape[0]
         dev = h.device
         if out is None:
@@ -96,6 +102,19 @@ class ShortlistHead:
         else:
             vals, ids, lse = out
         use_m = self.w1 is not None and prev is not None
+        if M > GEMV_ROWS:
+            if self.image is None:
+                for r0 in range(0, M, GEMV_ROWS):
+                    r1 = min(M, r0 + GEMV_ROWS)
+                    self.topk(h[r0:r1], k, None if not use_m else prev[r0 * prev_stride:], prev_stride,
+                              None if logits is None else logits[r0:r1], (vals[r0:r1], ids[r0:r1], lse[r0:r1]))
+                return vals, ids, lse
+            for r0 in range(0, M, GEMM_ROWS):
+                r1 = min(M, r0 + GEMM_ROWS)
+                pv = prev[r0 * prev_stride:r1 * prev_stride:prev_stride] if use_m else None
+                self.gemm_topk(h[r0:r1], k, pv, None if logits is None else logits[r0:r1],
+                               (vals[r0:r1], ids[r0:r1], lse[r0:r1]))
+            return vals, ids, lse
         ws = self.workspace(M, k, dev)
         if self.image is not None:
             _lib.check(_lib.lib().cfh_head_topk_packed(
@@ -110,6 +129,28 @@ class ShortlistHead:
             self.r, self.w2.data_ptr() if use_m else None, k, _lib.ptr(logits), vals.data_ptr(),
             ids.data_ptr(), lse.data_ptr(), ws.data_ptr(), _lib.stream_handle()),
             "cfh_head_topk")
+        return vals, ids, lse
+
+    def gemm_topk(self, h: torch.Tensor, k: int, prev: torch.Tensor | None, logits: torch.Tensor | None, out):
+        """``topk`` of up to 256 rows on the MFMA GEMM head (cfh_head_gemm16_topk) over the packed
+        image; with ``prev`` (one global id per row) the markov bias fp16(w1[prev] . w2_sl) first, as
+        logits of the image's markov rows, added before the head logits' last rounding."""
+        M = h.shape[0]
+        L = _lib.lib()
+        st = _lib.stream_handle()
+        h = h.contiguous()
+        bias = None
+        if prev is not None and self.w1 is not None:
+            a = self.w1.index_select(0, prev.to(torch.long)).contiguous()          # [M, r]
+            bias = torch.empty(M, self.n, dtype=torch.float16, device=h.device)
+            w2img = self.image.data_ptr() + int(L.cfh_head_packed_bytes(self.n, self.d, 0))
+            _lib.check(L.cfh_head_gemm16_topk(a.data_ptr(), M, self.r, w2img, self.n, None, 0, bias.data_ptr(),
+                                              None, None, None, None, st), "cfh_head_gemm16_topk (markov)")
+        vals, ids, lse = out
+        ws = self.workspace(M, k, h.device)
+        _lib.check(L.cfh_head_gemm16_topk(h.data_ptr(), M, self.d, self.image.data_ptr(), self.n, _lib.ptr(bias), k,
+                                          _lib.ptr(logits), vals.data_ptr(), ids.data_ptr(), lse.data_ptr(),
+                                          ws.data_ptr(), st), "cfh_head_gemm16_topk")
         return vals, ids, lse
 
     def candidates(self, hm: torch.Tensor, M: int, shared: bool = True, seed_res: torch.Tensor | None = None,
@@ -128,11 +169,9 @@ class ShortlistHead:
         prev = None if seed_prev is None else seed_prev.to(dev, torch.int32).repeat_interleave(n).contiguous()
         logits = torch.empty(B * n, self.n, dtype=torch.float16, device=dev)
         lse = torch.empty(B * n, dtype=torch.float32, device=dev)
-        for r0 in range(0, B * n, 8):                      # the head takes at most 8 rows a launch
-            r1 = min(B * n, r0 + 8)
-            self.topk(rows[r0:r1], 1, prev=None if prev is None else prev[r0:r1], logits=logits[r0:r1],
-                      out=(torch.empty(r1 - r0, 1, device=dev), torch.empty(r1 - r0, 1, dtype=torch.int32,
-                                                                               device=dev), lse[r0:r1]))
+        # every row in one head pass (the GEMM head above 8 rows): top-1 discarded, logits and lse kept
+        self.topk(rows, 1, prev=prev, logits=logits,
+                  out=(torch.empty(B * n, 1, device=dev), torch.empty(B * n, 1, dtype=torch.int32, device=dev), lse))
         nreq, nrow = (B, n) if shared else (B * n, 1)
         local = torch.empty(nreq, M, dtype=torch.int32, device=dev)
         glob = torch.empty(nreq, M, dtype=torch.int32, device=dev)
@@ -164,6 +203,11 @@ class ShortlistHead:
         """``topk`` over a ``pack_rows`` image of n rows: ids are positions in those rows."""
         Mh = h.shape[0]
         dev = h.device
+        if Mh > GEMV_ROWS:                                   # the GEMV head takes 8 rows a launch
+            parts = [self.topk_image(h[r0:r0 + GEMV_ROWS], k, image, n,
+                                     None if prev is None else prev[r0 * prev_stride:], prev_stride)
+                     for r0 in range(0, Mh, GEMV_ROWS)]
+            return tuple(torch.cat([p[i] for p in parts]) for i in range(3))
         vals = torch.empty(Mh, k, dtype=torch.float32, device=dev)
         ids = torch.empty(Mh, k, dtype=torch.int32, device=dev)
         lse = torch.empty(Mh, dtype=torch.float32, device=dev)
@@ -177,6 +221,47 @@ class ShortlistHead:
             h.data_ptr(), Mh, self.d, image.data_ptr(), n, self.w1.data_ptr() if use_m else None,
             prev.data_ptr() if use_m else None, prev_stride, self.r if use_m else 0, k, None, vals.data_ptr(),
             ids.data_ptr(), lse.data_ptr(), ws.data_ptr(), _lib.stream_handle()), "cfh_head_topk_packed")
+        return vals, ids, lse
+
+    def topk_groups(self, h: torch.Tensor, k: int, rows: torch.Tensor, prev: torch.Tensor | None = None,
+                    prev_stride: int = 1):
+        """Pass B for a batch in one launch (``cfh_head_topk_grouped``): h [G*F, d] (F consecutive rows
+        per request), rows [G, M] int32 global candidate ids of each request (read in place), the
+        head and markov bias over each request's own candidates, log-softmax over them, top-k.
+        -> (vals [G*F, k], ids [G*F, k] int32 positions in the request's row list, lse [G*F])."""
+        G, n = rows.shape
+        GF = h.shape[0]
+        F = GF // G
+        dev = h.device
+        vals = torch.empty(GF, k, dtype=torch.float32, device=dev)
+        ids = torch.empty(GF, k, dtype=torch.int32, device=dev)
+        lse = torch.empty(GF, dtype=torch.float32, device=dev)
+        use_m = self.w1 is not None and prev is not None
+        L = _lib.lib()
+        rows = rows.contiguous()
+        pid = prev.reshape(-1)[::prev_stride][:GF].view(G, F) if use_m else None   # markov parent of each row
+        for c0 in range(0, F, GEMV_ROWS):                    # a launch takes at most 8 rows per request
+            c1 = min(F, c0 + GEMV_ROWS)
+            m = c1 - c0
+            hv = h.view(G, F, -1)[:, c0:c1].contiguous() if (c0, c1) != (0, F) else h.contiguous()
+            pv = pid[:, c0:c1].contiguous() if use_m else None
+            v = torch.empty(G * m, k, dtype=torch.float32, device=dev)
+            i = torch.empty(G * m, k, dtype=torch.int32, device=dev)
+            ls = torch.empty(G * m, dtype=torch.float32, device=dev)
+            key = ("groups", G * m, n, k)
+            ws = self._ws.get(key)
+            if ws is None:
+                ws = self._ws[key] = torch.empty(int(L.cfh_head_ws_bytes(G * m, n, k)), dtype=torch.uint8, device=dev)
+            _lib.check(L.cfh_head_topk_grouped(
+                hv.data_ptr(), G, m, self.d, self.lm_w.data_ptr(), rows.data_ptr(), n, n,
+                self.w1.data_ptr() if use_m else None, pv.data_ptr() if use_m else None, 1,
+                self.r if use_m else 0, self.w2.data_ptr() if use_m else None, k, v.data_ptr(), i.data_ptr(),
+                ls.data_ptr(), ws.data_ptr(), _lib.stream_handle()), "cfh_head_topk_grouped")
+            if (c0, c1) == (0, F):
+                return v, i, ls
+            vals.view(G, F, k)[:, c0:c1] = v.view(G, m, k)
+            ids.view(G, F, k)[:, c0:c1] = i.view(G, m, k)
+            lse.view(G, F)[:, c0:c1] = ls.view(G, m)
         return vals, ids, lse
 
     def topk_rows(self, h: torch.Tensor, k: int, rows: torch.Tensor, prev: torch.Tensor | None = None,
@@ -309,14 +394,22 @@ class PathHead:
 
     def hidden(self, lastp: torch.Tensor, nlive: int | None, pred: torch.Tensor,
                out: torch.Tensor | None = None) -> torch.Tensor:
-        """lastp [M, order] int32 (global ids, -1 = none), pred [d] fp16 ->
-        fp16(pred + residual) [M, d] (the head's input at this depth)."""
+        """lastp [M, order] int32 (global ids, -1 = none); pred [d] fp16 shared by the M rows, or
+        [G, d] (one marginal hidden per request, M // G consecutive rows each; a strided view such as
+        pred[:, step] is fine) -> fp16(pred + residual) [M, d] (the head's input at this depth)."""
         M = lastp.shape[0]
+        if pred.dim() == 1:
+            pld, rpp = 0, 0
+        else:
+            G = pred.shape[0]
+            if M % G or pred.stride(1) != 1:
+                raise ValueError(f"pred [G, d] needs M % G == 0 and contiguous rows (M={M}, G={G})")
+            pld, rpp = pred.stride(0), M // G
         if out is None:
             out = torch.empty(M, self.d, dtype=torch.float16, device=pred.device)
-        ws = self._workspace(M, pred.device)
+        ws = self._workspace(min(M, 16), pred.device)
         _lib.check(_lib.lib().cfh_path_residual(
             self._ptrs, self.order, self.ffn, self.d, lastp.data_ptr(), M,
-            -1 if nlive is None else int(nlive), self.embed_w.data_ptr(), pred.data_ptr(),
+            -1 if nlive is None else int(nlive), self.embed_w.data_ptr(), pred.data_ptr(), pld, rpp,
             out.data_ptr(), ws.data_ptr(), _lib.stream_handle()), "cfh_path_residual")
         return out

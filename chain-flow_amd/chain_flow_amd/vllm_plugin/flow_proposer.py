@@ -181,6 +181,13 @@ class FlowDrafterProposer:
         self.K = int(spec.num_speculative_tokens) - (1 if self.tree else 0)
         self.draft_width = self.N if self.branching else self.K
         self.width = int(os.environ.get("CF_WIDTH", "4"))
+        # the beam kernels' limits: a chain step ranks W*W candidates, a tree step keep*topb children
+        if not self.tree and not 1 <= self.width <= 8:
+            raise ValueError(f"CF_WIDTH={self.width} is not supported by this build: the beam step ranks "
+                             f"width*width <= 64 candidates per request (CF_WIDTH 1..8)")
+        if self.tree and (self.tree_keep < 1 or self.tree_topb < 1 or self.tree_keep * self.tree_topb > 64):
+            raise ValueError(f"CF_TREE_KEEP={self.tree_keep} x CF_TREE_TOPB={self.tree_topb} is not supported by "
+                             f"this build: a tree step ranks keep*topb <= 64 children per request")
         self.ckd = os.environ.get("CF_DRAFTER_DIR")
         if not self.ckd:
             raise ValueError("set CF_DRAFTER_DIR to the drafter checkpoint dir")

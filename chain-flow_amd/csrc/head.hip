@@ -27,6 +27,8 @@ constexpr int HW = 8;       // waves per head workgroup (one 16-row vocabulary t
 constexpr int HCOLS = HW * 16;
 constexpr int HMAXM = 8;    // max activation rows of the in-place GEMV head
 constexpr int KMAX = 16;    // max top-k
+constexpr int PATH_CHUNK = 16;   // rows of one path-residual launch sequence (the GEMV's row limit)
+constexpr int PATH_MAXM = 256;   // rows of one cfh_path_residual call
 
 // (value, index) order: larger value first, equal values by lower index.
 __device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
@@ -158,6 +160,10 @@ struct HeadArgs {
   h16* logits;         // [M][n] or null
   void* ws;            // candidate sets (null: logits only)
   int M, d, n, r, a_ids_stride, k, nsets;
+  // request groups (grid.y): group g scores its own M rows (h + g M d) against its own n rows
+  // sl + g sl_stride; its candidates are rows g M .. g M + M - 1 of the workspace (G M rows)
+  int groups;
+  long long sl_stride;
 };
 
 // Packed head image (cfh_head_pack): the shortlisted rows of W, then those of the markov w2, in
@@ -179,6 +185,14 @@ template <bool PACKED>
 __global__ void __launch_bounds__(HW * 64) k_head(HeadArgs a) {
   extern __shared__ __align__(16) h16 sm[];
   __shared__ float Lt[HMAXM][HCOLS];
+  const int grp = blockIdx.y;
+  if (grp > 0) {
+    a.h += (size_t)grp * a.M * a.d;
+    if (a.sl) a.sl += (size_t)grp * a.sl_stride;
+    if (a.a_ids) a.a_ids += (size_t)grp * a.M * a.a_ids_stride;
+    else if (a.a) a.a += (size_t)grp * a.M * a.r;
+    if (a.logits) a.logits += (size_t)grp * a.M * a.n;
+  }
   const int ldh = a.d + 8, ldm = a.r + 8;
   h16* Ah = sm;
   h16* Am = sm + a.M * ldh;
@@ -242,7 +256,7 @@ __global__ void __launch_bounds__(HW * 64) k_head(HeadArgs a) {
   __syncthreads();
   if (wave >= a.M) return;
   // wave `wave` reduces row `wave` of this block's HCOLS columns
-  const Cands cd = carve_cands(a.ws, a.M, a.nsets, a.k);
+  const Cands cd = carve_cands(a.ws, a.M * max(a.groups, 1), a.nsets, a.k);
   const int m = wave;
   const int c0 = blockIdx.x * HCOLS + lane, c1 = c0 + 64;
   float x0 = Lt[m][lane], x1 = Lt[m][lane + 64];
@@ -253,7 +267,7 @@ __global__ void __launch_bounds__(HW * 64) k_head(HeadArgs a) {
     const float tv = x0; x0 = x1; x1 = tv;
     const int ti = i0; i0 = i1; i1 = ti;
   }
-  const size_t base = (size_t)m * a.nsets + blockIdx.x;
+  const size_t base = ((size_t)grp * a.M + m) * a.nsets + blockIdx.x;
   for (int r = 0; r < a.k; ++r) {
     float bv = x0;
     int bi = i0;
@@ -520,15 +534,36 @@ constexpr int GPF = 4;            // k-steps per LDS chunk
 constexpr int GKC = 32 * GPF;     // 128 columns per chunk: a row is 16 slots of 16 bytes
 
 struct GemmArgs {
-  const uint16_t* x;   // [M][d] bf16
-  const uint16_t* W;   // [V][d] bf16
+  const uint16_t* x;   // [M][d] bf16 (F16: fp16)
+  const uint16_t* W;   // [V][d] bf16 (F16: fp16)
   const int* sl;
-  uint16_t* logits;    // [M][n] bf16 or null
+  const uint16_t* bias;  // F16 only: [M][n] fp16 added before the last rounding, or null
+  uint16_t* logits;    // [M][n] bf16 (F16: fp16) or null
   void* ws;
-  int M, d, n, k, nsets;
+  int M, d, n, k, nsets;   // k = 0: logits only, no top-k
 };
 
-template <int MT, int NT, int GW, bool PK>
+// The 16-bit logit of a GEMM accumulator: bf16(acc), or fp16(acc) -- fp16(fp16(acc) + bias) with a
+// bias, the rounding points of the GEMV head's fp16(fp16(h.W) + fp16(A.W2)).
+template <bool F16>
+__device__ __forceinline__ uint16_t gemm_logit(float acc, const uint16_t* bias) {
+  if constexpr (F16) {
+    h16 v = (h16)acc;
+    if (bias) v = (h16)((float)v + (float)__builtin_bit_cast(h16, *bias));
+    return __builtin_bit_cast(uint16_t, v);
+  } else {
+    return __builtin_bit_cast(uint16_t, (__bf16)acc);
+  }
+}
+
+// The value of a 16-bit logit's bit pattern.
+template <bool F16>
+__device__ __forceinline__ float gemm_value(unsigned b) {
+  if constexpr (F16) return (float)__builtin_bit_cast(h16, (uint16_t)b);
+  else return __uint_as_float(b << 16);
+}
+
+template <int MT, int NT, int GW, bool PK, bool F16>
 __global__ void __launch_bounds__(GW * 64) k_head_gemm(GemmArgs a) {
   // [2][MT*16][GKC], each row's 16-byte slots XOR-swizzled by the row's low 4 bits: the 16 rows
   // an MFMA operand read touches then fall on 16 different bank groups
@@ -611,7 +646,11 @@ __global__ void __launch_bounds__(GW * 64) k_head_gemm(GemmArgs a) {
         const bf16x8 av = *(const bf16x8*)(xb + mt * 16 * GKC + slot * 8);
 #pragma unroll
         for (int t = 0; t < NT; ++t)
-          acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bq[p][t], acc[mt][t], 0, 0, 0);
+          if constexpr (F16)
+            acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h16x8, av),
+                                                                __builtin_bit_cast(h16x8, bq[p][t]), acc[mt][t], 0, 0, 0);
+          else
+            acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bq[p][t], acc[mt][t], 0, 0, 0);
       }
       // keep the reloads here: the scheduler would otherwise sink them to the end of the chunk
       __builtin_amdgcn_sched_barrier(0);
@@ -645,12 +684,14 @@ __global__ void __launch_bounds__(GW * 64) k_head_gemm(GemmArgs a) {
         for (int q = 0; q < 4; ++q) {
           const int r = mt * 16 + 4 * g + q;
           const int c = (wave * NT + t) * 16 + col;
-          const uint16_t b = __builtin_bit_cast(uint16_t, (__bf16)acc[mt][t][q]);
-          lg[r * LST + c] = b;
           const int j = blockIdx.x * COLS + c;
-          if (a.logits && r < a.M && j < a.n) a.logits[(size_t)r * a.n + j] = b;
+          const bool in = r < a.M && j < a.n;
+          const uint16_t b = gemm_logit<F16>(acc[mt][t][q], F16 && a.bias && in ? a.bias + (size_t)r * a.n + j : nullptr);
+          lg[r * LST + c] = b;
+          if (a.logits && in) a.logits[(size_t)r * a.n + j] = b;
         }
   }
+  if (a.k == 0) return;      // logits only
   lds_barrier();
   const Cands cd = carve_cands(a.ws, a.M, a.nsets, a.k);
   const int col = lane & 15;
@@ -667,7 +708,7 @@ __global__ void __launch_bounds__(GW * 64) k_head_gemm(GemmArgs a) {
         unsigned b = (w4[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
         if (b == 0x8000u) b = 0;                           // -0 ranks as +0
         const bool ok = blockIdx.x * COLS + c < a.n;
-        v[i] = ok ? __uint_as_float(b << 16) : -INFINITY;
+        v[i] = ok ? gemm_value<F16>(b) : -INFINITY;
         const unsigned o = (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
         key[i] = ok ? (o << 16) | (0xFFFFu - (unsigned)c) : 0u;
       }
@@ -686,7 +727,7 @@ __global__ void __launch_bounds__(GW * 64) k_head_gemm(GemmArgs a) {
       for (int i = 0; i < CPL; ++i) key[i] = key[i] == m ? 0u : key[i];
       const unsigned o = m >> 16;
       const unsigned b = (o & 0x8000u) ? (o & 0x7FFFu) : (~o & 0xFFFFu);
-      const float bv = m ? __uint_as_float(b << 16) : -INFINITY;
+      const float bv = m ? gemm_value<F16>(b) : -INFINITY;
       if (rr == 0) mx = bv;
       if (col == 0) {
         cd.cv[base * a.k + rr] = bv;
@@ -713,7 +754,7 @@ size_t gemm_lds() {
   return xbuf > lgt ? xbuf : lgt;
 }
 
-template <int MT, int NT, int GW, bool PK>
+template <int MT, int NT, int GW, bool PK, bool F16>
 int launch_gemm(const GemmArgs& a0, hipStream_t st) {
   // cfh_head_ws_bytes sizes the candidate lists for blocks of at least 128 columns
   static_assert(GW * NT * 16 >= 128, "a GEMM block must cover at least 128 shortlist columns");
@@ -722,9 +763,9 @@ int launch_gemm(const GemmArgs& a0, hipStream_t st) {
   a.nsets = (a.n + cols - 1) / cols;
   const size_t lds = gemm_lds<MT, NT, GW>();
   if (lds > 160 * 1024) return CFH_E_UNSUPPORTED;
-  CFH_HIP(hipFuncSetAttribute((const void*)k_head_gemm<MT, NT, GW, PK>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)lds));
-  hipLaunchKernelGGL((k_head_gemm<MT, NT, GW, PK>), dim3(a.nsets), dim3(GW * 64), lds, st, a);
+  CFH_HIP(hipFuncSetAttribute((const void*)k_head_gemm<MT, NT, GW, PK, F16>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+  hipLaunchKernelGGL((k_head_gemm<MT, NT, GW, PK, F16>), dim3(a.nsets), dim3(GW * 64), lds, st, a);
   CFH_LAUNCH_CHECK();
   return CFH_OK;
 }
@@ -780,9 +821,12 @@ __global__ void __launch_bounds__(ROWT) k_path_sum(PathSumArgs a) {
 struct PathOutArgs {
   const float* P;      // down-projection partials [ks][M][d]
   const h16* bias;     // mlp.3 bias
-  const h16* pred;     // [d] marginal hidden of this depth
+  const h16* pred;     // marginal hidden rows of this depth: row m uses pred + group(m) * pred_ld
   h16* hsum;           // [M][d] = fp16(pred + fp16(sum + b))
   int ks, M, d;
+  long long pred_ld;
+  int rows_per_pred;   // rows sharing one pred row (0: every row uses row 0)
+  int row0;            // row of this launch's first row in the whole call (for the grouping)
 };
 
 __global__ void __launch_bounds__(256) k_path_out(PathOutArgs a) {
@@ -790,9 +834,10 @@ __global__ void __launch_bounds__(256) k_path_out(PathOutArgs a) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
     float s = 0.f;
     for (int kc = 0; kc < a.ks; ++kc) s += a.P[kc * per_kc + i];
-    const int c = (int)(i % a.d);
+    const int m = (int)(i / a.d), c = (int)(i - (size_t)m * a.d);
+    const int g = a.rows_per_pred > 0 ? (a.row0 + m) / a.rows_per_pred : 0;
     const float res = r16(s + (float)a.bias[c]);
-    a.hsum[i] = (h16)((float)a.pred[c] + res);
+    a.hsum[i] = (h16)((float)a.pred[(size_t)g * a.pred_ld + c] + res);
   }
 }
 
@@ -919,8 +964,9 @@ int launch_head(const HeadArgs& ha0, hipStream_t st, bool packed = false) {
   const void* fn = packed ? (const void*)k_head<true> : (const void*)k_head<false>;
   CFH_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
   const int ntiles = (ha.n + 15) / 16;
-  if (packed) hipLaunchKernelGGL(k_head<true>, dim3((ntiles + HW - 1) / HW), dim3(HW * 64), lds, st, ha);
-  else hipLaunchKernelGGL(k_head<false>, dim3((ntiles + HW - 1) / HW), dim3(HW * 64), lds, st, ha);
+  const dim3 grid((ntiles + HW - 1) / HW, max(ha.groups, 1));
+  if (packed) hipLaunchKernelGGL(k_head<true>, grid, dim3(HW * 64), lds, st, ha);
+  else hipLaunchKernelGGL(k_head<false>, grid, dim3(HW * 64), lds, st, ha);
   CFH_LAUNCH_CHECK();
   return CFH_OK;
 }
@@ -977,29 +1023,30 @@ int launch_merge(const void* ws, int M, int nsets, int k, float* vals, int* ids,
   return CFH_OK;
 }
 
-template <bool PK>
-int gemm_topk(const void* x, int M, int d, const void* W, const int32_t* sl, int n, int k, void* logits,
-              float* vals, int32_t* ids, float* lse, void* ws, hipStream_t st) {
-  if (!x || !W || !vals || !ids || !ws || M < 1 || M > 256 || d < GKC || d % GKC || n < 1 || k < 1 || k > KMAX)
-    return CFH_E_INVALID;
+template <bool PK, bool F16>
+int gemm_topk(const void* x, int M, int d, const void* W, const int32_t* sl, int n, const void* bias, int k,
+              void* logits, float* vals, int32_t* ids, float* lse, void* ws, hipStream_t st) {
+  if (!x || !W || M < 1 || M > 256 || d < GKC || d % GKC || n < 1 || k < 0 || k > KMAX) return CFH_E_INVALID;
+  if (k == 0 ? !logits : (!vals || !ids || !ws)) return CFH_E_INVALID;
   GemmArgs ga = {};
   ga.x = (const uint16_t*)x; ga.W = (const uint16_t*)W; ga.sl = sl; ga.logits = (uint16_t*)logits; ga.ws = ws;
+  ga.bias = (const uint16_t*)bias;
   ga.M = M; ga.d = d; ga.n = n; ga.k = k;
   int rc, nsets;
   if (M <= 64) {
     nsets = gemm_nsets<4, 2, 8>(n);
     ga.nsets = nsets;
-    rc = launch_gemm<4, 2, 8, PK>(ga, st);
+    rc = launch_gemm<4, 2, 8, PK, F16>(ga, st);
   } else if (M <= 160) {
     nsets = gemm_nsets<10, 2, 8>(n);
     ga.nsets = nsets;
-    rc = launch_gemm<10, 2, 8, PK>(ga, st);
+    rc = launch_gemm<10, 2, 8, PK, F16>(ga, st);
   } else {
     nsets = gemm_nsets<16, 1, 8>(n);
     ga.nsets = nsets;
-    rc = launch_gemm<16, 1, 8, PK>(ga, st);
+    rc = launch_gemm<16, 1, 8, PK, F16>(ga, st);
   }
-  if (rc) return rc;
+  if (rc || k == 0) return rc;
   return launch_merge(ws, M, nsets, k, vals, ids, lse, st);
 }
 
@@ -1011,6 +1058,7 @@ int head_args(HeadArgs& ha, const void* h, int M, int d, const void* W, const in
   ha.h = (const h16*)h; ha.W = (const h16*)W; ha.sl = sl; ha.a = (const h16*)a; ha.a_ids = a_ids;
   ha.W2 = (const h16*)W2; ha.M = M; ha.d = d; ha.n = n; ha.r = W2 ? r : 0;
   ha.a_ids_stride = a_ids_stride > 0 ? a_ids_stride : 1;
+  ha.groups = 1;
   return CFH_OK;
 }
 
@@ -1092,31 +1140,52 @@ int cfh_head_topk_packed(const void* h, int M, int d, const void* packed, int n,
 
 int cfh_head_gemm_topk(const void* x, int M, int d, const void* W, const int32_t* sl, int n, int k, void* logits,
                        float* vals, int32_t* ids, float* lse, void* ws, void* stream) {
-  return gemm_topk<false>(x, M, d, W, sl, n, k, logits, vals, ids, lse, ws, (hipStream_t)stream);
+  if (k < 1) return CFH_E_INVALID;
+  return gemm_topk<false, false>(x, M, d, W, sl, n, nullptr, k, logits, vals, ids, lse, ws, (hipStream_t)stream);
 }
 
 int cfh_head_gemm_topk_packed(const void* x, int M, int d, const void* packed, int n, int k, void* logits,
                               float* vals, int32_t* ids, float* lse, void* ws, void* stream) {
   if (cfh_head_packed_bytes(n, d, 0) < 0) return CFH_E_INVALID;
-  return gemm_topk<true>(x, M, d, packed, nullptr, n, k, logits, vals, ids, lse, ws, (hipStream_t)stream);
+  if (k < 1) return CFH_E_INVALID;
+  return gemm_topk<true, false>(x, M, d, packed, nullptr, n, nullptr, k, logits, vals, ids, lse, ws,
+                                (hipStream_t)stream);
+}
+
+int cfh_head_topk_grouped(const void* h, int G, int M, int d, const void* W, const int32_t* sl, long long sl_stride,
+                          int n, const void* a, const int32_t* a_ids, int a_ids_stride, int r, const void* W2, int k,
+                          float* vals, int32_t* ids, float* lse, void* ws, void* stream) {
+  if (!vals || !ids || !ws || !sl || G < 1 || G > 65535 || sl_stride < n || k < 1 || k > KMAX) return CFH_E_INVALID;
+  HeadArgs ha;
+  int rc = head_args(ha, h, M, d, W, sl, n, a, a_ids, a_ids_stride, r, W2);
+  if (rc) return rc;
+  ha.ws = ws;
+  ha.k = k;
+  ha.nsets = (n + HCOLS - 1) / HCOLS;
+  ha.groups = G;
+  ha.sl_stride = sl_stride;
+  hipStream_t st = (hipStream_t)stream;
+  if ((rc = launch_head(ha, st))) return rc;
+  return launch_merge(ws, G * M, ha.nsets, k, vals, ids, lse, st);
+}
+
+int cfh_head_gemm16_topk(const void* x, int M, int d, const void* packed, int n, const void* bias, int k,
+                         void* logits, float* vals, int32_t* ids, float* lse, void* ws, void* stream) {
+  if (cfh_head_packed_bytes(n, d, 0) < 0) return CFH_E_INVALID;
+  return gemm_topk<true, true>(x, M, d, packed, nullptr, n, bias, k, logits, vals, ids, lse, ws,
+                               (hipStream_t)stream);
 }
 
 int64_t cfh_path_ws_bytes(int M, int d, int ffn_mult, int order) {
-  if (M < 1 || M > 16 || d < 512 || d % 512 || ffn_mult < 1 || order < 1 || order > MAXEX) return -1;
-  return (int64_t)path_plan(M, d, ffn_mult, order).total;
+  if (M < 1 || M > PATH_MAXM || d < 512 || d % 512 || ffn_mult < 1 || order < 1 || order > MAXEX) return -1;
+  return (int64_t)path_plan(std::min(M, PATH_CHUNK), d, ffn_mult, order).total;
 }
 
-int cfh_path_residual(const void* const* ph, int order, int ffn_mult, int d, const int32_t* lastp, int M,
-                      int nlive, const void* embed_w, const void* pred, void* hsum, void* ws, void* stream) {
-  if (!ph || !lastp || !embed_w || !pred || !hsum || !ws) return CFH_E_INVALID;
-  if (M < 1 || M > 16 || d < 512 || d % 512 || ffn_mult < 1 || order < 1 || order > MAXEX) return CFH_E_INVALID;
-  const int n_ptr = 2 * order + 6;
-  for (int i = 0; i < n_ptr; ++i)
-    if (!ph[i]) return CFH_E_INVALID;
-  hipStream_t st = (hipStream_t)stream;
-  const int o = (nlive < 0 || nlive > order) ? order : nlive;
+// One launch sequence of the path residual for M <= PATH_CHUNK rows (rows row0 .. of the call).
+static int path_chunk(const PathPlan& pp, const void* const* ph, int order, int ffn_mult, int d, const int32_t* lastp, int M,
+               int o, const void* embed_w, const void* pred, long long pred_ld, int rows_per_pred, int row0,
+               void* hsum, void* ws, hipStream_t st) {
   const int pf = ffn_mult * d;
-  const PathPlan pp = path_plan(M, d, ffn_mult, order);
   char* base = (char*)ws;
   float* P = (float*)(base + pp.off_P);
   h16* A = (h16*)(base + pp.off_a);
@@ -1166,8 +1235,31 @@ int cfh_path_residual(const void* const* ph, int order, int ffn_mult, int d, con
   }
   PathOutArgs po = {};
   po.P = Pdn; po.bias = b3; po.pred = (const h16*)pred; po.hsum = (h16*)hsum; po.ks = pp.dn_ks; po.M = M; po.d = d;
+  po.pred_ld = pred_ld; po.rows_per_pred = rows_per_pred; po.row0 = row0;
   hipLaunchKernelGGL(k_path_out, dim3(64), dim3(256), 0, st, po);
   CFH_LAUNCH_CHECK();
+  return CFH_OK;
+}
+
+int cfh_path_residual(const void* const* ph, int order, int ffn_mult, int d, const int32_t* lastp, int M,
+                      int nlive, const void* embed_w, const void* pred, long long pred_ld, int rows_per_pred,
+                      void* hsum, void* ws, void* stream) {
+  if (!ph || !lastp || !embed_w || !pred || !hsum || !ws) return CFH_E_INVALID;
+  if (M < 1 || M > PATH_MAXM || d < 512 || d % 512 || ffn_mult < 1 || order < 1 || order > MAXEX) return CFH_E_INVALID;
+  if (rows_per_pred < 0 || pred_ld < 0) return CFH_E_INVALID;
+  const int n_ptr = 2 * order + 6;
+  for (int i = 0; i < n_ptr; ++i)
+    if (!ph[i]) return CFH_E_INVALID;
+  const int o = (nlive < 0 || nlive > order) ? order : nlive;
+  const PathPlan pp = path_plan(std::min(M, PATH_CHUNK), d, ffn_mult, order);
+  // the GEMVs take at most PATH_CHUNK activation rows: chunks run one after another on the stream,
+  // each on the same workspace
+  for (int r0 = 0; r0 < M; r0 += PATH_CHUNK) {
+    const int m = std::min(PATH_CHUNK, M - r0);
+    const int rc = path_chunk(pp, ph, order, ffn_mult, d, lastp + (size_t)r0 * order, m, o, embed_w, pred, pred_ld,
+                              rows_per_pred, r0, (h16*)hsum + (size_t)r0 * d, ws, (hipStream_t)stream);
+    if (rc) return rc;
+  }
   return CFH_OK;
 }
 

@@ -242,20 +242,45 @@ int cfh_head_gemm_topk(const void* x, int M, int d, const void* W, const int32_t
 int cfh_head_gemm_topk_packed(const void* x, int M, int d, const void* packed, int n, int k, void* logits,
                               float* vals, int32_t* ids, float* lse, void* ws, void* stream);
 
+/* cfh_head_topk for G requests at once, each with its own rows and its own shortlist: request g
+ * scores its M rows h + g M d (M <= 8) against the n rows sl + g sl_stride (global ids into W and
+ * W2, read in place), with the markov rows a_ids + g M a_ids_stride (or A rows a + g M r); the
+ * per-row top-k over those n columns goes to rows g M .. g M + M - 1 of vals/ids/lse (ids are
+ * positions in that request's list).  ws: cfh_head_ws_bytes(G M, n, k) bytes.  The two-pass head's
+ * pass B for a batch (_gather_cand + _rescore, cf/vllm_plugin/flow_proposer.py:1167-1184, a bmm
+ * over per-request candidate rows) in one launch. */
+int cfh_head_topk_grouped(const void* h, int G, int M, int d, const void* W, const int32_t* sl, long long sl_stride,
+                          int n, const void* a, const int32_t* a_ids, int a_ids_stride, int r, const void* W2, int k,
+                          float* vals, int32_t* ids, float* lse, void* ws, void* stream);
+
+/* The drafter's fp16 form of the batched head, over a cfh_head_pack image (d % 256 == 0; an image
+ * packed with markov rows works too: its lm_head rows come first, and its markov w2 rows start at
+ * byte ((n + 15) / 16) * 16 * d * 2 as an r-column image of their own):
+ *   logits[m][j] = fp16( fp16(x[m] . W[row_j]) + bias[m][j] )   (bias [M][n] fp16, or NULL: no add)
+ * x [M][d] fp16, M <= 256.  k >= 1: the per-row log-softmax top-k into vals/ids/lse (ws of
+ * cfh_head_ws_bytes(M, n, k)), logits [M][n] fp16 optional; k = 0: the logits alone (required).
+ * With bias = the k = 0 logits of the markov rows against A[m] = w1[prev[m]], the logits are the GEMV
+ * head's fp16(fp16(h.W) + fp16(A.W2)).  Replaces the proposer's batched `_head` + `_bias` and
+ * log_softmax / topk over B*n rows (cf/vllm_plugin/flow_proposer.py:1021-1025, 1142-1165). */
+int cfh_head_gemm16_topk(const void* x, int M, int d, const void* packed, int n, const void* bias, int k,
+                         void* logits, float* vals, int32_t* ids, float* lse, void* ws, void* stream);
+
 /* ---------------------------------------------------------------- draft search
  * Path-conditioned residual of the PathHead, fused form (cf/vllm_plugin/fused.py:25-37;
  * un-fused twin cf/drafters/tree_flow.py:434-450):
- *   hsum[m] = fp16( pred + MLP(LN( fp16(sum_{j<nlive} mask_j fp16(W_j emb(lastp[m][j]) + b_j)) )) )
+ *   hsum[m] = fp16( pred_m + MLP(LN( fp16(sum_{j<nlive} mask_j fp16(W_j emb(lastp[m][j]) + b_j)) )) )
  * with emb = embed_w rows [V][d] of the global ids in lastp [M][order] (int32, -1 = no ancestor,
  * mask_j = lastp[m][j] >= 0), nlive = live offsets at this depth (_nlive, :1030-1037).
  * ph = path head fp16 parameters (2*order + 6 device pointers), matrices PACKED (cfh_pack_linear):
  *   offset_proj.{0..order-1}.weight [d][d], offset_proj.{0..order-1}.bias [d], norm.weight,
  *   norm.bias, mlp.0.weight [f*d][d], mlp.0.bias [f*d], mlp.3.weight [d][f*d], mlp.3.bias [d].
- * pred [d] fp16 = the marginal hidden of this depth, shared by the M rows.  ws: cfh_path_ws_bytes. */
+ * pred_m fp16 = the marginal hidden of this depth for row m's request: pred + (m / rows_per_pred) *
+ * pred_ld (rows_per_pred = 0: every row uses pred[0..d)), so B requests' beams go in one call.
+ * M <= 256.  ws: cfh_path_ws_bytes(M, ...) bytes (rows are processed 16 at a time). */
 int64_t cfh_path_ws_bytes(int M, int d, int ffn_mult, int order);
 int cfh_path_residual(const void* const* ph, int order, int ffn_mult, int d, const int32_t* lastp,
-                      int M, int nlive, const void* embed_w, const void* pred, void* hsum, void* ws,
-                      void* stream);
+                      int M, int nlive, const void* embed_w, const void* pred, long long pred_ld,
+                      int rows_per_pred, void* hsum, void* ws, void* stream);
 
 /* One depth of _beam_chains (cf/vllm_plugin/flow_proposer.py:1250-1259) for B chains of width W
  * (W*W <= 64): from the per-beam top-W rows vals/ids [B*W][W] (log-probs, shortlist-local ids),

@@ -1,0 +1,159 @@
+"""GPU: the batched drafting path -- many requests per launch, no per-request host loop.
+
+* the fp16 MFMA GEMM head (cfh_head_gemm16_topk, the drafter's head above 8 rows): logits within two
+  fp16 ulps of the oracle plus the fp32 dot product's rounding, with the markov bias added at the GEMV
+  head's rounding points; top-k ids equal where the margin exceeds 1e-3; log-sum-exp to 1e-5;
+* the grouped GEMV head (cfh_head_topk_grouped, pass B of the two-pass head for a batch) and the
+  batched path residual (one cfh_path_residual over every request's beams, each with its own
+  marginal hidden): bit for bit equal to the same kernels called once per request;
+* whole batched drafts -- 32 chains, 3 trees, 4 two-pass chains -- against the oracle's search on the
+  same predicted hiddens, request by request (ids equal unless a decision was within 1e-3 of a tie).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import to64
+from chain_flow_amd.config import flownet
+from chain_flow_amd.drafter import Drafter
+from chain_flow_amd.head import ShortlistHead
+from chain_flow_amd.weights import make_weights, synthetic_context
+from oracle import beam as obeam
+from oracle import head as ohead
+
+
+def _setup(d=512, V=4096, n=1024, seed=7):
+    cfg = flownet(d, layers=1, flow_steps=2)
+    W = make_weights(cfg, V, init="test", base_seed=seed)
+    W["lm_head.weight"] = (W["lm_head.weight"].float() * 8).half()
+    sl = torch.randperm(V, generator=torch.Generator().manual_seed(3))[:n].sort().values.to(torch.int32)
+    return cfg, W, sl
+
+
+def _bound(h64, w64, ref):
+    ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+    return 2 * ulp + 2.0 ** -20 * (np.abs(h64) @ np.abs(w64).T)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,n,markov", [(9, 1024, True), (40, 1000, False), (160, 1024, True), (256, 777, True)])
+def test_gemm16_head_matches_oracle(cuda, M, n, markov):
+    cfg, W, _ = _setup(n=n)
+    V = W["lm_head.weight"].shape[0]
+    sl = torch.randperm(V, generator=torch.Generator().manual_seed(M))[:n].sort().values.to(torch.int32)
+    head = ShortlistHead(W["lm_head.weight"].to(cuda), sl.to(cuda), W["markov.w1.weight"].to(cuda),
+                         W["markov.w2.weight"].to(cuda))
+    g = torch.Generator().manual_seed(M + 1)
+    h = (torch.randn(M, 512, generator=g) * 0.5).half()
+    prev = torch.randint(0, V, (M,), generator=g, dtype=torch.int32)
+    k = 8
+    logits = torch.empty(M, n, dtype=torch.float16, device=cuda)
+    print(f"[gemm16] M={M} n={n} markov={markov}", flush=True)
+    vals, ids, lse = head.topk(h.to(cuda), k, prev=prev.to(cuda) if markov else None, logits=logits)
+    torch.cuda.synchronize()
+    s64 = sl.long().numpy()
+    h64, w64 = to64(h), to64(W["lm_head.weight"])[s64]
+    hw = ohead.head_logits(h64, w64)
+    if markov:
+        mb = ohead.markov_bias(to64(W["markov.w1.weight"]), to64(W["markov.w2.weight"])[s64], prev.long().numpy())
+        ref = ohead.r16(hw + mb, "fp16")
+        bound = _bound(h64, w64, hw) + np.spacing(np.abs(mb).astype(np.float16)) + \
+            np.spacing(np.abs(ref).astype(np.float16))
+    else:
+        ref = hw
+        bound = _bound(h64, w64, hw)
+    got = to64(logits)
+    assert (np.abs(got - ref) <= bound).all()
+    lsm = ohead.log_softmax(ref)
+    _, want = ohead.topk(lsm, k)
+    ok = ohead.margins(lsm, k) > 1e-3
+    assert (ids.cpu().numpy()[ok] == want[ok]).all()
+    # the kernel's own log-softmax of its own logits, exactly as the GEMV head computes it
+    gl = got.astype(np.float64)
+    m = gl.max(1)
+    want_lse = m + np.log(np.exp(gl - m[:, None]).sum(1))
+    assert np.allclose(lse.cpu().numpy(), want_lse, atol=1e-5, rtol=0)
+    assert np.allclose(vals.cpu().numpy(), np.take_along_axis(gl, ids.cpu().long().numpy(), 1) - want_lse[:, None],
+                       atol=1e-5, rtol=0)
+
+
+@pytest.mark.gpu
+def test_grouped_head_and_batched_path_equal_per_request_calls(cuda):
+    cfg, W, sl = _setup()
+    dr = Drafter(cfg, {k: v.to(cuda) for k, v in W.items()}, sl.to(cuda), device=cuda)
+    B, F, Mc, d = 5, 4, 300, 512
+    g = torch.Generator().manual_seed(5)
+    rows = (torch.randn(B * F, d, generator=g) * 0.5).half().to(cuda)
+    cand = torch.stack([torch.randperm(4096, generator=g)[:Mc].sort().values for _ in range(B)]).to(torch.int32)
+    cand = cand.to(cuda)
+    lastp = torch.randint(0, 4096, (B * F, 4), generator=g, dtype=torch.int32)
+    lastp[1, 2:] = -1
+    lastp = lastp.to(cuda)
+    print("[grouped head / batched path]", flush=True)
+    v, i, l = dr.head.topk_groups(rows, 6, cand, prev=lastp.view(-1), prev_stride=4)
+    pred = (torch.randn(B, 8, d, generator=g) * 0.5).half().to(cuda)
+    hb = dr.path.hidden(lastp, 3, pred[:, 2])
+    torch.cuda.synchronize()
+    for b in range(B):
+        rv, ri, rl = dr.head.topk_rows(rows[b * F:(b + 1) * F], 6, cand[b].contiguous(),
+                                       prev=lastp[b * F:(b + 1) * F].contiguous().view(-1), prev_stride=4)
+        hr = dr.path.hidden(lastp[b * F:(b + 1) * F].contiguous(), 3, pred[b, 2].contiguous())
+        torch.cuda.synchronize()
+        assert torch.equal(v[b * F:(b + 1) * F], rv) and torch.equal(i[b * F:(b + 1) * F], ri), b
+        assert torch.equal(l[b * F:(b + 1) * F], rl), b
+        assert torch.equal(hb[b * F:(b + 1) * F], hr), b
+
+
+def _oracle(W, sl, cfg):
+    W64 = {k: to64(v) for k, v in W.items()}
+    s64 = sl.long().numpy()
+
+    def score(h, prev):
+        if prev is None:
+            return ohead.head_logits(h, W64["lm_head.weight"][s64])
+        return ohead.head_with_bias(h, W64["lm_head.weight"][s64], W64["markov.w1.weight"],
+                                    W64["markov.w2.weight"][s64], prev)
+
+    resid = lambda lp, nl: ohead.path_residual(W64, W64["embed_tokens.weight"], lp, nl, cfg.path_order)
+    return s64, score, resid
+
+
+def _near(trace, k1, k2):
+    return any((ohead.margins(t["lp"], k1) <= 1e-3).any() or (ohead.margins(t["cand"], k2) <= 1e-3).any()
+               for t in trace)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("search,B,twopass", [("chain", 32, 0), ("tree", 3, 0), ("chain", 4, 256), ("tree", 4, 256)])
+def test_batched_drafts_match_oracle(cuda, search, B, twopass):
+    cfg, W, sl = _setup()
+    dr = Drafter(cfg, {k: v.to(cuda) for k, v in W.items()}, sl.to(cuda), device=cuda, twopass_m=twopass,
+                 twopass_shared=True)
+    ctx = synthetic_context(B, cfg.context_size, 512, seed=9)
+    known0 = sl[torch.randperm(len(sl), generator=torch.Generator().manual_seed(B))[:B]].long()
+    print(f"[batched {search}] B={B} twopass={twopass}", flush=True)
+    pred = dr.predict_hidden(ctx.to(cuda))
+    if search == "chain":
+        got = dr.beam_chains(None, known0.to(cuda), 5, 4, pred=pred).cpu().numpy()
+    else:
+        got = dr.beam_tree(None, known0.to(cuda), keep=4, topb=8, depth=4, pred=pred).cpu().numpy()
+    torch.cuda.synchronize()
+    s64, score, resid = _oracle(W, sl, cfg)
+    pr = to64(pred)
+    bad = 0
+    for b in range(B):
+        if search == "chain":
+            ref, tr = obeam.beam_chains(pr[b:b + 1], known0[b:b + 1].numpy(), s64, 4, 5, cfg.path_order, score,
+                                        resid, return_trace=True, twopass_m=twopass, shared=True)
+            k1, k2 = 4, 4
+        else:
+            ref, tr = obeam.beam_tree(pr[b:b + 1], known0[b:b + 1].numpy(), s64, 4, 8, 4, cfg.path_order, score,
+                                      resid, return_trace=True, twopass_m=twopass, shared=True)
+            k1, k2 = 8, 4
+        if got[b].tolist() != ref[0].tolist():
+            print(f"  b={b} gpu {got[b].tolist()} oracle {ref[0].tolist()}", flush=True)
+            assert _near(tr, k1, k2), b
+            bad += 1
+    print(f"  {B - bad}/{B} requests equal to the oracle, the rest at near ties", flush=True)

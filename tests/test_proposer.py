@@ -56,6 +56,31 @@ def test_chain_mode_widths(monkeypatch, ckpt):
     assert (p.K, p.draft_width, p.width, p.branching) == (5, 5, 3, False)
 
 
+@pytest.mark.parametrize("env,match", [
+    (dict(CF_WIDTH=9), "CF_WIDTH=9 is not supported"),
+    (dict(CF_WIDTH=0), "CF_WIDTH=0 is not supported"),
+    (dict(VLLM_SPEC_TREE=1, CF_TREE_KEEP=9, CF_TREE_TOPB=9, CF_TREE_DEPTH=2), "CF_TREE_KEEP=9 x CF_TREE_TOPB=9"),
+])
+def test_beam_limits_are_refused_with_a_message(monkeypatch, ckpt, env, match):
+    """A beam wider than the kernels rank (width*width or keep*topb above 64) is refused at
+    construction, not by a failing launch (or a runaway recursion) at the first draft."""
+    _env(monkeypatch, CF_DRAFTER_DIR=ckpt[0], **env)
+    k = 2 * int(env.get("CF_TREE_KEEP", 0)) + 1 if "VLLM_SPEC_TREE" in env else 5
+    with pytest.raises(ValueError, match=match):
+        fp.FlowDrafterProposer(_vcfg(k=k))
+
+
+def test_drafter_refuses_unsupported_beams():
+    """Drafter.beam_chains / beam_tree check the same limits before any launch."""
+    from chain_flow_amd.drafter import Drafter
+    dr = Drafter.__new__(Drafter)
+    dr.device, dr.order = torch.device("cpu"), 4
+    with pytest.raises(ValueError, match="beam width 9"):
+        dr.beam_chains(None, torch.zeros(1), 5, width=9, pred=torch.zeros(1, 8, 16))
+    with pytest.raises(ValueError, match="keep 16 x top-b 8"):
+        dr.beam_tree(None, torch.zeros(1), keep=16, topb=8, depth=2, pred=torch.zeros(1, 8, 16))
+
+
 def test_tree_mode_sizes_and_checks(monkeypatch, ckpt):
     _env(monkeypatch, CF_DRAFTER_DIR=ckpt[0], VLLM_SPEC_TREE=1, CF_TREE_KEEP=4, CF_TREE_TOPB=8, CF_TREE_DEPTH=5)
     p = fp.FlowDrafterProposer(_vcfg(k=21))

@@ -4,6 +4,7 @@
     python bench.py --workload latent        # the shipped 4B latent drafter (see below)
     python bench.py --workload verify        # the tree-verify kernels at the tree-draft shapes
     python bench.py --workload gemm          # the batched head: 32 seqs x 5 depths, d=4096 bf16
+    python bench.py --workload batched       # 32 whole chain drafts at d=4096 (flow, pass A, beams)
 
 A step is one whole FlowDrafterProposer chain draft over inputs already resident in HBM:
 ``predict_hidden`` (init_latents + 8 Euler steps of both chunk experts, every block) followed by the
@@ -512,12 +513,72 @@ def gemm_bench(dev, iters=100, warmup=10):
     return times, nbytes, flops, (M, d, n, k)
 
 
+def batched_bench(dev, steps=3, warmup=1, B=32, d=4096, L=8, E=8, M=8192):
+    """The batched drafting step: B requests, each a 5-token width-4 chain at d=4096 fp16 with the
+    proposer's default two-pass head (M=8192 candidates shared across depths).  The flow drafts the
+    requests two to a weight stream; pass A scores the B*5 marginal hiddens in one fp16 MFMA GEMM
+    over the 62,642-row shortlist (M=160 rows at B=32); each depth's B*4 beams run through the
+    batched path residual and the grouped pass-B head.  Returns timings (ms, events on the stream)
+    and byte counts."""
+    import torch
+    from chain_flow_amd.config import flownet
+    from chain_flow_amd.drafter import Drafter
+    from chain_flow_amd.flow import caps
+    from chain_flow_amd.shortlist import synthetic
+    from chain_flow_amd.weights import make_weights, synthetic_context
+    K, Wd = 5, 4
+    cfg = flownet(d, layers=L, flow_steps=E)
+    W = make_weights(cfg, VOCAB, init="baseline", dtype=torch.float16, device=dev, base_seed=0, hidden=d)
+    sl = synthetic(VOCAB, SHORTLIST_ROWS, seed=2)
+    dr = Drafter(cfg, W, sl.to(dev), device=dev, twopass_m=M, twopass_shared=True)
+    del W
+    ctx = synthetic_context(B, cfg.context_size, d, seed=1).to(dev)
+    known0 = sl[torch.randperm(SHORTLIST_ROWS, generator=torch.Generator().manual_seed(3))[:B]].long().to(dev)
+
+    def step():
+        pred = dr.predict_hidden(ctx)
+        return pred, dr.beam_chains(None, known0, K, Wd, pred=pred)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    for i in range(steps):
+        ev[i][0].record()
+        pred = dr.predict_hidden(ctx)
+        ev[i][1].record()
+        dr.beam_chains(None, known0, K, Wd, pred=pred)
+        ev[i][2].record()
+    torch.cuda.synchronize()
+    med = lambda v: sorted(v)[len(v) // 2]
+    flow_ms = med([a.elapsed_time(b) for a, b, _ in ev])
+    head_ms = med([b.elapsed_time(c) for _, b, c in ev])
+    # pass A alone: the B*5 marginal hiddens through the fp16 GEMM head (the batched head of C4)
+    hm = pred[:, 1:K + 1].contiguous()
+    for _ in range(3):
+        dr.head.candidates(hm, M, True)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n_a = 20
+    e0.record()
+    for _ in range(n_a):
+        dr.head.candidates(hm, M, True)
+    e1.record()
+    torch.cuda.synchronize()
+    pass_a_ms = e0.elapsed_time(e1) / n_a
+    groups = (B + 1) // 2 if caps(cfg, 2) != caps(cfg, 1) else B
+    fb = groups * flow_bytes(d, L, E, cfg.num_chunks, fold=(d // cfg.num_heads) % 32 == 0)
+    return dict(flow_ms=flow_ms, head_ms=head_ms, pass_a_ms=pass_a_ms, flow_bytes=fb, groups=groups,
+                pass_a_bytes=SHORTLIST_ROWS * d * 2 + B * K * d * 2 + B * K * SHORTLIST_ROWS * 2,
+                B=B, d=d, L=L, E=E, M=M, K=K, W=Wd)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["target", "latent", "verify", "gemm"], default="target",
+    ap.add_argument("--workload", choices=["target", "latent", "verify", "gemm", "batched"], default="target",
                     help="target: the flow at the target width d (default); latent: the shipped 4B "
                          "latent drafter (hidden 2560, VAE latent 640, 8 blocks, 2 Euler steps)")
     ap.add_argument("--d", type=int, default=None, help="target hidden size (5120; latent: 2560)")
@@ -563,6 +624,30 @@ def main():
         }
         if args.calib_copy:
             calib_copy(dev)
+        print(json.dumps(out), flush=True)
+        return
+    if args.workload == "batched":
+        r = batched_bench(dev)
+        ms = r["flow_ms"] + r["head_ms"]
+        gbs = r["flow_bytes"] / (r["flow_ms"] * 1e-3) / 1e9
+        out = {
+            "metric": f"us per batched draft step ({r['B']} seqs x {r['K']} tokens, d={r['d']} fp16, two-pass head)",
+            "value": round(ms * 1e3, 1), "unit": "us per batched draft step", "n_gpus": 1, "steps": 3, "warmup": 1,
+            "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+            "dtype": "fp16", "data": "synthetic (seeded N(0,0.02) weights, N(0,1) RMS-1 contexts)",
+            "config": {"workload": f"batched chain draft: {r['B']} requests x {r['K']} tokens, width {r['W']}, "
+                                   f"d={r['d']} fp16, flow L={r['L']} E={r['E']} (requests drafted two to a weight "
+                                   f"stream: {r['groups']} groups), two-pass head M={r['M']} shared over a "
+                                   f"{SHORTLIST_ROWS}-row shortlist"},
+            "breakdown_ms": {"flow": round(r["flow_ms"], 3), "head_beam": round(r["head_ms"], 3),
+                             "pass_a_gemm": round(r["pass_a_ms"], 4)},
+            "per_request_us": round(ms * 1e3 / r["B"], 1),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                         "kernel": "flow pass (cfh_flow_integrate, request groups)", "algorithmic_bytes": r["flow_bytes"]},
+            "pass_a": {"rows": r["B"] * r["K"], "us": round(r["pass_a_ms"] * 1e3, 2),
+                       "gbs": round(r["pass_a_bytes"] / (r["pass_a_ms"] * 1e-3) / 1e9, 1)},
+        }
         print(json.dumps(out), flush=True)
         return
     if args.workload == "verify":

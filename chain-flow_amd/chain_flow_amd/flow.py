@@ -1,5 +1,8 @@
 """Host side of the fused flow: weight packing and ``predict_hidden`` through libcfhip.
 
+A batch is drafted in groups of requests whose rows share each weight stream (two 8-row drafts per
+16-row MFMA tile where the shape allows), so a batch of B costs about B/2 single drafts.
+
 Mirrors the reference's boundary ``cuda_block.FusedExpertBlocks`` (``cf/cuda_block.py:269-431``):
 the caller owns packed weights and a workspace that persist across drafts; one call runs the
 whole ``TreeFlowDrafter.predict_hidden`` (``cf/drafters/tree_flow.py:229-244``) -- init_latents
@@ -101,6 +104,12 @@ class FusedFlow:
         B = ctx.shape[0]
         if out is None:
             out = torch.empty(B, cfg.draft_length, d, dtype=torch.float16, device=self.device)
+        # a batch runs in groups of requests packed into one tile: its workspace grows with the group
+        need = caps(cfg, B)
+        if need is None:
+            raise ValueError(f"flow shape not supported by libcfhip at batch {B}: {cfg}")
+        if need > self.ws.numel():
+            self.ws = torch.empty(need, dtype=torch.uint8, device=self.device)
         self.dims.numerics = reference_numerics(cfg, B) if numerics is None else int(numerics)
         _lib.check(_lib.lib().cfh_flow_integrate(C.byref(self.dims), self._experts, ctx.data_ptr(),
                                                  out.data_ptr(), self.ws.data_ptr(), B,

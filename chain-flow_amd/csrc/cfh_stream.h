@@ -31,6 +31,7 @@ struct SEx {
   const h16* bias;     // E_BIAS16 / E_GELU16 bias [N]
   void* out;           // E_PART: float [ks][S][N]; E_PART16: h16 [ks][S][N]; otherwise h16 [S][N]
   int S;               // activation rows (<= 16)
+  int Sr;              // S_SELF / S_CROSS: rows per request (requests packed in the S rows; 0 = S)
 };
 
 // For the attention kinds a k-chunk of KC = K / ks columns holds KC / hd whole heads (one head
@@ -39,6 +40,7 @@ struct SArgs {
   SEx ex[4];
   int nex, N, K, ks, wpb, tpw, wg_per_kc;
   int d, hd, ks_in, Ck;
+  int Cr;              // S_CROSS: context rows per request (the Ck rows hold Ck / Cr requests; 0 = Ck)
   int sync;            // fragment groups between workgroup barriers in the stream (0: none)
   int causal;          // S_SELF: causal mask triu(-inf, 1) (the flow's draft rows) or none
   int gelu_r16;        // E_GELU16: round acc + bias to fp16 before the GELU (a Linear module
@@ -48,12 +50,14 @@ struct SArgs {
 // Attention of the KC / hd heads of a k-chunk for the S rows of one expert from q, k, v already in
 // LDS (sq [S][KC], sk and sv [Sk][KC], Sk <= 16; head hh in columns [hh hd, hh hd + hd)), written
 // as fp16 into As [S][lda].  Causal mask = triu(-inf, 1) (cf/drafters/chunked_flow.py:273-275);
-// scores and the weighted sum in fp32 on fp16 q/k/v, output rounded to fp16.
+// scores and the weighted sum in fp32 on fp16 q/k/v, output rounded to fp16.  Rows of several
+// requests may share the tile: query row i belongs to request i / Sr and key j to request j / Cr,
+// and a query attends only to its own request's keys (one request: Sr = S, Cr = Sk).
 // One wave per (head, query row): lane group j (LP lanes) holds key j, so the dot products, the
 // row max, exp and sum stay in registers (DPP reductions); every LDS read of a phase is issued
 // before the first is used.  (A wave per (i, j) pair with a serial softmax thread per row spent
 // 2-4 us here, almost all of it in dependent LDS round trips.)
-__device__ void attend(int S, int Sk, int hd, int KC, bool causal, const h16* sq, const h16* sk,
+__device__ void attend(int S, int Sk, int Sr, int Cr, int hd, int KC, bool causal, const h16* sq, const h16* sk,
                        const h16* sv, float* P, h16* As, int lda) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
   const int hpk = KC / hd;
@@ -76,7 +80,7 @@ __device__ void attend(int S, int Sk, int hd, int KC, bool causal, const h16* sq
     part += dpp_f32<DPP_XOR1>(part);
     part += dpp_f32<DPP_XOR2>(part);
     if (l8) part += dpp_f32<DPP_HMIRROR>(part);
-    const bool valid = j < Sk && !(causal && j > i);
+    const bool valid = j < Sk && j / Cr == i / Sr && !(causal && j > i);
     const float sc = valid ? part * scale : -INFINITY;
     const float m = wave_max(sc);
     const float e = valid ? expf(sc - m) : 0.f;
@@ -238,7 +242,9 @@ struct Stage {
           if (jj < gj && t + jj * nt < G) put_q(t + jj * nt, qs[jj], qb[jj]);
       }
       lds_barrier();
-      attend(S, Sk, a.hd, KC, SRC == S_SELF && a.causal, sq, sk, sv, P, As, lda);
+      const int Sr = ex.Sr > 0 ? ex.Sr : S;
+      const int Cr = SRC == S_SELF ? Sr : (a.Cr > 0 ? a.Cr : Sk);
+      attend(S, Sk, Sr, Cr, a.hd, KC, SRC == S_SELF && a.causal, sq, sk, sv, P, As, lda);
       lds_barrier();
     }
   }

@@ -10,9 +10,11 @@
 // torch's fp16 modules' (x = fp16(x + fp16(sublayer)); GELU of the fp16-rounded up-projection), as
 // cfh_flow_dims.numerics says; only the residual row kernel and the W1 epilogue differ.
 //
-// Execution plan.  One launch sequence per draft on the caller's stream; every launch covers both
-// chunk experts (they are independent within an Euler step), so each weight-streaming launch moves
-// the weights of two experts.  Work that needs a whole row sits in a small row kernel between two
+// Execution plan.  One launch sequence per group of requests on the caller's stream; every launch
+// covers both chunk experts (they are independent within an Euler step), so each weight-streaming
+// launch moves the weights of two experts.  A batch is drafted in groups of R requests whose rows
+// share one MFMA tile (R x draft_length <= 16: two 8-row drafts), so every weight stream serves R
+// drafts; attention masks keep each request to its own rows and context.  Work that needs a whole row sits in a small row kernel between two
 // streaming kernels; there is no cross-workgroup synchronisation inside any kernel (no fences, no
 // atomics, no spin-waits), so results are deterministic.  On MI355X a kernel boundary costs about
 // nothing on the stream, while a fenced grid barrier across the 8 XCDs costs ~12 us, which is why
@@ -58,10 +60,10 @@ namespace {
 // then, unless this was the last step, the next step's rows: for every expert c2 that reads z row
 // r: x = fp16(fp16(z + pos[r]) + [current rows] tau), residual x = that, a = LN_self of block 0.
 struct RowsArgs {
-  const h16* ctx;
-  float* ctx_mom;      // init: [C][2] (mean, rstd) of the fp16 context rows
-  float* z;
-  h16* z_out;
+  const h16* ctx;      // [R][C][d] context rows of the group's requests
+  float* ctx_mom;      // init: [R C][2] (mean, rstd) of the fp16 context rows
+  float* z;            // [R][KD][d]
+  h16* z_out;          // [R][KD][d]
   const float* Pout[4];
   const h16* bout[4];
   float* x[4];
@@ -71,16 +73,19 @@ struct RowsArgs {
   const h16* b[4];
   h16* a[4];
   float dt;
-  int euler, last, ks, d, C, CS, nch;
+  int euler, last, ks, d, C, CS, nch, KD;
+  int R;               // requests in the group (row r of the grid: request r / KD, draft row r % KD)
+  int out_all;         // the OUT launch covered every row of each expert (R > 1), not just the current chunk's
 };
 
 __global__ void __launch_bounds__(ROWT) k_rows(RowsArgs a) {
   __shared__ float red[ROWT / 64];
   const int r = blockIdx.x, d = a.d, nq = d / 4;
+  const int req = r / a.KD, rr = r - req * a.KD;
   float4 zv[ROWQ];
   if (!a.euler) {
     // moments of context rows r, r + gridDim.x, ... (read by the cross K/V GEMV)
-    for (int cr = r; cr < a.C; cr += gridDim.x) {
+    for (int cr = r; cr < a.R * a.C; cr += gridDim.x) {
       const h16* row = a.ctx + (size_t)cr * d;
       float sm = 0.f;
       for (int c = threadIdx.x; c < d; c += blockDim.x) sm += (float)row[c];
@@ -96,9 +101,9 @@ __global__ void __launch_bounds__(ROWT) k_rows(RowsArgs a) {
         a.ctx_mom[2 * cr + 1] = rs;
       }
     }
-    const h16* last = a.ctx + (size_t)(a.C - 1) * d;
-    const h16* prev = a.ctx + (size_t)(a.C - 2) * d;
-    const float step = (float)(r + 1);
+    const h16* last = a.ctx + (size_t)(req * a.C + a.C - 1) * d;
+    const h16* prev = a.ctx + (size_t)(req * a.C + a.C - 2) * d;
+    const float step = (float)(rr + 1);
 #pragma unroll
     for (int k = 0; k < ROWQ; ++k) {
       const int q = threadIdx.x + k * blockDim.x;
@@ -116,9 +121,10 @@ __global__ void __launch_bounds__(ROWT) k_rows(RowsArgs a) {
       }
     }
   } else {
-    const int c = r / a.CS, i = r - c * a.CS;
-    const size_t pst = (size_t)a.CS * d;
-    const float* Pr = a.Pout[c] + (size_t)i * d;
+    const int c = rr / a.CS, i = rr - c * a.CS;
+    const int Sc = (c + 1) * a.CS;
+    const size_t pst = (size_t)(a.out_all ? a.R * Sc : a.CS) * d;
+    const float* Pr = a.Pout[c] + (size_t)(a.out_all ? req * Sc + c * a.CS + i : i) * d;
     float4 acc[ROWQ], zo[ROWQ];
 #pragma unroll
     for (int k = 0; k < ROWQ; ++k) {
@@ -166,15 +172,16 @@ __global__ void __launch_bounds__(ROWT) k_rows(RowsArgs a) {
   }
   if (a.last) return;
   for (int c2 = 0; c2 < a.nch; ++c2) {
-    if (r >= (c2 + 1) * a.CS) continue;          // expert c2 reads z rows [0, (c2+1)*CS)
-    const bool cur = r >= c2 * a.CS;
+    if (rr >= (c2 + 1) * a.CS) continue;         // expert c2 reads z rows [0, (c2+1)*CS) of each draft
+    const bool cur = rr >= c2 * a.CS;
+    const size_t xr = (size_t)req * (c2 + 1) * a.CS + rr;   // the row in expert c2's request-major rows
     float4 vals[ROWQ];
 #pragma unroll
     for (int k = 0; k < ROWQ; ++k) {
       const int q = threadIdx.x + k * blockDim.x;
       vals[k] = make_float4(0.f, 0.f, 0.f, 0.f);
       if (q < nq) {
-        const h16* pp = a.pos[c2] + (size_t)r * d + q * 4;
+        const h16* pp = a.pos[c2] + (size_t)rr * d + q * 4;
         const h16* tt = a.tau[c2] + q * 4;
         float o[4] = {zv[k].x, zv[k].y, zv[k].z, zv[k].w};
 #pragma unroll
@@ -184,10 +191,10 @@ __global__ void __launch_bounds__(ROWT) k_rows(RowsArgs a) {
           o[t] = xv;
         }
         vals[k] = make_float4(o[0], o[1], o[2], o[3]);
-        *(float4*)(a.x[c2] + (size_t)r * d + q * 4) = vals[k];
+        *(float4*)(a.x[c2] + xr * d + q * 4) = vals[k];
       }
     }
-    ln_row4(vals, d, a.g[c2], a.b[c2], a.a[c2] + (size_t)r * d, red);
+    ln_row4(vals, d, a.g[c2], a.b[c2], a.a[c2] + xr * d, red);
   }
 }
 
@@ -209,7 +216,9 @@ struct XattArgs {
   const float* sb[4];    // this layer's sb [H][C]
   float* out[4];         // partials [H][S][d]
   int S[4];
-  int nex, d, H, C, nb;
+  int Sr[4];             // rows per request (the S rows hold S / Sr requests)
+  int nex, d, H, C, nb;  // C: context rows of all the group's requests
+  int Cq;                // context rows per request: row r scores only its request's rows
   float scale;
 };
 
@@ -262,7 +271,7 @@ __global__ void __launch_bounds__(XT) k_xattn(XattArgs a) {
     float v = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) v += red[w][t];
-    if (r < S) P[r][c] = c < C ? (v + a.sb[e][h * C + c]) * a.scale : -INFINITY;
+    if (r < S) P[r][c] = c < C && c / a.Cq == r / a.Sr[e] ? (v + a.sb[e][h * C + c]) * a.scale : -INFINITY;
   }
   __syncthreads();
   // softmax over the C context rows, one thread per row
@@ -272,7 +281,7 @@ __global__ void __launch_bounds__(XT) k_xattn(XattArgs a) {
     float z[16], sum = 0.f;
 #pragma unroll
     for (int c = 0; c < 16; ++c) {
-      z[c] = c < C ? expf(P[t][c] - m) : 0.f;
+      z[c] = c < C && P[t][c] != -INFINITY ? expf(P[t][c] - m) : 0.f;
       sum += z[c];
     }
     const float inv = 1.0f / sum;
@@ -346,6 +355,7 @@ int launch_xattn(const XattArgs& a, hipStream_t st) {
 
 struct Plan {
   int d, fd, CS, E, NL, C, KD, H, hd, nch, Smax;
+  int R, Ct;          // requests per group (rows packed in one tile) and their context rows R C
   int ks_att;         // k-chunks of the attention launches: H / heads per chunk
   int ks_qc, ks_w2, ks_out, ks_kv, ks_tau;
   int wpb_qc, wpb_w2, wpb_out, tpw_att, wpb_att, wpb_full, wpb_w1;
@@ -356,13 +366,16 @@ struct Plan {
   bool ok;
 };
 
-Plan make_plan(const cfh_flow_dims* dm) {
+Plan make_plan(const cfh_flow_dims* dm, int R = 1) {
   Plan p = {};
   p.d = dm->d; p.fd = dm->ffn_mult * dm->d; p.CS = dm->chunk_size; p.E = dm->flow_steps;
   p.NL = dm->layers; p.C = dm->ctx_rows; p.KD = dm->draft_length; p.H = dm->heads; p.hd = p.d / p.H;
   p.ks_att = cfh::heads_per_chunk(p.hd, p.H) ? p.H / cfh::heads_per_chunk(p.hd, p.H) : 0;
   p.nch = p.KD / p.CS;
-  p.Smax = p.KD;
+  p.R = R;
+  p.Ct = R * p.C;
+  p.Smax = R * p.KD;
+  const int out_rows = R == 1 ? p.CS : p.Smax;   // OUT: the current chunk's rows, or every row when packed
   p.res_mode = dm->numerics == CFH_FLOW_MODULES ? RES_ADD16 : RES_ADD32;
   p.fold = cfh::xattn_fold(dm);
   const int tiles_d = p.d / 16;
@@ -373,12 +386,12 @@ Plan make_plan(const cfh_flow_dims* dm) {
   // both run as one round of ~240 workgroups at one workgroup per CU; else split-K by wave count
   const bool w2_wide = tiles_d % 16 == 0 && stream_lds(S_BUF, p.Smax, p.d, p.hd, p.C) <= 150 * 1024;
   p.ks_w2 = w2_wide ? dm->ffn_mult : std::max(choose_ks(p.nch, tiles_d, p.fd, p.Smax, 4096, cap), 1);
-  p.ks_out = std::max(choose_ks(p.nch, tiles_d, p.d, p.CS, 2048, cap), 1);
-  p.ks_kv = ksplit_for(p.nch * p.NL, 2 * p.d / 16, p.d, p.C);
+  p.ks_out = std::max(choose_ks(p.nch, tiles_d, p.d, out_rows, 2048, cap), 1);
+  p.ks_kv = ksplit_for(p.nch * p.NL, 2 * p.d / 16, p.d, p.Ct);
   p.ks_tau = ksplit_for(p.nch, p.d / 16, p.d, p.E);
   p.wpb_w2 = w2_wide ? wpb_for_grid(tiles_d, p.nch * p.ks_w2, 16, p.Smax * (p.fd / p.ks_w2) / 8)
                      : std::min(4, pick_wpb(tiles_d, 1));
-  p.wpb_out = wpb_for_grid(tiles_d, p.nch * p.ks_out, 8, p.CS * (p.d / p.ks_out) / 8);
+  p.wpb_out = wpb_for_grid(tiles_d, p.nch * p.ks_out, 8, out_rows * (p.d / p.ks_out) / 8);
   p.tpw_att = (tiles_d % 16 == 0) ? 2 : 1;
   p.wpb_att = pick_wpb(tiles_d, p.tpw_att);   // (the attention staging needs the waves' slots)
   fit_grid(tiles_d, p.nch * p.ks_att, &p.wpb_att, &p.tpw_att);
@@ -389,7 +402,7 @@ Plan make_plan(const cfh_flow_dims* dm) {
   // the cross attention holds every q partial of its groups in registers: fewer QC splits if needed
   for (int ks = p.ks_qc; ks > 1; --ks) {
     SArgs a = {};
-    a.N = p.d; a.K = p.d; a.ks = p.ks_att; a.wpb = p.wpb_att; a.tpw = p.tpw_att; a.hd = p.hd; a.ks_in = ks; a.Ck = p.C;
+    a.N = p.d; a.K = p.d; a.ks = p.ks_att; a.wpb = p.wpb_att; a.tpw = p.tpw_att; a.hd = p.hd; a.ks_in = ks; a.Ck = p.Ct;
     if ((p.d / 32) % ks || stage_need(S_CROSS, a, p.Smax) > stage_slots(a.wpb)) continue;
     p.ks_qc = ks;
     break;
@@ -399,27 +412,36 @@ Plan make_plan(const cfh_flow_dims* dm) {
   fit_grid(tiles_d, p.nch * p.ks_out, &p.wpb_out, nullptr);
   p.pks = std::max(std::max(p.ks_att, p.ks_w2), p.ks_out);
   if (p.fold) {
-    p.wpb_fold = wpb_for_grid(tiles_d, 2 * p.nch * p.H, 8, p.C * p.hd / 8);
+    p.wpb_fold = wpb_for_grid(tiles_d, 2 * p.nch * p.H, 8, p.Ct * p.hd / 8);
     p.xnb = xattn_blocks(p.d, p.nch * p.H);
   }
-  p.ok = p.ks_qc > 0 && p.ks_qc <= 8 && p.ks_w2 > 0 && p.ks_out > 0 && p.ks_att > 0 && res_nq(p.d) > 0;
+  p.ok = p.ks_qc > 0 && p.ks_qc <= 8 && p.ks_w2 > 0 && p.ks_out > 0 && p.ks_att > 0 && res_nq(p.d) > 0 &&
+         p.Smax <= MAXR && p.Ct <= 16;
   if (!p.ok) return p;
   // every streaming launch of a draft, as block_pass and the OUT step issue them
   auto sa = [&](int N, int K, int ks, int wpb, int tpw) {
     SArgs a = {};
     a.nex = p.nch; a.N = N; a.K = K; a.ks = ks; a.wpb = wpb; a.tpw = tpw; a.d = p.d; a.hd = p.hd;
-    a.ks_in = p.ks_qc; a.Ck = p.C;
+    a.ks_in = p.ks_qc; a.Ck = p.Ct;
     return a;
   };
-  const bool cross_ok = p.fold ? !stream_check(S_BUF, sa(p.d, p.d, p.H, p.wpb_fold, 1), p.C) && p.xnb > 0
+  const bool cross_ok = p.fold ? !stream_check(S_BUF, sa(p.d, p.d, p.H, p.wpb_fold, 1), p.Ct) && p.xnb > 0
                               : !stream_check(S_BUF, sa(p.d, p.d, p.ks_qc, p.wpb_qc, 1), p.Smax) &&
                                     !stream_check(S_CROSS, sa(p.d, p.d, p.ks_att, p.wpb_att, p.tpw_att), p.Smax);
   p.ok = !stream_check(S_BUF, sa(3 * p.d, p.d, 1, p.wpb_full, 1), p.Smax) &&
          !stream_check(S_SELF, sa(p.d, p.d, p.ks_att, p.wpb_att, p.tpw_att), p.Smax) && cross_ok &&
          !stream_check(S_BUF, sa(p.fd, p.d, 1, p.wpb_w1, 1), p.Smax) &&
          !stream_check(S_BUF, sa(p.d, p.fd, p.ks_w2, p.wpb_w2, 1), p.Smax) &&
-         !stream_check(S_BUF, sa(p.d, p.d, p.ks_out, p.wpb_out, 1), p.CS);
+         !stream_check(S_BUF, sa(p.d, p.d, p.ks_out, p.wpb_out, 1), out_rows);
   return p;
+}
+
+// Requests per group for a batch: the most (up to `batch`) whose rows fit one tile and whose plan
+// this build runs; 1 always works when the shape is supported.
+int group_size(const cfh_flow_dims* dm, int batch) {
+  for (int R = std::min(batch, MAXR / dm->draft_length); R > 1; --R)
+    if (make_plan(dm, R).ok) return R;
+  return 1;
 }
 
 struct WS {
@@ -450,9 +472,9 @@ WS carve(const Plan& p, char* base) {
     return q;
   };
   const size_t d = p.d, fd = p.fd;
-  w.z = (float*)take((size_t)p.KD * d * 4);
+  w.z = (float*)take((size_t)p.R * p.KD * d * 4);
   for (int c = 0; c < p.nch; ++c) {
-    const size_t S = (size_t)(c + 1) * p.CS;
+    const size_t S = (size_t)p.R * (c + 1) * p.CS;
     w.x[c] = (float*)take(S * d * 4);
     w.abuf[c] = (h16*)take(S * d * 2);
     w.qkv[c] = (h16*)take(S * 3 * d * 2);
@@ -460,27 +482,28 @@ WS carve(const Plan& p, char* base) {
     w.P[c] = (float*)take((size_t)p.pks * S * d * 4);
     if (!p.fold) w.Pq[c] = (float*)take((size_t)p.ks_qc * S * d * 4);
     w.tau[c] = (h16*)take((size_t)p.E * d * 2);
-    w.kvc[c] = (h16*)take((size_t)p.NL * 2 * p.C * d * 2);
+    w.kvc[c] = (h16*)take((size_t)p.NL * 2 * p.Ct * d * 2);
     if (p.fold) {
-      w.fa[c] = (h16*)take((size_t)p.NL * p.H * p.C * d * 2);
-      w.fb[c] = (h16*)take((size_t)p.NL * p.H * p.C * d * 2);
-      w.fsb[c] = (float*)take((size_t)p.NL * p.H * p.C * 4);
+      w.fa[c] = (h16*)take((size_t)p.NL * p.H * p.Ct * d * 2);
+      w.fb[c] = (h16*)take((size_t)p.NL * p.H * p.Ct * d * 2);
+      w.fsb[c] = (float*)take((size_t)p.NL * p.H * p.Ct * 4);
     }
   }
-  w.Pkv = (float*)take((size_t)p.nch * p.NL * p.ks_kv * p.C * 2 * d * 4);
+  w.Pkv = (float*)take((size_t)p.nch * p.NL * p.ks_kv * p.Ct * 2 * d * 4);
   w.Ptau = (float*)take((size_t)p.nch * p.ks_tau * p.E * d * 4);
-  w.ctx_mom = (float*)take((size_t)p.C * 2 * 4);
+  w.ctx_mom = (float*)take((size_t)p.Ct * 2 * 4);
   w.total = off;
   return w;
 }
 
 // The nine launches of block l (both experts in each).
 int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w, const void* const* experts, int l,
-               hipStream_t st) {
-  const int d = p.d, fd = p.fd, NL = p.NL, nch = p.nch;
+               int Rg, hipStream_t st) {
+  const int d = p.d, fd = p.fd, NL = p.NL, nch = p.nch, Cg = Rg * p.C;
   auto PTR = [&](int c, size_t off) { return (const char*)experts[c] + off; };
   const size_t B = L.blk0 + (size_t)l * L.blkstride;
-  auto S_of = [&](int c) { return (c + 1) * p.CS; };
+  auto S_of = [&](int c) { return Rg * (c + 1) * p.CS; };     // rows of expert c: Rg requests
+  auto Sr_of = [&](int c) { return (c + 1) * p.CS; };         // rows per request
   int rc;
   // QKV: q, k, v = fp16(LN_self(x) W_in^T + b_in), full-K tiles
   {
@@ -502,7 +525,7 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w, const voi
     a.wg_per_kc = (d / 16) / (a.wpb * a.tpw);
     for (int c = 0; c < nch; ++c) {
       SEx& x = a.ex[c];
-      x.w = (const h16x8*)PTR(c, B + L.o); x.a = w.qkv[c]; x.out = w.P[c]; x.S = S_of(c);
+      x.w = (const h16x8*)PTR(c, B + L.o); x.a = w.qkv[c]; x.out = w.P[c]; x.S = S_of(c); x.Sr = Sr_of(c);
     }
     if ((rc = launch_stream<S_SELF, E_PART>(a, p.Smax, st))) return rc;
   }
@@ -518,12 +541,12 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w, const voi
   if ((rc = launch_res(r, st))) return rc;
   if (p.fold) {
     XattArgs x = {};
-    x.nex = nch; x.d = d; x.H = p.H; x.C = p.C; x.nb = p.xnb; x.scale = 1.0f / sqrtf((float)p.hd);
-    const size_t per_l = (size_t)p.H * p.C * d;
+    x.nex = nch; x.d = d; x.H = p.H; x.C = Cg; x.Cq = p.C; x.nb = p.xnb; x.scale = 1.0f / sqrtf((float)p.hd);
+    const size_t per_l = (size_t)p.H * Cg * d;
     for (int c = 0; c < nch; ++c) {
       x.xn[c] = w.abuf[c]; x.A[c] = w.fa[c] + (size_t)l * per_l; x.Bf[c] = w.fb[c] + (size_t)l * per_l;
-      x.sb[c] = w.fsb[c] + (size_t)l * p.H * p.C;
-      x.out[c] = w.P[c]; x.S[c] = S_of(c);
+      x.sb[c] = w.fsb[c] + (size_t)l * p.H * Cg;
+      x.out[c] = w.P[c]; x.S[c] = S_of(c); x.Sr[c] = Sr_of(c);
     }
     if ((rc = launch_xattn(x, st))) return rc;
   }
@@ -542,12 +565,12 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w, const voi
   if (!p.fold) {
     SArgs a = {};
     a.nex = nch; a.N = d; a.K = d; a.ks = p.ks_att; a.wpb = p.wpb_att; a.tpw = p.tpw_att; a.d = d; a.hd = p.hd;
-    a.ks_in = p.ks_qc; a.Ck = p.C;
+    a.ks_in = p.ks_qc; a.Ck = Cg; a.Cr = p.C;
     a.wg_per_kc = (d / 16) / (a.wpb * a.tpw);
     for (int c = 0; c < nch; ++c) {
       SEx& x = a.ex[c];
-      x.w = (const h16x8*)PTR(c, B + L.oc); x.a = w.kvc[c] + (size_t)l * 2 * p.C * d; x.pin = w.Pq[c];
-      x.bin = (const h16*)PTR(c, B + L.qc_b); x.out = w.P[c]; x.S = S_of(c);
+      x.w = (const h16x8*)PTR(c, B + L.oc); x.a = w.kvc[c] + (size_t)l * 2 * Cg * d; x.pin = w.Pq[c];
+      x.bin = (const h16*)PTR(c, B + L.qc_b); x.out = w.P[c]; x.S = S_of(c); x.Sr = Sr_of(c);
     }
     if ((rc = launch_stream<S_CROSS, E_PART>(a, p.Smax, st))) return rc;
   }
@@ -606,47 +629,49 @@ int integrate(const Plan& p, const cfh_flow_dims* dm, const void* const* experts
   auto PTR = [&](int c, size_t off) { return (const char*)experts[c] + off; };
   auto BLK = [&](int l) { return L.blk0 + (size_t)l * L.blkstride; };
 
-  for (int b = 0; b < batch; ++b) {
-    const h16* ctx_b = (const h16*)ctx + (size_t)b * C * d;
-    h16* zo_b = (h16*)z_out + (size_t)b * KD * d;
-
-    // ---- per draft: time embeddings of every step
-    {
-      GemvArgs a = {};
-      a.nex = nch; a.nl = 1; a.ks = p.ks_tau; a.tiles = d / 16; a.N = d; a.K = d; a.E = E;
-      for (int c = 0; c < nch; ++c) {
-        GemvEx& x = a.ex[c];
-        x.w = (const h16x8*)PTR(c, L.tw2);
-        x.g0 = (const h16*)PTR(c, L.tw0);
-        x.b0 = (const h16*)PTR(c, L.tb0);
-        x.pout = w.Ptau + (size_t)c * p.ks_tau * E * d;
-        x.rows = E;
-      }
-      if ((rc = launch_gemv<SRC_TAU>(a, E, st))) return rc;
-      ReduceArgs r = {};
-      r.nex = nch; r.nl = 1; r.ks = p.ks_tau; r.rows = E; r.N = d; r.d = d; r.kv = 0;
-      for (int c = 0; c < nch; ++c) {
-        r.P[c] = a.ex[c].pout;
-        r.b[c] = (const h16*)PTR(c, L.tb2);
-        r.out[c] = w.tau[c];
-      }
-      hipLaunchKernelGGL(k_reduce, dim3(256), dim3(256), 0, st, r);
-      CFH_LAUNCH_CHECK();
+  // ---- time embeddings of every step (the same for every request)
+  {
+    GemvArgs a = {};
+    a.nex = nch; a.nl = 1; a.ks = p.ks_tau; a.tiles = d / 16; a.N = d; a.K = d; a.E = E;
+    for (int c = 0; c < nch; ++c) {
+      GemvEx& x = a.ex[c];
+      x.w = (const h16x8*)PTR(c, L.tw2);
+      x.g0 = (const h16*)PTR(c, L.tw0);
+      x.b0 = (const h16*)PTR(c, L.tb0);
+      x.pout = w.Ptau + (size_t)c * p.ks_tau * E * d;
+      x.rows = E;
     }
+    if ((rc = launch_gemv<SRC_TAU>(a, E, st))) return rc;
+    ReduceArgs r = {};
+    r.nex = nch; r.nl = 1; r.ks = p.ks_tau; r.rows = E; r.N = d; r.d = d; r.kv = 0;
+    for (int c = 0; c < nch; ++c) {
+      r.P[c] = a.ex[c].pout;
+      r.b[c] = (const h16*)PTR(c, L.tb2);
+      r.out[c] = w.tau[c];
+    }
+    hipLaunchKernelGGL(k_reduce, dim3(256), dim3(256), 0, st, r);
+    CFH_LAUNCH_CHECK();
+  }
+
+  for (int g0 = 0; g0 < batch; g0 += p.R) {
+    const int Rg = std::min(p.R, batch - g0), Cg = Rg * C;     // this group's requests, context rows
+    const h16* ctx_b = (const h16*)ctx + (size_t)g0 * C * d;
+    h16* zo_b = (h16*)z_out + (size_t)g0 * KD * d;
+
     // ---- z0 and the step-0 rows
     {
       RowsArgs r = {};
       r.ctx = ctx_b; r.ctx_mom = w.ctx_mom; r.z = w.z; r.z_out = zo_b; r.euler = 0; r.last = 0; r.d = d; r.C = C;
-      r.CS = CS; r.nch = nch;
+      r.CS = CS; r.nch = nch; r.KD = KD; r.R = Rg; r.out_all = p.R > 1;
       for (int c = 0; c < nch; ++c) {
         r.x[c] = w.x[c]; r.pos[c] = (const h16*)PTR(c, L.pos); r.tau[c] = w.tau[c];
         r.g[c] = (const h16*)PTR(c, BLK(0) + L.sn_w); r.b[c] = (const h16*)PTR(c, BLK(0) + L.sn_b);
         r.a[c] = w.abuf[c];
       }
-      hipLaunchKernelGGL(k_rows, dim3(KD), dim3(ROWT), 0, st, r);
+      hipLaunchKernelGGL(k_rows, dim3(Rg * KD), dim3(ROWT), 0, st, r);
       CFH_LAUNCH_CHECK();
     }
-    // ---- cross K/V of every block (once per draft)
+    // ---- cross K/V of every block (once per draft), the group's context rows together
     {
       GemvArgs a = {};
       a.nex = nch; a.nl = NL; a.ks = p.ks_kv; a.tiles = 2 * d / 16; a.N = 2 * d; a.K = d; a.E = E;
@@ -657,13 +682,13 @@ int integrate(const Plan& p, const cfh_flow_dims* dm, const void* const* experts
         x.a = ctx_b;
         x.g0 = (const h16*)PTR(c, BLK(0) + L.cn_w);
         x.b0 = (const h16*)PTR(c, BLK(0) + L.cn_b);
-        x.pout = w.Pkv + (size_t)c * NL * p.ks_kv * C * 2 * d;
+        x.pout = w.Pkv + (size_t)c * NL * p.ks_kv * Cg * 2 * d;
         x.mom = w.ctx_mom;
-        x.rows = C;
+        x.rows = Cg;
       }
-      if ((rc = launch_gemv<SRC_CTX>(a, C, st))) return rc;
+      if ((rc = launch_gemv<SRC_CTX>(a, p.Ct, st))) return rc;
       ReduceArgs r = {};
-      r.nex = nch; r.nl = NL; r.ks = p.ks_kv; r.rows = C; r.N = 2 * d; r.d = d; r.kv = 1;
+      r.nex = nch; r.nl = NL; r.ks = p.ks_kv; r.rows = Cg; r.N = 2 * d; r.d = d; r.kv = 1;
       r.vstride = (long long)L.blkstride;
       for (int c = 0; c < nch; ++c) {
         r.P[c] = a.ex[c].pout;
@@ -675,18 +700,19 @@ int integrate(const Plan& p, const cfh_flow_dims* dm, const void* const* experts
     }
     // ---- the folded cross attention's factors of every block: A_h = Wq_h^T K_h^T from the
     // transposed query weight against the K rows, B_h = Wo_h V_h from the out-projection against
-    // the V rows, each split-K by head (the partial of head h, rounded to fp16, is the factor)
+    // the V rows, each split-K by head (the partial of head h, rounded to fp16, is the factor);
+    // the rows of the group's requests side by side
     if (p.fold) {
       XbiasArgs xb = {};
-      xb.nex = nch; xb.nl = NL; xb.d = d; xb.H = p.H; xb.C = C;
-      xb.kstride = (long long)2 * C * d; xb.bstride = (long long)L.blkstride;
+      xb.nex = nch; xb.nl = NL; xb.d = d; xb.H = p.H; xb.C = Cg;
+      xb.kstride = (long long)2 * Cg * d; xb.bstride = (long long)L.blkstride;
       for (int c = 0; c < nch; ++c) {
         xb.K[c] = w.kvc[c]; xb.bq[c] = (const h16*)PTR(c, BLK(0) + L.qc_b); xb.sb[c] = w.fsb[c];
       }
       hipLaunchKernelGGL(k_xbias, dim3(nch * NL), dim3(1024), 0, st, xb);
       CFH_LAUNCH_CHECK();
       for (int l = 0; l < NL; ++l) {
-        const size_t per_l = (size_t)p.H * C * d;
+        const size_t per_l = (size_t)p.H * Cg * d;
         for (int half = 0; half < 2; ++half) {
           // A and B of every expert in one launch when they fit the launch's four weight sets
           if (half == 1 && 2 * nch <= 4) break;
@@ -697,36 +723,43 @@ int integrate(const Plan& p, const cfh_flow_dims* dm, const void* const* experts
             if (2 * nch > 4 && part != half) continue;
             for (int c = 0; c < nch; ++c) {
               SEx& x = a.ex[a.nex++];
-              const h16* kv = w.kvc[c] + (size_t)l * 2 * C * d;
+              const h16* kv = w.kvc[c] + (size_t)l * 2 * Cg * d;
               x.w = (const h16x8*)PTR(c, BLK(l) + (part == 0 ? L.qc : L.oc));
-              x.a = part == 0 ? kv : kv + (size_t)C * d;
+              x.a = part == 0 ? kv : kv + (size_t)Cg * d;
               x.lda = d;
               x.out = (part == 0 ? w.fa[c] : w.fb[c]) + (size_t)l * per_l;
-              x.S = C;
+              x.S = Cg;
             }
           }
-          if ((rc = launch_stream<S_BUF, E_PART16>(a, C, st))) return rc;
+          if ((rc = launch_stream<S_BUF, E_PART16>(a, p.Ct, st))) return rc;
         }
       }
     }
     for (int s = 0; s < E; ++s) {
       for (int l = 0; l < NL; ++l)
-        if ((rc = block_pass(p, L, w, experts, l, st))) return rc;
-      // OUT: out_proj on the out_norm rows of each expert's current chunk
+        if ((rc = block_pass(p, L, w, experts, l, Rg, st))) return rc;
+      // OUT: out_proj on the out_norm rows of each expert's current chunk (every row when requests
+      // are packed: their current rows are not contiguous, and the weights stream once either way)
       {
         SArgs a = {};
         a.nex = nch; a.N = d; a.K = d; a.ks = p.ks_out; a.wpb = p.wpb_out; a.tpw = 1; a.d = d; a.hd = p.hd;
         a.wg_per_kc = (d / 16) / (a.wpb * a.tpw);
         for (int c = 0; c < nch; ++c) {
           SEx& x = a.ex[c];
-          x.w = (const h16x8*)PTR(c, L.out); x.a = w.abuf[c] + (size_t)c * CS * d; x.lda = d; x.out = w.P[c];
-          x.S = CS;
+          x.w = (const h16x8*)PTR(c, L.out); x.lda = d; x.out = w.P[c];
+          if (p.R == 1) {
+            x.a = w.abuf[c] + (size_t)c * CS * d;
+            x.S = CS;
+          } else {
+            x.a = w.abuf[c];
+            x.S = Rg * (c + 1) * CS;
+          }
         }
-        if ((rc = launch_stream<S_BUF, E_PART>(a, CS, st))) return rc;
+        if ((rc = launch_stream<S_BUF, E_PART>(a, p.R == 1 ? CS : p.Smax, st))) return rc;
       }
       RowsArgs r = {};
       r.ctx = ctx_b; r.z = w.z; r.z_out = zo_b; r.euler = 1; r.last = (s + 1 == E); r.ks = p.ks_out;
-      r.dt = 1.0f / (float)E; r.d = d; r.C = C; r.CS = CS; r.nch = nch;
+      r.dt = 1.0f / (float)E; r.d = d; r.C = C; r.CS = CS; r.nch = nch; r.KD = KD; r.R = Rg; r.out_all = p.R > 1;
       for (int c = 0; c < nch; ++c) {
         r.Pout[c] = w.P[c]; r.bout[c] = (const h16*)PTR(c, L.out_b);
         r.x[c] = w.x[c]; r.pos[c] = (const h16*)PTR(c, L.pos);
@@ -734,7 +767,7 @@ int integrate(const Plan& p, const cfh_flow_dims* dm, const void* const* experts
         r.g[c] = (const h16*)PTR(c, BLK(0) + L.sn_w); r.b[c] = (const h16*)PTR(c, BLK(0) + L.sn_b);
         r.a[c] = w.abuf[c];
       }
-      hipLaunchKernelGGL(k_rows, dim3(KD), dim3(ROWT), 0, st, r);
+      hipLaunchKernelGGL(k_rows, dim3(Rg * KD), dim3(ROWT), 0, st, r);
       CFH_LAUNCH_CHECK();
     }
   }
@@ -773,7 +806,7 @@ extern "C" {
 int cfh_caps(const cfh_flow_dims* dims, int batch, int64_t* ws_bytes) {
   if (!cfh::flow_dims_ok(dims) || batch < 1) return CFH_E_UNSUPPORTED;
   if (dims->d > ROWT * ROWE || dims->draft_length > MAXR) return CFH_E_UNSUPPORTED;
-  const Plan p = make_plan(dims);
+  const Plan p = make_plan(dims, group_size(dims, batch));
   if (!p.ok) return CFH_E_UNSUPPORTED;
   const WS w = carve(p, nullptr);
   if (ws_bytes) *ws_bytes = (int64_t)w.total;
@@ -784,7 +817,7 @@ int cfh_flow_integrate(const cfh_flow_dims* dm, const void* const* experts, cons
                        void* ws_ptr, int batch, void* stream) {
   if (!cfh::flow_dims_ok(dm) || dm->d > ROWT * ROWE || dm->draft_length > MAXR) return CFH_E_UNSUPPORTED;
   if (!experts || !ctx || !z_out || !ws_ptr || batch < 1) return CFH_E_INVALID;
-  const Plan p = make_plan(dm);
+  const Plan p = make_plan(dm, group_size(dm, batch));
   if (!p.ok) return CFH_E_UNSUPPORTED;
   for (int c = 0; c < p.nch; ++c)
     if (!experts[c]) return CFH_E_INVALID;
@@ -795,7 +828,7 @@ int cfh_flow_integrate_noalloc(const cfh_flow_dims* dm, const void* const* exper
                                int batch, void* stream) {
   if (!cfh::flow_dims_ok(dm) || dm->d > ROWT * ROWE || dm->draft_length > MAXR) return CFH_E_UNSUPPORTED;
   if (!experts || !ctx || !z_out || batch < 1) return CFH_E_INVALID;
-  const Plan p = make_plan(dm);
+  const Plan p = make_plan(dm, group_size(dm, batch));
   if (!p.ok) return CFH_E_UNSUPPORTED;
   for (int c = 0; c < p.nch; ++c)
     if (!experts[c]) return CFH_E_INVALID;

@@ -27,8 +27,9 @@ extern "C" {
 #define CFH_E_HIP 3              /* a HIP runtime call failed (cfh_last_hip_error)        */
 #define CFH_E_SCRATCH 4          /* the no-allocation entry point's workspace is too small */
 
-/* Size of the library's per-device scratch array behind cfh_flow_integrate_noalloc (64 MiB:
- * the flow workspace of d <= 5120 at 8 layers needs 57.3 MiB). */
+/* Size of the library's per-device scratch array behind cfh_flow_integrate_noalloc (64 MiB: the
+ * flow workspace of one request at d <= 5120 and 8 layers needs 37.3 MiB; a batch packs two
+ * requests per group where the shape allows, which can need more -- cfh_caps tells). */
 #define CFH_NOALLOC_SCRATCH_BYTES (64ll << 20)
 
 /* Library version (major*10000 + minor*100 + patch). */
@@ -98,7 +99,9 @@ int cfh_flow_pack_expert(const cfh_flow_dims* dims, const void* const* raw, int 
  *   experts : n_chunks = draft_length/chunk_size packed expert images (chunk order)
  *   ctx     : [batch][ctx_rows][d] fp16 context hidden states (already front-padded)
  *   z_out   : [batch][draft_length][d] fp16 predicted hiddens
- *   ws      : workspace of cfh_caps() bytes
+ *   ws      : workspace of cfh_caps(dims, batch) bytes
+ * A batch runs in groups of up to two requests whose rows share every weight stream (when both
+ * drafts fit one 16-row MFMA tile and the shape's operand staging allows it).
  * Replaces the per-Euler-step torch loop plus the fused kernel launch
  * (cf/cuda_block.py:407-431 / pybind `expert`, `cross_kv`, cf/csrc/fused_block.cu:793-862). */
 int cfh_flow_integrate(const cfh_flow_dims* dims, const void* const* experts, const void* ctx,

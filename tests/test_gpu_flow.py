@@ -121,3 +121,31 @@ def test_flow_latent_widths_match_oracle(cuda, d, heads, layers, steps):
     print(f"  rel err {err:.3e}", flush=True)
     assert np.isfinite(to64(z)).all()
     assert err < TOL_FP16
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("d,B,layers", [(512, 2, 2), (512, 5, 1), (640, 3, 1), (1024, 2, 2), (4096, 2, 1)])
+def test_packed_batch_matches_oracle_per_request(cuda, d, B, layers):
+    """A batch drafts in groups of two requests whose rows share every weight stream (16-row tiles,
+    attention masked to each request's own rows and context): each request's hiddens against the
+    oracle on its own context, and against the same request drafted alone in the same numerics.
+    d = 640 runs the unfolded cross attention (head width 80), the others the folded one; B = 5
+    and 3 end with a group of one."""
+    cfg = flownet(d, layers=layers, flow_steps=2)
+    W = _flow_weights(cfg, seed=13)
+    ctx = synthetic_context(B, cfg.context_size, d, seed=21)
+    print(f"[flow packed] d={d} B={B} L={layers}", flush=True)
+    ff = FusedFlow(cfg, {k: v.to(cuda) for k, v in W.items()}, device=cuda)
+    z = ff.predict_hidden(ctx.to(cuda))
+    num = ff.dims.numerics                               # the batch's numerics (torch's modules at B > 1)
+    singles = [ff.predict_hidden(ctx[b:b + 1].to(cuda), numerics=num).clone() for b in range(B)]
+    torch.cuda.synchronize()
+    onum = "fp16_modules" if num == 1 else "fp16"
+    W64 = weights64(W)
+    for b in range(B):
+        ref = oflow.predict_hidden(W64, to64(ctx[b:b + 1]), _ocfg(cfg), numerics=onum)
+        e = rel_err(to64(z[b:b + 1]), ref)
+        es = rel_err(to64(z[b:b + 1]), to64(singles[b]))
+        print(f"  request {b}: vs oracle {e:.3e}, vs drafted alone {es:.3e}", flush=True)
+        assert np.isfinite(to64(z[b:b + 1])).all()
+        assert e < TOL_FP16 and es < TOL_FP16

@@ -48,7 +48,7 @@ def test_candidate_select_argument_checks_without_a_device():
 
 def test_noalloc_flow_rejects_a_workspace_beyond_the_scratch_without_a_device():
     """cfh_flow_integrate_noalloc refuses, before any HIP call, a shape whose flow workspace exceeds
-    the 64 MiB scratch array (d = 8192 at 8 layers needs 108 MiB), with its own status."""
+    the 64 MiB scratch array (d = 8192 at 8 layers needs 75.8 MiB), with its own status."""
     import ctypes as C
 
     from chain_flow_amd.config import flownet

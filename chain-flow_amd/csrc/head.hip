@@ -531,6 +531,10 @@ __global__ void __launch_bounds__(TK_THREADS) k_topk(TopkArgs a) {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int GPF = 4;            // k-steps per LDS chunk
+// M <= 160 rows: 2 column tiles per wave, all 10 row tiles in each wave.  (Splitting the row tiles
+// over 2 waves with 4 column tiles each -- an x operand read feeding 4 MFMAs, twice the weights in
+// flight -- needs more than the 256 registers a wave has at 2 waves per SIMD: it spills.)
+constexpr int GEMM160_NT = 2, GEMM160_MS = 1;
 constexpr int GKC = 32 * GPF;     // 128 columns per chunk: a row is 16 slots of 16 bytes
 
 struct GemmArgs {
@@ -563,14 +567,19 @@ __device__ __forceinline__ float gemm_value(unsigned b) {
   else return __uint_as_float(b << 16);
 }
 
-template <int MT, int NT, int GW, bool PK, bool F16>
+// MS: the MT row tiles are split over MS waves that share the same NT column tiles (the waves of a
+// workgroup are NG = GW / MS column groups times MS row groups), so each x operand read from LDS
+// feeds NT MFMAs and each wave keeps NT tiles of weight fragments in flight.
+template <int MT, int NT, int GW, bool PK, bool F16, int MS>
 __global__ void __launch_bounds__(GW * 64) k_head_gemm(GemmArgs a) {
   // [2][MT*16][GKC], each row's 16-byte slots XOR-swizzled by the row's low 4 bits: the 16 rows
   // an MFMA operand read touches then fall on 16 different bank groups
   extern __shared__ __align__(16) uint16_t xs[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  constexpr int ROWS = MT * 16;
-  const int tile0 = (blockIdx.x * GW + wave) * NT;
+  constexpr int ROWS = MT * 16, NG = GW / MS, MTW = MT / MS;
+  static_assert(NG * MS == GW && MTW * MS == MT, "the row tiles and waves must split evenly");
+  const int ng = wave % NG, mh = wave / NG;
+  const int tile0 = (blockIdx.x * NG + ng) * NT;
   // fragment (tile, k-step s) of lane: wp[t][s * KS]; tiles past the shortlist re-read its last one
   constexpr int KS = PK ? 64 : 4;
   const bf16x8* wp[NT];
@@ -626,9 +635,9 @@ __global__ void __launch_bounds__(GW * 64) k_head_gemm(GemmArgs a) {
     store_x(0, xr);
   }
   lds_barrier();
-  f32x4 acc[MT][NT];
+  f32x4 acc[MTW][NT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+  for (int mt = 0; mt < MTW; ++mt)
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[mt][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
   auto step = [&](int c, bf16x8 (&bq)[GPF][NT]) {
@@ -637,12 +646,12 @@ __global__ void __launch_bounds__(GW * 64) k_head_gemm(GemmArgs a) {
     bf16x8 xr[XV];
     load_x(min(c + 1, nchunks - 1), xr);
     const int cw = min(c + 2, nchunks - 1);
-    const uint16_t* xb = xs + (size_t)(c & 1) * ROWS * GKC + (lane & 15) * GKC;
+    const uint16_t* xb = xs + (size_t)(c & 1) * ROWS * GKC + (size_t)(mh * MTW * 16 + (lane & 15)) * GKC;
 #pragma unroll
     for (int p = 0; p < GPF; ++p) {
       const int slot = (p * 4 + (lane >> 4)) ^ (lane & 15);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
+      for (int mt = 0; mt < MTW; ++mt) {
         const bf16x8 av = *(const bf16x8*)(xb + mt * 16 * GKC + slot * 8);
 #pragma unroll
         for (int t = 0; t < NT; ++t)
@@ -671,19 +680,19 @@ __global__ void __launch_bounds__(GW * 64) k_head_gemm(GemmArgs a) {
   // holds columns l*CPL .. l*CPL+CPL-1 as 32-bit keys (order-preserving bf16 bits << 16 |
   // 0xFFFF - column), so one integer max picks the larger logit and, on a tie, the lower column;
   // a round is CPL-1 maxes, 4 DPP steps and the winner's removal.  Key 0 = no column.
-  constexpr int COLS = GW * NT * 16, LST = COLS + 8, CPL = COLS / 16;
+  constexpr int COLS = NG * NT * 16, LST = COLS + 8, CPL = COLS / 16;
   static_assert(CPL % 8 == 0, "a lane's columns are read as 16-byte vectors");
   uint16_t* lg = xs;
   {
     const int g = lane >> 4, col = lane & 15;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int mt = 0; mt < MTW; ++mt)
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const int r = mt * 16 + 4 * g + q;
-          const int c = (wave * NT + t) * 16 + col;
+          const int r = (mh * MTW + mt) * 16 + 4 * g + q;
+          const int c = (ng * NT + t) * 16 + col;
           const int j = blockIdx.x * COLS + c;
           const bool in = r < a.M && j < a.n;
           const uint16_t b = gemm_logit<F16>(acc[mt][t][q], F16 && a.bias && in ? a.bias + (size_t)r * a.n + j : nullptr);
@@ -747,31 +756,31 @@ __global__ void __launch_bounds__(GW * 64) k_head_gemm(GemmArgs a) {
   }
 }
 
-template <int MT, int NT, int GW>
+template <int MT, int NT, int GW, int MS>
 size_t gemm_lds() {
-  const size_t xbuf = 2 * (size_t)MT * 16 * GKC * 2;               // x double buffer
-  const size_t lgt = (size_t)MT * 16 * (GW * NT * 16 + 8) * 2;     // the block's logits
+  const size_t xbuf = 2 * (size_t)MT * 16 * GKC * 2;                      // x double buffer
+  const size_t lgt = (size_t)MT * 16 * (GW / MS * NT * 16 + 8) * 2;       // the block's logits
   return xbuf > lgt ? xbuf : lgt;
 }
 
-template <int MT, int NT, int GW, bool PK, bool F16>
+template <int MT, int NT, int GW, bool PK, bool F16, int MS>
 int launch_gemm(const GemmArgs& a0, hipStream_t st) {
   // cfh_head_ws_bytes sizes the candidate lists for blocks of at least 128 columns
-  static_assert(GW * NT * 16 >= 128, "a GEMM block must cover at least 128 shortlist columns");
+  static_assert(GW / MS * NT * 16 >= 128, "a GEMM block must cover at least 128 shortlist columns");
   GemmArgs a = a0;
-  const int cols = GW * NT * 16;
+  const int cols = GW / MS * NT * 16;
   a.nsets = (a.n + cols - 1) / cols;
-  const size_t lds = gemm_lds<MT, NT, GW>();
+  const size_t lds = gemm_lds<MT, NT, GW, MS>();
   if (lds > 160 * 1024) return CFH_E_UNSUPPORTED;
-  CFH_HIP(hipFuncSetAttribute((const void*)k_head_gemm<MT, NT, GW, PK, F16>,
+  CFH_HIP(hipFuncSetAttribute((const void*)k_head_gemm<MT, NT, GW, PK, F16, MS>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-  hipLaunchKernelGGL((k_head_gemm<MT, NT, GW, PK, F16>), dim3(a.nsets), dim3(GW * 64), lds, st, a);
+  hipLaunchKernelGGL((k_head_gemm<MT, NT, GW, PK, F16, MS>), dim3(a.nsets), dim3(GW * 64), lds, st, a);
   CFH_LAUNCH_CHECK();
   return CFH_OK;
 }
 
-template <int MT, int NT, int GW>
-int gemm_nsets(int n) { return (n + GW * NT * 16 - 1) / (GW * NT * 16); }
+template <int MT, int NT, int GW, int MS>
+int gemm_nsets(int n) { return (n + GW / MS * NT * 16 - 1) / (GW / MS * NT * 16); }
 
 // ---------------------------------------------------------------------------- path residual
 struct PathSumArgs {
@@ -1034,17 +1043,17 @@ int gemm_topk(const void* x, int M, int d, const void* W, const int32_t* sl, int
   ga.M = M; ga.d = d; ga.n = n; ga.k = k;
   int rc, nsets;
   if (M <= 64) {
-    nsets = gemm_nsets<4, 2, 8>(n);
+    nsets = gemm_nsets<4, 2, 8, 1>(n);
     ga.nsets = nsets;
-    rc = launch_gemm<4, 2, 8, PK, F16>(ga, st);
+    rc = launch_gemm<4, 2, 8, PK, F16, 1>(ga, st);
   } else if (M <= 160) {
-    nsets = gemm_nsets<10, 2, 8>(n);
+    nsets = gemm_nsets<10, GEMM160_NT, 8, GEMM160_MS>(n);
     ga.nsets = nsets;
-    rc = launch_gemm<10, 2, 8, PK, F16>(ga, st);
+    rc = launch_gemm<10, GEMM160_NT, 8, PK, F16, GEMM160_MS>(ga, st);
   } else {
-    nsets = gemm_nsets<16, 1, 8>(n);
+    nsets = gemm_nsets<16, 1, 8, 1>(n);
     ga.nsets = nsets;
-    rc = launch_gemm<16, 1, 8, PK, F16>(ga, st);
+    rc = launch_gemm<16, 1, 8, PK, F16, 1>(ga, st);
   }
   if (rc || k == 0) return rc;
   return launch_merge(ws, M, nsets, k, vals, ids, lse, st);

@@ -530,10 +530,14 @@ __global__ void __launch_bounds__(TK_THREADS) k_topk(TopkArgs a) {
 // so every wave load is 1 KB contiguous (in place: 16 rows x 64 bytes).
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-// A weight fragment load of the GEMM heads: non-temporal, since each byte is read once per call
-// (measured on the 62,642-row, d=4096 stream: 6.2 against 5.5 TB/s with the default policy).
+// A weight fragment load of the GEMM heads.  From a packed image it is non-temporal, since each
+// byte is read once per call (measured on the 62,642-row, d=4096 stream: 6.2 against 5.5 TB/s
+// with the default policy); in place each lane reads 16 bytes of a row whose other bytes the next
+// k-steps read, so the lines should stay in L2 (non-temporal there fetched 663 MB for 515).
+template <bool PK>
 __device__ __forceinline__ bf16x8 wload(const bf16x8* p) {
-  return __builtin_bit_cast(bf16x8, __builtin_nontemporal_load((const h16x8*)p));
+  if constexpr (PK) return __builtin_bit_cast(bf16x8, __builtin_nontemporal_load((const h16x8*)p));
+  else return *p;
 }
 
 constexpr int GPF = 4;            // k-steps per LDS chunk
@@ -779,8 +783,8 @@ __global__ void __launch_bounds__(GW * 64) k_head_gemm(GemmArgs a) {
   for (int p = 0; p < GPF; ++p)
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      bqa[p][t] = wload(wp[t] + p * KS);
-      bqb[p][t] = wload(wp[t] + (min(1, nchunks - 1) * GPF + p) * KS);
+      bqa[p][t] = wload<PK>(wp[t] + p * KS);
+      bqb[p][t] = wload<PK>(wp[t] + (min(1, nchunks - 1) * GPF + p) * KS);
     }
   // x chunk: ROWS x 16 vectors of 8, XV a thread (vector idx = row*16 + v); branch-free, rows past
   // M repeat row M-1 (their products are never read), so the wait counts before the multiplies
@@ -838,7 +842,7 @@ __global__ void __launch_bounds__(GW * 64) k_head_gemm(GemmArgs a) {
       // keep the reloads here: the scheduler would otherwise sink them to the end of the chunk
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int t = 0; t < NT; ++t) bq[p][t] = wload(wp[t] + (cw * GPF + p) * KS);
+      for (int t = 0; t < NT; ++t) bq[p][t] = wload<PK>(wp[t] + (cw * GPF + p) * KS);
       __builtin_amdgcn_sched_barrier(0);
     }
     store_x((c + 1) & 1, xr);

@@ -203,12 +203,13 @@ __global__ void __launch_bounds__(ROWT) k_rows(RowsArgs a) {
 //   scores[r][c] = (LN(x)[r] . A_h[c] + sb_h[c]) / sqrt(hd),  P = softmax_c(scores),
 //   out_h[r][n] = sum_c P[r][c] B_h[c][n]
 // (exactly q_h . K_h with q = Wq LN(x) + bq, and Wo_h (P V_h); A and B are rounded to fp16 where
-// the reference rounds q and P V_h).  One workgroup per (expert, head, column block of n).  The
-// workgroup first puts its block of B_h in flight (it does not depend on the scores), then the
-// scores: one 16 x 16 MFMA tile (rows x context rows) over d with the k-steps split over the waves,
-// each wave issuing all its loads before its MFMAs, the wave tiles summed through LDS; the softmax;
-// and its column block of P_h B_h, written as the head's fp32 partial [H][S][d] that the residual
-// row kernel sums with the other heads and the out_proj bias, as for any split-K sublayer.
+// the reference rounds q and P V_h).  One workgroup per (expert, head, column block of n), one
+// column of the block per thread.  The workgroup first puts its columns of B_h in flight (they do
+// not depend on the scores), then the scores: one 16 x 16 MFMA tile (rows x context rows) over d
+// with the k-steps split over the waves, each wave issuing all its loads before its MFMAs, the wave
+// tiles summed through LDS; the softmax, 16 lanes a row; and its columns of P_h B_h, written as the
+// head's fp32 partial [H][S][d] that the residual row kernel sums with the other heads and the
+// out_proj bias, as for any split-K sublayer.
 struct XattArgs {
   const h16* xn[4];      // LN_cross(x) rows [S][d]
   const h16* A[4];       // this layer's A [H][C][d]
@@ -236,12 +237,12 @@ __global__ void __launch_bounds__(XT) k_xattn(XattArgs a) {
   const int h = b % a.H, e = b / a.H;
   const int S = a.S[e], C = a.C, d = a.d;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  // this thread's 8 columns of B_h (every context row), in flight before the scores
-  const int gpb = d / 8 / a.nb, g = cb * gpb + min(t, gpb - 1);
-  const h16* Bh = a.Bf[e] + (size_t)h * C * d + 8 * g;
-  h16x8 bv[CM];
+  // this thread's column of B_h (every context row), in flight before the scores
+  const int cpb = d / a.nb, n = cb * cpb + min(t, cpb - 1);
+  const h16* Bh = a.Bf[e] + (size_t)h * C * d + n;
+  h16 bv[CM];
 #pragma unroll
-  for (int c = 0; c < CM; ++c) bv[c] = *(const h16x8*)(Bh + (size_t)min(c, C - 1) * d);
+  for (int c = 0; c < CM; ++c) bv[c] = Bh[(size_t)min(c, C - 1) * d];
   // scores: lane row = lane % 16 (rows past S repeat row S-1: their products are never read),
   // context row = lane % 16 of the B operand (rows past C read row C-1, zeroed)
   const h16* Ah = a.A[e] + (size_t)h * C * d;
@@ -266,42 +267,36 @@ __global__ void __launch_bounds__(XT) k_xattn(XattArgs a) {
 #pragma unroll
   for (int q = 0; q < 4; ++q) red[wave][(4 * (lane >> 4) + q) * 16 + (lane & 15)] = acc[q];
   __syncthreads();
+  // the score of (row r, context row c) in thread 16 r + c; the softmax over the row's 16 lanes
+  // (every row r < S has its own request's context rows)
   if (t < 256) {
     const int r = t >> 4, c = t & 15;
     float v = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) v += red[w][t];
-    if (r < S) P[r][c] = c < C && c / a.Cq == r / a.Sr[e] ? (v + a.sb[e][h * C + c]) * a.scale : -INFINITY;
+    const bool ok = r < S && c < C && c / a.Cq == r / a.Sr[e];
+    const float sc = ok ? (v + a.sb[e][h * C + c]) * a.scale : -INFINITY;
+    float m = sc;
+    m = fmaxf(m, dpp_f32<DPP_XOR1>(m));
+    m = fmaxf(m, dpp_f32<DPP_XOR2>(m));
+    m = fmaxf(m, dpp_f32<DPP_HMIRROR>(m));
+    m = fmaxf(m, dpp_f32<DPP_MIRROR>(m));
+    const float z = ok ? expf(sc - m) : 0.f;
+    const float sum = row_sum(z);
+    if (r < S) P[r][c] = z * (1.0f / sum);     // 0 for masked and padding context rows
   }
   __syncthreads();
-  // softmax over the C context rows, one thread per row
-  if (t < S) {
-    float m = -INFINITY;
-    for (int c = 0; c < C; ++c) m = fmaxf(m, P[t][c]);
-    float z[16], sum = 0.f;
+  // this thread's column of P_h B_h
+  if (t < cpb) {
+    float* oh = a.out[e] + (size_t)h * S * d + n;
+    float bf[CM];
 #pragma unroll
-    for (int c = 0; c < 16; ++c) {
-      z[c] = c < C && P[t][c] != -INFINITY ? expf(P[t][c] - m) : 0.f;
-      sum += z[c];
-    }
-    const float inv = 1.0f / sum;
-#pragma unroll
-    for (int c = 0; c < 16; ++c) P[t][c] = z[c] * inv;
-  }
-  __syncthreads();
-  // this workgroup's columns of P_h B_h
-  if (t < gpb) {
-    float* oh = a.out[e] + (size_t)h * S * d + 8 * g;
+    for (int c = 0; c < CM; ++c) bf[c] = (float)bv[c];
     for (int r = 0; r < S; ++r) {
-      float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      float o = 0.f;
 #pragma unroll
-      for (int c = 0; c < CM; ++c) {
-        const float pw = P[r][c];   // 0 for the padding rows c >= C
-#pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] += pw * (float)bv[c][j];
-      }
-      *(float4*)(oh + (size_t)r * d) = make_float4(o[0], o[1], o[2], o[3]);
-      *(float4*)(oh + (size_t)r * d + 4) = make_float4(o[4], o[5], o[6], o[7]);
+      for (int c = 0; c < CM; ++c) o += P[r][c] * bf[c];
+      oh[(size_t)r * d] = o;
     }
   }
 }
@@ -331,14 +326,13 @@ __global__ void __launch_bounds__(1024) k_xbias(XbiasArgs a) {
   }
 }
 
-// Column blocks per (expert, head) of XATT: at least 64 workgroups in all, each block a whole
-// number of 8-column groups, at most one group per thread; 0 if d / 8 has no such split.
+// Column blocks per (expert, head) of XATT: the fewest that give each thread at most one column
+// (each block recomputes the head's scores, so more blocks only repeat that work); 0 if d has no
+// such split.
 int xattn_blocks(int d, int units) {
-  const int ng = d / 8;
-  for (int nb = 1; nb <= ng; ++nb)
-    if (ng % nb == 0 && ng / nb <= XT && units * nb >= 64) return nb;
-  for (int nb = 1; nb <= ng; ++nb)
-    if (ng % nb == 0 && ng / nb <= XT) return nb;
+  (void)units;
+  for (int nb = 1; nb <= d; ++nb)
+    if (d % nb == 0 && d / nb <= XT) return nb;
   return 0;
 }
 

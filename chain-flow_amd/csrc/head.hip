@@ -664,18 +664,23 @@ __device__ __forceinline__ void gemm_finish(const GemmArgs& a, const f32x4 (&acc
       }
     }
   };
+  // The winners and each row's (max, sum-exp) are staged in LDS after the logits, written by every
+  // lane of the group (the same value: no branch), rows past M into a dummy slot ROWS; one pass at
+  // the end copies them out.  Branches inside a round would split it into blocks the compiler
+  // cannot interleave across rows (and copy the rows' lists at each).
+  float* cstv = (float*)(lg + ROWS * LST);
+  int* csti = (int*)(cstv + (ROWS + 1) * KMAX);
+  float* cstm = (float*)(csti + (ROWS + 1) * KMAX);
+  float* csts = cstm + (ROWS + 1);
   for (int r0 = threadIdx.x >> 4; r0 < a.M; r0 += NGR * RB) {
     unsigned q[RB][4], fl[RB];
     bool full[RB];
     float mx[RB];
-    float* cvp[RB];
-    int* cip[RB];
+    int slot[RB];
 #pragma unroll
     for (int b = 0; b < RB; ++b) {
       const int r = r0 + b * NGR;
-      const size_t base = ((size_t)min(r, a.M - 1) * a.nsets + blockIdx.x) * a.k;
-      cvp[b] = cd.cv + base;
-      cip[b] = cd.ci + base;
+      slot[b] = r < a.M ? r : ROWS;
       if (r < a.M) lane_top4(r, 0u, false, q[b]);
       else q[b][0] = q[b][1] = q[b][2] = q[b][3] = 0u;
       fl[b] = 0xFFFFFFFFu;
@@ -691,29 +696,31 @@ __device__ __forceinline__ void gemm_finish(const GemmArgs& a, const f32x4 (&acc
       for (int b = 0; b < RB; ++b) m[b] = max(m[b], (unsigned)dpp_i32<DPP_HMIRROR>((int)m[b]));
 #pragma unroll
       for (int b = 0; b < RB; ++b) m[b] = max(m[b], (unsigned)dpp_i32<DPP_MIRROR>((int)m[b]));
+      bool need[RB], any = false;
 #pragma unroll
       for (int b = 0; b < RB; ++b) {
         const bool win = m[b] != 0u && q[b][0] == m[b];
-        if (win) {
-          fl[b] = m[b];
-          q[b][0] = q[b][1]; q[b][1] = q[b][2]; q[b][2] = q[b][3]; q[b][3] = 0u;
-        }
-        const int r = r0 + b * NGR;
-        const bool need = win && full[b] && q[b][0] == 0u;
-        if (__builtin_amdgcn_ballot_w64(need)) {
-          if (need) {
-            lane_top4(r, fl[b], true, q[b]);
-            full[b] = q[b][3] != 0u;
-          }
-        }
+        fl[b] = win ? m[b] : fl[b];
+        q[b][0] = win ? q[b][1] : q[b][0];
+        q[b][1] = win ? q[b][2] : q[b][1];
+        q[b][2] = win ? q[b][3] : q[b][2];
+        q[b][3] = win ? 0u : q[b][3];
+        need[b] = win && full[b] && q[b][0] == 0u;
+        any |= need[b];
         const unsigned o = m[b] >> 16;
         const unsigned v = (o & 0x8000u) ? (o & 0x7FFFu) : (~o & 0xFFFFu);
         const float bv = m[b] ? gemm_value<F16>(v) : -INFINITY;
-        if (rr == 0) mx[b] = bv;
-        if (col == 0 && r < a.M) {
-          cvp[b][rr] = bv;
-          cip[b][rr] = m[b] ? blockIdx.x * COLS + (int)(0xFFFFu - (m[b] & 0xFFFFu)) : INT_MAX;
-        }
+        mx[b] = rr == 0 ? bv : mx[b];
+        cstv[slot[b] * KMAX + rr] = bv;
+        csti[slot[b] * KMAX + rr] = m[b] ? blockIdx.x * COLS + (int)(0xFFFFu - (m[b] & 0xFFFFu)) : INT_MAX;
+      }
+      if (__builtin_amdgcn_ballot_w64(any)) {      // rare: a lane won a fifth time
+#pragma unroll
+        for (int b = 0; b < RB; ++b)
+          if (need[b]) {
+            lane_top4(r0 + b * NGR, fl[b], true, q[b]);
+            full[b] = q[b][3] != 0u;
+          }
       }
     }
     // the row's sum of exp(logit - max), from the logits parked in LDS (hardware exp2)
@@ -736,12 +743,21 @@ __device__ __forceinline__ void gemm_finish(const GemmArgs& a, const f32x4 (&acc
         }
       }
       se = row_sum(se);
-      if (col == 0 && r < a.M) {
-        const size_t base = (size_t)r * a.nsets + blockIdx.x;
-        cd.cs[base * 2] = mx[b];
-        cd.cs[base * 2 + 1] = se;
-      }
+      cstm[slot[b]] = mx[b];
+      csts[slot[b]] = se;
     }
+  }
+  lds_barrier();
+  for (int i = threadIdx.x; i < a.M * a.k; i += NTHR) {
+    const int r = i / a.k, rr = i - r * a.k;
+    const size_t base = ((size_t)r * a.nsets + blockIdx.x) * a.k + rr;
+    cd.cv[base] = cstv[r * KMAX + rr];
+    cd.ci[base] = csti[r * KMAX + rr];
+  }
+  for (int r = threadIdx.x; r < a.M; r += NTHR) {
+    const size_t base = (size_t)r * a.nsets + blockIdx.x;
+    cd.cs[base * 2] = cstm[r];
+    cd.cs[base * 2 + 1] = csts[r];
   }
 }
 
@@ -859,7 +875,8 @@ __global__ void __launch_bounds__(GW * 64) k_head_gemm(GemmArgs a) {
 template <int MT, int NT, int GW, int MS>
 size_t gemm_lds() {
   const size_t xbuf = 2 * (size_t)MT * 16 * GKC * 2;                      // x double buffer
-  const size_t lgt = (size_t)MT * 16 * (GW / MS * NT * 16 + 8) * 2;       // the block's logits
+  const size_t lgt = (size_t)MT * 16 * (GW / MS * NT * 16 + 8) * 2 +      // the block's logits,
+                     ((size_t)MT * 16 + 1) * (KMAX * 8 + 8);              // staged winners, (max, sum)
   return xbuf > lgt ? xbuf : lgt;
 }
 

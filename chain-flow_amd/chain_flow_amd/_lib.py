@@ -17,10 +17,11 @@ _lib = None
 class FlowDims(C.Structure):
     _fields_ = [("d", C.c_int), ("ffn_mult", C.c_int), ("heads", C.c_int), ("layers", C.c_int),
                 ("ctx_rows", C.c_int), ("draft_length", C.c_int), ("chunk_size", C.c_int),
-                ("flow_steps", C.c_int), ("numerics", C.c_int)]
+                ("flow_steps", C.c_int), ("numerics", C.c_int), ("init_mode", C.c_int)]
 
 
 FLOW_FUSED, FLOW_MODULES = 0, 1      # cfh_flow_dims.numerics (CFH_FLOW_FUSED / CFH_FLOW_MODULES)
+INIT_DELTA, INIT_REPEAT_LAST, INIT_GIVEN = 0, 1, 2   # cfh_flow_dims.init_mode (CFH_INIT_*)
 
 
 class VaeDims(C.Structure):

@@ -17,6 +17,7 @@ class TreeFlowConfig:
     num_drafter_layers: int = 8
     num_flow_steps: int = 2
     init_mode: str = "delta"
+    noise_scale: float = 1.0        # init_mode="noise": z0 = randn * noise_scale
     markov_rank: int = 256
     path_order: int = 4
     path_ffn_multiplier: int = 2

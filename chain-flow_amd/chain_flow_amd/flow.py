@@ -40,11 +40,17 @@ def reference_numerics(cfg: TreeFlowConfig, batch: int = 1) -> int:
     return _lib.FLOW_FUSED if fused else _lib.FLOW_MODULES
 
 
+# init_latents modes (cf/drafters/tree_flow.py:150-161) -> cfh_flow_dims.init_mode; "noise" draws
+# z0 here with torch's generator, as the reference does, and hands it over through z_out
+_INIT = {"delta": _lib.INIT_DELTA, "repeat_last": _lib.INIT_REPEAT_LAST, "noise": _lib.INIT_GIVEN}
+
+
 def flow_dims(cfg: TreeFlowConfig, numerics: int | None = None) -> _lib.FlowDims:
     """cfh_flow_dims of ``cfg``; ``numerics`` defaults to the reference's at batch 1."""
     num = reference_numerics(cfg) if numerics is None else int(numerics)
     return _lib.FlowDims(cfg.flow_dim, cfg.ffn_multiplier, cfg.num_heads, cfg.num_drafter_layers,
-                         cfg.context_size, cfg.draft_length, cfg.chunk_size, cfg.num_flow_steps, num)
+                         cfg.context_size, cfg.draft_length, cfg.chunk_size, cfg.num_flow_steps, num,
+                         _INIT[cfg.init_mode])
 
 
 def caps(cfg: TreeFlowConfig, batch: int = 1):
@@ -59,8 +65,6 @@ class FusedFlow:
     """Packed chunk experts + workspace for one drafter on one device."""
 
     def __init__(self, cfg: TreeFlowConfig, weights: dict, device="cuda"):
-        if cfg.init_mode != "delta":
-            raise ValueError("the fused flow implements init_mode='delta' (the drafter default)")
         self.cfg = cfg
         self.device = torch.device(device)
         if self.device.type == "cuda" and self.device.index is None:
@@ -93,7 +97,10 @@ class FusedFlow:
                        numerics: int | None = None) -> torch.Tensor:
         """ctx [B, context_size, d] fp16 (already front-padded; d = cfg.flow_dim) -> [B, draft_length, d]
         fp16, in the numerics the reference uses for this shape and batch (``reference_numerics``)
-        unless ``numerics`` names one."""
+        unless ``numerics`` names one.  With ``init_mode="noise"`` the initial latents are
+        ``torch.randn(B, draft_length, d, fp16) * noise_scale`` from torch's current generator on
+        the flow's device (``init_latents``, cf/drafters/tree_flow.py:154-155), written into ``out``
+        before the call."""
         cfg = self.cfg
         d = cfg.flow_dim
         if ctx.dim() != 3 or ctx.shape[1] != cfg.context_size or ctx.shape[2] != d:
@@ -111,6 +118,8 @@ class FusedFlow:
         if need > self.ws.numel():
             self.ws = torch.empty(need, dtype=torch.uint8, device=self.device)
         self.dims.numerics = reference_numerics(cfg, B) if numerics is None else int(numerics)
+        if cfg.init_mode == "noise":
+            out.copy_(torch.randn(B, cfg.draft_length, d, device=self.device, dtype=torch.float16) * cfg.noise_scale)
         _lib.check(_lib.lib().cfh_flow_integrate(C.byref(self.dims), self._experts, ctx.data_ptr(),
                                                  out.data_ptr(), self.ws.data_ptr(), B,
                                                  _lib.stream_handle()),

@@ -76,6 +76,7 @@ struct RowsArgs {
   int euler, last, ks, d, C, CS, nch, KD;
   int R;               // requests in the group (row r of the grid: request r / KD, draft row r % KD)
   int out_all;         // the OUT launch covered every row of each expert (R > 1), not just the current chunk's
+  int init;            // CFH_INIT_*: how z0 is formed
 };
 
 __global__ void __launch_bounds__(ROWT) k_rows(RowsArgs a) {
@@ -103,6 +104,7 @@ __global__ void __launch_bounds__(ROWT) k_rows(RowsArgs a) {
     }
     const h16* last = a.ctx + (size_t)(req * a.C + a.C - 1) * d;
     const h16* prev = a.ctx + (size_t)(req * a.C + a.C - 2) * d;
+    const h16* given = a.z_out + (size_t)r * d;
     const float step = (float)(rr + 1);
 #pragma unroll
     for (int k = 0; k < ROWQ; ++k) {
@@ -113,8 +115,14 @@ __global__ void __launch_bounds__(ROWT) k_rows(RowsArgs a) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const float lv = (float)last[q * 4 + t];
-          const float delta = r16(lv - (float)prev[q * 4 + t]);
-          o[t] = r16(lv + r16(step * delta));
+          if (a.init == CFH_INIT_GIVEN) {
+            o[t] = (float)given[q * 4 + t];
+          } else if (a.init == CFH_INIT_REPEAT_LAST) {
+            o[t] = lv;
+          } else {
+            const float delta = r16(lv - (float)prev[q * 4 + t]);
+            o[t] = r16(lv + r16(step * delta));
+          }
         }
         zv[k] = make_float4(o[0], o[1], o[2], o[3]);
         *(float4*)(a.z + (size_t)r * d + q * 4) = zv[k];
@@ -656,6 +664,7 @@ int integrate(const Plan& p, const cfh_flow_dims* dm, const void* const* experts
     {
       RowsArgs r = {};
       r.ctx = ctx_b; r.ctx_mom = w.ctx_mom; r.z = w.z; r.z_out = zo_b; r.euler = 0; r.last = 0; r.d = d; r.C = C;
+      r.init = dm->init_mode;
       r.CS = CS; r.nch = nch; r.KD = KD; r.R = Rg; r.out_all = p.R > 1;
       for (int c = 0; c < nch; ++c) {
         r.x[c] = w.x[c]; r.pos[c] = (const h16*)PTR(c, L.pos); r.tau[c] = w.tau[c];

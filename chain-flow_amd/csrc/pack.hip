@@ -34,6 +34,7 @@ bool flow_dims_ok(const cfh_flow_dims* d) {
   if (d->draft_length / d->chunk_size > 4) return false;
   if (d->flow_steps < 1 || d->flow_steps > 16) return false;
   if (d->numerics != CFH_FLOW_FUSED && d->numerics != CFH_FLOW_MODULES) return false;
+  if (d->init_mode < CFH_INIT_DELTA || d->init_mode > CFH_INIT_GIVEN) return false;
   return true;
 }
 

@@ -61,7 +61,19 @@ typedef struct cfh_flow_dims {
   int chunk_size;    /* chunk_size (4); draft_length % chunk_size == 0                     */
   int flow_steps;    /* num_flow_steps E (Euler steps); 1 <= E <= 16                       */
   int numerics;      /* CFH_FLOW_FUSED or CFH_FLOW_MODULES: the rounding points to follow      */
+  int init_mode;     /* CFH_INIT_DELTA, CFH_INIT_REPEAT_LAST or CFH_INIT_GIVEN (init_latents) */
 } cfh_flow_dims;
+
+/* The initial latents z0 of the Euler integration, per request (init_latents,
+ * cf/drafters/tree_flow.py:150-161), from the fp16 context rows c[0..C-1]:
+ *   CFH_INIT_DELTA        z0[k] = fp16(c[C-1] + fp16((k+1) * fp16(c[C-1] - c[C-2])))  ("delta")
+ *   CFH_INIT_REPEAT_LAST  z0[k] = c[C-1]                                              ("repeat_last")
+ *   CFH_INIT_GIVEN        z0 is read from z_out on entry ([batch][draft_length][d] fp16): for the
+ *                         reference's "noise" mode the caller draws randn(...) * noise_scale with
+ *                         its own generator, as the reference does. */
+#define CFH_INIT_DELTA 0
+#define CFH_INIT_REPEAT_LAST 1
+#define CFH_INIT_GIVEN 2
 
 /* The two fp16 numerics the reference runs its flow blocks in (both with fp32 accumulation, fp16
  * q/k/v, attention and LayerNorm outputs):

@@ -215,18 +215,20 @@ def expert_prefixes(num_chunks):
     return ["expert."] + [f"extra_experts.{i}." for i in range(num_chunks - 1)]
 
 
-def predict_hidden(W, context, cfg, numerics="fp16", return_trace=False):
+def predict_hidden(W, context, cfg, numerics="fp16", return_trace=False, z0=None):
     """``TreeFlowDrafter.predict_hidden`` (``cf/drafters/tree_flow.py:229-244``).
 
     context [B, C, d] (values in the expert dtype) -> z_E [B, draft_length, d].
-    cfg keys: draft_length, chunk_size, num_layers, num_heads, num_flow_steps, init_mode."""
+    cfg keys: draft_length, chunk_size, num_layers, num_heads, num_flow_steps, init_mode.
+    z0: the initial latents when given (``init_mode="noise"`` draws them from torch's generator,
+    ``tree_flow.py:154-155``: the caller passes the same draw)."""
     context = r16(context, numerics)
     K, cs, E = cfg["draft_length"], cfg["chunk_size"], cfg["num_flow_steps"]
     nch = K // cs
     pfxs = expert_prefixes(nch)
     kvs = [[cross_kv(W, f"{p}blocks.{l}.", context, numerics) for l in range(cfg["num_layers"])]
            for p in pfxs]
-    z = init_latents(context, K, numerics, cfg.get("init_mode", "delta"))
+    z = init_latents(context, K, numerics, cfg.get("init_mode", "delta")) if z0 is None else np.array(z0, copy=True)
     trace = [z.copy()]
     dt = 1.0 / E
     for s in range(E):

@@ -149,3 +149,33 @@ def test_packed_batch_matches_oracle_per_request(cuda, d, B, layers):
         print(f"  request {b}: vs oracle {e:.3e}, vs drafted alone {es:.3e}", flush=True)
         assert np.isfinite(to64(z[b:b + 1])).all()
         assert e < TOL_FP16 and es < TOL_FP16
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode,B", [("repeat_last", 1), ("noise", 1), ("noise", 2)])
+def test_init_modes_match_oracle(cuda, mode, B):
+    """init_latents' other modes (cf/drafters/tree_flow.py:150-161): "repeat_last" starts every
+    draft row from the last context row; "noise" from randn * noise_scale drawn with torch's
+    generator, which the oracle is given (the same seeded draw)."""
+    import dataclasses
+    cfg = dataclasses.replace(flownet(512, layers=2, flow_steps=2), init_mode=mode, noise_scale=0.5)
+    W = _flow_weights(cfg)
+    ctx = synthetic_context(B, cfg.context_size, 512, seed=5)
+    print(f"[flow init] mode={mode} B={B}", flush=True)
+    ff = FusedFlow(cfg, {k: v.to(cuda) for k, v in W.items()}, device=cuda)
+    torch.manual_seed(11)
+    z = ff.predict_hidden(ctx.to(cuda))
+    torch.cuda.synchronize()
+    z0 = None
+    if mode == "noise":
+        torch.manual_seed(11)
+        z0 = to64(torch.randn(B, cfg.draft_length, 512, device=cuda, dtype=torch.float16) * cfg.noise_scale)
+    ref = oflow.predict_hidden(weights64(W), to64(ctx), _ocfg(cfg), numerics=oracle_numerics(cfg, B), z0=z0)
+    err = rel_err(to64(z), ref)
+    print(f"  rel err {err:.3e}", flush=True)
+    assert np.isfinite(to64(z)).all()
+    assert err < TOL_FP16
+    if mode == "noise":     # a fresh draw gives a different draft
+        z2 = ff.predict_hidden(ctx.to(cuda))
+        torch.cuda.synchronize()
+        assert not torch.equal(z, z2)

@@ -63,3 +63,21 @@ def test_noalloc_flow_rejects_a_workspace_beyond_the_scratch_without_a_device():
     experts = _lib.ptr_array([p, p])
     assert L.cfh_flow_integrate_noalloc(C.byref(dims), experts, p, p, 1, None) == 4
     assert L.cfh_flow_integrate_noalloc(C.byref(dims), experts, p, p, 0, None) == 1    # batch < 1
+
+
+def test_flow_dims_carry_the_init_mode():
+    """init_latents' three modes reach cfh_flow_dims.init_mode ("noise" as a z0 the caller draws),
+    and a checkpoint's noise_scale survives the config loader (reference default 1.0,
+    cf/drafters/tree_flow.py:53)."""
+    import dataclasses
+    from chain_flow_amd.config import config_from_model_args, flownet
+    from chain_flow_amd.flow import flow_dims
+    base = flownet(512, layers=1, flow_steps=1)
+    assert base.noise_scale == 1.0
+    for mode, want in (("delta", _lib.INIT_DELTA), ("repeat_last", _lib.INIT_REPEAT_LAST),
+                       ("noise", _lib.INIT_GIVEN)):
+        assert flow_dims(dataclasses.replace(base, init_mode=mode)).init_mode == want
+    args = dict(context_size=8, draft_length=8, chunk_size=4, expert_dim=512, init_mode="noise",
+                noise_scale=0.25, drafter_dropout=0.1)
+    cfg = config_from_model_args(args)
+    assert cfg.init_mode == "noise" and cfg.noise_scale == 0.25

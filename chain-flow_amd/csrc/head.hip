@@ -518,10 +518,11 @@ __global__ void __launch_bounds__(TK_THREADS) k_topk(TopkArgs a) {
 }
 
 // ---------------------------------------------------------------------------- MFMA GEMM head
-// Batched head (M up to 256 rows, bf16): a workgroup of GW waves owns GW*NT*16 vocabulary rows;
-// each wave streams NT row tiles in place through the shortlist and multiplies every B fragment
-// against the MT 16-row tiles of the activations (v_mfma_f32_16x16x32_bf16), so one weight byte
-// feeds 16*MT rows.  The activations pass through LDS in 128-column chunks, double-buffered: the
+// Batched head (M up to 256 rows, bf16, or fp16 with the markov bias): a workgroup of GW waves
+// owns GW*NT*16 vocabulary rows; each wave streams NT row tiles (in place through the shortlist,
+// or from the packed image with non-temporal loads) and multiplies every B fragment against the MT
+// 16-row tiles of the activations (v_mfma_f32_16x16x32_bf16 / _f16), so one weight byte feeds
+// 16*MT rows.  The activations pass through LDS in 128-column chunks, double-buffered: the
 // next chunk's loads are in flight while the current one is multiplied.  The weight fragments
 // alternate between two register sets by chunk parity, so each chunk's weights are requested a
 // whole chunk of multiplies ahead.  Two waves a SIMD (GW = 8) keep the accumulators and both sets
@@ -582,9 +583,8 @@ __device__ __forceinline__ float gemm_value(unsigned b) {
 // parked in LDS as [rows][COLS + 8] over the operand buffers (the caller has passed a barrier after
 // its last operand read).  Then one 16-lane group a row ranks the block's COLS columns: lane l holds
 // columns l*CPL .. l*CPL+CPL-1 as 32-bit keys (order-preserving 16-bit logit << 16 | 0xFFFF -
-// column), so one integer max picks the larger logit and, on a tie, the lower column; a round is
-// CPL-1 maxes, 4 DPP steps and the winner's removal.  Key 0 = no column.  The block's top-k and
-// (max, sum of exp) go to the candidate lists for the merge.
+// column), so one integer max picks the larger logit and, on a tie, the lower column.  Key 0 = no
+// column.  The block's top-k and (max, sum of exp) go to the candidate lists for the merge.
 template <int MTW, int NT, int COLS, int NTHR, int ROWS, bool F16>
 __device__ __forceinline__ void gemm_finish(const GemmArgs& a, const f32x4 (&acc)[MTW][NT], uint16_t* lg, int rt0,
                                             int c0) {

@@ -49,6 +49,14 @@ constexpr float LN_EPS = 1e-5f;
 
 enum Src { SRC_BUF = 0, SRC_CTX, SRC_TAU, SRC_GATHER };
 
+// The MFMA operand image of an [S][N] fp16 block (S <= 16 rows): the 8 values (r, 32 s + 8 g .. +7)
+// of row r, which one lane of a 16x16x32 MFMA takes for k-step s and k-group g, form vector
+// (4 s + g) S + r.  A wave's load of one k-step then reads 4 S contiguous 16-byte vectors, one per
+// live lane, instead of 64-byte pieces of S rows a row apart.
+__host__ __device__ __forceinline__ size_t frag_index(int r, int n, int S) {
+  return (((size_t)(n >> 5) * 4 + ((n >> 3) & 3)) * S + r) * 8 + (n & 7);
+}
+
 // ---------------------------------------------------------------------------- GEMV
 struct GemvEx {
   const h16x8* w;      // packed weight fragments (layer 0 when nl > 1)

@@ -32,6 +32,7 @@ struct SEx {
   void* out;           // E_PART: float [ks][S][N]; E_PART16: h16 [ks][S][N]; otherwise h16 [S][N]
   int S;               // activation rows (<= 16)
   int Sr;              // S_SELF / S_CROSS: rows per request (requests packed in the S rows; 0 = S)
+  int pack;            // E_PART16: each k-chunk's [S][N] block in frag_index order
 };
 
 // For the attention kinds a k-chunk of KC = K / ks columns holds KC / hd whole heads (one head
@@ -318,7 +319,8 @@ __global__ void __launch_bounds__(WV * 64) k_stream(SArgs a) {
           if constexpr (EPI == E_PART) {
             ((float*)ex.out)[((size_t)kc * ex.S + r) * a.N + n] = acc[q];
           } else if constexpr (EPI == E_PART16) {
-            ((h16*)ex.out)[((size_t)kc * ex.S + r) * a.N + n] = (h16)acc[q];
+            h16* o = (h16*)ex.out + (size_t)kc * ex.S * a.N;
+            o[ex.pack ? frag_index(r, n, ex.S) : (size_t)r * a.N + n] = (h16)acc[q];
           } else {
             float bv;
             if (ct == 0) bv = bias0;
@@ -484,6 +486,7 @@ struct ResArgs {
   h16* a[4];
   int rows[4];
   int nex, ks, d, mode;
+  int pack;            // LN rows written in frag_index order (the folded cross attention's operand)
 };
 
 __device__ __forceinline__ float block_sum_rt(float v, float* red) {  // red[blockDim/64]
@@ -574,7 +577,7 @@ __device__ void res_row(const ResArgs& a, int e, int r) {
     o[1] = (h16)((vals[k].y - mean) * rstd * (float)gq[k][1] + (float)btq[k][1]);
     o[2] = (h16)((vals[k].z - mean) * rstd * (float)gq[k][2] + (float)btq[k][2]);
     o[3] = (h16)((vals[k].w - mean) * rstd * (float)gq[k][3] + (float)btq[k][3]);
-    if (c < d) *(h16x4*)(out + c) = o;
+    if (c < d) *(h16x4*)(a.pack ? a.a[e] + frag_index(r, c, a.rows[e]) : out + c) = o;
   }
 }
 

@@ -578,6 +578,9 @@ __device__ __forceinline__ float gemm_value(unsigned b) {
   else return __uint_as_float(b << 16);
 }
 
+// median of three (one v_med3_u32)
+__device__ __forceinline__ unsigned umed3(unsigned a, unsigned b, unsigned c) { return max(min(a, b), min(max(a, b), c)); }
+
 // Epilogue of the GEMM heads.  The wave's accumulators -- row tiles rt0 .. rt0+MTW-1, columns
 // c0 .. c0+NT*16-1 of the block's COLS -- become 16-bit logits (gemm_logit), written to a.logits and
 // parked in LDS as [rows][COLS + 8] over the operand buffers (the caller has passed a barrier after
@@ -634,9 +637,11 @@ __device__ __forceinline__ void gemm_finish(const GemmArgs& a, const f32x4 (&acc
   // wins a fifth time: a row's top k rarely takes more than four of one lane's sixteen columns.
   constexpr int NGR = NTHR / 16, RPG = (ROWS + NGR - 1) / NGR, NIT = (RPG + 4) / 5, RB = (RPG + NIT - 1) / NIT;
   const int nrem = a.n - (int)blockIdx.x * COLS - col * CPL;   // the lane's columns: i < nrem
+  const bool whole = (int)(blockIdx.x + 1) * COLS <= a.n;      // every column of the block is live
   // the four largest keys below lim of the lane's columns of row r (keys past the shortlist: 0).
-  // Arithmetic throughout: compares here would each hold an SGPR-pair mask.
-  auto lane_top4 = [&](int r, unsigned lim, bool limited, unsigned (&q)[4]) {
+  // Arithmetic throughout: compares here would each hold an SGPR-pair mask.  A key enters the
+  // sorted four with one max and three medians of three (v_med3_u32).
+  auto lane_top4 = [&](int r, unsigned lim, bool limited, bool masked, unsigned (&q)[4]) {
     q[0] = q[1] = q[2] = q[3] = 0u;
 #pragma unroll
     for (int h = 0; h < CPL / 8; ++h) {
@@ -652,37 +657,38 @@ __device__ __forceinline__ void gemm_finish(const GemmArgs& a, const f32x4 (&acc
         for (int e = 0; e < 2; ++e) {
           const int i = h * 8 + w * 2 + e, c = col * CPL + i;
           unsigned t = (e ? (x & 0xFFFF0000u) : (x << 16)) | (0xFFFFu - (unsigned)c);
-          t &= 0u - ((unsigned)(i - nrem) >> 31);
+          if (masked) t &= 0u - ((unsigned)(i - nrem) >> 31);
           if (limited) t = t < lim ? t : 0u;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const unsigned hi = max(q[j], t);
-            t = min(q[j], t);
-            q[j] = hi;
-          }
+          const unsigned n0 = max(q[0], t), n1 = umed3(q[0], q[1], t), n2 = umed3(q[1], q[2], t),
+                         n3 = umed3(q[2], q[3], t);
+          q[0] = n0; q[1] = n1; q[2] = n2; q[3] = n3;
         }
       }
     }
   };
-  // The winners and each row's (max, sum-exp) are staged in LDS after the logits, written by every
-  // lane of the group (the same value: no branch), rows past M into a dummy slot ROWS; one pass at
-  // the end copies them out.  Branches inside a round would split it into blocks the compiler
-  // cannot interleave across rows (and copy the rows' lists at each).
-  float* cstv = (float*)(lg + ROWS * LST);
-  int* csti = (int*)(cstv + (ROWS + 1) * KMAX);
-  float* cstm = (float*)(csti + (ROWS + 1) * KMAX);
+  // The winners' keys and each row's (max, sum-exp) are staged in LDS after the logits, written by
+  // every lane of the group (the same value: no branch), rows past M into a dummy slot ROWS; one
+  // pass at the end decodes the keys into (value, column) and copies them out.  Branches inside a
+  // round would split it into blocks the compiler cannot interleave across rows (and copy the
+  // rows' lists at each).
+  auto key_value = [](unsigned key) -> float {
+    const unsigned o = key >> 16;
+    return key ? gemm_value<F16>((o & 0x8000u) ? (o & 0x7FFFu) : (~o & 0xFFFFu)) : -INFINITY;
+  };
+  unsigned* cstk = (unsigned*)(lg + ROWS * LST);
+  float* cstm = (float*)(cstk + (ROWS + 1) * KMAX);
   float* csts = cstm + (ROWS + 1);
   for (int r0 = threadIdx.x >> 4; r0 < a.M; r0 += NGR * RB) {
-    unsigned q[RB][4], fl[RB];
+    unsigned q[RB][4], fl[RB], k0[RB];
     bool full[RB];
-    float mx[RB];
     int slot[RB];
 #pragma unroll
     for (int b = 0; b < RB; ++b) {
       const int r = r0 + b * NGR;
       slot[b] = r < a.M ? r : ROWS;
-      if (r < a.M) lane_top4(r, 0u, false, q[b]);
-      else q[b][0] = q[b][1] = q[b][2] = q[b][3] = 0u;
+      if (r >= a.M) q[b][0] = q[b][1] = q[b][2] = q[b][3] = 0u;
+      else if (whole) lane_top4(r, 0u, false, false, q[b]);
+      else lane_top4(r, 0u, false, true, q[b]);
       fl[b] = 0xFFFFFFFFu;
       full[b] = q[b][3] != 0u;
     }
@@ -707,18 +713,14 @@ __device__ __forceinline__ void gemm_finish(const GemmArgs& a, const f32x4 (&acc
         q[b][3] = win ? 0u : q[b][3];
         need[b] = win && full[b] && q[b][0] == 0u;
         any |= need[b];
-        const unsigned o = m[b] >> 16;
-        const unsigned v = (o & 0x8000u) ? (o & 0x7FFFu) : (~o & 0xFFFFu);
-        const float bv = m[b] ? gemm_value<F16>(v) : -INFINITY;
-        mx[b] = rr == 0 ? bv : mx[b];
-        cstv[slot[b] * KMAX + rr] = bv;
-        csti[slot[b] * KMAX + rr] = m[b] ? blockIdx.x * COLS + (int)(0xFFFFu - (m[b] & 0xFFFFu)) : INT_MAX;
+        k0[b] = rr == 0 ? m[b] : k0[b];
+        cstk[slot[b] * KMAX + rr] = m[b];
       }
       if (__builtin_amdgcn_ballot_w64(any)) {      // rare: a lane won a fifth time
 #pragma unroll
         for (int b = 0; b < RB; ++b)
           if (need[b]) {
-            lane_top4(r0 + b * NGR, fl[b], true, q[b]);
+            lane_top4(r0 + b * NGR, fl[b], true, true, q[b]);
             full[b] = q[b][3] != 0u;
           }
       }
@@ -727,9 +729,10 @@ __device__ __forceinline__ void gemm_finish(const GemmArgs& a, const f32x4 (&acc
 #pragma unroll
     for (int b = 0; b < RB; ++b) {
       const int r = r0 + b * NGR;
+      const float mx = key_value(k0[b]);
       float se = 0.f;
-      if (r < a.M && mx[b] != -INFINITY) {
-        const float nm = -mx[b] * 1.4426950408889634f;
+      if (r < a.M && mx != -INFINITY) {
+        const float nm = -mx * 1.4426950408889634f;
 #pragma unroll
         for (int h = 0; h < CPL / 8; ++h) {
           const uint4 u = *(const uint4*)(lg + r * LST + col * CPL + h * 8);
@@ -743,7 +746,7 @@ __device__ __forceinline__ void gemm_finish(const GemmArgs& a, const f32x4 (&acc
         }
       }
       se = row_sum(se);
-      cstm[slot[b]] = mx[b];
+      cstm[slot[b]] = mx;
       csts[slot[b]] = se;
     }
   }
@@ -751,8 +754,9 @@ __device__ __forceinline__ void gemm_finish(const GemmArgs& a, const f32x4 (&acc
   for (int i = threadIdx.x; i < a.M * a.k; i += NTHR) {
     const int r = i / a.k, rr = i - r * a.k;
     const size_t base = ((size_t)r * a.nsets + blockIdx.x) * a.k + rr;
-    cd.cv[base] = cstv[r * KMAX + rr];
-    cd.ci[base] = csti[r * KMAX + rr];
+    const unsigned key = cstk[r * KMAX + rr];
+    cd.cv[base] = key_value(key);
+    cd.ci[base] = key ? (int)blockIdx.x * COLS + (int)(0xFFFFu - (key & 0xFFFFu)) : INT_MAX;
   }
   for (int r = threadIdx.x; r < a.M; r += NTHR) {
     const size_t base = (size_t)r * a.nsets + blockIdx.x;
@@ -876,7 +880,7 @@ template <int MT, int NT, int GW, int MS>
 size_t gemm_lds() {
   const size_t xbuf = 2 * (size_t)MT * 16 * GKC * 2;                      // x double buffer
   const size_t lgt = (size_t)MT * 16 * (GW / MS * NT * 16 + 8) * 2 +      // the block's logits,
-                     ((size_t)MT * 16 + 1) * (KMAX * 8 + 8);              // staged winners, (max, sum)
+                     ((size_t)MT * 16 + 1) * (KMAX * 4 + 8);              // staged winners' keys, (max, sum)
   return xbuf > lgt ? xbuf : lgt;
 }
 

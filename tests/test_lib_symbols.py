@@ -81,3 +81,40 @@ def test_flow_dims_carry_the_init_mode():
                 noise_scale=0.25, drafter_dropout=0.1)
     cfg = config_from_model_args(args)
     assert cfg.init_mode == "noise" and cfg.noise_scale == 0.25
+
+
+def test_flow_caps_shape_checks_without_a_device():
+    """cfh_caps decides support and the workspace size on the host: the headline and latent
+    shapes are supported; at d = 4096 a batch of two shares each weight stream in one request group
+    (a larger workspace), at d = 5120 it runs one request a group (a 16-row operand of 5120 columns
+    would not fit the streaming kernels' LDS); each out-of-range field of cfh_flow_dims is refused
+    as unsupported."""
+    import ctypes as C
+    import dataclasses
+
+    from chain_flow_amd.config import flownet
+    from chain_flow_amd.flow import flow_dims
+    L = _lib.lib()
+
+    def caps(dims, batch=1):
+        ws = C.c_int64(-1)
+        rc = L.cfh_caps(C.byref(dims), batch, C.byref(ws))
+        return rc, ws.value
+
+    head = flownet(5120, layers=8, flow_steps=8)
+    rc1, ws1 = caps(flow_dims(head))
+    assert rc1 == 0 and ws1 > 0 and caps(flow_dims(head), 2) == (0, ws1)
+    c4 = flow_dims(flownet(4096, layers=8, flow_steps=8))
+    assert caps(c4)[0] == 0 and caps(c4, 2)[1] > caps(c4)[1]
+    assert caps(flow_dims(flownet(640, layers=8, flow_steps=2)))[0] == 0
+    assert caps(flow_dims(head), 0)[0] == 2                                   # batch < 1
+    bad = [("d", 5120 + 32), ("heads", 7), ("ffn_mult", 9), ("layers", 0), ("ctx_rows", 1),
+           ("ctx_rows", 17), ("chunk_size", 3), ("draft_length", 17), ("flow_steps", 17),
+           ("numerics", 7), ("init_mode", 3)]
+    for field, value in bad:
+        dims = flow_dims(head)
+        setattr(dims, field, value)
+        assert caps(dims)[0] == 2, (field, value)
+    assert L.cfh_caps(None, 1, None) == 2
+    # a config field the flow ignores leaves the plan alone
+    assert caps(flow_dims(dataclasses.replace(head, noise_scale=0.5)))[1] == ws1

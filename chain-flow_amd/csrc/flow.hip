@@ -14,7 +14,7 @@
 // covers both chunk experts (they are independent within an Euler step), so each weight-streaming
 // launch moves the weights of two experts.  A batch is drafted in groups of R requests whose rows
 // share one MFMA tile (R x draft_length <= 16: two 8-row drafts, where the 16-row operand fits the
-// streaming kernels' LDS, i.e. d <= 4096), so every weight stream serves R drafts; attention masks
+// streaming kernels' LDS: d <= 4096 of the supported widths), so every weight stream serves R drafts; attention masks
 // keep each request to its own rows and context.  Work that needs a whole row sits in a small row
 // kernel between two streaming kernels; there is no cross-workgroup synchronisation inside any kernel (no fences, no
 // atomics, no spin-waits), so results are deterministic.  On MI355X the gap between two kernels on

@@ -14,12 +14,13 @@
 // covers both chunk experts (they are independent within an Euler step), so each weight-streaming
 // launch moves the weights of two experts.  A batch is drafted in groups of R requests whose rows
 // share one MFMA tile (R x draft_length <= 16: two 8-row drafts, where the 16-row operand fits the
-// streaming kernels' LDS: d <= 4096 of the supported widths), so every weight stream serves R drafts; attention masks
-// keep each request to its own rows and context.  Work that needs a whole row sits in a small row
-// kernel between two streaming kernels; there is no cross-workgroup synchronisation inside any kernel (no fences, no
-// atomics, no spin-waits), so results are deterministic.  On MI355X the gap between two kernels on
-// the stream is 1.4-2 us (per-workgroup timestamps), while a fenced grid barrier across the 8 XCDs
-// costs ~12 us, which is why this is a kernel pipeline and not one persistent launch.
+// streaming kernels' LDS: d <= 4096 of the supported widths), so every weight stream serves R
+// drafts; attention masks keep each request to its own rows and context.  Work that needs a whole
+// row sits in a small row kernel between two streaming kernels; there is no cross-workgroup
+// synchronisation inside any kernel (no fences, no atomics, no spin-waits), so results are
+// deterministic.  On MI355X the gap between two kernels on the stream is 1.4-2 us (per-workgroup
+// timestamps), while a fenced grid barrier across the 8 XCDs costs ~12 us, which is why this is a
+// kernel pipeline and not one persistent launch.
 //
 //   per draft : TAU  time_mlp(tau_s) for all E steps     (GEMV + reduce)
 //               ROWS init_latents(ctx), step-0 rows x, a = LN_self(x) of block 0

@@ -10,9 +10,11 @@
 // torch's fp16 modules' (x = fp16(x + fp16(sublayer)); GELU of the fp16-rounded up-projection), as
 // cfh_flow_dims.numerics says; only the residual row kernel and the W1 epilogue differ.
 //
-// Execution plan.  One launch sequence per group of requests on the caller's stream; every launch
-// covers both chunk experts (they are independent within an Euler step), so each weight-streaming
-// launch moves the weights of two experts.  A batch is drafted in groups of R requests whose rows
+// Execution plan.  One launch sequence per group of requests.  The per-draft launches cover every
+// chunk expert at once; within an Euler step the experts are independent, so each runs its block
+// passes on its own stream (the caller's, then companion streams forked at the step and joined
+// before the Euler update), and one expert's row kernels and launch gaps overlap another's weight
+// streaming.  A batch is drafted in groups of R requests whose rows
 // share one MFMA tile (R x draft_length <= 16: two 8-row drafts, where the 16-row operand fits the
 // streaming kernels' LDS: d <= 4096 of the supported widths), so every weight stream serves R
 // drafts; attention masks keep each request to its own rows and context.  Work that needs a whole
@@ -26,7 +28,7 @@
 //               ROWS init_latents(ctx), step-0 rows x, a = LN_self(x) of block 0
 //               KV   cross K/V of every block             (GEMV + reduce)
 //               FOLD per block: A_h = Wq_h^T K_h^T, B_h = Wo_h V_h   (stream, split-K by head)
-//   per Euler step, per block l (both experts in every launch):
+//   per Euler step, per block l (each expert on its own stream):
 //     QKV   stream  A = a (LN_self rows)          epilogue q,k,v = fp16(acc + b)      full-K tiles
 //     O     stream  A = causal self attention of head h, computed while staging    split-K by head
 //     RES   row     x += sum_h P + b_o ; a = LN_cross(fp16(x))

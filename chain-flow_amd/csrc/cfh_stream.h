@@ -46,7 +46,15 @@ struct SArgs {
   int causal;          // S_SELF: causal mask triu(-inf, 1) (the flow's draft rows) or none
   int gelu_r16;        // E_GELU16: round acc + bias to fp16 before the GELU (a Linear module
                        // followed by a GELU module) instead of once after it (the fused block)
+  int conc;            // launches of this shape running concurrently (one per chunk expert's stream)
 };
+
+// LDS that concurrent streaming launches reserve when together they fit one workgroup a CU:
+// above half a CU's LDS, so their workgroups spread over the CUs.  Left to share, the two experts'
+// workgroups pile onto the CUs where they fit twice while other CUs idle (d = 2560: 7.92 against
+// 7.52 ms a flow pass reserved); when they do not fit one a CU (d = 1024), sharing is better
+// (3.97 against 4.48 ms), and where one a CU is the most that fits anyway (d = 5120) it is neutral.
+constexpr size_t CONC_LDS = 82 * 1024;
 
 // Attention of the KC / hd heads of a k-chunk for the S rows of one expert from q, k, v already in
 // LDS (sq [S][KC], sk and sv [Sk][KC], Sk <= 16; head hh in columns [hh hd, hh hd + hd)), written
@@ -386,6 +394,11 @@ int launch_stream_k(const SArgs& a, size_t lds, hipStream_t st) {
     attr_set |= 1ull << dev;
   }
   const long long wgs = (long long)a.nex * a.ks * a.wg_per_kc;
+  if (a.conc > 1) {
+    static int cus[64] = {};
+    if (dev < 64 && !cus[dev]) CFH_HIP(hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev));
+    if (dev < 64 && wgs * a.conc <= cus[dev]) lds = std::max(lds, CONC_LDS);
+  }
   hipLaunchKernelGGL((k_stream<SRC, EPI, SPF, NS, WV>), dim3((unsigned)wgs), dim3(a.wpb * 64), lds, st, a);
   CFH_LAUNCH_CHECK();
   return CFH_OK;

@@ -535,6 +535,7 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
   // QKV: q, k, v = fp16(LN_self(x) W_in^T + b_in), full-K tiles
   {
     SArgs a = {};
+    a.conc = p.nch / nc;
     a.nex = nch; a.N = 3 * d; a.K = d; a.ks = 1; a.wpb = p.wpb_full; a.tpw = 1; a.d = d; a.hd = p.hd;
     a.wg_per_kc = (3 * d / 16) / (a.wpb * a.tpw);
     for (int c = 0; c < nch; ++c) {
@@ -547,6 +548,7 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
   // O: causal self attention per head, staged, then out_proj split-K by head (group)
   {
     SArgs a = {};
+    a.conc = p.nch / nc;
     a.nex = nch; a.N = d; a.K = d; a.ks = p.ks_att; a.wpb = p.wpb_att; a.tpw = p.tpw_att; a.d = d; a.hd = p.hd;
     a.causal = 1;
     a.wg_per_kc = (d / 16) / (a.wpb * a.tpw);
@@ -582,6 +584,7 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
   // QC: cross-attention query projection, split-K partials
   if (!p.fold) {
     SArgs a = {};
+    a.conc = p.nch / nc;
     a.nex = nch; a.N = d; a.K = d; a.ks = p.ks_qc; a.wpb = p.wpb_qc; a.tpw = 1; a.d = d; a.hd = p.hd;
     a.wg_per_kc = (d / 16) / (a.wpb * a.tpw);
     for (int c = 0; c < nch; ++c) {
@@ -593,6 +596,7 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
   // OC: cross attention per head over the hoisted context K/V, staged, then out_proj split-K by head
   if (!p.fold) {
     SArgs a = {};
+    a.conc = p.nch / nc;
     a.nex = nch; a.N = d; a.K = d; a.ks = p.ks_att; a.wpb = p.wpb_att; a.tpw = p.tpw_att; a.d = d; a.hd = p.hd;
     a.ks_in = p.ks_qc; a.Ck = Cg; a.Cr = p.C;
     a.wg_per_kc = (d / 16) / (a.wpb * a.tpw);
@@ -612,6 +616,7 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
   // W1: g = fp16(gelu(LN_ffn(x) W1^T + b1)), full-K tiles
   {
     SArgs a = {};
+    a.conc = p.nch / nc;
     a.nex = nch; a.N = fd; a.K = d; a.ks = 1; a.wpb = p.wpb_w1; a.tpw = 1; a.d = d; a.hd = p.hd;
     a.gelu_r16 = p.res_mode == RES_ADD16;   // torch's Linear rounds before its GELU module
     a.wg_per_kc = (fd / 16) / (a.wpb * a.tpw);
@@ -625,6 +630,7 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
   // W2: split-K partials
   {
     SArgs a = {};
+    a.conc = p.nch / nc;
     a.nex = nch; a.N = d; a.K = fd; a.ks = p.ks_w2; a.wpb = p.wpb_w2; a.tpw = 1; a.d = d; a.hd = p.hd;
     a.wg_per_kc = (d / 16) / (a.wpb * a.tpw);
     for (int c = 0; c < nch; ++c) {
@@ -815,6 +821,7 @@ int integrate(const Plan& p, const cfh_flow_dims* dm, const void* const* experts
       // are packed: their current rows are not contiguous, and the weights stream once either way)
       for (int c = 0; c < nch; ++c) {
         SArgs a = {};
+        a.conc = nch;
         a.nex = 1; a.N = d; a.K = d; a.ks = p.ks_out; a.wpb = p.wpb_out; a.tpw = 1; a.d = d; a.hd = p.hd;
         a.wg_per_kc = (d / 16) / (a.wpb * a.tpw);
         SEx& x = a.ex[0];

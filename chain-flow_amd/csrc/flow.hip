@@ -375,6 +375,7 @@ struct Plan {
   int pks;            // partial slots per expert
   int res_mode;       // RES_ADD32 (fused-kernel numerics) or RES_ADD16 (torch fp16 modules)
   bool fold;          // cross attention folded into per-draft factors (cfh::xattn_fold)
+  bool conc;          // chunk experts on concurrent streams within an Euler step (conc_experts)
   int wpb_fold, xnb;  // fold hoist launch waves / XATT column blocks per (expert, head)
   bool ok;
 };
@@ -391,6 +392,10 @@ Plan make_plan(const cfh_flow_dims* dm, int R = 1) {
   const int out_rows = R == 1 ? p.CS : p.Smax;   // OUT: the current chunk's rows, or every row when packed
   p.res_mode = dm->numerics == CFH_FLOW_MODULES ? RES_ADD16 : RES_ADD32;
   p.fold = cfh::xattn_fold(dm);
+  // Concurrent chunk experts double the block passes' launches; below d = 1024 the host's launch
+  // rate, not the GPU, then sets the pace of an eager draft (the latent flow at d = 640: +0.13 ms a
+  // draft on two streams), so narrow shapes keep every expert in one launch.
+  p.conc = p.nch > 1 && p.d >= 1024;
   const int tiles_d = p.d / 16;
   const size_t cap = 96 * 1024;
   // (one k-chunk when K has fewer than 8 k-steps: small latent widths)
@@ -698,7 +703,7 @@ int integrate(const Plan& p, const cfh_flow_dims* dm, const void* const* experts
   auto BLK = [&](int l) { return L.blk0 + (size_t)l * L.blkstride; };
   Companions cp = {};
   if (nch > MAX_CHUNKS) return CFH_E_UNSUPPORTED;
-  if (nch > 1 && (rc = companions(st, &cp))) return rc;
+  if (p.conc && (rc = companions(st, &cp))) return rc;
 
   // ---- time embeddings of every step (the same for every request)
   {
@@ -810,35 +815,45 @@ int integrate(const Plan& p, const cfh_flow_dims* dm, const void* const* experts
     }
     for (int s = 0; s < E; ++s) {
       // each chunk expert on its own stream until the Euler update
-      if (nch > 1) {
+      if (p.conc) {
         CFH_HIP(hipEventRecord(cp.fork, st));
         for (int c = 1; c < nch; ++c) CFH_HIP(hipStreamWaitEvent(cp.s[c - 1], cp.fork, 0));
       }
-      for (int l = 0; l < NL; ++l)
+      for (int l = 0; l < NL; ++l) {
+        if (!p.conc) {
+          if ((rc = block_pass(p, L, w, experts, l, Rg, st, 0, nch))) return rc;
+          continue;
+        }
         for (int c = 0; c < nch; ++c)
           if ((rc = block_pass(p, L, w, experts, l, Rg, c == 0 ? st : cp.s[c - 1], c, 1))) return rc;
+      }
       // OUT: out_proj on the out_norm rows of each expert's current chunk (every row when requests
       // are packed: their current rows are not contiguous, and the weights stream once either way)
-      for (int c = 0; c < nch; ++c) {
+      // (each expert on its stream, or every expert in one launch)
+      for (int c0 = 0; c0 < nch; c0 += p.conc ? 1 : nch) {
+        const int nc = p.conc ? 1 : nch;
         SArgs a = {};
-        a.conc = nch;
-        a.nex = 1; a.N = d; a.K = d; a.ks = p.ks_out; a.wpb = p.wpb_out; a.tpw = 1; a.d = d; a.hd = p.hd;
+        a.conc = nch / nc;
+        a.nex = nc; a.N = d; a.K = d; a.ks = p.ks_out; a.wpb = p.wpb_out; a.tpw = 1; a.d = d; a.hd = p.hd;
         a.wg_per_kc = (d / 16) / (a.wpb * a.tpw);
-        SEx& x = a.ex[0];
-        x.w = (const h16x8*)PTR(c, L.out); x.lda = d; x.out = w.P[c];
-        if (p.R == 1) {
-          x.a = w.abuf[c] + (size_t)c * CS * d;
-          x.S = CS;
-        } else {
-          x.a = w.abuf[c];
-          x.S = Rg * (c + 1) * CS;
+        for (int c = c0; c < c0 + nc; ++c) {
+          SEx& x = a.ex[c - c0];
+          x.w = (const h16x8*)PTR(c, L.out); x.lda = d; x.out = w.P[c];
+          if (p.R == 1) {
+            x.a = w.abuf[c] + (size_t)c * CS * d;
+            x.S = CS;
+          } else {
+            x.a = w.abuf[c];
+            x.S = Rg * (c + 1) * CS;
+          }
         }
-        if ((rc = launch_stream<S_BUF, E_PART>(a, p.R == 1 ? CS : p.Smax, c == 0 ? st : cp.s[c - 1]))) return rc;
+        if ((rc = launch_stream<S_BUF, E_PART>(a, p.R == 1 ? CS : p.Smax, c0 == 0 ? st : cp.s[c0 - 1]))) return rc;
       }
-      for (int c = 1; c < nch; ++c) {
-        CFH_HIP(hipEventRecord(cp.join[c - 1], cp.s[c - 1]));
-        CFH_HIP(hipStreamWaitEvent(st, cp.join[c - 1], 0));
-      }
+      if (p.conc)
+        for (int c = 1; c < nch; ++c) {
+          CFH_HIP(hipEventRecord(cp.join[c - 1], cp.s[c - 1]));
+          CFH_HIP(hipStreamWaitEvent(st, cp.join[c - 1], 0));
+        }
       RowsArgs r = {};
       r.ctx = ctx_b; r.z = w.z; r.z_out = zo_b; r.euler = 1; r.last = (s + 1 == E); r.ks = p.ks_out;
       r.dt = 1.0f / (float)E; r.d = d; r.C = C; r.CS = CS; r.nch = nch; r.KD = KD; r.R = Rg; r.out_all = p.R > 1;

@@ -11,13 +11,14 @@
 // cfh_flow_dims.numerics says; only the residual row kernel and the W1 epilogue differ.
 //
 // Execution plan.  One launch sequence per group of requests.  The per-draft launches cover every
-// chunk expert at once; within an Euler step the experts are independent, so each runs its block
-// passes on its own stream (the caller's, then companion streams forked at the step and joined
-// before the Euler update), and one expert's row kernels and launch gaps overlap another's weight
-// streaming.  A batch is drafted in groups of R requests whose rows
-// share one MFMA tile (R x draft_length <= 16: two 8-row drafts, where the 16-row operand fits the
-// streaming kernels' LDS: d <= 4096 of the supported widths), so every weight stream serves R
-// drafts; attention masks keep each request to its own rows and context.  Work that needs a whole
+// chunk expert at once; then each expert runs its Euler steps on its own stream (the caller's, then
+// companion streams), and one expert's row kernels and launch gaps overlap another's weight
+// streaming.  Within a step the experts are independent; expert c's next rows read the rows of the
+// chunks before c as the step left them (tree_flow.py _chunk_args), so only its Euler update waits
+// for theirs (and an expert's next update waits until the next expert has read its chunk's rows).
+// A batch is drafted in groups of R requests whose rows share one MFMA tile (R x draft_length
+// <= 16: two 8-row drafts, where the 16-row operand fits the streaming kernels' LDS: d <= 4096 of
+// the supported widths), so every weight stream serves R drafts; attention masks keep each request to its own rows and context.  Work that needs a whole
 // row sits in a small row kernel between two streaming kernels; there is no cross-workgroup
 // synchronisation inside any kernel (no fences, no atomics, no spin-waits), so results are
 // deterministic.  On MI355X the gap between two kernels on the stream is 1.4-2 us (per-workgroup
@@ -28,7 +29,7 @@
 //               ROWS init_latents(ctx), step-0 rows x, a = LN_self(x) of block 0
 //               KV   cross K/V of every block             (GEMV + reduce)
 //               FOLD per block: A_h = Wq_h^T K_h^T, B_h = Wo_h V_h   (stream, split-K by head)
-//   per Euler step, per block l (each expert on its own stream):
+//   per Euler step, per block l (each expert on its own stream, the second starting ~1/3 block later):
 //     QKV   stream  A = a (LN_self rows)          epilogue q,k,v = fp16(acc + b)      full-K tiles
 //     O     stream  A = causal self attention of head h, computed while staging    split-K by head
 //     RES   row     x += sum_h P + b_o ; a = LN_cross(fp16(x))
@@ -39,6 +40,7 @@
 //     RES   row     x += sum P + b2 ; a = LN_self of block l+1 (out_norm after the last block)
 //   OUT   stream  A = out_norm rows of the current chunk                           split-K
 //   ROWS  row     v = fp16(sum P + b_out); z = fp16(z + fp16(dt v)); next step's rows and LN_self
+//                 (per expert: its chunk's update and its own rows)
 //
 // The cross attention's query and output projections are folded into the context: the context is
 // fixed for the whole draft, so q_h . K_h = LN(x) . (Wq_h^T K_h^T) + bq_h . K_h and
@@ -64,6 +66,8 @@ namespace {
 //           z[r] = fp16(z[r] + fp16(dt v))   (z_out[r] = z[r] after the last step)
 // then, unless this was the last step, the next step's rows: for every expert c2 that reads z row
 // r: x = fp16(fp16(z + pos[r]) + [current rows] tau), residual x = that, a = LN_self of block 0.
+// With `only` = c (each expert on its own stream) the launch updates chunk c's rows and builds
+// expert c's rows alone, reading the earlier chunks' rows from z.
 struct RowsArgs {
   const h16* ctx;      // [R][C][d] context rows of the group's requests
   float* ctx_mom;      // init: [R C][2] (mean, rstd) of the fp16 context rows
@@ -82,6 +86,8 @@ struct RowsArgs {
   int R;               // requests in the group (row r of the grid: request r / KD, draft row r % KD)
   int out_all;         // the OUT launch covered every row of each expert (R > 1), not just the current chunk's
   int init;            // CFH_INIT_*: how z0 is formed
+  int only;            // euler: -1 = every chunk; c = chunk c's update and expert c's next rows only
+                       // (the rows of earlier chunks are read from z, already updated)
 };
 
 __global__ void __launch_bounds__(ROWT) k_rows(RowsArgs a) {
@@ -132,6 +138,15 @@ __global__ void __launch_bounds__(ROWT) k_rows(RowsArgs a) {
         zv[k] = make_float4(o[0], o[1], o[2], o[3]);
         *(float4*)(a.z + (size_t)r * d + q * 4) = zv[k];
       }
+    }
+  } else if (a.only >= 0 && rr / a.CS != a.only) {
+    // a row of another chunk: past chunk `only`, no row of its expert; before it, read the row
+    // that chunk's own update wrote for the next step's rows
+    if (a.last || rr / a.CS > a.only) return;
+#pragma unroll
+    for (int k = 0; k < ROWQ; ++k) {
+      const int q = threadIdx.x + k * blockDim.x;
+      zv[k] = q < nq ? *(const float4*)(a.z + (size_t)r * d + q * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   } else {
     const int c = rr / a.CS, i = rr - c * a.CS;
@@ -184,7 +199,7 @@ __global__ void __launch_bounds__(ROWT) k_rows(RowsArgs a) {
     }
   }
   if (a.last) return;
-  for (int c2 = 0; c2 < a.nch; ++c2) {
+  for (int c2 = a.only >= 0 ? a.only : 0; c2 < (a.only >= 0 ? a.only + 1 : a.nch); ++c2) {
     if (rr >= (c2 + 1) * a.CS) continue;         // expert c2 reads z rows [0, (c2+1)*CS) of each draft
     const bool cur = rr >= c2 * a.CS;
     const size_t xr = (size_t)req * (c2 + 1) * a.CS + rr;   // the row in expert c2's request-major rows
@@ -525,10 +540,17 @@ WS expert_view(const WS& w, int c0) {
   return v;
 }
 
+// Where a chunk expert's first block pass of a draft may start, relative to the previous expert's
+// (concurrent experts): after that expert's STAGGER_AT-th launch of its first block (0: at once).
+// After the fifth (the residual row before W1, ~100 us into a ~290 us block at d = 5120) one
+// expert's row kernels and cross attention fall inside the other's W1 / W2 streams instead of
+// beside its own: measured -0.2 ms a draft at d = 5120, no change at d = 2560 or 4096.
+constexpr int STAGGER_AT = 5;
+
 // The eight launches of block l (nine unfolded) for chunk experts c0 .. c0 + nc - 1, every launch
-// covering those experts.
+// covering those experts; `mark`, if given, is recorded after the block's STAGGER_AT-th launch.
 int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const void* const* experts_all,
-               int l, int Rg, hipStream_t st, int c0, int nc) {
+               int l, int Rg, hipStream_t st, int c0, int nc, hipEvent_t mark = nullptr) {
   const WS w = expert_view(w_all, c0);
   const void* const* experts = experts_all + c0;
   const int d = p.d, fd = p.fd, NL = p.NL, nch = nc, Cg = Rg * p.C;
@@ -536,7 +558,11 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
   const size_t B = L.blk0 + (size_t)l * L.blkstride;
   auto S_of = [&](int c) { return Rg * (c0 + c + 1) * p.CS; };   // rows of expert c0 + c: Rg requests
   auto Sr_of = [&](int c) { return (c0 + c + 1) * p.CS; };       // rows per request
-  int rc;
+  int rc, launched = 0;
+  auto done = [&]() -> int {
+    if (mark && ++launched == STAGGER_AT) CFH_HIP(hipEventRecord(mark, st));
+    return CFH_OK;
+  };
   // QKV: q, k, v = fp16(LN_self(x) W_in^T + b_in), full-K tiles
   {
     SArgs a = {};
@@ -548,7 +574,7 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
       x.w = (const h16x8*)PTR(c, B + L.qkv); x.a = w.abuf[c]; x.lda = d; x.bias = (const h16*)PTR(c, B + L.qkv_b);
       x.out = w.qkv[c]; x.S = S_of(c);
     }
-    if ((rc = launch_stream<S_BUF, E_BIAS16>(a, p.Smax, st))) return rc;
+    if ((rc = launch_stream<S_BUF, E_BIAS16>(a, p.Smax, st)) || (rc = done())) return rc;
   }
   // O: causal self attention per head, staged, then out_proj split-K by head (group)
   {
@@ -561,7 +587,7 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
       SEx& x = a.ex[c];
       x.w = (const h16x8*)PTR(c, B + L.o); x.a = w.qkv[c]; x.out = w.P[c]; x.S = S_of(c); x.Sr = Sr_of(c);
     }
-    if ((rc = launch_stream<S_SELF, E_PART>(a, p.Smax, st))) return rc;
+    if ((rc = launch_stream<S_SELF, E_PART>(a, p.Smax, st)) || (rc = done())) return rc;
   }
   ResArgs r = {};
   r.nex = nch; r.d = d; r.mode = p.res_mode;
@@ -573,7 +599,7 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
     r.g[c] = (const h16*)PTR(c, B + L.xn_w); r.b[c] = (const h16*)PTR(c, B + L.xn_b);
   }
   r.pack = p.fold;   // the folded cross attention takes LN_cross(x) as an MFMA operand image
-  if ((rc = launch_res(r, st))) return rc;
+  if ((rc = launch_res(r, st)) || (rc = done())) return rc;
   r.pack = 0;
   if (p.fold) {
     XattArgs x = {};
@@ -584,7 +610,7 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
       x.sb[c] = w.fsb[c] + (size_t)l * p.H * Cg;
       x.out[c] = w.P[c]; x.S[c] = S_of(c); x.Sr[c] = Sr_of(c);
     }
-    if ((rc = launch_xattn(x, st))) return rc;
+    if ((rc = launch_xattn(x, st)) || (rc = done())) return rc;
   }
   // QC: cross-attention query projection, split-K partials
   if (!p.fold) {
@@ -596,7 +622,7 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
       SEx& x = a.ex[c];
       x.w = (const h16x8*)PTR(c, B + L.qc); x.a = w.abuf[c]; x.lda = d; x.out = w.Pq[c]; x.S = S_of(c);
     }
-    if ((rc = launch_stream<S_BUF, E_PART>(a, p.Smax, st))) return rc;
+    if ((rc = launch_stream<S_BUF, E_PART>(a, p.Smax, st)) || (rc = done())) return rc;
   }
   // OC: cross attention per head over the hoisted context K/V, staged, then out_proj split-K by head
   if (!p.fold) {
@@ -610,14 +636,14 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
       x.w = (const h16x8*)PTR(c, B + L.oc); x.a = w.kvc[c] + (size_t)l * 2 * Cg * d; x.pin = w.Pq[c];
       x.bin = (const h16*)PTR(c, B + L.qc_b); x.out = w.P[c]; x.S = S_of(c); x.Sr = Sr_of(c);
     }
-    if ((rc = launch_stream<S_CROSS, E_PART>(a, p.Smax, st))) return rc;
+    if ((rc = launch_stream<S_CROSS, E_PART>(a, p.Smax, st)) || (rc = done())) return rc;
   }
   // residual + LN_ffn
   for (int c = 0; c < nch; ++c) {
     r.bias[c] = (const h16*)PTR(c, B + L.oc_b);
     r.g[c] = (const h16*)PTR(c, B + L.fn_w); r.b[c] = (const h16*)PTR(c, B + L.fn_b);
   }
-  if ((rc = launch_res(r, st))) return rc;
+  if ((rc = launch_res(r, st)) || (rc = done())) return rc;
   // W1: g = fp16(gelu(LN_ffn(x) W1^T + b1)), full-K tiles
   {
     SArgs a = {};
@@ -630,7 +656,7 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
       x.w = (const h16x8*)PTR(c, B + L.w1); x.a = w.abuf[c]; x.lda = d; x.bias = (const h16*)PTR(c, B + L.w1_b);
       x.out = w.g[c]; x.S = S_of(c);
     }
-    if ((rc = launch_stream<S_BUF, E_GELU16>(a, p.Smax, st))) return rc;
+    if ((rc = launch_stream<S_BUF, E_GELU16>(a, p.Smax, st)) || (rc = done())) return rc;
   }
   // W2: split-K partials
   {
@@ -642,7 +668,7 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
       SEx& x = a.ex[c];
       x.w = (const h16x8*)PTR(c, B + L.w2); x.a = w.g[c]; x.lda = fd; x.out = w.P[c]; x.S = S_of(c);
     }
-    if ((rc = launch_stream<S_BUF, E_PART>(a, p.Smax, st))) return rc;
+    if ((rc = launch_stream<S_BUF, E_PART>(a, p.Smax, st)) || (rc = done())) return rc;
   }
   // residual + LayerNorm of the next block (out_norm after the last block)
   r.ks = p.ks_w2;
@@ -655,39 +681,53 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
       r.g[c] = (const h16*)PTR(c, L.on_w); r.b[c] = (const h16*)PTR(c, L.on_b);
     }
   }
-  return launch_res(r, st);
+  if ((rc = launch_res(r, st))) return rc;
+  return done();
 }
 
-// Companion streams of a caller stream: chunk expert c > 0 runs its block passes on companion c-1
-// (default priority), forked from the caller's stream at each Euler step and joined back before
-// the Euler update.  One expert's row kernels, cross attention and launch gaps then overlap the
-// other's weight streaming (its launches half the grid of a both-experts launch): measured -0.5 ms
-// a draft at d = 5120, L = 8, E = 8, bit-identical.  Created on first use per (device, caller
-// stream) and kept for the life of the process; events are re-recorded at every step (a wait
-// takes the event's state when it is enqueued), which also holds under stream capture.
+// Companion streams of a caller stream: chunk expert c > 0 runs its block passes, its OUT launch
+// and its Euler update on companion c-1 (default priority) for the whole draft, forked from the
+// caller's stream after the per-draft launches and joined back at the end; one expert's row
+// kernels, cross attention and launch gaps then overlap another's weight streaming (its launches
+// half the grid of a both-experts launch).  Each companion needs a hardware queue of its own: HIP
+// maps streams onto GPU_MAX_HW_QUEUES queues (4 by default), and two streams on one queue run in
+// submission order.  Created on first use per (device, caller stream), only as many as the flow's
+// chunk experts need, and kept for the life of the process; events are re-recorded at every step
+// (a wait takes the event's state when it is enqueued), which also holds under stream capture.
 constexpr int MAX_CHUNKS = 4;      // chunk experts of a flow (cfh::flow_dims_ok)
 struct Companions {
+  int made;                          // companions created so far
   hipStream_t s[MAX_CHUNKS - 1];
   hipEvent_t fork, join[MAX_CHUNKS - 1];
+  hipEvent_t up[MAX_CHUNKS - 1];     // expert c's Euler update of its chunk done (waited by c + 1)
+  hipEvent_t down[MAX_CHUNKS - 1];   // expert c + 1 has read chunk c's rows (waited by c, next step)
+  hipEvent_t mark[MAX_CHUNKS - 1];   // expert c's first block reached the stagger point
 };
 std::mutex g_comp_mu;
 std::map<std::pair<int, hipStream_t>, Companions> g_comp;
 
-int companions(hipStream_t st, Companions* out) {
+// The companions of caller stream st on the current device, at least n of them.
+int companions(hipStream_t st, int n, Companions* out) {
   int dev = 0;
   CFH_HIP(hipGetDevice(&dev));
+  if (n < 0 || n > MAX_CHUNKS - 1) return CFH_E_UNSUPPORTED;
   std::lock_guard<std::mutex> lock(g_comp_mu);
   auto it = g_comp.find({dev, st});
   if (it == g_comp.end()) {
     Companions c = {};
-    for (int i = 0; i < MAX_CHUNKS - 1; ++i) {
-      CFH_HIP(hipStreamCreateWithFlags(&c.s[i], hipStreamNonBlocking));
-      CFH_HIP(hipEventCreateWithFlags(&c.join[i], hipEventDisableTiming));
-    }
     CFH_HIP(hipEventCreateWithFlags(&c.fork, hipEventDisableTiming));
     it = g_comp.emplace(std::make_pair(dev, st), c).first;
   }
-  *out = it->second;
+  Companions& c = it->second;
+  for (; c.made < n; ++c.made) {
+    const int i = c.made;
+    CFH_HIP(hipStreamCreateWithFlags(&c.s[i], hipStreamNonBlocking));
+    CFH_HIP(hipEventCreateWithFlags(&c.join[i], hipEventDisableTiming));
+    CFH_HIP(hipEventCreateWithFlags(&c.up[i], hipEventDisableTiming));
+    CFH_HIP(hipEventCreateWithFlags(&c.down[i], hipEventDisableTiming));
+    CFH_HIP(hipEventCreateWithFlags(&c.mark[i], hipEventDisableTiming));
+  }
+  *out = c;
   return CFH_OK;
 }
 
@@ -703,7 +743,7 @@ int integrate(const Plan& p, const cfh_flow_dims* dm, const void* const* experts
   auto BLK = [&](int l) { return L.blk0 + (size_t)l * L.blkstride; };
   Companions cp = {};
   if (nch > MAX_CHUNKS) return CFH_E_UNSUPPORTED;
-  if (p.conc && (rc = companions(st, &cp))) return rc;
+  if (p.conc && (rc = companions(st, nch - 1, &cp))) return rc;
 
   // ---- time embeddings of every step (the same for every request)
   {
@@ -739,6 +779,7 @@ int integrate(const Plan& p, const cfh_flow_dims* dm, const void* const* experts
       RowsArgs r = {};
       r.ctx = ctx_b; r.ctx_mom = w.ctx_mom; r.z = w.z; r.z_out = zo_b; r.euler = 0; r.last = 0; r.d = d; r.C = C;
       r.init = dm->init_mode;
+      r.only = -1;
       r.CS = CS; r.nch = nch; r.KD = KD; r.R = Rg; r.out_all = p.R > 1;
       for (int c = 0; c < nch; ++c) {
         r.x[c] = w.x[c]; r.pos[c] = (const h16*)PTR(c, L.pos); r.tau[c] = w.tau[c];
@@ -813,50 +854,15 @@ int integrate(const Plan& p, const cfh_flow_dims* dm, const void* const* experts
         }
       }
     }
-    for (int s = 0; s < E; ++s) {
-      // each chunk expert on its own stream until the Euler update
-      if (p.conc) {
-        CFH_HIP(hipEventRecord(cp.fork, st));
-        for (int c = 1; c < nch; ++c) CFH_HIP(hipStreamWaitEvent(cp.s[c - 1], cp.fork, 0));
-      }
-      for (int l = 0; l < NL; ++l) {
-        if (!p.conc) {
-          if ((rc = block_pass(p, L, w, experts, l, Rg, st, 0, nch))) return rc;
-          continue;
-        }
-        for (int c = 0; c < nch; ++c)
-          if ((rc = block_pass(p, L, w, experts, l, Rg, c == 0 ? st : cp.s[c - 1], c, 1))) return rc;
-      }
-      // OUT: out_proj on the out_norm rows of each expert's current chunk (every row when requests
-      // are packed: their current rows are not contiguous, and the weights stream once either way)
-      // (each expert on its stream, or every expert in one launch)
-      for (int c0 = 0; c0 < nch; c0 += p.conc ? 1 : nch) {
-        const int nc = p.conc ? 1 : nch;
-        SArgs a = {};
-        a.conc = nch / nc;
-        a.nex = nc; a.N = d; a.K = d; a.ks = p.ks_out; a.wpb = p.wpb_out; a.tpw = 1; a.d = d; a.hd = p.hd;
-        a.wg_per_kc = (d / 16) / (a.wpb * a.tpw);
-        for (int c = c0; c < c0 + nc; ++c) {
-          SEx& x = a.ex[c - c0];
-          x.w = (const h16x8*)PTR(c, L.out); x.lda = d; x.out = w.P[c];
-          if (p.R == 1) {
-            x.a = w.abuf[c] + (size_t)c * CS * d;
-            x.S = CS;
-          } else {
-            x.a = w.abuf[c];
-            x.S = Rg * (c + 1) * CS;
-          }
-        }
-        if ((rc = launch_stream<S_BUF, E_PART>(a, p.R == 1 ? CS : p.Smax, c0 == 0 ? st : cp.s[c0 - 1]))) return rc;
-      }
-      if (p.conc)
-        for (int c = 1; c < nch; ++c) {
-          CFH_HIP(hipEventRecord(cp.join[c - 1], cp.s[c - 1]));
-          CFH_HIP(hipStreamWaitEvent(st, cp.join[c - 1], 0));
-        }
+    if (p.conc) {   // companions start after the per-draft launches
+      CFH_HIP(hipEventRecord(cp.fork, st));
+      for (int c = 1; c < nch; ++c) CFH_HIP(hipStreamWaitEvent(cp.s[c - 1], cp.fork, 0));
+    }
+    auto rows_args = [&](int s, int only) {
       RowsArgs r = {};
       r.ctx = ctx_b; r.z = w.z; r.z_out = zo_b; r.euler = 1; r.last = (s + 1 == E); r.ks = p.ks_out;
       r.dt = 1.0f / (float)E; r.d = d; r.C = C; r.CS = CS; r.nch = nch; r.KD = KD; r.R = Rg; r.out_all = p.R > 1;
+      r.only = only;
       for (int c = 0; c < nch; ++c) {
         r.Pout[c] = w.P[c]; r.bout[c] = (const h16*)PTR(c, L.out_b);
         r.x[c] = w.x[c]; r.pos[c] = (const h16*)PTR(c, L.pos);
@@ -864,9 +870,70 @@ int integrate(const Plan& p, const cfh_flow_dims* dm, const void* const* experts
         r.g[c] = (const h16*)PTR(c, BLK(0) + L.sn_w); r.b[c] = (const h16*)PTR(c, BLK(0) + L.sn_b);
         r.a[c] = w.abuf[c];
       }
-      hipLaunchKernelGGL(k_rows, dim3(Rg * KD), dim3(ROWT), 0, st, r);
-      CFH_LAUNCH_CHECK();
+      return r;
+    };
+    // OUT: out_proj on the out_norm rows of experts c0 .. c0 + nc - 1's current chunks (every row
+    // when requests are packed: their current rows are not contiguous, and the weights stream once
+    // either way)
+    auto out_proj = [&](int c0, int nc, hipStream_t sc) {
+      SArgs a = {};
+      a.conc = nch / nc;
+      a.nex = nc; a.N = d; a.K = d; a.ks = p.ks_out; a.wpb = p.wpb_out; a.tpw = 1; a.d = d; a.hd = p.hd;
+      a.wg_per_kc = (d / 16) / (a.wpb * a.tpw);
+      for (int c = c0; c < c0 + nc; ++c) {
+        SEx& x = a.ex[c - c0];
+        x.w = (const h16x8*)PTR(c, L.out); x.lda = d; x.out = w.P[c];
+        if (p.R == 1) {
+          x.a = w.abuf[c] + (size_t)c * CS * d;
+          x.S = CS;
+        } else {
+          x.a = w.abuf[c];
+          x.S = Rg * (c + 1) * CS;
+        }
+      }
+      return launch_stream<S_BUF, E_PART>(a, p.R == 1 ? CS : p.Smax, sc);
+    };
+    for (int s = 0; s < E; ++s) {
+      if (!p.conc) {
+        for (int l = 0; l < NL; ++l)
+          if ((rc = block_pass(p, L, w, experts, l, Rg, st, 0, nch))) return rc;
+        if ((rc = out_proj(0, nch, st))) return rc;
+        const RowsArgs r = rows_args(s, -1);
+        hipLaunchKernelGGL(k_rows, dim3(Rg * KD), dim3(ROWT), 0, st, r);
+        CFH_LAUNCH_CHECK();
+        continue;
+      }
+      // Each chunk expert on its own stream through the whole draft.  Expert c's next rows read
+      // the rows of chunks before c, so its Euler update waits for expert c - 1's of the same
+      // step (`up`), and expert c - 1 overwrites them at the next step only after expert c has
+      // read them (`down`); expert 0 never waits for a later one within a step.
+      // (the launches are issued block by block across the experts, so that where the host's
+      // launch rate bounds the draft every stream has work queued)
+      for (int l = 0; l < NL; ++l)
+        for (int c = 0; c < nch; ++c) {
+          hipStream_t sc = c == 0 ? st : cp.s[c - 1];
+          const bool first = s == 0 && l == 0 && STAGGER_AT > 0;
+          if (first && c > 0) CFH_HIP(hipStreamWaitEvent(sc, cp.mark[c - 1], 0));
+          hipEvent_t mk = first && c + 1 < nch ? cp.mark[c] : nullptr;
+          if ((rc = block_pass(p, L, w, experts, l, Rg, sc, c, 1, mk))) return rc;
+        }
+      for (int c = 0; c < nch; ++c) {
+        hipStream_t sc = c == 0 ? st : cp.s[c - 1];
+        if ((rc = out_proj(c, 1, sc))) return rc;
+        if (c > 0) CFH_HIP(hipStreamWaitEvent(sc, cp.up[c - 1], 0));
+        if (c + 1 < nch && s > 0) CFH_HIP(hipStreamWaitEvent(sc, cp.down[c], 0));
+        const RowsArgs r = rows_args(s, c);
+        hipLaunchKernelGGL(k_rows, dim3(Rg * KD), dim3(ROWT), 0, sc, r);
+        CFH_LAUNCH_CHECK();
+        if (c + 1 < nch) CFH_HIP(hipEventRecord(cp.up[c], sc));
+        if (c > 0) CFH_HIP(hipEventRecord(cp.down[c - 1], sc));
+      }
     }
+    if (p.conc)   // the caller's stream waits for every companion (the next group reuses the workspace)
+      for (int c = 1; c < nch; ++c) {
+        CFH_HIP(hipEventRecord(cp.join[c - 1], cp.s[c - 1]));
+        CFH_HIP(hipStreamWaitEvent(st, cp.join[c - 1], 0));
+      }
   }
   return CFH_OK;
 }

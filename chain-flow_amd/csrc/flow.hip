@@ -697,6 +697,7 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
 constexpr int MAX_CHUNKS = 4;      // chunk experts of a flow (cfh::flow_dims_ok)
 struct Companions {
   int made;                          // companions created so far
+  int overlap;                       // 1: the companions' work overlaps the caller's (checked once)
   hipStream_t s[MAX_CHUNKS - 1];
   hipEvent_t fork, join[MAX_CHUNKS - 1];
   hipEvent_t up[MAX_CHUNKS - 1];     // expert c's Euler update of its chunk done (waited by c + 1)
@@ -705,6 +706,58 @@ struct Companions {
 };
 std::mutex g_comp_mu;
 std::map<std::pair<int, hipStream_t>, Companions> g_comp;
+
+// The companion check's kernel: one wave that waits `ticks` of the constant wall clock (at most
+// `cap` clock reads) and records when it started and ended.
+__device__ long long g_wait_stamps[8][2];
+__global__ void __launch_bounds__(64) k_wait(long long ticks, long long cap, int slot) {
+  const long long t0 = wall_clock64();
+  long long t = t0, n = 0;
+  while (t - t0 < ticks && n < cap) {
+    t = wall_clock64();
+    ++n;
+  }
+  if (threadIdx.x == 0) {
+    g_wait_stamps[slot][0] = t0;
+    g_wait_stamps[slot][1] = t;
+  }
+}
+
+// Whether work on the companions overlaps work on the caller's stream: HIP maps a process's
+// streams onto a few hardware queues, and two streams that share one run in submission order
+// (measured: the d = 5120 flow at 29.4 instead of 18.7 ms a pass, and 19.6 on one stream).  A
+// 200 us wait is launched on each stream at once; their wall-clock intervals overlap by most of
+// that when the streams run side by side, and not at all when one waits for the other.  The
+// kernels' own clocks decide, so a stall of the host between the launches (the first launch of a
+// kernel loads it) does not.
+int companions_overlap(hipStream_t st, const Companions& c, int n, int* overlap) {
+  int dev = 0, khz = 0;
+  CFH_HIP(hipGetDevice(&dev));
+  CFH_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
+  *overlap = 0;
+  if (khz <= 0 || n < 1 || n > 7) return CFH_OK;
+  const long long ticks = (long long)khz / 5, cap = 1ll << 22;
+  CFH_HIP(hipEventRecord(c.fork, st));
+  for (int i = 0; i < n; ++i) CFH_HIP(hipStreamWaitEvent(c.s[i], c.fork, 0));
+  hipLaunchKernelGGL(k_wait, dim3(1), dim3(64), 0, st, ticks, cap, 0);
+  CFH_LAUNCH_CHECK();
+  for (int i = 0; i < n; ++i) {
+    hipLaunchKernelGGL(k_wait, dim3(1), dim3(64), 0, c.s[i], ticks, cap, i + 1);
+    CFH_LAUNCH_CHECK();
+    CFH_HIP(hipEventRecord(c.join[i], c.s[i]));
+    CFH_HIP(hipStreamWaitEvent(st, c.join[i], 0));
+  }
+  CFH_HIP(hipStreamSynchronize(st));
+  long long stamps[8][2] = {};
+  CFH_HIP(hipMemcpyFromSymbol(stamps, HIP_SYMBOL(g_wait_stamps), sizeof(stamps), 0, hipMemcpyDeviceToHost));
+  long long lo = stamps[0][0], hi = stamps[0][1];
+  for (int i = 1; i <= n; ++i) {
+    lo = std::max(lo, stamps[i][0]);
+    hi = std::min(hi, stamps[i][1]);
+  }
+  *overlap = hi - lo > ticks / 2;
+  return CFH_OK;
+}
 
 // The companions of caller stream st on the current device, at least n of them.
 int companions(hipStream_t st, int n, Companions* out) {
@@ -726,6 +779,10 @@ int companions(hipStream_t st, int n, Companions* out) {
     CFH_HIP(hipEventCreateWithFlags(&c.up[i], hipEventDisableTiming));
     CFH_HIP(hipEventCreateWithFlags(&c.down[i], hipEventDisableTiming));
     CFH_HIP(hipEventCreateWithFlags(&c.mark[i], hipEventDisableTiming));
+    if (c.made + 1 == n) {
+      int rc = companions_overlap(st, c, n, &c.overlap);
+      if (rc) return rc;
+    }
   }
   *out = c;
   return CFH_OK;
@@ -733,8 +790,15 @@ int companions(hipStream_t st, int n, Companions* out) {
 
 // The whole draft of `batch` requests on workspace ws (the plan's carve() layout): per request the
 // per-draft launches, then E Euler steps of L block passes and the OUT / ROWS step.
-int integrate(const Plan& p, const cfh_flow_dims* dm, const void* const* experts, const void* ctx, void* z_out,
+int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* experts, const void* ctx, void* z_out,
               void* ws_ptr, int batch, hipStream_t st) {
+  // Under stream capture every expert stays on the caller's stream: a replayed graph of the
+  // two-stream form ran slower than the one-stream form (d = 5120: 21.7 against 19.6 ms a flow
+  // pass; d = 4096: 15.2 against 14.8), while eager calls gain from the overlap (19.0 ms).
+  Plan p = p0;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  CFH_HIP(hipStreamIsCapturing(st, &cap));
+  if (cap != hipStreamCaptureStatusNone) p.conc = false;
   const cfh::ExpertLayout L = cfh::expert_layout(dm);
   const WS w = carve(p, (char*)ws_ptr);
   const int d = p.d, CS = p.CS, E = p.E, NL = p.NL, C = p.C, KD = p.KD, nch = p.nch;
@@ -744,6 +808,7 @@ int integrate(const Plan& p, const cfh_flow_dims* dm, const void* const* experts
   Companions cp = {};
   if (nch > MAX_CHUNKS) return CFH_E_UNSUPPORTED;
   if (p.conc && (rc = companions(st, nch - 1, &cp))) return rc;
+  if (p.conc && !cp.overlap) p.conc = false;   // the companions would run after the caller's work
 
   // ---- time embeddings of every step (the same for every request)
   {

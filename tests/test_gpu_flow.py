@@ -82,6 +82,29 @@ def test_flow_is_bit_reproducible(cuda):
 
 
 @pytest.mark.gpu
+def test_flow_same_on_every_caller_stream(cuda):
+    """From d = 1024 an eager flow runs its second chunk expert on a companion of the caller's
+    stream, created (and checked for overlap with the caller's stream) on the first call per caller
+    stream: the draft is bit-identical on the default stream and on a side stream, first call and
+    repeated."""
+    cfg = flownet(1024, layers=2, flow_steps=2)
+    assert cfg.draft_length // cfg.chunk_size == 2
+    W = {k: v.to(cuda) for k, v in _flow_weights(cfg, seed=5).items()}
+    ctx = synthetic_context(1, cfg.context_size, 1024, seed=6).to(cuda)
+    ff = FusedFlow(cfg, W, device=cuda)
+    a = ff.predict_hidden(ctx).clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        b = ff.predict_hidden(ctx).clone()
+        c = ff.predict_hidden(ctx).clone()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    assert torch.equal(a, c)
+
+
+@pytest.mark.gpu
 def test_flow_full_width_matches_oracle(cuda):
     """The benchmark's width (d = 5120: head_dim 640, ffn 30720, the 16-wave and one-round grids,
     the deep operand staging) against the oracle: one block, two Euler steps."""

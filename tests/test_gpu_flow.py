@@ -105,6 +105,36 @@ def test_flow_same_on_every_caller_stream(cuda):
 
 
 @pytest.mark.gpu
+def test_flow_graph_replays_equal_eager(cuda):
+    """Under stream capture the flow keeps both chunk experts on the caller's stream (the eager call
+    at d = 1024 runs the second on a companion): every replay of the captured flow, with eager
+    work and synchronisations between the replays, equals the eager draft bit for bit."""
+    cfg = flownet(1024, layers=2, flow_steps=2)
+    W = {k: v.to(cuda) for k, v in _flow_weights(cfg, seed=8).items()}
+    ctx = synthetic_context(1, cfg.context_size, 1024, seed=9).to(cuda)
+    ff = FusedFlow(cfg, W, device=cuda)
+    want = ff.predict_hidden(ctx).clone()
+    out = torch.empty_like(want)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ff.predict_hidden(ctx, out=out)                  # warm-up off the default stream
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ff.predict_hidden(ctx, out=out)
+    for rep in range(3):
+        out.zero_()
+        junk = torch.randn(256, 256, device=cuda) @ torch.randn(256, 256, device=cuda)
+        g.replay()
+        torch.cuda.synchronize()
+        del junk
+        assert torch.equal(out, want), rep
+        assert torch.equal(ff.predict_hidden(ctx), want), rep
+
+
+@pytest.mark.gpu
 def test_flow_full_width_matches_oracle(cuda):
     """The benchmark's width (d = 5120: head_dim 640, ffn 30720, the 16-wave and one-round grids,
     the deep operand staging) against the oracle: one block, two Euler steps."""

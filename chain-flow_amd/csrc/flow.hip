@@ -772,6 +772,7 @@ int companions(hipStream_t st, int n, Companions* out) {
     it = g_comp.emplace(std::make_pair(dev, st), c).first;
   }
   Companions& c = it->second;
+  const int made0 = c.made;
   for (; c.made < n; ++c.made) {
     const int i = c.made;
     CFH_HIP(hipStreamCreateWithFlags(&c.s[i], hipStreamNonBlocking));
@@ -779,10 +780,10 @@ int companions(hipStream_t st, int n, Companions* out) {
     CFH_HIP(hipEventCreateWithFlags(&c.up[i], hipEventDisableTiming));
     CFH_HIP(hipEventCreateWithFlags(&c.down[i], hipEventDisableTiming));
     CFH_HIP(hipEventCreateWithFlags(&c.mark[i], hipEventDisableTiming));
-    if (c.made + 1 == n) {
-      int rc = companions_overlap(st, c, n, &c.overlap);
-      if (rc) return rc;
-    }
+  }
+  if (c.made != made0) {   // new companions: check them all against the caller's stream
+    const int rc = companions_overlap(st, c, c.made, &c.overlap);
+    if (rc) return rc;
   }
   *out = c;
   return CFH_OK;

@@ -848,17 +848,23 @@ __global__ void __launch_bounds__(GW * 64) k_head_gemm(GemmArgs a) {
 #pragma unroll
     for (int p = 0; p < GPF; ++p) {
       const int slot = (p * 4 + (lane >> 4)) ^ (lane & 15);
+      // every x read of the k-step first, then the multiplies (the reads' latencies overlap
+      // instead of each pair being waited for before its two multiplies)
+      bf16x8 av[MTW];
+#pragma unroll
+      for (int mt = 0; mt < MTW; ++mt) av[mt] = *(const bf16x8*)(xb + mt * 16 * GKC + slot * 8);
 #pragma unroll
       for (int mt = 0; mt < MTW; ++mt) {
-        const bf16x8 av = *(const bf16x8*)(xb + mt * 16 * GKC + slot * 8);
 #pragma unroll
         for (int t = 0; t < NT; ++t)
           if constexpr (F16)
-            acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h16x8, av),
+            acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h16x8, av[mt]),
                                                                 __builtin_bit_cast(h16x8, bq[p][t]), acc[mt][t], 0, 0, 0);
           else
-            acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bq[p][t], acc[mt][t], 0, 0, 0);
+            acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mt], bq[p][t], acc[mt][t], 0, 0, 0);
       }
+      __builtin_amdgcn_sched_group_barrier(0x100, MTW, 0);        // the LDS reads
+      __builtin_amdgcn_sched_group_barrier(0x008, MTW * NT, 0);   // then the multiplies
       // keep the reloads here: the scheduler would otherwise sink them to the end of the chunk
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll

@@ -2,8 +2,8 @@
 
 TEST INFRASTRUCTURE ONLY. Nothing in the product (``chain-flow_amd/``) imports, links or calls
 anything under ``oracle/``; only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
-``cpu_baseline`` leg use it, and only as the checker or the timed CPU baseline, never as the
-thing measured or shipped.
+``cpu_baseline`` leg use it, and only as the reference results are compared against or as the timed
+CPU baseline, never as the thing measured or shipped.
 
 It is a plain numpy restatement of the reference algorithm (Cosmos-YTU/chain-flow), one module per
 part of the path, each function citing the reference ``file:line`` it follows (``cf/`` =

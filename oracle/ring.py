@@ -1,6 +1,6 @@
 """Oracle: the serving proposer's context ring (``_ring_write`` + ``_ring_gather``).
 
-Test infrastructure only (the tests use it as the checker).
+Test infrastructure only (the tests compare the GPU results against it).
 
 Follows ``cf/vllm_plugin/flow_proposer.py:916-945`` (``_ring_write``: rows j < Kmax of request b
 come from ``sh[start_b + srcoff_j]``, srcoff_j = j, or 0 then ``1 + path[slot][j-1]`` for a tree's

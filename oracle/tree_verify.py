@@ -1,7 +1,7 @@
 """Oracle: the rest of the tree verify -- tree causal conv1d, the draft-tree attention's suffix half
 with the log-sum-exp merge, and the greedy tree descent.
 
-Test infrastructure only (the tests use it as the checker).
+Test infrastructure only (the tests compare the GPU results against it).
 
 Follows, in the reference:
 * ``cf/vllm_tree/tree_ssm.py:393-423`` ``_tree_scan_conv_kernel``: node-serial in BFS order; node n

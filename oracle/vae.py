@@ -1,7 +1,7 @@
 """Oracle: the hidden-state VAE of the latent drafters and the latent drafter's ``predict_hidden``.
 
-Test infrastructure only: the tests, the smoke check and the benchmark's CPU leg use it as the
-checker; no product code imports it.
+Test infrastructure only: the tests and the smoke check compare the GPU results against it and the
+benchmark's CPU leg times it; no product code imports it.
 
 Follows, in the reference (``cf/`` = ``src/chain_flow/``):
 

@@ -759,13 +759,18 @@ int companions_overlap(hipStream_t st, const Companions& c, int n, int* overlap)
   return CFH_OK;
 }
 
-// The companions of caller stream st on the current device, at least n of them.
-int companions(hipStream_t st, int n, Companions* out) {
+// The companions of caller stream st on the current device, at least n of them; with `create`
+// false nothing is created (out->made < n then says they are not there).
+int companions(hipStream_t st, int n, bool create, Companions* out) {
   int dev = 0;
   CFH_HIP(hipGetDevice(&dev));
   if (n < 0 || n > MAX_CHUNKS - 1) return CFH_E_UNSUPPORTED;
   std::lock_guard<std::mutex> lock(g_comp_mu);
   auto it = g_comp.find({dev, st});
+  if (!create) {
+    *out = it == g_comp.end() ? Companions{} : it->second;
+    return CFH_OK;
+  }
   if (it == g_comp.end()) {
     Companions c = {};
     CFH_HIP(hipEventCreateWithFlags(&c.fork, hipEventDisableTiming));
@@ -792,7 +797,7 @@ int companions(hipStream_t st, int n, Companions* out) {
 // The whole draft of `batch` requests on workspace ws (the plan's carve() layout): per request the
 // per-draft launches, then E Euler steps of L block passes and the OUT / ROWS step.
 int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* experts, const void* ctx, void* z_out,
-              void* ws_ptr, int batch, hipStream_t st) {
+              void* ws_ptr, int batch, hipStream_t st, bool may_create = true) {
   // Under stream capture every expert stays on the caller's stream: a replayed graph of the
   // two-stream form ran slower than the one-stream form (d = 5120: 21.7 against 19.6 ms a flow
   // pass; d = 4096: 15.2 against 14.8), while eager calls gain from the overlap (19.0 ms).
@@ -808,8 +813,10 @@ int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* expert
   auto BLK = [&](int l) { return L.blk0 + (size_t)l * L.blkstride; };
   Companions cp = {};
   if (nch > MAX_CHUNKS) return CFH_E_UNSUPPORTED;
-  if (p.conc && (rc = companions(st, nch - 1, &cp))) return rc;
-  if (p.conc && !cp.overlap) p.conc = false;   // the companions would run after the caller's work
+  if (p.conc && (rc = companions(st, nch - 1, may_create, &cp))) return rc;
+  // one stream when the companions would run after the caller's work, or are not there and may not
+  // be created (creating a stream allocates its hardware queue)
+  if (p.conc && (cp.made < nch - 1 || !cp.overlap)) p.conc = false;
 
   // ---- time embeddings of every step (the same for every request)
   {
@@ -1066,7 +1073,8 @@ int cfh_flow_integrate_noalloc(const cfh_flow_dims* dm, const void* const* exper
   void* ws = nullptr;
   int rc = scratch_address(&ws);
   if (rc) return rc;
-  return integrate(p, dm, experts, ctx, z_out, ws, batch, (hipStream_t)stream);
+  // companion streams only if an earlier call on this caller stream created them
+  return integrate(p, dm, experts, ctx, z_out, ws, batch, (hipStream_t)stream, false);
 }
 
 }  // extern "C"

@@ -125,7 +125,10 @@ int cfh_flow_integrate(const cfh_flow_dims* dims, const void* const* experts, co
  * CFH_NOALLOC_SCRATCH_BYTES, one per device, resolved on the first call on each device; nothing
  * is allocated or freed.  Shapes whose workspace (cfh_caps) exceeds it return CFH_E_SCRATCH.
  * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (two streams, two
- * host threads) race and must be serialised by the caller.  Same results as cfh_flow_integrate. */
+ * host threads) race and must be serialised by the caller.  It creates no stream or event either:
+ * the chunk experts run on companion streams only if an earlier cfh_flow_integrate call on the
+ * same caller stream created them, else all on the caller's stream.  Same results as
+ * cfh_flow_integrate. */
 int cfh_flow_integrate_noalloc(const cfh_flow_dims* dims, const void* const* experts, const void* ctx,
                                void* z_out, int batch, void* stream);
 

@@ -41,3 +41,23 @@ def test_noalloc_flow_equals_workspace_flow(cuda):
         torch.cuda.synchronize()
         assert torch.isfinite(got.float()).all()
         assert torch.equal(got, want), f"d={d}: noalloc differs from the workspace flow"
+
+
+@pytest.mark.gpu
+def test_noalloc_first_on_a_stream_runs_one_stream(cuda):
+    """The no-allocation entry point creates no companion stream: called first on a fresh caller
+    stream it runs both chunk experts on that stream (d = 1024 would otherwise overlap them), and
+    the draft is bit-identical to the workspace flow's; a second call, smaller, still matches."""
+    cfg = flownet(1024, layers=2, flow_steps=2)
+    ff = _flow(cfg, cuda, 9)
+    for batch in (2, 1):
+        ctx = synthetic_context(batch, cfg.context_size, 1024, seed=10 + batch).to(cuda)
+        want = ff.predict_hidden(ctx).clone()
+        torch.cuda.synchronize()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            got = _noalloc(ff, ctx)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"batch {batch}: noalloc on a fresh stream differs"

@@ -32,6 +32,8 @@ struct ExpertLayout {
   size_t on_w, on_b, out, out_b;           // out_norm, out_proj
   size_t total;
   bool fold;                               // cross attention folded (xattn_fold): qc holds Wq^T
+  bool fold2;                              // xattn_fold2: qct holds Wq^T beside qc
+  size_t qct;                              // (fold2 only, inside a block region)
 };
 
 bool flow_dims_ok(const cfh_flow_dims* d);
@@ -44,5 +46,10 @@ ExpertLayout expert_layout(const cfh_flow_dims* d);
 // layout depends on it (the query weight is stored transposed), so packing and the flow plan both
 // decide by this one function of the shape.
 bool xattn_fold(const cfh_flow_dims* d);
+// Two heads per attention k-chunk (head widths such as 80 or 240) and 2 x ctx_rows <= 16: the flow
+// folds the cross attention of single-request groups, building the factors two heads a chunk from
+// operand rows masked per head; packed request groups keep the unfolded launches.  The packed
+// layout then holds the query weight twice (qc as is, qct transposed).
+bool xattn_fold2(const cfh_flow_dims* d);
 
 }  // namespace cfh

@@ -33,6 +33,8 @@ struct SEx {
   int S;               // activation rows (<= 16)
   int Sr;              // S_SELF / S_CROSS: rows per request (requests packed in the S rows; 0 = S)
   int pack;            // E_PART16: each k-chunk's [S][N] block in frag_index order
+  int hrows;           // E_PART16: rows per output block (0 = S): row r of k-chunk kc goes to block
+                       // kc * (S / hrows) + r / hrows, as its row r % hrows
 };
 
 // For the attention kinds a k-chunk of KC = K / ks columns holds KC / hd whole heads (one head
@@ -327,8 +329,9 @@ __global__ void __launch_bounds__(WV * 64) k_stream(SArgs a) {
           if constexpr (EPI == E_PART) {
             ((float*)ex.out)[((size_t)kc * ex.S + r) * a.N + n] = acc[q];
           } else if constexpr (EPI == E_PART16) {
-            h16* o = (h16*)ex.out + (size_t)kc * ex.S * a.N;
-            o[ex.pack ? frag_index(r, n, ex.S) : (size_t)r * a.N + n] = (h16)acc[q];
+            const int hr = ex.hrows > 0 ? ex.hrows : ex.S, hb = r / hr, rr = r - hb * hr;
+            h16* o = (h16*)ex.out + ((size_t)kc * (ex.S / hr) + hb) * hr * a.N;
+            o[ex.pack ? frag_index(rr, n, hr) : (size_t)rr * a.N + n] = (h16)acc[q];
           } else {
             float bv;
             if (ct == 0) bv = bias0;

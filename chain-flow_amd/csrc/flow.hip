@@ -47,8 +47,11 @@
 // Wo (P V) = sum_h P_h (Wo_h V_h); the two d x (H C) factors are built once per draft from Wq and
 // Wo, and no block pass streams those two d x d matrices again (2 d^2 of the 18 d^2 halves a block
 // pass reads).  Same products in exact arithmetic; q and the attention output are not rounded to
-// fp16 on the way.  Shapes with several heads per MFMA k-chunk (head width not a multiple of 32)
-// keep the unfolded QC / OC streaming launches.
+// fp16 on the way.  With two heads per MFMA k-chunk (head widths such as 80 or 240) one k-chunk's
+// operand holds the context rows twice, each copy masked to one of its heads, so one weight stream
+// still yields every head's factor apart (single-request groups: 2 C rows fill the 16-row tile;
+// packed groups keep the unfolded QC / OC launches, and the packed image holds Wq both ways).
+// Four heads per k-chunk keep the unfolded launches.
 //
 #include <stdio.h>
 
@@ -360,6 +363,36 @@ __global__ void __launch_bounds__(1024) k_xbias(XbiasArgs a) {
   }
 }
 
+// The two-heads fold's operand rows: for every expert, block l and part (context K, then V), rows
+// [j][c] = row c of the part with the columns of all but the j-th head of each 2 hd-wide k-chunk set
+// to zero, so that one k-chunk's 2 C rows give both of its heads' factors apart.
+struct FoldMaskArgs {
+  const h16* kv[4];      // [L][2][C][d] (the cross K/V rows)
+  h16* out[4];           // [L][2][2][C][d]
+  int nex, nl, C, d, hd;
+};
+
+__global__ void __launch_bounds__(256) k_fold_mask(FoldMaskArgs a) {
+  const int nv = a.d / 8;                                        // 8-column vectors a row
+  const size_t per_ex = (size_t)a.nl * 2 * 2 * a.C * nv;
+  const size_t total = per_ex * a.nex;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    const int e = (int)(i / per_ex);
+    size_t t = i - (size_t)e * per_ex;
+    const int v = (int)(t % nv);
+    t /= nv;
+    const int c = (int)(t % a.C);
+    t /= a.C;
+    const int j = (int)(t % 2);
+    const size_t lp = t / 2;                                     // l * 2 + part
+    const int col = v * 8;                                       // a vector lies inside one head
+    const bool keep = ((col % (2 * a.hd)) >= a.hd) == (j == 1);
+    const h16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+    const h16x8 x = *(const h16x8*)(a.kv[e] + (lp * a.C + c) * a.d + col);
+    *(h16x8*)(a.out[e] + ((lp * 2 + j) * a.C + c) * a.d + col) = keep ? x : zero;
+  }
+}
+
 // Column blocks per (expert, head) of XATT: the fewest that give each thread at most one column
 // (each block recomputes the head's scores, so more blocks only repeat that work); 0 if d has no
 // such split.
@@ -389,7 +422,9 @@ struct Plan {
   int wpb_qc, wpb_w2, wpb_out, tpw_att, wpb_att, wpb_full, wpb_w1;
   int pks;            // partial slots per expert
   int res_mode;       // RES_ADD32 (fused-kernel numerics) or RES_ADD16 (torch fp16 modules)
-  bool fold;          // cross attention folded into per-draft factors (cfh::xattn_fold)
+  bool fold;          // cross attention folded into per-draft factors (cfh::xattn_fold / xattn_fold2)
+  bool fold2;         // ... built two heads a k-chunk from operand rows masked per head (xattn_fold2)
+  int ks_fold, S_fold; // the factor launch's k-chunks and operand rows
   bool conc;          // chunk experts on concurrent streams within an Euler step (conc_experts)
   int wpb_fold, xnb;  // fold hoist launch waves / XATT column blocks per (expert, head)
   bool ok;
@@ -407,6 +442,11 @@ Plan make_plan(const cfh_flow_dims* dm, int R = 1) {
   const int out_rows = R == 1 ? p.CS : p.Smax;   // OUT: the current chunk's rows, or every row when packed
   p.res_mode = dm->numerics == CFH_FLOW_MODULES ? RES_ADD16 : RES_ADD32;
   p.fold = cfh::xattn_fold(dm);
+  // two heads per k-chunk: folded for single-request groups only (2 x Ct operand rows per tile)
+  p.fold2 = !p.fold && cfh::xattn_fold2(dm) && 2 * p.Ct <= 16;
+  p.fold = p.fold || p.fold2;
+  p.ks_fold = p.fold2 ? p.H / 2 : p.H;
+  p.S_fold = p.fold2 ? 2 * p.Ct : p.Ct;
   // Concurrent chunk experts double the block passes' launches; below d = 1024 the host's launch
   // rate, not the GPU, then sets the pace of an eager draft (the latent flow at d = 640: +0.13 ms a
   // draft on two streams), so narrow shapes keep every expert in one launch.
@@ -444,8 +484,9 @@ Plan make_plan(const cfh_flow_dims* dm, int R = 1) {
   fit_grid(tiles_d, p.nch * p.ks_qc, &p.wpb_qc, nullptr);
   fit_grid(tiles_d, p.nch * p.ks_out, &p.wpb_out, nullptr);
   p.pks = std::max(std::max(p.ks_att, p.ks_w2), p.ks_out);
+  if (p.fold) p.pks = std::max(p.pks, p.H);   // the folded cross attention's per-head partials
   if (p.fold) {
-    p.wpb_fold = wpb_for_grid(tiles_d, 2 * p.nch * p.H, 8, p.Ct * p.hd / 8);
+    p.wpb_fold = wpb_for_grid(tiles_d, 2 * p.nch * p.ks_fold, 8, p.S_fold * (p.d / p.ks_fold) / 8);
     p.xnb = xattn_blocks(p.d, p.nch * p.H);
   }
   p.ok = p.ks_qc > 0 && p.ks_qc <= 8 && p.ks_w2 > 0 && p.ks_out > 0 && p.ks_att > 0 && res_nq(p.d) > 0 &&
@@ -458,7 +499,7 @@ Plan make_plan(const cfh_flow_dims* dm, int R = 1) {
     a.ks_in = p.ks_qc; a.Ck = p.Ct;
     return a;
   };
-  const bool cross_ok = p.fold ? !stream_check(S_BUF, sa(p.d, p.d, p.H, p.wpb_fold, 1), p.Ct) && p.xnb > 0
+  const bool cross_ok = p.fold ? !stream_check(S_BUF, sa(p.d, p.d, p.ks_fold, p.wpb_fold, 1), p.S_fold) && p.xnb > 0
                               : !stream_check(S_BUF, sa(p.d, p.d, p.ks_qc, p.wpb_qc, 1), p.Smax) &&
                                     !stream_check(S_CROSS, sa(p.d, p.d, p.ks_att, p.wpb_att, p.tpw_att), p.Smax);
   p.ok = !stream_check(S_BUF, sa(3 * p.d, p.d, 1, p.wpb_full, 1), p.Smax) &&
@@ -490,6 +531,7 @@ struct WS {
   h16* fa[4];         // folded shapes: A [L][H][C][d] = Wq_h^T K_h^T
   h16* fb[4];         //                B [L][H][C][d] = Wo_h V_h
   float* fsb[4];      //                sb [L][H][C] = bq_h . K_h
+  h16* fm[4];         // fold2: context K / V rows masked per head [L][2][2][C][d] (K/V, head in chunk)
   float* Pkv;         // [nch][L][ks][C][2d]
   float* Ptau;        // [nch][ks][E][d]
   float* ctx_mom;     // [C][2]
@@ -521,6 +563,7 @@ WS carve(const Plan& p, char* base) {
       w.fb[c] = (h16*)take((size_t)p.NL * p.H * p.Ct * d * 2);
       w.fsb[c] = (float*)take((size_t)p.NL * p.H * p.Ct * 4);
     }
+    if (p.fold2) w.fm[c] = (h16*)take((size_t)p.NL * 2 * 2 * p.Ct * d * 2);
   }
   w.Pkv = (float*)take((size_t)p.nch * p.NL * p.ks_kv * p.Ct * 2 * d * 4);
   w.Ptau = (float*)take((size_t)p.nch * p.ks_tau * p.E * d * 4);
@@ -535,7 +578,7 @@ WS expert_view(const WS& w, int c0) {
   for (int c = 0; c + c0 < 4; ++c) {
     v.x[c] = w.x[c + c0]; v.abuf[c] = w.abuf[c + c0]; v.qkv[c] = w.qkv[c + c0]; v.g[c] = w.g[c + c0];
     v.P[c] = w.P[c + c0]; v.Pq[c] = w.Pq[c + c0]; v.tau[c] = w.tau[c + c0]; v.kvc[c] = w.kvc[c + c0];
-    v.fa[c] = w.fa[c + c0]; v.fb[c] = w.fb[c + c0]; v.fsb[c] = w.fsb[c + c0];
+    v.fa[c] = w.fa[c + c0]; v.fb[c] = w.fb[c + c0]; v.fsb[c] = w.fsb[c + c0]; v.fm[c] = w.fm[c + c0];
   }
   return v;
 }
@@ -638,7 +681,8 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
     }
     if ((rc = launch_stream<S_CROSS, E_PART>(a, p.Smax, st)) || (rc = done())) return rc;
   }
-  // residual + LN_ffn
+  // residual + LN_ffn (the folded cross attention leaves one partial per head, OC one per k-chunk)
+  r.ks = p.fold ? p.H : p.ks_att;
   for (int c = 0; c < nch; ++c) {
     r.bias[c] = (const h16*)PTR(c, B + L.oc_b);
     r.g[c] = (const h16*)PTR(c, B + L.fn_w); r.b[c] = (const h16*)PTR(c, B + L.fn_b);
@@ -902,28 +946,41 @@ int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* expert
       }
       hipLaunchKernelGGL(k_xbias, dim3(nch * NL), dim3(1024), 0, st, xb);
       CFH_LAUNCH_CHECK();
+      if (p.fold2) {
+        FoldMaskArgs fm = {};
+        fm.nex = nch; fm.nl = NL; fm.C = Cg; fm.d = d; fm.hd = p.hd;
+        for (int c = 0; c < nch; ++c) { fm.kv[c] = w.kvc[c]; fm.out[c] = w.fm[c]; }
+        hipLaunchKernelGGL(k_fold_mask, dim3(256), dim3(256), 0, st, fm);
+        CFH_LAUNCH_CHECK();
+      }
       for (int l = 0; l < NL; ++l) {
         const size_t per_l = (size_t)p.H * Cg * d;
         for (int half = 0; half < 2; ++half) {
           // A and B of every expert in one launch when they fit the launch's four weight sets
           if (half == 1 && 2 * nch <= 4) break;
           SArgs a = {};
-          a.N = d; a.K = d; a.ks = p.H; a.wpb = p.wpb_fold; a.tpw = 1; a.d = d; a.hd = p.hd;
+          a.N = d; a.K = d; a.ks = p.ks_fold; a.wpb = p.wpb_fold; a.tpw = 1; a.d = d; a.hd = p.hd;
           a.wg_per_kc = (d / 16) / a.wpb;
           for (int part = 0; part < 2; ++part) {
             if (2 * nch > 4 && part != half) continue;
             for (int c = 0; c < nch; ++c) {
               SEx& x = a.ex[a.nex++];
               const h16* kv = w.kvc[c] + (size_t)l * 2 * Cg * d;
-              x.w = (const h16x8*)PTR(c, BLK(l) + (part == 0 ? L.qc : L.oc));
-              x.a = part == 0 ? kv : kv + (size_t)Cg * d;
+              x.w = (const h16x8*)PTR(c, BLK(l) + (part == 0 ? (p.fold2 ? L.qct : L.qc) : L.oc));
+              if (p.fold2) {   // 2 Cg rows a k-chunk: its first head's, then its second head's
+                x.a = w.fm[c] + (size_t)(l * 2 + part) * 2 * Cg * d;
+                x.S = 2 * Cg;
+              } else {
+                x.a = part == 0 ? kv : kv + (size_t)Cg * d;
+                x.S = Cg;
+              }
+              x.hrows = Cg;         // one head's factor block per Cg rows
               x.lda = d;
               x.out = (part == 0 ? w.fa[c] : w.fb[c]) + (size_t)l * per_l;
-              x.S = Cg;
               x.pack = part == 0;   // A: the cross attention's score operand image
             }
           }
-          if ((rc = launch_stream<S_BUF, E_PART16>(a, p.Ct, st))) return rc;
+          if ((rc = launch_stream<S_BUF, E_PART16>(a, p.S_fold, st))) return rc;
         }
       }
     }

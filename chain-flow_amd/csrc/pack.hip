@@ -43,9 +43,15 @@ bool xattn_fold(const cfh_flow_dims* d) {
   return heads_per_chunk(hd, d->heads) == 1 && d->ctx_rows <= 16;
 }
 
+bool xattn_fold2(const cfh_flow_dims* d) {
+  const int hd = d->d / d->heads;
+  return heads_per_chunk(hd, d->heads) == 2 && 2 * d->ctx_rows <= 16;
+}
+
 ExpertLayout expert_layout(const cfh_flow_dims* dm) {
   const size_t d = dm->d, fd = (size_t)dm->ffn_mult * dm->d, H = 2;  // 2 bytes per element
   ExpertLayout L;
+  L.fold2 = xattn_fold2(dm);
   size_t off = 0;
   auto take = [&](size_t bytes) {
     size_t o = off;
@@ -87,6 +93,7 @@ ExpertLayout expert_layout(const cfh_flow_dims* dm) {
   L.oc = btake(d * d * H);
   L.w1 = btake(fd * d * H);
   L.w2 = btake(d * fd * H);
+  L.qct = L.fold2 ? btake(d * d * H) : 0;
   L.blkstride = b;
   off = L.blk0 + b * dm->layers;
   L.on_w = take(d * H);
@@ -216,6 +223,12 @@ int cfh_flow_pack_expert(const cfh_flow_dims* dims, const void* const* raw, int 
       CFH_HIP(hipGetLastError());
     } else {
       CFH_TRY(pk(B + L.qc, r[10], (int)d, (int)d));
+    }
+    if (L.fold2) {
+      // and transposed, for the fold of single-request groups
+      hipLaunchKernelGGL(k_pack_linear_t, dim3(1024), dim3(256), 0, st, (const uint16_t*)r[10], (int)d, (int)d,
+                         (uint4*)(base + B + L.qct));
+      CFH_HIP(hipGetLastError());
     }
     CFH_TRY(pk(B + L.kv, (const char*)r[10] + d * d * 2, (int)(2 * d), (int)d));
     CFH_TRY(cp(B + L.qc_b, r[11], d));

@@ -118,3 +118,24 @@ def test_flow_caps_shape_checks_without_a_device():
     assert L.cfh_caps(None, 1, None) == 2
     # a config field the flow ignores leaves the plan alone
     assert caps(flow_dims(dataclasses.replace(head, noise_scale=0.5)))[1] == ws1
+
+
+def test_flow_two_heads_fold_layout_without_a_device():
+    """A head width that puts two heads in an MFMA k-chunk (640 / 8 = 80) folds the cross attention
+    of single-request groups and keeps the unfolded launches for packed groups, so the expert image
+    holds the query weight twice: exactly one d x d fp16 matrix per block more than the same width
+    with one head a k-chunk (640 / 10 = 64).  Both batch sizes are supported."""
+    import ctypes as C
+
+    from chain_flow_amd.config import flownet
+    from chain_flow_amd.flow import flow_dims
+    L = _lib.lib()
+    layers, d = 3, 640
+    two = flow_dims(flownet(d, layers=layers, flow_steps=2, num_heads=8))
+    one = flow_dims(flownet(d, layers=layers, flow_steps=2, num_heads=10))
+    extra = L.cfh_flow_expert_bytes(C.byref(two)) - L.cfh_flow_expert_bytes(C.byref(one))
+    assert extra == layers * d * d * 2
+    for dims in (two, one):
+        for batch in (1, 2, 3):
+            ws = C.c_int64(-1)
+            assert L.cfh_caps(C.byref(dims), batch, C.byref(ws)) == 0 and ws.value > 0

@@ -499,9 +499,16 @@ Plan make_plan(const cfh_flow_dims* dm, int R = 1) {
     a.ks_in = p.ks_qc; a.Ck = p.Ct;
     return a;
   };
-  const bool cross_ok = p.fold ? !stream_check(S_BUF, sa(p.d, p.d, p.ks_fold, p.wpb_fold, 1), p.S_fold) && p.xnb > 0
-                              : !stream_check(S_BUF, sa(p.d, p.d, p.ks_qc, p.wpb_qc, 1), p.Smax) &&
-                                    !stream_check(S_CROSS, sa(p.d, p.d, p.ks_att, p.wpb_att, p.tpw_att), p.Smax);
+  auto unfolded_ok = [&]() {
+    return !stream_check(S_BUF, sa(p.d, p.d, p.ks_qc, p.wpb_qc, 1), p.Smax) &&
+           !stream_check(S_CROSS, sa(p.d, p.d, p.ks_att, p.wpb_att, p.tpw_att), p.Smax);
+  };
+  bool cross_ok = p.fold ? !stream_check(S_BUF, sa(p.d, p.d, p.ks_fold, p.wpb_fold, 1), p.S_fold) && p.xnb > 0
+                         : unfolded_ok();
+  if (!cross_ok && p.fold2) {   // the two-heads fold does not fit this shape: the unfolded launches
+    p.fold = p.fold2 = false;
+    cross_ok = unfolded_ok();
+  }
   p.ok = !stream_check(S_BUF, sa(3 * p.d, p.d, 1, p.wpb_full, 1), p.Smax) &&
          !stream_check(S_SELF, sa(p.d, p.d, p.ks_att, p.wpb_att, p.tpw_att), p.Smax) && cross_ok &&
          !stream_check(S_BUF, sa(p.fd, p.d, 1, p.wpb_w1, 1), p.Smax) &&

@@ -315,6 +315,13 @@ def cpu_baseline_c1(dev, reps=3):
             greedy = chain(pred, 1)
             ts.append(t1 - t0)
             tg.append(time.perf_counter() - t1)
+        # (untimed) the searches' decision margins, for the same-run comparison with the GPU's ids
+        near = {}
+        for name, width in (("chain", Wd), ("greedy", 1)):
+            _, tr = obeam.beam_chains(pred, known0, s64, width, K, cfg.path_order, score, resid, numerics="fp32",
+                                      return_trace=True)
+            near[name] = min(float(min(ohead.margins(t["lp"], width).min(), ohead.margins(t["cand"], width).min()))
+                             for t in tr)
     assert pred.dtype == np.float32
     med = lambda v: sorted(v)[len(v) // 2]
     return {"value": round(med(ts) * 1e6, 1), "unit": "us per draft step", "cores": n, "kind": "port",
@@ -324,7 +331,75 @@ def cpu_baseline_c1(dev, reps=3):
                        f"{cpu_model()} host (os.cpu_count() {os.cpu_count()})"),
             "runs_s": [round(t, 3) for t in ts],
             "greedy_chain_us": round(med(tg) * 1e6, 1),
-            "chain_ids": [int(x) for x in ids[0]], "greedy_ids": [int(x) for x in greedy[0]]}
+            "chain_ids": [int(x) for x in ids[0]], "greedy_ids": [int(x) for x in greedy[0]],
+            "min_decision_margin": {k: round(v, 6) for k, v in near.items()},
+            "_pred": pred}
+
+
+def c1_gpu_vs_cpu(dev, c1):
+    """The same C1 draft on the GPU in fp16 (the weights of the CPU run rounded to fp16, the same
+    context and known token): the predicted hiddens against the CPU's fp32 ones, and the chain and
+    greedy ids against the CPU's, which must be equal wherever every decision margin of the CPU's
+    search exceeds 1e-3."""
+    import numpy as np
+    import torch
+    from chain_flow_amd.config import flownet
+    from chain_flow_amd.drafter import Drafter
+    from chain_flow_amd.shortlist import synthetic
+    from chain_flow_amd.weights import make_weights, synthetic_context
+    d, K = 2560, 5
+    cfg = flownet(d, layers=8, flow_steps=8)
+    W = make_weights(cfg, VOCAB, init="baseline", dtype=torch.float16, device=dev, base_seed=0)
+    sl = synthetic(VOCAB, SHORTLIST_ROWS, seed=2)
+    dr = Drafter(cfg, W, sl.to(dev), device=dev)
+    del W
+    ctx = synthetic_context(1, cfg.context_size, d, seed=1).to(dev)
+    known0 = sl[1234:1235].long().to(dev)
+    pred = dr.predict_hidden(ctx)
+    chain = dr.beam_chains(None, known0, K, 4, pred=pred)[0].tolist()
+    greedy = dr.beam_chains(None, known0, K, 1, pred=pred)[0].tolist()
+    torch.cuda.synchronize()
+    cpu_pred = c1["_pred"].astype(np.float64)
+    gp = pred.double().cpu().numpy()
+    err = float(np.linalg.norm(gp - cpu_pred) / np.linalg.norm(cpu_pred))
+    out = {"pred_rel_err_fp16_vs_fp32": round(err, 6), "tolerance": 2e-3}
+    for name, ids in (("chain", chain), ("greedy", greedy)):
+        want = c1[f"{name}_ids"]
+        margin = c1["min_decision_margin"][name]
+        out[name] = {"gpu_ids": ids, "cpu_ids": want, "equal": ids == want, "cpu_min_margin": margin,
+                     "required": margin > 1e-3}
+    out["parity"] = all(out[n]["equal"] or not out[n]["required"] for n in ("chain", "greedy")) and err < 2e-3
+    del dr
+    torch.cuda.empty_cache()
+    return out
+
+
+def graph_replay_ms(step, warmup=10, replays=200):
+    """The whole draft captured once in a HIP graph, ``warmup`` replays, then ``replays`` replays
+    each timed with events on the replaying stream: (median ms, 10th and 90th percentiles)."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(replays)]
+    for a, b in ev:
+        a.record()
+        g.replay()
+        b.record()
+    torch.cuda.synchronize()
+    t = sorted(a.elapsed_time(b) for a, b in ev)
+    del g
+    return t[len(t) // 2], t[len(t) // 10], t[(9 * len(t)) // 10]
 
 
 def cpu_baseline(W, cfg, sl, d):
@@ -455,8 +530,8 @@ def verify_bench(dev, iters=200, warmup=20):
             par_d.data_ptr(), N, H, Dk, Dv, 1, 0, out.data_ptr(), None, st),
         "gdn_serving_bf16_slots": lambda: L.cfh_gdn_tree_vllm(
             mixed.data_ptr(), a_.data_ptr(), b_.data_ptr(), A_log.data_ptr(), dt_bias.data_ptr(), slots.data_ptr(), 1,
-            node_slots.data_ptr(), par_d.data_ptr(), 1, N, H, HV, Dk, Dv, 1, C.c_float(Dk ** -0.5), o_vllm.data_ptr(),
-            st),
+            N + 2, node_slots.data_ptr(), par_d.data_ptr(), 1, N, H, HV, Dk, Dv, 1, C.c_float(Dk ** -0.5),
+            o_vllm.data_ptr(), None, st),
         "tree_conv": lambda: L.cfh_tree_conv(
             cx.data_ptr(), dim, cst.data_ptr(), cw.data_ptr(), cb.data_ptr(), node_slots.data_ptr(), par_d.data_ptr(),
             1, N, dim, 1, cout.data_ptr(), dim, st),
@@ -720,6 +795,11 @@ def main():
     if args.twopass:
         workload += f", two-pass head M={args.twopass} shared"
     flow_gbs = fb / (med(flow_ms) * 1e-3) / 1e9
+    # the flow's bytes as the reference's algorithm needs them (cross q / out projections streamed in
+    # every block pass), beside the folded algorithm's that `fb` counts
+    fb_unfolded = flow_bytes(LATENT if latent else d, L, E, cfg.num_chunks, fold=False) + (vae_bytes(d) if latent else 0)
+    print("[bench] graph replays", file=sys.stderr, flush=True)
+    g_med, g_p10, g_p90 = graph_replay_ms(lambda: dr.beam_chains(None, known0, K, Wd, pred=dr.predict_hidden(ctx)))
     out = {
         "metric": metric,
         "value": round(ms * 1e3, 1),
@@ -736,9 +816,23 @@ def main():
                    "shortlist_rows": SHORTLIST_ROWS, "vocab": VOCAB},
         "breakdown_ms": {"flow": round(med(flow_ms), 4), "head_beam": round(med(head_ms), 4),
                          "step_event": round(med(step_ms), 4)},
-        "algorithmic_bytes": {"flow": fb, "head": hb, "draft_gbs": round((fb + hb) / (ms * 1e-3) / 1e9, 1)},
+        "algorithmic_bytes": {"flow": fb, "flow_unfolded": fb_unfolded, "head": hb,
+                              "draft_gbs": round((fb + hb) / (ms * 1e-3) / 1e9, 1),
+                              "draft_gbs_unfolded": round((fb_unfolded + hb) / (ms * 1e-3) / 1e9, 1)},
         "roofline": {"bound": "hbm", "achieved": round(flow_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(flow_gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": kern},
+                     "frac": round(flow_gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": kern,
+                     "algorithmic_bytes": fb,
+                     "frac_on_unfolded_bytes": round(fb_unfolded / (med(flow_ms) * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "note": ("frac counts the bytes the folded cross attention needs; frac_on_unfolded_bytes the "
+                              "reference algorithm's (cross q / out projections in every block pass)")},
+        "graph_replay": {"median_ms": round(g_med, 4), "p10_ms": round(g_p10, 4), "p90_ms": round(g_p90, 4),
+                         "replays": 200, "warmup": 10,
+                         "draft_frac": round((fb + hb) / (g_med * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                         "draft_frac_on_unfolded_bytes": round((fb_unfolded + hb) / (g_med * 1e-3) / 1e9
+                                                               / HBM_PEAK_GBS, 4),
+                         "what": "the whole draft (predict_hidden + beam) captured once as a HIP graph, "
+                                 "each replay timed with events; a captured flow keeps its chunk experts on "
+                                 "one stream"},
     }
     if latent:
         out["config"].update({"latent": LATENT, "vae_intermediate": VAE_INTER, "vae_layers": VAE_LAYERS})
@@ -755,7 +849,11 @@ def main():
             out[f"cpu_baseline_d{d}_extrapolated"] = cpu_baseline(W, cfg, dr.head.sl, d)
             del W, dr
             torch.cuda.empty_cache()
-            out["cpu_baseline"] = cpu_baseline_c1(dev)
+            c1 = cpu_baseline_c1(dev)
+            print("[bench] C1 on the GPU against the CPU run", file=sys.stderr, flush=True)
+            out["c1_gpu_vs_cpu"] = c1_gpu_vs_cpu(dev, c1)
+            c1.pop("_pred")
+            out["cpu_baseline"] = c1
     print(json.dumps(out), flush=True)
 
 

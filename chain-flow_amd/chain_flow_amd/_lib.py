@@ -44,6 +44,9 @@ SIGNATURES = {
     "cfh_flow_pack_expert": (_I, [C.POINTER(FlowDims), C.POINTER(_VP), _I, _VP, _VP]),
     "cfh_flow_integrate": (_I, [C.POINTER(FlowDims), C.POINTER(_VP), _VP, _VP, _VP, _I, _VP]),
     "cfh_flow_integrate_noalloc": (_I, [C.POINTER(FlowDims), C.POINTER(_VP), _VP, _VP, _I, _VP]),
+    "cfh_flow_prepare_streams": (_I, [C.POINTER(FlowDims), _VP, C.POINTER(_I)]),
+    "cfh_flow_query_streams": (_I, [_VP, C.POINTER(_I), C.POINTER(_I)]),
+    "cfh_flow_release_streams": (_I, [_VP]),
     "cfh_vae_bytes": (_I64, [C.POINTER(VaeDims)]),
     "cfh_vae_pack": (_I, [C.POINTER(VaeDims), C.POINTER(_VP), _I, _VP, _VP]),
     "cfh_vae_caps": (_I, [C.POINTER(VaeDims), _I, C.POINTER(_I64)]),
@@ -77,8 +80,8 @@ SIGNATURES = {
     "cfh_beam_tree_step": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _I, _VP]),
     "cfh_beam_backtrack": (_I, [_VP, _VP, _VP, _I, _I, _I, _VP, _VP]),
     "cfh_gdn_tree": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _VP, _VP, _VP]),
-    "cfh_gdn_tree_vllm": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _I, _VP, _VP, _I, _I, _I, _I, _I, _I, _I,
-                               C.c_float, _VP, _VP]),
+    "cfh_gdn_tree_vllm": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _VP, _VP, _I, _I, _I, _I, _I, _I, _I,
+                               C.c_float, _VP, _VP, _VP]),
 }
 
 

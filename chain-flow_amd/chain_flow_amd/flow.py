@@ -64,16 +64,18 @@ def caps(cfg: TreeFlowConfig, batch: int = 1):
 class FusedFlow:
     """Packed chunk experts + workspace for one drafter on one device."""
 
-    def __init__(self, cfg: TreeFlowConfig, weights: dict, device="cuda"):
+    def __init__(self, cfg: TreeFlowConfig, weights: dict, device="cuda", max_batch: int = 256):
         self.cfg = cfg
         self.device = torch.device(device)
         if self.device.type == "cuda" and self.device.index is None:
             self.device = torch.device("cuda", torch.cuda.current_device())
         self.dims = flow_dims(cfg)
         L = _lib.lib()
-        ws = caps(cfg, 1)
-        if ws is None:
+        if caps(cfg, 1) is None:
             raise ValueError(f"flow shape not supported by libcfhip: {cfg}")
+        # One workspace for every batch up to max_batch (the largest request group's), allocated
+        # once: a captured draft graph holds its address, so it is never swapped or freed.
+        ws = caps(cfg, max(1, int(max_batch)))
         nbytes = int(L.cfh_flow_expert_bytes(C.byref(self.dims)))
         self.packed = []
         stream = _lib.stream_handle()
@@ -88,6 +90,19 @@ class FusedFlow:
             self.packed.append(buf)
         self._experts = _lib.ptr_array([b.data_ptr() for b in self.packed])
         self.ws = torch.empty(ws, dtype=torch.uint8, device=self.device)
+        self._retired = []   # outgrown workspaces, kept alive for graphs that may still use them
+        self.concurrent = self.prepare_streams()
+
+    def prepare_streams(self, stream=None) -> bool:
+        """Creates the companion streams of ``stream`` (default: the current one) and runs their
+        one-time overlap check now, so that no later ``predict_hidden`` on it synchronises
+        (``cfh_flow_prepare_streams``).  True if the chunk experts will run concurrently."""
+        if self.device.type != "cuda" or torch.cuda.is_current_stream_capturing():
+            return False
+        conc = C.c_int(0)
+        _lib.check(_lib.lib().cfh_flow_prepare_streams(C.byref(self.dims), _lib.stream_handle(stream),
+                                                       C.byref(conc)), "cfh_flow_prepare_streams")
+        return bool(conc.value)
 
     @property
     def weight_bytes(self) -> int:
@@ -116,6 +131,8 @@ class FusedFlow:
         if need is None:
             raise ValueError(f"flow shape not supported by libcfhip at batch {B}: {cfg}")
         if need > self.ws.numel():
+            # (a batch above max_batch: the old workspace stays referenced, never freed)
+            self._retired.append(self.ws)
             self.ws = torch.empty(need, dtype=torch.uint8, device=self.device)
         self.dims.numerics = reference_numerics(cfg, B) if numerics is None else int(numerics)
         if cfg.init_mode == "noise":

@@ -46,17 +46,21 @@ def tree_gated_delta_scan(q, k, v, g, beta, parent, S0, *, use_qk_l2norm: bool =
 
 
 def tree_gdn_vllm(mixed_qkv, a, b, A_log, dt_bias, ssm_state, node_slots, parent, *, num_q_heads: int,
-                  prefix_slot: int = 1, scale: float | None = None, use_qk_l2norm: bool = True):
+                  prefix_slot: int = 1, scale: float | None = None, use_qk_l2norm: bool = True,
+                  status: torch.Tensor | None = None):
     """The serving form of the tree GDN (``tree_scan_gdn_recurrence_path``,
     ``cf/vllm_tree/tree_ssm.py:256-351``; bit-identical by construction to the per-node slot form
-    ``:34-96``): one launch of ``cfh_gdn_tree_vllm``.
+    ``:34-96``): one launch of ``cfh_gdn_tree_vllm``, with no host synchronisation (a verify step
+    of many layers can be captured in one graph).
 
     mixed_qkv [N, 2 H K + HV V] bf16 (q heads | k heads | value heads), a, b [N, HV] bf16, A_log,
     dt_bias [HV], ssm_state [slots, HV, V, K] bf16 or fp32 (updated in place: node n's state goes to
     slot node_slots[n]; every node starts from slot ``prefix_slot``), parent [N] (BFS, -1 = root).
-    -> o [N, HV, V] bf16."""
+    -> o [N, HV, V] bf16.  The node slots are checked on the device: a node whose slot lies outside
+    ssm_state, equals the prefix slot or repeats another node's gets NaN outputs and writes no
+    slot, and ``status`` (int32 [1] on the device, zeroed by the caller), if given, is set to 1."""
     N, conv = mixed_qkv.shape
-    _, HV, V, K = ssm_state.shape
+    nslots, HV, V, K = ssm_state.shape
     H = int(num_q_heads)
     if conv != 2 * H * K + HV * V:
         raise ValueError(f"mixed_qkv width {conv} != 2*{H}*{K} + {HV}*{V}")
@@ -64,15 +68,14 @@ def tree_gdn_vllm(mixed_qkv, a, b, A_log, dt_bias, ssm_state, node_slots, parent
         raise ValueError("mixed_qkv, a, b must be bf16")
     if ssm_state.dtype not in (torch.bfloat16, torch.float32) or not ssm_state.is_contiguous():
         raise ValueError("ssm_state must be a contiguous bf16 or fp32 [slots, HV, V, K] tensor")
-    if a.shape != (N, HV) or b.shape != (N, HV):
-        raise ValueError("a, b must be [N, HV]")
+    if a.shape != (N, HV) or b.shape != (N, HV) or node_slots.numel() != N:
+        raise ValueError("a, b must be [N, HV] and node_slots [N]")
+    if not 0 <= int(prefix_slot) < nslots:
+        raise ValueError(f"prefix slot {prefix_slot} is outside ssm_state's {nslots} slots")
+    if status is not None and (status.dtype != torch.int32 or status.device != mixed_qkv.device):
+        raise ValueError("status must be an int32 tensor on the GDN's device")
     dev = mixed_qkv.device
     slots = node_slots.to(dev, torch.int32).contiguous()
-    nslots = ssm_state.shape[0]
-    if int(slots.min()) < 0 or int(slots.max()) >= nslots or not 0 <= prefix_slot < nslots:
-        raise ValueError("slot index out of range of ssm_state")
-    if len(set(slots.tolist())) != N or prefix_slot in set(slots.tolist()):
-        raise ValueError("node slots must be distinct from each other and from the prefix slot")
     x, a, b = mixed_qkv.contiguous(), a.contiguous(), b.contiguous()
     A_log = A_log.to(dev, torch.float32).contiguous()
     dt_bias = dt_bias.to(dev, torch.float32).contiguous()
@@ -80,7 +83,7 @@ def tree_gdn_vllm(mixed_qkv, a, b, A_log, dt_bias, ssm_state, node_slots, parent
     out = torch.empty(N, HV, V, dtype=torch.bfloat16, device=dev)
     _lib.check(_lib.lib().cfh_gdn_tree_vllm(
         x.data_ptr(), a.data_ptr(), b.data_ptr(), A_log.data_ptr(), dt_bias.data_ptr(), ssm_state.data_ptr(),
-        int(ssm_state.dtype == torch.bfloat16), slots.data_ptr(), parent.data_ptr(), int(prefix_slot), N, H, HV,
-        K, V, int(bool(use_qk_l2norm)), float(K ** -0.5 if scale is None else scale), out.data_ptr(),
-        _lib.stream_handle()), "cfh_gdn_tree_vllm")
+        int(ssm_state.dtype == torch.bfloat16), nslots, slots.data_ptr(), parent.data_ptr(), int(prefix_slot), N,
+        H, HV, K, V, int(bool(use_qk_l2norm)), float(K ** -0.5 if scale is None else scale), out.data_ptr(),
+        _lib.ptr(status), _lib.stream_handle()), "cfh_gdn_tree_vllm")
     return out

@@ -22,7 +22,10 @@ Mirrors ``chain_flow.vllm_plugin.flow_proposer.FlowDrafterProposer`` (``cf/vllm_
   ``:916-961``; ``cfh_ring_step``), with the slot lifecycle of ``_ctx_gpu`` (``:2045-2105``: a new
   request resets or seeds its slot, a request moved by vLLM's batch condense carries its history),
   and the ring step + draft run as one captured graph per batch bucket (``CF_CUDAGRAPH``,
-  ``CF_DRAFT_BUCKETS``; ``:1342-1365, 1511-1589``).
+  ``CF_DRAFT_BUCKETS``; ``:1342-1365, 1511-1589``) wherever the draft is launch-bound; where the
+  flow's chunk experts run on concurrent streams the draft runs eagerly (the reference pairs its
+  chunk experts on two streams inside its graphs, ``cf/cuda_block.py:452-466``; a captured HIP
+  flow keeps them on one stream, which is slower than the eager overlap).
 
 Drafters: the reference builds every checkpoint as the latent ``TreeVAEFlowDrafter``
 (``:583, 616-632``), with the VAE from ``CF_VAE_DIR`` / the config's ``vae_dir`` overlaid by the
@@ -197,7 +200,15 @@ class FlowDrafterProposer:
         self.shortlist_path = os.environ.get("CF_SHORTLIST")
         self.max_reqs = int(vllm_config.scheduler_config.max_num_seqs)
         self.path_trim = os.environ.get("CF_PATH_TRIM", "1") != "0"
-        self.use_cg = os.environ.get("CF_CUDAGRAPH", "1") == "1"
+        # CF_CUDAGRAPH: "1" (default) captures the ring step + draft per batch bucket where the draft
+        # is bound by launch latency, and runs it eagerly where the flow's chunk experts run on
+        # concurrent streams (a captured flow keeps them on one stream and is slower: d = 5120,
+        # 20.9 against 19.7 ms a draft); "force" always captures, "0" never does
+        cg = os.environ.get("CF_CUDAGRAPH", "1")
+        if cg not in ("0", "1", "force"):
+            raise ValueError(f"CF_CUDAGRAPH={cg!r}: expected 0, 1 or force")
+        self.use_cg = cg != "0"
+        self.force_cg = cg == "force"
         # two-pass candidate head, on by default as in the reference's defaults table
         # (cf/defaults.py:123-127): M = CF_TWOPASS_M (8192), one candidate set for all depths
         # (CF_TWOPASS_SHARED=1), pass A on the bare marginals (CF_TWOPASS_SEED=0)
@@ -275,8 +286,9 @@ class FlowDrafterProposer:
         # rows one request can append per step: the committed token plus every accepted draft
         self.kmax = (self.tree_depth + 1) if self.branching else (self.K + 1)
         self.ring = ContextRing(self.max_reqs, self.ctx_size, H, device=self.dev)
+        capture = self.use_cg and (self.force_cg or not self.drafter.flow.concurrent)
         self.graphs = (DraftGraphs(self.ring, self._draft_fn, self.kmax, bucket_ladder(self.max_reqs))
-                       if self.use_cg else None)
+                       if capture else None)
 
     # ---- drafting --------------------------------------------------------------------------
     def _draft_fn(self, ctx: torch.Tensor, known0: torch.Tensor) -> torch.Tensor:

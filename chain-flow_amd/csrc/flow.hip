@@ -845,6 +845,30 @@ int companions(hipStream_t st, int n, bool create, Companions* out) {
   return CFH_OK;
 }
 
+// Destroys the companions of caller stream st on the current device (none: nothing to do).  The
+// streams are destroyed after their queued work ends (hipStreamDestroy's contract).
+int release_companions(hipStream_t st) {
+  int dev = 0;
+  CFH_HIP(hipGetDevice(&dev));
+  Companions c = {};
+  {
+    std::lock_guard<std::mutex> lock(g_comp_mu);
+    auto it = g_comp.find({dev, st});
+    if (it == g_comp.end()) return CFH_OK;
+    c = it->second;
+    g_comp.erase(it);
+  }
+  for (int i = 0; i < c.made; ++i) {
+    CFH_HIP(hipStreamDestroy(c.s[i]));
+    CFH_HIP(hipEventDestroy(c.join[i]));
+    CFH_HIP(hipEventDestroy(c.up[i]));
+    CFH_HIP(hipEventDestroy(c.down[i]));
+    CFH_HIP(hipEventDestroy(c.mark[i]));
+  }
+  if (c.fork) CFH_HIP(hipEventDestroy(c.fork));
+  return CFH_OK;
+}
+
 // The whole draft of `batch` requests on workspace ws (the plan's carve() layout): per request the
 // per-draft launches, then E Euler steps of L block passes and the OUT / ROWS step.
 int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* experts, const void* ctx, void* z_out,
@@ -1124,6 +1148,34 @@ int cfh_flow_integrate(const cfh_flow_dims* dm, const void* const* experts, cons
     if (!experts[c]) return CFH_E_INVALID;
   return integrate(p, dm, experts, ctx, z_out, ws_ptr, batch, (hipStream_t)stream);
 }
+
+int cfh_flow_prepare_streams(const cfh_flow_dims* dm, void* stream, int* concurrent) {
+  if (concurrent) *concurrent = 0;
+  if (!cfh::flow_dims_ok(dm) || dm->d > ROWT * ROWE || dm->draft_length > MAXR) return CFH_E_UNSUPPORTED;
+  const Plan p = make_plan(dm, 1);
+  if (!p.ok) return CFH_E_UNSUPPORTED;
+  if (!p.conc) return CFH_OK;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  CFH_HIP(hipStreamIsCapturing((hipStream_t)stream, &cap));
+  if (cap != hipStreamCaptureStatusNone) return CFH_E_INVALID;   // the check synchronises the stream
+  Companions cp = {};
+  const int rc = companions((hipStream_t)stream, p.nch - 1, true, &cp);
+  if (rc) return rc;
+  if (concurrent) *concurrent = cp.made >= p.nch - 1 && cp.overlap;
+  return CFH_OK;
+}
+
+int cfh_flow_query_streams(void* stream, int* companions_made, int* concurrent) {
+  if (!companions_made || !concurrent) return CFH_E_INVALID;
+  Companions cp = {};
+  const int rc = companions((hipStream_t)stream, 0, false, &cp);
+  if (rc) return rc;
+  *companions_made = cp.made;
+  *concurrent = cp.made > 0 && cp.overlap;
+  return CFH_OK;
+}
+
+int cfh_flow_release_streams(void* stream) { return release_companions((hipStream_t)stream); }
 
 int cfh_flow_integrate_noalloc(const cfh_flow_dims* dm, const void* const* experts, const void* ctx, void* z_out,
                                int batch, void* stream) {

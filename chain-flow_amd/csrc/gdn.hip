@@ -225,7 +225,8 @@ struct GdnVArgs {
   const int* slots;      // [N]
   const int* parent;     // [N]
   uint16_t* out;         // [N][HV][V] bf16
-  int N, H, HV, V, ld, prefix, bf16_state, l2norm;
+  int* status;           // [1] or null: set to 1 when a node's slot is refused
+  int N, H, HV, V, ld, prefix, nslots, bf16_state, l2norm;
   float scale;
 };
 
@@ -341,7 +342,16 @@ __global__ void __launch_bounds__(64 * GDN_NW) k_gdn_tree_vllm(GdnVArgs a) {
   else
     rows_in((const float*)a.state + (size_t)a.prefix * srow + sblk, S, rows);
   const float Aexp = expf(a.A_log[hv]), dtb = a.dt_bias[hv];
-  if (gdn_path(a.parent, n, par, path, &plen_s, &bad_s)) {   // not BFS-ordered: NaN outputs, slot untouched
+  // the node's slot must lie in ssm_state, differ from the prefix slot and from every other node's
+  // (checked here rather than on the host, so that a caller never synchronises to validate them)
+  const int my = a.slots[n];
+  int clash = 0;
+  for (int m = threadIdx.x; m < a.N; m += blockDim.x) clash |= m != n && a.slots[m] == my;
+  clash = __syncthreads_or(clash);
+  const bool refused = clash || my < 0 || my >= a.nslots || my == a.prefix;
+  if (refused && a.status && threadIdx.x == 0) a.status[0] = 1;
+  if (refused || gdn_path(a.parent, n, par, path, &plen_s, &bad_s)) {
+    // refused slot or not BFS-ordered: NaN outputs, no slot written
     if (wave == 0) a.out[((size_t)n * a.HV + hv) * a.V + j] = 0x7fc0;
     return;
   }
@@ -442,19 +452,20 @@ int cfh_gdn_tree(const void* q, const void* k, const void* v, const float* g, co
 }
 
 int cfh_gdn_tree_vllm(const void* mixed_qkv, const void* a, const void* b, const float* A_log, const float* dt_bias,
-                      void* ssm_state, int state_bf16, const int32_t* node_slots, const int32_t* parent,
+                      void* ssm_state, int state_bf16, int nslots, const int32_t* node_slots, const int32_t* parent,
                       int prefix_slot, int N, int H, int HV, int K, int V, int use_l2norm, float scale,
-                      void* out, void* stream) {
+                      void* out, int32_t* status, void* stream) {
   if (!mixed_qkv || !a || !b || !A_log || !dt_bias || !ssm_state || !node_slots || !parent || !out)
     return CFH_E_INVALID;
-  if (N < 1 || N > GDN_MAXN || H < 1 || HV < H || HV % H || V < 64 || V % 64 || prefix_slot < 0)
+  if (N < 1 || N > GDN_MAXN || H < 1 || HV < H || HV % H || V < 64 || V % 64 || prefix_slot < 0 ||
+      prefix_slot >= nslots)
     return CFH_E_INVALID;
   if (K != GDN_DK) return CFH_E_UNSUPPORTED;
   GdnVArgs g = {};
   g.qkv = (const uint16_t*)mixed_qkv; g.ga = (const uint16_t*)a; g.gb = (const uint16_t*)b;
   g.A_log = A_log; g.dt_bias = dt_bias; g.state = ssm_state; g.slots = node_slots; g.parent = parent;
   g.out = (uint16_t*)out; g.N = N; g.H = H; g.HV = HV; g.V = V; g.ld = 2 * H * K + HV * V;
-  g.prefix = prefix_slot; g.bf16_state = state_bf16 ? 1 : 0; g.l2norm = use_l2norm ? 1 : 0; g.scale = scale;
+  g.prefix = prefix_slot; g.nslots = nslots; g.status = status; g.bf16_state = state_bf16 ? 1 : 0; g.l2norm = use_l2norm ? 1 : 0; g.scale = scale;
   const long long blocks = (long long)N * HV * (V / 64);
   hipLaunchKernelGGL(k_gdn_tree_vllm, dim3((unsigned)blocks), dim3(64 * GDN_NW), 0, (hipStream_t)stream, g);
   CFH_LAUNCH_CHECK();

@@ -28,7 +28,6 @@ constexpr int HCOLS = HW * 16;
 constexpr int HMAXM = 8;    // max activation rows of the in-place GEMV head
 constexpr int KMAX = 16;    // max top-k
 constexpr int PATH_CHUNK = 16;   // rows of one path-residual launch sequence (the GEMV's row limit)
-constexpr int PATH_MAXM = 256;   // rows of one cfh_path_residual call
 
 // (value, index) order: larger value first, equal values by lower index.
 __device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
@@ -1313,7 +1312,7 @@ int cfh_head_gemm16_topk(const void* x, int M, int d, const void* packed, int n,
 }
 
 int64_t cfh_path_ws_bytes(int M, int d, int ffn_mult, int order) {
-  if (M < 1 || M > PATH_MAXM || d < 512 || d % 512 || ffn_mult < 1 || order < 1 || order > MAXEX) return -1;
+  if (M < 1 || d < 512 || d % 512 || ffn_mult < 1 || order < 1 || order > MAXEX) return -1;
   return (int64_t)path_plan(std::min(M, PATH_CHUNK), d, ffn_mult, order).total;
 }
 
@@ -1381,7 +1380,7 @@ int cfh_path_residual(const void* const* ph, int order, int ffn_mult, int d, con
                       int nlive, const void* embed_w, const void* pred, long long pred_ld, int rows_per_pred,
                       void* hsum, void* ws, void* stream) {
   if (!ph || !lastp || !embed_w || !pred || !hsum || !ws) return CFH_E_INVALID;
-  if (M < 1 || M > PATH_MAXM || d < 512 || d % 512 || ffn_mult < 1 || order < 1 || order > MAXEX) return CFH_E_INVALID;
+  if (M < 1 || d < 512 || d % 512 || ffn_mult < 1 || order < 1 || order > MAXEX) return CFH_E_INVALID;
   if (rows_per_pred < 0 || pred_ld < 0) return CFH_E_INVALID;
   const int n_ptr = 2 * order + 6;
   for (int i = 0; i < n_ptr; ++i)

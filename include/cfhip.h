@@ -4,7 +4,11 @@
  * passed as void*; NULL = the null stream) and returns 0 (CFH_OK) or an error code
  * (cfh_error_string() names it).  Nothing here allocates device memory: callers own the weights,
  * the workspace and the outputs.  All launches are asynchronous on the given stream and may be
- * recorded into a HIP graph (no memset nodes, no host synchronisation inside).
+ * recorded into a HIP graph (no memset nodes).  One exception to "no host synchronisation": the
+ * first eager cfh_flow_integrate on a caller stream (for flows whose chunk experts run
+ * concurrently) creates that stream's companion streams and events and checks once, with a
+ * synchronisation of the caller's stream, that they run alongside it; cfh_flow_prepare_streams
+ * does that at set-up time instead, and nothing under stream capture ever does it.
  *
  * The reference (Cosmos-YTU/chain-flow, `cf/` = src/chain_flow/) binds its hot path through a
  * pybind torch extension (cf/csrc/fused_block.cu:793-862) plus plain torch ops; each entry point
@@ -114,10 +118,35 @@ int cfh_flow_pack_expert(const cfh_flow_dims* dims, const void* const* raw, int 
  *   ws      : workspace of cfh_caps(dims, batch) bytes
  * A batch runs in groups of up to two requests whose rows share every weight stream (when both
  * drafts fit one 16-row MFMA tile and the shape's operand staging allows it).
+ * Chunk experts (d >= 1024, two or more chunks) run their Euler steps on companion streams of the
+ * caller's stream, forked after the per-draft launches and joined before return.  The first eager
+ * call on a caller stream without companions creates them (streams, events: kept until
+ * cfh_flow_release_streams) and runs the overlap check of cfh_flow_prepare_streams, which
+ * synchronises the caller's stream once; under stream capture every expert stays on the caller's
+ * stream and nothing is created.  Same results on one stream or several, bit for bit.
  * Replaces the per-Euler-step torch loop plus the fused kernel launch
- * (cf/cuda_block.py:407-431 / pybind `expert`, `cross_kv`, cf/csrc/fused_block.cu:793-862). */
+ * (cf/cuda_block.py:407-431 / pybind `expert`, `cross_kv`, cf/csrc/fused_block.cu:793-862) and the
+ * reference's two-stream chunk pair (cf/cuda_block.py:452-466). */
 int cfh_flow_integrate(const cfh_flow_dims* dims, const void* const* experts, const void* ctx,
                        void* z_out, void* ws, int batch, void* stream);
+
+/* Set-up of the companion streams of a caller stream, so that no later cfh_flow_integrate on it
+ * synchronises: creates the companions `dims`'s chunk experts need (none for flows that stay on one
+ * stream) and checks once that work on them overlaps work on the caller's stream (two 200 us wait
+ * kernels, then a synchronisation of the caller's stream).  HIP maps a process's streams onto a
+ * few hardware queues, and streams that share one run in submission order: then the flow keeps
+ * every expert on the caller's stream.  *concurrent = 1 when the experts will run concurrently.
+ * CFH_E_INVALID under stream capture.  Mirrors the reference's side-stream set-up for its chunk
+ * pair (cf/cuda_block.py:452-466). */
+int cfh_flow_prepare_streams(const cfh_flow_dims* dims, void* stream, int* concurrent);
+/* The companions of a caller stream on the current device: how many exist, and whether the flow
+ * runs its chunk experts on them (the overlap check passed).  Creates nothing. */
+int cfh_flow_query_streams(void* stream, int* companions, int* concurrent);
+/* Destroys the companions of a caller stream (their queued work completes first).  Call it before
+ * destroying the caller's stream: the companions are keyed by the stream handle, and a later
+ * stream that reuses the handle would inherit their overlap verdict.  Not concurrently with a
+ * flow call on that stream. */
+int cfh_flow_release_streams(void* stream);
 
 /* cfh_flow_integrate without a caller workspace, for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  It has no
@@ -294,7 +323,8 @@ int cfh_head_gemm16_topk(const void* x, int M, int d, const void* packed, int n,
  *   norm.bias, mlp.0.weight [f*d][d], mlp.0.bias [f*d], mlp.3.weight [d][f*d], mlp.3.bias [d].
  * pred_m fp16 = the marginal hidden of this depth for row m's request: pred + (m / rows_per_pred) *
  * pred_ld (rows_per_pred = 0: every row uses pred[0..d)), so B requests' beams go in one call.
- * M <= 256.  ws: cfh_path_ws_bytes(M, ...) bytes (rows are processed 16 at a time). */
+ * Any M >= 1: rows are processed 16 at a time on one workspace of cfh_path_ws_bytes(M, ...) bytes
+ * (the same size for every M >= 16). */
 int64_t cfh_path_ws_bytes(int M, int d, int ffn_mult, int order);
 int cfh_path_residual(const void* const* ph, int order, int ffn_mult, int d, const int32_t* lastp,
                       int M, int nlive, const void* embed_w, const void* pred, long long pred_ld,
@@ -343,12 +373,16 @@ int cfh_gdn_tree(const void* q, const void* k, const void* v, const float* g, co
  *   ssm_state [slots][HV][V][K], bf16 (state_bf16 = 1) or fp32: every node starts from slot
  *   prefix_slot, replays its root->node path with each ancestor's state rounded to the storage
  *   type, writes its state to slot node_slots[n] and o [N][HV][V] bf16.
- * parent [N] int32 (BFS order, -1 = root).  K == 128, V % 64 == 0, N <= 256; node slots must be
- * distinct from each other and from prefix_slot.  Replaces tree_scan_gdn_recurrence[_path]. */
+ * parent [N] int32 (BFS order, -1 = root).  K == 128, V % 64 == 0, N <= 256; ssm_state holds
+ * nslots slots and 0 <= prefix_slot < nslots.  Node slots are validated on the device, so the call
+ * never synchronises and can be captured: a node whose slot lies outside [0, nslots), equals
+ * prefix_slot or is shared with another node gets NaN outputs, writes no slot, and sets status[0]
+ * to 1 (status: one int32 the caller zeroes, or NULL).  Replaces tree_scan_gdn_recurrence[_path]. */
 int cfh_gdn_tree_vllm(const void* mixed_qkv, const void* a, const void* b, const float* A_log,
-                      const float* dt_bias, void* ssm_state, int state_bf16, const int32_t* node_slots,
-                      const int32_t* parent, int prefix_slot, int N, int H, int HV, int K, int V,
-                      int use_l2norm, float scale, void* out, void* stream);
+                      const float* dt_bias, void* ssm_state, int state_bf16, int nslots,
+                      const int32_t* node_slots, const int32_t* parent, int prefix_slot, int N, int H,
+                      int HV, int K, int V, int use_l2norm, float scale, void* out, int32_t* status,
+                      void* stream);
 
 /* ---------------------------------------------------------------- rest of the tree verify
  * Tree causal conv1d, width 4 (cf/vllm_tree/tree_ssm.py:393-438; depth form :189-253): node n

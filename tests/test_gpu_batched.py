@@ -157,3 +157,29 @@ def test_batched_drafts_match_oracle(cuda, search, B, twopass):
             assert _near(tr, k1, k2), b
             bad += 1
     print(f"  {B - bad}/{B} requests equal to the oracle, the rest at near ties", flush=True)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("search,B", [("chain", 80), ("tree", 70)])
+def test_batches_past_256_beam_rows_equal_smaller_batches(cuda, search, B):
+    """80 width-4 chains (320 beam rows a depth) and 70 keep-4 trees (280): the path residual and
+    the head take every row in one call (16-row path chunks, 256-row head launches), and each
+    request's draft equals the same request drafted in a batch of half the size, bit for bit (every
+    kernel computes a row from that row's inputs alone)."""
+    cfg, W, sl = _setup()
+    dr = Drafter(cfg, {k: v.to(cuda) for k, v in W.items()}, sl.to(cuda), device=cuda)
+    ctx = synthetic_context(B, cfg.context_size, 512, seed=21).to(cuda)
+    known0 = sl[torch.randperm(len(sl), generator=torch.Generator().manual_seed(B))[:B]].long().to(cuda)
+    print(f"[batched {search}] B={B}: {4 * B} beam rows a depth", flush=True)
+    pred = dr.predict_hidden(ctx)
+
+    def run(lo, hi):
+        if search == "chain":
+            return dr.beam_chains(None, known0[lo:hi], 5, 4, pred=pred[lo:hi].contiguous())
+        return dr.beam_tree(None, known0[lo:hi], keep=4, topb=8, depth=4, pred=pred[lo:hi].contiguous())
+
+    whole = run(0, B)
+    h = B // 2
+    parts = torch.cat([run(0, h), run(h, B)])
+    torch.cuda.synchronize()
+    assert torch.equal(whole, parts)

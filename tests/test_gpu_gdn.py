@@ -188,3 +188,39 @@ def test_gdn_vllm_fp32_states_equal_research_kernel(cuda):
     assert rel_err(o.float().cpu().numpy(), ref_o.cpu().numpy()) < 4e-3
     got = st_d[2:N + 2].transpose(2, 3).cpu().numpy()
     assert rel_err(got, states.cpu().numpy()) < 1e-6
+
+
+@pytest.mark.gpu
+def test_gdn_vllm_refuses_bad_slots_on_the_device(cuda):
+    """Slot validation happens in the kernel (no host synchronisation): nodes 3 and 5 sharing a
+    slot, node 7 given the prefix slot and node 9 a slot past the state buffer get NaN outputs and
+    write nothing, the status word is set, and every other node equals the run with valid slots."""
+    from chain_flow_amd.gdn import tree_gdn_vllm
+    parent = beam_tree_parents()
+    N, H, K, V = len(parent), 16, 128, 128
+    X, a, b, A_log, dt_bias, st = _vllm_inputs(N, H, H, K, V, 13, torch.bfloat16)
+    good = torch.arange(2, N + 2, dtype=torch.int32)
+    bad = good.clone()
+    bad[5] = bad[3]
+    bad[7] = 1
+    bad[9] = st.shape[0]
+    args = (X.to(cuda), a.to(cuda), b.to(cuda), A_log, dt_bias)
+    st_good, st_bad = st.to(cuda), st.to(cuda)
+    s_good = torch.zeros(1, dtype=torch.int32, device=cuda)
+    s_bad = torch.zeros(1, dtype=torch.int32, device=cuda)
+    print("[gdn vllm refused slots] 31 nodes, slots 3 = 5, 7 = prefix, 9 past the end", flush=True)
+    og = tree_gdn_vllm(*args, st_good, good, torch.tensor(parent), num_q_heads=H, status=s_good)
+    ob = tree_gdn_vllm(*args, st_bad, bad, torch.tensor(parent), num_q_heads=H, status=s_bad)
+    torch.cuda.synchronize()
+    assert int(s_good.item()) == 0 and int(s_bad.item()) == 1
+    refused = [3, 5, 7, 9]
+    assert torch.isnan(ob[refused].float()).all()
+    keep = [n for n in range(N) if n not in refused]
+    assert torch.equal(ob[keep], og[keep])
+    stb = st_bad.cpu()
+    for n in keep:
+        assert torch.equal(stb[int(bad[n])], st_good.cpu()[int(good[n])])
+    assert torch.equal(stb[int(bad[3])], st[int(bad[3])])          # the shared slot: untouched
+    assert torch.equal(stb[1], st[1])                               # the prefix slot: only read
+    for n in (7, 9):                                                # their valid slots: never written
+        assert torch.equal(stb[int(good[n])], st[int(good[n])])

@@ -68,3 +68,36 @@ def test_draft_graph_replays_equal_eager(cuda, kind, search, twopass):
         assert torch.equal(got, want), step
         assert torch.equal(graph_ring.ring[:, :C], eager_ring.ring[:, :C])
         assert torch.equal(graph_ring.rpos, eager_ring.rpos) and torch.equal(graph_ring.nval, eager_ring.nval)
+
+
+@pytest.mark.gpu
+def test_graph_of_a_smaller_bucket_survives_later_captures(cuda):
+    """Capturing bucket 2 after bucket 1 must not move anything graph 1 references: the flow's
+    workspace is sized for the largest request group when the drafter is built and never swapped.
+    After both captures a guard tensor takes whatever memory is free; replaying graph 1 leaves it
+    unchanged and still equals the eager draft."""
+    dr, d, sl = _drafter("target", cuda)
+    R, C, kmax = 2, 8, 4
+    eager_ring = ContextRing(R, C, d, device=cuda)
+    graph_ring = ContextRing(R, C, d, device=cuda)
+    draft = lambda ctx, k0: dr.beam_chains(ctx, k0, 5, 4)
+    graphs = DraftGraphs(graph_ring, draft, kmax, [1, 2])
+    rng = np.random.default_rng(4)
+    print("[graph guard] bucket 1, bucket 2, guard, bucket 1 again", flush=True)
+    guard = None
+    for step, B in enumerate([1, 2, 1, 1]):
+        rows = rng.permutation(R)[:B].tolist()
+        cnt = rng.integers(1, kmax + 1, size=B).tolist()
+        starts = np.concatenate([[0], np.cumsum(cnt)[:-1]]).tolist()
+        sh = torch.randn(sum(cnt), d, generator=torch.Generator().manual_seed(300 + step)).half().to(cuda)
+        k0 = sl[rng.integers(0, len(sl), size=B)].long().tolist()
+        ctx = eager_ring.step(sh, rows, starts, cnt, kmax=kmax)
+        want = draft(ctx, torch.tensor(k0, device=cuda)).clone()
+        got = graphs.run(sh, rows, starts, cnt, k0).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), step
+        if step == 1:
+            torch.cuda.empty_cache()
+            guard = torch.full((64 << 20,), 7, dtype=torch.uint8, device=cuda)
+    torch.cuda.synchronize()
+    assert int((guard != 7).sum()) == 0, "a graph replay wrote into memory it does not own"

@@ -43,11 +43,20 @@ def test_noalloc_flow_equals_workspace_flow(cuda):
         assert torch.equal(got, want), f"d={d}: noalloc differs from the workspace flow"
 
 
+def _companions(stream):
+    made, conc = C.c_int(-1), C.c_int(-1)
+    _lib.check(_lib.lib().cfh_flow_query_streams(_lib.stream_handle(stream), C.byref(made), C.byref(conc)),
+               "cfh_flow_query_streams")
+    return made.value, conc.value
+
+
 @pytest.mark.gpu
-def test_noalloc_first_on_a_stream_runs_one_stream(cuda):
-    """The no-allocation entry point creates no companion stream: called first on a fresh caller
-    stream it runs both chunk experts on that stream (d = 1024 would otherwise overlap them), and
-    the draft is bit-identical to the workspace flow's; a second call, smaller, still matches."""
+def test_noalloc_creates_no_streams(cuda):
+    """The no-allocation entry point creates no companion stream: on a caller stream the workspace
+    flow has not used, the companion count (cfh_flow_query_streams) is the same after the call as
+    before it -- zero unless a pooled stream handle already had companions -- and the draft is
+    bit-identical to the workspace flow's (d = 1024: the workspace flow runs its chunk experts
+    concurrently); a second call, smaller, still matches."""
     cfg = flownet(1024, layers=2, flow_steps=2)
     ff = _flow(cfg, cuda, 9)
     for batch in (2, 1):
@@ -56,8 +65,12 @@ def test_noalloc_first_on_a_stream_runs_one_stream(cuda):
         torch.cuda.synchronize()
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
+        before = _companions(side)
         with torch.cuda.stream(side):
             got = _noalloc(ff, ctx)
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
-        assert torch.equal(got, want), f"batch {batch}: noalloc on a fresh stream differs"
+        after = _companions(side)
+        print(f"  batch {batch}: companions of the side stream before {before}, after {after}", flush=True)
+        assert after == before, "the no-allocation entry point created companion streams"
+        assert torch.equal(got, want), f"batch {batch}: noalloc on a side stream differs"

@@ -320,8 +320,8 @@ def cpu_baseline_c1(dev, reps=3):
         for name, width in (("chain", Wd), ("greedy", 1)):
             _, tr = obeam.beam_chains(pred, known0, s64, width, K, cfg.path_order, score, resid, numerics="fp32",
                                       return_trace=True)
-            near[name] = min(float(min(ohead.margins(t["lp"], width).min(), ohead.margins(t["cand"], width).min()))
-                             for t in tr)
+            ms = [m for t in tr for m in (ohead.margins(t["lp"], width), ohead.margins(t["cand"], width)) if m.size]
+            near[name] = min(float(m.min()) for m in ms)
     assert pred.dtype == np.float32
     med = lambda v: sorted(v)[len(v) // 2]
     return {"value": round(med(ts) * 1e6, 1), "unit": "us per draft step", "cores": n, "kind": "port",

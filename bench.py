@@ -591,14 +591,15 @@ def gemm_bench(dev, iters=100, warmup=10):
 def batched_bench(dev, steps=3, warmup=1, B=32, d=4096, L=8, E=8, M=8192):
     """The batched drafting step: B requests, each a 5-token width-4 chain at d=4096 fp16 with the
     proposer's default two-pass head (M=8192 candidates shared across depths).  The flow drafts the
-    requests two to a weight stream; pass A scores the B*5 marginal hiddens in one fp16 MFMA GEMM
+    requests in groups that share every weight stream (cfh_flow_group_size: 16 requests a group at
+    d=4096); pass A scores the B*5 marginal hiddens in one fp16 MFMA GEMM
     over the 62,642-row shortlist (M=160 rows at B=32); each depth's B*4 beams run through the
     batched path residual and the grouped pass-B head.  Returns timings (ms, events on the stream)
     and byte counts."""
     import torch
     from chain_flow_amd.config import flownet
     from chain_flow_amd.drafter import Drafter
-    from chain_flow_amd.flow import caps
+    from chain_flow_amd.flow import group_size
     from chain_flow_amd.shortlist import synthetic
     from chain_flow_amd.weights import make_weights, synthetic_context
     K, Wd = 5, 4
@@ -641,11 +642,12 @@ def batched_bench(dev, steps=3, warmup=1, B=32, d=4096, L=8, E=8, M=8192):
     e1.record()
     torch.cuda.synchronize()
     pass_a_ms = e0.elapsed_time(e1) / n_a
-    groups = (B + 1) // 2 if caps(cfg, 2) != caps(cfg, 1) else B
+    R = group_size(cfg, B)
+    groups = (B + R - 1) // R
     fb = groups * flow_bytes(d, L, E, cfg.num_chunks, fold=(d // cfg.num_heads) % 32 == 0)
     return dict(flow_ms=flow_ms, head_ms=head_ms, pass_a_ms=pass_a_ms, flow_bytes=fb, groups=groups,
                 pass_a_bytes=SHORTLIST_ROWS * d * 2 + B * K * d * 2 + B * K * SHORTLIST_ROWS * 2,
-                B=B, d=d, L=L, E=E, M=M, K=K, W=Wd)
+                R=R, B=B, d=d, L=L, E=E, M=M, K=K, W=Wd)
 
 
 def main():
@@ -711,8 +713,8 @@ def main():
             "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
             "dtype": "fp16", "data": "synthetic (seeded N(0,0.02) weights, N(0,1) RMS-1 contexts)",
             "config": {"workload": f"batched chain draft: {r['B']} requests x {r['K']} tokens, width {r['W']}, "
-                                   f"d={r['d']} fp16, flow L={r['L']} E={r['E']} (requests drafted two to a weight "
-                                   f"stream: {r['groups']} groups), two-pass head M={r['M']} shared over a "
+                                   f"d={r['d']} fp16, flow L={r['L']} E={r['E']} (requests drafted {r['R']} to a "
+                                   f"weight stream: {r['groups']} groups), two-pass head M={r['M']} shared over a "
                                    f"{SHORTLIST_ROWS}-row shortlist"},
             "breakdown_ms": {"flow": round(r["flow_ms"], 3), "head_beam": round(r["head_ms"], 3),
                              "pass_a_gemm": round(r["pass_a_ms"], 4)},

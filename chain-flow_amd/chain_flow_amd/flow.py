@@ -61,6 +61,15 @@ def caps(cfg: TreeFlowConfig, batch: int = 1):
     return int(ws.value) if rc == 0 else None
 
 
+def group_size(cfg: TreeFlowConfig, batch: int) -> int:
+    """Requests per group that share every weight stream when ``batch`` requests are drafted."""
+    r = C.c_int(0)
+    rc = _lib.lib().cfh_flow_group_size(C.byref(flow_dims(cfg)), int(batch), C.byref(r))
+    if rc != 0:
+        raise ValueError(f"flow shape not supported by libcfhip at batch {batch}: {cfg}")
+    return int(r.value)
+
+
 class FusedFlow:
     """Packed chunk experts + workspace for one drafter on one device."""
 

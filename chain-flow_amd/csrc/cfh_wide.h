@@ -1,0 +1,318 @@
+// Wide request groups of the flow: many drafts share every weight stream.
+//
+// A batch of drafts is run in groups of up to 16 requests (128 activation rows for the second
+// chunk expert at draft_length 8) whose rows all multiply each packed weight fragment as it
+// streams past, so a group costs about one draft's weight traffic instead of one per two drafts.
+// The narrow streaming kernel (cfh_stream.h) stages its whole K chunk once and holds at most 16
+// rows; here the activation rows are staged in K chunks of WCH columns through two LDS buffers,
+// refilled while the weights stream:
+//
+//   chunk c:  issue the loads of chunk c+1's rows into registers (they return after the weight
+//             fragments already in flight, which the multiplies need first anyway)
+//             multiply WCH/32 fragments, each against every 16-row group of the rows in LDS
+//             place chunk c+1's rows in the other buffer, one LDS barrier
+//
+// A wave owns one 16-column tile of one (expert, k-split) unit and keeps one accumulator per
+// 16-row group.  Self attention, which the narrow kernel computes while staging, runs as its own
+// small kernel per (request, head), and the context rows' LayerNorm of every block is computed
+// once per draft into rows the cross K/V stream reads.
+#pragma once
+#include <algorithm>
+
+#include "cfh_stream.h"
+
+namespace {
+
+constexpr int WCH = 128;          // K columns staged per chunk (4 k-steps)
+constexpr int WKS = WCH / 32;     // k-steps per chunk
+constexpr int WSPF = 8;           // fragment loads in flight per wave (two chunks)
+constexpr int WMAXR = 128;        // max activation rows of one expert in a wide group
+constexpr int WLDA = WCH + 8;     // LDS row stride (halves): rows of a chunk start on different banks
+
+struct WEx {
+  const h16x8* w;      // packed weights: fragment (tile t, k-step s) at ((t * K/32) + s) * 64
+  const h16* a;        // activation rows [S][lda]; the unit's K range [kc K/ks, (kc+1) K/ks) is read
+  int lda;
+  const h16* bias;     // E_BIAS16 / E_GELU16 bias [N]
+  void* out;           // E_PART: float [ks][S][N]; E_PART16: h16 (as SEx); otherwise h16 (below)
+  int S;               // activation rows (1 .. WMAXR)
+  int pack, hrows;     // E_PART16: as SEx
+  int nsplit;          // E_BIAS16: column n goes to block n / nsplit, stored [blocks][S][nsplit] (0: [S][N])
+};
+
+struct WArgs {
+  WEx ex[4];
+  int nex, N, K, ks, wg_per_kc;
+  int gelu_r16;        // E_GELU16: as SArgs
+};
+
+template <int EPI, int NG, int WV>
+__global__ void __launch_bounds__(WV * 64) k_wide(WArgs a) {
+  extern __shared__ __align__(16) h16 lds[];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  int b = blockIdx.x;
+  const int per_ex = a.ks * a.wg_per_kc;
+  const int e = b / per_ex;
+  b -= e * per_ex;
+  const int kc = b / a.wg_per_kc;
+  const int tg = b - kc * a.wg_per_kc;
+  const WEx& ex = a.ex[e];
+  const int S = ex.S;
+  const int ksteps = a.K / 32;
+  const int KCW = a.K / a.ks, nsteps = KCW / 32, nchunk = KCW / WCH;
+  const int t = tg * WV + wave;                       // this wave's 16-column tile
+  const int k0 = kc * KCW;
+  // staging of one chunk: vector idx = u * nt + thread, row idx / 16, columns (idx % 16) * 8 .. +7;
+  // indices past the rows re-read the last vector (every load unconditional, see Stage)
+  constexpr int NT = WV * 64;
+  constexpr int NVR = WCH / 8;                        // 16-byte vectors per row of a chunk
+  constexpr int NSV = (NG * 16 * NVR + NT - 1) / NT;  // vectors per thread at the most rows
+  const int total = S * NVR;
+  h16x8 st[NSV];
+  auto load_chunk = [&](int c) {
+    const h16* base = ex.a + k0 + c * WCH;
+#pragma unroll
+    for (int u = 0; u < NSV; ++u) {
+      const int idx = min(u * NT + (int)threadIdx.x, total - 1);
+      const int i = idx / NVR, kk = (idx - i * NVR) * 8;
+      st[u] = *(const h16x8*)(base + (size_t)i * ex.lda + kk);
+    }
+  };
+  auto place_chunk = [&](h16* buf) {
+#pragma unroll
+    for (int u = 0; u < NSV; ++u) {
+      const int idx = min(u * NT + (int)threadIdx.x, total - 1);
+      const int i = idx / NVR, kk = (idx - i * NVR) * 8;
+      *(h16x8*)(buf + i * WLDA + kk) = st[u];
+    }
+  };
+  // the wave's fragments, walked one at a time; past the last one the pointer stays there, so the
+  // ring's surplus refills re-read a line just fetched
+  const h16x8* lw = ex.w + ((size_t)t * ksteps + (size_t)kc * nsteps) * 64 + lane;
+  int lleft = nsteps;
+  auto issue = [&]() -> h16x8 {
+    const h16x8 v = __builtin_nontemporal_load(lw);
+    const bool adv = lleft > 1;
+    lw += adv ? 64 : 0;
+    lleft -= adv;
+    return v;
+  };
+  const int col = lane & 15, rbase = 4 * (lane >> 4);
+  const int n = t * 16 + col;
+  float bias = 0.f;
+  if constexpr (EPI == E_BIAS16 || EPI == E_GELU16) bias = (float)ex.bias[n];
+  // operand chunk 0 first, then the weight prefetch (independent of it), then LDS
+  load_chunk(0);
+  __builtin_amdgcn_sched_barrier(0);
+  h16x8 ring[WSPF];
+#pragma unroll
+  for (int p = 0; p < WSPF; ++p) {
+    ring[p] = issue();
+    // issued in slot order: the loop's first multiply then waits for slot 0 alone (with the order
+    // left free, slot 0 went out seventh and that multiply waited for the whole ring)
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  h16* buf0 = lds;
+  h16* buf1 = lds + (size_t)S * WLDA;
+  place_chunk(buf0);
+  lds_barrier();
+  const int row = lane & 15, kg = lane >> 4;
+  const h16x8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+  f32x4 acc[NG];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) acc[g] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  // lanes of rows past S read row 0: their products land in output rows that are never stored
+  int roff[NG];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) roff[g] = (g * 16 + row < S ? g * 16 + row : 0) * WLDA + kg * 8;
+  // two chunks per ring cycle (WSPF = 2 WKS): slot p holds k-step p % WKS of chunk c0 + p / WKS
+  for (int c0 = 0; c0 < nchunk; c0 += 2) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = c0 + h;
+      // past the last chunk (an odd count) the zero fragments multiply the last chunk's rows, which
+      // are finite: the other buffer was never written, and 0 x NaN would poison the sums
+      const h16* cur = (min(c, nchunk - 1) & 1) ? buf1 : buf0;
+      h16* nxt = (c & 1) ? buf0 : buf1;
+      load_chunk(min(c + 1, nchunk - 1));
+#pragma unroll
+      for (int q = 0; q < WKS; ++q) {
+        const int p = h * WKS + q;
+        // (an odd chunk count leaves the last ring cycle's second half empty: its fragments are
+        // replaced by zeros rather than skipped, which keeps the loop free of branches; every row
+        // group is multiplied, rows past S reading row 0, for the same reason)
+        const h16x8 bf = c < nchunk ? ring[p] : zero8;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) acc[g] = mfma_f16(*(const h16x8*)(cur + roff[g] + q * 32), bf, acc[g]);
+        ring[p] = issue();
+        // one fragment's LDS reads and multiplies at a time: left free, the scheduler hoists every
+        // read of both chunks ahead of the multiplies and runs out of registers
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // chunk c + 1 goes to the other buffer (nobody reads it: every wave finished chunk c - 1
+      // before the last barrier); one barrier orders the stores before chunk c + 1's reads
+      if (c + 1 < nchunk) place_chunk(nxt);
+      lds_barrier();
+    }
+  }
+  // epilogue: rows g * 16 + rbase + q of column n
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    if (g * 16 >= S) continue;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r = g * 16 + rbase + q;
+      if (r >= S) continue;
+      const float v = acc[g][q];
+      if constexpr (EPI == E_PART) {
+        ((float*)ex.out)[((size_t)kc * S + r) * a.N + n] = v;
+      } else if constexpr (EPI == E_PART16) {
+        const int hr = ex.hrows > 0 ? ex.hrows : S, hb = r / hr, rr = r - hb * hr;
+        h16* o = (h16*)ex.out + ((size_t)kc * (S / hr) + hb) * hr * a.N;
+        o[ex.pack ? frag_index(rr, n, hr) : (size_t)rr * a.N + n] = (h16)v;
+      } else if constexpr (EPI == E_BIAS16) {
+        if (ex.nsplit > 0) {
+          const int part = n / ex.nsplit, nn = n - part * ex.nsplit;
+          ((h16*)ex.out)[((size_t)part * S + r) * ex.nsplit + nn] = (h16)(v + bias);
+        } else {
+          ((h16*)ex.out)[(size_t)r * a.N + n] = (h16)(v + bias);
+        }
+      } else {
+        const float u = v + bias;
+        ((h16*)ex.out)[(size_t)r * a.N + n] = (h16)gelu_erf(a.gelu_r16 ? r16(u) : u);
+      }
+    }
+  }
+}
+
+size_t wide_lds(int S_max) { return (size_t)2 * S_max * WLDA * 2; }
+
+template <int EPI, int NG, int WV>
+int launch_wide_k(const WArgs& a, size_t lds, hipStream_t st) {
+  static unsigned long long attr_set = 0;
+  int dev = 0;
+  CFH_HIP(hipGetDevice(&dev));
+  if (dev < 64 && !(attr_set & (1ull << dev))) {
+    CFH_HIP(hipFuncSetAttribute((const void*)k_wide<EPI, NG, WV>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                150 * 1024));
+    attr_set |= 1ull << dev;
+  }
+  const long long wgs = (long long)a.nex * a.ks * a.wg_per_kc;
+  hipLaunchKernelGGL((k_wide<EPI, NG, WV>), dim3((unsigned)wgs), dim3(WV * 64), lds, st, a);
+  CFH_LAUNCH_CHECK();
+  return CFH_OK;
+}
+
+// Shape checks of a wide launch (also used by the plan): CFH_OK when every unit of wv waves covers
+// whole tiles, every k-split a whole number of chunks, and the rows fit.
+int wide_check(const WArgs& a, int wv, int S_max) {
+  if (a.nex < 1 || a.nex > 4 || a.N <= 0 || a.N % 16 || a.ks <= 0 || a.K % a.ks || (a.K / a.ks) % WCH)
+    return CFH_E_UNSUPPORTED;
+  if ((wv != 4 && wv != 8) || (a.N / 16) % wv || S_max < 1 || S_max > WMAXR || wide_lds(S_max) > 150 * 1024)
+    return CFH_E_UNSUPPORTED;
+  return CFH_OK;
+}
+
+template <int EPI>
+int launch_wide(const WArgs& a0, int wv, hipStream_t st) {
+  WArgs a = a0;
+  int S_max = 0;
+  for (int e = 0; e < a.nex; ++e) S_max = std::max(S_max, a.ex[e].S);
+  if (wide_check(a, wv, S_max)) return CFH_E_UNSUPPORTED;
+  for (int e = 0; e < a.nex; ++e)
+    if (a.ex[e].S < 1 || a.ex[e].lda < a.K || !a.ex[e].w || !a.ex[e].a || !a.ex[e].out) return CFH_E_INVALID;
+  a.wg_per_kc = (a.N / 16) / wv;
+  const size_t lds = wide_lds(S_max);
+  const int ng = (S_max + 15) / 16;
+#define CFH_WIDE(G)                                                              \
+  if (ng <= G) return wv == 8 ? launch_wide_k<EPI, G, 8>(a, lds, st) : launch_wide_k<EPI, G, 4>(a, lds, st);
+  CFH_WIDE(2) CFH_WIDE(4) CFH_WIDE(8)
+#undef CFH_WIDE
+  return CFH_E_UNSUPPORTED;
+}
+
+// Causal self attention of a wide group, one workgroup per (expert, request, head): the request's
+// Sr rows of q, k, v (columns of head h of the [S][3d] rows) staged in LDS, then `attend` (the
+// narrow kernel's attention, same arithmetic), written as fp16 rows [S][d] of the attention output.
+struct SelfArgs {
+  const h16* qkv[4];   // [S][3d]
+  h16* out[4];         // [S][d]
+  int S[4], Sr[4];     // rows, rows per request
+  int nex, R, H, d, hd;
+};
+
+constexpr int SAT = 256;          // threads of a self-attention workgroup
+
+__global__ void __launch_bounds__(SAT) k_self_attn(SelfArgs a) {
+  extern __shared__ __align__(16) h16 sm[];
+  int b = blockIdx.x;
+  const int h = b % a.H;
+  b /= a.H;
+  const int j = b % a.R, e = b / a.R;
+  const int Sr = a.Sr[e], hd = a.hd, d = a.d;
+  if ((j + 1) * Sr > a.S[e]) return;                  // (a request the group does not hold)
+  const h16* src = a.qkv[e] + (size_t)j * Sr * 3 * d + h * hd;
+  h16* sq = sm;
+  h16* sk = sq + Sr * hd;
+  h16* sv = sk + Sr * hd;
+  float* P = (float*)(sv + Sr * hd);                  // [Sr][Sr]
+  const int nv = hd / 8;
+  for (int idx = threadIdx.x; idx < 3 * Sr * nv; idx += blockDim.x) {
+    const int part = idx / (Sr * nv), rem = idx - part * Sr * nv;
+    const int i = rem / nv, c = (rem - i * nv) * 8;
+    *(h16x8*)(sq + (size_t)(part * Sr + i) * hd + c) = *(const h16x8*)(src + (size_t)i * 3 * d + part * d + c);
+  }
+  lds_barrier();
+  attend(Sr, Sr, Sr, Sr, hd, hd, true, sq, sk, sv, P, a.out[e] + (size_t)j * Sr * d + h * hd, d);
+}
+
+int launch_self_attn(const SelfArgs& a, hipStream_t st) {
+  if (a.hd % 8 || a.hd <= 0 || a.nex < 1 || a.nex > 4) return CFH_E_UNSUPPORTED;
+  int Srm = 0;
+  for (int e = 0; e < a.nex; ++e) {
+    if (a.Sr[e] < 1 || a.Sr[e] > 16 || a.S[e] > a.R * a.Sr[e]) return CFH_E_UNSUPPORTED;
+    Srm = std::max(Srm, a.Sr[e]);
+  }
+  const size_t lds = (size_t)3 * Srm * a.hd * 2 + (size_t)Srm * Srm * 4;
+  if (lds > 64 * 1024) return CFH_E_UNSUPPORTED;
+  hipLaunchKernelGGL(k_self_attn, dim3((unsigned)(a.nex * a.R * a.H)), dim3(SAT), lds, st, a);
+  CFH_LAUNCH_CHECK();
+  return CFH_OK;
+}
+
+// The context rows' LayerNorm of every block, once per draft: rows[e][l][c] =
+// fp16((ctx[c] - mean_c) rstd_c g_l + b_l) with the row moments the ROWS kernel left in mom (the
+// narrow cross K/V stream applies the same formula while staging).
+struct CtxLnArgs {
+  const h16* ctx;      // [Ct][d]
+  const float* mom;    // [Ct][2]
+  const h16* g0[4];    // block 0's context_norm weight of each expert; block l at + l * vstride bytes
+  const h16* b0[4];
+  h16* out[4];         // [L][Ct][d]
+  long long vstride;
+  int nex, nl, Ct, d;
+};
+
+__global__ void __launch_bounds__(256) k_ctx_ln(CtxLnArgs a) {
+  const int nv = a.d / 8;
+  const size_t per_l = (size_t)a.Ct * nv, per_e = per_l * a.nl, total = per_e * a.nex;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    const int e = (int)(i / per_e);
+    size_t r = i - (size_t)e * per_e;
+    const int l = (int)(r / per_l);
+    r -= (size_t)l * per_l;
+    const int c = (int)(r / nv), k = (int)(r - (size_t)c * nv) * 8;
+    const h16* gw = (const h16*)((const char*)a.g0[e] + (size_t)l * a.vstride);
+    const h16* gb = (const h16*)((const char*)a.b0[e] + (size_t)l * a.vstride);
+    const h16x8 xv = *(const h16x8*)(a.ctx + (size_t)c * a.d + k);
+    const h16x8 gv = *(const h16x8*)(gw + k);
+    const h16x8 bv = *(const h16x8*)(gb + k);
+    const float mu = a.mom[2 * c], rs = a.mom[2 * c + 1];
+    h16x8 o;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) o[t] = (h16)(((float)xv[t] - mu) * rs * (float)gv[t] + (float)bv[t]);
+    *(h16x8*)(a.out[e] + ((size_t)l * a.Ct + c) * a.d + k) = o;
+  }
+}
+
+}  // namespace

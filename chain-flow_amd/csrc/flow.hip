@@ -59,7 +59,7 @@
 #include <map>
 #include <mutex>
 
-#include "cfh_stream.h"
+#include "cfh_wide.h"
 
 namespace {
 
@@ -252,8 +252,11 @@ struct XattArgs {
   float* out[4];         // partials [H][S][d]
   int S[4];
   int Sr[4];             // rows per request (the S rows hold S / Sr requests)
+  int Ssg[4];            // rows per subgroup (0: S): workgroups take the rows in subgroups of at
+                         // most 16, each with its own requests' context rows
   int nex, d, H, C, nb;  // C: context rows of all the group's requests
   int Cq;                // context rows per request: row r scores only its request's rows
+  int nsg, Csg;          // subgroups, context rows per subgroup (0: C)
   float scale;
 };
 
@@ -268,23 +271,31 @@ __global__ void __launch_bounds__(XT) k_xattn(XattArgs a) {
   int b = blockIdx.x;
   const int cb = b % a.nb;
   b /= a.nb;
+  const int sg = b % a.nsg;
+  b /= a.nsg;
   const int h = b % a.H, e = b / a.H;
-  const int S = a.S[e], C = a.C, d = a.d;
+  // this subgroup's rows [r0, r0 + S) of the expert's St rows and context rows [c0, c0 + C) of Ct
+  const int St = a.S[e], Ct = a.C, d = a.d;
+  const int Ssg = a.Ssg[e] > 0 ? a.Ssg[e] : St, Csg = a.Csg > 0 ? a.Csg : Ct;
+  const int r0 = sg * Ssg, c0 = sg * Csg;
+  const int S = min(Ssg, St - r0), C = min(Csg, Ct - c0);
+  if (S <= 0 || C <= 0) return;                      // (a subgroup past the group's requests)
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  // this thread's column of B_h (every context row), in flight before the scores
+  // this thread's column of B_h (every context row of the subgroup), in flight before the scores
   const int cpb = d / a.nb, n = cb * cpb + min(t, cpb - 1);
-  const h16* Bh = a.Bf[e] + (size_t)h * C * d + n;
+  const h16* Bh = a.Bf[e] + ((size_t)h * Ct + c0) * d + n;
   h16 bv[CM];
 #pragma unroll
   for (int c = 0; c < CM; ++c) bv[c] = Bh[(size_t)min(c, C - 1) * d];
   // scores: lane row = lane % 16, context row = lane % 16 of the B operand, k-group lane / 16.
-  // Lanes of rows past S or context rows past C load nothing (zero operands).
-  const h16* Ah = a.A[e] + (size_t)h * C * d;
+  // Lanes of rows past S or context rows past C load nothing (zero operands).  The operand
+  // images hold every row of the expert (St) and every context row (Ct).
+  const h16* Ah = a.A[e] + (size_t)h * Ct * d;
   const int ns = d / 32, per = (ns + NW - 1) / NW, s0 = wave * per, s1 = min(ns, s0 + per);
   const int ci = lane & 15, kg = lane >> 4;
   const bool xl = ci < S, al = ci < C;
-  const h16* xrow = a.xn[e] + ((size_t)kg * S + min(ci, S - 1)) * 8;    // + k-step * 4 S vectors
-  const h16* arow = Ah + ((size_t)kg * C + min(ci, C - 1)) * 8;
+  const h16* xrow = a.xn[e] + ((size_t)kg * St + r0 + min(ci, S - 1)) * 8;    // + k-step * 4 St vectors
+  const h16* arow = Ah + ((size_t)kg * Ct + c0 + min(ci, C - 1)) * 8;
   const h16x8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int r0 = s0; r0 < s1; r0 += XRS) {
@@ -294,8 +305,8 @@ __global__ void __launch_bounds__(XT) k_xattn(XattArgs a) {
       const int st = min(r0 + u, s1 - 1);
       xv[u] = zero8;
       av[u] = zero8;
-      if (xl) xv[u] = *(const h16x8*)(xrow + (size_t)st * 32 * S);
-      if (al) av[u] = *(const h16x8*)(arow + (size_t)st * 32 * C);
+      if (xl) xv[u] = *(const h16x8*)(xrow + (size_t)st * 32 * St);
+      if (al) av[u] = *(const h16x8*)(arow + (size_t)st * 32 * Ct);
     }
 #pragma unroll
     for (int u = 0; u < XRS; ++u)
@@ -312,7 +323,7 @@ __global__ void __launch_bounds__(XT) k_xattn(XattArgs a) {
 #pragma unroll
     for (int w = 0; w < NW; ++w) v += red[w][t];
     const bool ok = r < S && c < C && c / a.Cq == r / a.Sr[e];
-    const float sc = ok ? (v + a.sb[e][h * C + c]) * a.scale : -INFINITY;
+    const float sc = ok ? (v + a.sb[e][h * Ct + c0 + c]) * a.scale : -INFINITY;
     float m = sc;
     m = fmaxf(m, dpp_f32<DPP_XOR1>(m));
     m = fmaxf(m, dpp_f32<DPP_XOR2>(m));
@@ -325,7 +336,7 @@ __global__ void __launch_bounds__(XT) k_xattn(XattArgs a) {
   __syncthreads();
   // this thread's column of P_h B_h
   if (t < cpb) {
-    float* oh = a.out[e] + (size_t)h * S * d + n;
+    float* oh = a.out[e] + ((size_t)h * St + r0) * d + n;
     float bf[CM];
 #pragma unroll
     for (int c = 0; c < CM; ++c) bf[c] = (float)bv[c];
@@ -404,11 +415,14 @@ int xattn_blocks(int d, int units) {
 }
 
 int launch_xattn(const XattArgs& a, hipStream_t st) {
-  if (a.C > 16 || a.nb <= 0) return CFH_E_UNSUPPORTED;
-  for (int e = 0; e < a.nex; ++e)
-    if (a.S[e] > MAXR) return CFH_E_UNSUPPORTED;
-  const dim3 grid((unsigned)(a.nex * a.H * a.nb));
-  if (a.C <= 8) hipLaunchKernelGGL(k_xattn<8>, grid, dim3(XT), 0, st, a);
+  const int Csg = a.Csg > 0 ? a.Csg : a.C;
+  if (Csg > 16 || a.nb <= 0 || a.nsg < 1 || (long long)a.nsg * Csg < a.C) return CFH_E_UNSUPPORTED;
+  for (int e = 0; e < a.nex; ++e) {
+    const int Ssg = a.Ssg[e] > 0 ? a.Ssg[e] : a.S[e];
+    if (Ssg > MAXR || (long long)a.nsg * Ssg < a.S[e]) return CFH_E_UNSUPPORTED;
+  }
+  const dim3 grid((unsigned)(a.nex * a.H * a.nsg * a.nb));
+  if (Csg <= 8) hipLaunchKernelGGL(k_xattn<8>, grid, dim3(XT), 0, st, a);
   else hipLaunchKernelGGL(k_xattn<16>, grid, dim3(XT), 0, st, a);
   CFH_LAUNCH_CHECK();
   return CFH_OK;
@@ -427,8 +441,56 @@ struct Plan {
   int ks_fold, S_fold; // the factor launch's k-chunks and operand rows
   bool conc;          // chunk experts on concurrent streams within an Euler step (conc_experts)
   int wpb_fold, xnb;  // fold hoist launch waves / XATT column blocks per (expert, head)
+  bool wide;          // more than two requests a group: every row of the group shares each weight
+                      // stream through the chunked-staging kernels (cfh_wide.h)
+  int wv_qkv, wv_w1, wv_kv;        // wide full-K launches: waves per workgroup
+  int ks_wo, ks_ww2, ks_wout;      // wide split-K launches (4-wave workgroups): k-splits
   bool ok;
 };
+
+// Wide plan: launch shapes that give each streaming launch about one workgroup per CU (both chunk
+// experts in one launch), and whether every launch of the draft fits the wide kernels.
+void make_wide_plan(Plan& p, const cfh_flow_dims* dm) {
+  p.wide = true;
+  p.conc = false;
+  p.fold = cfh::xattn_fold(dm);
+  p.fold2 = false;
+  p.ks_fold = p.H;
+  p.S_fold = p.Ct;
+  p.ok = p.fold && p.hd % WCH == 0 && p.d % WCH == 0 && p.fd % WCH == 0 && p.Smax <= WMAXR && p.Ct <= WMAXR &&
+         p.C <= 8 && 2 * p.KD <= MAXR && res_nq(p.d) > 0;
+  if (!p.ok) return;
+  constexpr int CUS = 256;
+  auto wv_full = [&](int N) { return ((N / 16) % 8 == 0 && p.nch * (N / 16) / 8 >= CUS) ? 8 : 4; };
+  auto ks_split = [&](int N, int K) {
+    int best = 0;
+    for (int ks = 1; ks <= K / WCH; ++ks) {
+      if (K % ks || (K / ks) % WCH) continue;
+      best = ks;
+      if ((long long)p.nch * (N / 16 / 4) * ks >= CUS) break;
+    }
+    return best;
+  };
+  p.wv_qkv = wv_full(3 * p.d);
+  p.wv_w1 = wv_full(p.fd);
+  p.wv_kv = wv_full(2 * p.d);
+  p.ks_wo = ks_split(p.d, p.d);
+  p.ks_ww2 = ks_split(p.d, p.fd);
+  p.ks_wout = ks_split(p.d, p.d);
+  p.pks = std::max(std::max(p.H, p.ks_wo), std::max(p.ks_ww2, p.ks_wout));
+  p.xnb = xattn_blocks(p.d, p.nch * p.H);
+  auto wa = [&](int N, int K, int ks) {
+    WArgs a = {};
+    a.nex = p.nch; a.N = N; a.K = K; a.ks = ks;
+    return a;
+  };
+  p.ok = p.ks_wo > 0 && p.ks_ww2 > 0 && p.ks_wout > 0 && p.xnb > 0 &&
+         !wide_check(wa(3 * p.d, p.d, 1), p.wv_qkv, p.Smax) && !wide_check(wa(p.fd, p.d, 1), p.wv_w1, p.Smax) &&
+         !wide_check(wa(2 * p.d, p.d, 1), p.wv_kv, p.Ct) && !wide_check(wa(p.d, p.d, p.ks_wo), 4, p.Smax) &&
+         !wide_check(wa(p.d, p.fd, p.ks_ww2), 4, p.Smax) && !wide_check(wa(p.d, p.d, p.ks_wout), 4, p.Smax) &&
+         !wide_check(wa(p.d, p.d, p.H), 4, p.Ct) &&
+         (size_t)3 * p.KD * p.hd * 2 + (size_t)p.KD * p.KD * 4 <= 64 * 1024;   // self attention's LDS
+}
 
 Plan make_plan(const cfh_flow_dims* dm, int R = 1) {
   Plan p = {};
@@ -441,6 +503,11 @@ Plan make_plan(const cfh_flow_dims* dm, int R = 1) {
   p.Smax = R * p.KD;
   const int out_rows = R == 1 ? p.CS : p.Smax;   // OUT: the current chunk's rows, or every row when packed
   p.res_mode = dm->numerics == CFH_FLOW_MODULES ? RES_ADD16 : RES_ADD32;
+  p.ks_tau = ksplit_for(p.nch, p.d / 16, p.d, p.E);
+  if (p.Smax > MAXR) {
+    make_wide_plan(p, dm);
+    return p;
+  }
   p.fold = cfh::xattn_fold(dm);
   // two heads per k-chunk: folded for single-request groups only (2 x Ct operand rows per tile)
   p.fold2 = !p.fold && cfh::xattn_fold2(dm) && 2 * p.Ct <= 16;
@@ -517,10 +584,17 @@ Plan make_plan(const cfh_flow_dims* dm, int R = 1) {
   return p;
 }
 
-// Requests per group for a batch: the most (up to `batch`) whose rows fit one tile and whose plan
-// this build runs; 1 always works when the shape is supported.
-int group_size(const cfh_flow_dims* dm, int batch) {
-  for (int R = std::min(batch, MAXR / dm->draft_length); R > 1; --R)
+// Requests per group for a batch.  Wide groups (allow_wide, more than two requests): the batch in
+// as few groups of at most WMAXR / draft_length requests as possible, balanced; otherwise the
+// most requests (up to `batch`) whose rows fit one 16-row tile and whose plan this build runs.
+// 1 always works when the shape is supported.
+int group_size(const cfh_flow_dims* dm, int batch, bool allow_wide = true) {
+  const int KD = dm->draft_length;
+  if (allow_wide && batch * KD > MAXR && WMAXR / KD >= 3) {
+    const int rmax = WMAXR / KD, ng = (batch + rmax - 1) / rmax, R = (batch + ng - 1) / ng;
+    if (R * KD > MAXR && make_plan(dm, R).ok) return R;
+  }
+  for (int R = std::min(batch, MAXR / KD); R > 1; --R)
     if (make_plan(dm, R).ok) return R;
   return 1;
 }
@@ -539,6 +613,7 @@ struct WS {
   h16* fb[4];         //                B [L][H][C][d] = Wo_h V_h
   float* fsb[4];      //                sb [L][H][C] = bq_h . K_h
   h16* fm[4];         // fold2: context K / V rows masked per head [L][2][2][C][d] (K/V, head in chunk)
+  h16* cln[4];        // wide: context_norm(ctx) rows of every block [L][C][d]
   float* Pkv;         // [nch][L][ks][C][2d]
   float* Ptau;        // [nch][ks][E][d]
   float* ctx_mom;     // [C][2]
@@ -571,8 +646,9 @@ WS carve(const Plan& p, char* base) {
       w.fsb[c] = (float*)take((size_t)p.NL * p.H * p.Ct * 4);
     }
     if (p.fold2) w.fm[c] = (h16*)take((size_t)p.NL * 2 * 2 * p.Ct * d * 2);
+    if (p.wide) w.cln[c] = (h16*)take((size_t)p.NL * p.Ct * d * 2);
   }
-  w.Pkv = (float*)take((size_t)p.nch * p.NL * p.ks_kv * p.Ct * 2 * d * 4);
+  if (!p.wide) w.Pkv = (float*)take((size_t)p.nch * p.NL * p.ks_kv * p.Ct * 2 * d * 4);
   w.Ptau = (float*)take((size_t)p.nch * p.ks_tau * p.E * d * 4);
   w.ctx_mom = (float*)take((size_t)p.Ct * 2 * 4);
   w.total = off;
@@ -586,6 +662,7 @@ WS expert_view(const WS& w, int c0) {
     v.x[c] = w.x[c + c0]; v.abuf[c] = w.abuf[c + c0]; v.qkv[c] = w.qkv[c + c0]; v.g[c] = w.g[c + c0];
     v.P[c] = w.P[c + c0]; v.Pq[c] = w.Pq[c + c0]; v.tau[c] = w.tau[c + c0]; v.kvc[c] = w.kvc[c + c0];
     v.fa[c] = w.fa[c + c0]; v.fb[c] = w.fb[c + c0]; v.fsb[c] = w.fsb[c + c0]; v.fm[c] = w.fm[c + c0];
+    v.cln[c] = w.cln[c + c0];
   }
   return v;
 }
@@ -654,6 +731,7 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
   if (p.fold) {
     XattArgs x = {};
     x.nex = nch; x.d = d; x.H = p.H; x.C = Cg; x.Cq = p.C; x.nb = p.xnb; x.scale = 1.0f / sqrtf((float)p.hd);
+    x.nsg = 1;
     const size_t per_l = (size_t)p.H * Cg * d;
     for (int c = 0; c < nch; ++c) {
       x.xn[c] = w.abuf[c]; x.A[c] = w.fa[c] + (size_t)l * per_l; x.Bf[c] = w.fb[c] + (size_t)l * per_l;
@@ -734,6 +812,178 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
   }
   if ((rc = launch_res(r, st))) return rc;
   return done();
+}
+
+// The launches of block l for a wide group (every chunk expert in each launch, Rg requests): QKV,
+// self attention, O, residual, folded cross attention (in subgroups of two requests), residual,
+// W1, W2, residual.
+int block_pass_wide(const Plan& p, const cfh::ExpertLayout& L, const WS& w, const void* const* experts, int l,
+                    int Rg, hipStream_t st) {
+  const int d = p.d, fd = p.fd, NL = p.NL, nch = p.nch, Cg = Rg * p.C;
+  auto PTR = [&](int c, size_t off) { return (const char*)experts[c] + off; };
+  const size_t B = L.blk0 + (size_t)l * L.blkstride;
+  auto S_of = [&](int c) { return Rg * (c + 1) * p.CS; };
+  auto Sr_of = [&](int c) { return (c + 1) * p.CS; };
+  int rc;
+  auto wargs = [&](int N, int K, int ks) {
+    WArgs a = {};
+    a.nex = nch; a.N = N; a.K = K; a.ks = ks;
+    return a;
+  };
+  // QKV: q, k, v = fp16(LN_self(x) W_in^T + b_in)
+  {
+    WArgs a = wargs(3 * d, d, 1);
+    for (int c = 0; c < nch; ++c) {
+      WEx& x = a.ex[c];
+      x.w = (const h16x8*)PTR(c, B + L.qkv); x.a = w.abuf[c]; x.lda = d; x.bias = (const h16*)PTR(c, B + L.qkv_b);
+      x.out = w.qkv[c]; x.S = S_of(c);
+    }
+    if ((rc = launch_wide<E_BIAS16>(a, p.wv_qkv, st))) return rc;
+  }
+  // causal self attention of every (request, head), into the LN rows' buffer (free until the residual)
+  {
+    SelfArgs sa = {};
+    sa.nex = nch; sa.R = Rg; sa.H = p.H; sa.d = d; sa.hd = p.hd;
+    for (int c = 0; c < nch; ++c) { sa.qkv[c] = w.qkv[c]; sa.out[c] = w.abuf[c]; sa.S[c] = S_of(c); sa.Sr[c] = Sr_of(c); }
+    if ((rc = launch_self_attn(sa, st))) return rc;
+  }
+  // O: out_proj, split-K partials
+  {
+    WArgs a = wargs(d, d, p.ks_wo);
+    for (int c = 0; c < nch; ++c) {
+      WEx& x = a.ex[c];
+      x.w = (const h16x8*)PTR(c, B + L.o); x.a = w.abuf[c]; x.lda = d; x.out = w.P[c]; x.S = S_of(c);
+    }
+    if ((rc = launch_wide<E_PART>(a, 4, st))) return rc;
+  }
+  ResArgs r = {};
+  r.nex = nch; r.d = d; r.mode = p.res_mode;
+  for (int c = 0; c < nch; ++c) { r.x[c] = w.x[c]; r.P[c] = w.P[c]; r.a[c] = w.abuf[c]; r.rows[c] = S_of(c); }
+  // residual + LN_cross (as the folded cross attention's operand image)
+  r.ks = p.ks_wo;
+  for (int c = 0; c < nch; ++c) {
+    r.bias[c] = (const h16*)PTR(c, B + L.o_b);
+    r.g[c] = (const h16*)PTR(c, B + L.xn_w); r.b[c] = (const h16*)PTR(c, B + L.xn_b);
+  }
+  r.pack = 1;
+  if ((rc = launch_res(r, st))) return rc;
+  r.pack = 0;
+  // folded cross attention, two requests a subgroup
+  {
+    XattArgs x = {};
+    x.nex = nch; x.d = d; x.H = p.H; x.C = Cg; x.Cq = p.C; x.nb = p.xnb; x.scale = 1.0f / sqrtf((float)p.hd);
+    x.nsg = (Rg + 1) / 2; x.Csg = 2 * p.C;
+    const size_t per_l = (size_t)p.H * Cg * d;
+    for (int c = 0; c < nch; ++c) {
+      x.xn[c] = w.abuf[c]; x.A[c] = w.fa[c] + (size_t)l * per_l; x.Bf[c] = w.fb[c] + (size_t)l * per_l;
+      x.sb[c] = w.fsb[c] + (size_t)l * p.H * Cg;
+      x.out[c] = w.P[c]; x.S[c] = S_of(c); x.Sr[c] = Sr_of(c); x.Ssg[c] = 2 * Sr_of(c);
+    }
+    if ((rc = launch_xattn(x, st))) return rc;
+  }
+  // residual + LN_ffn (one partial per head)
+  r.ks = p.H;
+  for (int c = 0; c < nch; ++c) {
+    r.bias[c] = (const h16*)PTR(c, B + L.oc_b);
+    r.g[c] = (const h16*)PTR(c, B + L.fn_w); r.b[c] = (const h16*)PTR(c, B + L.fn_b);
+  }
+  if ((rc = launch_res(r, st))) return rc;
+  // W1: g = fp16(gelu(LN_ffn(x) W1^T + b1))
+  {
+    WArgs a = wargs(fd, d, 1);
+    a.gelu_r16 = p.res_mode == RES_ADD16;
+    for (int c = 0; c < nch; ++c) {
+      WEx& x = a.ex[c];
+      x.w = (const h16x8*)PTR(c, B + L.w1); x.a = w.abuf[c]; x.lda = d; x.bias = (const h16*)PTR(c, B + L.w1_b);
+      x.out = w.g[c]; x.S = S_of(c);
+    }
+    if ((rc = launch_wide<E_GELU16>(a, p.wv_w1, st))) return rc;
+  }
+  // W2: split-K partials
+  {
+    WArgs a = wargs(d, fd, p.ks_ww2);
+    for (int c = 0; c < nch; ++c) {
+      WEx& x = a.ex[c];
+      x.w = (const h16x8*)PTR(c, B + L.w2); x.a = w.g[c]; x.lda = fd; x.out = w.P[c]; x.S = S_of(c);
+    }
+    if ((rc = launch_wide<E_PART>(a, 4, st))) return rc;
+  }
+  // residual + LayerNorm of the next block (out_norm after the last block)
+  r.ks = p.ks_ww2;
+  for (int c = 0; c < nch; ++c) {
+    r.bias[c] = (const h16*)PTR(c, B + L.w2_b);
+    if (l + 1 < NL) {
+      const size_t Bn = L.blk0 + (size_t)(l + 1) * L.blkstride;
+      r.g[c] = (const h16*)PTR(c, Bn + L.sn_w); r.b[c] = (const h16*)PTR(c, Bn + L.sn_b);
+    } else {
+      r.g[c] = (const h16*)PTR(c, L.on_w); r.b[c] = (const h16*)PTR(c, L.on_b);
+    }
+  }
+  return launch_res(r, st);
+}
+
+// Per-draft launches of a wide group: the context rows' LayerNorm of every block, the cross K/V
+// of every block (context rows of every request as rows of one stream), and the folded factors.
+int per_draft_wide(const Plan& p, const cfh::ExpertLayout& L, const WS& w, const void* const* experts,
+                   const h16* ctx_b, int Rg, hipStream_t st) {
+  const int d = p.d, NL = p.NL, nch = p.nch, Cg = Rg * p.C;
+  auto PTR = [&](int c, size_t off) { return (const char*)experts[c] + off; };
+  auto BLK = [&](int l) { return L.blk0 + (size_t)l * L.blkstride; };
+  int rc;
+  {
+    CtxLnArgs a = {};
+    a.ctx = ctx_b; a.mom = w.ctx_mom; a.vstride = (long long)L.blkstride; a.nex = nch; a.nl = NL; a.Ct = Cg; a.d = d;
+    for (int c = 0; c < nch; ++c) {
+      a.g0[c] = (const h16*)PTR(c, BLK(0) + L.cn_w); a.b0[c] = (const h16*)PTR(c, BLK(0) + L.cn_b);
+      a.out[c] = w.cln[c];
+    }
+    hipLaunchKernelGGL(k_ctx_ln, dim3(512), dim3(256), 0, st, a);
+    CFH_LAUNCH_CHECK();
+  }
+  // cross K/V = fp16(LN_c(ctx) W_kv^T + b_kv) as [2][Cg][d] per block, four weight sets a launch
+  for (int i0 = 0; i0 < nch * NL; i0 += 4) {
+    WArgs a = {};
+    a.N = 2 * d; a.K = d; a.ks = 1;
+    for (int i = i0; i < std::min(nch * NL, i0 + 4); ++i) {
+      const int c = i / NL, l = i - c * NL;
+      WEx& x = a.ex[a.nex++];
+      x.w = (const h16x8*)PTR(c, BLK(l) + L.kv); x.a = w.cln[c] + (size_t)l * Cg * d; x.lda = d;
+      x.bias = (const h16*)PTR(c, BLK(l) + L.kv_b); x.out = w.kvc[c] + (size_t)l * 2 * Cg * d; x.S = Cg;
+      x.nsplit = d;
+    }
+    if ((rc = launch_wide<E_BIAS16>(a, p.wv_kv, st))) return rc;
+  }
+  XbiasArgs xb = {};
+  xb.nex = nch; xb.nl = NL; xb.d = d; xb.H = p.H; xb.C = Cg;
+  xb.kstride = (long long)2 * Cg * d; xb.bstride = (long long)L.blkstride;
+  for (int c = 0; c < nch; ++c) {
+    xb.K[c] = w.kvc[c]; xb.bq[c] = (const h16*)PTR(c, BLK(0) + L.qc_b); xb.sb[c] = w.fsb[c];
+  }
+  hipLaunchKernelGGL(k_xbias, dim3(nch * NL), dim3(1024), 0, st, xb);
+  CFH_LAUNCH_CHECK();
+  // A_h = Wq_h^T K_h^T (the transposed query weight against the K rows) and B_h = Wo_h V_h, split-K
+  // by head: the partial of k-split h, rounded to fp16, is head h's factor
+  const size_t per_l = (size_t)p.H * Cg * d;
+  for (int l = 0; l < NL; ++l)
+    for (int half = 0; half < 2; ++half) {
+      if (half == 1 && 2 * nch <= 4) break;
+      WArgs a = {};
+      a.N = d; a.K = d; a.ks = p.H;
+      for (int part = 0; part < 2; ++part) {
+        if (2 * nch > 4 && part != half) continue;
+        for (int c = 0; c < nch; ++c) {
+          WEx& x = a.ex[a.nex++];
+          const h16* kv = w.kvc[c] + (size_t)l * 2 * Cg * d;
+          x.w = (const h16x8*)PTR(c, BLK(l) + (part == 0 ? L.qc : L.oc));
+          x.a = part == 0 ? kv : kv + (size_t)Cg * d;
+          x.lda = d; x.S = Cg; x.hrows = Cg;
+          x.out = (part == 0 ? w.fa[c] : w.fb[c]) + (size_t)l * per_l;
+          x.pack = part == 0;
+        }
+      }
+      if ((rc = launch_wide<E_PART16>(a, 4, st))) return rc;
+    }
+  return CFH_OK;
 }
 
 // Companion streams of a caller stream: chunk expert c > 0 runs its block passes, its OUT launch
@@ -937,8 +1187,11 @@ int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* expert
       hipLaunchKernelGGL(k_rows, dim3(Rg * KD), dim3(ROWT), 0, st, r);
       CFH_LAUNCH_CHECK();
     }
+    if (p.wide) {
+      if ((rc = per_draft_wide(p, L, w, experts, ctx_b, Rg, st))) return rc;
+    }
     // ---- cross K/V of every block (once per draft), the group's context rows together
-    {
+    if (!p.wide) {
       GemvArgs a = {};
       a.nex = nch; a.nl = NL; a.ks = p.ks_kv; a.tiles = 2 * d / 16; a.N = 2 * d; a.K = d; a.E = E;
       a.wstride = (long long)L.blkstride; a.vstride = (long long)L.blkstride;
@@ -968,7 +1221,7 @@ int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* expert
     // transposed query weight against the K rows, B_h = Wo_h V_h from the out-projection against
     // the V rows, each split-K by head (the partial of head h, rounded to fp16, is the factor);
     // the rows of the group's requests side by side
-    if (p.fold) {
+    if (p.fold && !p.wide) {
       XbiasArgs xb = {};
       xb.nex = nch; xb.nl = NL; xb.d = d; xb.H = p.H; xb.C = Cg;
       xb.kstride = (long long)2 * Cg * d; xb.bstride = (long long)L.blkstride;
@@ -1021,7 +1274,7 @@ int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* expert
     }
     auto rows_args = [&](int s, int only) {
       RowsArgs r = {};
-      r.ctx = ctx_b; r.z = w.z; r.z_out = zo_b; r.euler = 1; r.last = (s + 1 == E); r.ks = p.ks_out;
+      r.ctx = ctx_b; r.z = w.z; r.z_out = zo_b; r.euler = 1; r.last = (s + 1 == E); r.ks = p.wide ? p.ks_wout : p.ks_out;
       r.dt = 1.0f / (float)E; r.d = d; r.C = C; r.CS = CS; r.nch = nch; r.KD = KD; r.R = Rg; r.out_all = p.R > 1;
       r.only = only;
       for (int c = 0; c < nch; ++c) {
@@ -1054,7 +1307,26 @@ int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* expert
       }
       return launch_stream<S_BUF, E_PART>(a, p.R == 1 ? CS : p.Smax, sc);
     };
+    // OUT of a wide group: every row of every expert (the current chunk's rows are not contiguous)
+    auto out_wide = [&]() {
+      WArgs a = {};
+      a.nex = nch; a.N = d; a.K = d; a.ks = p.ks_wout;
+      for (int c = 0; c < nch; ++c) {
+        WEx& x = a.ex[c];
+        x.w = (const h16x8*)PTR(c, L.out); x.a = w.abuf[c]; x.lda = d; x.out = w.P[c]; x.S = Rg * (c + 1) * CS;
+      }
+      return launch_wide<E_PART>(a, 4, st);
+    };
     for (int s = 0; s < E; ++s) {
+      if (p.wide) {
+        for (int l = 0; l < NL; ++l)
+          if ((rc = block_pass_wide(p, L, w, experts, l, Rg, st))) return rc;
+        if ((rc = out_wide())) return rc;
+        const RowsArgs r = rows_args(s, -1);
+        hipLaunchKernelGGL(k_rows, dim3(Rg * KD), dim3(ROWT), 0, st, r);
+        CFH_LAUNCH_CHECK();
+        continue;
+      }
       if (!p.conc) {
         for (int l = 0; l < NL; ++l)
           if ((rc = block_pass(p, L, w, experts, l, Rg, st, 0, nch))) return rc;
@@ -1133,8 +1405,27 @@ int cfh_caps(const cfh_flow_dims* dims, int batch, int64_t* ws_bytes) {
   if (dims->d > ROWT * ROWE || dims->draft_length > MAXR) return CFH_E_UNSUPPORTED;
   const Plan p = make_plan(dims, group_size(dims, batch));
   if (!p.ok) return CFH_E_UNSUPPORTED;
-  const WS w = carve(p, nullptr);
-  if (ws_bytes) *ws_bytes = (int64_t)w.total;
+  // the workspace of every batch up to `batch`: the group sizes 1, 2 (narrow) and the widest group
+  // (wide group sizes grow with the batch up to WMAXR / draft_length requests)
+  size_t total = carve(p, nullptr).total;
+  const int wide_max = std::min(batch, WMAXR / dims->draft_length);
+  for (int b : {1, 2, wide_max}) {
+    if (b > batch) continue;
+    const Plan q = make_plan(dims, group_size(dims, b));
+    if (q.ok) total = std::max(total, carve(q, nullptr).total);
+  }
+  if (ws_bytes) *ws_bytes = (int64_t)total;
+  return CFH_OK;
+}
+
+int cfh_flow_group_size(const cfh_flow_dims* dims, int batch, int* requests) {
+  if (!requests) return CFH_E_INVALID;
+  *requests = 0;
+  if (!cfh::flow_dims_ok(dims) || batch < 1) return CFH_E_UNSUPPORTED;
+  if (dims->d > ROWT * ROWE || dims->draft_length > MAXR) return CFH_E_UNSUPPORTED;
+  const int R = group_size(dims, batch);
+  if (!make_plan(dims, R).ok) return CFH_E_UNSUPPORTED;
+  *requests = R;
   return CFH_OK;
 }
 
@@ -1181,7 +1472,8 @@ int cfh_flow_integrate_noalloc(const cfh_flow_dims* dm, const void* const* exper
                                int batch, void* stream) {
   if (!cfh::flow_dims_ok(dm) || dm->d > ROWT * ROWE || dm->draft_length > MAXR) return CFH_E_UNSUPPORTED;
   if (!experts || !ctx || !z_out || batch < 1) return CFH_E_INVALID;
-  const Plan p = make_plan(dm, group_size(dm, batch));
+  // narrow groups (at most two requests a weight stream): their workspace fits the scratch array
+  const Plan p = make_plan(dm, group_size(dm, batch, false));
   if (!p.ok) return CFH_E_UNSUPPORTED;
   for (int c = 0; c < p.nch; ++c)
     if (!experts[c]) return CFH_E_INVALID;

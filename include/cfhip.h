@@ -116,8 +116,9 @@ int cfh_flow_pack_expert(const cfh_flow_dims* dims, const void* const* raw, int 
  *   ctx     : [batch][ctx_rows][d] fp16 context hidden states (already front-padded)
  *   z_out   : [batch][draft_length][d] fp16 predicted hiddens
  *   ws      : workspace of cfh_caps(dims, batch) bytes
- * A batch runs in groups of up to two requests whose rows share every weight stream (when both
- * drafts fit one 16-row MFMA tile and the shape's operand staging allows it).
+ * A batch runs in groups of requests whose rows share every weight stream: up to sixteen (wide
+ * groups, rows staged in K chunks; head width a multiple of 128 and the folded cross attention),
+ * else up to two (both drafts in one 16-row MFMA tile); cfh_flow_group_size tells.
  * Chunk experts (d >= 1024, two or more chunks) run their Euler steps on companion streams of the
  * caller's stream, forked after the per-draft launches and joined before return.  The first eager
  * call on a caller stream without companions creates them (streams, events: kept until
@@ -129,6 +130,11 @@ int cfh_flow_pack_expert(const cfh_flow_dims* dims, const void* const* raw, int 
  * reference's two-stream chunk pair (cf/cuda_block.py:452-466). */
 int cfh_flow_integrate(const cfh_flow_dims* dims, const void* const* experts, const void* ctx,
                        void* z_out, void* ws, int batch, void* stream);
+
+/* Requests per group (*requests) that cfh_flow_integrate drafts together for a batch of `batch`:
+ * every weight byte streams once per group.  No counterpart in the reference, whose batched flow
+ * runs torch modules over the whole batch (cf/drafters/chunked_flow.py:295-331). */
+int cfh_flow_group_size(const cfh_flow_dims* dims, int batch, int* requests);
 
 /* Set-up of the companion streams of a caller stream, so that no later cfh_flow_integrate on it
  * synchronises: creates the companions `dims`'s chunk experts need (none for flows that stay on one

@@ -208,9 +208,30 @@ int launch_wide_k(const WArgs& a, size_t lds, hipStream_t st) {
 int wide_check(const WArgs& a, int wv, int S_max) {
   if (a.nex < 1 || a.nex > 4 || a.N <= 0 || a.N % 16 || a.ks <= 0 || a.K % a.ks || (a.K / a.ks) % WCH)
     return CFH_E_UNSUPPORTED;
-  if ((wv != 4 && wv != 8) || (a.N / 16) % wv || S_max < 1 || S_max > WMAXR || wide_lds(S_max) > 150 * 1024)
+  if ((wv != 4 && wv != 6 && wv != 8 && wv != 12 && wv != 16) || (a.N / 16) % wv || S_max < 1 || S_max > WMAXR ||
+      wide_lds(S_max) > 150 * 1024)
     return CFH_E_UNSUPPORTED;
   return CFH_OK;
+}
+
+// Waves per workgroup of a full-K wide launch over `units` units of `tiles` column tiles: the
+// count (dividing tiles) that loads the busiest CU least -- rounds of 256 workgroups times waves
+// a workgroup -- preferring fewer waves a workgroup on ties (measured on the 4096-wide flow: 384
+// workgroups of 8 waves left half the CUs with two workgroups, 256 of 12 none).
+int wide_wv(int tiles, int units) {
+  constexpr int CUS = 256;
+  int best = 0;
+  long long best_load = 0;
+  for (int wv : {4, 6, 8, 12, 16}) {
+    if (tiles % wv) continue;
+    const long long wgs = (long long)units * tiles / wv;
+    const long long load = (wgs + CUS - 1) / CUS * wv;
+    if (!best || load < best_load) {
+      best = wv;
+      best_load = load;
+    }
+  }
+  return best;
 }
 
 template <int EPI>
@@ -224,10 +245,26 @@ int launch_wide(const WArgs& a0, int wv, hipStream_t st) {
   a.wg_per_kc = (a.N / 16) / wv;
   const size_t lds = wide_lds(S_max);
   const int ng = (S_max + 15) / 16;
-#define CFH_WIDE(G)                                                              \
-  if (ng <= G) return wv == 8 ? launch_wide_k<EPI, G, 8>(a, lds, st) : launch_wide_k<EPI, G, 4>(a, lds, st);
-  CFH_WIDE(2) CFH_WIDE(4) CFH_WIDE(8)
+  // the split-K launches run 4-wave workgroups; the full-K ones (bias epilogues) any of the counts
+  if constexpr (EPI == E_PART || EPI == E_PART16) {
+    if (wv != 4) return CFH_E_UNSUPPORTED;
+    if (ng <= 2) return launch_wide_k<EPI, 2, 4>(a, lds, st);
+    if (ng <= 4) return launch_wide_k<EPI, 4, 4>(a, lds, st);
+    return launch_wide_k<EPI, 8, 4>(a, lds, st);
+  } else {
+#define CFH_WIDE(G)                                                                 \
+  if (ng <= G) {                                                                    \
+    switch (wv) {                                                                   \
+      case 4: return launch_wide_k<EPI, G, 4>(a, lds, st);                          \
+      case 6: return launch_wide_k<EPI, G, 6>(a, lds, st);                          \
+      case 8: return launch_wide_k<EPI, G, 8>(a, lds, st);                          \
+      case 12: return launch_wide_k<EPI, G, 12>(a, lds, st);                        \
+      default: return launch_wide_k<EPI, G, 16>(a, lds, st);                        \
+    }                                                                               \
+  }
+    CFH_WIDE(2) CFH_WIDE(4) CFH_WIDE(8)
 #undef CFH_WIDE
+  }
   return CFH_E_UNSUPPORTED;
 }
 

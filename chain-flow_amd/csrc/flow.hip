@@ -281,12 +281,13 @@ __global__ void __launch_bounds__(XT) k_xattn(XattArgs a) {
   const int S = min(Ssg, St - r0), C = min(Csg, Ct - c0);
   if (S <= 0 || C <= 0) return;                      // (a subgroup past the group's requests)
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  // this thread's column of B_h (every context row of the subgroup), in flight before the scores
+  // this thread's first column of B_h (every context row of the subgroup), in flight before the
+  // scores; a block of more than XT columns gives the thread further columns XT apart
   const int cpb = d / a.nb, n = cb * cpb + min(t, cpb - 1);
-  const h16* Bh = a.Bf[e] + ((size_t)h * Ct + c0) * d + n;
+  const h16* Bbase = a.Bf[e] + ((size_t)h * Ct + c0) * d;
   h16 bv[CM];
 #pragma unroll
-  for (int c = 0; c < CM; ++c) bv[c] = Bh[(size_t)min(c, C - 1) * d];
+  for (int c = 0; c < CM; ++c) bv[c] = Bbase[(size_t)min(c, C - 1) * d + n];
   // scores: lane row = lane % 16, context row = lane % 16 of the B operand, k-group lane / 16.
   // Lanes of rows past S or context rows past C load nothing (zero operands).  The operand
   // images hold every row of the expert (St) and every context row (Ct).
@@ -334,12 +335,18 @@ __global__ void __launch_bounds__(XT) k_xattn(XattArgs a) {
     if (r < S) P[r][c] = z * (1.0f / sum);     // 0 for masked and padding context rows
   }
   __syncthreads();
-  // this thread's column of P_h B_h
-  if (t < cpb) {
-    float* oh = a.out[e] + ((size_t)h * St + r0) * d + n;
+  // this thread's columns of P_h B_h
+  for (int cc = t; cc < cpb; cc += XT) {
+    const int nn = cb * cpb + cc;
+    float* oh = a.out[e] + ((size_t)h * St + r0) * d + nn;
     float bf[CM];
+    if (cc == t) {
 #pragma unroll
-    for (int c = 0; c < CM; ++c) bf[c] = (float)bv[c];
+      for (int c = 0; c < CM; ++c) bf[c] = (float)bv[c];
+    } else {
+#pragma unroll
+      for (int c = 0; c < CM; ++c) bf[c] = (float)Bbase[(size_t)min(c, C - 1) * d + nn];
+    }
     for (int r = 0; r < S; ++r) {
       float o = 0.f;
 #pragma unroll
@@ -407,10 +414,12 @@ __global__ void __launch_bounds__(256) k_fold_mask(FoldMaskArgs a) {
 // Column blocks per (expert, head) of XATT: the fewest that give each thread at most one column
 // (each block recomputes the head's scores, so more blocks only repeat that work); 0 if d has no
 // such split.
-int xattn_blocks(int d, int units) {
+// cols: the most columns a thread may take (each block recomputes its head's scores: the wide
+// groups' many subgroups already fill the chip, so there a thread takes several columns).
+int xattn_blocks(int d, int units, int cols = 1) {
   (void)units;
   for (int nb = 1; nb <= d; ++nb)
-    if (d % nb == 0 && d / nb <= XT) return nb;
+    if (d % nb == 0 && d / nb <= XT * cols && (d / nb <= XT || (d / nb) % XT == 0)) return nb;
   return 0;
 }
 
@@ -461,7 +470,7 @@ void make_wide_plan(Plan& p, const cfh_flow_dims* dm) {
          p.C <= 8 && 2 * p.KD <= MAXR && res_nq(p.d) > 0;
   if (!p.ok) return;
   constexpr int CUS = 256;
-  auto wv_full = [&](int N) { return ((N / 16) % 8 == 0 && p.nch * (N / 16) / 8 >= CUS) ? 8 : 4; };
+  auto wv_full = [&](int N) { return wide_wv(N / 16, p.nch); };
   auto ks_split = [&](int N, int K) {
     int best = 0;
     for (int ks = 1; ks <= K / WCH; ++ks) {
@@ -473,12 +482,12 @@ void make_wide_plan(Plan& p, const cfh_flow_dims* dm) {
   };
   p.wv_qkv = wv_full(3 * p.d);
   p.wv_w1 = wv_full(p.fd);
-  p.wv_kv = wv_full(2 * p.d);
+  p.wv_kv = wide_wv(2 * p.d / 16, std::min(4, p.nch * p.NL));
   p.ks_wo = ks_split(p.d, p.d);
   p.ks_ww2 = ks_split(p.d, p.fd);
   p.ks_wout = ks_split(p.d, p.d);
   p.pks = std::max(std::max(p.H, p.ks_wo), std::max(p.ks_ww2, p.ks_wout));
-  p.xnb = xattn_blocks(p.d, p.nch * p.H);
+  p.xnb = xattn_blocks(p.d, p.nch * p.H, 4);
   auto wa = [&](int N, int K, int ks) {
     WArgs a = {};
     a.nex = p.nch; a.N = N; a.K = K; a.ks = ks;

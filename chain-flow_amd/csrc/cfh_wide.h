@@ -9,11 +9,12 @@
 //
 //   chunk c:  issue the loads of chunk c+1's rows into registers (they return after the weight
 //             fragments already in flight, which the multiplies need first anyway)
-//             multiply WCH/32 fragments, each against every 16-row group of the rows in LDS
+//             multiply the chunk's WCH/32 k-steps of fragments, each against every 16-row group
+//             of the rows in LDS
 //             place chunk c+1's rows in the other buffer, one LDS barrier
 //
-// A wave owns one 16-column tile of one (expert, k-split) unit and keeps one accumulator per
-// 16-row group.  Self attention, which the narrow kernel computes while staging, runs as its own
+// A wave owns WT adjacent 16-column tiles of one (expert, k-split) unit and keeps one accumulator
+// per (tile, 16-row group).  Self attention, which the narrow kernel computes while staging, runs as its own
 // small kernel per (request, head), and the context rows' LayerNorm of every block is computed
 // once per draft into rows the cross K/V stream reads.
 #pragma once
@@ -25,7 +26,8 @@ namespace {
 
 constexpr int WCH = 128;          // K columns staged per chunk (4 k-steps)
 constexpr int WKS = WCH / 32;     // k-steps per chunk
-constexpr int WSPF = 8;           // fragment loads in flight per wave (two chunks)
+constexpr int WT = 2;             // 16-column tiles per wave: each operand read from LDS feeds WT multiplies
+constexpr int WSPF = WKS * WT;    // fragment loads in flight per wave (one chunk)
 constexpr int WMAXR = 128;        // max activation rows of one expert in a wide group
 constexpr int WLDA = WCH + 8;     // LDS row stride (halves): rows of a chunk start on different banks
 
@@ -60,7 +62,7 @@ __global__ void __launch_bounds__(WV * 64) k_wide(WArgs a) {
   const int S = ex.S;
   const int ksteps = a.K / 32;
   const int KCW = a.K / a.ks, nsteps = KCW / 32, nchunk = KCW / WCH;
-  const int t = tg * WV + wave;                       // this wave's 16-column tile
+  const int t0 = (tg * WV + wave) * WT;               // this wave's WT adjacent 16-column tiles
   const int k0 = kc * KCW;
   // staging of one chunk: vector idx = u * nt + thread, row idx / 16, columns (idx % 16) * 8 .. +7;
   // indices past the rows re-read the last vector (every load unconditional, see Stage)
@@ -86,30 +88,35 @@ __global__ void __launch_bounds__(WV * 64) k_wide(WArgs a) {
       *(h16x8*)(buf + i * WLDA + kk) = st[u];
     }
   };
-  // the wave's fragments, walked one at a time; past the last one the pointer stays there, so the
-  // ring's surplus refills re-read a line just fetched
-  const h16x8* lw = ex.w + ((size_t)t * ksteps + (size_t)kc * nsteps) * 64 + lane;
-  int lleft = nsteps;
-  auto issue = [&]() -> h16x8 {
-    const h16x8 v = __builtin_nontemporal_load(lw);
-    const bool adv = lleft > 1;
-    lw += adv ? 64 : 0;
-    lleft -= adv;
+  // the wave's fragments, k-step by k-step, the WT tiles of a k-step together; past the last
+  // k-step the pointers stay there, so the ring's surplus refills re-read lines just fetched
+  const h16x8* lw = ex.w + ((size_t)t0 * ksteps + (size_t)kc * nsteps) * 64 + lane;
+  const size_t tstride = (size_t)ksteps * 64;         // next tile, same k-step
+  int lleft = nsteps * WT;
+  auto issue = [&](int u) -> h16x8 {
+    const h16x8 v = __builtin_nontemporal_load(lw + u * tstride);
+    if (u == WT - 1) {
+      const bool adv = lleft > WT;
+      lw += adv ? 64 : 0;
+      lleft -= adv ? WT : 0;
+    }
     return v;
   };
   const int col = lane & 15, rbase = 4 * (lane >> 4);
-  const int n = t * 16 + col;
-  float bias = 0.f;
-  if constexpr (EPI == E_BIAS16 || EPI == E_GELU16) bias = (float)ex.bias[n];
+  float bias[WT] = {};
+  if constexpr (EPI == E_BIAS16 || EPI == E_GELU16) {
+#pragma unroll
+    for (int u = 0; u < WT; ++u) bias[u] = (float)ex.bias[(t0 + u) * 16 + col];
+  }
   // operand chunk 0 first, then the weight prefetch (independent of it), then LDS
   load_chunk(0);
   __builtin_amdgcn_sched_barrier(0);
   h16x8 ring[WSPF];
 #pragma unroll
   for (int p = 0; p < WSPF; ++p) {
-    ring[p] = issue();
-    // issued in slot order: the loop's first multiply then waits for slot 0 alone (with the order
-    // left free, slot 0 went out seventh and that multiply waited for the whole ring)
+    ring[p] = issue(p % WT);
+    // issued in slot order: each multiply then waits for its own slot alone (with the order left
+    // free, slot 0 went out seventh and the first multiply waited for the whole ring)
     __builtin_amdgcn_sched_barrier(0);
   }
   h16* buf0 = lds;
@@ -117,69 +124,70 @@ __global__ void __launch_bounds__(WV * 64) k_wide(WArgs a) {
   place_chunk(buf0);
   lds_barrier();
   const int row = lane & 15, kg = lane >> 4;
-  const h16x8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
-  f32x4 acc[NG];
+  f32x4 acc[WT][NG];
 #pragma unroll
-  for (int g = 0; g < NG; ++g) acc[g] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int u = 0; u < WT; ++u)
+#pragma unroll
+    for (int g = 0; g < NG; ++g) acc[u][g] = (f32x4){0.f, 0.f, 0.f, 0.f};
   // lanes of rows past S read row 0: their products land in output rows that are never stored
+  // (every row group is multiplied, which keeps the loop free of branches)
   int roff[NG];
 #pragma unroll
   for (int g = 0; g < NG; ++g) roff[g] = (g * 16 + row < S ? g * 16 + row : 0) * WLDA + kg * 8;
-  // two chunks per ring cycle (WSPF = 2 WKS): slot p holds k-step p % WKS of chunk c0 + p / WKS
-  for (int c0 = 0; c0 < nchunk; c0 += 2) {
+  // one chunk per ring cycle (WSPF = WKS WT): slot p holds tile p % WT of the chunk's k-step p / WT
+  for (int c = 0; c < nchunk; ++c) {
+    const h16* cur = (c & 1) ? buf1 : buf0;
+    h16* nxt = (c & 1) ? buf0 : buf1;
+    load_chunk(min(c + 1, nchunk - 1));
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int c = c0 + h;
-      // past the last chunk (an odd count) the zero fragments multiply the last chunk's rows, which
-      // are finite: the other buffer was never written, and 0 x NaN would poison the sums
-      const h16* cur = (min(c, nchunk - 1) & 1) ? buf1 : buf0;
-      h16* nxt = (c & 1) ? buf0 : buf1;
-      load_chunk(min(c + 1, nchunk - 1));
+    for (int q = 0; q < WKS; ++q) {
+      // one k-step at a time: each row group's operand read once, multiplied by the WT fragments
 #pragma unroll
-      for (int q = 0; q < WKS; ++q) {
-        const int p = h * WKS + q;
-        // (an odd chunk count leaves the last ring cycle's second half empty: its fragments are
-        // replaced by zeros rather than skipped, which keeps the loop free of branches; every row
-        // group is multiplied, rows past S reading row 0, for the same reason)
-        const h16x8 bf = c < nchunk ? ring[p] : zero8;
+      for (int g = 0; g < NG; ++g) {
+        const h16x8 av = *(const h16x8*)(cur + roff[g] + q * 32);
 #pragma unroll
-        for (int g = 0; g < NG; ++g) acc[g] = mfma_f16(*(const h16x8*)(cur + roff[g] + q * 32), bf, acc[g]);
-        ring[p] = issue();
-        // one fragment's LDS reads and multiplies at a time: left free, the scheduler hoists every
-        // read of both chunks ahead of the multiplies and runs out of registers
-        __builtin_amdgcn_sched_barrier(0);
+        for (int u = 0; u < WT; ++u) acc[u][g] = mfma_f16(av, ring[q * WT + u], acc[u][g]);
       }
-      // chunk c + 1 goes to the other buffer (nobody reads it: every wave finished chunk c - 1
-      // before the last barrier); one barrier orders the stores before chunk c + 1's reads
-      if (c + 1 < nchunk) place_chunk(nxt);
-      lds_barrier();
+#pragma unroll
+      for (int u = 0; u < WT; ++u) ring[q * WT + u] = issue(u);
+      // left free, the scheduler hoists every read of the chunk ahead of the multiplies and runs
+      // out of registers
+      __builtin_amdgcn_sched_barrier(0);
     }
+    // chunk c + 1 goes to the other buffer (nobody reads it: every wave finished chunk c - 1
+    // before the last barrier); one barrier orders the stores before chunk c + 1's reads
+    if (c + 1 < nchunk) place_chunk(nxt);
+    lds_barrier();
   }
-  // epilogue: rows g * 16 + rbase + q of column n
+  // epilogue: rows g * 16 + rbase + q of column (t0 + u) * 16 + col
 #pragma unroll
-  for (int g = 0; g < NG; ++g) {
-    if (g * 16 >= S) continue;
+  for (int u = 0; u < WT; ++u) {
+    const int n = (t0 + u) * 16 + col;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int r = g * 16 + rbase + q;
-      if (r >= S) continue;
-      const float v = acc[g][q];
-      if constexpr (EPI == E_PART) {
-        ((float*)ex.out)[((size_t)kc * S + r) * a.N + n] = v;
-      } else if constexpr (EPI == E_PART16) {
-        const int hr = ex.hrows > 0 ? ex.hrows : S, hb = r / hr, rr = r - hb * hr;
-        h16* o = (h16*)ex.out + ((size_t)kc * (S / hr) + hb) * hr * a.N;
-        o[ex.pack ? frag_index(rr, n, hr) : (size_t)rr * a.N + n] = (h16)v;
-      } else if constexpr (EPI == E_BIAS16) {
-        if (ex.nsplit > 0) {
-          const int part = n / ex.nsplit, nn = n - part * ex.nsplit;
-          ((h16*)ex.out)[((size_t)part * S + r) * ex.nsplit + nn] = (h16)(v + bias);
+    for (int g = 0; g < NG; ++g) {
+      if (g * 16 >= S) continue;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = g * 16 + rbase + q;
+        if (r >= S) continue;
+        const float v = acc[u][g][q];
+        if constexpr (EPI == E_PART) {
+          ((float*)ex.out)[((size_t)kc * S + r) * a.N + n] = v;
+        } else if constexpr (EPI == E_PART16) {
+          const int hr = ex.hrows > 0 ? ex.hrows : S, hb = r / hr, rr = r - hb * hr;
+          h16* o = (h16*)ex.out + ((size_t)kc * (S / hr) + hb) * hr * a.N;
+          o[ex.pack ? frag_index(rr, n, hr) : (size_t)rr * a.N + n] = (h16)v;
+        } else if constexpr (EPI == E_BIAS16) {
+          if (ex.nsplit > 0) {
+            const int part = n / ex.nsplit, nn = n - part * ex.nsplit;
+            ((h16*)ex.out)[((size_t)part * S + r) * ex.nsplit + nn] = (h16)(v + bias[u]);
+          } else {
+            ((h16*)ex.out)[(size_t)r * a.N + n] = (h16)(v + bias[u]);
+          }
         } else {
-          ((h16*)ex.out)[(size_t)r * a.N + n] = (h16)(v + bias);
+          const float w = v + bias[u];
+          ((h16*)ex.out)[(size_t)r * a.N + n] = (h16)gelu_erf(a.gelu_r16 ? r16(w) : w);
         }
-      } else {
-        const float u = v + bias;
-        ((h16*)ex.out)[(size_t)r * a.N + n] = (h16)gelu_erf(a.gelu_r16 ? r16(u) : u);
       }
     }
   }
@@ -208,23 +216,22 @@ int launch_wide_k(const WArgs& a, size_t lds, hipStream_t st) {
 int wide_check(const WArgs& a, int wv, int S_max) {
   if (a.nex < 1 || a.nex > 4 || a.N <= 0 || a.N % 16 || a.ks <= 0 || a.K % a.ks || (a.K / a.ks) % WCH)
     return CFH_E_UNSUPPORTED;
-  if ((wv != 4 && wv != 6 && wv != 8 && wv != 12 && wv != 16) || (a.N / 16) % wv || S_max < 1 || S_max > WMAXR ||
+  if ((wv != 4 && wv != 6 && wv != 8 && wv != 12) || (a.N / 16) % (WT * wv) || S_max < 1 || S_max > WMAXR ||
       wide_lds(S_max) > 150 * 1024)
     return CFH_E_UNSUPPORTED;
   return CFH_OK;
 }
 
-// Waves per workgroup of a full-K wide launch over `units` units of `tiles` column tiles: the
-// count (dividing tiles) that loads the busiest CU least -- rounds of 256 workgroups times waves
-// a workgroup -- preferring fewer waves a workgroup on ties (measured on the 4096-wide flow: 384
-// workgroups of 8 waves left half the CUs with two workgroups, 256 of 12 none).
+// Waves per workgroup of a wide launch over `units` units of `tiles` column tiles: the count
+// (WT tiles a wave, dividing tiles) that loads the busiest CU least -- rounds of 256 workgroups
+// times waves a workgroup -- preferring fewer waves a workgroup on ties.
 int wide_wv(int tiles, int units) {
   constexpr int CUS = 256;
   int best = 0;
   long long best_load = 0;
-  for (int wv : {4, 6, 8, 12, 16}) {
-    if (tiles % wv) continue;
-    const long long wgs = (long long)units * tiles / wv;
+  for (int wv : {4, 6, 8, 12}) {
+    if (tiles % (WT * wv)) continue;
+    const long long wgs = (long long)units * tiles / (WT * wv);
     const long long load = (wgs + CUS - 1) / CUS * wv;
     if (!best || load < best_load) {
       best = wv;
@@ -242,29 +249,20 @@ int launch_wide(const WArgs& a0, int wv, hipStream_t st) {
   if (wide_check(a, wv, S_max)) return CFH_E_UNSUPPORTED;
   for (int e = 0; e < a.nex; ++e)
     if (a.ex[e].S < 1 || a.ex[e].lda < a.K || !a.ex[e].w || !a.ex[e].a || !a.ex[e].out) return CFH_E_INVALID;
-  a.wg_per_kc = (a.N / 16) / wv;
+  a.wg_per_kc = (a.N / 16) / (WT * wv);
   const size_t lds = wide_lds(S_max);
   const int ng = (S_max + 15) / 16;
-  // the split-K launches run 4-wave workgroups; the full-K ones (bias epilogues) any of the counts
-  if constexpr (EPI == E_PART || EPI == E_PART16) {
-    if (wv != 4) return CFH_E_UNSUPPORTED;
-    if (ng <= 2) return launch_wide_k<EPI, 2, 4>(a, lds, st);
-    if (ng <= 4) return launch_wide_k<EPI, 4, 4>(a, lds, st);
-    return launch_wide_k<EPI, 8, 4>(a, lds, st);
-  } else {
 #define CFH_WIDE(G)                                                                 \
   if (ng <= G) {                                                                    \
     switch (wv) {                                                                   \
       case 4: return launch_wide_k<EPI, G, 4>(a, lds, st);                          \
       case 6: return launch_wide_k<EPI, G, 6>(a, lds, st);                          \
       case 8: return launch_wide_k<EPI, G, 8>(a, lds, st);                          \
-      case 12: return launch_wide_k<EPI, G, 12>(a, lds, st);                        \
-      default: return launch_wide_k<EPI, G, 16>(a, lds, st);                        \
+      default: return launch_wide_k<EPI, G, 12>(a, lds, st);                        \
     }                                                                               \
   }
-    CFH_WIDE(2) CFH_WIDE(4) CFH_WIDE(8)
+  CFH_WIDE(2) CFH_WIDE(4) CFH_WIDE(8)
 #undef CFH_WIDE
-  }
   return CFH_E_UNSUPPORTED;
 }
 

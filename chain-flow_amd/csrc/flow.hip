@@ -453,7 +453,8 @@ struct Plan {
   bool wide;          // more than two requests a group: every row of the group shares each weight
                       // stream through the chunked-staging kernels (cfh_wide.h)
   int wv_qkv, wv_w1, wv_kv;        // wide full-K launches: waves per workgroup
-  int ks_wo, ks_ww2, ks_wout;      // wide split-K launches (4-wave workgroups): k-splits
+  int wv_split;                    // wide split-K launches: waves per workgroup
+  int ks_wo, ks_ww2, ks_wout;      //                        and k-splits
   bool ok;
 };
 
@@ -471,12 +472,13 @@ void make_wide_plan(Plan& p, const cfh_flow_dims* dm) {
   if (!p.ok) return;
   constexpr int CUS = 256;
   auto wv_full = [&](int N) { return wide_wv(N / 16, p.nch); };
+  p.wv_split = 4;
   auto ks_split = [&](int N, int K) {
     int best = 0;
     for (int ks = 1; ks <= K / WCH; ++ks) {
       if (K % ks || (K / ks) % WCH) continue;
       best = ks;
-      if ((long long)p.nch * (N / 16 / 4) * ks >= CUS) break;
+      if ((long long)p.nch * (N / 16 / (WT * p.wv_split)) * ks >= CUS) break;
     }
     return best;
   };
@@ -495,9 +497,9 @@ void make_wide_plan(Plan& p, const cfh_flow_dims* dm) {
   };
   p.ok = p.ks_wo > 0 && p.ks_ww2 > 0 && p.ks_wout > 0 && p.xnb > 0 &&
          !wide_check(wa(3 * p.d, p.d, 1), p.wv_qkv, p.Smax) && !wide_check(wa(p.fd, p.d, 1), p.wv_w1, p.Smax) &&
-         !wide_check(wa(2 * p.d, p.d, 1), p.wv_kv, p.Ct) && !wide_check(wa(p.d, p.d, p.ks_wo), 4, p.Smax) &&
-         !wide_check(wa(p.d, p.fd, p.ks_ww2), 4, p.Smax) && !wide_check(wa(p.d, p.d, p.ks_wout), 4, p.Smax) &&
-         !wide_check(wa(p.d, p.d, p.H), 4, p.Ct) &&
+         !wide_check(wa(2 * p.d, p.d, 1), p.wv_kv, p.Ct) && !wide_check(wa(p.d, p.d, p.ks_wo), p.wv_split, p.Smax) &&
+         !wide_check(wa(p.d, p.fd, p.ks_ww2), p.wv_split, p.Smax) &&
+         !wide_check(wa(p.d, p.d, p.ks_wout), p.wv_split, p.Smax) && !wide_check(wa(p.d, p.d, p.H), 4, p.Ct) &&
          (size_t)3 * p.KD * p.hd * 2 + (size_t)p.KD * p.KD * 4 <= 64 * 1024;   // self attention's LDS
 }
 
@@ -863,7 +865,7 @@ int block_pass_wide(const Plan& p, const cfh::ExpertLayout& L, const WS& w, cons
       WEx& x = a.ex[c];
       x.w = (const h16x8*)PTR(c, B + L.o); x.a = w.abuf[c]; x.lda = d; x.out = w.P[c]; x.S = S_of(c);
     }
-    if ((rc = launch_wide<E_PART>(a, 4, st))) return rc;
+    if ((rc = launch_wide<E_PART>(a, p.wv_split, st))) return rc;
   }
   ResArgs r = {};
   r.nex = nch; r.d = d; r.mode = p.res_mode;
@@ -915,7 +917,7 @@ int block_pass_wide(const Plan& p, const cfh::ExpertLayout& L, const WS& w, cons
       WEx& x = a.ex[c];
       x.w = (const h16x8*)PTR(c, B + L.w2); x.a = w.g[c]; x.lda = fd; x.out = w.P[c]; x.S = S_of(c);
     }
-    if ((rc = launch_wide<E_PART>(a, 4, st))) return rc;
+    if ((rc = launch_wide<E_PART>(a, p.wv_split, st))) return rc;
   }
   // residual + LayerNorm of the next block (out_norm after the last block)
   r.ks = p.ks_ww2;
@@ -1324,7 +1326,7 @@ int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* expert
         WEx& x = a.ex[c];
         x.w = (const h16x8*)PTR(c, L.out); x.a = w.abuf[c]; x.lda = d; x.out = w.P[c]; x.S = Rg * (c + 1) * CS;
       }
-      return launch_wide<E_PART>(a, 4, st);
+      return launch_wide<E_PART>(a, p.wv_split, st);
     };
     for (int s = 0; s < E; ++s) {
       if (p.wide) {

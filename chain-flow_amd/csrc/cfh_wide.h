@@ -27,7 +27,8 @@ namespace {
 constexpr int WCH = 128;          // K columns staged per chunk (4 k-steps)
 constexpr int WKS = WCH / 32;     // k-steps per chunk
 constexpr int WT = 2;             // 16-column tiles per wave: each operand read from LDS feeds WT multiplies
-constexpr int WSPF = WKS * WT;    // fragment loads in flight per wave (one chunk)
+constexpr int WRC = 1;            // chunks of fragments in flight per wave
+constexpr int WSPF = WRC * WKS * WT;   // fragment loads in flight per wave
 constexpr int WMAXR = 128;        // max activation rows of one expert in a wide group
 constexpr int WLDA = WCH + 8;     // LDS row stride (halves): rows of a chunk start on different banks
 
@@ -134,30 +135,43 @@ __global__ void __launch_bounds__(WV * 64) k_wide(WArgs a) {
   int roff[NG];
 #pragma unroll
   for (int g = 0; g < NG; ++g) roff[g] = (g * 16 + row < S ? g * 16 + row : 0) * WLDA + kg * 8;
-  // one chunk per ring cycle (WSPF = WKS WT): slot p holds tile p % WT of the chunk's k-step p / WT
-  for (int c = 0; c < nchunk; ++c) {
-    const h16* cur = (c & 1) ? buf1 : buf0;
-    h16* nxt = (c & 1) ? buf0 : buf1;
-    load_chunk(min(c + 1, nchunk - 1));
+  const h16x8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+  // WRC chunks per ring cycle: slot p holds tile p % WT of k-step (p / WT) % WKS of chunk
+  // c0 + p / (WT WKS)
+  for (int c0 = 0; c0 < nchunk; c0 += WRC) {
 #pragma unroll
-    for (int q = 0; q < WKS; ++q) {
-      // one k-step at a time: each row group's operand read once, multiplied by the WT fragments
+    for (int h = 0; h < WRC; ++h) {
+      const int c = c0 + h;
+      // past the last chunk (a count that is not a multiple of WRC) zero fragments multiply the last
+      // chunk's rows, which are finite (0 x NaN from a buffer never written would poison the sums);
+      // the loop keeps no branches
+      const h16* cur = (min(c, nchunk - 1) & 1) ? buf1 : buf0;
+      h16* nxt = (c & 1) ? buf0 : buf1;
+      load_chunk(min(c + 1, nchunk - 1));
 #pragma unroll
-      for (int g = 0; g < NG; ++g) {
-        const h16x8 av = *(const h16x8*)(cur + roff[g] + q * 32);
+      for (int q = 0; q < WKS; ++q) {
+        const int p0 = (h * WKS + q) * WT;
+        h16x8 bf[WT];
 #pragma unroll
-        for (int u = 0; u < WT; ++u) acc[u][g] = mfma_f16(av, ring[q * WT + u], acc[u][g]);
+        for (int u = 0; u < WT; ++u) bf[u] = (WRC == 1 || c < nchunk) ? ring[p0 + u] : zero8;
+        // one k-step at a time: each row group's operand read once, multiplied by the WT fragments
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          const h16x8 av = *(const h16x8*)(cur + roff[g] + q * 32);
+#pragma unroll
+          for (int u = 0; u < WT; ++u) acc[u][g] = mfma_f16(av, bf[u], acc[u][g]);
+        }
+#pragma unroll
+        for (int u = 0; u < WT; ++u) ring[p0 + u] = issue(u);
+        // left free, the scheduler hoists every read of the chunk ahead of the multiplies and runs
+        // out of registers
+        __builtin_amdgcn_sched_barrier(0);
       }
-#pragma unroll
-      for (int u = 0; u < WT; ++u) ring[q * WT + u] = issue(u);
-      // left free, the scheduler hoists every read of the chunk ahead of the multiplies and runs
-      // out of registers
-      __builtin_amdgcn_sched_barrier(0);
+      // chunk c + 1 goes to the other buffer (nobody reads it: every wave finished chunk c - 1
+      // before the last barrier); one barrier orders the stores before chunk c + 1's reads
+      if (c + 1 < nchunk) place_chunk(nxt);
+      lds_barrier();
     }
-    // chunk c + 1 goes to the other buffer (nobody reads it: every wave finished chunk c - 1
-    // before the last barrier); one barrier orders the stores before chunk c + 1's reads
-    if (c + 1 < nchunk) place_chunk(nxt);
-    lds_barrier();
   }
   // epilogue: rows g * 16 + rbase + q of column (t0 + u) * 16 + col
 #pragma unroll

@@ -407,7 +407,8 @@ class PathHead:
             pld, rpp = pred.stride(0), M // G
         if out is None:
             out = torch.empty(M, self.d, dtype=torch.float16, device=pred.device)
-        ws = self._workspace(min(M, 16), pred.device)
+        # (16 rows at a time, or wide groups of up to 128 rows: the workspace depends on min(M, 128))
+        ws = self._workspace(min(M, 128), pred.device)
         _lib.check(_lib.lib().cfh_path_residual(
             self._ptrs, self.order, self.ffn, self.d, lastp.data_ptr(), M,
             -1 if nlive is None else int(nlive), self.embed_w.data_ptr(), pred.data_ptr(), pld, rpp,

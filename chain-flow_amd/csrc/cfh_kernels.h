@@ -207,7 +207,8 @@ __global__ void __launch_bounds__(256) k_reduce(ReduceArgs a) {
 }
 
 // ---------------------------------------------------------------------------- GELU
-// g = fp16(gelu(sum_kc P[kc] + b1)) for every row of every expert.
+// g = fp16(gelu(fp16(sum_kc P[kc] + b1))) for every row of every expert: the sum is rounded to fp16
+// first, as torch's fp16 Linear module hands its output to the GELU module.
 struct GeluArgs {
   const float* P[4];
   const h16* b[4];
@@ -233,10 +234,10 @@ __global__ void __launch_bounds__(256) k_gelu(GeluArgs a) {
     const int n = (int)((j * 4) % a.N);
     const h16* bb = a.b[e] + n;
     h16* g = a.g[e] + j * 4;
-    g[0] = (h16)gelu_erf(s4.x + (float)bb[0]);
-    g[1] = (h16)gelu_erf(s4.y + (float)bb[1]);
-    g[2] = (h16)gelu_erf(s4.z + (float)bb[2]);
-    g[3] = (h16)gelu_erf(s4.w + (float)bb[3]);
+    g[0] = (h16)gelu_erf(r16(s4.x + (float)bb[0]));
+    g[1] = (h16)gelu_erf(r16(s4.y + (float)bb[1]));
+    g[2] = (h16)gelu_erf(r16(s4.z + (float)bb[2]));
+    g[3] = (h16)gelu_erf(r16(s4.w + (float)bb[3]));
   }
 }
 

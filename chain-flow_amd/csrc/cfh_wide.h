@@ -41,6 +41,8 @@ struct WEx {
   int S;               // activation rows (1 .. WMAXR)
   int pack, hrows;     // E_PART16: as SEx
   int nsplit;          // E_BIAS16: column n goes to block n / nsplit, stored [blocks][S][nsplit] (0: [S][N])
+  const int* ids;      // row i of the operand is a[max(ids[i * ids_stride], 0)] (a gather), or row i (null)
+  int ids_stride;
 };
 
 struct WArgs {
@@ -71,15 +73,21 @@ __global__ void __launch_bounds__(WV * 64) k_wide(WArgs a) {
   constexpr int NVR = WCH / 8;                        // 16-byte vectors per row of a chunk
   constexpr int NSV = (NG * 16 * NVR + NT - 1) / NT;  // vectors per thread at the most rows
   const int total = S * NVR;
+  // each staging slot's element offset in the operand, the same at every chunk (a gathered row's
+  // index is read once)
+  size_t soff[NSV];
+#pragma unroll
+  for (int u = 0; u < NSV; ++u) {
+    const int idx = min(u * NT + (int)threadIdx.x, total - 1);
+    const int i = idx / NVR, kk = (idx - i * NVR) * 8;
+    const size_t src = ex.ids ? (size_t)max(ex.ids[(size_t)i * ex.ids_stride], 0) : (size_t)i;
+    soff[u] = src * ex.lda + kk;
+  }
   h16x8 st[NSV];
   auto load_chunk = [&](int c) {
     const h16* base = ex.a + k0 + c * WCH;
 #pragma unroll
-    for (int u = 0; u < NSV; ++u) {
-      const int idx = min(u * NT + (int)threadIdx.x, total - 1);
-      const int i = idx / NVR, kk = (idx - i * NVR) * 8;
-      st[u] = *(const h16x8*)(base + (size_t)i * ex.lda + kk);
-    }
+    for (int u = 0; u < NSV; ++u) st[u] = *(const h16x8*)(base + soff[u]);
   };
   auto place_chunk = [&](h16* buf) {
 #pragma unroll

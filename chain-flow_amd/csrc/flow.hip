@@ -372,7 +372,8 @@ __global__ void __launch_bounds__(1024) k_xbias(XbiasArgs a) {
   const int hd = a.d / a.H;
   const h16* K = a.K[e] + (size_t)l * a.kstride;
   const h16* bq = (const h16*)((const char*)a.bq[e] + (size_t)l * a.bstride);
-  for (int p = wave; p < a.H * a.C; p += nw) {
+  // (the pairs of a wide group's many context rows spread over gridDim.y workgroups)
+  for (int p = blockIdx.y * nw + wave; p < a.H * a.C; p += gridDim.y * nw) {
     const int h = p / a.C, c = p - h * a.C;
     float s = 0.f;
     for (int j = lane; j < hd; j += 64) s += (float)bq[h * hd + j] * (float)K[(size_t)c * a.d + h * hd + j];
@@ -970,7 +971,7 @@ int per_draft_wide(const Plan& p, const cfh::ExpertLayout& L, const WS& w, const
   for (int c = 0; c < nch; ++c) {
     xb.K[c] = w.kvc[c]; xb.bq[c] = (const h16*)PTR(c, BLK(0) + L.qc_b); xb.sb[c] = w.fsb[c];
   }
-  hipLaunchKernelGGL(k_xbias, dim3(nch * NL), dim3(1024), 0, st, xb);
+  hipLaunchKernelGGL(k_xbias, dim3(nch * NL, (p.H * Cg + 63) / 64), dim3(1024), 0, st, xb);
   CFH_LAUNCH_CHECK();
   // A_h = Wq_h^T K_h^T (the transposed query weight against the K rows) and B_h = Wo_h V_h, split-K
   // by head: the partial of k-split h, rounded to fp16, is head h's factor

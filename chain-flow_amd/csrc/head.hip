@@ -19,7 +19,7 @@
 // kernel combines the blocks into the row's log-sum-exp and top-k.
 #include <limits.h>
 
-#include "cfh_kernels.h"
+#include "cfh_wide.h"
 
 namespace {
 
@@ -1002,6 +1002,55 @@ PathPlan path_plan(int M, int d, int ffn, int order) {
   return p;
 }
 
+// The path residual of many rows (the beams of a batch) in groups of up to WMAXR rows: every weight
+// of the path head streams once per group through the wide kernel (cfh_wide.h) instead of once
+// per 16 rows.  offsets: one k_wide launch over the live offset projections (the embedding rows
+// gathered by the ancestor ids), split-K partials; k_path_sum; up: k_wide with the GELU epilogue
+// (fp16 rounding before the GELU, as torch's Linear then GELU modules); down: split-K partials;
+// k_path_out.
+struct PathWide {
+  bool ok;
+  int o_ks, dn_ks, up_wv;
+  size_t off_P, off_a, off_g, off_dn, total;
+};
+
+PathWide path_wide_plan(int M, int d, int ffn, int order) {
+  PathWide p = {};
+  const int pf = ffn * d;
+  constexpr int CUS = 256, WV = 4;
+  auto ks_for = [&](int units, int N, int K) {
+    int best = 0;
+    for (int ks = 1; ks <= K / WCH; ++ks) {
+      if (K % ks || (K / ks) % WCH) continue;
+      best = ks;
+      if ((long long)units * (N / 16 / (WT * WV)) * ks >= CUS) break;
+    }
+    return best;
+  };
+  p.o_ks = ks_for(order, d, d);
+  p.dn_ks = ks_for(1, d, pf);
+  p.up_wv = wide_wv(pf / 16, 1);
+  auto wa = [&](int nex, int N, int K, int ks) {
+    WArgs a = {};
+    a.nex = nex; a.N = N; a.K = K; a.ks = ks;
+    return a;
+  };
+  p.ok = order <= 4 && p.o_ks > 0 && p.dn_ks > 0 && p.up_wv > 0 && !wide_check(wa(order, d, d, p.o_ks), WV, M) &&
+         !wide_check(wa(1, pf, d, 1), p.up_wv, M) && !wide_check(wa(1, d, pf, p.dn_ks), WV, M);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off = cfh::align256(off + bytes);
+    return o;
+  };
+  p.off_P = take((size_t)order * p.o_ks * M * d * 4);
+  p.off_a = take((size_t)M * d * 2);
+  p.off_g = take((size_t)M * pf * 2);
+  p.off_dn = take((size_t)p.dn_ks * M * d * 4);
+  p.total = off;
+  return p;
+}
+
 // ---------------------------------------------------------------------------- beam steps
 // Chain beam step (one wave per batch row, W*W <= 64): cand = cum[w] + lp[w][j];
 // (cum, flat) = top-W(cand); src = flat / W; tok = sl[ids[src][flat % W]];
@@ -1313,7 +1362,60 @@ int cfh_head_gemm16_topk(const void* x, int M, int d, const void* packed, int n,
 
 int64_t cfh_path_ws_bytes(int M, int d, int ffn_mult, int order) {
   if (M < 1 || d < 512 || d % 512 || ffn_mult < 1 || order < 1 || order > MAXEX) return -1;
-  return (int64_t)path_plan(std::min(M, PATH_CHUNK), d, ffn_mult, order).total;
+  size_t total = path_plan(std::min(M, PATH_CHUNK), d, ffn_mult, order).total;
+  if (M > PATH_CHUNK) {
+    const PathWide pw = path_wide_plan(std::min(M, WMAXR), d, ffn_mult, order);
+    if (pw.ok) total = std::max(total, pw.total);
+  }
+  return (int64_t)total;
+}
+
+// One launch sequence of the path residual for a wide group of M <= WMAXR rows.
+static int path_group_wide(const PathWide& pw, const void* const* ph, int order, int ffn_mult, int d,
+                           const int32_t* lastp, int M, int o, const void* embed_w, const void* pred, long long pred_ld,
+                           int rows_per_pred, int row0, void* hsum, void* ws, hipStream_t st) {
+  const int pf = ffn_mult * d;
+  char* base = (char*)ws;
+  float* P = (float*)(base + pw.off_P);
+  h16* A = (h16*)(base + pw.off_a);
+  h16* G = (h16*)(base + pw.off_g);
+  float* Pdn = (float*)(base + pw.off_dn);
+  int rc;
+  if (o > 0) {
+    WArgs a = {};
+    a.nex = o; a.N = d; a.K = d; a.ks = pw.o_ks;
+    for (int j = 0; j < o; ++j) {
+      WEx& x = a.ex[j];
+      x.w = (const h16x8*)ph[j]; x.a = (const h16*)embed_w; x.lda = d; x.ids = lastp + j; x.ids_stride = order;
+      x.out = P + (size_t)j * pw.o_ks * M * d; x.S = M;
+    }
+    if ((rc = launch_wide<E_PART>(a, 4, st))) return rc;
+  }
+  PathSumArgs ps = {};
+  ps.P = P; ps.lastp = lastp; ps.g = (const h16*)ph[2 * order]; ps.b = (const h16*)ph[2 * order + 1]; ps.a = A;
+  ps.order = order; ps.o = o; ps.ks = pw.o_ks; ps.M = M; ps.d = d;
+  for (int j = 0; j < o; ++j) ps.bias[j] = (const h16*)ph[order + j];
+  hipLaunchKernelGGL(k_path_sum, dim3(M), dim3(ROWT), 0, st, ps);
+  CFH_LAUNCH_CHECK();
+  {
+    WArgs a = {};
+    a.nex = 1; a.N = pf; a.K = d; a.ks = 1; a.gelu_r16 = 1;
+    a.ex[0].w = (const h16x8*)ph[2 * order + 2]; a.ex[0].a = A; a.ex[0].lda = d;
+    a.ex[0].bias = (const h16*)ph[2 * order + 3]; a.ex[0].out = G; a.ex[0].S = M;
+    if ((rc = launch_wide<E_GELU16>(a, pw.up_wv, st))) return rc;
+  }
+  {
+    WArgs a = {};
+    a.nex = 1; a.N = d; a.K = pf; a.ks = pw.dn_ks;
+    a.ex[0].w = (const h16x8*)ph[2 * order + 4]; a.ex[0].a = G; a.ex[0].lda = pf; a.ex[0].out = Pdn; a.ex[0].S = M;
+    if ((rc = launch_wide<E_PART>(a, 4, st))) return rc;
+  }
+  PathOutArgs po = {};
+  po.P = Pdn; po.bias = (const h16*)ph[2 * order + 5]; po.pred = (const h16*)pred; po.hsum = (h16*)hsum;
+  po.ks = pw.dn_ks; po.M = M; po.d = d; po.pred_ld = pred_ld; po.rows_per_pred = rows_per_pred; po.row0 = row0;
+  hipLaunchKernelGGL(k_path_out, dim3(64), dim3(256), 0, st, po);
+  CFH_LAUNCH_CHECK();
+  return CFH_OK;
 }
 
 // One launch sequence of the path residual for M <= PATH_CHUNK rows (rows row0 .. of the call).
@@ -1386,6 +1488,21 @@ int cfh_path_residual(const void* const* ph, int order, int ffn_mult, int d, con
   for (int i = 0; i < n_ptr; ++i)
     if (!ph[i]) return CFH_E_INVALID;
   const int o = (nlive < 0 || nlive > order) ? order : nlive;
+  if (M > PATH_CHUNK) {
+    // many rows (a batch's beams): wide groups of up to WMAXR rows, balanced
+    const PathWide pw = path_wide_plan(std::min(M, WMAXR), d, ffn_mult, order);
+    if (pw.ok) {
+      const int ng = (M + WMAXR - 1) / WMAXR, per = (M + ng - 1) / ng;
+      for (int r0 = 0; r0 < M; r0 += per) {
+        const int m = std::min(per, M - r0);
+        const int rc = path_group_wide(pw, ph, order, ffn_mult, d, lastp + (size_t)r0 * order, m, o, embed_w, pred,
+                                       pred_ld, rows_per_pred, r0, (h16*)hsum + (size_t)r0 * d, ws,
+                                       (hipStream_t)stream);
+        if (rc) return rc;
+      }
+      return CFH_OK;
+    }
+  }
   const PathPlan pp = path_plan(std::min(M, PATH_CHUNK), d, ffn_mult, order);
   // the GEMVs take at most PATH_CHUNK activation rows: chunks run one after another on the stream,
   // each on the same workspace

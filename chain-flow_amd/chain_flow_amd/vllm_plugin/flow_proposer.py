@@ -32,6 +32,9 @@ Drafters: the reference builds every checkpoint as the latent ``TreeVAEFlowDraft
 checkpoint's own ``drafter.vae.*`` tensors; so does this proposer for any checkpoint that carries
 VAE fields or tensors.  A checkpoint with neither is served as the target-width ``TreeFlowDrafter``
 (``expert_dim`` = target hidden size), the form the synthetic d = 2560 / 5120 workloads use.
+Profiling: ``CF_PROFILE=1`` (host-timed sections of every draft, draft graphs off) and
+``CF_DRAFTPROF=1`` (a one-off event timing of the draft and its pieces per batch bucket), as the
+reference's hooks of the same names (``:400-401, 1364-1424``).
 What differs, by design: no Hugging Face download (``CF_DRAFTER_DIR`` must be a local directory),
 no torch.compile, and the latent drafter's ``lag_context`` / ``anchor_token`` options are refused
 with a message (not built).
@@ -207,7 +210,16 @@ class FlowDrafterProposer:
         cg = os.environ.get("CF_CUDAGRAPH", "1")
         if cg not in ("0", "1", "force"):
             raise ValueError(f"CF_CUDAGRAPH={cg!r}: expected 0, 1 or force")
-        self.use_cg = cg != "0"
+        # CF_PROFILE=1: host-timed sections of every draft (each section synchronises), printed every
+        # CF_PROFILE_EVERY steps; it turns the draft graphs off, as in the reference (:400-401).
+        # CF_DRAFTPROF=1: a one-off GPU timing of the draft and its pieces when a batch bucket is
+        # first drafted (events, no per-step synchronisation; :1364-1424).
+        self.prof = os.environ.get("CF_PROFILE", "0") == "1"
+        self.prof_every = int(os.environ.get("CF_PROFILE_EVERY", "100") or 100)
+        self.draftprof = os.environ.get("CF_DRAFTPROF", "0") == "1"
+        self._t = {"ring": 0.0, "flow": 0.0, "search": 0.0, "steps": 0}
+        self._draftprof_done: set = set()
+        self.use_cg = cg != "0" and not self.prof
         self.force_cg = cg == "force"
         # two-pass candidate head, on by default as in the reference's defaults table
         # (cf/defaults.py:123-127): M = CF_TWOPASS_M (8192), one candidate set for all depths
@@ -291,11 +303,69 @@ class FlowDrafterProposer:
                        if capture else None)
 
     # ---- drafting --------------------------------------------------------------------------
-    def _draft_fn(self, ctx: torch.Tensor, known0: torch.Tensor) -> torch.Tensor:
+    def _search(self, ctx: torch.Tensor, known0: torch.Tensor, pred: torch.Tensor | None = None) -> torch.Tensor:
         if self.branching:
             return self.drafter.beam_tree(ctx, known0, keep=self.tree_keep, topb=self.tree_topb,
-                                          depth=self.tree_depth)
-        return self.drafter.beam_chains(ctx, known0, self.K, width=self.width)
+                                          depth=self.tree_depth, pred=pred)
+        return self.drafter.beam_chains(ctx, known0, self.K, width=self.width, pred=pred)
+
+    def _draft_fn(self, ctx: torch.Tensor, known0: torch.Tensor) -> torch.Tensor:
+        if not self.prof:
+            return self._search(ctx, known0)
+        import time
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        pred = self.drafter.predict_hidden(ctx)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        out = self._search(ctx, known0, pred)
+        torch.cuda.synchronize()
+        self._t["flow"] += t1 - t0
+        self._t["search"] += time.perf_counter() - t1
+        return out
+
+    def _profile_step(self, t_ring: float) -> None:
+        """CF_PROFILE: accumulate this step and print the running means every prof_every steps."""
+        t = self._t
+        t["ring"] += t_ring
+        t["steps"] += 1
+        if t["steps"] % self.prof_every == 0:
+            n = t["steps"]
+            print(f"[chain-flow] profile over {n} drafts (ms each, host-synchronised): ring "
+                  f"{t['ring'] * 1e3 / n:.3f}, predict_hidden {t['flow'] * 1e3 / n:.3f}, "
+                  f"{'tree' if self.branching else 'beam'} search {t['search'] * 1e3 / n:.3f}", flush=True)
+
+    def _draft_breakdown(self, ctx: torch.Tensor, known0: torch.Tensor, bucket: int) -> None:
+        """CF_DRAFTPROF: one GPU timing (events, mean of 20 after 3 warm-ups) of the draft and its pieces
+        for this batch bucket, printed once: whether a draft is launch-bound or GPU-bound."""
+        d = self.drafter
+
+        def t(fn, n=20):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(n):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            return a.elapsed_time(b) / n
+
+        pred = d.predict_hidden(ctx)
+        parts = [("predict_hidden", lambda: d.predict_hidden(ctx))]
+        if d.vae is not None:
+            lat = d.vae.encode(ctx.to(d.device, torch.float16))
+            z = d.flow.predict_hidden(lat)
+            parts += [("  vae encode", lambda: d.vae.encode(ctx.to(d.device, torch.float16))),
+                      ("  flow integrate", lambda: d.flow.predict_hidden(lat)),
+                      ("  vae decode", lambda: d.vae.decode(z))]
+        parts += [("beam/tree search", lambda: self._search(ctx, known0, pred)),
+                  ("  one shortlist head", lambda: d.head.topk(pred[:, 0].contiguous(), 8)),
+                  ("eager whole draft", lambda: self._search(ctx, known0))]
+        print(f"[cf-draftprof] bucket={bucket} GPU ms (mean of 20):", flush=True)
+        for name, fn in parts:
+            print(f"[cf-draftprof]   {name:28s} {t(fn):8.3f}", flush=True)
 
     def _lifecycle(self, rows, req_ids) -> list[int]:
         """Slot bookkeeping of ``_ctx_gpu`` (``:2045-2080``): returns the slots that hold a NEW request
@@ -380,9 +450,39 @@ class FlowDrafterProposer:
         sh = hidden[:off]
         if self.graphs is not None and self.graphs.bucket_for(len(rows)) is not None:
             draft = self.graphs.run(sh, rows, starts, cnt, known, wmask)
+            bucket = self.graphs.bucket_for(len(rows))
+            if self.draftprof and bucket not in self._draftprof_done:
+                self._draftprof_done.add(bucket)
+                g = self.graphs._g[bucket]
+                # replays with zero counts append nothing to the ring: each recomputes this step's draft
+                cnt = g[1]["cnt"].clone()
+                g[1]["cnt"].zero_()
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                for _ in range(20):
+                    g[0].replay()
+                b.record()
+                g[1]["cnt"].copy_(cnt)
+                torch.cuda.synchronize()
+                print(f"[cf-draftprof] bucket={bucket} graph replay (ring step + whole draft, mean of 20) "
+                      f"{a.elapsed_time(b) / 20:8.3f} ms", flush=True)
+                self._draft_breakdown(g[1]["ctx"], g[1]["k0"], bucket)
         else:
+            import time
+            t0 = time.perf_counter()
+            if self.prof:
+                torch.cuda.synchronize()
             ctx = self.ring.step(sh, rows, starts, cnt, wmask, kmax=self.kmax)
-            draft = self._draft_fn(ctx, torch.tensor(known, device=self.dev, dtype=torch.long))
+            if self.prof:
+                torch.cuda.synchronize()
+                t_ring = time.perf_counter() - t0
+            k0 = torch.tensor(known, device=self.dev, dtype=torch.long)
+            if self.draftprof and len(rows) not in self._draftprof_done:
+                self._draftprof_done.add(len(rows))
+                self._draft_breakdown(ctx, k0, len(rows))
+            draft = self._draft_fn(ctx, k0)
+            if self.prof:
+                self._profile_step(t_ring)
         if self.async_spec:
             return self._async_draft_tensor(draft, rows, nreq)
         draft = draft.cpu().tolist()                 # the one device -> host sync

@@ -128,3 +128,38 @@ def test_proposer_ring_steps_and_async(cuda, tmp_path, monkeypatch, graph):
         assert outa.dtype == torch.int32 and outa.is_cuda and outa.shape == (2, 5)
         for i in range(2):
             assert outa[i].cpu().tolist() == (out[i] if toks[i] else [0] * 5), (step, i)
+
+
+@pytest.mark.gpu
+def test_proposer_profiling_hooks_leave_drafts_unchanged(cuda, tmp_path, monkeypatch, capsys):
+    """CF_DRAFTPROF=1 (one event timing per batch bucket, the draft graph's profiling replays append
+    nothing to the ring) and CF_PROFILE=1 (host-timed sections, no graphs) give the same drafts as the
+    plain proposer, step after step, and print their timings."""
+    d = 512
+    cfg, W, slv = _ckpt(tmp_path)
+    for k in ("VLLM_SPEC_TREE", "CF_SHORTLIST", "CF_FLOW_STEPS", "CF_DRAFT_BUCKETS", "CF_ASYNC_SPEC"):
+        monkeypatch.delenv(k, raising=False)
+    monkeypatch.setenv("CF_DRAFTER_DIR", str(tmp_path))
+    vc = SimpleNamespace(speculative_config=SimpleNamespace(num_speculative_tokens=5),
+                         scheduler_config=SimpleNamespace(max_num_seqs=4))
+    props = {}
+    for name, env in (("plain", {}), ("draftprof", {"CF_DRAFTPROF": "1"}),
+                      ("profile", {"CF_PROFILE": "1", "CF_PROFILE_EVERY": "2"})):
+        for k in ("CF_DRAFTPROF", "CF_PROFILE", "CF_PROFILE_EVERY"):
+            monkeypatch.delenv(k, raising=False)
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
+        props[name] = fp.FlowDrafterProposer(vc)
+        props[name].bind_target(W["embed_tokens.weight"].to(cuda), W["lm_head.weight"].to(cuda))
+    assert props["profile"].use_cg is False
+    rng = np.random.default_rng(8)
+    for step in range(3):
+        toks = [[int(t) for t in slv[rng.integers(0, len(slv), size=int(rng.integers(1, 4)))]] for _ in range(2)]
+        n = sum(len(t) for t in toks)
+        hid = torch.randn(n, d, generator=torch.Generator().manual_seed(70 + step)).half().to(cuda)
+        outs = {k: p.propose(toks, hidden_states=hid, req_ids=["a", "b"]) for k, p in props.items()}
+        torch.cuda.synchronize()
+        print(f"[proposer profiling] step {step}: {outs}", flush=True)
+        assert outs["draftprof"] == outs["plain"] and outs["profile"] == outs["plain"], step
+    text = capsys.readouterr().out
+    assert "[cf-draftprof]" in text and "[chain-flow] profile over 2 drafts" in text

@@ -46,6 +46,9 @@ SIGNATURES = {
     "cfh_flow_integrate_noalloc": (_I, [C.POINTER(FlowDims), C.POINTER(_VP), _VP, _VP, _I, _VP]),
     "cfh_flow_prepare_streams": (_I, [C.POINTER(FlowDims), _VP, C.POINTER(_I)]),
     "cfh_flow_group_size": (_I, [C.POINTER(FlowDims), _I, C.POINTER(_I)]),
+    "cfh_flow_anchor_ws_bytes": (_I64, [C.POINTER(FlowDims), _I]),
+    "cfh_flow_anchor": (_I, [C.POINTER(FlowDims), _I, C.POINTER(_VP), _VP, _VP, _I, _VP, _VP, _VP]),
+    "cfh_flow_integrate_anchored": (_I, [C.POINTER(FlowDims), C.POINTER(_VP), _VP, _VP, _VP, _VP, _I, _VP]),
     "cfh_flow_query_streams": (_I, [_VP, C.POINTER(_I), C.POINTER(_I)]),
     "cfh_flow_release_streams": (_I, [_VP]),
     "cfh_vae_bytes": (_I64, [C.POINTER(VaeDims)]),

@@ -47,10 +47,9 @@ class Drafter:
         self.path_trim = path_trim
         self.vae = None
         if isinstance(cfg, TreeVAEFlowConfig):
-            for flag in ("lag_context", "anchor_token"):
-                if getattr(cfg, flag):
-                    raise ValueError(f"{flag}=True is not built: this build runs the latent drafter "
-                                     f"without the lag slot / token anchor (the shipped default)")
+            # lag_context only changes how training builds the context (build_context,
+            # cf/drafters/tree_vae_flow.py:144-160, called from training/train_tree_flow.py:233); the
+            # proposer never calls it, so at inference its lag_proj weights are unused.
             hidden = weights["lm_head.weight"].shape[1]
             self.vae = HiddenVAE(cfg, hidden, weights, device=dev)
         self.flow = FusedFlow(cfg, weights, device=dev)
@@ -110,13 +109,25 @@ class Drafter:
         """``_nlive`` (``cf/vllm_plugin/flow_proposer.py:1030-1037``)."""
         return depth if self.path_trim else None
 
-    def predict_hidden(self, ctx: torch.Tensor) -> torch.Tensor:
+    @property
+    def anchored(self) -> bool:
+        """True for a latent drafter trained with ``anchor_token``: its flow is conditioned on the
+        committed token's embedding (``cf/drafters/tree_vae_flow.py:45, 128-129``)."""
+        return bool(self.flow.anchor_params)
+
+    def predict_hidden(self, ctx: torch.Tensor, known0: torch.Tensor | None = None) -> torch.Tensor:
         """ctx [B, C, hidden] (front-padded) -> marginal hiddens [B, draft_length, hidden]
-        (``TreeFlowDrafter.predict_hidden``; latent drafter: decode(integrate(encode(ctx).mu)))."""
+        (``TreeFlowDrafter.predict_hidden``; latent drafter: decode(integrate(encode(ctx).mu))).
+        known0 [B]: the committed tokens; an anchored drafter is given their embeddings as the
+        reference's proposer does (``predict_hidden(ctx, anchor_embed(known0))``,
+        ``cf/vllm_plugin/flow_proposer.py:1203, 1285``); ignored by an unanchored one."""
         ctx = ctx.to(self.device, torch.float16)
         if self.vae is None:
             return self.flow.predict_hidden(ctx)
-        return self.vae.decode(self.flow.predict_hidden(self.vae.encode(ctx)))
+        anchor = None
+        if known0 is not None and self.anchored:
+            anchor = self.flow.anchor(known0, self.path.embed_w)
+        return self.vae.decode(self.flow.predict_hidden(self.vae.encode(ctx), anchor=anchor))
 
     def beam_chains(self, ctx: torch.Tensor, known0: torch.Tensor, K: int, width: int = 4,
                     pred: torch.Tensor | None = None) -> torch.Tensor:
@@ -128,7 +139,7 @@ class Drafter:
             raise ValueError(f"beam width {W} is not supported: the beam step keeps W*W <= 64 candidates "
                              f"per chain (width 1..8)")
         if pred is None:
-            pred = self.predict_hidden(ctx)
+            pred = self.predict_hidden(ctx, known0)
         B, Kd, d = pred.shape
         steps = min(K + 1, Kd)
         lastp = torch.full((B, W, order), -1, dtype=torch.int32, device=dev)
@@ -166,7 +177,7 @@ class Drafter:
             raise ValueError(f"tree keep {keep} x top-b {topb} is not supported: a tree step ranks at most 64 "
                              f"children per request (keep * topb <= 64)")
         if pred is None:
-            pred = self.predict_hidden(ctx)
+            pred = self.predict_hidden(ctx, known0)
         B, Kd, d = pred.shape
         nstep = min(depth, Kd - 1)
         sizes, fr = [], 1

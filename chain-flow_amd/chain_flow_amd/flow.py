@@ -17,7 +17,8 @@ import torch
 
 from chain_flow_amd import _lib
 from chain_flow_amd.config import TreeFlowConfig
-from chain_flow_amd.weights import expert_param_names, expert_prefixes
+from chain_flow_amd.head import pack_linear
+from chain_flow_amd.weights import anchor_param_names, expert_param_names, expert_prefixes
 
 
 # the shapes the reference's fused block kernel is built for (cf/cuda_block.py:46-51)
@@ -98,8 +99,27 @@ class FusedFlow:
             torch.cuda.current_stream().synchronize()   # raw copies may be freed after this
             self.packed.append(buf)
         self._experts = _lib.ptr_array([b.data_ptr() for b in self.packed])
+        self._retired = []   # outgrown buffers, kept alive for graphs that may still use them
+        # the anchored latent drafter (anchor_token): anchor_in + each expert's anchor_mlp, matrices
+        # packed, in cfh_flow_anchor's order
+        self.anchor_params = []
+        self.anchor_hidden = 0
+        names = anchor_param_names(cfg)
+        if names:
+            for n in names:
+                t = weights[n].to(self.device, torch.float16).contiguous()
+                self.anchor_params.append(pack_linear(t) if t.dim() == 2 else t)
+            self.anchor_hidden = int(weights["anchor_in.weight"].shape[1])
+            self._anchor_w = _lib.ptr_array([t.data_ptr() for t in self.anchor_params])
+            nws = int(L.cfh_flow_anchor_ws_bytes(C.byref(self.dims), self.anchor_hidden))
+            if nws < 0:
+                raise ValueError(f"anchor shape not supported by libcfhip: hidden={self.anchor_hidden}")
+            self.anchor_ws = torch.empty(nws, dtype=torch.uint8, device=self.device)
+            # one buffer for every batch up to max_batch (a captured draft graph holds its address)
+            nch = cfg.draft_length // cfg.chunk_size
+            self._anchor_buf = torch.empty(nch * max(1, int(max_batch)) * cfg.flow_dim, dtype=torch.float16,
+                                           device=self.device)
         self.ws = torch.empty(ws, dtype=torch.uint8, device=self.device)
-        self._retired = []   # outgrown workspaces, kept alive for graphs that may still use them
         self.concurrent = self.prepare_streams()
 
     def prepare_streams(self, stream=None) -> bool:
@@ -117,14 +137,41 @@ class FusedFlow:
     def weight_bytes(self) -> int:
         return sum(b.numel() for b in self.packed)
 
+    def anchor(self, tokens: torch.Tensor, embed_w: torch.Tensor) -> torch.Tensor:
+        """The anchored drafter's per-expert anchor rows [n_chunks, B, d] fp16 for the committed
+        tokens [B] (``anchor_embed`` then each expert's ``anchor_mlp``, cf/drafters/tree_flow.py:237-241,
+        cf/drafters/chunked_flow.py:256-262; ``cfh_flow_anchor``).  embed_w: the LM's input embedding
+        table [V, hidden] fp16 on the flow's device.  A token below 0 reads row 0."""
+        if not self.anchor_params:
+            raise ValueError("this drafter has no anchor_token parameters")
+        cfg = self.cfg
+        if embed_w.dtype != torch.float16 or embed_w.device != self.device or embed_w.dim() != 2 \
+                or embed_w.shape[1] != self.anchor_hidden:
+            raise ValueError(f"embed_w must be [V, {self.anchor_hidden}] fp16 on the flow's device")
+        tok = tokens.reshape(-1).to(self.device, torch.int32).contiguous()
+        B = tok.numel()
+        nch = cfg.draft_length // cfg.chunk_size
+        n = nch * B * cfg.flow_dim
+        if n > self._anchor_buf.numel():
+            # (a batch above max_batch: the old buffer stays referenced, never freed)
+            self._retired.append(self._anchor_buf)
+            self._anchor_buf = torch.empty(n, dtype=torch.float16, device=self.device)
+        rows = self._anchor_buf[:n].view(nch, B, cfg.flow_dim)
+        _lib.check(_lib.lib().cfh_flow_anchor(C.byref(self.dims), self.anchor_hidden, self._anchor_w,
+                                              embed_w.contiguous().data_ptr(), tok.data_ptr(), B,
+                                              rows.data_ptr(), self.anchor_ws.data_ptr(),
+                                              _lib.stream_handle()), "cfh_flow_anchor")
+        return rows
+
     def predict_hidden(self, ctx: torch.Tensor, out: torch.Tensor | None = None,
-                       numerics: int | None = None) -> torch.Tensor:
+                       numerics: int | None = None, anchor: torch.Tensor | None = None) -> torch.Tensor:
         """ctx [B, context_size, d] fp16 (already front-padded; d = cfg.flow_dim) -> [B, draft_length, d]
         fp16, in the numerics the reference uses for this shape and batch (``reference_numerics``)
         unless ``numerics`` names one.  With ``init_mode="noise"`` the initial latents are
         ``torch.randn(B, draft_length, d, fp16) * noise_scale`` from torch's current generator on
         the flow's device (``init_latents``, cf/drafters/tree_flow.py:154-155), written into ``out``
-        before the call."""
+        before the call.  ``anchor``: the anchor rows of ``anchor()`` [n_chunks, B, d], added to
+        every row of every block (cf/drafters/chunked_flow.py:376), or None."""
         cfg = self.cfg
         d = cfg.flow_dim
         if ctx.dim() != 3 or ctx.shape[1] != cfg.context_size or ctx.shape[2] != d:
@@ -146,6 +193,16 @@ class FusedFlow:
         self.dims.numerics = reference_numerics(cfg, B) if numerics is None else int(numerics)
         if cfg.init_mode == "noise":
             out.copy_(torch.randn(B, cfg.draft_length, d, device=self.device, dtype=torch.float16) * cfg.noise_scale)
+        if anchor is not None:
+            nch = cfg.draft_length // cfg.chunk_size
+            if tuple(anchor.shape) != (nch, B, d) or anchor.dtype != torch.float16 \
+                    or anchor.device != self.device or not anchor.is_contiguous():
+                raise ValueError(f"anchor must be contiguous [{nch}, {B}, {d}] fp16 on the flow's device")
+            _lib.check(_lib.lib().cfh_flow_integrate_anchored(C.byref(self.dims), self._experts, ctx.data_ptr(),
+                                                              anchor.data_ptr(), out.data_ptr(),
+                                                              self.ws.data_ptr(), B, _lib.stream_handle()),
+                       "cfh_flow_integrate_anchored")
+            return out
         _lib.check(_lib.lib().cfh_flow_integrate(C.byref(self.dims), self._experts, ctx.data_ptr(),
                                                  out.data_ptr(), self.ws.data_ptr(), B,
                                                  _lib.stream_handle()),

@@ -36,8 +36,9 @@ Profiling: ``CF_PROFILE=1`` (host-timed sections of every draft, draft graphs of
 ``CF_DRAFTPROF=1`` (a one-off event timing of the draft and its pieces per batch bucket), as the
 reference's hooks of the same names (``:400-401, 1364-1424``).
 What differs, by design: no Hugging Face download (``CF_DRAFTER_DIR`` must be a local directory),
-no torch.compile, and the latent drafter's ``lag_context`` / ``anchor_token`` options are refused
-with a message (not built).
+no torch.compile.  An ``anchor_token`` drafter is given the committed token's embedding on every
+draft (``:1199-1203``); ``lag_context`` only changes training contexts, so it loads and drafts as
+the reference's proposer runs it (its ``lag_proj`` unused).
 The target's final hidden states reach the proposer through :meth:`stash_hidden_states` (the
 reference monkeypatches ``GPUModelRunner.propose_draft_token_ids`` to stash
 ``sample_hidden_states``, ``:40-59``) and the target's input embeddings and ``lm_head`` weight
@@ -315,7 +316,7 @@ class FlowDrafterProposer:
         import time
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        pred = self.drafter.predict_hidden(ctx)
+        pred = self.drafter.predict_hidden(ctx, known0)
         torch.cuda.synchronize()
         t1 = time.perf_counter()
         out = self._search(ctx, known0, pred)
@@ -352,13 +353,16 @@ class FlowDrafterProposer:
             torch.cuda.synchronize()
             return a.elapsed_time(b) / n
 
-        pred = d.predict_hidden(ctx)
-        parts = [("predict_hidden", lambda: d.predict_hidden(ctx))]
+        pred = d.predict_hidden(ctx, known0)
+        parts = [("predict_hidden", lambda: d.predict_hidden(ctx, known0))]
         if d.vae is not None:
             lat = d.vae.encode(ctx.to(d.device, torch.float16))
-            z = d.flow.predict_hidden(lat)
+            anc = d.flow.anchor(known0, d.path.embed_w) if d.anchored else None
+            z = d.flow.predict_hidden(lat, anchor=anc)
+            if d.anchored:
+                parts += [("  anchor rows", lambda: d.flow.anchor(known0, d.path.embed_w))]
             parts += [("  vae encode", lambda: d.vae.encode(ctx.to(d.device, torch.float16))),
-                      ("  flow integrate", lambda: d.flow.predict_hidden(lat)),
+                      ("  flow integrate", lambda: d.flow.predict_hidden(lat, anchor=anc)),
                       ("  vae decode", lambda: d.vae.decode(z))]
         parts += [("beam/tree search", lambda: self._search(ctx, known0, pred)),
                   ("  one shortlist head", lambda: d.head.topk(pred[:, 0].contiguous(), 8)),

@@ -53,6 +53,19 @@ def expert_param_names(cfg: TreeFlowConfig, prefix: str):
     return names
 
 
+def anchor_param_names(cfg: TreeFlowConfig):
+    """The anchored latent drafter's parameters in the order cfh_flow_anchor takes them: anchor_in,
+    then each chunk expert's anchor_mlp (``cf/drafters/tree_vae_flow.py:116-125``,
+    ``cf/drafters/chunked_flow.py:256-262``); none unless ``anchor_token``."""
+    if not getattr(cfg, "anchor_token", False):
+        return []
+    names = ["anchor_in.weight", "anchor_in.bias"]
+    for p in expert_prefixes(cfg):
+        names += [p + "anchor_mlp.0.weight", p + "anchor_mlp.0.bias", p + "anchor_mlp.2.weight",
+                  p + "anchor_mlp.2.bias"]
+    return names
+
+
 def vae_half_names(cfg: TreeVAEFlowConfig, side: str):
     """State-dict names (``vae.`` prefix) of one VAE half, ``side`` = "encoder" or "decoder", in
     the order cfh_vae_pack expects."""
@@ -153,6 +166,16 @@ def param_specs(cfg: TreeFlowConfig, vocab: int, target: bool = True, hidden: in
     specs["path_head.mlp.3.bias"] = ((d,), "bias", pf)
     if isinstance(cfg, TreeVAEFlowConfig):
         specs.update(_vae_specs(cfg, hidden))
+    for n in anchor_param_names(cfg):
+        dz = cfg.flow_dim
+        if n == "anchor_in.weight":
+            specs[n] = ((dz, d), "linear", d)
+        elif n == "anchor_in.bias":
+            specs[n] = ((dz,), "bias", d)
+        elif n.endswith(".weight"):
+            specs[n] = ((dz, dz), "linear", dz)
+        else:
+            specs[n] = ((dz,), "bias", dz)
     if target:
         specs["lm_head.weight"] = ((vocab, d), "linear", d)
         specs["embed_tokens.weight"] = ((vocab, d), "embedding_tok", d)

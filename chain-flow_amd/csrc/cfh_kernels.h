@@ -171,12 +171,14 @@ __global__ void __launch_bounds__(WPB * 64) k_gemv(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------- partial reduce
-// out = fp16(sum_kc P[kc] + b), used for the per-draft cross K/V and time embeddings.
+// out = fp16(sum_kc P[kc] + b), used for the per-draft cross K/V and time embeddings; with act = 1,
+// out = fp16(silu(fp16(sum_kc P[kc] + b))) (a Linear module then a SiLU module, as the anchor MLP).
 struct ReduceArgs {
   const float* P[4];
   const h16* b[4];
   h16* out[4];
   int nex, nl, ks, rows, N, d, kv;   // kv: N = 2d split into [2][rows][d] per layer
+  int act;
   long long vstride;
 };
 
@@ -194,7 +196,8 @@ __global__ void __launch_bounds__(256) k_reduce(ReduceArgs a) {
     float s = 0.f;
     for (int q = 0; q < a.ks; ++q) s += P[(size_t)q * per_l];
     const h16* b = (const h16*)((const char*)a.b[e] + (size_t)l * a.vstride);
-    const float v = s + (float)b[n];
+    float v = s + (float)b[n];
+    if (a.act == 1) v = silu(r16(v));
     size_t o;
     if (a.kv) {
       const int part = n / a.d, nn = n - part * a.d;

@@ -91,6 +91,7 @@ struct RowsArgs {
   int init;            // CFH_INIT_*: how z0 is formed
   int only;            // euler: -1 = every chunk; c = chunk c's update and expert c's next rows only
                        // (the rows of earlier chunks are read from z, already updated)
+  const h16* anchor[4];  // per expert, the group's anchor rows [R][d] (the anchored latent drafter), or null
 };
 
 __global__ void __launch_bounds__(ROWT) k_rows(RowsArgs a) {
@@ -214,11 +215,13 @@ __global__ void __launch_bounds__(ROWT) k_rows(RowsArgs a) {
       if (q < nq) {
         const h16* pp = a.pos[c2] + (size_t)rr * d + q * 4;
         const h16* tt = a.tau[c2] + q * 4;
+        const h16* an = a.anchor[c2] ? a.anchor[c2] + (size_t)req * d + q * 4 : nullptr;
         float o[4] = {zv[k].x, zv[k].y, zv[k].z, zv[k].w};
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           float xv = r16(o[t] + (float)pp[t]);
           if (cur) xv = r16(xv + (float)tt[t]);
+          if (an) xv = r16(xv + (float)an[t]);   // the anchor conditions every row of every block
           o[t] = xv;
         }
         vals[k] = make_float4(o[0], o[1], o[2], o[3]);
@@ -1133,8 +1136,9 @@ int release_companions(hipStream_t st) {
 
 // The whole draft of `batch` requests on workspace ws (the plan's carve() layout): per request the
 // per-draft launches, then E Euler steps of L block passes and the OUT / ROWS step.
+// anchor: null, or the anchored latent drafter's anchor rows [n_chunks][batch][d] fp16 (cfh_flow_anchor).
 int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* experts, const void* ctx, void* z_out,
-              void* ws_ptr, int batch, hipStream_t st, bool may_create = true) {
+              void* ws_ptr, int batch, hipStream_t st, bool may_create = true, const void* anchor = nullptr) {
   // Under stream capture every expert stays on the caller's stream: a replayed graph of the
   // two-stream form ran slower than the one-stream form (d = 5120: 21.7 against 19.6 ms a flow
   // pass; d = 4096: 15.2 against 14.8), while eager calls gain from the overlap (19.0 ms).
@@ -1195,6 +1199,7 @@ int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* expert
         r.x[c] = w.x[c]; r.pos[c] = (const h16*)PTR(c, L.pos); r.tau[c] = w.tau[c];
         r.g[c] = (const h16*)PTR(c, BLK(0) + L.sn_w); r.b[c] = (const h16*)PTR(c, BLK(0) + L.sn_b);
         r.a[c] = w.abuf[c];
+        r.anchor[c] = anchor ? (const h16*)anchor + ((size_t)c * batch + g0) * d : nullptr;
       }
       hipLaunchKernelGGL(k_rows, dim3(Rg * KD), dim3(ROWT), 0, st, r);
       CFH_LAUNCH_CHECK();
@@ -1295,6 +1300,7 @@ int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* expert
         r.tau[c] = w.tau[c] + (size_t)(s + 1 < E ? s + 1 : s) * d;
         r.g[c] = (const h16*)PTR(c, BLK(0) + L.sn_w); r.b[c] = (const h16*)PTR(c, BLK(0) + L.sn_b);
         r.a[c] = w.abuf[c];
+        r.anchor[c] = anchor ? (const h16*)anchor + ((size_t)c * batch + g0) * d : nullptr;
       }
       return r;
     };
@@ -1383,6 +1389,76 @@ int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* expert
   return CFH_OK;
 }
 
+// The anchored latent drafter's anchor rows (TreeVAEFlowDrafter.anchor_embed then each chunk
+// expert's anchor_mlp, cf/drafters/tree_flow.py:237-241, cf/drafters/chunked_flow.py:256-262, 376):
+//   t1 = fp16(W_in emb[max(token, 0)] + b_in)                       [rows][d]   (anchor_in)
+//   a_c = fp16(W2_c fp16(silu(fp16(W1_c t1 + b1_c))) + b2_c)       per chunk expert c
+// as split-K GEMVs over at most MAXR rows a launch and their reductions.
+struct AnchorPlan {
+  int ks_in, ks_d;
+  size_t off_P, off_t1, off_t3, total;
+};
+
+AnchorPlan anchor_plan(int d, int hidden, int nch) {
+  AnchorPlan p = {};
+  p.ks_in = ksplit_for(1, d / 16, hidden, MAXR);
+  p.ks_d = ksplit_for(nch, d / 16, d, MAXR);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off = cfh::align256(off + bytes);
+    return o;
+  };
+  p.off_P = take((size_t)std::max(p.ks_in, nch * p.ks_d) * MAXR * d * 4);
+  p.off_t1 = take((size_t)MAXR * d * 2);
+  p.off_t3 = take((size_t)nch * MAXR * d * 2);
+  p.total = off;
+  return p;
+}
+
+int anchor_rows(const cfh_flow_dims* dm, int hidden, const void* const* aw, const void* embed_w, const int32_t* tokens,
+                int batch, void* out, void* ws, hipStream_t st) {
+  const int d = dm->d, nch = dm->draft_length / dm->chunk_size;
+  const AnchorPlan ap = anchor_plan(d, hidden, nch);
+  float* P = (float*)((char*)ws + ap.off_P);
+  h16* t1 = (h16*)((char*)ws + ap.off_t1);
+  h16* t3 = (h16*)((char*)ws + ap.off_t3);
+  int rc;
+  for (int r0 = 0; r0 < batch; r0 += MAXR) {
+    const int m = std::min(MAXR, batch - r0);
+    {   // anchor_in over the gathered embedding rows
+      GemvArgs a = {};
+      a.nex = 1; a.nl = 1; a.ks = ap.ks_in; a.tiles = d / 16; a.N = d; a.K = hidden;
+      a.ex[0].w = (const h16x8*)aw[0]; a.ex[0].a = (const h16*)embed_w; a.ex[0].lda = hidden;
+      a.ex[0].ids = tokens + r0; a.ex[0].ids_stride = 1; a.ex[0].pout = P; a.ex[0].rows = m;
+      if ((rc = launch_gemv<SRC_GATHER>(a, m, st))) return rc;
+      ReduceArgs r = {};
+      r.nex = 1; r.nl = 1; r.ks = ap.ks_in; r.rows = m; r.N = d; r.d = d;
+      r.P[0] = P; r.b[0] = (const h16*)aw[1]; r.out[0] = t1;
+      hipLaunchKernelGGL(k_reduce, dim3(64), dim3(256), 0, st, r);
+      CFH_LAUNCH_CHECK();
+    }
+    for (int layer = 0; layer < 2; ++layer) {   // anchor_mlp.0 then SiLU, anchor_mlp.2; every expert at once
+      GemvArgs a = {};
+      a.nex = nch; a.nl = 1; a.ks = ap.ks_d; a.tiles = d / 16; a.N = d; a.K = d;
+      ReduceArgs r = {};
+      r.nex = nch; r.nl = 1; r.ks = ap.ks_d; r.rows = m; r.N = d; r.d = d; r.act = layer == 0;
+      for (int c = 0; c < nch; ++c) {
+        GemvEx& x = a.ex[c];
+        x.w = (const h16x8*)aw[2 + 4 * c + 2 * layer];
+        x.a = layer == 0 ? t1 : t3 + (size_t)c * MAXR * d;
+        x.lda = d; x.pout = P + (size_t)c * ap.ks_d * m * d; x.rows = m;
+        r.P[c] = x.pout; r.b[c] = (const h16*)aw[3 + 4 * c + 2 * layer];
+        r.out[c] = layer == 0 ? t3 + (size_t)c * MAXR * d : (h16*)out + ((size_t)c * batch + r0) * d;
+      }
+      if ((rc = launch_gemv<SRC_BUF>(a, m, st))) return rc;
+      hipLaunchKernelGGL(k_reduce, dim3(64), dim3(256), 0, st, r);
+      CFH_LAUNCH_CHECK();
+    }
+  }
+  return CFH_OK;
+}
+
 // The no-allocation entry point's workspace: one array per device, resolved to its device address
 // on the first call on each device (the array's name in host code is a host-side stand-in, never a
 // device address).  Its contents persist between calls; the flow writes every workspace element
@@ -1450,6 +1526,33 @@ int cfh_flow_integrate(const cfh_flow_dims* dm, const void* const* experts, cons
   for (int c = 0; c < p.nch; ++c)
     if (!experts[c]) return CFH_E_INVALID;
   return integrate(p, dm, experts, ctx, z_out, ws_ptr, batch, (hipStream_t)stream);
+}
+
+int cfh_flow_integrate_anchored(const cfh_flow_dims* dm, const void* const* experts, const void* ctx,
+                                const void* anchor, void* z_out, void* ws_ptr, int batch, void* stream) {
+  if (!cfh::flow_dims_ok(dm) || dm->d > ROWT * ROWE || dm->draft_length > MAXR) return CFH_E_UNSUPPORTED;
+  if (!experts || !ctx || !anchor || !z_out || !ws_ptr || batch < 1) return CFH_E_INVALID;
+  const Plan p = make_plan(dm, group_size(dm, batch));
+  if (!p.ok) return CFH_E_UNSUPPORTED;
+  for (int c = 0; c < p.nch; ++c)
+    if (!experts[c]) return CFH_E_INVALID;
+  return integrate(p, dm, experts, ctx, z_out, ws_ptr, batch, (hipStream_t)stream, true, anchor);
+}
+
+int64_t cfh_flow_anchor_ws_bytes(const cfh_flow_dims* dm, int hidden) {
+  if (!cfh::flow_dims_ok(dm) || hidden < 32 || hidden % 32) return -1;
+  return (int64_t)anchor_plan(dm->d, hidden, dm->draft_length / dm->chunk_size).total;
+}
+
+int cfh_flow_anchor(const cfh_flow_dims* dm, int hidden, const void* const* aw, const void* embed_w,
+                    const int32_t* tokens, int batch, void* anchor, void* ws, void* stream) {
+  if (!cfh::flow_dims_ok(dm) || hidden < 32 || hidden % 32 || (dm->d / 16) % WPB) return CFH_E_UNSUPPORTED;
+  if (!aw || !embed_w || !tokens || !anchor || !ws || batch < 1) return CFH_E_INVALID;
+  const int nch = dm->draft_length / dm->chunk_size;
+  if (nch > 4) return CFH_E_UNSUPPORTED;
+  for (int i = 0; i < 2 + 4 * nch; ++i)
+    if (!aw[i]) return CFH_E_INVALID;
+  return anchor_rows(dm, hidden, aw, embed_w, tokens, batch, anchor, ws, (hipStream_t)stream);
 }
 
 int cfh_flow_prepare_streams(const cfh_flow_dims* dm, void* stream, int* concurrent) {

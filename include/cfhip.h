@@ -131,6 +131,24 @@ int cfh_flow_pack_expert(const cfh_flow_dims* dims, const void* const* raw, int 
 int cfh_flow_integrate(const cfh_flow_dims* dims, const void* const* experts, const void* ctx,
                        void* z_out, void* ws, int batch, void* stream);
 
+/* The anchored latent drafter (TreeVAEFlowConfig.anchor_token): the embedding of each request's
+ * committed token, through the drafter's anchor_in and each chunk expert's anchor_mlp, conditions
+ * every row of every block (cf/drafters/tree_flow.py:237-241, cf/drafters/chunked_flow.py:256-262,
+ * 376: x = fp16(x + anchor_mlp(anchor)) after the position and time embeddings):
+ *   cfh_flow_anchor: anchor[c][b] = fp16(W2_c fp16(silu(fp16(W1_c t_b + b1_c))) + b2_c) with
+ *     t_b = fp16(W_in embed_w[max(tokens[b], 0)] + b_in); aw = 2 + 4 n_chunks device pointers:
+ *     anchor_in.weight (PACKED, [d][hidden]), anchor_in.bias, then per chunk expert
+ *     anchor_mlp.0.weight (PACKED [d][d]), anchor_mlp.0.bias, anchor_mlp.2.weight (PACKED), anchor_mlp.2.bias;
+ *     embed_w [V][hidden] fp16, tokens [batch] int32, anchor [n_chunks][batch][d] fp16 out,
+ *     ws of cfh_flow_anchor_ws_bytes bytes.
+ *   cfh_flow_integrate_anchored: cfh_flow_integrate with those rows added (the reference's
+ *     predict_hidden(ctx, anchor_embed(known0)), flow_proposer.py:1203, 1285). */
+int64_t cfh_flow_anchor_ws_bytes(const cfh_flow_dims* dims, int hidden);
+int cfh_flow_anchor(const cfh_flow_dims* dims, int hidden, const void* const* aw, const void* embed_w,
+                    const int32_t* tokens, int batch, void* anchor, void* ws, void* stream);
+int cfh_flow_integrate_anchored(const cfh_flow_dims* dims, const void* const* experts, const void* ctx,
+                                const void* anchor, void* z_out, void* ws, int batch, void* stream);
+
 /* Requests per group (*requests) that cfh_flow_integrate drafts together for a batch of `batch`:
  * every weight byte streams once per group.  No counterpart in the reference, whose batched flow
  * runs torch modules over the whole batch (cf/drafters/chunked_flow.py:295-331). */

@@ -11,6 +11,9 @@ Follows, in the reference (``cf/`` = ``src/chain_flow/``):
 * ``cf/drafters/chunked_flow.py:185-202``  ``HiddenKVFlowBlock.forward`` (pre-LN self-MHA, cross-MHA,
   LN -> Linear(d, f*d) -> erf-GELU -> Linear(f*d, d))
 * ``cf/drafters/chunked_flow.py:382-384``  ``post_blocks`` (out_norm + out_proj on the current rows)
+* ``cf/drafters/tree_flow.py:237-241``, ``cf/drafters/chunked_flow.py:256-262, 376``  the anchored
+  latent drafter: ``anchor_in(emb(token))`` through each expert's ``anchor_mlp`` (Linear, SiLU,
+  Linear), added to every row after the position and time embeddings
 * ``cf/csrc/fused_block.cu:280-325, 452-668, 674-722``  the fused-kernel numerics: fp32 residual,
   fp16-parked LayerNorm rows, fp16 q/k/v, attention output and GELU output; cross K/V from
   ``context_norm(ctx)`` computed once per draft.
@@ -192,9 +195,24 @@ def fused_kernel_shape(d, ffn_mult, heads, chunk_rows, ctx_rows, batch):
             and 0 < ctx_rows <= 16 and batch == 1)
 
 
-def expert_velocity(W, pfx, prev, cur, tau_add, chunk_start, kvs, cfg, numerics):
+def anchor_rows(W, emb_rows, prefixes, numerics):
+    """The anchored latent drafter's per-expert anchor vectors: ``anchor_embed`` =
+    ``anchor_in(emb(token))`` (``cf/drafters/tree_flow.py:237-241``), then each chunk expert's
+    ``anchor_mlp`` = Linear -> SiLU -> Linear (``cf/drafters/chunked_flow.py:256-262``), each module's
+    output materialised in the expert dtype.  emb_rows [B, hidden] -> [expert][B, d]."""
+    t1 = r16(_lin(r16(emb_rows, numerics), W["anchor_in.weight"], W["anchor_in.bias"]), numerics)
+    out = []
+    for p in prefixes:
+        t2 = r16(_lin(t1, W[p + "anchor_mlp.0.weight"], W[p + "anchor_mlp.0.bias"]), numerics)
+        t3 = r16(silu(t2), numerics)
+        out.append(r16(_lin(t3, W[p + "anchor_mlp.2.weight"], W[p + "anchor_mlp.2.bias"]), numerics))
+    return out
+
+
+def expert_velocity(W, pfx, prev, cur, tau_add, chunk_start, kvs, cfg, numerics, anchor=None):
     """``HiddenKVFlowExpert.forward`` = pre_blocks -> L blocks -> post_blocks
-    (``cf/drafters/chunked_flow.py:333-414``).  prev [B, P, d], cur [B, c, d] -> velocity [B, c, d]."""
+    (``cf/drafters/chunked_flow.py:333-414``).  prev [B, P, d], cur [B, c, d] -> velocity [B, c, d].
+    anchor [B, d]: the expert's anchor vector, added to every row (``:376``)."""
     x = np.concatenate([prev, cur], axis=1)
     P, c = prev.shape[1], cur.shape[1]
     pos = np.concatenate([np.arange(P), chunk_start + np.arange(c)])
@@ -202,6 +220,8 @@ def expert_velocity(W, pfx, prev, cur, tau_add, chunk_start, kvs, cfg, numerics)
         raise ValueError("hidden_kv_flow position exceeds configured draft length")
     x = r16(x + W[pfx + "position_embedding.weight"][pos][None], numerics)
     x[:, P:] = r16(x[:, P:] + tau_add[None, None, :], numerics)
+    if anchor is not None:
+        x = r16(x + anchor[:, None, :], numerics)
     mask = causal_mask(P + c)
     res = x.copy()
     for l in range(cfg["num_layers"]):
@@ -215,19 +235,22 @@ def expert_prefixes(num_chunks):
     return ["expert."] + [f"extra_experts.{i}." for i in range(num_chunks - 1)]
 
 
-def predict_hidden(W, context, cfg, numerics="fp16", return_trace=False, z0=None):
+def predict_hidden(W, context, cfg, numerics="fp16", return_trace=False, z0=None, anchor=None):
     """``TreeFlowDrafter.predict_hidden`` (``cf/drafters/tree_flow.py:229-244``).
 
     context [B, C, d] (values in the expert dtype) -> z_E [B, draft_length, d].
     cfg keys: draft_length, chunk_size, num_layers, num_heads, num_flow_steps, init_mode.
     z0: the initial latents when given (``init_mode="noise"`` draws them from torch's generator,
-    ``tree_flow.py:154-155``: the caller passes the same draw)."""
+    ``tree_flow.py:154-155``: the caller passes the same draw).
+    anchor: the committed tokens' embeddings [B, hidden] for an anchored drafter (``anchor_rows``
+    turns them into each expert's vector), or None."""
     context = r16(context, numerics)
     K, cs, E = cfg["draft_length"], cfg["chunk_size"], cfg["num_flow_steps"]
     nch = K // cs
     pfxs = expert_prefixes(nch)
     kvs = [[cross_kv(W, f"{p}blocks.{l}.", context, numerics) for l in range(cfg["num_layers"])]
            for p in pfxs]
+    anc = anchor_rows(W, anchor, pfxs, numerics) if anchor is not None else [None] * len(pfxs)
     z = init_latents(context, K, numerics, cfg.get("init_mode", "delta")) if z0 is None else np.array(z0, copy=True)
     trace = [z.copy()]
     dt = 1.0 / E
@@ -238,7 +261,7 @@ def predict_hidden(W, context, cfg, numerics="fp16", return_trace=False, z0=None
             start = ci * cs
             tau_add = tau_embedding(W, p, tau, numerics)
             vels.append(expert_velocity(W, p, z[:, :start], z[:, start:start + cs], tau_add, start,
-                                        kvs[ci], cfg, numerics))
+                                        kvs[ci], cfg, numerics, anc[ci]))
         v = np.concatenate(vels, axis=1)
         z = r16(z + r16(dt * v, numerics), numerics)
         trace.append(z.copy())

@@ -88,11 +88,13 @@ def vae_weights(W):
     return {k[4:]: v for k, v in W.items() if k.startswith("vae.")}
 
 
-def predict_hidden(W, context, vae_cfg, flow_cfg, numerics="fp16", flow_numerics=None):
+def predict_hidden(W, context, vae_cfg, flow_cfg, numerics="fp16", flow_numerics=None, anchor=None):
     """``TreeVAEFlowDrafter.predict_hidden`` (``cf/drafters/tree_vae_flow.py:172-175``):
-    context [B, C, hidden] -> decode(integrate(encode(context).mu)) [B, draft_length, hidden].
-    ``flow_numerics`` (default ``numerics``) is the latent flow's mode (``oracle.flow``)."""
+    context [B, C, hidden] -> decode(integrate(encode(context).mu, anchor)) [B, draft_length, hidden].
+    ``flow_numerics`` (default ``numerics``) is the latent flow's mode (``oracle.flow``); ``anchor``
+    the committed tokens' embeddings [B, hidden] of an anchored drafter."""
     V = vae_weights(W)
     ctx_lat = encode_sequence_mu(V, context, vae_cfg, numerics)
-    z = oflow.predict_hidden(W, ctx_lat, flow_cfg, numerics=numerics if flow_numerics is None else flow_numerics)
+    z = oflow.predict_hidden(W, ctx_lat, flow_cfg, numerics=numerics if flow_numerics is None else flow_numerics,
+                             anchor=anchor)
     return decode_sequence(V, z, vae_cfg, numerics)

@@ -162,3 +162,60 @@ def test_latent_proposer_chain_matches_oracle(cuda, tmp_path, monkeypatch):
         near = any((ohead.margins(t["lp"], 4) <= 1e-3).any() or (ohead.margins(t["cand"], 4) <= 1e-3).any()
                    for t in trace)
         assert near, (out[0], ref[0].tolist())
+
+
+@pytest.mark.gpu
+def test_anchored_latent_drafter_matches_oracle(cuda):
+    """An anchor_token drafter at the shipped 4B shapes (hidden 2560, latent 640 = expert_dim): the
+    committed tokens' embeddings through anchor_in and each expert's anchor_mlp condition every
+    flow block (cf/drafters/tree_flow.py:237-244, chunked_flow.py:256-262, 376), three requests."""
+    hidden, V, B = 2560, 512, 3
+    cfg = _cfg(640, 1920, 8, 2, layers=2, steps=2, expert_dim=640, anchor_token=True)
+    W = make_weights(cfg, V, init="test", base_seed=23, hidden=hidden)
+    print("[anchored latent drafter] hidden=2560 latent=640 L=2 E=2 B=3", flush=True)
+    dr = Drafter(cfg, {k: v.to(cuda) for k, v in W.items()}, None, device=cuda)
+    assert dr.anchored
+    ctx = synthetic_context(B, 8, hidden, seed=31)
+    tok = torch.tensor([5, 300, 0])
+    pred = dr.predict_hidden(ctx.to(cuda), tok.to(cuda))
+    plain = dr.predict_hidden(ctx.to(cuda))
+    torch.cuda.synchronize()
+    W64 = {k: to64(v) for k, v in W.items()}
+    emb = W64["embed_tokens.weight"][tok.numpy()]
+    ref = ovae.predict_hidden(W64, to64(ctx), _vcfg(cfg), _fcfg(cfg), "fp16", oracle_numerics(cfg, B), anchor=emb)
+    err = rel_err(to64(pred), ref)
+    moved = rel_err(to64(pred), to64(plain))
+    print(f"  rel err {err:.3e} (anchor moves the draft by {moved:.3e})", flush=True)
+    assert np.isfinite(to64(pred)).all() and err < TOL_FP16 and moved > 10 * TOL_FP16
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("d,B", [(640, 1), (1024, 5), (1024, 24)])
+def test_anchor_rows_and_anchored_flow_match_oracle(cuda, d, B):
+    """cfh_flow_anchor (anchor_in + every expert's anchor_mlp, bit-for-bit in fp16 up to summation
+    order) and cfh_flow_integrate_anchored against the oracle's flow with the anchor; d=1024 x 24
+    requests runs the wide request groups."""
+    from chain_flow_amd.flow import FusedFlow
+    hidden, V = 2048, 256
+    cfg = _cfg(d, 256, 4, 1, layers=2, steps=2, expert_dim=d, anchor_token=True)
+    names = {n for n in param_specs(cfg, V, hidden=hidden) if not n.startswith(("vae.", "path_head.", "markov."))}
+    W = make_weights(cfg, V, init="test", base_seed=29, names=names, hidden=hidden)
+    print(f"[anchored flow] d={d} B={B}", flush=True)
+    ff = FusedFlow(cfg, {k: v.to(cuda) for k, v in W.items()}, device=cuda)
+    ctx = synthetic_context(B, 8, d, seed=B)
+    tok = torch.randint(0, V, (B,), generator=torch.Generator().manual_seed(B))
+    emb_w = W["embed_tokens.weight"].to(cuda, torch.float16)
+    rows = ff.anchor(tok.to(cuda), emb_w)
+    z = ff.predict_hidden(ctx.to(cuda), anchor=rows)
+    torch.cuda.synchronize()
+    W64 = {k: to64(v) for k, v in W.items()}
+    emb = W64["embed_tokens.weight"][tok.numpy()]
+    prefixes = ["expert."] + [f"extra_experts.{i}." for i in range(cfg.draft_length // cfg.chunk_size - 1)]
+    ref_rows = oflow.anchor_rows(W64, emb, prefixes, "fp16")
+    for c, r in enumerate(ref_rows):
+        assert rel_err(to64(rows[c]), r) < 1e-3, c
+    num = oracle_numerics(cfg, B)
+    ref = oflow.predict_hidden(W64, to64(ctx), _fcfg(cfg), numerics=num, anchor=emb)
+    err = rel_err(to64(z), ref)
+    print(f"  rel err {err:.3e} ({num})", flush=True)
+    assert np.isfinite(to64(z)).all() and err < TOL_FP16

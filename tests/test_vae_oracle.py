@@ -5,6 +5,9 @@
   fallback, and TreeVAEFlowDrafter.predict_hidden (encode -> latent flow -> decode);
 * one encoder layer against torch's own nn.TransformerEncoderLayer (norm_first, GELU), the library
   module the reference instantiates, in float64;
+* the anchored drafter (anchor_token): anchor_embed, each expert's anchor_mlp and
+  predict_hidden(hidden, anchor_embed(tokens)) against the reference's own outputs, and that the
+  anchor changes the draft (so the pin bites);
 * that the fp16 restatement stays close to the fp32 one, and the row-count guard.
 """
 from __future__ import annotations
@@ -19,6 +22,7 @@ import torch
 from conftest import rel_err
 from chain_flow_amd.config import TreeVAEFlowConfig, config_from_model_args
 from chain_flow_amd.weights import make_weights, param_specs, vae_param_names
+from oracle import flow as oflow
 from oracle import vae as ovae
 
 G = np.load(Path(__file__).parent / "golden" / "reference_vae_tiny.npz")
@@ -26,12 +30,12 @@ HIDDEN, LATENT, VOCAB, RANK, SEED = 64, 32, 96, 16, 5
 TOL = 1e-5
 
 
-def _cfg(E=2, inter=48, heads=4):
-    return TreeVAEFlowConfig(context_size=8, draft_length=8, chunk_size=4, expert_dim=HIDDEN, num_heads=8,
-                             ffn_multiplier=6, num_drafter_layers=2, num_flow_steps=E, init_mode="delta",
-                             markov_rank=RANK, path_order=4, path_ffn_multiplier=2, latent_size=LATENT,
-                             vae_intermediate_size=inter, vae_num_layers=2, vae_num_heads=heads,
-                             vae_max_sequence_length=16)
+def _cfg(E=2, inter=48, heads=4, anchor=False):
+    return TreeVAEFlowConfig(context_size=8, draft_length=8, chunk_size=4, expert_dim=LATENT if anchor else HIDDEN,
+                             num_heads=8, ffn_multiplier=6, num_drafter_layers=2, num_flow_steps=E,
+                             init_mode="delta", markov_rank=RANK, path_order=4, path_ffn_multiplier=2,
+                             latent_size=LATENT, vae_intermediate_size=inter, vae_num_layers=2,
+                             vae_num_heads=heads, vae_max_sequence_length=16, anchor_token=anchor)
 
 
 def _vcfg(cfg):
@@ -89,6 +93,42 @@ def test_latent_predict_hidden_matches_reference(E):
     W = _weights(cfg)
     pred = ovae.predict_hidden(W, G["hidden"].astype(np.float64), _vcfg(cfg), _fcfg(cfg), numerics="fp32")
     assert rel_err(pred, G[f"pred_E{E}"]) < TOL
+
+
+def test_anchored_predict_hidden_matches_reference():
+    """anchor_embed = anchor_in(emb(token)), each expert's anchor_mlp (Linear, SiLU, Linear), and the
+    anchored predict_hidden (cf/drafters/tree_flow.py:237-244, chunked_flow.py:256-262, 376)."""
+    cfg = _cfg(2, anchor=True)
+    W = _weights(cfg, "weights_sha_anchor")
+    tok = G["anchor_tokens"]
+    emb = W["embed_tokens.weight"][tok]
+    t1 = oflow._lin(emb, W["anchor_in.weight"], W["anchor_in.bias"])
+    assert rel_err(t1, G["anchor_in"]) < TOL
+    rows = oflow.anchor_rows(W, emb, ["expert.", "extra_experts.0."], "fp32")
+    for c in range(2):
+        assert rel_err(rows[c], G[f"anchor_mlp_c{c}"]) < TOL
+    hidden = G["anchor_hidden"].astype(np.float64)
+    pred = ovae.predict_hidden(W, hidden, _vcfg(cfg), _fcfg(cfg), numerics="fp32", anchor=emb)
+    assert rel_err(pred, G["pred_anchor_E2"]) < TOL
+    none = ovae.predict_hidden(W, hidden, _vcfg(cfg), _fcfg(cfg), numerics="fp32")
+    assert rel_err(none, G["pred_anchor_none_E2"]) < TOL
+    # the anchor moves the draft well beyond the tolerance, and a per-expert mix-up would show
+    assert rel_err(pred, none) > 1e-2
+    assert rel_err(rows[0], rows[1]) > 1e-2
+
+
+def test_anchor_names_follow_the_module_tree():
+    """anchor_in then per expert anchor_mlp.{0,2}; nothing for an unanchored config."""
+    from chain_flow_amd.weights import anchor_param_names
+    assert anchor_param_names(_cfg()) == []
+    names = anchor_param_names(_cfg(anchor=True))
+    assert names[:2] == ["anchor_in.weight", "anchor_in.bias"]
+    assert names[2:6] == ["expert.anchor_mlp.0.weight", "expert.anchor_mlp.0.bias",
+                          "expert.anchor_mlp.2.weight", "expert.anchor_mlp.2.bias"]
+    assert len(names) == 2 + 4 * 2
+    specs = param_specs(_cfg(anchor=True), VOCAB, hidden=HIDDEN)
+    assert specs["anchor_in.weight"][0] == (LATENT, HIDDEN)
+    assert specs["extra_experts.0.anchor_mlp.2.weight"][0] == (LATENT, LATENT)
 
 
 def test_encoder_layer_equals_torch_library():

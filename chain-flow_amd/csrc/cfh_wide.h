@@ -49,6 +49,8 @@ struct WArgs {
   WEx ex[4];
   int nex, N, K, ks, wg_per_kc;
   int gelu_r16;        // E_GELU16: as SArgs
+  int pair;            // entries e and e + nex/2 stream the same weights (two request groups of one
+                       // expert): their workgroups for a unit run side by side on one XCD
 };
 
 template <int EPI, int NG, int WV>
@@ -57,6 +59,13 @@ __global__ void __launch_bounds__(WV * 64) k_wide(WArgs a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   int b = blockIdx.x;
   const int per_ex = a.ks * a.wg_per_kc;
+  if (a.pair) {
+    // workgroups b and b + 8 (dispatched together, on the same XCD: workgroups go to the XCDs
+    // round robin) take the same unit of the two groups, so the second reads the weight fragments
+    // the first has just brought into the XCD's L2 instead of from HBM
+    const int lo = b & 7, hi = b >> 3;
+    b = (((hi >> 1) << 3) | lo) + (hi & 1) * (a.nex / 2) * per_ex;
+  }
   const int e = b / per_ex;
   b -= e * per_ex;
   const int kc = b / a.wg_per_kc;
@@ -240,6 +249,9 @@ int wide_check(const WArgs& a, int wv, int S_max) {
     return CFH_E_UNSUPPORTED;
   if ((wv != 4 && wv != 6 && wv != 8 && wv != 12) || (a.N / 16) % (WT * wv) || S_max < 1 || S_max > WMAXR ||
       wide_lds(S_max) > 150 * 1024)
+    return CFH_E_UNSUPPORTED;
+  // pairing: an even entry count and a whole number of 8-workgroup runs per half
+  if (a.pair && (a.nex % 2 || ((long long)(a.nex / 2) * a.ks * ((a.N / 16) / (WT * wv))) % 8))
     return CFH_E_UNSUPPORTED;
   return CFH_OK;
 }

@@ -257,7 +257,8 @@ struct XattArgs {
   int Sr[4];             // rows per request (the S rows hold S / Sr requests)
   int Ssg[4];            // rows per subgroup (0: S): workgroups take the rows in subgroups of at
                          // most 16, each with its own requests' context rows
-  int nex, d, H, C, nb;  // C: context rows of all the group's requests
+  int Ce[4];             // context rows of the entry's group (0: C)
+  int nex, d, H, C, nb;  // C: context rows of all the group's requests (the most of any entry)
   int Cq;                // context rows per request: row r scores only its request's rows
   int nsg, Csg;          // subgroups, context rows per subgroup (0: C)
   float scale;
@@ -278,7 +279,7 @@ __global__ void __launch_bounds__(XT) k_xattn(XattArgs a) {
   b /= a.nsg;
   const int h = b % a.H, e = b / a.H;
   // this subgroup's rows [r0, r0 + S) of the expert's St rows and context rows [c0, c0 + C) of Ct
-  const int St = a.S[e], Ct = a.C, d = a.d;
+  const int St = a.S[e], Ct = a.Ce[e] > 0 ? a.Ce[e] : a.C, d = a.d;
   const int Ssg = a.Ssg[e] > 0 ? a.Ssg[e] : St, Csg = a.Csg > 0 ? a.Csg : Ct;
   const int r0 = sg * Ssg, c0 = sg * Csg;
   const int S = min(Ssg, St - r0), C = min(Csg, Ct - c0);
@@ -441,6 +442,15 @@ int launch_xattn(const XattArgs& a, hipStream_t st) {
   return CFH_OK;
 }
 
+// Launch shapes of the wide kernels with `groups` request groups a launch.
+struct WideShape {
+  int groups;
+  int wv_qkv, wv_w1, wv_kv;        // full-K launches: waves per workgroup
+  int wv_split;                    // split-K launches: waves per workgroup
+  int ks_wo, ks_ww2, ks_wout;      //                   and k-splits
+  bool ok;
+};
+
 struct Plan {
   int d, fd, CS, E, NL, C, KD, H, hd, nch, Smax;
   int R, Ct;          // requests per group (rows packed in one tile) and their context rows R C
@@ -456,14 +466,79 @@ struct Plan {
   int wpb_fold, xnb;  // fold hoist launch waves / XATT column blocks per (expert, head)
   bool wide;          // more than two requests a group: every row of the group shares each weight
                       // stream through the chunked-staging kernels (cfh_wide.h)
-  int wv_qkv, wv_w1, wv_kv;        // wide full-K launches: waves per workgroup
-  int wv_split;                    // wide split-K launches: waves per workgroup
-  int ks_wo, ks_ww2, ks_wout;      //                        and k-splits
+  WideShape ws[2];    // wide launch shapes for one group a launch, and for two (ws[1].ok: a batch of
+                      // several groups runs two at a time, both groups' entries in every launch)
   bool ok;
 };
 
-// Wide plan: launch shapes that give each streaming launch about one workgroup per CU (both chunk
-// experts in one launch), and whether every launch of the draft fits the wide kernels.
+// Waves per workgroup of a wide launch whose workgroups should all be resident at once: the most
+// workgroups up to one per CU, then the most waves.  Two request groups of one expert then stream
+// each weight fragment side by side (on one XCD, `WArgs::pair`), and the second read hits the L2:
+// W1 at d = 4096 for two 16-request groups took 96.7 us a launch as 256 workgroups of 12 waves
+// (one group alone: 79.5 us), 127-135 us as 512 of 6 or 768 of 4, 159 us when the groups' reads
+// did not coincide.
+int wide_wv_resident(int tiles, int units) {
+  constexpr int CUS = 256;
+  int best = 0;
+  long long best_wgs = 0;
+  for (int wv : {4, 6, 8, 12}) {
+    if (tiles % (WT * wv)) continue;
+    const long long wgs = (long long)units * tiles / (WT * wv);
+    if (wgs > CUS) continue;
+    if (!best || wgs > best_wgs || (wgs == best_wgs && wv > best)) {
+      best = wv;
+      best_wgs = wgs;
+    }
+  }
+  return best ? best : wide_wv(tiles, units);
+}
+
+// Wide launch shapes for `groups` request groups a launch: about one workgroup per CU for each
+// streaming launch (every chunk expert of every group in one launch).
+WideShape wide_shape(const Plan& p, int groups) {
+  WideShape s = {};
+  s.groups = groups;
+  const int units = groups * p.nch;
+  if (units > 4) return s;
+  constexpr int CUS = 256;
+  // split-K launches: 4-wave workgroups for one group; for two, 8-wave ones at one workgroup per CU,
+  // so that the two groups' workgroups of a unit run together (d = 4096, 16 + 16 requests, E = 2:
+  // 8.34 against 8.90 ms a flow pass with 4-wave workgroups)
+  s.wv_split = groups > 1 && (p.d / 16) % (WT * 8) == 0 ? 8 : 4;
+  auto ks_split = [&](int N, int K) {
+    int best = 0;
+    for (int ks = 1; ks <= K / WCH; ++ks) {
+      if (K % ks || (K / ks) % WCH) continue;
+      best = ks;
+      if ((long long)units * (N / 16 / (WT * s.wv_split)) * ks >= CUS) break;
+    }
+    return best;
+  };
+  auto wv_full = [&](int N) { return groups > 1 ? wide_wv_resident(N / 16, units) : wide_wv(N / 16, units); };
+  s.wv_qkv = wv_full(3 * p.d);
+  s.wv_w1 = wv_full(p.fd);
+  s.wv_kv = wide_wv(2 * p.d / 16, std::min(4, groups * std::min(4 / groups, p.nch * p.NL)));
+  s.ks_wo = ks_split(p.d, p.d);
+  s.ks_ww2 = ks_split(p.d, p.fd);
+  s.ks_wout = ks_split(p.d, p.d);
+  auto wa = [&](int N, int K, int ks, int nex) {
+    WArgs a = {};
+    a.nex = nex; a.N = N; a.K = K; a.ks = ks; a.pair = groups > 1;
+    return a;
+  };
+  const int kv_nex = groups * std::min(4 / groups, p.nch * p.NL);
+  s.ok = s.ks_wo > 0 && s.ks_ww2 > 0 && s.ks_wout > 0 &&
+         !wide_check(wa(3 * p.d, p.d, 1, units), s.wv_qkv, p.Smax) &&
+         !wide_check(wa(p.fd, p.d, 1, units), s.wv_w1, p.Smax) &&
+         !wide_check(wa(2 * p.d, p.d, 1, kv_nex), s.wv_kv, p.Ct) &&
+         !wide_check(wa(p.d, p.d, s.ks_wo, units), s.wv_split, p.Smax) &&
+         !wide_check(wa(p.d, p.fd, s.ks_ww2, units), s.wv_split, p.Smax) &&
+         !wide_check(wa(p.d, p.d, s.ks_wout, units), s.wv_split, p.Smax) &&
+         !wide_check(wa(p.d, p.d, p.H, groups * p.nch), 4, p.Ct);
+  return s;
+}
+
+// Wide plan: both launch shapes, and whether every launch of the draft fits the wide kernels.
 void make_wide_plan(Plan& p, const cfh_flow_dims* dm) {
   p.wide = true;
   p.conc = false;
@@ -474,36 +549,13 @@ void make_wide_plan(Plan& p, const cfh_flow_dims* dm) {
   p.ok = p.fold && p.hd % WCH == 0 && p.d % WCH == 0 && p.fd % WCH == 0 && p.Smax <= WMAXR && p.Ct <= WMAXR &&
          p.C <= 8 && 2 * p.KD <= MAXR && res_nq(p.d) > 0;
   if (!p.ok) return;
-  constexpr int CUS = 256;
-  auto wv_full = [&](int N) { return wide_wv(N / 16, p.nch); };
-  p.wv_split = 4;
-  auto ks_split = [&](int N, int K) {
-    int best = 0;
-    for (int ks = 1; ks <= K / WCH; ++ks) {
-      if (K % ks || (K / ks) % WCH) continue;
-      best = ks;
-      if ((long long)p.nch * (N / 16 / (WT * p.wv_split)) * ks >= CUS) break;
-    }
-    return best;
-  };
-  p.wv_qkv = wv_full(3 * p.d);
-  p.wv_w1 = wv_full(p.fd);
-  p.wv_kv = wide_wv(2 * p.d / 16, std::min(4, p.nch * p.NL));
-  p.ks_wo = ks_split(p.d, p.d);
-  p.ks_ww2 = ks_split(p.d, p.fd);
-  p.ks_wout = ks_split(p.d, p.d);
-  p.pks = std::max(std::max(p.H, p.ks_wo), std::max(p.ks_ww2, p.ks_wout));
+  p.ws[0] = wide_shape(p, 1);
+  p.ws[1] = wide_shape(p, 2);
+  p.pks = p.H;
+  for (const WideShape& w : p.ws)
+    if (w.ok) p.pks = std::max(p.pks, std::max(w.ks_wo, std::max(w.ks_ww2, w.ks_wout)));
   p.xnb = xattn_blocks(p.d, p.nch * p.H, 4);
-  auto wa = [&](int N, int K, int ks) {
-    WArgs a = {};
-    a.nex = p.nch; a.N = N; a.K = K; a.ks = ks;
-    return a;
-  };
-  p.ok = p.ks_wo > 0 && p.ks_ww2 > 0 && p.ks_wout > 0 && p.xnb > 0 &&
-         !wide_check(wa(3 * p.d, p.d, 1), p.wv_qkv, p.Smax) && !wide_check(wa(p.fd, p.d, 1), p.wv_w1, p.Smax) &&
-         !wide_check(wa(2 * p.d, p.d, 1), p.wv_kv, p.Ct) && !wide_check(wa(p.d, p.d, p.ks_wo), p.wv_split, p.Smax) &&
-         !wide_check(wa(p.d, p.fd, p.ks_ww2), p.wv_split, p.Smax) &&
-         !wide_check(wa(p.d, p.d, p.ks_wout), p.wv_split, p.Smax) && !wide_check(wa(p.d, p.d, p.H), 4, p.Ct) &&
+  p.ok = p.ws[0].ok && p.xnb > 0 &&
          (size_t)3 * p.KD * p.hd * 2 + (size_t)p.KD * p.KD * 4 <= 64 * 1024;   // self attention's LDS
 }
 
@@ -832,170 +884,218 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
 // The launches of block l for a wide group (every chunk expert in each launch, Rg requests): QKV,
 // self attention, O, residual, folded cross attention (in subgroups of two requests), residual,
 // W1, W2, residual.
-int block_pass_wide(const Plan& p, const cfh::ExpertLayout& L, const WS& w, const void* const* experts, int l,
-                    int Rg, hipStream_t st) {
-  const int d = p.d, fd = p.fd, NL = p.NL, nch = p.nch, Cg = Rg * p.C;
+// One request group of a wide launch sequence: its workspace, its requests [g0, g0 + Rg) of the
+// batch and their context rows.
+struct GroupRun {
+  WS w;
+  int g0, Rg;
+  const h16* ctx;
+};
+
+// The launches of block l for `ng` request groups (one, or two whose entries share every launch:
+// entry g * nch + c is expert c of group g, and `WArgs::pair` runs the two groups' workgroups of a
+// weight unit side by side).
+int block_pass_wide(const Plan& p, const WideShape& sh, const cfh::ExpertLayout& L, const GroupRun* gr, int ng,
+                    const void* const* experts, int l, hipStream_t st) {
+  const int d = p.d, fd = p.fd, NL = p.NL, nch = p.nch, nex = ng * nch;
   auto PTR = [&](int c, size_t off) { return (const char*)experts[c] + off; };
   const size_t B = L.blk0 + (size_t)l * L.blkstride;
-  auto S_of = [&](int c) { return Rg * (c + 1) * p.CS; };
+  auto S_of = [&](int g, int c) { return gr[g].Rg * (c + 1) * p.CS; };
   auto Sr_of = [&](int c) { return (c + 1) * p.CS; };
   int rc;
   auto wargs = [&](int N, int K, int ks) {
     WArgs a = {};
-    a.nex = nch; a.N = N; a.K = K; a.ks = ks;
+    a.nex = nex; a.N = N; a.K = K; a.ks = ks; a.pair = ng > 1;
     return a;
   };
   // QKV: q, k, v = fp16(LN_self(x) W_in^T + b_in)
   {
     WArgs a = wargs(3 * d, d, 1);
-    for (int c = 0; c < nch; ++c) {
-      WEx& x = a.ex[c];
-      x.w = (const h16x8*)PTR(c, B + L.qkv); x.a = w.abuf[c]; x.lda = d; x.bias = (const h16*)PTR(c, B + L.qkv_b);
-      x.out = w.qkv[c]; x.S = S_of(c);
-    }
-    if ((rc = launch_wide<E_BIAS16>(a, p.wv_qkv, st))) return rc;
+    for (int g = 0; g < ng; ++g)
+      for (int c = 0; c < nch; ++c) {
+        WEx& x = a.ex[g * nch + c];
+        x.w = (const h16x8*)PTR(c, B + L.qkv); x.a = gr[g].w.abuf[c]; x.lda = d;
+        x.bias = (const h16*)PTR(c, B + L.qkv_b); x.out = gr[g].w.qkv[c]; x.S = S_of(g, c);
+      }
+    if ((rc = launch_wide<E_BIAS16>(a, sh.wv_qkv, st))) return rc;
   }
   // causal self attention of every (request, head), into the LN rows' buffer (free until the residual)
   {
     SelfArgs sa = {};
-    sa.nex = nch; sa.R = Rg; sa.H = p.H; sa.d = d; sa.hd = p.hd;
-    for (int c = 0; c < nch; ++c) { sa.qkv[c] = w.qkv[c]; sa.out[c] = w.abuf[c]; sa.S[c] = S_of(c); sa.Sr[c] = Sr_of(c); }
+    sa.nex = nex; sa.H = p.H; sa.d = d; sa.hd = p.hd;
+    for (int g = 0; g < ng; ++g) {
+      sa.R = std::max(sa.R, gr[g].Rg);
+      for (int c = 0; c < nch; ++c) {
+        const int e = g * nch + c;
+        sa.qkv[e] = gr[g].w.qkv[c]; sa.out[e] = gr[g].w.abuf[c]; sa.S[e] = S_of(g, c); sa.Sr[e] = Sr_of(c);
+      }
+    }
     if ((rc = launch_self_attn(sa, st))) return rc;
   }
   // O: out_proj, split-K partials
   {
-    WArgs a = wargs(d, d, p.ks_wo);
-    for (int c = 0; c < nch; ++c) {
-      WEx& x = a.ex[c];
-      x.w = (const h16x8*)PTR(c, B + L.o); x.a = w.abuf[c]; x.lda = d; x.out = w.P[c]; x.S = S_of(c);
-    }
-    if ((rc = launch_wide<E_PART>(a, p.wv_split, st))) return rc;
+    WArgs a = wargs(d, d, sh.ks_wo);
+    for (int g = 0; g < ng; ++g)
+      for (int c = 0; c < nch; ++c) {
+        WEx& x = a.ex[g * nch + c];
+        x.w = (const h16x8*)PTR(c, B + L.o); x.a = gr[g].w.abuf[c]; x.lda = d; x.out = gr[g].w.P[c];
+        x.S = S_of(g, c);
+      }
+    if ((rc = launch_wide<E_PART>(a, sh.wv_split, st))) return rc;
   }
   ResArgs r = {};
-  r.nex = nch; r.d = d; r.mode = p.res_mode;
-  for (int c = 0; c < nch; ++c) { r.x[c] = w.x[c]; r.P[c] = w.P[c]; r.a[c] = w.abuf[c]; r.rows[c] = S_of(c); }
+  r.nex = nex; r.d = d; r.mode = p.res_mode;
+  for (int g = 0; g < ng; ++g)
+    for (int c = 0; c < nch; ++c) {
+      const int e = g * nch + c;
+      r.x[e] = gr[g].w.x[c]; r.P[e] = gr[g].w.P[c]; r.a[e] = gr[g].w.abuf[c]; r.rows[e] = S_of(g, c);
+    }
+  auto res_params = [&](size_t bias_off, size_t g_off, size_t b_off) {
+    for (int g = 0; g < ng; ++g)
+      for (int c = 0; c < nch; ++c) {
+        const int e = g * nch + c;
+        r.bias[e] = (const h16*)PTR(c, bias_off);
+        r.g[e] = (const h16*)PTR(c, g_off); r.b[e] = (const h16*)PTR(c, b_off);
+      }
+  };
   // residual + LN_cross (as the folded cross attention's operand image)
-  r.ks = p.ks_wo;
-  for (int c = 0; c < nch; ++c) {
-    r.bias[c] = (const h16*)PTR(c, B + L.o_b);
-    r.g[c] = (const h16*)PTR(c, B + L.xn_w); r.b[c] = (const h16*)PTR(c, B + L.xn_b);
-  }
+  r.ks = sh.ks_wo;
+  res_params(B + L.o_b, B + L.xn_w, B + L.xn_b);
   r.pack = 1;
   if ((rc = launch_res(r, st))) return rc;
   r.pack = 0;
   // folded cross attention, two requests a subgroup
   {
     XattArgs x = {};
-    x.nex = nch; x.d = d; x.H = p.H; x.C = Cg; x.Cq = p.C; x.nb = p.xnb; x.scale = 1.0f / sqrtf((float)p.hd);
-    x.nsg = (Rg + 1) / 2; x.Csg = 2 * p.C;
-    const size_t per_l = (size_t)p.H * Cg * d;
-    for (int c = 0; c < nch; ++c) {
-      x.xn[c] = w.abuf[c]; x.A[c] = w.fa[c] + (size_t)l * per_l; x.Bf[c] = w.fb[c] + (size_t)l * per_l;
-      x.sb[c] = w.fsb[c] + (size_t)l * p.H * Cg;
-      x.out[c] = w.P[c]; x.S[c] = S_of(c); x.Sr[c] = Sr_of(c); x.Ssg[c] = 2 * Sr_of(c);
+    x.nex = nex; x.d = d; x.H = p.H; x.Cq = p.C; x.nb = p.xnb; x.scale = 1.0f / sqrtf((float)p.hd);
+    x.Csg = 2 * p.C;
+    for (int g = 0; g < ng; ++g) {
+      const int Cg = gr[g].Rg * p.C;
+      const size_t per_l = (size_t)p.H * Cg * d;
+      x.C = std::max(x.C, Cg);
+      x.nsg = std::max(x.nsg, (gr[g].Rg + 1) / 2);
+      for (int c = 0; c < nch; ++c) {
+        const int e = g * nch + c;
+        const WS& w = gr[g].w;
+        x.xn[e] = w.abuf[c]; x.A[e] = w.fa[c] + (size_t)l * per_l; x.Bf[e] = w.fb[c] + (size_t)l * per_l;
+        x.sb[e] = w.fsb[c] + (size_t)l * p.H * Cg;
+        x.out[e] = w.P[c]; x.S[e] = S_of(g, c); x.Sr[e] = Sr_of(c); x.Ssg[e] = 2 * Sr_of(c); x.Ce[e] = Cg;
+      }
     }
     if ((rc = launch_xattn(x, st))) return rc;
   }
   // residual + LN_ffn (one partial per head)
   r.ks = p.H;
-  for (int c = 0; c < nch; ++c) {
-    r.bias[c] = (const h16*)PTR(c, B + L.oc_b);
-    r.g[c] = (const h16*)PTR(c, B + L.fn_w); r.b[c] = (const h16*)PTR(c, B + L.fn_b);
-  }
+  res_params(B + L.oc_b, B + L.fn_w, B + L.fn_b);
   if ((rc = launch_res(r, st))) return rc;
   // W1: g = fp16(gelu(LN_ffn(x) W1^T + b1))
   {
     WArgs a = wargs(fd, d, 1);
     a.gelu_r16 = p.res_mode == RES_ADD16;
-    for (int c = 0; c < nch; ++c) {
-      WEx& x = a.ex[c];
-      x.w = (const h16x8*)PTR(c, B + L.w1); x.a = w.abuf[c]; x.lda = d; x.bias = (const h16*)PTR(c, B + L.w1_b);
-      x.out = w.g[c]; x.S = S_of(c);
-    }
-    if ((rc = launch_wide<E_GELU16>(a, p.wv_w1, st))) return rc;
+    for (int g = 0; g < ng; ++g)
+      for (int c = 0; c < nch; ++c) {
+        WEx& x = a.ex[g * nch + c];
+        x.w = (const h16x8*)PTR(c, B + L.w1); x.a = gr[g].w.abuf[c]; x.lda = d;
+        x.bias = (const h16*)PTR(c, B + L.w1_b); x.out = gr[g].w.g[c]; x.S = S_of(g, c);
+      }
+    if ((rc = launch_wide<E_GELU16>(a, sh.wv_w1, st))) return rc;
   }
   // W2: split-K partials
   {
-    WArgs a = wargs(d, fd, p.ks_ww2);
-    for (int c = 0; c < nch; ++c) {
-      WEx& x = a.ex[c];
-      x.w = (const h16x8*)PTR(c, B + L.w2); x.a = w.g[c]; x.lda = fd; x.out = w.P[c]; x.S = S_of(c);
-    }
-    if ((rc = launch_wide<E_PART>(a, p.wv_split, st))) return rc;
+    WArgs a = wargs(d, fd, sh.ks_ww2);
+    for (int g = 0; g < ng; ++g)
+      for (int c = 0; c < nch; ++c) {
+        WEx& x = a.ex[g * nch + c];
+        x.w = (const h16x8*)PTR(c, B + L.w2); x.a = gr[g].w.g[c]; x.lda = fd; x.out = gr[g].w.P[c];
+        x.S = S_of(g, c);
+      }
+    if ((rc = launch_wide<E_PART>(a, sh.wv_split, st))) return rc;
   }
   // residual + LayerNorm of the next block (out_norm after the last block)
-  r.ks = p.ks_ww2;
-  for (int c = 0; c < nch; ++c) {
-    r.bias[c] = (const h16*)PTR(c, B + L.w2_b);
-    if (l + 1 < NL) {
-      const size_t Bn = L.blk0 + (size_t)(l + 1) * L.blkstride;
-      r.g[c] = (const h16*)PTR(c, Bn + L.sn_w); r.b[c] = (const h16*)PTR(c, Bn + L.sn_b);
-    } else {
-      r.g[c] = (const h16*)PTR(c, L.on_w); r.b[c] = (const h16*)PTR(c, L.on_b);
-    }
+  r.ks = sh.ks_ww2;
+  if (l + 1 < NL) {
+    const size_t Bn = L.blk0 + (size_t)(l + 1) * L.blkstride;
+    res_params(B + L.w2_b, Bn + L.sn_w, Bn + L.sn_b);
+  } else {
+    res_params(B + L.w2_b, L.on_w, L.on_b);
   }
   return launch_res(r, st);
 }
 
-// Per-draft launches of a wide group: the context rows' LayerNorm of every block, the cross K/V
+// Per-draft launches of `ng` wide groups: the context rows' LayerNorm of every block, the cross K/V
 // of every block (context rows of every request as rows of one stream), and the folded factors.
-int per_draft_wide(const Plan& p, const cfh::ExpertLayout& L, const WS& w, const void* const* experts,
-                   const h16* ctx_b, int Rg, hipStream_t st) {
-  const int d = p.d, NL = p.NL, nch = p.nch, Cg = Rg * p.C;
+int per_draft_wide(const Plan& p, const WideShape& sh, const cfh::ExpertLayout& L, const GroupRun* gr, int ng,
+                   const void* const* experts, hipStream_t st) {
+  const int d = p.d, NL = p.NL, nch = p.nch;
   auto PTR = [&](int c, size_t off) { return (const char*)experts[c] + off; };
   auto BLK = [&](int l) { return L.blk0 + (size_t)l * L.blkstride; };
   int rc;
-  {
+  for (int g = 0; g < ng; ++g) {
     CtxLnArgs a = {};
-    a.ctx = ctx_b; a.mom = w.ctx_mom; a.vstride = (long long)L.blkstride; a.nex = nch; a.nl = NL; a.Ct = Cg; a.d = d;
+    a.ctx = gr[g].ctx; a.mom = gr[g].w.ctx_mom; a.vstride = (long long)L.blkstride; a.nex = nch; a.nl = NL;
+    a.Ct = gr[g].Rg * p.C; a.d = d;
     for (int c = 0; c < nch; ++c) {
       a.g0[c] = (const h16*)PTR(c, BLK(0) + L.cn_w); a.b0[c] = (const h16*)PTR(c, BLK(0) + L.cn_b);
-      a.out[c] = w.cln[c];
+      a.out[c] = gr[g].w.cln[c];
     }
     hipLaunchKernelGGL(k_ctx_ln, dim3(512), dim3(256), 0, st, a);
     CFH_LAUNCH_CHECK();
   }
-  // cross K/V = fp16(LN_c(ctx) W_kv^T + b_kv) as [2][Cg][d] per block, four weight sets a launch
-  for (int i0 = 0; i0 < nch * NL; i0 += 4) {
+  // cross K/V = fp16(LN_c(ctx) W_kv^T + b_kv) as [2][Cg][d] per block: per launch `per` weight sets
+  // (expert, block), each once per group
+  const int per = std::min(4 / ng, nch * NL);
+  for (int i0 = 0; i0 < nch * NL; i0 += per) {
     WArgs a = {};
     a.N = 2 * d; a.K = d; a.ks = 1;
-    for (int i = i0; i < std::min(nch * NL, i0 + 4); ++i) {
-      const int c = i / NL, l = i - c * NL;
-      WEx& x = a.ex[a.nex++];
-      x.w = (const h16x8*)PTR(c, BLK(l) + L.kv); x.a = w.cln[c] + (size_t)l * Cg * d; x.lda = d;
-      x.bias = (const h16*)PTR(c, BLK(l) + L.kv_b); x.out = w.kvc[c] + (size_t)l * 2 * Cg * d; x.S = Cg;
-      x.nsplit = d;
+    const int n = std::min(per, nch * NL - i0);
+    a.pair = ng > 1;
+    for (int g = 0; g < ng; ++g)
+      for (int i = i0; i < i0 + n; ++i) {
+        const int c = i / NL, l = i - c * NL, Cg = gr[g].Rg * p.C;
+        WEx& x = a.ex[a.nex++];
+        x.w = (const h16x8*)PTR(c, BLK(l) + L.kv); x.a = gr[g].w.cln[c] + (size_t)l * Cg * d; x.lda = d;
+        x.bias = (const h16*)PTR(c, BLK(l) + L.kv_b); x.out = gr[g].w.kvc[c] + (size_t)l * 2 * Cg * d; x.S = Cg;
+        x.nsplit = d;
+      }
+    if (a.pair && wide_check(a, sh.wv_kv, WMAXR)) a.pair = 0;   // (an odd tail: no side-by-side runs)
+    if ((rc = launch_wide<E_BIAS16>(a, sh.wv_kv, st))) return rc;
+  }
+  for (int g = 0; g < ng; ++g) {
+    const int Cg = gr[g].Rg * p.C;
+    XbiasArgs xb = {};
+    xb.nex = nch; xb.nl = NL; xb.d = d; xb.H = p.H; xb.C = Cg;
+    xb.kstride = (long long)2 * Cg * d; xb.bstride = (long long)L.blkstride;
+    for (int c = 0; c < nch; ++c) {
+      xb.K[c] = gr[g].w.kvc[c]; xb.bq[c] = (const h16*)PTR(c, BLK(0) + L.qc_b); xb.sb[c] = gr[g].w.fsb[c];
     }
-    if ((rc = launch_wide<E_BIAS16>(a, p.wv_kv, st))) return rc;
+    hipLaunchKernelGGL(k_xbias, dim3(nch * NL, (p.H * Cg + 63) / 64), dim3(1024), 0, st, xb);
+    CFH_LAUNCH_CHECK();
   }
-  XbiasArgs xb = {};
-  xb.nex = nch; xb.nl = NL; xb.d = d; xb.H = p.H; xb.C = Cg;
-  xb.kstride = (long long)2 * Cg * d; xb.bstride = (long long)L.blkstride;
-  for (int c = 0; c < nch; ++c) {
-    xb.K[c] = w.kvc[c]; xb.bq[c] = (const h16*)PTR(c, BLK(0) + L.qc_b); xb.sb[c] = w.fsb[c];
-  }
-  hipLaunchKernelGGL(k_xbias, dim3(nch * NL, (p.H * Cg + 63) / 64), dim3(1024), 0, st, xb);
-  CFH_LAUNCH_CHECK();
   // A_h = Wq_h^T K_h^T (the transposed query weight against the K rows) and B_h = Wo_h V_h, split-K
   // by head: the partial of k-split h, rounded to fp16, is head h's factor
-  const size_t per_l = (size_t)p.H * Cg * d;
   for (int l = 0; l < NL; ++l)
-    for (int half = 0; half < 2; ++half) {
-      if (half == 1 && 2 * nch <= 4) break;
+    for (int part = 0; part < 2; ++part) {
+      // both parts of every expert in one launch when they fit the launch's four entries
+      const bool both = 2 * nch * ng <= 4;
+      if (both && part == 1) break;
       WArgs a = {};
-      a.N = d; a.K = d; a.ks = p.H;
-      for (int part = 0; part < 2; ++part) {
-        if (2 * nch > 4 && part != half) continue;
-        for (int c = 0; c < nch; ++c) {
-          WEx& x = a.ex[a.nex++];
-          const h16* kv = w.kvc[c] + (size_t)l * 2 * Cg * d;
-          x.w = (const h16x8*)PTR(c, BLK(l) + (part == 0 ? L.qc : L.oc));
-          x.a = part == 0 ? kv : kv + (size_t)Cg * d;
-          x.lda = d; x.S = Cg; x.hrows = Cg;
-          x.out = (part == 0 ? w.fa[c] : w.fb[c]) + (size_t)l * per_l;
-          x.pack = part == 0;
+      a.N = d; a.K = d; a.ks = p.H; a.pair = ng > 1;
+      for (int g = 0; g < ng; ++g)
+        for (int q = 0; q < 2; ++q) {
+          if (!both && q != part) continue;
+          const int Cg = gr[g].Rg * p.C;
+          const size_t per_l = (size_t)p.H * Cg * d;
+          for (int c = 0; c < nch; ++c) {
+            WEx& x = a.ex[a.nex++];
+            const h16* kv = gr[g].w.kvc[c] + (size_t)l * 2 * Cg * d;
+            x.w = (const h16x8*)PTR(c, BLK(l) + (q == 0 ? L.qc : L.oc));
+            x.a = q == 0 ? kv : kv + (size_t)Cg * d;
+            x.lda = d; x.S = Cg; x.hrows = Cg;
+            x.out = (q == 0 ? gr[g].w.fa[c] : gr[g].w.fb[c]) + (size_t)l * per_l;
+            x.pack = q == 0;
+          }
         }
-      }
+      if (a.pair && wide_check(a, 4, WMAXR)) a.pair = 0;
       if ((rc = launch_wide<E_PART16>(a, 4, st))) return rc;
     }
   return CFH_OK;
@@ -1137,6 +1237,85 @@ int release_companions(hipStream_t st) {
 // The whole draft of `batch` requests on workspace ws (the plan's carve() layout): per request the
 // per-draft launches, then E Euler steps of L block passes and the OUT / ROWS step.
 // anchor: null, or the anchored latent drafter's anchor rows [n_chunks][batch][d] fp16 (cfh_flow_anchor).
+// Bytes between the two groups' workspaces of a paired wide launch sequence.
+size_t group_ws_stride(const Plan& p) { return cfh::align256(carve(p, nullptr).total); }
+
+// Workspace of a batch: one group's, or two groups' when the wide path pairs them.
+size_t flow_ws_bytes(const cfh_flow_dims* dm, int batch) {
+  const Plan p = make_plan(dm, group_size(dm, batch));
+  if (!p.ok) return 0;
+  if (p.wide && (batch + p.R - 1) / p.R > 1 && p.ws[1].ok) return 2 * group_ws_stride(p);
+  return carve(p, nullptr).total;
+}
+
+// The wide path after the time embeddings (w0: the first group's workspace, which holds them):
+// groups of p.R requests, two at a time when the batch has several and the paired launch shapes
+// fit (every launch then covers both groups' rows, the second group's workspace after the first's).
+int integrate_wide(const Plan& p, const cfh_flow_dims* dm, const cfh::ExpertLayout& L, const void* const* experts,
+                   const void* ctx, void* z_out, char* ws, const WS& w0, int batch, hipStream_t st,
+                   const void* anchor) {
+  const int d = p.d, CS = p.CS, E = p.E, NL = p.NL, C = p.C, KD = p.KD, nch = p.nch;
+  auto PTR = [&](int c, size_t off) { return (const char*)experts[c] + off; };
+  auto BLK = [&](int l) { return L.blk0 + (size_t)l * L.blkstride; };
+  const int ngroups = (batch + p.R - 1) / p.R;
+  const int gp = ngroups > 1 && p.ws[1].ok ? 2 : 1;
+  const WS w1 = gp > 1 ? carve(p, ws + group_ws_stride(p)) : w0;
+  int rc;
+  // the ROWS launch of a group: z0 and the step-0 rows (s < 0), or step s's Euler update
+  auto rows = [&](const GroupRun& G, int s, int ks_out) {
+    RowsArgs r = {};
+    r.ctx = G.ctx; r.ctx_mom = G.w.ctx_mom; r.z = G.w.z; r.z_out = (h16*)z_out + (size_t)G.g0 * KD * d;
+    r.d = d; r.C = C; r.CS = CS; r.nch = nch; r.KD = KD; r.R = G.Rg; r.out_all = 1; r.only = -1;
+    if (s < 0) {
+      r.euler = 0; r.last = 0; r.init = dm->init_mode;
+    } else {
+      r.euler = 1; r.last = s + 1 == E; r.ks = ks_out; r.dt = 1.0f / (float)E;
+    }
+    for (int c = 0; c < nch; ++c) {
+      r.x[c] = G.w.x[c]; r.pos[c] = (const h16*)PTR(c, L.pos);
+      r.tau[c] = w0.tau[c] + (s < 0 ? 0 : (size_t)(s + 1 < E ? s + 1 : s) * d);
+      r.g[c] = (const h16*)PTR(c, BLK(0) + L.sn_w); r.b[c] = (const h16*)PTR(c, BLK(0) + L.sn_b);
+      r.a[c] = G.w.abuf[c];
+      r.anchor[c] = anchor ? (const h16*)anchor + ((size_t)c * batch + G.g0) * d : nullptr;
+      if (s >= 0) { r.Pout[c] = G.w.P[c]; r.bout[c] = (const h16*)PTR(c, L.out_b); }
+    }
+    hipLaunchKernelGGL(k_rows, dim3(G.Rg * KD), dim3(ROWT), 0, st, r);
+    CFH_LAUNCH_CHECK();
+    return CFH_OK;
+  };
+  for (int q0 = 0; q0 < ngroups; q0 += gp) {
+    GroupRun gr[2];
+    const int ng = std::min(gp, ngroups - q0);
+    for (int g = 0; g < ng; ++g) {
+      gr[g].w = g == 0 ? w0 : w1;
+      gr[g].g0 = (q0 + g) * p.R;
+      gr[g].Rg = std::min(p.R, batch - gr[g].g0);
+      gr[g].ctx = (const h16*)ctx + (size_t)gr[g].g0 * C * d;
+    }
+    const WideShape& sh = p.ws[ng - 1];
+    for (int g = 0; g < ng; ++g)
+      if ((rc = rows(gr[g], -1, 0))) return rc;
+    if ((rc = per_draft_wide(p, sh, L, gr, ng, experts, st))) return rc;
+    for (int s = 0; s < E; ++s) {
+      for (int l = 0; l < NL; ++l)
+        if ((rc = block_pass_wide(p, sh, L, gr, ng, experts, l, st))) return rc;
+      // OUT: every row of every expert (the current chunk's rows are not contiguous)
+      WArgs a = {};
+      a.nex = ng * nch; a.N = d; a.K = d; a.ks = sh.ks_wout; a.pair = ng > 1;
+      for (int g = 0; g < ng; ++g)
+        for (int c = 0; c < nch; ++c) {
+          WEx& x = a.ex[g * nch + c];
+          x.w = (const h16x8*)PTR(c, L.out); x.a = gr[g].w.abuf[c]; x.lda = d; x.out = gr[g].w.P[c];
+          x.S = gr[g].Rg * (c + 1) * CS;
+        }
+      if ((rc = launch_wide<E_PART>(a, sh.wv_split, st))) return rc;
+      for (int g = 0; g < ng; ++g)
+        if ((rc = rows(gr[g], s, sh.ks_wout))) return rc;
+    }
+  }
+  return CFH_OK;
+}
+
 int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* experts, const void* ctx, void* z_out,
               void* ws_ptr, int batch, hipStream_t st, bool may_create = true, const void* anchor = nullptr) {
   // Under stream capture every expert stays on the caller's stream: a replayed graph of the
@@ -1182,6 +1361,7 @@ int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* expert
     hipLaunchKernelGGL(k_reduce, dim3(256), dim3(256), 0, st, r);
     CFH_LAUNCH_CHECK();
   }
+  if (p.wide) return integrate_wide(p, dm, L, experts, ctx, z_out, (char*)ws_ptr, w, batch, st, anchor);
 
   for (int g0 = 0; g0 < batch; g0 += p.R) {
     const int Rg = std::min(p.R, batch - g0), Cg = Rg * C;     // this group's requests, context rows
@@ -1204,11 +1384,8 @@ int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* expert
       hipLaunchKernelGGL(k_rows, dim3(Rg * KD), dim3(ROWT), 0, st, r);
       CFH_LAUNCH_CHECK();
     }
-    if (p.wide) {
-      if ((rc = per_draft_wide(p, L, w, experts, ctx_b, Rg, st))) return rc;
-    }
     // ---- cross K/V of every block (once per draft), the group's context rows together
-    if (!p.wide) {
+    {
       GemvArgs a = {};
       a.nex = nch; a.nl = NL; a.ks = p.ks_kv; a.tiles = 2 * d / 16; a.N = 2 * d; a.K = d; a.E = E;
       a.wstride = (long long)L.blkstride; a.vstride = (long long)L.blkstride;
@@ -1238,7 +1415,7 @@ int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* expert
     // transposed query weight against the K rows, B_h = Wo_h V_h from the out-projection against
     // the V rows, each split-K by head (the partial of head h, rounded to fp16, is the factor);
     // the rows of the group's requests side by side
-    if (p.fold && !p.wide) {
+    if (p.fold) {
       XbiasArgs xb = {};
       xb.nex = nch; xb.nl = NL; xb.d = d; xb.H = p.H; xb.C = Cg;
       xb.kstride = (long long)2 * Cg * d; xb.bstride = (long long)L.blkstride;
@@ -1291,7 +1468,7 @@ int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* expert
     }
     auto rows_args = [&](int s, int only) {
       RowsArgs r = {};
-      r.ctx = ctx_b; r.z = w.z; r.z_out = zo_b; r.euler = 1; r.last = (s + 1 == E); r.ks = p.wide ? p.ks_wout : p.ks_out;
+      r.ctx = ctx_b; r.z = w.z; r.z_out = zo_b; r.euler = 1; r.last = (s + 1 == E); r.ks = p.ks_out;
       r.dt = 1.0f / (float)E; r.d = d; r.C = C; r.CS = CS; r.nch = nch; r.KD = KD; r.R = Rg; r.out_all = p.R > 1;
       r.only = only;
       for (int c = 0; c < nch; ++c) {
@@ -1325,26 +1502,7 @@ int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* expert
       }
       return launch_stream<S_BUF, E_PART>(a, p.R == 1 ? CS : p.Smax, sc);
     };
-    // OUT of a wide group: every row of every expert (the current chunk's rows are not contiguous)
-    auto out_wide = [&]() {
-      WArgs a = {};
-      a.nex = nch; a.N = d; a.K = d; a.ks = p.ks_wout;
-      for (int c = 0; c < nch; ++c) {
-        WEx& x = a.ex[c];
-        x.w = (const h16x8*)PTR(c, L.out); x.a = w.abuf[c]; x.lda = d; x.out = w.P[c]; x.S = Rg * (c + 1) * CS;
-      }
-      return launch_wide<E_PART>(a, p.wv_split, st);
-    };
     for (int s = 0; s < E; ++s) {
-      if (p.wide) {
-        for (int l = 0; l < NL; ++l)
-          if ((rc = block_pass_wide(p, L, w, experts, l, Rg, st))) return rc;
-        if ((rc = out_wide())) return rc;
-        const RowsArgs r = rows_args(s, -1);
-        hipLaunchKernelGGL(k_rows, dim3(Rg * KD), dim3(ROWT), 0, st, r);
-        CFH_LAUNCH_CHECK();
-        continue;
-      }
       if (!p.conc) {
         for (int l = 0; l < NL; ++l)
           if ((rc = block_pass(p, L, w, experts, l, Rg, st, 0, nch))) return rc;
@@ -1493,14 +1651,14 @@ int cfh_caps(const cfh_flow_dims* dims, int batch, int64_t* ws_bytes) {
   if (dims->d > ROWT * ROWE || dims->draft_length > MAXR) return CFH_E_UNSUPPORTED;
   const Plan p = make_plan(dims, group_size(dims, batch));
   if (!p.ok) return CFH_E_UNSUPPORTED;
-  // the workspace of every batch up to `batch`: the group sizes 1, 2 (narrow) and the widest group
-  // (wide group sizes grow with the batch up to WMAXR / draft_length requests)
-  size_t total = carve(p, nullptr).total;
-  const int wide_max = std::min(batch, WMAXR / dims->draft_length);
-  for (int b : {1, 2, wide_max}) {
+  // the workspace of every batch up to `batch`: the group sizes 1, 2 (narrow), the widest single
+  // group, two of them (wide group sizes grow with the batch up to WMAXR / draft_length requests;
+  // a batch of several groups runs them two at a time), and the batch itself
+  size_t total = flow_ws_bytes(dims, batch);
+  const int wide_max = WMAXR / dims->draft_length;
+  for (int b : {1, 2, wide_max, 2 * wide_max}) {
     if (b > batch) continue;
-    const Plan q = make_plan(dims, group_size(dims, b));
-    if (q.ok) total = std::max(total, carve(q, nullptr).total);
+    total = std::max(total, flow_ws_bytes(dims, b));
   }
   if (ws_bytes) *ws_bytes = (int64_t)total;
   return CFH_OK;

@@ -178,7 +178,8 @@ def test_flow_latent_widths_match_oracle(cuda, d, heads, layers, steps):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("d,B,layers", [(512, 2, 2), (512, 5, 1), (640, 3, 1), (1024, 2, 2), (4096, 2, 1),
-                                        (1024, 3, 2), (1024, 16, 1), (1024, 21, 1), (2048, 8, 1), (4096, 5, 1)])
+                                        (1024, 3, 2), (1024, 16, 1), (1024, 21, 1), (1024, 40, 1), (2048, 8, 1),
+                                        (4096, 5, 1)])
 def test_packed_batch_matches_oracle_per_request(cuda, d, B, layers):
     """A batch drafts in groups whose rows share every weight stream: two requests a 16-row tile
     (attention masked to each request's own rows and context), or, above two requests where the
@@ -187,7 +188,8 @@ def test_packed_batch_matches_oracle_per_request(cuda, d, B, layers):
     against the oracle on its own context, and against the same request drafted alone in the same
     numerics.  d = 640 runs the unfolded cross attention (head width 80), the others the folded
     one; B = 5 and 3 at d <= 640 end with a group of one; B = 21 at d = 1024 runs two wide groups
-    (11 and 10 requests), B = 3 at d = 1024 one wide group of an odd request count."""
+    (11 and 10 requests) side by side in every launch, B = 40 a pair of 14-request groups then one
+    of 12, B = 3 at d = 1024 one wide group of an odd request count."""
     cfg = flownet(d, layers=layers, flow_steps=2)
     W = _flow_weights(cfg, seed=13)
     ctx = synthetic_context(B, cfg.context_size, d, seed=21)

@@ -51,7 +51,19 @@ struct WArgs {
   int gelu_r16;        // E_GELU16: as SArgs
   int pair;            // entries e and e + nex/2 stream the same weights (two request groups of one
                        // expert): their workgroups for a unit run side by side on one XCD
+  int map;             // workgroup order (set by launch_wide): MAP_PLAIN, MAP_PAIR or MAP_XCD
 };
+
+// Workgroup -> (entry, k-split, tile group) orders.  Workgroups go to the 8 XCDs round robin
+// (workgroup b to XCD b % 8), each XCD with its own L2.
+//   MAP_PLAIN: entry-major.
+//   MAP_PAIR:  workgroups b and b + 8 take the same unit of entries e and e + nex/2.
+//   MAP_XCD:   (split-K) XCD x takes every unit of the (entry, k-split) combinations x, x + 8, ...:
+//              each XCD reads the operand rows of its own K ranges only, instead of every XCD
+//              reading all of them (W2's 128 rows x 24576 columns are 6.3 MB an entry), and with
+//              nex/2 * ks a multiple of 8 the two groups' combinations of one weight range share
+//              an XCD.
+enum { MAP_PLAIN = 0, MAP_PAIR = 1, MAP_XCD = 2 };
 
 template <int EPI, int NG, int WV>
 __global__ void __launch_bounds__(WV * 64) k_wide(WArgs a) {
@@ -59,17 +71,27 @@ __global__ void __launch_bounds__(WV * 64) k_wide(WArgs a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   int b = blockIdx.x;
   const int per_ex = a.ks * a.wg_per_kc;
-  if (a.pair) {
-    // workgroups b and b + 8 (dispatched together, on the same XCD: workgroups go to the XCDs
-    // round robin) take the same unit of the two groups, so the second reads the weight fragments
-    // the first has just brought into the XCD's L2 instead of from HBM
-    const int lo = b & 7, hi = b >> 3;
-    b = (((hi >> 1) << 3) | lo) + (hi & 1) * (a.nex / 2) * per_ex;
+  int e, kc, tg;
+  if (a.map == MAP_XCD) {
+    const int x = b & 7, j = b >> 3;
+    const int cl = j / a.wg_per_kc;
+    const int combo = x + 8 * cl;
+    tg = j - cl * a.wg_per_kc;
+    e = combo / a.ks;
+    kc = combo - e * a.ks;
+  } else {
+    if (a.map == MAP_PAIR) {
+      // workgroups b and b + 8 (dispatched together, on the same XCD) take the same unit of the
+      // two groups, so the second reads the weight fragments the first has just brought into the
+      // XCD's L2 instead of from HBM
+      const int lo = b & 7, hi = b >> 3;
+      b = (((hi >> 1) << 3) | lo) + (hi & 1) * (a.nex / 2) * per_ex;
+    }
+    e = b / per_ex;
+    b -= e * per_ex;
+    kc = b / a.wg_per_kc;
+    tg = b - kc * a.wg_per_kc;
   }
-  const int e = b / per_ex;
-  b -= e * per_ex;
-  const int kc = b / a.wg_per_kc;
-  const int tg = b - kc * a.wg_per_kc;
   const WEx& ex = a.ex[e];
   const int S = ex.S;
   const int ksteps = a.K / 32;
@@ -275,6 +297,8 @@ int wide_wv(int tiles, int units) {
   return best;
 }
 
+inline bool wide_xcd_off() { return false; }
+
 template <int EPI>
 int launch_wide(const WArgs& a0, int wv, hipStream_t st) {
   WArgs a = a0;
@@ -284,6 +308,10 @@ int launch_wide(const WArgs& a0, int wv, hipStream_t st) {
   for (int e = 0; e < a.nex; ++e)
     if (a.ex[e].S < 1 || a.ex[e].lda < a.K || !a.ex[e].w || !a.ex[e].a || !a.ex[e].out) return CFH_E_INVALID;
   a.wg_per_kc = (a.N / 16) / (WT * wv);
+  if (a.ks > 1 && (a.nex * a.ks) % 8 == 0 && (!a.pair || ((a.nex / 2) * a.ks) % 8 == 0) && !wide_xcd_off())
+    a.map = MAP_XCD;
+  else
+    a.map = a.pair ? MAP_PAIR : MAP_PLAIN;
   const size_t lds = wide_lds(S_max);
   const int ng = (S_max + 15) / 16;
 #define CFH_WIDE(G)                                                                 \

@@ -976,10 +976,119 @@ __global__ void __launch_bounds__(256) k_path_out(PathOutArgs a) {
   }
 }
 
+// The path head's two MLP layers for up to PATH_CHUNK rows, each as one launch: one workgroup per
+// 16-column tile whose WK waves each stream 1/WK of K (PF fragments in flight), the wave sums
+// added in LDS, the epilogue applied in place of the separate partial-sum kernels:
+//   PG_GELU    g = fp16(gelu(fp16(acc + b)))                         (mlp.0 -> GELU)
+//   PG_PATHOUT hsum = fp16(pred[group(m)] + fp16(acc + b))             (mlp.3, then + the marginal hidden)
+// The activation rows are read straight from global memory by each lane (every workgroup reads the
+// same few rows, which stay in L2); lanes of rows past M re-read row M-1 and store nothing.
+enum { PG_GELU = 0, PG_PATHOUT = 1 };
+
+struct PathGemvArgs {
+  const h16x8* w;      // packed [N][K]
+  const h16* a;        // activation rows [M][K]
+  const h16* bias;     // [N]
+  h16* out;            // [M][N]
+  const h16* pred;     // PG_PATHOUT: the marginal hidden rows (row g at pred + g * pred_ld)
+  long long pred_ld;
+  int rows_per_pred;   // rows sharing one pred row (0: every row uses row 0)
+  int row0;            // the first row's index in the whole call (for the grouping)
+  int M, N, K;
+};
+
+template <int EPI, int WK, int PFK>
+__global__ void __launch_bounds__(WK * 64) k_path_gemv(PathGemvArgs g) {
+  __shared__ f32x4 red[WK][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = blockIdx.x;
+  const int ksteps = g.K / 32, per = ksteps / WK, s0 = wave * per;
+  const int row = lane & 15, kg = lane >> 4;
+  const h16* arow = g.a + (size_t)min(row, g.M - 1) * g.K + (size_t)s0 * 32 + kg * 8;
+  const h16x8* wp = g.w + ((size_t)t * ksteps + s0) * 64 + lane;
+  h16x8 bw[PFK], ba[PFK];
+#pragma unroll
+  for (int p = 0; p < PFK; ++p) {
+    bw[p] = __builtin_nontemporal_load(wp + (size_t)p * 64);
+    ba[p] = *(const h16x8*)(arow + p * 32);
+  }
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  int s = 0;
+  for (; s < per - PFK; s += PFK) {
+#pragma unroll
+    for (int p = 0; p < PFK; ++p) {
+      acc = mfma_f16(ba[p], bw[p], acc);
+      bw[p] = __builtin_nontemporal_load(wp + (size_t)(s + PFK + p) * 64);
+      ba[p] = *(const h16x8*)(arow + (s + PFK + p) * 32);
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < PFK; ++p) acc = mfma_f16(ba[p], bw[p], acc);
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+  f32x4 v = red[0][lane];
+#pragma unroll
+  for (int w = 1; w < WK; ++w) {
+    const f32x4 u = red[w][lane];
+    v[0] += u[0]; v[1] += u[1]; v[2] += u[2]; v[3] += u[3];
+  }
+  const int n = t * 16 + (lane & 15), rbase = 4 * (lane >> 4);
+  const float b = (float)g.bias[n];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int m = rbase + j;
+    if (m >= g.M) continue;
+    if constexpr (EPI == PG_GELU) {
+      g.out[(size_t)m * g.N + n] = (h16)gelu_erf(r16(v[j] + b));
+    } else {
+      const int grp = g.rows_per_pred > 0 ? (g.row0 + m) / g.rows_per_pred : 0;
+      g.out[(size_t)m * g.N + n] = (h16)((float)g.pred[(size_t)grp * g.pred_ld + n] + r16(v[j] + b));
+    }
+  }
+}
+
+// (WK, PF) of a path_gemv launch over `tiles` tiles and K: a whole number of PF-fragment blocks a
+// wave, and as close to 2048 waves as the choices allow; 0 if none fits.
+int path_gemv_shape(int tiles, int K, int* wk, int* pf) {
+  static const int cand[][2] = {{8, 8}, {4, 8}, {8, 4}, {4, 4}, {2, 8}, {2, 4}};
+  int best = -1;
+  long long best_waves = 0;
+  for (int i = 0; i < 6; ++i) {
+    const int w = cand[i][0], f = cand[i][1], steps = K / 32;
+    if (K % 32 || steps % w || (steps / w) % f || steps / w < f) continue;
+    const long long waves = (long long)tiles * w;
+    const bool better_fit = best < 0 || (best_waves < 2048 ? waves > best_waves : (waves >= 2048 && waves < best_waves));
+    if (better_fit) {
+      best = i;
+      best_waves = waves;
+    }
+  }
+  if (best < 0) return 0;
+  *wk = cand[best][0];
+  *pf = cand[best][1];
+  return 1;
+}
+
+template <int EPI>
+int launch_path_gemv(const PathGemvArgs& g, hipStream_t st) {
+  int wk = 0, pf = 0;
+  if (g.N % 16 || g.M < 1 || g.M > 16 || !path_gemv_shape(g.N / 16, g.K, &wk, &pf)) return CFH_E_UNSUPPORTED;
+  const dim3 grid((unsigned)(g.N / 16));
+#define CFH_PG(W, F) \
+  if (wk == W && pf == F) { hipLaunchKernelGGL((k_path_gemv<EPI, W, F>), grid, dim3(W * 64), 0, st, g); CFH_LAUNCH_CHECK(); return CFH_OK; }
+  CFH_PG(8, 8) CFH_PG(4, 8) CFH_PG(8, 4) CFH_PG(4, 4) CFH_PG(2, 8) CFH_PG(2, 4)
+#undef CFH_PG
+  return CFH_E_UNSUPPORTED;
+}
+
 struct PathPlan {
   int o_ks, up_ks, dn_ks;
+  bool fused;          // the MLP layers as two path_gemv launches (else split-K GEMVs + reductions)
   size_t off_P, off_a, off_up, off_g, off_dn, total;
 };
+
+inline bool path_unfused() { return false; }
 
 PathPlan path_plan(int M, int d, int ffn, int order) {
   PathPlan p;
@@ -987,6 +1096,8 @@ PathPlan path_plan(int M, int d, int ffn, int order) {
   p.o_ks = ksplit_for(order, d / 16, d, M);
   p.up_ks = ksplit_for(1, pf / 16, d, M);
   p.dn_ks = ksplit_for(1, d / 16, pf, M);
+  int wk, pfk;
+  p.fused = !path_unfused() && path_gemv_shape(pf / 16, d, &wk, &pfk) && path_gemv_shape(d / 16, pf, &wk, &pfk);
   size_t off = 0;
   auto take = [&](size_t bytes) {
     const size_t o = off;
@@ -1454,6 +1565,14 @@ static int path_chunk(const PathPlan& pp, const void* const* ph, int order, int 
   for (int j = 0; j < o; ++j) ps.bias[j] = (const h16*)bj[j];
   hipLaunchKernelGGL(k_path_sum, dim3(M), dim3(ROWT), 0, st, ps);
   CFH_LAUNCH_CHECK();
+  if (pp.fused) {
+    PathGemvArgs g = {};
+    g.w = W0; g.a = A; g.bias = b0; g.out = G; g.M = M; g.N = pf; g.K = d;
+    if ((rc = launch_path_gemv<PG_GELU>(g, st))) return rc;
+    g.w = W3; g.a = G; g.bias = b3; g.out = (h16*)hsum; g.N = d; g.K = pf;
+    g.pred = (const h16*)pred; g.pred_ld = pred_ld; g.rows_per_pred = rows_per_pred; g.row0 = row0;
+    return launch_path_gemv<PG_PATHOUT>(g, st);
+  }
   {
     GemvArgs a = {};
     a.nex = 1; a.nl = 1; a.ks = pp.up_ks; a.tiles = pf / 16; a.N = pf; a.K = d;

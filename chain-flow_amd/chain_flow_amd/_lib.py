@@ -80,6 +80,7 @@ SIGNATURES = {
     "cfh_path_ws_bytes": (_I64, [_I, _I, _I, _I]),
     "cfh_path_residual": (_I, [C.POINTER(_VP), _I, _I, _I, _VP, _I, _I, _VP, _VP, C.c_longlong, _I, _VP, _VP,
                                _VP]),
+    "cfh_beam_init": (_I, [_VP, _VP, _VP, _VP, _I, _I, _I, _I, _VP]),
     "cfh_beam_chain_step": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _VP]),
     "cfh_beam_tree_step": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _I, _VP]),
     "cfh_beam_backtrack": (_I, [_VP, _VP, _VP, _I, _I, _I, _VP, _VP]),

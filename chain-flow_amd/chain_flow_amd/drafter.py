@@ -142,16 +142,18 @@ class Drafter:
             pred = self.predict_hidden(ctx, known0)
         B, Kd, d = pred.shape
         steps = min(K + 1, Kd)
-        lastp = torch.full((B, W, order), -1, dtype=torch.int32, device=dev)
-        lastp[:, :, 0] = known0.to(dev, torch.int32).view(B, 1)
-        cum = torch.full((B, W), float("-inf"), dtype=torch.float32, device=dev)
-        cum[:, 0] = 0.0
+        L = _lib.lib()
+        st = _lib.stream_handle()
+        # lastp = -1 but the committed token in every beam's position 0; cum = 0 for beam 0, -inf else
+        lastp = torch.empty(B, W, order, dtype=torch.int32, device=dev)
+        cum = torch.empty(B, W, dtype=torch.float32, device=dev)
+        k0 = known0.to(dev, torch.int64).contiguous()
+        _lib.check(L.cfh_beam_init(k0.data_ptr(), lastp.data_ptr(), cum.data_ptr(), None, B, W, order, 0, st),
+                   "cfh_beam_init")
         nst = steps - 1
         toks = torch.empty(max(nst, 1), B, W, dtype=torch.int32, device=dev)
         bps = torch.empty_like(toks)
         hbuf = torch.empty(B * W, d, dtype=torch.float16, device=dev)
-        L = _lib.lib()
-        st = _lib.stream_handle()
         cands = self._pass_a(pred, lastp, 1, steps, W) if self.twopass_m and steps > 1 else None
         image = self._candidate_image(cands, B)
         for step in range(1, steps):
@@ -187,13 +189,16 @@ class Drafter:
             fr = k
         N = sum(sizes)
         out = torch.empty(B, 2 * N, dtype=torch.int32, device=dev)
-        lastp = torch.full((B, keep, order), -1, dtype=torch.int32, device=dev)
-        lastp[:, 0, 0] = known0.to(dev, torch.int32)
-        cum = torch.zeros(B, keep, dtype=torch.float32, device=dev)
-        prev_ids = torch.full((B, keep), -1, dtype=torch.int32, device=dev)
-        hbuf = torch.empty(B * keep, d, dtype=torch.float16, device=dev)
         L = _lib.lib()
         st = _lib.stream_handle()
+        # lastp = -1 but the committed token in slot 0's position 0; cum = 0; prev_ids = -1
+        lastp = torch.empty(B, keep, order, dtype=torch.int32, device=dev)
+        cum = torch.empty(B, keep, dtype=torch.float32, device=dev)
+        prev_ids = torch.empty(B, keep, dtype=torch.int32, device=dev)
+        k0 = known0.to(dev, torch.int64).contiguous()
+        _lib.check(L.cfh_beam_init(k0.data_ptr(), lastp.data_ptr(), cum.data_ptr(), prev_ids.data_ptr(), B, keep,
+                                   order, 1, st), "cfh_beam_init")
+        hbuf = torch.empty(B * keep, d, dtype=torch.float16, device=dev)
         cands = self._pass_a(pred, lastp, 1, nstep + 1, keep) if self.twopass_m and nstep > 0 else None
         image = self._candidate_image(cands, B)
         fr, base = 1, 0

@@ -1357,6 +1357,28 @@ int head_args(HeadArgs& ha, const void* h, int M, int d, const void* W, const in
   return CFH_OK;
 }
 
+// Depth 0 of a search (one thread per (request, beam)): lastp = -1 but for the committed token in
+// position 0 (every beam of a chain, beam 0 of a tree), cum = 0 for beam 0 and -inf for the others
+// (chain) or 0 (tree), prev_ids = -1 (tree).
+struct BeamInitArgs {
+  const int64_t* known0;
+  int32_t* lastp;
+  float* cum;
+  int32_t* prev_ids;
+  int B, W, order, tree;
+};
+
+__global__ void __launch_bounds__(256) k_beam_init(BeamInitArgs a) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= a.B * a.W) return;
+  const int b = i / a.W, w = i - b * a.W;
+  int32_t* lp = a.lastp + (size_t)i * a.order;
+  lp[0] = (!a.tree || w == 0) ? (int32_t)a.known0[b] : -1;
+  for (int j = 1; j < a.order; ++j) lp[j] = -1;
+  a.cum[i] = (a.tree || w == 0) ? 0.f : -INFINITY;
+  if (a.tree) a.prev_ids[i] = -1;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1631,6 +1653,18 @@ int cfh_path_residual(const void* const* ph, int order, int ffn_mult, int d, con
                               rows_per_pred, r0, (h16*)hsum + (size_t)r0 * d, ws, (hipStream_t)stream);
     if (rc) return rc;
   }
+  return CFH_OK;
+}
+
+int cfh_beam_init(const int64_t* known0, int32_t* lastp, float* cum, int32_t* prev_ids, int B, int W, int order,
+                  int tree, void* stream) {
+  if (!known0 || !lastp || !cum || (tree && !prev_ids) || B < 1 || W < 1 || W > 64 || order < 1 || order > 8)
+    return CFH_E_INVALID;
+  BeamInitArgs a = {};
+  a.known0 = known0; a.lastp = lastp; a.cum = cum; a.prev_ids = prev_ids; a.B = B; a.W = W; a.order = order;
+  a.tree = tree;
+  hipLaunchKernelGGL(k_beam_init, dim3((B * W + 255) / 256), dim3(256), 0, (hipStream_t)stream, a);
+  CFH_LAUNCH_CHECK();
   return CFH_OK;
 }
 

@@ -354,6 +354,13 @@ int cfh_path_residual(const void* const* ph, int order, int ffn_mult, int d, con
                       int M, int nlive, const void* embed_w, const void* pred, long long pred_ld,
                       int rows_per_pred, void* hsum, void* ws, void* stream);
 
+/* Depth 0 of _beam_chains / _beam_tree (cf/vllm_plugin/flow_proposer.py:1208, 1221-1225, 1288-1291) in one
+ * launch: lastp [B][W][order] = -1 except lastp[b][w][0] = known0[b] (every beam of a chain, beam 0
+ * of a tree), cum [B][W] = 0 for beam 0 and -inf for the others (chain; tree: 0 everywhere),
+ * prev_ids [B][W] = -1 (tree; null for a chain).  known0: int64 [B] committed tokens. */
+int cfh_beam_init(const int64_t* known0, int32_t* lastp, float* cum, int32_t* prev_ids, int B, int W,
+                  int order, int tree, void* stream);
+
 /* One depth of _beam_chains (cf/vllm_plugin/flow_proposer.py:1250-1259) for B chains of width W
  * (W*W <= 64): from the per-beam top-W rows vals/ids [B*W][W] (log-probs, shortlist-local ids),
  * cand = cum[b][w] + vals; (cum, flat) = top-W(cand) (ties to the lower flat index);

@@ -682,6 +682,9 @@ def main():
     ap.add_argument("--twopass", type=int, default=0,
                     help="two-pass candidate head with M candidates (0: the one-pass head of the metric)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="skip the graph-replay timing (counter-collection runs: the profiler's counter "
+                         "pass does not survive graph launches)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="after timing, copy one 1 GiB buffer (a kernel of known traffic for calibrating "
                          "the profiler's FETCH_SIZE / WRITE_SIZE counters)")
@@ -825,8 +828,16 @@ def main():
     # the flow's bytes as the reference's algorithm needs them (cross q / out projections streamed in
     # every block pass), beside the folded algorithm's that `fb` counts
     fb_unfolded = flow_bytes(LATENT if latent else d, L, E, cfg.num_chunks, fold=False) + (vae_bytes(d) if latent else 0)
-    print("[bench] graph replays", file=sys.stderr, flush=True)
-    g_med, g_p10, g_p90 = graph_replay_ms(lambda: dr.beam_chains(None, known0, K, Wd, pred=dr.predict_hidden(ctx)))
+    graph = None
+    if not args.no_graph:
+        print("[bench] graph replays", file=sys.stderr, flush=True)
+        g_med, g_p10, g_p90 = graph_replay_ms(lambda: dr.beam_chains(None, known0, K, Wd, pred=dr.predict_hidden(ctx)))
+        graph = {"median_ms": round(g_med, 4), "p10_ms": round(g_p10, 4), "p90_ms": round(g_p90, 4),
+                 "replays": 200, "warmup": 10,
+                 "draft_frac": round((fb + hb) / (g_med * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                 "draft_frac_on_unfolded_bytes": round((fb_unfolded + hb) / (g_med * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                 "what": "the whole draft (predict_hidden + beam) captured once as a HIP graph, each replay "
+                         "timed with events; a captured flow keeps its chunk experts on one stream"}
     out = {
         "metric": metric,
         "value": round(ms * 1e3, 1),
@@ -852,14 +863,7 @@ def main():
                      "frac_on_unfolded_bytes": round(fb_unfolded / (med(flow_ms) * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                      "note": ("frac counts the bytes the folded cross attention needs; frac_on_unfolded_bytes the "
                               "reference algorithm's (cross q / out projections in every block pass)")},
-        "graph_replay": {"median_ms": round(g_med, 4), "p10_ms": round(g_p10, 4), "p90_ms": round(g_p90, 4),
-                         "replays": 200, "warmup": 10,
-                         "draft_frac": round((fb + hb) / (g_med * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                         "draft_frac_on_unfolded_bytes": round((fb_unfolded + hb) / (g_med * 1e-3) / 1e9
-                                                               / HBM_PEAK_GBS, 4),
-                         "what": "the whole draft (predict_hidden + beam) captured once as a HIP graph, "
-                                 "each replay timed with events; a captured flow keeps its chunk experts on "
-                                 "one stream"},
+        "graph_replay": graph,
     }
     if latent:
         out["config"].update({"latent": LATENT, "vae_intermediate": VAE_INTER, "vae_layers": VAE_LAYERS})

@@ -83,6 +83,14 @@ class FusedFlow:
         L = _lib.lib()
         if caps(cfg, 1) is None:
             raise ValueError(f"flow shape not supported by libcfhip: {cfg}")
+        dz = cfg.flow_dim
+        for n in anchor_param_names(cfg):
+            want = (dz,) if n.endswith(".bias") else (dz, dz) if "anchor_mlp" in n else (dz, None)
+            got = tuple(weights[n].shape)
+            if len(got) != len(want) or any(w is not None and w != g for w, g in zip(want, got)):
+                # (the reference's anchor_in projects to expert_dim, which must equal latent_size)
+                raise ValueError(f"{n} has shape {got}; the anchored latent drafter needs "
+                                 f"{tuple('hidden' if w is None else w for w in want)} (latent_size {dz})")
         # One workspace for every batch up to max_batch (the largest request group's), allocated
         # once: a captured draft graph holds its address, so it is never swapped or freed.
         ws = caps(cfg, max(1, int(max_batch)))

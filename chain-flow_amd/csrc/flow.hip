@@ -881,9 +881,6 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
   return done();
 }
 
-// The launches of block l for a wide group (every chunk expert in each launch, Rg requests): QKV,
-// self attention, O, residual, folded cross attention (in subgroups of two requests), residual,
-// W1, W2, residual.
 // One request group of a wide launch sequence: its workspace, its requests [g0, g0 + Rg) of the
 // batch and their context rows.
 struct GroupRun {
@@ -892,7 +889,9 @@ struct GroupRun {
   const h16* ctx;
 };
 
-// The launches of block l for `ng` request groups (one, or two whose entries share every launch:
+// The launches of block l for `ng` request groups -- QKV, self attention, O, residual, folded cross
+// attention (in subgroups of two requests), residual, W1, W2, residual; every chunk expert of every
+// group in each launch (one group, or two whose entries share every launch:
 // entry g * nch + c is expert c of group g, and `WArgs::pair` runs the two groups' workgroups of a
 // weight unit side by side).
 int block_pass_wide(const Plan& p, const WideShape& sh, const cfh::ExpertLayout& L, const GroupRun* gr, int ng,

@@ -176,3 +176,17 @@ def test_config_and_names():
     specs = {k for k in param_specs(c, VOCAB, hidden=HIDDEN) if k.startswith("vae.")}
     assert len(names) == 14 + 24 * c.vae_num_layers == len(set(names))
     assert specs - set(names) == {"vae.logvar.weight", "vae.logvar.bias"}
+
+
+def test_anchor_weight_shapes_are_checked_before_any_device_work():
+    """An anchor_in projecting to expert_dim != latent_size (the reference's module would fail at
+    its first anchor_mlp) is refused with the parameter's name, before anything is packed."""
+    from chain_flow_amd.config import flownet
+    from chain_flow_amd.flow import FusedFlow
+    cfg = TreeVAEFlowConfig(**{**flownet(640, layers=1, flow_steps=1).to_dict(), "latent_size": 640,
+                               "anchor_token": True, "expert_dim": 640})
+    W = {n: torch.zeros(shape[0], *(shape[1:])) for n, (shape, _, _) in param_specs(cfg, VOCAB, hidden=2560).items()
+         if not n.startswith("vae.")}
+    W["anchor_in.weight"] = torch.zeros(2560, 2560)
+    with pytest.raises(ValueError, match="anchor_in.weight has shape"):
+        FusedFlow(cfg, W, device="cpu")

@@ -639,8 +639,14 @@ Plan make_plan(const cfh_flow_dims* dm, int R = 1) {
   };
   bool cross_ok = p.fold ? !stream_check(S_BUF, sa(p.d, p.d, p.ks_fold, p.wpb_fold, 1), p.S_fold) && p.xnb > 0
                          : unfolded_ok();
-  if (!cross_ok && p.fold2) {   // the two-heads fold does not fit this shape: the unfolded launches
+  if (!cross_ok && p.fold2) {
+    // the two-heads fold does not fit this shape: the unfolded launches, with the partial slots they
+    // need (a host-side scan of every supported shape -- d up to 16384, 1-128 heads, 4-16 context
+    // rows, ffn 2/4/6, draft length 8/16 -- found none that takes this branch; it is kept so that a
+    // shape the scan missed still runs)
     p.fold = p.fold2 = false;
+    p.pks = std::max(std::max(p.ks_att, p.ks_w2), p.ks_out);
+    p.ks_fold = p.S_fold = p.wpb_fold = p.xnb = 0;
     cross_ok = unfolded_ok();
   }
   p.ok = !stream_check(S_BUF, sa(3 * p.d, p.d, 1, p.wpb_full, 1), p.Smax) &&

@@ -15,7 +15,7 @@ import torch
 from chain_flow_amd import _lib
 from chain_flow_amd.config import TreeFlowConfig, TreeVAEFlowConfig
 from chain_flow_amd.flow import FusedFlow
-from chain_flow_amd.head import PathHead, ShortlistHead
+from chain_flow_amd.head import PathHead, ShortlistHead, row_topk
 from chain_flow_amd.vae import HiddenVAE
 
 
@@ -74,9 +74,13 @@ class Drafter:
                                  out=res0[b * width:(b + 1) * width])
             sr = res0.view(B, width, -1)[:, 0]
             sp = lastp[:, 0, 0]
-        _, glob = self.head.candidates(pred[:, n0:n1].contiguous(), self.twopass_m, self.twopass_shared, sr, sp)
+        local, glob = self.head.candidates(pred[:, n0:n1].contiguous(), self.twopass_m, self.twopass_shared, sr, sp)
         if self.twopass_shared:
             glob = glob[:, None].expand(B, n1 - n0, self.twopass_m)
+            local = local[:, None].expand(B, n1 - n0, self.twopass_m)
+        # (the shortlist positions of the same rows: pass B of a large batch gathers them from one
+        # full-shortlist head pass)
+        self._cand_local = local
         return glob
 
     def _candidate_image(self, cands, B):
@@ -87,7 +91,7 @@ class Drafter:
         return self._cimg
 
     def _scores(self, rows: torch.Tensor, k: int, prev: torch.Tensor, order: int, cand: torch.Tensor | None, B: int,
-                image: torch.Tensor | None = None):
+                image: torch.Tensor | None = None, local: torch.Tensor | None = None):
         """Per-depth top-k of rows [B*F, d]: (vals [B*F, k], ids [B*F, k] int32, map) -- one-pass over the
         shortlist (ids shortlist-local, map = the shortlist), two-pass over one request's packed
         candidate image (ids local to the candidates, map = their global ids), or over every
@@ -100,8 +104,25 @@ class Drafter:
             vals, ids, _ = self.head.topk_image(rows, k, image, cand.shape[-1], prev=prev, prev_stride=order)
             return vals, ids, cand[0]
         cb = cand.contiguous()                                          # [B, M]
-        vals, ids, _ = self.head.topk_groups(rows, k, cb, prev=prev, prev_stride=order)
         F = rows.shape[0] // B
+        M = cb.shape[1]
+        if local is not None and B * M > self.head.n and self.head.image is not None:
+            # Many requests: their candidate rows (B M, with repeats) outnumber the shortlist, so one
+            # head pass over the whole shortlist for every row (the GEMM head, the markov bias at the
+            # same rounding points, logits kept) reads less than each request's rows in place; each
+            # row's log-softmax top-k then runs over its request's candidates gathered from those
+            # logits (cfh_row_topk: the head's own top-k rule, ids = positions in the candidate list).
+            BF, n = rows.shape[0], self.head.n
+            lg = torch.empty(BF, n, dtype=torch.float16, device=rows.device)
+            scratch = (torch.empty(BF, 1, dtype=torch.float32, device=rows.device),
+                       torch.empty(BF, 1, dtype=torch.int32, device=rows.device),
+                       torch.empty(BF, dtype=torch.float32, device=rows.device))
+            self.head.topk(rows, 1, prev=prev, prev_stride=order, logits=lg, out=scratch)
+            idx = local.contiguous().long().view(B, 1, M).expand(B, F, M)
+            sub = torch.gather(lg.view(B, F, n), 2, idx).view(BF, M)
+            vals, ids, _ = row_topk(sub, k)
+        else:
+            vals, ids, _ = self.head.topk_groups(rows, k, cb, prev=prev, prev_stride=order)
         glob = torch.gather(cb, 1, ids.view(B, F * k).long()).view(B * F, k)
         return vals, glob, None
 
@@ -160,7 +181,8 @@ class Drafter:
             # every request's W beams in one call, each request's rows with its own marginal hidden
             self.path.hidden(lastp.view(B * W, order), self._nlive(step), pred[:, step], out=hbuf)
             vals, ids, smap = self._scores(hbuf, W, lastp.view(-1), order,
-                                           None if cands is None else cands[:, step - 1], B, image)
+                                           None if cands is None else cands[:, step - 1], B, image,
+                                           None if cands is None else self._cand_local[:, step - 1])
             _lib.check(L.cfh_beam_chain_step(vals.data_ptr(), ids.data_ptr(), cum.data_ptr(), lastp.data_ptr(),
                                              _lib.ptr(smap), toks[step - 1].data_ptr(),
                                              bps[step - 1].data_ptr(), B, W, order, st), "cfh_beam_chain_step")
@@ -207,7 +229,8 @@ class Drafter:
             lp_rows = lastp[:, :fr].reshape(B * fr, order).contiguous()
             self.path.hidden(lp_rows, self._nlive(step), pred[:, step], out=rows)
             vals, ids, smap = self._scores(rows, topb, lp_rows.view(-1), order,
-                                           None if cands is None else cands[:, step - 1], B, image)
+                                           None if cands is None else cands[:, step - 1], B, image,
+                                           None if cands is None else self._cand_local[:, step - 1])
             _lib.check(L.cfh_beam_tree_step(vals.data_ptr(), ids.data_ptr(), cum.data_ptr(), lastp.data_ptr(),
                                             prev_ids.data_ptr(), _lib.ptr(smap), out.data_ptr(), 2 * N,
                                             base, B, fr, topb, keep, order, st), "cfh_beam_tree_step")

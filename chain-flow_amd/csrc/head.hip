@@ -964,16 +964,30 @@ struct PathOutArgs {
   int row0;            // row of this launch's first row in the whole call (for the grouping)
 };
 
+// Four columns a thread (d % 4 == 0): every partial read is one 16-byte load, all of a thread's
+// loads issued before its sums.
 __global__ void __launch_bounds__(256) k_path_out(PathOutArgs a) {
-  const size_t total = (size_t)a.M * a.d, per_kc = total;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
-    float s = 0.f;
-    for (int kc = 0; kc < a.ks; ++kc) s += a.P[kc * per_kc + i];
+  const size_t total = (size_t)a.M * a.d, per_kc = total, nq = total / 4;
+  for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < nq; q += (size_t)gridDim.x * blockDim.x) {
+    const size_t i = q * 4;
+    float4 s = *(const float4*)(a.P + i);
+    for (int kc = 1; kc < a.ks; ++kc) {
+      const float4 t = *(const float4*)(a.P + kc * per_kc + i);
+      s.x += t.x; s.y += t.y; s.z += t.z; s.w += t.w;
+    }
     const int m = (int)(i / a.d), c = (int)(i - (size_t)m * a.d);
     const int g = a.rows_per_pred > 0 ? (a.row0 + m) / a.rows_per_pred : 0;
-    const float res = r16(s + (float)a.bias[c]);
-    a.hsum[i] = (h16)((float)a.pred[(size_t)g * a.pred_ld + c] + res);
+    const h16* pr = a.pred + (size_t)g * a.pred_ld + c;
+    const float v[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) a.hsum[i + t] = (h16)((float)pr[t] + r16(v[t] + (float)a.bias[c + t]));
   }
+}
+
+// Workgroups of a k_path_out launch over M rows of d: one float4 column group a thread, at most 1024.
+unsigned path_out_blocks(int M, int d) {
+  const long long q = (long long)M * d / 4;
+  return (unsigned)std::max(1LL, std::min(1024LL, (q + 255) / 256));
 }
 
 // The path head's two MLP layers for up to PATH_CHUNK rows, each as one launch: one workgroup per
@@ -1546,7 +1560,7 @@ static int path_group_wide(const PathWide& pw, const void* const* ph, int order,
   PathOutArgs po = {};
   po.P = Pdn; po.bias = (const h16*)ph[2 * order + 5]; po.pred = (const h16*)pred; po.hsum = (h16*)hsum;
   po.ks = pw.dn_ks; po.M = M; po.d = d; po.pred_ld = pred_ld; po.rows_per_pred = rows_per_pred; po.row0 = row0;
-  hipLaunchKernelGGL(k_path_out, dim3(64), dim3(256), 0, st, po);
+  hipLaunchKernelGGL(k_path_out, dim3(path_out_blocks(M, d)), dim3(256), 0, st, po);
   CFH_LAUNCH_CHECK();
   return CFH_OK;
 }
@@ -1614,7 +1628,7 @@ static int path_chunk(const PathPlan& pp, const void* const* ph, int order, int 
   PathOutArgs po = {};
   po.P = Pdn; po.bias = b3; po.pred = (const h16*)pred; po.hsum = (h16*)hsum; po.ks = pp.dn_ks; po.M = M; po.d = d;
   po.pred_ld = pred_ld; po.rows_per_pred = rows_per_pred; po.row0 = row0;
-  hipLaunchKernelGGL(k_path_out, dim3(64), dim3(256), 0, st, po);
+  hipLaunchKernelGGL(k_path_out, dim3(path_out_blocks(M, d)), dim3(256), 0, st, po);
   CFH_LAUNCH_CHECK();
   return CFH_OK;
 }

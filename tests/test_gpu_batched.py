@@ -135,7 +135,8 @@ def _near(trace, k1, k2):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("search,B,twopass", [("chain", 32, 0), ("tree", 3, 0), ("chain", 4, 256), ("tree", 4, 256)])
+@pytest.mark.parametrize("search,B,twopass", [("chain", 32, 0), ("tree", 3, 0), ("chain", 4, 256), ("tree", 4, 256),
+                                              ("chain", 8, 256), ("tree", 6, 256)])
 def test_batched_drafts_match_oracle(cuda, search, B, twopass):
     cfg, W, sl = _setup()
     dr = Drafter(cfg, {k: v.to(cuda) for k, v in W.items()}, sl.to(cuda), device=cuda, twopass_m=twopass,
@@ -192,3 +193,32 @@ def test_batches_past_256_beam_rows_equal_smaller_batches(cuda, search, B):
     parts = torch.cat([run(0, h), run(h, B)])
     torch.cuda.synchronize()
     assert torch.equal(whole, parts)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("F,k", [(4, 4), (1, 8)])
+def test_passb_over_the_shortlist_equals_grouped_rows(cuda, F, k):
+    """Pass B of a large batch (B M > shortlist rows): one full-shortlist head pass, each row's
+    log-softmax top-k over its request's candidates gathered from the logits, against the grouped
+    in-place pass B over the same candidates: log-probs within 2e-3, ids equal away from ties."""
+    cfg, W, sl = _setup()
+    dr = Drafter(cfg, {k_: v.to(cuda) for k_, v in W.items()}, sl.to(cuda), device=cuda, twopass_m=256,
+                 twopass_shared=True)
+    B, d, M = 8, 512, 256
+    g = torch.Generator().manual_seed(F)
+    hm = (torch.randn(B, 4, d, generator=g)).half().to(cuda)
+    local, glob = dr.head.candidates(hm, M, True)
+    rows = (torch.randn(B * F, d, generator=g)).half().to(cuda)
+    prev = sl[torch.randint(0, len(sl), (B * F * cfg.path_order,), generator=g)].to(torch.int32).to(cuda)
+    v1, i1, _ = dr._scores(rows, k, prev, cfg.path_order, glob, B, None, None)
+    v2, i2, _ = dr._scores(rows, k, prev, cfg.path_order, glob, B, None, local)
+    torch.cuda.synchronize()
+    v1, v2, i1, i2 = v1.cpu().numpy(), v2.cpu().numpy(), i1.cpu().numpy(), i2.cpu().numpy()
+    print(f"  max |dlogp| {np.abs(v1 - v2).max():.2e}, ids equal {(i1 == i2).mean():.3f}", flush=True)
+    assert np.abs(v1 - v2).max() < 2e-3
+    gaps = np.diff(-v1, axis=1)
+    for r in range(B * F):
+        for j in range(k):
+            if i1[r, j] != i2[r, j]:   # only where a neighbouring rank is within 1e-3
+                near = (j > 0 and gaps[r, j - 1] <= 1e-3) or (j < k - 1 and gaps[r, j] <= 1e-3)
+                assert near, (r, j)

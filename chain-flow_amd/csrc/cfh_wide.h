@@ -272,9 +272,7 @@ int wide_check(const WArgs& a, int wv, int S_max) {
   if ((wv != 4 && wv != 6 && wv != 8 && wv != 12) || (a.N / 16) % (WT * wv) || S_max < 1 || S_max > WMAXR ||
       wide_lds(S_max) > 150 * 1024)
     return CFH_E_UNSUPPORTED;
-  // pairing: an even entry count and a whole number of 8-workgroup runs per half
-  if (a.pair && (a.nex % 2 || ((long long)(a.nex / 2) * a.ks * ((a.N / 16) / (WT * wv))) % 8))
-    return CFH_E_UNSUPPORTED;
+  if (a.pair && a.nex % 2) return CFH_E_UNSUPPORTED;
   return CFH_OK;
 }
 
@@ -308,10 +306,13 @@ int launch_wide(const WArgs& a0, int wv, hipStream_t st) {
   for (int e = 0; e < a.nex; ++e)
     if (a.ex[e].S < 1 || a.ex[e].lda < a.K || !a.ex[e].w || !a.ex[e].a || !a.ex[e].out) return CFH_E_INVALID;
   a.wg_per_kc = (a.N / 16) / (WT * wv);
+  // the side-by-side order needs a whole number of 8-workgroup runs per half (narrow widths such as
+  // d = 640 have 5 a k-split: their paired launches keep the plain order, still one launch for both)
+  const bool pair_runs = a.pair && ((long long)(a.nex / 2) * a.ks * a.wg_per_kc) % 8 == 0;
   if (a.ks > 1 && (a.nex * a.ks) % 8 == 0 && (!a.pair || ((a.nex / 2) * a.ks) % 8 == 0) && !wide_xcd_off())
     a.map = MAP_XCD;
   else
-    a.map = a.pair ? MAP_PAIR : MAP_PLAIN;
+    a.map = pair_runs ? MAP_PAIR : MAP_PLAIN;
   const size_t lds = wide_lds(S_max);
   const int ng = (S_max + 15) / 16;
 #define CFH_WIDE(G)                                                                 \
@@ -373,6 +374,60 @@ int launch_self_attn(const SelfArgs& a, hipStream_t st) {
   const size_t lds = (size_t)3 * Srm * a.hd * 2 + (size_t)Srm * Srm * 4;
   if (lds > 64 * 1024) return CFH_E_UNSUPPORTED;
   hipLaunchKernelGGL(k_self_attn, dim3((unsigned)(a.nex * a.R * a.H)), dim3(SAT), lds, st, a);
+  CFH_LAUNCH_CHECK();
+  return CFH_OK;
+}
+
+// Cross attention of a wide group whose heads do not fold (head widths such as 80: two heads an
+// MFMA k-chunk), one workgroup per (expert, request, head): the request's Sr rows of q (columns of
+// head h of the [S][d] rows, bias included), its C context rows of K and V (block l's [2][Ct][d]
+// image, the request's rows [j C, j C + C)), staged in LDS, then `attend` without a mask, written
+// as fp16 rows [S][d] of the attention output.
+struct CrossArgs {
+  const h16* q[4];     // [S][d]
+  const h16* kv[4];    // [2][Ct][d]: K rows then V rows
+  h16* out[4];         // [S][d]
+  int S[4], Sr[4], Ct[4];
+  int nex, R, H, d, hd, C;
+};
+
+__global__ void __launch_bounds__(SAT) k_cross_attn(CrossArgs a) {
+  extern __shared__ __align__(16) h16 sm[];
+  int b = blockIdx.x;
+  const int h = b % a.H;
+  b /= a.H;
+  const int j = b % a.R, e = b / a.R;
+  const int Sr = a.Sr[e], C = a.C, hd = a.hd, d = a.d;
+  if ((j + 1) * Sr > a.S[e] || (j + 1) * C > a.Ct[e]) return;   // (a request the group does not hold)
+  const h16* qs = a.q[e] + (size_t)j * Sr * d + h * hd;
+  const h16* ks = a.kv[e] + (size_t)j * C * d + h * hd;
+  const h16* vs = ks + (size_t)a.Ct[e] * d;
+  h16* sq = sm;
+  h16* sk = sq + Sr * hd;
+  h16* sv = sk + C * hd;
+  float* P = (float*)(sv + C * hd);                   // [Sr][C]
+  const int nv = hd / 8;
+  for (int idx = threadIdx.x; idx < (Sr + 2 * C) * nv; idx += blockDim.x) {
+    const int i = idx / nv, c = (idx - i * nv) * 8;
+    const h16* src = i < Sr ? qs + (size_t)i * d : i < Sr + C ? ks + (size_t)(i - Sr) * d : vs + (size_t)(i - Sr - C) * d;
+    *(h16x8*)(sq + (size_t)i * hd + c) = *(const h16x8*)(src + c);
+  }
+  lds_barrier();
+  attend(Sr, C, Sr, C, hd, hd, false, sq, sk, sv, P, a.out[e] + (size_t)j * Sr * d + h * hd, d);
+}
+
+size_t cross_attn_lds(int Sr, int C, int hd) { return (size_t)(Sr + 2 * C) * hd * 2 + (size_t)Sr * C * 4; }
+
+int launch_cross_attn(const CrossArgs& a, hipStream_t st) {
+  if (a.hd % 8 || a.hd <= 0 || a.nex < 1 || a.nex > 4 || a.C < 1 || a.C > 16) return CFH_E_UNSUPPORTED;
+  int Srm = 0;
+  for (int e = 0; e < a.nex; ++e) {
+    if (a.Sr[e] < 1 || a.Sr[e] > 16 || a.S[e] > a.R * a.Sr[e] || a.Ct[e] > a.R * a.C) return CFH_E_UNSUPPORTED;
+    Srm = std::max(Srm, a.Sr[e]);
+  }
+  const size_t lds = cross_attn_lds(Srm, a.C, a.hd);
+  if (lds > 64 * 1024) return CFH_E_UNSUPPORTED;
+  hipLaunchKernelGGL(k_cross_attn, dim3((unsigned)(a.nex * a.R * a.H)), dim3(SAT), lds, st, a);
   CFH_LAUNCH_CHECK();
   return CFH_OK;
 }

@@ -445,9 +445,9 @@ int launch_xattn(const XattArgs& a, hipStream_t st) {
 // Launch shapes of the wide kernels with `groups` request groups a launch.
 struct WideShape {
   int groups;
-  int wv_qkv, wv_w1, wv_kv;        // full-K launches: waves per workgroup
+  int wv_qkv, wv_w1, wv_kv, wv_qc; // full-K launches: waves per workgroup (wv_qc: unfolded cross q)
   int wv_split;                    // split-K launches: waves per workgroup
-  int ks_wo, ks_ww2, ks_wout;      //                   and k-splits
+  int ks_wo, ks_ww2, ks_wout, ks_oc;  //                and k-splits (ks_oc: unfolded cross out-proj)
   bool ok;
 };
 
@@ -521,6 +521,8 @@ WideShape wide_shape(const Plan& p, int groups) {
   s.ks_wo = ks_split(p.d, p.d);
   s.ks_ww2 = ks_split(p.d, p.fd);
   s.ks_wout = ks_split(p.d, p.d);
+  s.wv_qc = p.fold ? 0 : wv_full(p.d);
+  s.ks_oc = p.fold ? 0 : ks_split(p.d, p.d);
   auto wa = [&](int N, int K, int ks, int nex) {
     WArgs a = {};
     a.nex = nex; a.N = N; a.K = K; a.ks = ks; a.pair = groups > 1;
@@ -534,7 +536,9 @@ WideShape wide_shape(const Plan& p, int groups) {
          !wide_check(wa(p.d, p.d, s.ks_wo, units), s.wv_split, p.Smax) &&
          !wide_check(wa(p.d, p.fd, s.ks_ww2, units), s.wv_split, p.Smax) &&
          !wide_check(wa(p.d, p.d, s.ks_wout, units), s.wv_split, p.Smax) &&
-         !wide_check(wa(p.d, p.d, p.H, groups * p.nch), 4, p.Ct);
+         (p.fold ? !wide_check(wa(p.d, p.d, p.H, groups * p.nch), 4, p.Ct)
+                 : s.ks_oc > 0 && !wide_check(wa(p.d, p.d, 1, units), s.wv_qc, p.Smax) &&
+                       !wide_check(wa(p.d, p.d, s.ks_oc, units), s.wv_split, p.Smax));
   return s;
 }
 
@@ -546,17 +550,20 @@ void make_wide_plan(Plan& p, const cfh_flow_dims* dm) {
   p.fold2 = false;
   p.ks_fold = p.H;
   p.S_fold = p.Ct;
-  p.ok = p.fold && p.hd % WCH == 0 && p.d % WCH == 0 && p.fd % WCH == 0 && p.Smax <= WMAXR && p.Ct <= WMAXR &&
-         p.C <= 8 && 2 * p.KD <= MAXR && res_nq(p.d) > 0;
+  // the cross attention folded (one head a k-chunk: its factors split-K by head need head widths
+  // of whole staging chunks) or unfolded (q projection, attention per (request, head), out-proj)
+  p.ok = (p.fold ? p.hd % WCH == 0 : p.hd % 8 == 0) && p.d % WCH == 0 && p.fd % WCH == 0 &&
+         p.Smax <= WMAXR && p.Ct <= WMAXR && p.C <= 8 && 2 * p.KD <= MAXR && res_nq(p.d) > 0;
   if (!p.ok) return;
   p.ws[0] = wide_shape(p, 1);
   p.ws[1] = wide_shape(p, 2);
-  p.pks = p.H;
+  p.pks = p.fold ? p.H : 1;
   for (const WideShape& w : p.ws)
-    if (w.ok) p.pks = std::max(p.pks, std::max(w.ks_wo, std::max(w.ks_ww2, w.ks_wout)));
-  p.xnb = xattn_blocks(p.d, p.nch * p.H, 4);
-  p.ok = p.ws[0].ok && p.xnb > 0 &&
-         (size_t)3 * p.KD * p.hd * 2 + (size_t)p.KD * p.KD * 4 <= 64 * 1024;   // self attention's LDS
+    if (w.ok) p.pks = std::max({p.pks, w.ks_wo, w.ks_ww2, w.ks_wout, w.ks_oc});
+  p.xnb = p.fold ? xattn_blocks(p.d, p.nch * p.H, 4) : 0;
+  p.ok = p.ws[0].ok && (!p.fold || p.xnb > 0) &&
+         (size_t)3 * p.KD * p.hd * 2 + (size_t)p.KD * p.KD * 4 <= 64 * 1024 &&   // self attention's LDS
+         (p.fold || cross_attn_lds(p.KD, p.C, p.hd) <= 64 * 1024);
 }
 
 Plan make_plan(const cfh_flow_dims* dm, int R = 1) {
@@ -963,14 +970,46 @@ int block_pass_wide(const Plan& p, const WideShape& sh, const cfh::ExpertLayout&
         r.g[e] = (const h16*)PTR(c, g_off); r.b[e] = (const h16*)PTR(c, b_off);
       }
   };
-  // residual + LN_cross (as the folded cross attention's operand image)
+  // residual + LN_cross (as the folded cross attention's operand image, or plain rows)
   r.ks = sh.ks_wo;
   res_params(B + L.o_b, B + L.xn_w, B + L.xn_b);
-  r.pack = 1;
+  r.pack = p.fold;
   if ((rc = launch_res(r, st))) return rc;
   r.pack = 0;
-  // folded cross attention, two requests a subgroup
-  {
+  if (!p.fold) {
+    // unfolded: q = fp16(LN_cross(x) Wq^T + bq) into the q|k|v buffer (free after the self
+    // attention), attention per (request, head) over its context K/V into the LN rows' buffer,
+    // out-projection split-K
+    WArgs a = wargs(d, d, 1);
+    for (int g = 0; g < ng; ++g)
+      for (int c = 0; c < nch; ++c) {
+        WEx& x = a.ex[g * nch + c];
+        x.w = (const h16x8*)PTR(c, B + L.qc); x.a = gr[g].w.abuf[c]; x.lda = d;
+        x.bias = (const h16*)PTR(c, B + L.qc_b); x.out = gr[g].w.qkv[c]; x.S = S_of(g, c);
+      }
+    if ((rc = launch_wide<E_BIAS16>(a, sh.wv_qc, st))) return rc;
+    CrossArgs ca = {};
+    ca.nex = nex; ca.H = p.H; ca.d = d; ca.hd = p.hd; ca.C = p.C;
+    for (int g = 0; g < ng; ++g) {
+      ca.R = std::max(ca.R, gr[g].Rg);
+      const int Cg = gr[g].Rg * p.C;
+      for (int c = 0; c < nch; ++c) {
+        const int e = g * nch + c;
+        ca.q[e] = gr[g].w.qkv[c]; ca.kv[e] = gr[g].w.kvc[c] + (size_t)l * 2 * Cg * d; ca.out[e] = gr[g].w.abuf[c];
+        ca.S[e] = S_of(g, c); ca.Sr[e] = Sr_of(c); ca.Ct[e] = Cg;
+      }
+    }
+    if ((rc = launch_cross_attn(ca, st))) return rc;
+    WArgs o = wargs(d, d, sh.ks_oc);
+    for (int g = 0; g < ng; ++g)
+      for (int c = 0; c < nch; ++c) {
+        WEx& x = o.ex[g * nch + c];
+        x.w = (const h16x8*)PTR(c, B + L.oc); x.a = gr[g].w.abuf[c]; x.lda = d; x.out = gr[g].w.P[c];
+        x.S = S_of(g, c);
+      }
+    if ((rc = launch_wide<E_PART>(o, sh.wv_split, st))) return rc;
+  } else {
+    // folded cross attention, two requests a subgroup
     XattArgs x = {};
     x.nex = nex; x.d = d; x.H = p.H; x.Cq = p.C; x.nb = p.xnb; x.scale = 1.0f / sqrtf((float)p.hd);
     x.Csg = 2 * p.C;
@@ -989,8 +1028,8 @@ int block_pass_wide(const Plan& p, const WideShape& sh, const cfh::ExpertLayout&
     }
     if ((rc = launch_xattn(x, st))) return rc;
   }
-  // residual + LN_ffn (one partial per head)
-  r.ks = p.H;
+  // residual + LN_ffn (one partial per head, or the out-projection's k-splits)
+  r.ks = p.fold ? p.H : sh.ks_oc;
   res_params(B + L.oc_b, B + L.fn_w, B + L.fn_b);
   if ((rc = launch_res(r, st))) return rc;
   // W1: g = fp16(gelu(LN_ffn(x) W1^T + b1))
@@ -1062,9 +1101,9 @@ int per_draft_wide(const Plan& p, const WideShape& sh, const cfh::ExpertLayout& 
         x.bias = (const h16*)PTR(c, BLK(l) + L.kv_b); x.out = gr[g].w.kvc[c] + (size_t)l * 2 * Cg * d; x.S = Cg;
         x.nsplit = d;
       }
-    if (a.pair && wide_check(a, sh.wv_kv, WMAXR)) a.pair = 0;   // (an odd tail: no side-by-side runs)
     if ((rc = launch_wide<E_BIAS16>(a, sh.wv_kv, st))) return rc;
   }
+  if (!p.fold) return CFH_OK;   // (the unfolded cross attention needs only the K/V rows)
   for (int g = 0; g < ng; ++g) {
     const int Cg = gr[g].Rg * p.C;
     XbiasArgs xb = {};
@@ -1100,7 +1139,6 @@ int per_draft_wide(const Plan& p, const WideShape& sh, const cfh::ExpertLayout& 
             x.pack = q == 0;
           }
         }
-      if (a.pair && wide_check(a, 4, WMAXR)) a.pair = 0;
       if ((rc = launch_wide<E_PART16>(a, 4, st))) return rc;
     }
   return CFH_OK;

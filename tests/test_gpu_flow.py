@@ -179,17 +179,18 @@ def test_flow_latent_widths_match_oracle(cuda, d, heads, layers, steps):
 @pytest.mark.gpu
 @pytest.mark.parametrize("d,B,layers", [(512, 2, 2), (512, 5, 1), (640, 3, 1), (1024, 2, 2), (4096, 2, 1),
                                         (1024, 3, 2), (1024, 16, 1), (1024, 21, 1), (1024, 40, 1), (2048, 8, 1),
-                                        (4096, 5, 1)])
+                                        (4096, 5, 1), (640, 20, 2)])
 def test_packed_batch_matches_oracle_per_request(cuda, d, B, layers):
     """A batch drafts in groups whose rows share every weight stream: two requests a 16-row tile
-    (attention masked to each request's own rows and context), or, above two requests where the
-    head width is a multiple of 128, wide groups of up to 16 requests (rows staged in K chunks,
-    self attention per request, cross attention in subgroups of two); each request's hiddens
-    against the oracle on its own context, and against the same request drafted alone in the same
-    numerics.  d = 640 runs the unfolded cross attention (head width 80), the others the folded
-    one; B = 5 and 3 at d <= 640 end with a group of one; B = 21 at d = 1024 runs two wide groups
-    (11 and 10 requests) side by side in every launch, B = 40 a pair of 14-request groups then one
-    of 12, B = 3 at d = 1024 one wide group of an odd request count."""
+    (attention masked to each request's own rows and context), or, above two requests, wide groups
+    of up to 16 requests (rows staged in K chunks, self attention per request; the cross attention
+    folded in subgroups of two where the head width is a multiple of 128, else unfolded: q
+    projection, attention per request and head, out-projection); two wide groups at a time share
+    every launch.  Each request's hiddens against the oracle on its own context, and against the
+    same request drafted alone in the same numerics.  d = 512 (head width 64) keeps the two-request
+    tiles, B = 5 ending with a group of one; d = 640 (head width 80) runs B = 3 as one unfolded wide
+    group and B = 20 as two; d = 1024: B = 3 one wide group of an odd request count, B = 21 two (11
+    and 10 requests), B = 40 a pair of 14-request groups then one of 12."""
     cfg = flownet(d, layers=layers, flow_steps=2)
     W = _flow_weights(cfg, seed=13)
     ctx = synthetic_context(B, cfg.context_size, d, seed=21)

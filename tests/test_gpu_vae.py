@@ -190,11 +190,12 @@ def test_anchored_latent_drafter_matches_oracle(cuda):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("d,B", [(640, 1), (1024, 5), (1024, 24)])
+@pytest.mark.parametrize("d,B", [(640, 1), (640, 12), (1024, 5), (1024, 24)])
 def test_anchor_rows_and_anchored_flow_match_oracle(cuda, d, B):
     """cfh_flow_anchor (anchor_in + every expert's anchor_mlp, bit-for-bit in fp16 up to summation
     order) and cfh_flow_integrate_anchored against the oracle's flow with the anchor; d=1024 x 24
-    requests runs the wide request groups."""
+    requests runs two wide request groups side by side, d=640 x 12 one wide group with the unfolded
+    cross attention."""
     from chain_flow_amd.flow import FusedFlow
     hidden, V = 2048, 256
     cfg = _cfg(d, 256, 4, 1, layers=2, steps=2, expert_dim=d, anchor_token=True)

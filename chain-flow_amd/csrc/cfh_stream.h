@@ -503,6 +503,7 @@ struct ResArgs {
   int rows[4];
   int nex, ks, d, mode;
   int pack;            // LN rows written in frag_index order (the folded cross attention's operand)
+  int pos_period;      // RES_POS16: row r takes position row r % pos_period (sequences stacked; 0: r)
 };
 
 __device__ __forceinline__ float block_sum_rt(float v, float* red) {  // red[blockDim/64]
@@ -524,7 +525,7 @@ __device__ void res_row(const ResArgs& a, int e, int r) {
   const size_t pst = (size_t)a.rows[e] * d;
   float* xr = a.x[e] + (size_t)r * d;
   const float* Pr = a.P[e] + (size_t)r * d;
-  const h16* pr = a.mode == RES_POS16 ? a.pos[e] + (size_t)r * d : a.bias[e];
+  const h16* pr = a.mode == RES_POS16 ? a.pos[e] + (size_t)(a.pos_period > 0 ? r % a.pos_period : r) * d : a.bias[e];
   // every load of the row is issued up front (the bias, gamma and beta too, so that the LayerNorm
   // does not pay a second memory round trip after the statistics); lanes past the row read its
   // last group

@@ -329,14 +329,16 @@ int launch_wide(const WArgs& a0, int wv, hipStream_t st) {
   return CFH_E_UNSUPPORTED;
 }
 
-// Causal self attention of a wide group, one workgroup per (expert, request, head): the request's
-// Sr rows of q, k, v (columns of head h of the [S][3d] rows) staged in LDS, then `attend` (the
-// narrow kernel's attention, same arithmetic), written as fp16 rows [S][d] of the attention output.
+// Self attention of a wide group (causal, or with no mask), one workgroup per (entry, request,
+// head): the request's Sr rows of q, k, v (columns of head h of the [S][3d] rows) staged in LDS,
+// then `attend` (the narrow kernel's attention, same arithmetic), written as fp16 rows [S][d] of
+// the attention output.
 struct SelfArgs {
   const h16* qkv[4];   // [S][3d]
   h16* out[4];         // [S][d]
   int S[4], Sr[4];     // rows, rows per request
   int nex, R, H, d, hd;
+  int bidir;           // 0: causal (the flow's draft rows); 1: no mask (the VAE's sequences)
 };
 
 constexpr int SAT = 256;          // threads of a self-attention workgroup
@@ -361,7 +363,7 @@ __global__ void __launch_bounds__(SAT) k_self_attn(SelfArgs a) {
     *(h16x8*)(sq + (size_t)(part * Sr + i) * hd + c) = *(const h16x8*)(src + (size_t)i * 3 * d + part * d + c);
   }
   lds_barrier();
-  attend(Sr, Sr, Sr, Sr, hd, hd, true, sq, sk, sv, P, a.out[e] + (size_t)j * Sr * d + h * hd, d);
+  attend(Sr, Sr, Sr, Sr, hd, hd, !a.bidir, sq, sk, sv, P, a.out[e] + (size_t)j * Sr * d + h * hd, d);
 }
 
 int launch_self_attn(const SelfArgs& a, hipStream_t st) {

@@ -8,7 +8,8 @@
 // with a GELU module after linear1 (so linear1's output is rounded before the GELU).
 //
 // One half (encoder or decoder) is a launch sequence on the caller's stream over the rows of one
-// sequence (<= 16), built from the flow's streaming kernels (cfh_stream.h):
+// sequence (<= 16) -- or, for a batch, of a group of up to 128 / rows sequences stacked (the wide
+// kernels of cfh_wide.h, same launches) -- built from the flow's streaming kernels (cfh_stream.h):
 //   IN    stream  A = input rows                  fp32 partials                        split-K
 //   RES   row     x = fp16(fp16(sum P + b_in) + pos[r]) ; a = norm1 of layer 0
 //   per layer l:
@@ -22,7 +23,7 @@
 //   SUM   reduce  out = fp16(sum P + b_out)
 #include <algorithm>
 
-#include "cfh_stream.h"
+#include "cfh_wide.h"
 
 namespace {
 
@@ -257,6 +258,137 @@ int run_half(const VaePlan& p, const HalfPlan& hp, const HalfLayout& L, const ch
   return CFH_OK;
 }
 
+// Many sequences: up to WMAXR / rows of them stacked as the rows of one launch sequence through the
+// wide kernels (cfh_wide.h), so that a batch of sequences streams every weight once per group
+// instead of once per sequence.  Same launches and rounding points as the per-sequence form; the
+// self attention runs per (sequence, head) without a mask, the position rows repeat per sequence.
+struct WideHalf {
+  int ks_in, wv_qkv, ks_o, wv_w1, ks_w2, ks_out;
+};
+
+struct VaeWide {
+  int G, S;           // sequences a group, its rows
+  WideHalf enc, dec;
+  int pks, pcols;
+  bool ok;
+};
+
+VaeWide vae_wide_plan(const cfh_vae_dims* dm, int rows, int G) {
+  VaeWide p = {};
+  const int I = dm->inter, F = 4 * I, H = dm->heads, hd = I / H;
+  p.G = G;
+  p.S = G * rows;
+  p.pcols = std::max({I, dm->hidden, dm->latent});
+  if (G < 2 || p.S > WMAXR || I % WCH || hd % 8 || (size_t)3 * rows * hd * 2 + (size_t)rows * rows * 4 > 64 * 1024)
+    return p;
+  constexpr int CUS = 256, WVS = 4;
+  auto ks_split = [&](int N, int K) {
+    int best = 0;
+    for (int ks = 1; ks <= K / WCH; ++ks) {
+      if (K % ks || (K / ks) % WCH) continue;
+      best = ks;
+      if ((long long)(N / 16 / (WT * WVS)) * ks >= CUS) break;
+    }
+    return best;
+  };
+  auto wa = [&](int N, int K, int ks) {
+    WArgs a = {};
+    a.nex = 1; a.N = N; a.K = K; a.ks = ks;
+    return a;
+  };
+  p.ok = true;
+  p.pks = 1;
+  auto half = [&](WideHalf& h, int kin, int nout) {
+    h.ks_in = kin % WCH ? 0 : ks_split(I, kin);
+    h.wv_qkv = wide_wv(3 * I / 16, 1);
+    h.ks_o = ks_split(I, I);
+    h.wv_w1 = wide_wv(F / 16, 1);
+    h.ks_w2 = ks_split(I, F);
+    h.ks_out = ks_split(nout, I);
+    p.ok = p.ok && h.ks_in > 0 && h.ks_o > 0 && h.ks_w2 > 0 && h.ks_out > 0 && h.wv_qkv > 0 && h.wv_w1 > 0 &&
+           !wide_check(wa(I, kin, h.ks_in), WVS, p.S) && !wide_check(wa(3 * I, I, 1), h.wv_qkv, p.S) &&
+           !wide_check(wa(I, I, h.ks_o), WVS, p.S) && !wide_check(wa(F, I, 1), h.wv_w1, p.S) &&
+           !wide_check(wa(I, F, h.ks_w2), WVS, p.S) && !wide_check(wa(nout, I, h.ks_out), WVS, p.S);
+    p.pks = std::max({p.pks, h.ks_in, h.ks_o, h.ks_w2, h.ks_out});
+  };
+  half(p.enc, dm->hidden, dm->latent);
+  half(p.dec, dm->latent, dm->hidden);
+  return p;
+}
+
+VaeWS vae_wide_carve(const VaeWide& p, const cfh_vae_dims* dm, char* base) {
+  VaePlan q = {};
+  q.I = dm->inter; q.T = p.S; q.pks = p.pks; q.pcols = p.pcols;
+  return vae_carve(q, base);
+}
+
+int run_half_wide(const VaeWide& p, const WideHalf& hp, const HalfLayout& L, const char* W, const cfh_vae_dims* dm,
+                  int rows, int G, const h16* in, h16* out, const VaeWS& w, hipStream_t st) {
+  const int I = dm->inter, F = 4 * I, H = dm->heads, S = G * rows;
+  const bool enc = &hp == &p.enc;
+  const int Kin = enc ? dm->hidden : dm->latent, Nout = enc ? dm->latent : dm->hidden;
+  auto V = [&](size_t o) { return (const h16*)(W + o); };
+  auto M = [&](size_t o) { return (const h16x8*)(W + o); };
+  auto one = [&](int N, int K, int ks, const h16x8* wt, const h16* a, int lda, void* o, const h16* b) {
+    WArgs x = {};
+    x.nex = 1; x.N = N; x.K = K; x.ks = ks;
+    x.ex[0].w = wt; x.ex[0].a = a; x.ex[0].lda = lda; x.ex[0].out = o; x.ex[0].bias = b; x.ex[0].S = S;
+    return x;
+  };
+  constexpr int WVS = 4;
+  int rc;
+  ResArgs r = {};
+  r.nex = 1; r.d = I; r.x[0] = w.x; r.P[0] = w.P; r.a[0] = w.a; r.rows[0] = S;
+  // IN + position rows (row i of the group is position i % rows of its sequence), norm1 of layer 0
+  if ((rc = launch_wide<E_PART>(one(I, Kin, hp.ks_in, M(L.in), in, Kin, w.P, nullptr), WVS, st))) return rc;
+  r.mode = RES_POS16; r.ks = hp.ks_in; r.bias[0] = V(L.in_b); r.pos[0] = V(L.pos); r.pos_period = rows;
+  r.g[0] = V(L.blk0 + L.n1_w); r.b[0] = V(L.blk0 + L.n1_b);
+  if ((rc = launch_res(r, st))) return rc;
+  r.mode = RES_ADD16;
+  r.pos_period = 0;
+  for (int l = 0; l < dm->layers; ++l) {
+    const size_t B = L.blk0 + (size_t)l * L.blkstride;
+    if ((rc = launch_wide<E_BIAS16>(one(3 * I, I, 1, M(B + L.qkv), w.a, I, w.qkv, V(B + L.qkv_b)), hp.wv_qkv, st)))
+      return rc;
+    SelfArgs sa = {};
+    sa.nex = 1; sa.R = G; sa.H = H; sa.d = I; sa.hd = I / H; sa.bidir = 1;
+    sa.qkv[0] = w.qkv; sa.out[0] = w.a; sa.S[0] = S; sa.Sr[0] = rows;
+    if ((rc = launch_self_attn(sa, st))) return rc;
+    if ((rc = launch_wide<E_PART>(one(I, I, hp.ks_o, M(B + L.o), w.a, I, w.P, nullptr), WVS, st))) return rc;
+    r.ks = hp.ks_o; r.bias[0] = V(B + L.o_b); r.g[0] = V(B + L.n2_w); r.b[0] = V(B + L.n2_b);
+    if ((rc = launch_res(r, st))) return rc;
+    {
+      WArgs a = one(F, I, 1, M(B + L.w1), w.a, I, w.g, V(B + L.w1_b));
+      a.gelu_r16 = 1;
+      if ((rc = launch_wide<E_GELU16>(a, hp.wv_w1, st))) return rc;
+    }
+    if ((rc = launch_wide<E_PART>(one(I, F, hp.ks_w2, M(B + L.w2), w.g, F, w.P, nullptr), WVS, st))) return rc;
+    r.ks = hp.ks_w2; r.bias[0] = V(B + L.w2_b);
+    if (l + 1 < dm->layers) {
+      r.g[0] = V(B + L.blkstride + L.n1_w); r.b[0] = V(B + L.blkstride + L.n1_b);
+    } else {
+      r.g[0] = V(L.nrm_w); r.b[0] = V(L.nrm_b);
+    }
+    if ((rc = launch_res(r, st))) return rc;
+  }
+  if ((rc = launch_wide<E_PART>(one(Nout, I, hp.ks_out, M(L.out), w.a, I, w.P, nullptr), WVS, st))) return rc;
+  ReduceArgs ra = {};
+  ra.nex = 1; ra.nl = 1; ra.ks = hp.ks_out; ra.rows = S; ra.N = Nout; ra.d = Nout; ra.kv = 0;
+  ra.P[0] = w.P; ra.b[0] = V(L.out_b); ra.out[0] = out;
+  hipLaunchKernelGGL(k_reduce, dim3(256), dim3(256), 0, st, ra);
+  CFH_LAUNCH_CHECK();
+  return CFH_OK;
+}
+
+// Sequences a wide group holds for `batch` sequences of `rows` rows: as few groups of at most
+// WMAXR / rows as the batch needs, balanced; 1 (per-sequence launches) if the wide plan does not fit.
+int vae_group(const cfh_vae_dims* dm, int rows, int batch) {
+  const int gmax = WMAXR / rows;
+  if (batch < 2 || gmax < 2) return 1;
+  const int ng = (batch + gmax - 1) / gmax, G = (batch + ng - 1) / ng;
+  return G >= 2 && vae_wide_plan(dm, rows, G).ok ? G : 1;
+}
+
 int vae_run(const cfh_vae_dims* dm, const void* packed, const void* in, void* out, int batch, int rows,
             void* ws, void* stream, bool encode) {
   if (!vae_dims_ok(dm) || rows < 1 || rows > MAXR || rows > dm->max_rows) return CFH_E_UNSUPPORTED;
@@ -267,6 +399,24 @@ int vae_run(const cfh_vae_dims* dm, const void* packed, const void* in, void* ou
   const VaeWS w = vae_carve(p, (char*)ws);
   const HalfPlan& hp = encode ? p.enc : p.dec;
   const HalfLayout& hl = encode ? L.enc : L.dec;
+  const int G = vae_group(dm, rows, batch);
+  if (G > 1) {
+    const VaeWide pw = vae_wide_plan(dm, rows, G);
+    const VaeWS ww = vae_wide_carve(pw, dm, (char*)ws);
+    for (int b0 = 0; b0 < batch; b0 += G) {
+      const int g = std::min(G, batch - b0);
+      const h16* ib = (const h16*)in + (size_t)b0 * rows * hp.Kin;
+      h16* ob = (h16*)out + (size_t)b0 * rows * hp.Nout;
+      int rc;
+      if (g >= 2)
+        rc = run_half_wide(pw, encode ? pw.enc : pw.dec, hl, (const char*)packed, dm, rows, g, ib, ob, ww,
+                           (hipStream_t)stream);
+      else
+        rc = run_half(p, hp, hl, (const char*)packed, dm->layers, ib, ob, w, (hipStream_t)stream);
+      if (rc) return rc;
+    }
+    return CFH_OK;
+  }
   for (int b = 0; b < batch; ++b) {
     const h16* ib = (const h16*)in + (size_t)b * rows * hp.Kin;
     h16* ob = (h16*)out + (size_t)b * rows * hp.Nout;
@@ -342,7 +492,13 @@ int cfh_vae_caps(const cfh_vae_dims* dims, int rows, int64_t* ws_bytes) {
   if (!vae_dims_ok(dims) || rows < 1 || rows > MAXR || rows > dims->max_rows) return CFH_E_UNSUPPORTED;
   const VaePlan p = vae_plan(dims, rows);
   if (!p.ok) return CFH_E_UNSUPPORTED;
-  if (ws_bytes) *ws_bytes = (int64_t)vae_carve(p, nullptr).total;
+  // the per-sequence workspace, or a wide group's (every group size up to WMAXR / rows sequences)
+  size_t total = vae_carve(p, nullptr).total;
+  for (int G = 2; G * rows <= WMAXR; ++G) {
+    const VaeWide pw = vae_wide_plan(dims, rows, G);
+    if (pw.ok) total = std::max(total, vae_wide_carve(pw, dims, nullptr).total);
+  }
+  if (ws_bytes) *ws_bytes = (int64_t)total;
   return CFH_OK;
 }
 

@@ -215,7 +215,8 @@ int64_t cfh_vae_bytes(const cfh_vae_dims* dims);
 int cfh_vae_pack(const cfh_vae_dims* dims, const void* const* raw, int n_raw, void* packed, void* stream);
 
 /* 0 if this build runs `dims` on sequences of `rows` rows (rows <= 16 and <= max_rows), with the
- * workspace size in *ws_bytes; CFH_E_UNSUPPORTED otherwise. */
+ * workspace size in *ws_bytes (enough for any batch: a batch of sequences runs in groups of up to
+ * 128 / rows sequences stacked, one launch sequence a group); CFH_E_UNSUPPORTED otherwise. */
 int cfh_vae_caps(const cfh_vae_dims* dims, int rows, int64_t* ws_bytes);
 
 /* encode_sequence(hidden).mu (cf/vae/transformer_hidden.py:52-59): hidden [batch][rows][hidden]

@@ -84,7 +84,7 @@ def test_vae_matches_oracle(cuda, hidden, latent, inter, heads, vlayers):
 @pytest.mark.gpu
 def test_vae_batch_equals_single_sequences(cuda):
     """Sequences of a batch do not see each other: a batch of two encodes/decodes bit-identically to
-    the two sequences alone."""
+    the two sequences alone (width 320 is not a multiple of 128: the per-sequence launches)."""
     hidden = 1024
     cfg = _cfg(256, 320, 8, 1)
     W = {k: v.to(cuda) for k, v in _vae_weights(cfg, hidden, seed=2).items()}
@@ -96,6 +96,33 @@ def test_vae_batch_equals_single_sequences(cuda):
     dec1 = torch.cat([vae.decode(both[:1]).clone(), vae.decode(both[1:]).clone()], 0)
     torch.cuda.synchronize()
     assert torch.equal(both, one) and torch.equal(dec, dec1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B", [3, 20])
+def test_vae_wide_batch_matches_oracle(cuda, B):
+    """A batch of sequences at the shipped VAE's shapes (hidden 2560, latent 640, width 1920, 2
+    layers) runs as groups of stacked sequences through the wide kernels (B = 20: two groups of
+    10): each sequence's encode / decode within 2e-3 of the oracle and of the sequence alone."""
+    hidden = 2560
+    cfg = _cfg(640, 1920, 8, 2)
+    W = _vae_weights(cfg, hidden, seed=4)
+    vae = HiddenVAE(cfg, hidden, {k: v.to(cuda) for k, v in W.items()}, device=cuda)
+    h = synthetic_context(B, 8, hidden, seed=B).to(cuda)
+    print(f"[vae wide batch] B={B}", flush=True)
+    mu = vae.encode(h).clone()
+    dec = vae.decode(mu).clone()
+    mu1 = [vae.encode(h[b:b + 1]).clone() for b in range(B)]
+    dec1 = [vae.decode(mu[b:b + 1]).clone() for b in range(B)]
+    torch.cuda.synchronize()
+    V = ovae.vae_weights({k: to64(v) for k, v in W.items()})
+    for b in range(B):
+        rm = ovae.encode_sequence_mu(V, to64(h[b:b + 1]), _vcfg(cfg), "fp16")
+        rd = ovae.decode_sequence(V, to64(mu[b:b + 1]), _vcfg(cfg), "fp16")
+        e = (rel_err(to64(mu[b:b + 1]), rm), rel_err(to64(dec[b:b + 1]), rd),
+             rel_err(to64(mu[b:b + 1]), to64(mu1[b])), rel_err(to64(dec[b:b + 1]), to64(dec1[b])))
+        print(f"  sequence {b}: encode {e[0]:.2e} decode {e[1]:.2e} (vs alone {e[2]:.2e} {e[3]:.2e})", flush=True)
+        assert max(e) < TOL_FP16
 
 
 @pytest.mark.gpu

@@ -588,7 +588,7 @@ def gemm_bench(dev, iters=100, warmup=10):
     return times, nbytes, flops, (M, d, n, k)
 
 
-def batched_bench(dev, steps=3, warmup=1, B=32, d=4096, L=8, E=8, M=8192):
+def batched_bench(dev, steps=3, warmup=1, B=32, d=4096, L=8, E=8, M=8192, latent=False):
     """The batched drafting step: B requests, each a 5-token width-4 chain at d=4096 fp16 with the
     proposer's default two-pass head (M=8192 candidates shared across depths).  The flow drafts the
     requests in groups that share every weight stream (cfh_flow_group_size: 16 requests a group at
@@ -602,8 +602,17 @@ def batched_bench(dev, steps=3, warmup=1, B=32, d=4096, L=8, E=8, M=8192):
     from chain_flow_amd.flow import group_size
     from chain_flow_amd.shortlist import synthetic
     from chain_flow_amd.weights import make_weights, synthetic_context
+    from chain_flow_amd.config import TreeVAEFlowConfig
     K, Wd = 5, 4
-    cfg = flownet(d, layers=L, flow_steps=E)
+    if latent:
+        # the shipped latent drafter (hidden d, VAE latent 640, the flow inside it at that width)
+        cfg = TreeVAEFlowConfig(context_size=8, draft_length=8, chunk_size=4, expert_dim=d, num_heads=8,
+                                ffn_multiplier=6, num_drafter_layers=L, num_flow_steps=E, init_mode="delta",
+                                path_order=4, path_ffn_multiplier=2, markov_rank=256, latent_size=LATENT,
+                                vae_intermediate_size=VAE_INTER, vae_num_layers=VAE_LAYERS, vae_num_heads=8,
+                                vae_max_sequence_length=16)
+    else:
+        cfg = flownet(d, layers=L, flow_steps=E)
     W = make_weights(cfg, VOCAB, init="baseline", dtype=torch.float16, device=dev, base_seed=0, hidden=d)
     sl = synthetic(VOCAB, SHORTLIST_ROWS, seed=2)
     dr = Drafter(cfg, W, sl.to(dev), device=dev, twopass_m=M, twopass_shared=True)
@@ -661,11 +670,12 @@ def batched_bench(dev, steps=3, warmup=1, B=32, d=4096, L=8, E=8, M=8192):
     # the algorithm's bytes: every flow weight once for the whole batch (the reference's batched
     # path runs all 8 B rows against each weight tile); the kernels issue one stream per group, two
     # groups' streams side by side in every launch
-    fb = flow_bytes(d, L, E, cfg.num_chunks, fold=(d // cfg.num_heads) % 32 == 0)
+    fd = LATENT if latent else d
+    fb = flow_bytes(fd, L, E, cfg.num_chunks, fold=(fd // cfg.num_heads) % 32 == 0) + (vae_bytes(d) if latent else 0)
     return dict(flow_ms=flow_ms, head_ms=head_ms, pass_a_ms=pass_a_ms, pass_a_gemm_ms=pass_a_gemm_ms,
                 flow_bytes=fb, groups=groups,
                 pass_a_bytes=SHORTLIST_ROWS * d * 2 + B * K * d * 2 + B * K * SHORTLIST_ROWS * 2,
-                R=R, B=B, d=d, L=L, E=E, M=M, K=K, W=Wd)
+                R=R, B=B, d=d, L=L, E=E, M=M, K=K, W=Wd, latent=latent)
 
 
 def main():
@@ -682,6 +692,8 @@ def main():
     ap.add_argument("--twopass", type=int, default=0,
                     help="two-pass candidate head with M candidates (0: the one-pass head of the metric)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--latent", action="store_true",
+                    help="--workload batched: the shipped latent drafter (hidden 2560, VAE latent 640, L=8, E=2)")
     ap.add_argument("--no-graph", action="store_true",
                     help="skip the graph-replay timing (counter-collection runs: the profiler's counter "
                          "pass does not survive graph launches)")
@@ -725,16 +737,21 @@ def main():
         print(json.dumps(out), flush=True)
         return
     if args.workload == "batched":
-        r = batched_bench(dev)
+        r = batched_bench(dev, latent=True, d=2560, E=2) if args.latent else batched_bench(dev)
         ms = r["flow_ms"] + r["head_ms"]
         gbs = r["flow_bytes"] / (r["flow_ms"] * 1e-3) / 1e9
         out = {
-            "metric": f"us per batched draft step ({r['B']} seqs x {r['K']} tokens, d={r['d']} fp16, two-pass head)",
+            "metric": (f"us per batched draft step ({r['B']} seqs x {r['K']} tokens, "
+                       + (f"latent drafter hidden {r['d']} latent {LATENT}" if r["latent"] else f"d={r['d']}")
+                       + " fp16, two-pass head)"),
             "value": round(ms * 1e3, 1), "unit": "us per batched draft step", "n_gpus": 1, "steps": 3, "warmup": 1,
             "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
             "dtype": "fp16", "data": "synthetic (seeded N(0,0.02) weights, N(0,1) RMS-1 contexts)",
             "config": {"workload": f"batched chain draft: {r['B']} requests x {r['K']} tokens, width {r['W']}, "
-                                   f"d={r['d']} fp16, flow L={r['L']} E={r['E']} (requests drafted {r['R']} to a "
+                                   + (f"latent drafter (hidden {r['d']}, VAE latent {LATENT} width {VAE_INTER} "
+                                      f"{VAE_LAYERS}+{VAE_LAYERS} layers, the flow at the latent width) "
+                                      if r["latent"] else f"d={r['d']} ")
+                                   + f"fp16, flow L={r['L']} E={r['E']} (requests drafted {r['R']} to a "
                                    f"weight stream: {r['groups']} groups), two-pass head M={r['M']} shared over a "
                                    f"{SHORTLIST_ROWS}-row shortlist"},
             "breakdown_ms": {"flow": round(r["flow_ms"], 3), "head_beam": round(r["head_ms"], 3)},
@@ -742,9 +759,10 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                          "kernel": "flow pass (cfh_flow_integrate, request groups)", "algorithmic_bytes": r["flow_bytes"],
-                         "note": f"algorithmic bytes: every flow weight once for the whole batch; the kernels issue "
-                                 f"{r['groups']} weight streams ({r['R']} requests a group), two groups' streams "
-                                 f"side by side in each launch"},
+                         "note": f"algorithmic bytes: every flow weight once for the whole batch"
+                                 + (" (and the VAE's, encode + decode)" if r["latent"] else "")
+                                 + f"; the kernels issue {r['groups']} weight streams ({r['R']} requests a "
+                                 f"group), two groups' streams side by side in each launch"},
             "pass_a": {"rows": r["B"] * r["K"], "us": round(r["pass_a_ms"] * 1e3, 2),
                        "gemm_head_us": round(r["pass_a_gemm_ms"] * 1e3, 2),
                        "gemm_head_gbs": round(r["pass_a_bytes"] / (r["pass_a_gemm_ms"] * 1e-3) / 1e9, 1),

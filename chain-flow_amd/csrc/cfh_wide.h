@@ -54,8 +54,10 @@ struct WArgs {
   int map;             // workgroup order (set by launch_wide): MAP_PLAIN, MAP_PAIR or MAP_XCD
 };
 
-// Workgroup -> (entry, k-split, tile group) orders.  Workgroups go to the 8 XCDs round robin
-// (workgroup b to XCD b % 8), each XCD with its own L2.
+// Workgroup -> (entry, k-split, tile group) orders.  Workgroups go to the 8 XCDs round robin,
+// each XCD with its own L2, starting from an XCD that depends on the dispatches before the launch:
+// workgroups b and b' share an XCD when b = b' mod 8 (below, "XCD x" is the XCD of the workgroups
+// b = x mod 8, whichever it is).
 //   MAP_PLAIN: entry-major.
 //   MAP_PAIR:  workgroups b and b + 8 take the same unit of entries e and e + nex/2.
 //   MAP_XCD:   (split-K) XCD x takes every unit of the (entry, k-split) combinations x, x + 8, ...:
@@ -295,7 +297,6 @@ int wide_wv(int tiles, int units) {
   return best;
 }
 
-inline bool wide_xcd_off() { return false; }
 
 template <int EPI>
 int launch_wide(const WArgs& a0, int wv, hipStream_t st) {
@@ -309,7 +310,7 @@ int launch_wide(const WArgs& a0, int wv, hipStream_t st) {
   // the side-by-side order needs a whole number of 8-workgroup runs per half (narrow widths such as
   // d = 640 have 5 a k-split: their paired launches keep the plain order, still one launch for both)
   const bool pair_runs = a.pair && ((long long)(a.nex / 2) * a.ks * a.wg_per_kc) % 8 == 0;
-  if (a.ks > 1 && (a.nex * a.ks) % 8 == 0 && (!a.pair || ((a.nex / 2) * a.ks) % 8 == 0) && !wide_xcd_off())
+  if (a.ks > 1 && (a.nex * a.ks) % 8 == 0 && (!a.pair || ((a.nex / 2) * a.ks) % 8 == 0))
     a.map = MAP_XCD;
   else
     a.map = pair_runs ? MAP_PAIR : MAP_PLAIN;

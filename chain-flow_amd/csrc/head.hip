@@ -1102,8 +1102,6 @@ struct PathPlan {
   size_t off_P, off_a, off_up, off_g, off_dn, total;
 };
 
-inline bool path_unfused() { return false; }
-
 PathPlan path_plan(int M, int d, int ffn, int order) {
   PathPlan p;
   const int pf = ffn * d;
@@ -1111,7 +1109,7 @@ PathPlan path_plan(int M, int d, int ffn, int order) {
   p.up_ks = ksplit_for(1, pf / 16, d, M);
   p.dn_ks = ksplit_for(1, d / 16, pf, M);
   int wk, pfk;
-  p.fused = !path_unfused() && path_gemv_shape(pf / 16, d, &wk, &pfk) && path_gemv_shape(d / 16, pf, &wk, &pfk);
+  p.fused = path_gemv_shape(pf / 16, d, &wk, &pfk) && path_gemv_shape(d / 16, pf, &wk, &pfk);
   size_t off = 0;
   auto take = [&](size_t bytes) {
     const size_t o = off;

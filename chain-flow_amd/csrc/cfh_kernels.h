@@ -261,12 +261,13 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 // t, t + blockDim, ... (vals[k] = group k); two-pass moments; fp16 output.
 constexpr int ROWQ = ROWE / 4;   // float4 groups per thread
 
+template <int RQ = ROWQ>
 __device__ void ln_row4(const float4* vals, int d, const h16* g, const h16* b, h16* out, float* red) {
   const int nq = d / 4;
   // gamma and beta are loaded before the statistics, not after them
-  h16x4 gq[ROWQ], bq[ROWQ];
+  h16x4 gq[RQ], bq[RQ];
 #pragma unroll
-  for (int k = 0; k < ROWQ; ++k) {
+  for (int k = 0; k < RQ; ++k) {
     const int q = threadIdx.x + k * blockDim.x;
     if (q < nq) {
       gq[k] = *(const h16x4*)(g + q * 4);
@@ -275,14 +276,14 @@ __device__ void ln_row4(const float4* vals, int d, const h16* g, const h16* b, h
   }
   float s = 0.f;
 #pragma unroll
-  for (int k = 0; k < ROWQ; ++k) {
+  for (int k = 0; k < RQ; ++k) {
     const int q = threadIdx.x + k * blockDim.x;
     if (q < nq) s += (vals[k].x + vals[k].y) + (vals[k].z + vals[k].w);
   }
   const float mean = block_sum(s, red) / (float)d;
   float v = 0.f;
 #pragma unroll
-  for (int k = 0; k < ROWQ; ++k) {
+  for (int k = 0; k < RQ; ++k) {
     const int q = threadIdx.x + k * blockDim.x;
     if (q < nq) {
       const float a0 = vals[k].x - mean, a1 = vals[k].y - mean, a2 = vals[k].z - mean, a3 = vals[k].w - mean;
@@ -291,7 +292,7 @@ __device__ void ln_row4(const float4* vals, int d, const h16* g, const h16* b, h
   }
   const float rstd = 1.0f / sqrtf(block_sum(v, red) / (float)d + LN_EPS);
 #pragma unroll
-  for (int k = 0; k < ROWQ; ++k) {
+  for (int k = 0; k < RQ; ++k) {
     const int q = threadIdx.x + k * blockDim.x;
     if (q < nq) {
       h16x4 o;

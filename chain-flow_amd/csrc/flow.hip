@@ -94,11 +94,14 @@ struct RowsArgs {
   const h16* anchor[4];  // per expert, the group's anchor rows [R][d] (the anchored latent drafter), or null
 };
 
+template <int RQ>   // float4 groups a thread: d / 4 <= RQ * ROWT
 __global__ void __launch_bounds__(ROWT) k_rows(RowsArgs a) {
   __shared__ float red[ROWT / 64];
   const int r = blockIdx.x, d = a.d, nq = d / 4;
   const int req = r / a.KD, rr = r - req * a.KD;
-  float4 zv[ROWQ];
+  float4 zv[RQ];
+  h16x4 pp4[RQ], tt4[RQ];   // position and time rows of expert c2pre's next rows, loaded up front
+  int c2pre = -1;
   if (!a.euler) {
     // moments of context rows r, r + gridDim.x, ... (read by the cross K/V GEMV)
     for (int cr = r; cr < a.R * a.C; cr += gridDim.x) {
@@ -122,7 +125,7 @@ __global__ void __launch_bounds__(ROWT) k_rows(RowsArgs a) {
     const h16* given = a.z_out + (size_t)r * d;
     const float step = (float)(rr + 1);
 #pragma unroll
-    for (int k = 0; k < ROWQ; ++k) {
+    for (int k = 0; k < RQ; ++k) {
       const int q = threadIdx.x + k * blockDim.x;
       zv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
       if (q < nq) {
@@ -148,7 +151,7 @@ __global__ void __launch_bounds__(ROWT) k_rows(RowsArgs a) {
     // that chunk's own update wrote for the next step's rows
     if (a.last || rr / a.CS > a.only) return;
 #pragma unroll
-    for (int k = 0; k < ROWQ; ++k) {
+    for (int k = 0; k < RQ; ++k) {
       const int q = threadIdx.x + k * blockDim.x;
       zv[k] = q < nq ? *(const float4*)(a.z + (size_t)r * d + q * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
@@ -157,37 +160,48 @@ __global__ void __launch_bounds__(ROWT) k_rows(RowsArgs a) {
     const int Sc = (c + 1) * a.CS;
     const size_t pst = (size_t)(a.out_all ? a.R * Sc : a.CS) * d;
     const float* Pr = a.Pout[c] + (size_t)(a.out_all ? req * Sc + c * a.CS + i : i) * d;
-    float4 acc[ROWQ], zo[ROWQ];
+    // every load of the row in one batch: the out_proj partials, z, b_out and, unless this is the
+    // last step, the position and time rows of expert c's next rows (the first expert that reads
+    // this row), instead of a chain of dependent round trips
+    if (!a.last) c2pre = c;
+    float4 acc[RQ], zo[RQ];
+    h16x4 bo4[RQ];
 #pragma unroll
-    for (int k = 0; k < ROWQ; ++k) {
+    for (int k = 0; k < RQ; ++k) {
       const int q = threadIdx.x + k * blockDim.x;
       if (q < nq) {
         acc[k] = *(const float4*)(Pr + q * 4);
         zo[k] = *(const float4*)(a.z + (size_t)r * d + q * 4);
+        bo4[k] = *(const h16x4*)(a.bout[c] + q * 4);
+        if (c2pre >= 0) {
+          pp4[k] = *(const h16x4*)(a.pos[c] + (size_t)rr * d + q * 4);
+          tt4[k] = *(const h16x4*)(a.tau[c] + q * 4);
+        }
       }
     }
-    for (int kc = 1; kc < a.ks; kc += 2) {
-      float4 t[2][ROWQ];
+    constexpr int PB = RQ <= 2 ? 4 : 2;   // partial rows a batch (registers)
+    for (int kc = 1; kc < a.ks; kc += PB) {
+      float4 t[PB][RQ];
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
+      for (int u = 0; u < PB; ++u)
 #pragma unroll
-        for (int k = 0; k < ROWQ; ++k) {
+        for (int k = 0; k < RQ; ++k) {
           const int q = threadIdx.x + k * blockDim.x;
           t[u][k] = (q < nq && kc + u < a.ks) ? *(const float4*)(Pr + (kc + u) * pst + q * 4)
                                               : make_float4(0.f, 0.f, 0.f, 0.f);
         }
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
+      for (int u = 0; u < PB; ++u)
 #pragma unroll
-        for (int k = 0; k < ROWQ; ++k)
+        for (int k = 0; k < RQ; ++k)
           if (kc + u < a.ks) { acc[k].x += t[u][k].x; acc[k].y += t[u][k].y; acc[k].z += t[u][k].z; acc[k].w += t[u][k].w; }
     }
 #pragma unroll
-    for (int k = 0; k < ROWQ; ++k) {
+    for (int k = 0; k < RQ; ++k) {
       const int q = threadIdx.x + k * blockDim.x;
       zv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
       if (q < nq) {
-        const h16* bo = a.bout[c] + q * 4;
+        const h16x4 bo = bo4[k];
         float4 zn;
         zn.x = r16(zo[k].x + r16(a.dt * r16(acc[k].x + (float)bo[0])));
         zn.y = r16(zo[k].y + r16(a.dt * r16(acc[k].y + (float)bo[1])));
@@ -207,14 +221,20 @@ __global__ void __launch_bounds__(ROWT) k_rows(RowsArgs a) {
     if (rr >= (c2 + 1) * a.CS) continue;         // expert c2 reads z rows [0, (c2+1)*CS) of each draft
     const bool cur = rr >= c2 * a.CS;
     const size_t xr = (size_t)req * (c2 + 1) * a.CS + rr;   // the row in expert c2's request-major rows
-    float4 vals[ROWQ];
+    float4 vals[RQ];
 #pragma unroll
-    for (int k = 0; k < ROWQ; ++k) {
+    for (int k = 0; k < RQ; ++k) {
       const int q = threadIdx.x + k * blockDim.x;
       vals[k] = make_float4(0.f, 0.f, 0.f, 0.f);
       if (q < nq) {
-        const h16* pp = a.pos[c2] + (size_t)rr * d + q * 4;
-        const h16* tt = a.tau[c2] + q * 4;
+        h16x4 pp, tt;
+        if (c2 == c2pre) {
+          pp = pp4[k];
+          tt = tt4[k];
+        } else {
+          pp = *(const h16x4*)(a.pos[c2] + (size_t)rr * d + q * 4);
+          tt = *(const h16x4*)(a.tau[c2] + q * 4);
+        }
         const h16* an = a.anchor[c2] ? a.anchor[c2] + (size_t)req * d + q * 4 : nullptr;
         float o[4] = {zv[k].x, zv[k].y, zv[k].z, zv[k].w};
 #pragma unroll
@@ -228,8 +248,16 @@ __global__ void __launch_bounds__(ROWT) k_rows(RowsArgs a) {
         *(float4*)(a.x[c2] + xr * d + q * 4) = vals[k];
       }
     }
-    ln_row4(vals, d, a.g[c2], a.b[c2], a.a[c2] + xr * d, red);
+    ln_row4<RQ>(vals, d, a.g[c2], a.b[c2], a.a[c2] + xr * d, red);
   }
+}
+
+// k_rows with the fewest float4 groups a thread that cover a row of d
+void launch_rows(const RowsArgs& r, int rows, hipStream_t st) {
+  const int nq = r.d / 4;
+  if (nq <= ROWT) hipLaunchKernelGGL(k_rows<1>, dim3(rows), dim3(ROWT), 0, st, r);
+  else if (nq <= 2 * ROWT) hipLaunchKernelGGL(k_rows<2>, dim3(rows), dim3(ROWT), 0, st, r);
+  else hipLaunchKernelGGL(k_rows<ROWQ>, dim3(rows), dim3(ROWT), 0, st, r);
 }
 
 // XATT: the cross attention of one block pass from the per-draft factors A_h = Wq_h^T K_h^T and
@@ -1322,7 +1350,7 @@ int integrate_wide(const Plan& p, const cfh_flow_dims* dm, const cfh::ExpertLayo
       r.anchor[c] = anchor ? (const h16*)anchor + ((size_t)c * batch + G.g0) * d : nullptr;
       if (s >= 0) { r.Pout[c] = G.w.P[c]; r.bout[c] = (const h16*)PTR(c, L.out_b); }
     }
-    hipLaunchKernelGGL(k_rows, dim3(G.Rg * KD), dim3(ROWT), 0, st, r);
+    launch_rows(r, G.Rg * KD, st);
     CFH_LAUNCH_CHECK();
     return CFH_OK;
   };
@@ -1424,7 +1452,7 @@ int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* expert
         r.a[c] = w.abuf[c];
         r.anchor[c] = anchor ? (const h16*)anchor + ((size_t)c * batch + g0) * d : nullptr;
       }
-      hipLaunchKernelGGL(k_rows, dim3(Rg * KD), dim3(ROWT), 0, st, r);
+      launch_rows(r, Rg * KD, st);
       CFH_LAUNCH_CHECK();
     }
     // ---- cross K/V of every block (once per draft), the group's context rows together
@@ -1551,7 +1579,7 @@ int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* expert
           if ((rc = block_pass(p, L, w, experts, l, Rg, st, 0, nch))) return rc;
         if ((rc = out_proj(0, nch, st))) return rc;
         const RowsArgs r = rows_args(s, -1);
-        hipLaunchKernelGGL(k_rows, dim3(Rg * KD), dim3(ROWT), 0, st, r);
+        launch_rows(r, Rg * KD, st);
         CFH_LAUNCH_CHECK();
         continue;
       }
@@ -1575,7 +1603,7 @@ int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* expert
         if (c > 0) CFH_HIP(hipStreamWaitEvent(sc, cp.up[c - 1], 0));
         if (c + 1 < nch && s > 0) CFH_HIP(hipStreamWaitEvent(sc, cp.down[c], 0));
         const RowsArgs r = rows_args(s, c);
-        hipLaunchKernelGGL(k_rows, dim3(Rg * KD), dim3(ROWT), 0, sc, r);
+        launch_rows(r, Rg * KD, sc);
         CFH_LAUNCH_CHECK();
         if (c + 1 < nch) CFH_HIP(hipEventRecord(cp.up[c], sc));
         if (c > 0) CFH_HIP(hipEventRecord(cp.down[c - 1], sc));

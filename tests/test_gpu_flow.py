@@ -212,11 +212,12 @@ def test_packed_batch_matches_oracle_per_request(cuda, d, B, layers):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("mode,B", [("repeat_last", 1), ("noise", 1), ("noise", 2)])
+@pytest.mark.parametrize("mode,B", [("repeat_last", 1), ("noise", 1), ("noise", 2), ("repeat_last", 6), ("noise", 6)])
 def test_init_modes_match_oracle(cuda, mode, B):
     """init_latents' other modes (cf/drafters/tree_flow.py:150-161): "repeat_last" starts every
     draft row from the last context row; "noise" from randn * noise_scale drawn with torch's
-    generator, which the oracle is given (the same seeded draw)."""
+    generator, which the oracle is given (the same seeded draw).  B = 6 (48 rows) runs as one wide
+    request group, whose row kernels build the initial latents of every request."""
     import dataclasses
     cfg = dataclasses.replace(flownet(512, layers=2, flow_steps=2), init_mode=mode, noise_scale=0.5)
     W = _flow_weights(cfg)

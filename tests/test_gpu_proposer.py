@@ -14,7 +14,7 @@ from conftest import oracle_numerics, to64
 from chain_flow_amd import shortlist as slmod
 from chain_flow_amd.config import flownet
 from chain_flow_amd.vllm_plugin import flow_proposer as fp
-from chain_flow_amd.weights import make_weights, param_specs
+from chain_flow_amd.weights import make_weights
 from oracle import beam as obeam
 from oracle import flow as oflow
 from oracle import head as ohead

@@ -30,7 +30,6 @@ drafter-level helpers take the drafter's names (``vae.encoder_in.weight``, ``exp
 """
 from __future__ import annotations
 
-
 from oracle import flow as oflow
 from oracle.flow import _lin, attention, gelu, layer_norm, r16
 

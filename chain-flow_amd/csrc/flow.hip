@@ -470,6 +470,286 @@ int launch_xattn(const XattArgs& a, hipStream_t st) {
   return CFH_OK;
 }
 
+// XBLK: the residual row after the self attention, the folded cross attention and the residual row
+// after it, for one expert's S <= 8 rows in ONE workgroup, in place of RES -> XATT -> RES (one-request
+// flows of width d <= 640, where those three launches cost ~17 us a block pass whatever they move):
+//   x1 = x + (sum_kc P[kc] + b_o);  xn = fp16(LN_cross(fp16(x1)))
+//   scores_h[r][c] = (xn[r] . A_h[c] + sb_h[c]) / sqrt(hd),  P_h = softmax_c
+//   x2 = x1 + (sum_h sum_c P_h[r][c] B_h[c][n] + b_oc);  x <- x2;  a = fp16(LN_ffn(fp16(x2)))
+// (fp16 residual mode: each add rounded as in RES).  The same operations as those kernels; the sums
+// over d (LayerNorm statistics, scores) and over the heads' outputs run in another order, all in
+// fp32.  The workgroup is one chain of dependent steps, so every load that does not depend on it --
+// the partial rows, the residual row, both LayerNorms' weights, this wave's A and B fragments -- is
+// issued first, and each phase then reads registers and LDS only.  Phases: a wave a row (x1,
+// LN_cross into LDS); the scores of two heads as one 16 x 16 MFMA tile (rows x both heads' C <= 8
+// context rows), k-steps split over two waves; the softmax, 8 lanes a (head, row); the heads'
+// outputs as 16-column MFMA tiles over k = (head, context row); a wave a row (LN_ffn).
+// Every load is unconditional, from a clamped address, the value selected afterwards: a load under
+// a branch is waited for before the branch joins.
+struct XbEx {
+  float* x;               // residual rows [S][d], x -> x2 in place
+  const float* P;         // self-attention out_proj partials [ks][S][d]
+  h16* a;                 // out: LN_ffn rows [S][d]
+  const h16* bo;          // self_attn.out_proj.bias
+  const h16* gx;          // cross_norm weight / bias
+  const h16* bx;
+  const h16* A;           // this layer's A [H][C][d], each head's [C][d] in frag_index order
+  const h16* Bf;          // this layer's B [H][C][d]
+  const float* sb;        // this layer's sb [H][C]
+  const h16* boc;         // cross_attn.out_proj.bias
+  const h16* gf;          // ffn LayerNorm weight / bias
+  const h16* bf;
+  int S;
+};
+
+struct XblkArgs {
+  XbEx ex[4];
+  int nex, d, H, C, ks, mode;
+  float scale;
+};
+
+constexpr int XBT = 512;        // threads of an XBLK workgroup: 8 waves, 256 VGPRs a lane
+constexpr int XBR = XBT / 64;   // most rows (a wave a row)
+constexpr int XBH = 8;          // most heads
+constexpr int XBC = 8;          // most context rows (two heads' scores share a 16-column tile)
+
+size_t xblock_lds(int S, int d, int H) {
+  return (size_t)S * d * 4 + (size_t)S * (d + 8) * 2 + (size_t)XBR * 256 * 4 + (size_t)H * XBR * XBC * 4;
+}
+
+template <int MODE>   // RES_ADD32 or RES_ADD16
+__device__ __forceinline__ float xb_upd(float x, float s, float b) {
+  return MODE == RES_ADD16 ? r16(x + r16(s + b)) : x + (s + b);
+}
+
+__device__ __forceinline__ float h_lo(unsigned u) { return (float)__builtin_bit_cast(h16, (unsigned short)(u & 0xFFFFu)); }
+__device__ __forceinline__ float h_hi(unsigned u) { return (float)__builtin_bit_cast(h16, (unsigned short)(u >> 16)); }
+
+// LN of the fp16-rounded row v (NQJ float4 groups a lane, q = lane + 64 j) into out[0 .. d)
+template <int NQJ>
+__device__ __forceinline__ void xb_ln(float4 (&v)[NQJ], int d, const h16x4 (&g)[NQJ], const h16x4 (&b)[NQJ], h16* out) {
+  const int lane = threadIdx.x & 63, nq = d / 4;
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < NQJ; ++j) {
+    v[j] = lane + 64 * j < nq ? r16x4(v[j]) : make_float4(0.f, 0.f, 0.f, 0.f);
+    s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+  }
+  const float mean = wave_sum(s) / (float)d;
+  float q2 = 0.f;
+#pragma unroll
+  for (int j = 0; j < NQJ; ++j) {
+    const float a0 = v[j].x - mean, a1 = v[j].y - mean, a2 = v[j].z - mean, a3 = v[j].w - mean;
+    if (lane + 64 * j < nq) q2 += (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
+  }
+  const float rstd = 1.0f / sqrtf(wave_sum(q2) / (float)d + LN_EPS);
+#pragma unroll
+  for (int j = 0; j < NQJ; ++j) {
+    const int q = lane + 64 * j;
+    h16x4 o;
+    o[0] = (h16)((v[j].x - mean) * rstd * (float)g[j][0] + (float)b[j][0]);
+    o[1] = (h16)((v[j].y - mean) * rstd * (float)g[j][1] + (float)b[j][1]);
+    o[2] = (h16)((v[j].z - mean) * rstd * (float)g[j][2] + (float)b[j][2]);
+    o[3] = (h16)((v[j].w - mean) * rstd * (float)g[j][3] + (float)b[j][3]);
+    if (q < nq) *(h16x4*)(out + q * 4) = o;
+  }
+}
+
+// MODE: residual update; NQJ: float4 groups a lane in a row (d <= 256 NQJ); KP: partial rows
+// loaded up front (ks <= KP); TPW >= d / 128: column tiles of B a wave holds (and 2 TPW >= d / 64
+// k-steps of A, half of d).
+template <int MODE, int NQJ, int KP, int TPW>
+__global__ void __launch_bounds__(XBT) k_xblock(XblkArgs a) {
+  extern __shared__ __align__(16) float xl[];
+  constexpr int XBA = 2 * TPW;
+  const XbEx& ex = a.ex[blockIdx.x];
+  const int S = ex.S, d = a.d, H = a.H, C = a.C, ks = a.ks, nq = d / 4, ldn = d + 8;
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  float* x1 = xl;                                   // [S][d]: x1, then x2
+  h16* xn = (h16*)(x1 + (size_t)S * d);             // [S][ldn]
+  float* red = (float*)(xn + (size_t)S * ldn);      // [XBR][256] score tiles
+  float* Pp = red + XBR * 256;                      // [H][XBR][XBC] probabilities
+  const size_t Sd = (size_t)S * d;
+  // ---- loads first.  Row phases: this wave's row (clamped), its partials, residual and weights
+  const int rw = min(wave, S - 1);
+  float4 pv[KP][NQJ], xo[NQJ];
+  h16x4 bo[NQJ], gx[NQJ], bx[NQJ], gf[NQJ], bf[NQJ];
+#pragma unroll
+  for (int j = 0; j < NQJ; ++j) {
+    const int q = min(lane + 64 * j, nq - 1);
+#pragma unroll
+    for (int u = 0; u < KP; ++u) pv[u][j] = *(const float4*)(ex.P + min(u, ks - 1) * Sd + (size_t)rw * d + q * 4);
+    xo[j] = *(const float4*)(ex.x + (size_t)rw * d + q * 4);
+    bo[j] = *(const h16x4*)(ex.bo + q * 4);
+    gx[j] = *(const h16x4*)(ex.gx + q * 4);
+    bx[j] = *(const h16x4*)(ex.bx + q * 4);
+    gf[j] = *(const h16x4*)(ex.gf + q * 4);
+    bf[j] = *(const h16x4*)(ex.bf + q * 4);
+  }
+  // scores: wave = pair + 4 kgrp takes heads 2 pair, 2 pair + 1 (tile columns ci < 8, >= 8) over
+  // k-steps [kgrp half, ...); lanes of context rows past C or heads past H load clamped rows, whose
+  // scores are masked
+  const int ns = d / 32, half = (ns + 1) / 2, pair = wave & 3, st0 = (wave >> 2) * half;
+  const int ci = lane & 15, kg = lane >> 4;
+  const int hh = min(2 * pair + (ci >> 3), H - 1), cc = min(ci & 7, C - 1);
+  const h16* arow = ex.A + (size_t)hh * C * d + ((size_t)kg * C + cc) * 8;
+  const h16x8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+  h16x8 av[XBA];
+#pragma unroll
+  for (int u = 0; u < XBA; ++u) av[u] = *(const h16x8*)(arow + (size_t)min(st0 + u, ns - 1) * 32 * C);
+  // the softmax thread's score bias: head t >> 6, row (t >> 3) & 7, context row t & 7
+  const float sbv = ex.sb[min(t >> 6, H - 1) * C + min(t & 7, C - 1)];
+  // the heads' outputs as MFMA tiles (rows x 16 columns, k = 8 h + c over four heads a k-step): this
+  // wave's column tiles T = wave + 8 u; lane (n, kg) holds B[h][c][16 T + n] for head h = 4 kc + kg,
+  // c = 0 .. 7 (rows past C and heads past H clamped; their probabilities are zero)
+  const int ntile = d / 16;
+  h16x8 bfr[TPW][2];
+  h16 bocv[TPW];
+#pragma unroll
+  for (int u = 0; u < TPW; ++u) {
+    const int n = 16 * min(wave + 8 * u, ntile - 1) + ci;
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) {
+      const h16* bp = ex.Bf + (size_t)min(4 * kc + kg, H - 1) * C * d + n;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) bfr[u][kc][c] = bp[(size_t)min(c, C - 1) * d];
+    }
+    bocv[u] = ex.boc[n];
+  }
+  // ---- x1 = x + (sum of the partials in order + b_o); LN_cross -> xn
+  if (wave < S) {
+    float4 v[NQJ];
+#pragma unroll
+    for (int j = 0; j < NQJ; ++j) {
+      v[j] = pv[0][j];
+#pragma unroll
+      for (int u = 1; u < KP; ++u)
+        if (u < ks) { v[j].x += pv[u][j].x; v[j].y += pv[u][j].y; v[j].z += pv[u][j].z; v[j].w += pv[u][j].w; }
+      float4 y;
+      y.x = xb_upd<MODE>(xo[j].x, v[j].x, (float)bo[j][0]);
+      y.y = xb_upd<MODE>(xo[j].y, v[j].y, (float)bo[j][1]);
+      y.z = xb_upd<MODE>(xo[j].z, v[j].z, (float)bo[j][2]);
+      y.w = xb_upd<MODE>(xo[j].w, v[j].w, (float)bo[j][3]);
+      const int q = lane + 64 * j;
+      if (q < nq) *(float4*)(x1 + (size_t)wave * d + q * 4) = y;
+      v[j] = y;
+    }
+    xb_ln<NQJ>(v, d, gx, bx, xn + (size_t)wave * ldn);
+  }
+  __syncthreads();
+  // ---- score tiles (A operand: xn rows, rows past S read row 0 and are never used)
+  if (2 * pair < H) {
+    const h16* xrow = xn + (size_t)(ci < S ? ci : 0) * ldn + kg * 8;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < XBA; ++u) {
+      const int st = st0 + u;
+      const bool in = u < half && st < ns;
+      acc = mfma_f16(*(const h16x8*)(xrow + min(st, ns - 1) * 32), in ? av[u] : zero8, acc);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) red[wave * 256 + (4 * kg + q) * 16 + ci] = acc[q];
+  }
+  __syncthreads();
+  // ---- softmax over the context rows, 8 lanes a (head, row)
+  {
+    const int h = t >> 6, r = (t >> 3) & 7, c = t & 7, pr = h >> 1, n = (h & 1) * 8 + c;
+    if (h < H) {
+      const float v = red[pr * 256 + r * 16 + n] + red[(pr + 4) * 256 + r * 16 + n];
+      const bool ok = r < S && c < C;
+      const float sc = ok ? (v + sbv) * a.scale : -INFINITY;
+      float m = sc;
+      m = fmaxf(m, dpp_f32<DPP_XOR1>(m));
+      m = fmaxf(m, dpp_f32<DPP_XOR2>(m));
+      m = fmaxf(m, dpp_f32<DPP_HMIRROR>(m));
+      const float z = ok ? expf(sc - m) : 0.f;
+      float sum = z;
+      sum += dpp_f32<DPP_XOR1>(sum);
+      sum += dpp_f32<DPP_XOR2>(sum);
+      sum += dpp_f32<DPP_HMIRROR>(sum);
+      Pp[(h * XBR + r) * XBC + c] = ok ? z * (1.0f / sum) : 0.f;
+    }
+  }
+  __syncthreads();
+  // ---- x2 = x1 + (sum_h P_h B_h + b_oc) as MFMA tiles.  The probabilities enter as fp16 pairs
+  // p = hi + lo (hi = fp16(p), lo = fp16(p - hi)), so the products keep ~22 bits of p and every sum
+  // is in fp32 (the sums over the context rows and heads in the MFMA's order)
+  {
+    const int r = ci;
+    h16x8 ph[2], pl[2];
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) {
+      const int h = 4 * kc + kg;
+      const bool in = h < H && r < XBR;
+      const float* pp = Pp + (min(h, H - 1) * XBR + min(r, XBR - 1)) * XBC;
+      const float4 p0 = *(const float4*)pp, p1 = *(const float4*)(pp + 4);
+      const float pc[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const float v = in ? pc[c] : 0.f;
+        ph[kc][c] = (h16)v;
+        pl[kc][c] = (h16)(v - (float)ph[kc][c]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < TPW; ++u) {
+      const int T = wave + 8 * u;
+      if (T >= ntile) break;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        if (4 * kc >= H) break;
+        acc = mfma_f16(ph[kc], bfr[u][kc], acc);
+        acc = mfma_f16(pl[kc], bfr[u][kc], acc);
+      }
+      const int n = 16 * T + ci;
+      const float b = (float)bocv[u];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int i = 4 * kg + q;
+        if (i < S) {
+          const float y = xb_upd<MODE>(x1[(size_t)i * d + n], acc[q], b);
+          x1[(size_t)i * d + n] = y;
+          ex.x[(size_t)i * d + n] = y;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // ---- LN_ffn of x2, a wave a row
+  if (wave < S) {
+    float4 v[NQJ];
+#pragma unroll
+    for (int j = 0; j < NQJ; ++j) v[j] = *(const float4*)(x1 + (size_t)wave * d + min(lane + 64 * j, nq - 1) * 4);
+    xb_ln<NQJ>(v, d, gf, bf, ex.a + (size_t)wave * d);
+  }
+}
+
+template <int MODE>
+void launch_xblock_m(const XblkArgs& a, size_t lds, hipStream_t st) {
+  const dim3 g(a.nex), b(XBT);
+  if (a.d <= 512) {
+    if (a.ks <= 4) hipLaunchKernelGGL((k_xblock<MODE, 2, 4, 4>), g, b, lds, st, a);
+    else hipLaunchKernelGGL((k_xblock<MODE, 2, 8, 4>), g, b, lds, st, a);
+  } else {
+    hipLaunchKernelGGL((k_xblock<MODE, 3, 4, 5>), g, b, lds, st, a);   // (eight partial rows there spill)
+  }
+}
+
+int launch_xblock(const XblkArgs& a, hipStream_t st) {
+  int smax = 0;
+  for (int e = 0; e < a.nex; ++e) smax = std::max(smax, a.ex[e].S);
+  if (a.nex < 1 || a.nex > 4 || smax < 1 || smax > XBR || a.d > 640 || a.d % 32 || a.C < 1 || a.C > XBC ||
+      a.H < 1 || a.H > XBH || a.ks < 1 || a.ks > (a.d <= 512 ? 8 : 4) || (a.mode != RES_ADD32 && a.mode != RES_ADD16))
+    return CFH_E_UNSUPPORTED;
+  const size_t lds = xblock_lds(smax, a.d, a.H);
+  if (lds > 64 * 1024) return CFH_E_UNSUPPORTED;
+  if (a.mode == RES_ADD16) launch_xblock_m<RES_ADD16>(a, lds, st);
+  else launch_xblock_m<RES_ADD32>(a, lds, st);
+  CFH_LAUNCH_CHECK();
+  return CFH_OK;
+}
+
 // Launch shapes of the wide kernels with `groups` request groups a launch.
 struct WideShape {
   int groups;
@@ -492,6 +772,8 @@ struct Plan {
   int ks_fold, S_fold; // the factor launch's k-chunks and operand rows
   bool conc;          // chunk experts on concurrent streams within an Euler step (conc_experts)
   int wpb_fold, xnb;  // fold hoist launch waves / XATT column blocks per (expert, head)
+  bool xblk;          // one request, folded, d <= 640: residual, cross attention and residual
+                      // rows in one XBLK launch (k_xblock) instead of three
   bool wide;          // more than two requests a group: every row of the group shares each weight
                       // stream through the chunked-staging kernels (cfh_wide.h)
   WideShape ws[2];    // wide launch shapes for one group a launch, and for two (ws[1].ok: a batch of
@@ -689,6 +971,8 @@ Plan make_plan(const cfh_flow_dims* dm, int R = 1) {
          !stream_check(S_BUF, sa(p.fd, p.d, 1, p.wpb_w1, 1), p.Smax) &&
          !stream_check(S_BUF, sa(p.d, p.fd, p.ks_w2, p.wpb_w2, 1), p.Smax) &&
          !stream_check(S_BUF, sa(p.d, p.d, p.ks_out, p.wpb_out, 1), out_rows);
+  p.xblk = p.ok && p.fold && R == 1 && p.d <= 640 && p.d % 32 == 0 && p.H <= XBH && p.Ct <= XBC &&
+           p.Smax <= XBR && p.ks_att <= (p.d <= 512 ? 8 : 4) && xblock_lds(p.Smax, p.d, p.H) <= 64 * 1024;
   return p;
 }
 
@@ -782,7 +1066,7 @@ WS expert_view(const WS& w, int c0) {
 // beside its own: measured -0.2 ms a draft at d = 5120, no change at d = 2560 or 4096.
 constexpr int STAGGER_AT = 5;
 
-// The eight launches of block l (nine unfolded) for chunk experts c0 .. c0 + nc - 1, every launch
+// The eight launches of block l (nine unfolded, six with XBLK) for chunk experts c0 .. c0 + nc - 1, every launch
 // covering those experts; `mark`, if given, is recorded after the block's STAGGER_AT-th launch.
 int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const void* const* experts_all,
                int l, int Rg, hipStream_t st, int c0, int nc, hipEvent_t mark = nullptr) {
@@ -794,8 +1078,9 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
   auto S_of = [&](int c) { return Rg * (c0 + c + 1) * p.CS; };   // rows of expert c0 + c: Rg requests
   auto Sr_of = [&](int c) { return (c0 + c + 1) * p.CS; };       // rows per request
   int rc, launched = 0;
+  const int stagger = p.xblk ? STAGGER_AT - 2 : STAGGER_AT;   // (XBLK: two launches fewer before W1)
   auto done = [&]() -> int {
-    if (mark && ++launched == STAGGER_AT) CFH_HIP(hipEventRecord(mark, st));
+    if (mark && ++launched == stagger) CFH_HIP(hipEventRecord(mark, st));
     return CFH_OK;
   };
   // QKV: q, k, v = fp16(LN_self(x) W_in^T + b_in), full-K tiles
@@ -824,6 +1109,24 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
     }
     if ((rc = launch_stream<S_SELF, E_PART>(a, p.Smax, st)) || (rc = done())) return rc;
   }
+  // XBLK: residual + LN_cross, the folded cross attention, residual + LN_ffn in one launch
+  if (p.xblk) {
+    XblkArgs x = {};
+    x.nex = nch; x.d = d; x.H = p.H; x.C = Cg; x.ks = p.ks_att; x.mode = p.res_mode;
+    x.scale = 1.0f / sqrtf((float)p.hd);
+    const size_t per_l = (size_t)p.H * Cg * d;
+    for (int c = 0; c < nch; ++c) {
+      XbEx& e = x.ex[c];
+      e.x = w.x[c]; e.P = w.P[c]; e.a = w.abuf[c]; e.S = S_of(c);
+      e.bo = (const h16*)PTR(c, B + L.o_b);
+      e.gx = (const h16*)PTR(c, B + L.xn_w); e.bx = (const h16*)PTR(c, B + L.xn_b);
+      e.A = w.fa[c] + (size_t)l * per_l; e.Bf = w.fb[c] + (size_t)l * per_l;
+      e.sb = w.fsb[c] + (size_t)l * p.H * Cg;
+      e.boc = (const h16*)PTR(c, B + L.oc_b);
+      e.gf = (const h16*)PTR(c, B + L.fn_w); e.bf = (const h16*)PTR(c, B + L.fn_b);
+    }
+    if ((rc = launch_xblock(x, st)) || (rc = done())) return rc;
+  }
   ResArgs r = {};
   r.nex = nch; r.d = d; r.mode = p.res_mode;
   for (int c = 0; c < nch; ++c) { r.x[c] = w.x[c]; r.P[c] = w.P[c]; r.a[c] = w.abuf[c]; r.rows[c] = S_of(c); }
@@ -834,9 +1137,9 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
     r.g[c] = (const h16*)PTR(c, B + L.xn_w); r.b[c] = (const h16*)PTR(c, B + L.xn_b);
   }
   r.pack = p.fold;   // the folded cross attention takes LN_cross(x) as an MFMA operand image
-  if ((rc = launch_res(r, st)) || (rc = done())) return rc;
+  if (!p.xblk && ((rc = launch_res(r, st)) || (rc = done()))) return rc;
   r.pack = 0;
-  if (p.fold) {
+  if (p.fold && !p.xblk) {
     XattArgs x = {};
     x.nex = nch; x.d = d; x.H = p.H; x.C = Cg; x.Cq = p.C; x.nb = p.xnb; x.scale = 1.0f / sqrtf((float)p.hd);
     x.nsg = 1;
@@ -880,7 +1183,7 @@ int block_pass(const Plan& p, const cfh::ExpertLayout& L, const WS& w_all, const
     r.bias[c] = (const h16*)PTR(c, B + L.oc_b);
     r.g[c] = (const h16*)PTR(c, B + L.fn_w); r.b[c] = (const h16*)PTR(c, B + L.fn_b);
   }
-  if ((rc = launch_res(r, st)) || (rc = done())) return rc;
+  if (!p.xblk && ((rc = launch_res(r, st)) || (rc = done()))) return rc;
   // W1: g = fp16(gelu(LN_ffn(x) W1^T + b1)), full-K tiles
   {
     SArgs a = {};

@@ -103,21 +103,26 @@ def test_row_topk_bit_exact(cuda, k):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("nlive", [1, 2, 3, 4])
-def test_path_residual_matches_oracle(cuda, nlive):
+@pytest.mark.parametrize("nlive,M", [(0, 4), (1, 4), (2, 4), (3, 4), (4, 4), (4, 16), (2, 13)])
+def test_path_residual_matches_oracle(cuda, nlive, M):
+    """Offsets of the live ancestors + masked sum, LayerNorm, the 2x MLP, plus the marginal hidden;
+    nlive = 0 (no offset live) is checked against every ancestor masked, the oracle's form of an
+    empty path; 16 rows fill one launch sequence, 13 leave a ragged last 16-row tile."""
     d, V = 512, 4096
     cfg, W = _head_weights(d, V)
     ph = PathHead({k: v.to(cuda) for k, v in W.items()}, W["embed_tokens.weight"].to(cuda), cfg.path_order,
                   cfg.path_ffn_multiplier, cuda)
-    g = torch.Generator().manual_seed(5)
-    M = 4
+    g = torch.Generator().manual_seed(5 + M)
     lastp = torch.randint(0, V, (M, cfg.path_order), generator=g, dtype=torch.int32)
     lastp[1, 2:] = -1
     lastp[3, 1:] = -1
+    lastp[M - 1, :] = -1                                   # a row with no ancestor at all
     pred = torch.randn(d, generator=g).half()
     got = to64(ph.hidden(lastp.to(cuda), nlive, pred.to(cuda)))
     W64 = {k: to64(v) for k, v in W.items() if k.startswith("path_head.")}
-    res = ohead.path_residual(W64, to64(W["embed_tokens.weight"]), lastp.long().numpy(), nlive, cfg.path_order)
+    lp_ref = lastp.long().numpy() if nlive > 0 else np.full((M, cfg.path_order), -1)
+    res = ohead.path_residual(W64, to64(W["embed_tokens.weight"]), lp_ref, nlive if nlive > 0 else None,
+                              cfg.path_order)
     ref = ohead.r16(to64(pred)[None] + res, "fp16")
     assert rel_err(got, ref) < 2e-3
 

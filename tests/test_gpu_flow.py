@@ -177,6 +177,28 @@ def test_flow_latent_widths_match_oracle(cuda, d, heads, layers, steps):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("d,heads,ctx,kd,cs", [(640, 8, 4, 8, 4), (640, 8, 6, 8, 4), (320, 4, 8, 8, 4),
+                                               (512, 8, 3, 4, 4), (640, 8, 8, 4, 2), (448, 7, 5, 8, 4)])
+def test_flow_one_launch_cross_attention_shapes(cuda, d, heads, ctx, kd, cs):
+    """One-request flows of width <= 640 run the residual rows and the folded cross attention as
+    one launch a block pass; its edge cases against the oracle: fewer than 8 context rows (4, 6, 3,
+    5), four and seven heads (a pair of heads a score tile, the last pair half empty), two partial
+    rows of the out-projection, a single expert of 4 rows, experts of 2 and 4 rows."""
+    cfg = flownet(d, layers=2, flow_steps=2, num_heads=heads, context_size=ctx, draft_length=kd, chunk_size=cs)
+    W = _flow_weights(cfg, seed=17)
+    c = synthetic_context(1, cfg.context_size, d, seed=8)
+    print(f"[flow one-launch xattn] d={d} H={heads} C={ctx} draft={kd} chunk={cs}", flush=True)
+    ff = FusedFlow(cfg, {k: v.to(cuda) for k, v in W.items()}, device=cuda)
+    z = ff.predict_hidden(c.to(cuda))
+    torch.cuda.synchronize()
+    ref = oflow.predict_hidden(weights64(W), to64(c), _ocfg(cfg), numerics=oracle_numerics(cfg))
+    err = rel_err(to64(z), ref)
+    print(f"  rel err {err:.3e}", flush=True)
+    assert np.isfinite(to64(z)).all()
+    assert err < TOL_FP16
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("d,B,layers", [(512, 2, 2), (512, 5, 1), (640, 3, 1), (1024, 2, 2), (4096, 2, 1),
                                         (1024, 3, 2), (1024, 16, 1), (1024, 21, 1), (1024, 40, 1), (2048, 8, 1),
                                         (4096, 5, 1), (640, 20, 2)])

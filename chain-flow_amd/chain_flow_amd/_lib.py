@@ -22,6 +22,7 @@ class FlowDims(C.Structure):
 
 FLOW_FUSED, FLOW_MODULES = 0, 1      # cfh_flow_dims.numerics (CFH_FLOW_FUSED / CFH_FLOW_MODULES)
 INIT_DELTA, INIT_REPEAT_LAST, INIT_GIVEN = 0, 1, 2   # cfh_flow_dims.init_mode (CFH_INIT_*)
+PLAN_FOLD, PLAN_FOLD2, PLAN_XBLK, PLAN_WIDE, PLAN_CONC = 1, 2, 4, 8, 16   # cfh_flow_plan flags (CFH_PLAN_*)
 
 
 class VaeDims(C.Structure):
@@ -46,6 +47,7 @@ SIGNATURES = {
     "cfh_flow_integrate_noalloc": (_I, [C.POINTER(FlowDims), C.POINTER(_VP), _VP, _VP, _I, _VP]),
     "cfh_flow_prepare_streams": (_I, [C.POINTER(FlowDims), _VP, C.POINTER(_I)]),
     "cfh_flow_group_size": (_I, [C.POINTER(FlowDims), _I, C.POINTER(_I)]),
+    "cfh_flow_plan": (_I, [C.POINTER(FlowDims), _I, C.POINTER(_I)]),
     "cfh_flow_anchor_ws_bytes": (_I64, [C.POINTER(FlowDims), _I]),
     "cfh_flow_anchor": (_I, [C.POINTER(FlowDims), _I, C.POINTER(_VP), _VP, _VP, _I, _VP, _VP, _VP]),
     "cfh_flow_integrate_anchored": (_I, [C.POINTER(FlowDims), C.POINTER(_VP), _VP, _VP, _VP, _VP, _I, _VP]),

@@ -71,6 +71,15 @@ def group_size(cfg: TreeFlowConfig, batch: int) -> int:
     return int(r.value)
 
 
+def plan_flags(cfg: TreeFlowConfig, batch: int = 1) -> int:
+    """The launch forms the flow uses for ``batch`` requests (``_lib.PLAN_*`` bits; cfh_flow_plan)."""
+    f = C.c_int(0)
+    rc = _lib.lib().cfh_flow_plan(C.byref(flow_dims(cfg)), int(batch), C.byref(f))
+    if rc != 0:
+        raise ValueError(f"flow shape not supported by libcfhip at batch {batch}: {cfg}")
+    return int(f.value)
+
+
 class FusedFlow:
     """Packed chunk experts + workspace for one drafter on one device."""
 

@@ -2049,6 +2049,18 @@ int cfh_flow_group_size(const cfh_flow_dims* dims, int batch, int* requests) {
   return CFH_OK;
 }
 
+int cfh_flow_plan(const cfh_flow_dims* dims, int batch, int* flags) {
+  if (!flags) return CFH_E_INVALID;
+  *flags = 0;
+  if (!cfh::flow_dims_ok(dims) || batch < 1) return CFH_E_UNSUPPORTED;
+  if (dims->d > ROWT * ROWE || dims->draft_length > MAXR) return CFH_E_UNSUPPORTED;
+  const Plan p = make_plan(dims, group_size(dims, batch));
+  if (!p.ok) return CFH_E_UNSUPPORTED;
+  *flags = (p.fold ? CFH_PLAN_FOLD : 0) | (p.fold2 ? CFH_PLAN_FOLD2 : 0) | (p.xblk ? CFH_PLAN_XBLK : 0) |
+           (p.wide ? CFH_PLAN_WIDE : 0) | (p.conc ? CFH_PLAN_CONC : 0);
+  return CFH_OK;
+}
+
 int cfh_flow_integrate(const cfh_flow_dims* dm, const void* const* experts, const void* ctx, void* z_out,
                        void* ws_ptr, int batch, void* stream) {
   if (!cfh::flow_dims_ok(dm) || dm->d > ROWT * ROWE || dm->draft_length > MAXR) return CFH_E_UNSUPPORTED;

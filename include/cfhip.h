@@ -154,6 +154,16 @@ int cfh_flow_integrate_anchored(const cfh_flow_dims* dims, const void* const* ex
  * runs torch modules over the whole batch (cf/drafters/chunked_flow.py:295-331). */
 int cfh_flow_group_size(const cfh_flow_dims* dims, int batch, int* requests);
 
+/* The launch forms cfh_flow_integrate uses for `batch` requests of this shape (*flags, bits below):
+ * a diagnostic with no counterpart in the reference, for callers and tests that need to know which
+ * kernels a shape runs.  Host only: touches no device. */
+#define CFH_PLAN_FOLD 1      /* cross attention folded into per-draft factors (k_xattn)                 */
+#define CFH_PLAN_FOLD2 2     /* ... with two heads a k-chunk (head widths such as 80)                   */
+#define CFH_PLAN_XBLK 4      /* residual rows and folded cross attention in one launch a block pass     */
+#define CFH_PLAN_WIDE 8      /* wide request groups (more than two requests share each weight stream)   */
+#define CFH_PLAN_CONC 16     /* chunk experts on companion streams (when the overlap check passes)      */
+int cfh_flow_plan(const cfh_flow_dims* dims, int batch, int* flags);
+
 /* Set-up of the companion streams of a caller stream, so that no later cfh_flow_integrate on it
  * synchronises: creates the companions `dims`'s chunk experts need (none for flows that stay on one
  * stream) and checks once that work on them overlaps work on the caller's stream (two 200 us wait

@@ -13,7 +13,8 @@ import torch
 
 from conftest import oracle_numerics, rel_err, to64, weights64
 from chain_flow_amd.config import flownet
-from chain_flow_amd.flow import FusedFlow
+from chain_flow_amd import _lib
+from chain_flow_amd.flow import FusedFlow, plan_flags
 from chain_flow_amd.weights import make_weights, synthetic_context
 from oracle import flow as oflow
 
@@ -185,6 +186,7 @@ def test_flow_one_launch_cross_attention_shapes(cuda, d, heads, ctx, kd, cs):
     5), four and seven heads (a pair of heads a score tile, the last pair half empty), two partial
     rows of the out-projection, a single expert of 4 rows, experts of 2 and 4 rows."""
     cfg = flownet(d, layers=2, flow_steps=2, num_heads=heads, context_size=ctx, draft_length=kd, chunk_size=cs)
+    assert plan_flags(cfg) & _lib.PLAN_XBLK                # the form under test is the one that runs
     W = _flow_weights(cfg, seed=17)
     c = synthetic_context(1, cfg.context_size, d, seed=8)
     print(f"[flow one-launch xattn] d={d} H={heads} C={ctx} draft={kd} chunk={cs}", flush=True)

@@ -139,3 +139,29 @@ def test_flow_two_heads_fold_layout_without_a_device():
         for batch in (1, 2, 3):
             ws = C.c_int64(-1)
             assert L.cfh_caps(C.byref(dims), batch, C.byref(ws)) == 0 and ws.value > 0
+
+
+def test_flow_plan_flags_without_a_device():
+    """cfh_flow_plan reports the launch forms on the host: the shipped latent width (640, 8 heads of
+    80) folds its cross attention two heads a k-chunk and, for one request, runs the residual rows
+    and the cross attention as one launch; a packed pair of requests keeps the unfolded launches;
+    d = 512 (heads of 64) folds one head a k-chunk with the one-launch form; d = 1024 and the
+    headline d = 5120 fold without it and plan concurrent chunk experts; 32 requests at d = 4096 run
+    in wide groups."""
+    from chain_flow_amd.config import flownet
+    from chain_flow_amd.flow import plan_flags
+    F, F2, X, W, CC = _lib.PLAN_FOLD, _lib.PLAN_FOLD2, _lib.PLAN_XBLK, _lib.PLAN_WIDE, _lib.PLAN_CONC
+    latent = flownet(640, layers=8, flow_steps=2)
+    assert plan_flags(latent) == F | F2 | X
+    assert plan_flags(latent, 2) & (F | X) == 0
+    assert plan_flags(flownet(512, layers=2, flow_steps=2)) == F | X
+    assert plan_flags(flownet(1024, layers=2, flow_steps=2)) == F | CC
+    assert plan_flags(flownet(5120, layers=8, flow_steps=8)) == F | CC
+    assert plan_flags(flownet(4096, layers=8, flow_steps=8), 32) & W
+    # fewer context rows, four or seven heads, short experts: still the one-launch form
+    for d, h, ctx, kd, cs in [(640, 8, 4, 8, 4), (320, 4, 8, 8, 4), (512, 8, 3, 4, 4), (448, 7, 5, 8, 4)]:
+        cfg = flownet(d, layers=2, flow_steps=2, num_heads=h, context_size=ctx, draft_length=kd, chunk_size=cs)
+        assert plan_flags(cfg) & X, (d, h, ctx, kd, cs)
+    # 16 draft rows exceed the one-launch form's 8 rows a workgroup
+    assert not plan_flags(flownet(640, layers=1, flow_steps=2, draft_length=16, chunk_size=8)) & X
+

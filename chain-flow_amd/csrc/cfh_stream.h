@@ -49,6 +49,10 @@ struct SArgs {
   int gelu_r16;        // E_GELU16: round acc + bias to fp16 before the GELU (a Linear module
                        // followed by a GELU module) instead of once after it (the fused block)
   int conc;            // launches of this shape running concurrently (one per chunk expert's stream)
+  // E_PART16 only: nl layers in one launch, layer l's entries at the same pointers advanced by
+  // l * (lwb, lab, lob) bytes (weights, operand rows, output)
+  int nl;
+  long long lwb, lab, lob;
 };
 
 // LDS that concurrent streaming launches reserve when together they fit one workgroup a CU:
@@ -267,11 +271,24 @@ __global__ void __launch_bounds__(WV * 64) k_stream(SArgs a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   int b = blockIdx.x;
   const int per_ex = a.ks * a.wg_per_kc;
+  int l = 0;
+  if constexpr (EPI == E_PART16) {
+    const int per_l = a.nex * per_ex;
+    l = b / per_l;
+    b -= l * per_l;
+  }
   const int e = b / per_ex;
   b -= e * per_ex;
   const int kc = b / a.wg_per_kc;
   const int tg = b - kc * a.wg_per_kc;
-  const SEx& ex = a.ex[e];
+  SEx exl;   // (E_PART16: layer l's copy of the entry; the other kinds read the entry in place)
+  if constexpr (EPI == E_PART16) {
+    exl = a.ex[e];
+    exl.w = (const h16x8*)((const char*)exl.w + l * a.lwb);
+    exl.a = (const h16*)((const char*)exl.a + l * a.lab);
+    exl.out = (char*)exl.out + l * a.lob;
+  }
+  const SEx& ex = EPI == E_PART16 ? exl : a.ex[e];
   const int ksteps = a.K / 32;
   const int KC = a.K / a.ks, nsteps = KC / 32;
   const int t0 = (tg * a.wpb + wave) * a.tpw;
@@ -396,7 +413,7 @@ int launch_stream_k(const SArgs& a, size_t lds, hipStream_t st) {
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024));
     attr_set |= 1ull << dev;
   }
-  const long long wgs = (long long)a.nex * a.ks * a.wg_per_kc;
+  const long long wgs = (long long)a.nex * a.ks * a.wg_per_kc * (EPI == E_PART16 ? std::max(a.nl, 1) : 1);
   if (a.conc > 1) {
     static int cus[64] = {};
     if (dev < 64 && !cus[dev]) CFH_HIP(hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev));

@@ -1805,22 +1805,33 @@ int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* expert
         hipLaunchKernelGGL(k_fold_mask, dim3(256), dim3(256), 0, st, fm);
         CFH_LAUNCH_CHECK();
       }
-      for (int l = 0; l < NL; ++l) {
-        const size_t per_l = (size_t)p.H * Cg * d;
+      // several blocks' factors a launch (block l's entries advanced by l block strides) while the
+      // launch's weights stay under FOLD_LAUNCH_BYTES: the narrow widths' per-block launches are
+      // bound by their fixed cost (latent width 640: 8 launches of 5.5 us became one), the widest
+      // keep one block a launch (d = 5120: 210 MB a block; merged, +15 us a draft); A and B of every
+      // expert together when they fit the launch's four weight sets
+      constexpr size_t FOLD_LAUNCH_BYTES = 256u << 20;
+      const size_t per_l = (size_t)p.H * Cg * d;
+      const size_t blk_bytes = (size_t)nch * 2 * d * d * 2;
+      const int lpl = (int)std::max<size_t>(1, std::min<size_t>(NL, FOLD_LAUNCH_BYTES / blk_bytes));
+      for (int l0 = 0; l0 < NL; l0 += lpl)
         for (int half = 0; half < 2; ++half) {
-          // A and B of every expert in one launch when they fit the launch's four weight sets
           if (half == 1 && 2 * nch <= 4) break;
           SArgs a = {};
           a.N = d; a.K = d; a.ks = p.ks_fold; a.wpb = p.wpb_fold; a.tpw = 1; a.d = d; a.hd = p.hd;
           a.wg_per_kc = (d / 16) / a.wpb;
+          a.nl = std::min(lpl, NL - l0);
+          a.lwb = (long long)L.blkstride;
+          a.lab = (long long)(p.fold2 ? 2 * 2 * Cg * d : 2 * Cg * d) * 2;
+          a.lob = (long long)per_l * 2;
           for (int part = 0; part < 2; ++part) {
             if (2 * nch > 4 && part != half) continue;
             for (int c = 0; c < nch; ++c) {
               SEx& x = a.ex[a.nex++];
-              const h16* kv = w.kvc[c] + (size_t)l * 2 * Cg * d;
-              x.w = (const h16x8*)PTR(c, BLK(l) + (part == 0 ? (p.fold2 ? L.qct : L.qc) : L.oc));
+              const h16* kv = w.kvc[c] + (size_t)l0 * 2 * Cg * d;
+              x.w = (const h16x8*)PTR(c, BLK(l0) + (part == 0 ? (p.fold2 ? L.qct : L.qc) : L.oc));
               if (p.fold2) {   // 2 Cg rows a k-chunk: its first head's, then its second head's
-                x.a = w.fm[c] + (size_t)(l * 2 + part) * 2 * Cg * d;
+                x.a = w.fm[c] + (size_t)(l0 * 2 + part) * 2 * Cg * d;
                 x.S = 2 * Cg;
               } else {
                 x.a = part == 0 ? kv : kv + (size_t)Cg * d;
@@ -1828,13 +1839,12 @@ int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* expert
               }
               x.hrows = Cg;         // one head's factor block per Cg rows
               x.lda = d;
-              x.out = (part == 0 ? w.fa[c] : w.fb[c]) + (size_t)l * per_l;
+              x.out = (part == 0 ? w.fa[c] : w.fb[c]) + (size_t)l0 * per_l;
               x.pack = part == 0;   // A: the cross attention's score operand image
             }
           }
           if ((rc = launch_stream<S_BUF, E_PART16>(a, p.S_fold, st))) return rc;
         }
-      }
     }
     if (p.conc) {   // companions start after the per-draft launches
       CFH_HIP(hipEventRecord(cp.fork, st));

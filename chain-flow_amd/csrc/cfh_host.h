@@ -30,6 +30,8 @@ struct ExpertLayout {
   size_t sn_w, sn_b, qkv, qkv_b, o, o_b, xn_w, xn_b, cn_w, cn_b, qc, qc_b, kv, kv_b, oc, oc_b,
       fn_w, fn_b, w1, w1_b, w2, w2_b;
   size_t on_w, on_b, out, out_b;           // out_norm, out_proj
+  size_t tau;                              // time embeddings of every Euler step, fp16 [E][d]
+  size_t tau_p;                            // their split-K partials while packing, fp32 [tau_ks][E][d]
   size_t total;
   bool fold;                               // cross attention folded (xattn_fold): qc holds Wq^T
   bool fold2;                              // xattn_fold2: qct holds Wq^T beside qc
@@ -41,6 +43,12 @@ bool flow_dims_ok(const cfh_flow_dims* d);
 // a multiple of 32, the MFMA k-step; 0 if none (head widths must be multiples of 8).
 int heads_per_chunk(int hd, int H);
 ExpertLayout expert_layout(const cfh_flow_dims* d);
+// The k-chunks of the time-MLP GEMV (the split the flow plan has always used for it).
+int tau_ks(const cfh_flow_dims* d);
+// The time embeddings tau_s = time_mlp(s / E) of every Euler step into a packed expert image
+// (fp16 [E][d] at L.tau): a function of the weights and E alone, computed once at packing instead
+// of in every draft.
+int pack_tau(const cfh_flow_dims* d, const ExpertLayout& L, char* base, hipStream_t st);
 // Whether the flow folds the cross attention's query and output projections into per-draft
 // factors of the context K/V (one head per k-chunk: head width a multiple of 32).  The packed
 // layout depends on it (the query weight is stored transposed), so packing and the flow plan both

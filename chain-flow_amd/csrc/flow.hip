@@ -763,7 +763,7 @@ struct Plan {
   int d, fd, CS, E, NL, C, KD, H, hd, nch, Smax;
   int R, Ct;          // requests per group (rows packed in one tile) and their context rows R C
   int ks_att;         // k-chunks of the attention launches: H / heads per chunk
-  int ks_qc, ks_w2, ks_out, ks_kv, ks_tau;
+  int ks_qc, ks_w2, ks_out, ks_kv;
   int wpb_qc, wpb_w2, wpb_out, tpw_att, wpb_att, wpb_full, wpb_w1;
   int pks;            // partial slots per expert
   int res_mode;       // RES_ADD32 (fused-kernel numerics) or RES_ADD16 (torch fp16 modules)
@@ -887,7 +887,6 @@ Plan make_plan(const cfh_flow_dims* dm, int R = 1) {
   p.Smax = R * p.KD;
   const int out_rows = R == 1 ? p.CS : p.Smax;   // OUT: the current chunk's rows, or every row when packed
   p.res_mode = dm->numerics == CFH_FLOW_MODULES ? RES_ADD16 : RES_ADD32;
-  p.ks_tau = ksplit_for(p.nch, p.d / 16, p.d, p.E);
   if (p.Smax > MAXR) {
     make_wide_plan(p, dm);
     return p;
@@ -912,7 +911,6 @@ Plan make_plan(const cfh_flow_dims* dm, int R = 1) {
   p.ks_w2 = w2_wide ? dm->ffn_mult : std::max(choose_ks(p.nch, tiles_d, p.fd, p.Smax, 4096, cap), 1);
   p.ks_out = std::max(choose_ks(p.nch, tiles_d, p.d, out_rows, 2048, cap), 1);
   p.ks_kv = ksplit_for(p.nch * p.NL, 2 * p.d / 16, p.d, p.Ct);
-  p.ks_tau = ksplit_for(p.nch, p.d / 16, p.d, p.E);
   p.wpb_w2 = w2_wide ? wpb_for_grid(tiles_d, p.nch * p.ks_w2, 16, p.Smax * (p.fd / p.ks_w2) / 8)
                      : std::min(4, pick_wpb(tiles_d, 1));
   p.wpb_out = wpb_for_grid(tiles_d, p.nch * p.ks_out, 8, out_rows * (p.d / p.ks_out) / 8);
@@ -999,7 +997,6 @@ struct WS {
   h16* g[4];
   float* P[4];        // partials of the split-K kernels (O, OC, W2, OUT)
   float* Pq[4];       // cross-q partials (QC), read by OC (unfolded shapes)
-  h16* tau[4];        // [E][d]
   h16* kvc[4];        // [L][2][C][d]
   h16* fa[4];         // folded shapes: A [L][H][C][d] = Wq_h^T K_h^T
   h16* fb[4];         //                B [L][H][C][d] = Wo_h V_h
@@ -1007,7 +1004,6 @@ struct WS {
   h16* fm[4];         // fold2: context K / V rows masked per head [L][2][2][C][d] (K/V, head in chunk)
   h16* cln[4];        // wide: context_norm(ctx) rows of every block [L][C][d]
   float* Pkv;         // [nch][L][ks][C][2d]
-  float* Ptau;        // [nch][ks][E][d]
   float* ctx_mom;     // [C][2]
   size_t total;
 };
@@ -1030,7 +1026,6 @@ WS carve(const Plan& p, char* base) {
     w.g[c] = (h16*)take(S * fd * 2);
     w.P[c] = (float*)take((size_t)p.pks * S * d * 4);
     if (!p.fold) w.Pq[c] = (float*)take((size_t)p.ks_qc * S * d * 4);
-    w.tau[c] = (h16*)take((size_t)p.E * d * 2);
     w.kvc[c] = (h16*)take((size_t)p.NL * 2 * p.Ct * d * 2);
     if (p.fold) {
       w.fa[c] = (h16*)take((size_t)p.NL * p.H * p.Ct * d * 2);
@@ -1041,7 +1036,6 @@ WS carve(const Plan& p, char* base) {
     if (p.wide) w.cln[c] = (h16*)take((size_t)p.NL * p.Ct * d * 2);
   }
   if (!p.wide) w.Pkv = (float*)take((size_t)p.nch * p.NL * p.ks_kv * p.Ct * 2 * d * 4);
-  w.Ptau = (float*)take((size_t)p.nch * p.ks_tau * p.E * d * 4);
   w.ctx_mom = (float*)take((size_t)p.Ct * 2 * 4);
   w.total = off;
   return w;
@@ -1052,7 +1046,7 @@ WS expert_view(const WS& w, int c0) {
   WS v = w;
   for (int c = 0; c + c0 < 4; ++c) {
     v.x[c] = w.x[c + c0]; v.abuf[c] = w.abuf[c + c0]; v.qkv[c] = w.qkv[c + c0]; v.g[c] = w.g[c + c0];
-    v.P[c] = w.P[c + c0]; v.Pq[c] = w.Pq[c + c0]; v.tau[c] = w.tau[c + c0]; v.kvc[c] = w.kvc[c + c0];
+    v.P[c] = w.P[c + c0]; v.Pq[c] = w.Pq[c + c0]; v.kvc[c] = w.kvc[c + c0];
     v.fa[c] = w.fa[c + c0]; v.fb[c] = w.fb[c + c0]; v.fsb[c] = w.fsb[c + c0]; v.fm[c] = w.fm[c + c0];
     v.cln[c] = w.cln[c + c0];
   }
@@ -1622,9 +1616,9 @@ size_t flow_ws_bytes(const cfh_flow_dims* dm, int batch) {
   return carve(p, nullptr).total;
 }
 
-// The wide path after the time embeddings (w0: the first group's workspace, which holds them):
-// groups of p.R requests, two at a time when the batch has several and the paired launch shapes
-// fit (every launch then covers both groups' rows, the second group's workspace after the first's).
+// The wide path (w0: the first group's workspace): groups of p.R requests, two at a time when the
+// batch has several and the paired launch shapes fit (every launch then covers both groups' rows,
+// the second group's workspace after the first's).
 int integrate_wide(const Plan& p, const cfh_flow_dims* dm, const cfh::ExpertLayout& L, const void* const* experts,
                    const void* ctx, void* z_out, char* ws, const WS& w0, int batch, hipStream_t st,
                    const void* anchor) {
@@ -1647,7 +1641,7 @@ int integrate_wide(const Plan& p, const cfh_flow_dims* dm, const cfh::ExpertLayo
     }
     for (int c = 0; c < nch; ++c) {
       r.x[c] = G.w.x[c]; r.pos[c] = (const h16*)PTR(c, L.pos);
-      r.tau[c] = w0.tau[c] + (s < 0 ? 0 : (size_t)(s + 1 < E ? s + 1 : s) * d);
+      r.tau[c] = (const h16*)PTR(c, L.tau) + (s < 0 ? 0 : (size_t)(s + 1 < E ? s + 1 : s) * d);
       r.g[c] = (const h16*)PTR(c, BLK(0) + L.sn_w); r.b[c] = (const h16*)PTR(c, BLK(0) + L.sn_b);
       r.a[c] = G.w.abuf[c];
       r.anchor[c] = anchor ? (const h16*)anchor + ((size_t)c * batch + G.g0) * d : nullptr;
@@ -1712,29 +1706,6 @@ int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* expert
   // be created (creating a stream allocates its hardware queue)
   if (p.conc && (cp.made < nch - 1 || !cp.overlap)) p.conc = false;
 
-  // ---- time embeddings of every step (the same for every request)
-  {
-    GemvArgs a = {};
-    a.nex = nch; a.nl = 1; a.ks = p.ks_tau; a.tiles = d / 16; a.N = d; a.K = d; a.E = E;
-    for (int c = 0; c < nch; ++c) {
-      GemvEx& x = a.ex[c];
-      x.w = (const h16x8*)PTR(c, L.tw2);
-      x.g0 = (const h16*)PTR(c, L.tw0);
-      x.b0 = (const h16*)PTR(c, L.tb0);
-      x.pout = w.Ptau + (size_t)c * p.ks_tau * E * d;
-      x.rows = E;
-    }
-    if ((rc = launch_gemv<SRC_TAU>(a, E, st))) return rc;
-    ReduceArgs r = {};
-    r.nex = nch; r.nl = 1; r.ks = p.ks_tau; r.rows = E; r.N = d; r.d = d; r.kv = 0;
-    for (int c = 0; c < nch; ++c) {
-      r.P[c] = a.ex[c].pout;
-      r.b[c] = (const h16*)PTR(c, L.tb2);
-      r.out[c] = w.tau[c];
-    }
-    hipLaunchKernelGGL(k_reduce, dim3(256), dim3(256), 0, st, r);
-    CFH_LAUNCH_CHECK();
-  }
   if (p.wide) return integrate_wide(p, dm, L, experts, ctx, z_out, (char*)ws_ptr, w, batch, st, anchor);
 
   for (int g0 = 0; g0 < batch; g0 += p.R) {
@@ -1750,7 +1721,7 @@ int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* expert
       r.only = -1;
       r.CS = CS; r.nch = nch; r.KD = KD; r.R = Rg; r.out_all = p.R > 1;
       for (int c = 0; c < nch; ++c) {
-        r.x[c] = w.x[c]; r.pos[c] = (const h16*)PTR(c, L.pos); r.tau[c] = w.tau[c];
+        r.x[c] = w.x[c]; r.pos[c] = (const h16*)PTR(c, L.pos); r.tau[c] = (const h16*)PTR(c, L.tau);
         r.g[c] = (const h16*)PTR(c, BLK(0) + L.sn_w); r.b[c] = (const h16*)PTR(c, BLK(0) + L.sn_b);
         r.a[c] = w.abuf[c];
         r.anchor[c] = anchor ? (const h16*)anchor + ((size_t)c * batch + g0) * d : nullptr;
@@ -1858,7 +1829,7 @@ int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* expert
       for (int c = 0; c < nch; ++c) {
         r.Pout[c] = w.P[c]; r.bout[c] = (const h16*)PTR(c, L.out_b);
         r.x[c] = w.x[c]; r.pos[c] = (const h16*)PTR(c, L.pos);
-        r.tau[c] = w.tau[c] + (size_t)(s + 1 < E ? s + 1 : s) * d;
+        r.tau[c] = (const h16*)PTR(c, L.tau) + (size_t)(s + 1 < E ? s + 1 : s) * d;
         r.g[c] = (const h16*)PTR(c, BLK(0) + L.sn_w); r.b[c] = (const h16*)PTR(c, BLK(0) + L.sn_b);
         r.a[c] = w.abuf[c];
         r.anchor[c] = anchor ? (const h16*)anchor + ((size_t)c * batch + g0) * d : nullptr;
@@ -2027,6 +1998,36 @@ int scratch_address(void** out) {
 }
 
 }  // namespace
+
+namespace cfh {
+
+int tau_ks(const cfh_flow_dims* dm) {
+  return ksplit_for(dm->draft_length / dm->chunk_size, dm->d / 16, dm->d, dm->flow_steps);
+}
+
+int pack_tau(const cfh_flow_dims* dm, const ExpertLayout& L, char* base, hipStream_t st) {
+  const int d = dm->d, E = dm->flow_steps, ks = tau_ks(dm);
+  GemvArgs a = {};
+  a.nex = 1; a.nl = 1; a.ks = ks; a.tiles = d / 16; a.N = d; a.K = d; a.E = E;
+  GemvEx& x = a.ex[0];
+  x.w = (const h16x8*)(base + L.tw2);
+  x.g0 = (const h16*)(base + L.tw0);
+  x.b0 = (const h16*)(base + L.tb0);
+  x.pout = (float*)(base + L.tau_p);
+  x.rows = E;
+  int rc;
+  if ((rc = launch_gemv<SRC_TAU>(a, E, st))) return rc;
+  ReduceArgs r = {};
+  r.nex = 1; r.nl = 1; r.ks = ks; r.rows = E; r.N = d; r.d = d; r.kv = 0;
+  r.P[0] = x.pout;
+  r.b[0] = (const h16*)(base + L.tb2);
+  r.out[0] = (h16*)(base + L.tau);
+  hipLaunchKernelGGL(k_reduce, dim3(256), dim3(256), 0, st, r);
+  CFH_LAUNCH_CHECK();
+  return CFH_OK;
+}
+
+}  // namespace cfh
 
 extern "C" {
 

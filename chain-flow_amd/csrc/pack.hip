@@ -100,6 +100,8 @@ ExpertLayout expert_layout(const cfh_flow_dims* dm) {
   L.on_b = take(d * H);
   L.out_b = take(d * H);
   L.out = take(d * d * H);
+  L.tau = take((size_t)dm->flow_steps * d * H);
+  L.tau_p = take((size_t)tau_ks(dm) * dm->flow_steps * d * 4);
   L.total = off;
   L.fold = xattn_fold(dm);
   return L;
@@ -247,6 +249,7 @@ int cfh_flow_pack_expert(const cfh_flow_dims* dims, const void* const* raw, int 
   CFH_TRY(cp(L.on_b, r[1], d));
   CFH_TRY(pk(L.out, r[2], (int)d, (int)d));
   CFH_TRY(cp(L.out_b, r[3], d));
+  CFH_TRY(cfh::pack_tau(dims, L, base, st));
 #undef CFH_TRY
   return CFH_OK;
 }

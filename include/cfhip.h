@@ -32,7 +32,7 @@ extern "C" {
 #define CFH_E_SCRATCH 4          /* the no-allocation entry point's workspace is too small */
 
 /* Size of the library's per-device scratch array behind cfh_flow_integrate_noalloc (64 MiB: the
- * flow workspace of one request at d <= 5120 and 8 layers needs 37.3 MiB; a batch packs two
+ * flow workspace of one request at d <= 5120 and 8 layers needs 35.9 MiB; a batch packs two
  * requests per group where the shape allows, which can need more -- cfh_caps tells). */
 #define CFH_NOALLOC_SCRATCH_BYTES (64ll << 20)
 
@@ -106,6 +106,8 @@ int64_t cfh_flow_expert_bytes(const cfh_flow_dims* dims);
  *   self_attn.out_proj.{weight,bias}, cross_norm.{weight,bias}, context_norm.{weight,bias},
  *   cross_attn.in_proj_{weight,bias}, cross_attn.out_proj.{weight,bias}, ffn.0.{weight,bias},
  *   ffn.1.{weight,bias}, ffn.4.{weight,bias}, then out_norm.{weight,bias}, out_proj.{weight,bias}.
+ * The image also holds the time embeddings of every Euler step (time_mlp(s / flow_steps), a function
+ * of the weights alone), which packing computes on `stream`.
  * Replaces FusedExpertBlocks.__init__ packing (cf/cuda_block.py:269-318). */
 int cfh_flow_pack_expert(const cfh_flow_dims* dims, const void* const* raw, int n_raw, void* packed,
                          void* stream);

@@ -18,23 +18,25 @@
 // for theirs (and an expert's next update waits until the next expert has read its chunk's rows).
 // A batch is drafted in groups of R requests whose rows share one MFMA tile (R x draft_length
 // <= 16: two 8-row drafts, where the 16-row operand fits the streaming kernels' LDS: d <= 4096 of
-// the supported widths), so every weight stream serves R drafts; attention masks keep each request to its own rows and context.  Work that needs a whole
-// row sits in a small row kernel between two streaming kernels; there is no cross-workgroup
-// synchronisation inside any kernel (no fences, no atomics, no spin-waits), so results are
-// deterministic.  On MI355X the gap between two kernels on the stream is 1.4-2 us (per-workgroup
+// the supported widths), so every weight stream serves R drafts; attention masks keep each request
+// to its own rows and context.  Work that needs a whole row sits in a small row kernel between two
+// streaming kernels; there is no cross-workgroup synchronisation inside any kernel (no fences, no
+// atomics, no spin-waits), so results are deterministic.  On MI355X the gap between two kernels on the stream is 1.4-2 us (per-workgroup
 // timestamps), while a fenced grid barrier across the 8 XCDs costs ~12 us, which is why this is a
 // kernel pipeline and not one persistent launch.
 //
-//   per draft : TAU  time_mlp(tau_s) for all E steps     (GEMV + reduce)
-//               ROWS init_latents(ctx), step-0 rows x, a = LN_self(x) of block 0
+//   per expert: TAU  time_mlp(tau_s) for all E steps, computed when the expert is packed
+//   per draft : ROWS init_latents(ctx), step-0 rows x, a = LN_self(x) of block 0
 //               KV   cross K/V of every block             (GEMV + reduce)
-//               FOLD per block: A_h = Wq_h^T K_h^T, B_h = Wo_h V_h   (stream, split-K by head)
+//               FOLD A_h = Wq_h^T K_h^T, B_h = Wo_h V_h of every block (stream, split-K by head;
+//                    several blocks a launch at narrow widths)
 //   per Euler step, per block l (each expert on its own stream, the second starting ~1/3 block later):
 //     QKV   stream  A = a (LN_self rows)          epilogue q,k,v = fp16(acc + b)      full-K tiles
 //     O     stream  A = causal self attention of head h, computed while staging    split-K by head
 //     RES   row     x += sum_h P + b_o ; a = LN_cross(fp16(x))
 //     XATT  small   scores_h = a A_h + bq_h K_h^T, softmax, P_h B_h per head (fp32 partials)
 //     RES   row     x += sum_h P + b_oc ; a = LN_ffn(fp16(x))
+//           (one-request flows of width <= 640: RES, XATT, RES as one XBLK launch)
 //     W1    stream  A = a                         epilogue g = fp16(gelu(acc + b1))  full-K tiles
 //     W2    stream  A = g                         fp32 partials                     split-K
 //     RES   row     x += sum P + b2 ; a = LN_self of block l+1 (out_norm after the last block)

@@ -69,6 +69,8 @@ struct GemvEx {
   const int* ids;      // SRC_GATHER: row i of A = a[max(ids[i * ids_stride], 0)] (a row-major, lda)
   int ids_stride;
   int rows;
+  h16* hout;           // ks == 1: out = fp16(acc + hb) written here instead of partials (the
+  const h16* hb;       // partial reduce's arithmetic), hb layer l at + l * vstride bytes
 };
 
 constexpr int MAXEX = 8;          // weight sets (experts / path offsets) per GEMV launch
@@ -77,6 +79,7 @@ struct GemvArgs {
   GemvEx ex[MAXEX];
   int nex, nl, ks, tiles, N, K, E;
   long long wstride, vstride;   // bytes between consecutive layers (packed weights / vectors)
+  int kvout;                    // hout layout: 0 [l][rows][N], 1 [l][2][rows][N/2] (cross K | V)
 };
 
 template <int SRC>
@@ -164,6 +167,17 @@ __global__ void __launch_bounds__(WPB * 64) k_gemv(GemvArgs a) {
   acc = ts.run(As, lda, ep.rows, acc);
 
   const int col = lane & 15, rbase = 4 * (lane >> 4);
+  if (ep.hout) {
+    const int n = t * 16 + col;
+    const float b = (float)((const h16*)((const char*)ep.hb + (size_t)l * a.vstride))[n];
+    const int half = a.N / 2, part = a.kvout ? n / half : 0, nn = a.kvout ? n - part * half : n;
+    const int ld = a.kvout ? half : a.N;
+    h16* ho = ep.hout + ((size_t)(l * (a.kvout ? 2 : 1) + part) * ep.rows) * ld + nn;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (rbase + j < ep.rows) ho[(size_t)(rbase + j) * ld] = (h16)(acc[j] + b);
+    return;
+  }
   float* po = ep.pout + ((size_t)(l * a.ks + kc) * ep.rows) * a.N + t * 16 + col;
 #pragma unroll
   for (int j = 0; j < 4; ++j)
@@ -331,6 +345,8 @@ int ksplit_for(int nex_units, int tiles, int K, int rows) {
 template <int SRC>
 int launch_gemv(const GemvArgs& a, int rows_max, hipStream_t st) {
   if (a.tiles % WPB != 0) return CFH_E_UNSUPPORTED;
+  for (int e = 0; e < a.nex; ++e)
+    if (a.ex[e].hout && a.ks != 1) return CFH_E_UNSUPPORTED;   // direct output needs the whole K
   const size_t lds = lds_bytes(rows_max, a.K / a.ks);
   if (lds > 64 * 1024) return CFH_E_UNSUPPORTED;
   const long long units = (long long)a.nex * a.nl * a.ks * a.tiles;

@@ -1745,18 +1745,25 @@ int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* expert
         x.pout = w.Pkv + (size_t)c * NL * p.ks_kv * Cg * 2 * d;
         x.mom = w.ctx_mom;
         x.rows = Cg;
+        if (p.ks_kv == 1) {   // whole-K tiles: the bias and the fp16 rows written by the GEMV itself
+          x.hout = w.kvc[c];
+          x.hb = (const h16*)PTR(c, BLK(0) + L.kv_b);
+        }
       }
+      a.kvout = 1;
       if ((rc = launch_gemv<SRC_CTX>(a, p.Ct, st))) return rc;
-      ReduceArgs r = {};
-      r.nex = nch; r.nl = NL; r.ks = p.ks_kv; r.rows = Cg; r.N = 2 * d; r.d = d; r.kv = 1;
-      r.vstride = (long long)L.blkstride;
-      for (int c = 0; c < nch; ++c) {
-        r.P[c] = a.ex[c].pout;
-        r.b[c] = (const h16*)PTR(c, BLK(0) + L.kv_b);
-        r.out[c] = w.kvc[c];
+      if (p.ks_kv > 1) {
+        ReduceArgs r = {};
+        r.nex = nch; r.nl = NL; r.ks = p.ks_kv; r.rows = Cg; r.N = 2 * d; r.d = d; r.kv = 1;
+        r.vstride = (long long)L.blkstride;
+        for (int c = 0; c < nch; ++c) {
+          r.P[c] = a.ex[c].pout;
+          r.b[c] = (const h16*)PTR(c, BLK(0) + L.kv_b);
+          r.out[c] = w.kvc[c];
+        }
+        hipLaunchKernelGGL(k_reduce, dim3(1024), dim3(256), 0, st, r);
+        CFH_LAUNCH_CHECK();
       }
-      hipLaunchKernelGGL(k_reduce, dim3(1024), dim3(256), 0, st, r);
-      CFH_LAUNCH_CHECK();
     }
     // ---- the folded cross attention's factors of every block: A_h = Wq_h^T K_h^T from the
     // transposed query weight against the K rows, B_h = Wo_h V_h from the out-projection against

@@ -390,32 +390,6 @@ __global__ void __launch_bounds__(XT) k_xattn(XattArgs a) {
   }
 }
 
-// The query bias's share of every block's scores, sb[l][h][c] = bq_h . K_h[c], once per draft:
-// one workgroup per (expert, block), one wave per (head, context row) pair at a time.
-struct XbiasArgs {
-  const h16* K[4];       // block 0's context K rows [C][d]; block l at + l * kstride halves
-  const h16* bq[4];      // block 0's cross_attn.in_proj_bias[0:d]; block l at + l * bstride bytes
-  float* sb[4];          // [L][H][C]
-  long long kstride, bstride;
-  int nex, nl, d, H, C;
-};
-
-__global__ void __launch_bounds__(1024) k_xbias(XbiasArgs a) {
-  const int e = blockIdx.x / a.nl, l = blockIdx.x - e * a.nl;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  const int hd = a.d / a.H;
-  const h16* K = a.K[e] + (size_t)l * a.kstride;
-  const h16* bq = (const h16*)((const char*)a.bq[e] + (size_t)l * a.bstride);
-  // (the pairs of a wide group's many context rows spread over gridDim.y workgroups)
-  for (int p = blockIdx.y * nw + wave; p < a.H * a.C; p += gridDim.y * nw) {
-    const int h = p / a.C, c = p - h * a.C;
-    float s = 0.f;
-    for (int j = lane; j < hd; j += 64) s += (float)bq[h * hd + j] * (float)K[(size_t)c * a.d + h * hd + j];
-    s = wave_sum(s);
-    if (lane == 0) a.sb[e][((size_t)l * a.H + h) * a.C + c] = s;
-  }
-}
-
 // The two-heads fold's operand rows: for every expert, block l and part (context K, then V), rows
 // [j][c] = row c of the part with the columns of all but the j-th head of each 2 hd-wide k-chunk set
 // to zero, so that one k-chunk's 2 C rows give both of its heads' factors apart.
@@ -425,11 +399,12 @@ struct FoldMaskArgs {
   int nex, nl, C, d, hd;
 };
 
-__global__ void __launch_bounds__(256) k_fold_mask(FoldMaskArgs a) {
+// (workgroup b of nb taking every nb-th run of blockDim vectors)
+__device__ void fold_mask_rows(const FoldMaskArgs& a, int b, int nb) {
   const int nv = a.d / 8;                                        // 8-column vectors a row
   const size_t per_ex = (size_t)a.nl * 2 * 2 * a.C * nv;
   const size_t total = per_ex * a.nex;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+  for (size_t i = (size_t)b * blockDim.x + threadIdx.x; i < total; i += (size_t)nb * blockDim.x) {
     const int e = (int)(i / per_ex);
     size_t t = i - (size_t)e * per_ex;
     const int v = (int)(t % nv);
@@ -443,6 +418,38 @@ __global__ void __launch_bounds__(256) k_fold_mask(FoldMaskArgs a) {
     const h16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
     const h16x8 x = *(const h16x8*)(a.kv[e] + (lp * a.C + c) * a.d + col);
     *(h16x8*)(a.out[e] + ((lp * 2 + j) * a.C + c) * a.d + col) = keep ? x : zero;
+  }
+}
+
+// The query bias's share of every block's scores, sb[l][h][c] = bq_h . K_h[c], once per draft:
+// one workgroup per (expert, block), one wave per (head, context row) pair at a time.
+struct XbiasArgs {
+  const h16* K[4];       // block 0's context K rows [C][d]; block l at + l * kstride halves
+  const h16* bq[4];      // block 0's cross_attn.in_proj_bias[0:d]; block l at + l * bstride bytes
+  float* sb[4];          // [L][H][C]
+  long long kstride, bstride;
+  int nex, nl, d, H, C;
+  FoldMaskArgs fm;       // two-heads fold: its masked operand rows, by mask_wgs more workgroups
+  int mask_wgs;
+};
+
+__global__ void __launch_bounds__(1024) k_xbias(XbiasArgs a) {
+  if ((int)blockIdx.x >= a.nex * a.nl) {   // (independent of the scores: the same launch)
+    fold_mask_rows(a.fm, blockIdx.x - a.nex * a.nl, a.mask_wgs);
+    return;
+  }
+  const int e = blockIdx.x / a.nl, l = blockIdx.x - e * a.nl;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int hd = a.d / a.H;
+  const h16* K = a.K[e] + (size_t)l * a.kstride;
+  const h16* bq = (const h16*)((const char*)a.bq[e] + (size_t)l * a.bstride);
+  // (the pairs of a wide group's many context rows spread over gridDim.y workgroups)
+  for (int p = blockIdx.y * nw + wave; p < a.H * a.C; p += gridDim.y * nw) {
+    const int h = p / a.C, c = p - h * a.C;
+    float s = 0.f;
+    for (int j = lane; j < hd; j += 64) s += (float)bq[h * hd + j] * (float)K[(size_t)c * a.d + h * hd + j];
+    s = wave_sum(s);
+    if (lane == 0) a.sb[e][((size_t)l * a.H + h) * a.C + c] = s;
   }
 }
 
@@ -1776,15 +1783,14 @@ int integrate(const Plan& p0, const cfh_flow_dims* dm, const void* const* expert
       for (int c = 0; c < nch; ++c) {
         xb.K[c] = w.kvc[c]; xb.bq[c] = (const h16*)PTR(c, BLK(0) + L.qc_b); xb.sb[c] = w.fsb[c];
       }
-      hipLaunchKernelGGL(k_xbias, dim3(nch * NL), dim3(1024), 0, st, xb);
-      CFH_LAUNCH_CHECK();
-      if (p.fold2) {
-        FoldMaskArgs fm = {};
+      if (p.fold2) {   // the masked operand rows by 64 more workgroups of the same launch
+        FoldMaskArgs& fm = xb.fm;
         fm.nex = nch; fm.nl = NL; fm.C = Cg; fm.d = d; fm.hd = p.hd;
         for (int c = 0; c < nch; ++c) { fm.kv[c] = w.kvc[c]; fm.out[c] = w.fm[c]; }
-        hipLaunchKernelGGL(k_fold_mask, dim3(256), dim3(256), 0, st, fm);
-        CFH_LAUNCH_CHECK();
+        xb.mask_wgs = 64;
       }
+      hipLaunchKernelGGL(k_xbias, dim3(nch * NL + xb.mask_wgs), dim3(1024), 0, st, xb);
+      CFH_LAUNCH_CHECK();
       // several blocks' factors a launch (block l's entries advanced by l block strides) while the
       // launch's weights stay under FOLD_LAUNCH_BYTES: the narrow widths' per-block launches are
       // bound by their fixed cost (latent width 640: 8 launches of 5.5 us became one), the widest

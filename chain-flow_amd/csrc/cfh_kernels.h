@@ -185,8 +185,9 @@ __global__ void __launch_bounds__(WPB * 64) k_gemv(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------- partial reduce
-// out = fp16(sum_kc P[kc] + b), used for the per-draft cross K/V and time embeddings; with act = 1,
-// out = fp16(silu(fp16(sum_kc P[kc] + b))) (a Linear module then a SiLU module, as the anchor MLP).
+// out = fp16(sum_kc P[kc] + b), used for split-K cross K/V rows and the packed time embeddings;
+// with act = 1, out = fp16(silu(fp16(sum_kc P[kc] + b))) (a Linear module then a SiLU module, as the
+// anchor MLP).
 struct ReduceArgs {
   const float* P[4];
   const h16* b[4];

@@ -84,6 +84,8 @@ SIGNATURES = {
                                _VP]),
     "cfh_beam_init": (_I, [_VP, _VP, _VP, _VP, _I, _I, _I, _I, _VP]),
     "cfh_beam_chain_step": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _VP]),
+    "cfh_head_topk_packed_beam_chain": (_I, [_VP, _I, _I, _VP, _I, _VP, _VP, _I, _I, _VP, _VP, _VP, _VP, _VP, _VP,
+                                           _VP, _VP, _VP, _I, _I, _I, _VP]),
     "cfh_beam_tree_step": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _I, _VP]),
     "cfh_beam_backtrack": (_I, [_VP, _VP, _VP, _I, _I, _I, _VP, _VP]),
     "cfh_gdn_tree": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _VP, _VP, _VP]),

@@ -15,7 +15,7 @@ import torch
 from chain_flow_amd import _lib
 from chain_flow_amd.config import TreeFlowConfig, TreeVAEFlowConfig
 from chain_flow_amd.flow import FusedFlow
-from chain_flow_amd.head import PathHead, ShortlistHead, row_topk
+from chain_flow_amd.head import GEMV_ROWS, PathHead, ShortlistHead, row_topk
 from chain_flow_amd.vae import HiddenVAE
 
 
@@ -177,9 +177,18 @@ class Drafter:
         hbuf = torch.empty(B * W, d, dtype=torch.float16, device=dev)
         cands = self._pass_a(pred, lastp, 1, steps, W) if self.twopass_m and steps > 1 else None
         image = self._candidate_image(cands, B)
+        # a packed image and at most 8 beam rows: each depth's top-k merge and beam step in one launch
+        fused = W <= 4 and B * W <= GEMV_ROWS and ((cands is None and self.head.image is not None)
+                                                   or image is not None)
         for step in range(1, steps):
             # every request's W beams in one call, each request's rows with its own marginal hidden
             self.path.hidden(lastp.view(B * W, order), self._nlive(step), pred[:, step], out=hbuf)
+            if fused:
+                img, n, smap = ((None, self.head.n, self.head.sl) if cands is None
+                                else (image, cands.shape[-1], cands[0, step - 1]))
+                self.head.topk_beam_chain(hbuf, img, n, lastp.view(-1), order, cum, lastp, smap,
+                                          toks[step - 1], bps[step - 1], B, W, order)
+                continue
             vals, ids, smap = self._scores(hbuf, W, lastp.view(-1), order,
                                            None if cands is None else cands[:, step - 1], B, image,
                                            None if cands is None else self._cand_local[:, step - 1])

@@ -223,6 +223,38 @@ class ShortlistHead:
             ids.data_ptr(), lse.data_ptr(), ws.data_ptr(), _lib.stream_handle()), "cfh_head_topk_packed")
         return vals, ids, lse
 
+    def topk_beam_chain(self, h: torch.Tensor, image: torch.Tensor | None, n: int, prev: torch.Tensor,
+                        prev_stride: int, cum: torch.Tensor, lastp: torch.Tensor, smap: torch.Tensor | None,
+                        toks: torch.Tensor, bps: torch.Tensor, B: int, W: int, order: int):
+        """One depth of a chain search over B chains of W beams (h [B*W, d], B*W <= 8 rows): the top-W
+        of every beam row over a packed image (the head's own, ``image=None``, or a ``pack_rows``
+        image of n rows) and the beam step (cum, lastp, toks, bps in place; ``smap`` maps the ids),
+        the merge and the step in one launch (``cfh_head_topk_packed_beam_chain``).
+        -> (vals [B*W, W], ids [B*W, W] int32, lse [B*W]) as ``topk`` / ``topk_image`` return them."""
+        M = h.shape[0]
+        dev = h.device
+        img = self.image if image is None else image
+        if img is None or M != B * W or M > GEMV_ROWS:
+            raise ValueError("topk_beam_chain needs a packed image and at most 8 beam rows")
+        vals = torch.empty(M, W, dtype=torch.float32, device=dev)
+        ids = torch.empty(M, W, dtype=torch.int32, device=dev)
+        lse = torch.empty(M, dtype=torch.float32, device=dev)
+        if image is None:
+            ws = self.workspace(M, W, dev)
+        else:
+            key = ("image", M, n, W)
+            ws = self._ws.get(key)
+            if ws is None:
+                ws = self._ws[key] = torch.empty(int(_lib.lib().cfh_head_ws_bytes(M, n, W)), dtype=torch.uint8,
+                                                 device=dev)
+        use_m = self.w1 is not None and prev is not None
+        _lib.check(_lib.lib().cfh_head_topk_packed_beam_chain(
+            h.data_ptr(), M, self.d, img.data_ptr(), n, self.w1.data_ptr() if use_m else None,
+            prev.data_ptr() if use_m else None, prev_stride, self.r if use_m else 0, vals.data_ptr(),
+            ids.data_ptr(), lse.data_ptr(), ws.data_ptr(), cum.data_ptr(), lastp.data_ptr(), _lib.ptr(smap),
+            toks.data_ptr(), bps.data_ptr(), B, W, order, _lib.stream_handle()), "cfh_head_topk_packed_beam_chain")
+        return vals, ids, lse
+
     def topk_groups(self, h: torch.Tensor, k: int, rows: torch.Tensor, prev: torch.Tensor | None = None,
                     prev_stride: int = 1):
         """Pass B for a batch in one launch (``cfh_head_topk_grouped``): h [G*F, d] (F consecutive rows

@@ -342,15 +342,12 @@ __global__ void __launch_bounds__(MT_THREADS) k_topk_merge(MergeArgs a) {
 // and the winning lane moves to its list's next entry.  Same results as k_topk_merge.
 constexpr int MW_LDS = 64 * 1024;
 
+// Row m by one wave, its lists staged at sv (nsets k floats, then as many ints).
 template <int S>
-__global__ void __launch_bounds__(256) k_merge_wave(MergeArgs a) {
-  extern __shared__ __align__(16) float mw[];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int m = blockIdx.x * (blockDim.x >> 6) + wave;
-  if (m >= a.M) return;                                  // (no workgroup barrier below)
+__device__ void merge_row(const MergeArgs& a, int m, float* sv) {
+  const int lane = threadIdx.x & 63;
   const Cands cd = carve_cands((void*)a.ws, a.M, a.nsets, a.k);
   const int k = a.k, total = a.nsets * k;
-  float* sv = mw + (size_t)wave * total * 2;
   int* si = (int*)(sv + total);
   const float* cv = cd.cv + (size_t)m * total;
   const int* ci = cd.ci + (size_t)m * total;
@@ -456,6 +453,15 @@ __global__ void __launch_bounds__(256) k_merge_wave(MergeArgs a) {
       ids[r] = ok ? gi : -1;
     }
   }
+}
+
+template <int S>
+__global__ void __launch_bounds__(256) k_merge_wave(MergeArgs a) {
+  extern __shared__ __align__(16) float mw[];
+  const int wave = threadIdx.x >> 6;
+  const int m = blockIdx.x * (blockDim.x >> 6) + wave;
+  if (m >= a.M) return;                                  // (no workgroup barrier below)
+  merge_row<S>(a, m, mw + (size_t)wave * a.nsets * a.k * 2);
 }
 
 // ---------------------------------------------------------------------------- row top-k
@@ -1191,51 +1197,91 @@ struct BeamArgs {
   int tree;
 };
 
-__global__ void __launch_bounds__(64) k_beam_step(BeamArgs a) {
-  __shared__ int old_lastp[64 * 8];   // F <= 64 frontier slots x order <= 8
-  __shared__ int old_prev[64];
-  __shared__ int win_flat[64];
-  __shared__ float win_val[64];
-  const int b = blockIdx.x, lane = threadIdx.x;
+// The beam step in three phases around two workgroup barriers, run by one wave (lane = 0 .. 63):
+// the lane's candidate and the old frontier state into LDS; the k rounds of the wave's best; the
+// winners' outputs.
+struct BeamSmem {
+  int old_lastp[64 * 8];   // F <= 64 frontier slots x order <= 8
+  int old_prev[64];
+  int win_flat[64];
+  float win_val[64];
+};
+
+__device__ __forceinline__ void beam_phase1(const BeamArgs& a, int b, int lane, BeamSmem& s, float& cv, int& ci) {
   const int ncand = a.F * a.TB;
-  const int k = min(a.keep, ncand);
-  // candidate of this lane
-  float cv = -INFINITY;
-  int ci = INT_MAX;
+  cv = -INFINITY;
+  ci = INT_MAX;
   if (lane < ncand) {
     const int f = lane / a.TB, jj = lane - f * a.TB;
     cv = a.cum[b * a.keep + f] + a.vals[((size_t)b * a.F + f) * a.TB + jj];
     ci = lane;
   }
-  for (int q = lane; q < a.F * a.order; q += 64) old_lastp[q] = a.lastp[(size_t)b * a.keep * a.order + q];
-  if (a.tree && lane < a.F) old_prev[lane] = a.prev_ids[b * a.keep + lane];
-  __syncthreads();
+  for (int q = lane; q < a.F * a.order; q += 64) s.old_lastp[q] = a.lastp[(size_t)b * a.keep * a.order + q];
+  if (a.tree && lane < a.F) s.old_prev[lane] = a.prev_ids[b * a.keep + lane];
+}
+
+__device__ __forceinline__ void beam_phase2(int k, int lane, BeamSmem& s, float cv, int ci) {
   for (int r = 0; r < k; ++r) {
     float bv = cv;
     int bi = ci;
     group_best<64>(bv, bi);
     if (ci == bi) { cv = -INFINITY; ci = INT_MAX; }
-    if (lane == 0) { win_val[r] = bv; win_flat[r] = bi; }
+    if (lane == 0) { s.win_val[r] = bv; s.win_flat[r] = bi; }
   }
-  __syncthreads();
+}
+
+__device__ __forceinline__ void beam_phase3(const BeamArgs& a, int b, int lane, const BeamSmem& s, int k) {
   if (lane < k) {
-    const int flat = win_flat[lane];
+    const int flat = s.win_flat[lane];
     const int src = flat / a.TB;
     const int loc = a.ids[((size_t)b * a.F + src) * a.TB + (flat - src * a.TB)];
     const int tok = loc < 0 ? -1 : (a.sl ? a.sl[loc] : loc);
-    a.cum[b * a.keep + lane] = win_val[lane];
+    a.cum[b * a.keep + lane] = s.win_val[lane];
     int* lp = a.lastp + ((size_t)b * a.keep + lane) * a.order;
     lp[0] = tok;
-    for (int q = 1; q < a.order; ++q) lp[q] = old_lastp[src * a.order + q - 1];
+    for (int q = 1; q < a.order; ++q) lp[q] = s.old_lastp[src * a.order + q - 1];
     if (a.tree) {
       a.toks[(size_t)b * a.ld_out + a.base + lane] = tok;
-      a.bps[(size_t)b * a.ld_out + a.base + lane] = old_prev[src];
+      a.bps[(size_t)b * a.ld_out + a.base + lane] = s.old_prev[src];
       a.prev_ids[b * a.keep + lane] = a.base + lane;
     } else {
       a.toks[b * a.keep + lane] = tok;
       a.bps[b * a.keep + lane] = src;
     }
   }
+}
+
+__global__ void __launch_bounds__(64) k_beam_step(BeamArgs a) {
+  __shared__ BeamSmem s;
+  const int b = blockIdx.x, lane = threadIdx.x;
+  const int k = min(a.keep, a.F * a.TB);
+  float cv;
+  int ci;
+  beam_phase1(a, b, lane, s, cv, ci);
+  __syncthreads();
+  beam_phase2(k, lane, s, cv, ci);
+  __syncthreads();
+  beam_phase3(a, b, lane, s, k);
+}
+
+// The merge of the head's candidate lists and the chain beam step in one launch: workgroup b holds
+// chain b's F beam rows, a wave each (k_merge_wave's row merge, values to vals / ids / lse as there),
+// then its first wave runs the beam step on those rows (every wave meets the barriers).
+template <int S>
+__global__ void __launch_bounds__(256) k_merge_beam(MergeArgs m, BeamArgs a) {
+  extern __shared__ __align__(16) float mw[];
+  __shared__ BeamSmem s;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, b = blockIdx.x;
+  merge_row<S>(m, b * a.F + wave, mw + (size_t)wave * m.nsets * m.k * 2);
+  __syncthreads();                                       // the chain's rows in vals / ids
+  const int k = min(a.keep, a.F * a.TB);
+  float cv = 0.f;
+  int ci = 0;
+  if (wave == 0) beam_phase1(a, b, lane, s, cv, ci);
+  __syncthreads();
+  if (wave == 0) beam_phase2(k, lane, s, cv, ci);
+  __syncthreads();
+  if (wave == 0) beam_phase3(a, b, lane, s, k);
 }
 
 // Best chain: idx = first arg-max of cum; walk the back-pointers from the last depth.
@@ -1465,6 +1511,49 @@ int cfh_head_topk_packed(const void* h, int M, int d, const void* packed, int n,
   hipStream_t st = (hipStream_t)stream;
   if ((rc = launch_head(ha, st, true))) return rc;
   return launch_merge(ws, M, ha.nsets, k, vals, ids, lse, st);
+}
+
+int cfh_head_topk_packed_beam_chain(const void* h, int M, int d, const void* packed, int n, const void* a,
+                                    const int32_t* a_ids, int a_ids_stride, int r, float* vals, int32_t* ids,
+                                    float* lse, void* ws, float* cum, int32_t* lastp, const int32_t* sl,
+                                    int32_t* toks, int32_t* bps, int B, int W, int order, void* stream) {
+  if (!packed || !vals || !ids || !ws || !cum || !lastp || !toks || !bps || B < 1 || W < 1 || W * W > 64 ||
+      W > KMAX || order < 1 || order > 8 || M != B * W || cfh_head_packed_bytes(n, d, r) < 0)
+    return CFH_E_INVALID;
+  const void* W2 = r > 0 ? (const char*)packed + head_packed_w_bytes(n, d) : nullptr;
+  HeadArgs ha;
+  int rc = head_args(ha, h, M, d, packed, nullptr, n, a, a_ids, a_ids_stride, r, W2);
+  if (rc) return rc;
+  ha.logits = nullptr;
+  ha.ws = ws;
+  ha.k = W;
+  ha.nsets = (n + HCOLS - 1) / HCOLS;
+  hipStream_t st = (hipStream_t)stream;
+  if ((rc = launch_head(ha, st, true))) return rc;
+  BeamArgs ba = {};
+  ba.vals = vals; ba.ids = ids; ba.cum = cum; ba.lastp = lastp; ba.sl = sl; ba.toks = toks; ba.bps = bps;
+  ba.B = B; ba.F = W; ba.TB = W; ba.keep = W; ba.order = order; ba.tree = 0;
+  MergeArgs mg = {};
+  mg.ws = ws; mg.M = M; mg.nsets = ha.nsets; mg.k = W; mg.vals = vals; mg.ids = ids; mg.lse = lse;
+  const size_t row_bytes = (size_t)ha.nsets * W * 8;
+  const int S = (ha.nsets + 63) / 64;
+  if (W <= 4 && S <= 8 && row_bytes * W <= 150 * 1024) {
+    const size_t lds = row_bytes * W;
+#define CFH_MB(SS)                                                                                          \
+  if (S <= SS) {                                                                                            \
+    CFH_HIP(hipFuncSetAttribute((const void*)k_merge_beam<SS>, hipFuncAttributeMaxDynamicSharedMemorySize,  \
+                                (int)lds));                                                                 \
+    hipLaunchKernelGGL(k_merge_beam<SS>, dim3(B), dim3(W * 64), lds, st, mg, ba);                          \
+    CFH_LAUNCH_CHECK();                                                                                     \
+    return CFH_OK;                                                                                          \
+  }
+    CFH_MB(1) CFH_MB(2) CFH_MB(4) CFH_MB(8)
+#undef CFH_MB
+  }
+  if ((rc = launch_merge(ws, M, ha.nsets, W, vals, ids, lse, st))) return rc;
+  hipLaunchKernelGGL(k_beam_step, dim3(B), dim3(64), 0, st, ba);
+  CFH_LAUNCH_CHECK();
+  return CFH_OK;
 }
 
 int cfh_head_gemm_topk(const void* x, int M, int d, const void* W, const int32_t* sl, int n, int k, void* logits,

@@ -383,6 +383,17 @@ int cfh_beam_chain_step(const float* vals, const int32_t* ids, float* cum, int32
                         const int32_t* sl, int32_t* toks, int32_t* bps, int B, int W, int order,
                         void* stream);
 
+/* cfh_head_topk_packed with k = W over the M = B W beam rows, then cfh_beam_chain_step on them (sl:
+ * the ids' map, as there): the merge of the head's candidate lists and the beam step run as one
+ * launch, a workgroup a chain, a wave a beam row, then the step on the chain's rows.  vals / ids /
+ * lse are written as cfh_head_topk_packed writes them and cum / lastp / toks / bps as
+ * cfh_beam_chain_step does; same results as the two calls.  One depth of _beam_chains' _head +
+ * _bias + top-k + chain step (cf/vllm_plugin/flow_proposer.py:1234-1259). */
+int cfh_head_topk_packed_beam_chain(const void* h, int M, int d, const void* packed, int n, const void* a,
+                                    const int32_t* a_ids, int a_ids_stride, int r, float* vals, int32_t* ids,
+                                    float* lse, void* ws, float* cum, int32_t* lastp, const int32_t* sl,
+                                    int32_t* toks, int32_t* bps, int B, int W, int order, void* stream);
+
 /* One depth of _beam_tree (:1300-1330): F live frontier slots, topb children each, keep the best
  * k = min(keep, F*topb); writes node tokens to out[b][base + i] and parent node indices to
  * out[b][ld_out/2 + base + i]; cum/lastp/prev_ids are [B][keep](...) frontier arrays, updated. */

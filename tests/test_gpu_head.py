@@ -306,3 +306,56 @@ def test_packed_head_full_width_matches_oracle(cuda):
             hi = np.inf if r == 0 else rv[r - 1] - rv[r]
             if min(lo, hi) > MARGIN:
                 assert gid[m, r] == order[m, r], (m, r)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,W,img", [(1, 4, False), (2, 4, False), (1, 2, False), (2, 1, False), (1, 4, True),
+                                     (2, 3, True)])
+def test_merged_topk_and_beam_step_equal_the_two_calls(cuda, B, W, img):
+    """cfh_head_topk_packed_beam_chain (the candidate merge and the chain step in one launch) against
+    cfh_head_topk_packed followed by cfh_beam_chain_step, bit for bit, over four depths of evolving
+    beams: vals / ids / lse, cum, lastp, toks and bps; over the head's own packed image (ids mapped
+    through the shortlist) and over a packed image of 1,000 candidate rows (ids mapped through them)."""
+    from chain_flow_amd import _lib
+    d, V, n, order = 512, 4096, 3000, 4
+    cfg, W_ = _head_weights(d, V, seed=3)
+    sl = _shortlist(V, n, seed=5).to(cuda)
+    head = ShortlistHead(W_["lm_head.weight"].to(cuda), sl, W_["markov.w1.weight"].to(cuda),
+                         W_["markov.w2.weight"].to(cuda))
+    g = torch.Generator().manual_seed(11 + B * W)
+    if img:
+        cand = sl[torch.randperm(n, generator=g)[:1000].sort().values.to(cuda)].contiguous()
+        image, nimg, smap = head.pack_rows(cand), 1000, cand
+    else:
+        image, nimg, smap = None, n, sl
+    L = _lib.lib()
+    st = _lib.stream_handle()
+    states = []
+    for fused in (False, True):
+        lastp = torch.full((B, W, order), -1, dtype=torch.int32, device=cuda)
+        lastp[:, :, 0] = sl[torch.arange(B) * 7 % n].view(B, 1).to(torch.int32)
+        cum = torch.full((B, W), float("-inf"), device=cuda)
+        cum[:, 0] = 0.0
+        out = []
+        for depth in range(4):
+            h = torch.randn(B * W, d, generator=torch.Generator().manual_seed(100 + depth)).half().to(cuda)
+            toks = torch.empty(B, W, dtype=torch.int32, device=cuda)
+            bps = torch.empty(B, W, dtype=torch.int32, device=cuda)
+            if fused:
+                vals, ids, lse = head.topk_beam_chain(h, image, nimg, lastp.view(-1), order, cum, lastp, smap,
+                                                      toks, bps, B, W, order)
+            else:
+                if img:
+                    vals, ids, lse = head.topk_image(h, W, image, nimg, prev=lastp.view(-1), prev_stride=order)
+                else:
+                    vals, ids, lse = head.topk(h, W, prev=lastp.view(-1), prev_stride=order)
+                _lib.check(L.cfh_beam_chain_step(vals.data_ptr(), ids.data_ptr(), cum.data_ptr(), lastp.data_ptr(),
+                                                 smap.data_ptr(), toks.data_ptr(), bps.data_ptr(), B, W, order, st),
+                           "cfh_beam_chain_step")
+            torch.cuda.synchronize()
+            out.append([t.clone().cpu() for t in (vals, ids, lse, cum, lastp, toks, bps)])
+        states.append(out)
+    print(f"[merged beam] B={B} W={W} image={img} toks {states[1][-1][5].tolist()}", flush=True)
+    for depth, (a, b) in enumerate(zip(*states)):
+        for name, x, y in zip(("vals", "ids", "lse", "cum", "lastp", "toks", "bps"), a, b):
+            assert torch.equal(x, y), (depth, name)

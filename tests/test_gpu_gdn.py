@@ -104,6 +104,18 @@ def test_gdn_forest_sqrt_eps_and_outputs_only(cuda):
 
 
 @pytest.mark.gpu
+def test_gdn_large_deep_tree_matches_oracle(cuda):
+    """A random 100-node tree of depth 9: paths longer than one staging batch of eight steps, and
+    parents anywhere before their nodes."""
+    rng = np.random.default_rng(4)
+    parent = np.array([-1] + [int(rng.integers(0, i)) for i in range(1, 100)])
+    out, st, ro, rs, _ = _run(cuda, parent, H=4, Dv=64, seed=13)
+    print(f"[gdn] N=100 out err {rel_err(to64(out), ro):.2e} state err {rel_err(to64(st), rs):.2e}", flush=True)
+    assert rel_err(to64(out), ro) < TOL
+    assert rel_err(to64(st), rs) < TOL
+
+
+@pytest.mark.gpu
 def test_gdn_refuses_non_bfs_order(cuda):
     """A parent index at or after its node breaks the BFS contract: the kernel writes NaN for that
     node instead of reading a state that does not exist yet."""

@@ -46,6 +46,26 @@ def test_candidate_select_argument_checks_without_a_device():
     assert L.cfh_cand_topm(p, 1003, p, 0, 5, 1001, 77, None, p, None, p, None) == 0         # nothing to do
 
 
+def test_merged_topk_beam_argument_checks_without_a_device():
+    """cfh_head_topk_packed_beam_chain returns before any launch when the rows are not B x W beams,
+    the chain's W x W candidates exceed one wave, the markov order is outside 1..8 or a search-state
+    pointer is missing."""
+    L = _lib.lib()
+    p = 4096   # stand-in addresses: never dereferenced, the checks fail first
+
+    def call(M=8, B=2, W=4, order=4, cum=p):
+        # (h, M, d, packed, n, a, a_ids, a_ids_stride, r, vals, ids, lse, ws, cum, lastp, sl, toks, bps,
+        #  B, W, order, stream)
+        return L.cfh_head_topk_packed_beam_chain(p, M, 512, p, 1000, None, None, 0, 0, p, p, p, p, cum, p,
+                                                  None, p, p, B, W, order, None)
+    assert call(M=7) == 1            # M != B W
+    assert call(M=9, B=1, W=9) == 1  # W x W > 64
+    assert call(order=0) == 1
+    assert call(order=9) == 1
+    assert call(cum=None) == 1
+    assert call(M=0, B=0) == 1
+
+
 def test_noalloc_flow_rejects_a_workspace_beyond_the_scratch_without_a_device():
     """cfh_flow_integrate_noalloc refuses, before any HIP call, a shape whose flow workspace exceeds
     the 64 MiB scratch array (d = 8192 at 8 layers needs 75.8 MiB), with its own status."""

@@ -67,7 +67,10 @@ class DraftGraphs:
         torch.cuda.current_stream().wait_stream(st)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
+        # captured in inference mode whatever the caller's mode: torch's capture updates the CUDA
+        # generator's graph state in place, and that state is an inference tensor once a capture
+        # has run inside inference mode (the proposer's propose() captures there)
+        with torch.inference_mode(), torch.cuda.graph(g):
             out = self._body(b)
         self._g[bkt] = (g, b, out)
 

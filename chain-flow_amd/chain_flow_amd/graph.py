@@ -77,7 +77,8 @@ class DraftGraphs:
     def run(self, sh: torch.Tensor, rows, starts, cnt, k0, wmask=None) -> torch.Tensor:
         """One step for B requests (B <= the largest bucket): rows / starts / cnt / k0 sequences or
         tensors of length B, sh [T, H] with every request's rows.  Returns the draft's [B, ...] rows
-        of the bucket's output buffer (valid until the next run on the same bucket)."""
+        of the bucket's output buffer (valid until the next run on the same bucket; an inference tensor,
+        so clone it before updating it in place outside inference mode)."""
         B = len(rows)
         bkt = self.bucket_for(B)
         if bkt is None:
